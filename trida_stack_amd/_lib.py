@@ -1,0 +1,65 @@
+"""ctypes binding of libtrida_hip.so, the C ABI declared in include/trida_hip.h.
+
+The library is the only compute path of this package: there is no CPU or PyTorch fallback, and every
+wrapper raises when the library is missing.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libtrida_hip.so"
+
+TRIDA_OK = 0
+TRIDA_ERR_ARG = -1
+TRIDA_ERR_NULL = -2
+TRIDA_ERR_ALIGN = -3
+TRIDA_ERR_WORKSPACE = -4
+TRIDA_ERR_LAUNCH = -5
+
+P = C.c_void_p
+I64 = C.c_int64
+I32 = C.c_int32
+F32 = C.c_float
+
+# name -> (restype, argtypes); one line per entry point of include/trida_hip.h
+SIGNATURES = {
+    "trida_version": (C.c_int, []),
+    "trida_last_error": (C.c_char_p, []),
+    "trida_greedy_accept_scratch_bytes": (I64, [I64, I64, I64, I64]),
+    "trida_greedy_accept": (C.c_int, [P, I64, I64, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, P, I64, I64, P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> C.CDLL:
+    """Loads and types the library once per process; raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is missing: build it with `python -m trida_stack_amd.build` "
+                    "(there is no fallback path)")
+            lib = C.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Maps a C-ABI status to the exception the caller sees (ValueError for a rejected argument)."""
+    if rc == TRIDA_OK:
+        return
+    msg = load().trida_last_error().decode(errors="replace")
+    if rc == TRIDA_ERR_LAUNCH:
+        raise RuntimeError(f"{what}: {msg}")
+    raise ValueError(f"{what}: {msg} (status {rc})")

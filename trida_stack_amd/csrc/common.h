@@ -1,0 +1,74 @@
+// Shared device helpers and host-side error plumbing for the gfx950 kernels behind include/trida_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/trida_hip.h"
+
+namespace trida {
+
+// ---------------------------------------------------------------- bf16 storage (uint16 bits)
+// Round-to-nearest-even, quiet NaN preserved: the same rounding torch applies on fp32 -> bf16.
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------- wave64 helpers
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+// Sum across aligned groups of `width` lanes (width a power of two <= 64).
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Device-scope release/acquire used by the last-block-done reductions. On gfx950 these lower to the
+// L2 write-back / invalidate that make one XCD's stores visible to a block running on another XCD.
+// Arrive with release only: the acquire (an L2 invalidate on gfx950) is paid once, by the block
+// that finds itself last, through fence_acquire().
+__device__ __forceinline__ unsigned arrive_release(unsigned* counter) {
+  return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void fence_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ void reset_counter(unsigned* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------- host error plumbing
+void set_error(const char* fmt, ...);
+int launch_status(const char* what);
+
+inline int64_t align_up(int64_t x, int64_t a) { return (x + a - 1) / a * a; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace trida
+
+#define TRIDA_CHECK(cond, code, ...)      \
+  do {                                    \
+    if (!(cond)) {                        \
+      trida::set_error(__VA_ARGS__);      \
+      return (code);                      \
+    }                                     \
+  } while (0)
