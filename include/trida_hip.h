@@ -59,6 +59,71 @@ int trida_greedy_accept(const float* logits, int64_t B, int64_t R, int64_t V, in
                         int32_t* n_acc, int64_t* bonus, int64_t* crop, void* scratch,
                         int64_t scratch_bytes, int64_t splits, void* stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * GDN layer front half: depthwise causal conv (width Kc in 2..4) over [window ++ x] + SiLU, split into
+ * q / k / v, per-head l2norm of q and k (eps 1e-6), gates g = -exp(A_log) * softplus(a + dt_bias) and
+ * beta = sigmoid(b). Replaces the conv / split / normalise / gate steps of TridaRuntime._gdn
+ *   (inference/zoro-1/mlx/trida_mlx/model.py:285-303) and the fused prep inside
+ *   fused_selfspec_gdn_layer (inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:2211-2220).
+ * x [B, T, C] bf16 pre-conv rows (batch stride x_sb, row stride x_st, elements), C = 2*Hk*Dk + Hv*Dv;
+ * window [B, Kc-1, C] bf16; conv_w [C, Kc] bf16; a, b [B, T, Hv] bf16 (strides ab_sb, ab_st);
+ * A_log, dt_bias [Hv] fp32. Outputs (contiguous): q, k [B, T, Hk, Dk] bf16 unit-norm, v [B, T, Hv, Dv]
+ * bf16, g, beta [B, T, Hv] fp32, and window_out [B, Kc-1, C] (last Kc-1 rows of [window ++ x]) when
+ * not NULL; window_out must not alias window. Dk in {32, 64, 128}, Dv % 8 == 0.
+ */
+int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w, const uint16_t* a,
+                   const uint16_t* b, const float* A_log, const float* dt_bias, uint16_t* q, uint16_t* k,
+                   uint16_t* v, float* g, float* beta, uint16_t* window_out, int64_t B, int64_t T,
+                   int64_t Kc, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb, int64_t x_st,
+                   int64_t ab_sb, int64_t ab_st, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Gated delta rule, recurrent form, with the block-causal canvas readout.
+ * Replaces canvas_gdn_fused (inference/zoro-1/mlx/trida_mlx/kernels.py:118-131) and
+ *   fused_recurrent_block_causal_gated_delta_rule(..., causal_mode, num_clean, initial_state,
+ *   output_final_state) (qwen3_5_diffusion.py:2408-2415).
+ * Per value head h (key head h / (Hv/Hk)) and row t, with g the log decay and q scaled by `scale`:
+ *   S = e^g S; delta = beta (v - S k); S += delta k^T; o_t = S q_t.
+ * causal_mode 1: every row reads its own state. causal_mode 2: rows t < num_clean read their own
+ * state, rows t >= num_clean read the block-end state.
+ * q, k [B, T, Hk, Dk] bf16, v [B, T, Hv, Dv] bf16, g, beta [B, T, Hv] fp32 (all contiguous);
+ * state_in [B, Hv, Dv, Dk] fp32 (row v of head h holds S[:, v]); out [B, T, Hv, Dv] bf16.
+ * state_out (NULL or, may alias state_in): state after all T rows. state_clean (NULL or a separate
+ * buffer): state after min(num_clean, T) rows. Dk in {32, 64, 128, 256}, Dv % 4 == 0.
+ */
+int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                        const float* beta, const float* state_in, uint16_t* out, float* state_out,
+                        float* state_clean, int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk,
+                        int64_t Dv, int causal_mode, int64_t num_clean, float scale, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * GDN state snapshot: one coalesced copy of state_elems fp32 recurrent-state values and window_elems
+ * bf16 conv-window values (any number of layers and sequences laid out contiguously).
+ * Replaces the GDN backup before a draft/verify block (SGLang patch
+ *   inference/zoro-1/sglang/two_stream_diffusion.patch:521-549, 557-569) and
+ *   SeqCache.snapshot (inference/zoro-1/mlx/trida_mlx/model.py:184-190).
+ * state_elems % 4 == 0, window_elems % 8 == 0, all buffers 16-byte aligned.
+ */
+int trida_gdn_snapshot(const float* state, float* snap_state, int64_t state_elems, const uint16_t* window,
+                       uint16_t* snap_window, int64_t window_elems, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * GDN rollback to an accepted prefix of the block. Replaces TridaRuntime.commit
+ *   (inference/zoro-1/mlx/trida_mlx/model.py:486-507) and the conv-window rebuild of _selfspec_step
+ *   (qwen3_5_diffusion.py:963-975).
+ * For each of NB (layer, sequence) slots b, with n = n_keep[b % seq_mod] clamped to [0, T]:
+ *   state[b]  = snap_state[b] advanced by block rows 0..n-1 (k, v, g, beta as trida_gdn_prep writes
+ *               them, [NB, T, ...]); may alias snap_state.
+ *   window[b] = last Kc-1 rows of (snap_window[b] ++ preconv[b, :n]); may alias snap_window.
+ * preconv [NB, T, C] bf16 with strides x_sb, x_st. Either part is skipped when its pointers are NULL.
+ * skip_full != 0 leaves slots with n == T untouched (their state already covers the whole block).
+ */
+int trida_gdn_restore(const float* snap_state, float* state, const uint16_t* k, const uint16_t* v,
+                      const float* g, const float* beta, const uint16_t* snap_window, uint16_t* window,
+                      const uint16_t* preconv, const int32_t* n_keep, int64_t NB, int64_t seq_mod, int64_t T,
+                      int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t C, int64_t Kc, int64_t x_sb,
+                      int64_t x_st, int skip_full, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

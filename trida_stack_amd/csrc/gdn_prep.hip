@@ -1,0 +1,198 @@
+// GDN layer front half, fused: depthwise causal conv (width Kc) over [window ++ x] + SiLU, split
+// into q / k / v, l2norm of q and k per head, and the gates g = -exp(A_log) softplus(a + dt_bias),
+// beta = sigmoid(b).
+//
+// Launch: one 256-thread block per (sequence, row). A thread owns 8 consecutive channels (one 16-byte
+// piece); the Dk/8 threads of a q or k head reduce its sum of squares with a row-local reduction.
+// Rounding follows the CPU oracle: conv and SiLU in fp32, rounded to bf16, then l2norm in fp32 of the
+// rounded values, rounded to bf16 again.
+#include "common.h"
+
+namespace trida {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxKc = 4;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// Sum over aligned groups of W lanes (W = 4, 8 or 16); every lane receives its group's total.
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  if (W == 16) {
+    v += dpp<0x128>(v);
+    v += dpp<0x124>(v);
+  } else if (W == 8) {
+    v += __shfl_xor(v, 4, kWave);
+  }
+  v += dpp<0x4E>(v);
+  v += dpp<0xB1>(v);
+  return v;
+}
+
+struct PrepArgs {
+  const uint16_t* x;  // [B, T, C] (batch stride x_sb, row stride x_st)
+  const uint16_t* window;  // [B, Kc-1, C]
+  const uint16_t* conv_w;  // [C, Kc]
+  const uint16_t* a_in;    // [B, T, Hv] (batch stride ab_sb, row stride ab_st)
+  const uint16_t* b_in;
+  const float* A_log;  // [Hv]
+  const float* dt_bias;
+  uint16_t* q;  // [B, T, Hk, Dk]
+  uint16_t* k;
+  uint16_t* v;  // [B, T, Hv, Dv]
+  float* g;     // [B, T, Hv]
+  float* beta;
+  uint16_t* window_out;  // [B, Kc-1, C] or null
+  int T, C, Kc, Hk, Hv, Dk, Dv;
+  int64_t x_sb, x_st, ab_sb, ab_st;
+};
+
+__device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
+  f[0] = bf2f((uint16_t)(w.x & 0xffff));
+  f[1] = bf2f((uint16_t)(w.x >> 16));
+  f[2] = bf2f((uint16_t)(w.y & 0xffff));
+  f[3] = bf2f((uint16_t)(w.y >> 16));
+  f[4] = bf2f((uint16_t)(w.z & 0xffff));
+  f[5] = bf2f((uint16_t)(w.z >> 16));
+  f[6] = bf2f((uint16_t)(w.w & 0xffff));
+  f[7] = bf2f((uint16_t)(w.w >> 16));
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 w;
+  w.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+  w.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+  w.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
+  w.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+  return w;
+}
+
+__device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
+// torch.nn.functional.softplus with beta 1 and threshold 20
+__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+template <int GW, int KC>  // lanes per q/k head = Dk / 8; conv width
+__global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
+  const int t = blockIdx.x % a.T;
+  const int b = blockIdx.x / a.T;
+  const int tid = threadIdx.x;
+  const int key_dim = a.Hk * a.Dk;
+  const int pieces = a.C / 8;
+  const uint16_t* xb = a.x + (int64_t)b * a.x_sb;
+  const uint16_t* wb = a.window + (int64_t)b * (a.Kc - 1) * a.C;
+
+  // the q/k pieces come first (2 * key_dim / 8 of them, a multiple of GW), so every group of GW
+  // lanes of one pass belongs to one head and the whole group is active together
+  for (int p0 = 0; p0 < pieces; p0 += kThreads) {
+    const int p = p0 + tid;
+    const bool live = p < pieces;
+    const int c = (live ? p : 0) * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (live) {
+      float w[8][KC];
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+        for (int j = 0; j < KC; ++j) w[ch][j] = bf2f(a.conv_w[(int64_t)(c + ch) * KC + j]);
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const int tau = t - (KC - 1) + j;  // source row; negative rows come from the window
+        const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(KC - 1 + tau) * a.C + c;
+        float f[8];
+        unpack8(*reinterpret_cast<const u32x4*>(src), f);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) acc[ch] = fmaf(w[ch][j], f[ch], acc[ch]);
+      }
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) acc[ch] = bf2f(f2bf(silu(acc[ch])));
+    }
+    const bool is_qk = c < 2 * key_dim;  // uniform across a GW-lane group
+    if (p0 < 2 * key_dim / 8) {
+      // this pass may hold q/k pieces: per-head l2norm (all lanes take part in the reduction)
+      float ss = 0.f;
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) ss = fmaf(acc[ch], acc[ch], ss);
+      ss = lane_group_sum<GW>(ss);
+      if (live && is_qk) {
+        const float inv = rsqrtf(ss + 1e-6f);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) acc[ch] *= inv;
+      }
+    }
+    if (live) {
+      const u32x4 w = pack8(acc);
+      const int64_t row = (int64_t)b * a.T + t;
+      if (c < key_dim)
+        *reinterpret_cast<u32x4*>(a.q + row * key_dim + c) = w;
+      else if (c < 2 * key_dim)
+        *reinterpret_cast<u32x4*>(a.k + row * key_dim + (c - key_dim)) = w;
+      else
+        *reinterpret_cast<u32x4*>(a.v + row * (int64_t)a.Hv * a.Dv + (c - 2 * key_dim)) = w;
+    }
+  }
+
+  if (tid < a.Hv) {
+    const float av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
+    const float bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
+    const int64_t o = ((int64_t)b * a.T + t) * a.Hv + tid;
+    a.g[o] = -__expf(a.A_log[tid]) * softplus(av + a.dt_bias[tid]);
+    a.beta[o] = 1.f / (1.f + __expf(-bv));
+  }
+
+  // the new conv window (last Kc-1 rows of [window ++ x]) is written by the last row's block
+  if (a.window_out && t == a.T - 1) {
+    for (int p = tid; p < (a.Kc - 1) * pieces; p += kThreads) {
+      const int wr = p / pieces, c = (p % pieces) * 8;
+      const int tau = a.T - (a.Kc - 1) + wr;
+      const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(a.Kc - 1 + tau) * a.C + c;
+      *reinterpret_cast<u32x4*>(a.window_out + ((int64_t)b * (a.Kc - 1) + wr) * a.C + c) =
+          *reinterpret_cast<const u32x4*>(src);
+    }
+  }
+}
+
+}  // namespace
+}  // namespace trida
+
+using namespace trida;
+
+extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w,
+                              const uint16_t* a_in, const uint16_t* b_in, const float* A_log,
+                              const float* dt_bias, uint16_t* q, uint16_t* k, uint16_t* v, float* g,
+                              float* beta, uint16_t* window_out, int64_t B, int64_t T, int64_t Kc,
+                              int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb, int64_t x_st,
+                              int64_t ab_sb, int64_t ab_st, void* stream) {
+  TRIDA_CHECK(x && window && conv_w && a_in && b_in && A_log && dt_bias && q && k && v && g && beta,
+              TRIDA_ERR_NULL, "gdn_prep: a required pointer is NULL");
+  TRIDA_CHECK(B > 0 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0 && Kc >= 2 && Kc <= kMaxKc, TRIDA_ERR_ARG,
+              "gdn_prep: bad sizes B=%lld T=%lld Hk=%lld Hv=%lld Kc=%lld", (long long)B, (long long)T,
+              (long long)Hk, (long long)Hv, (long long)Kc);
+  TRIDA_CHECK(Dk == 32 || Dk == 64 || Dk == 128, TRIDA_ERR_ARG, "gdn_prep: Dk must be 32, 64 or 128");
+  TRIDA_CHECK(Dv % 8 == 0 && Hv <= kThreads, TRIDA_ERR_ARG, "gdn_prep: Dv % 8 == 0 and Hv <= 256 required");
+  const int64_t C = 2 * Hk * Dk + Hv * Dv;
+  TRIDA_CHECK(x_st % 8 == 0 && x_sb % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)window & 15) == 0,
+              TRIDA_ERR_ALIGN, "gdn_prep: x / window must be 16-byte aligned with strides in multiples of 8");
+  TRIDA_CHECK(x_st >= C, TRIDA_ERR_ARG, "gdn_prep: row stride of x smaller than conv_dim");
+  TRIDA_CHECK(window_out == nullptr || window_out != window, TRIDA_ERR_ARG,
+              "gdn_prep: window_out must not alias window");
+  TRIDA_CHECK(B * T < INT32_MAX, TRIDA_ERR_ARG, "gdn_prep: too many rows");
+  PrepArgs a{x, window, conv_w, a_in, b_in, A_log, dt_bias, q, k, v, g, beta, window_out,
+             (int)T, (int)C, (int)Kc, (int)Hk, (int)Hv, (int)Dk, (int)Dv, x_sb, x_st, ab_sb, ab_st};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(B * T));
+#define TRIDA_PREP_LAUNCH(GW)                                                                   \
+  switch (Kc) {                                                                                 \
+    case 2: hipLaunchKernelGGL((gdn_prep_kernel<GW, 2>), grid, dim3(kThreads), 0, st, a); break; \
+    case 3: hipLaunchKernelGGL((gdn_prep_kernel<GW, 3>), grid, dim3(kThreads), 0, st, a); break; \
+    default: hipLaunchKernelGGL((gdn_prep_kernel<GW, 4>), grid, dim3(kThreads), 0, st, a); break; \
+  }
+  switch (Dk) {
+    case 32: TRIDA_PREP_LAUNCH(4) break;
+    case 64: TRIDA_PREP_LAUNCH(8) break;
+    default: TRIDA_PREP_LAUNCH(16) break;
+  }
+#undef TRIDA_PREP_LAUNCH
+  return launch_status("gdn_prep");
+}

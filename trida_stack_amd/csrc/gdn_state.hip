@@ -1,0 +1,249 @@
+// GDN state snapshot and rollback.
+//
+// snapshot: coalesced copy of recurrent states (fp32) and conv windows (bf16) into snapshot buffers,
+//   any number of layers / sequences in one launch (the caller passes them as flat regions).
+// restore:  state = the block-entry snapshot advanced by the first n_keep rows of the block (the
+//   accepted prefix), and conv window = last Kc-1 rows of (snapshot window ++ pre-conv rows[:n_keep]).
+//   Layers stacked along the batch axis share the per-sequence n_keep (index b % seq_mod), so one
+//   launch rolls back every GDN layer. The output may alias the snapshot: every thread reads its whole
+//   slice before it writes.
+#include "common.h"
+
+namespace trida {
+namespace {
+
+constexpr int kLanesPerV = 16;
+constexpr int kVPerWave = kWave / kLanesPerV;
+constexpr int kTC = 32;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp<0x128>(v);
+  v += dpp<0x124>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0xB1>(v);
+  return v;
+}
+
+// ------------------------------------------------------------------ snapshot (flat copy)
+__global__ __launch_bounds__(256) void copy2_kernel(const u32x4* __restrict__ s0, u32x4* __restrict__ d0, int64_t n0,
+                                                    const u32x4* __restrict__ s1, u32x4* __restrict__ d1, int64_t n1) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  // 4 independent 16-byte copies in flight per thread per iteration
+  for (; i + 3 * stride < n0; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(s0 + i), b = __builtin_nontemporal_load(s0 + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(s0 + i + 2 * stride), d = __builtin_nontemporal_load(s0 + i + 3 * stride);
+    d0[i] = a;
+    d0[i + stride] = b;
+    d0[i + 2 * stride] = c;
+    d0[i + 3 * stride] = d;
+  }
+  for (; i < n0; i += stride) d0[i] = __builtin_nontemporal_load(s0 + i);
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n1; j += stride) d1[j] = s1[j];
+}
+
+// ------------------------------------------------------------------ restore: recurrent state
+struct RestoreArgs {
+  const float* snap;  // [NB, Hv, Dv, Dk]
+  float* state;
+  const uint16_t* k;  // [NB, T, Hk, Dk]
+  const uint16_t* v;  // [NB, T, Hv, Dv]
+  const float* g;     // [NB, T, Hv]
+  const float* beta;
+  const int32_t* n_keep;
+  int seq_mod, T, Hk, Hv, Dv, skip_full;
+};
+
+template <int KPL, int NW>
+__global__ __launch_bounds__(NW* kWave) void restore_state_kernel(RestoreArgs a) {
+  constexpr int Dk = KPL * kLanesPerV;
+  constexpr int VPB = NW * kVPerWave;
+  const int tiles = a.Dv / VPB;
+  const int vt = blockIdx.x % tiles;
+  const int h = (blockIdx.x / tiles) % a.Hv;
+  const int b = blockIdx.x / (tiles * a.Hv);
+  const int hk = h / (a.Hv / a.Hk);
+  const int n = min(max(a.n_keep[b % a.seq_mod], 0), a.T);
+  if (a.skip_full && n == a.T) return;  // the state already holds the whole block
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int vl = wave * kVPerWave + lane / kLanesPerV;
+  const int v = vt * VPB + vl;
+  const int kl = lane % kLanesPerV;
+  const int64_t off = (((int64_t)b * a.Hv + h) * a.Dv + v) * Dk + kl * KPL;
+  float s[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) s[i] = a.snap[off + i];
+
+  __shared__ __align__(16) uint16_t s_k[kTC][Dk];
+  __shared__ float s_v[kTC][VPB];
+  __shared__ float s_g[kTC], s_b[kTC];
+  const int64_t qk_row = (int64_t)a.Hk * Dk;
+  const uint16_t* kb = a.k + (int64_t)b * a.T * qk_row + (int64_t)hk * Dk;
+  const int64_t v_row = (int64_t)a.Hv * a.Dv;
+  const uint16_t* vb = a.v + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + vt * VPB;
+  const float* gb = a.g + (int64_t)b * a.T * a.Hv + h;
+  const float* bb = a.beta + (int64_t)b * a.T * a.Hv + h;
+  for (int t0 = 0; t0 < n; t0 += kTC) {
+    const int tn = min(kTC, n - t0);
+    __syncthreads();
+    constexpr int kPieces = Dk / 8;
+    for (int p = tid; p < tn * kPieces; p += NW * kWave) {
+      const int r = p / kPieces, c = (p % kPieces) * 8;
+      *reinterpret_cast<u32x4*>(&s_k[r][c]) = *reinterpret_cast<const u32x4*>(kb + (int64_t)(t0 + r) * qk_row + c);
+    }
+    for (int p = tid; p < tn * VPB; p += NW * kWave) {
+      const int r = p / VPB, c = p % VPB;
+      s_v[r][c] = bf2f(vb[(int64_t)(t0 + r) * v_row + c]);
+    }
+    for (int p = tid; p < tn; p += NW * kWave) {
+      s_g[p] = __expf(gb[(int64_t)(t0 + p) * a.Hv]);
+      s_b[p] = bb[(int64_t)(t0 + p) * a.Hv];
+    }
+    __syncthreads();
+    for (int r = 0; r < tn; ++r) {
+      float kk[KPL];
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) kk[i] = bf2f(s_k[r][kl * KPL + i]);
+      const float eg = s_g[r];
+      float kv = 0.f;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) {
+        s[i] *= eg;
+        kv = fmaf(s[i], kk[i], kv);
+      }
+      kv = row16_sum(kv);
+      const float delta = (s_v[r][vl] - kv) * s_b[r];
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) s[i] = fmaf(kk[i], delta, s[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < KPL; ++i) a.state[off + i] = s[i];
+}
+
+// ------------------------------------------------------------------ restore: conv window
+struct WindowArgs {
+  const uint16_t* snap_window;  // [NB, Kc-1, C]
+  uint16_t* window;
+  const uint16_t* preconv;  // [NB, T, C] (batch stride x_sb, row stride x_st)
+  const int32_t* n_keep;
+  int seq_mod, T, C, Kc, skip_full;
+  int64_t x_sb, x_st;
+  int64_t total;  // NB * C / 8 threads do work
+};
+
+__global__ __launch_bounds__(256) void restore_window_kernel(WindowArgs a) {
+  constexpr int kMaxRows = 7;
+  const int pieces = a.C / 8;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= a.total) return;
+  const int b = (int)(gid / pieces);
+  const int c = (int)(gid % pieces) * 8;
+  const int n = min(max(a.n_keep[b % a.seq_mod], 0), a.T);
+  if (a.skip_full && n == a.T) return;
+  const int W = a.Kc - 1;
+  u32x4 rows[kMaxRows];
+  // window row w of (snapshot ++ preconv[:n]) tail: source index m = n + w over the concatenation
+  // all reads before any write: the output may alias the snapshot window
+#pragma unroll
+  for (int w = 0; w < kMaxRows; ++w) {
+    if (w < W) {
+      const int m = n + w;  // position in [snapshot rows 0..W-1, preconv rows 0..n-1]
+      const uint16_t* src = m < W ? a.snap_window + ((int64_t)b * W + m) * a.C + c
+                                  : a.preconv + (int64_t)b * a.x_sb + (int64_t)(m - W) * a.x_st + c;
+      rows[w] = *reinterpret_cast<const u32x4*>(src);
+    }
+  }
+#pragma unroll
+  for (int w = 0; w < kMaxRows; ++w)
+    if (w < W) *reinterpret_cast<u32x4*>(a.window + ((int64_t)b * W + w) * a.C + c) = rows[w];
+}
+
+template <int KPL>
+int launch_restore(const RestoreArgs& ra, int64_t NB, hipStream_t st) {
+  int nw = 4;
+  while (nw > 1 && (ra.Dv % (nw * kVPerWave) != 0 || NB * ra.Hv * (ra.Dv / (nw * kVPerWave)) < 256)) nw /= 2;
+  if (ra.Dv % (nw * kVPerWave) != 0) return TRIDA_ERR_ARG;
+  const unsigned grid = (unsigned)(NB * ra.Hv * (ra.Dv / (nw * kVPerWave)));
+  switch (nw) {
+    case 4: hipLaunchKernelGGL((restore_state_kernel<KPL, 4>), dim3(grid), dim3(4 * kWave), 0, st, ra); break;
+    case 2: hipLaunchKernelGGL((restore_state_kernel<KPL, 2>), dim3(grid), dim3(2 * kWave), 0, st, ra); break;
+    default: hipLaunchKernelGGL((restore_state_kernel<KPL, 1>), dim3(grid), dim3(kWave), 0, st, ra); break;
+  }
+  return launch_status("gdn_restore/state");
+}
+
+}  // namespace
+}  // namespace trida
+
+using namespace trida;
+
+extern "C" int trida_gdn_snapshot(const float* state, float* snap_state, int64_t state_elems,
+                                  const uint16_t* window, uint16_t* snap_window, int64_t window_elems,
+                                  void* stream) {
+  TRIDA_CHECK(state_elems >= 0 && window_elems >= 0, TRIDA_ERR_ARG, "gdn_snapshot: negative size");
+  TRIDA_CHECK(state_elems % 4 == 0 && window_elems % 8 == 0, TRIDA_ERR_ARG,
+              "gdn_snapshot: state elements must be a multiple of 4 and window elements of 8");
+  TRIDA_CHECK((state_elems == 0 || (state && snap_state)) && (window_elems == 0 || (window && snap_window)),
+              TRIDA_ERR_NULL, "gdn_snapshot: NULL buffer with a non-zero size");
+  TRIDA_CHECK((((uintptr_t)state | (uintptr_t)snap_state | (uintptr_t)window | (uintptr_t)snap_window) & 15) == 0,
+              TRIDA_ERR_ALIGN, "gdn_snapshot: buffers must be 16-byte aligned");
+  const int64_t n0 = state_elems / 4, n1 = window_elems / 8;
+  if (n0 + n1 == 0) return TRIDA_OK;
+  // enough blocks for every CU, at most ~8 KiB per thread-row pass
+  int64_t blocks = cdiv(n0 > n1 ? n0 : n1, 256 * 4);
+  blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
+  hipLaunchKernelGGL(copy2_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const u32x4*>(state), reinterpret_cast<u32x4*>(snap_state), n0,
+                     reinterpret_cast<const u32x4*>(window), reinterpret_cast<u32x4*>(snap_window), n1);
+  return launch_status("gdn_snapshot");
+}
+
+extern "C" int trida_gdn_restore(const float* snap_state, float* state, const uint16_t* k, const uint16_t* v,
+                                 const float* g, const float* beta, const uint16_t* snap_window,
+                                 uint16_t* window, const uint16_t* preconv, const int32_t* n_keep,
+                                 int64_t NB, int64_t seq_mod, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk,
+                                 int64_t Dv, int64_t C, int64_t Kc, int64_t x_sb, int64_t x_st, int skip_full,
+                                 void* stream) {
+  TRIDA_CHECK(n_keep, TRIDA_ERR_NULL, "gdn_restore: n_keep is required");
+  TRIDA_CHECK(NB > 0 && T > 0 && seq_mod > 0 && NB % seq_mod == 0, TRIDA_ERR_ARG,
+              "gdn_restore: bad NB=%lld seq_mod=%lld T=%lld", (long long)NB, (long long)seq_mod, (long long)T);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (snap_state || state) {
+    TRIDA_CHECK(snap_state && state && k && v && g && beta, TRIDA_ERR_NULL,
+                "gdn_restore: state rollback needs snap_state, state, k, v, g and beta");
+    TRIDA_CHECK(Hk > 0 && Hv > 0 && Hv % Hk == 0 && Dv > 0 && Dv % 4 == 0, TRIDA_ERR_ARG,
+                "gdn_restore: bad head sizes");
+    TRIDA_CHECK(Dk == 32 || Dk == 64 || Dk == 128 || Dk == 256, TRIDA_ERR_ARG,
+                "gdn_restore: Dk must be 32, 64, 128 or 256");
+    TRIDA_CHECK(((uintptr_t)k & 15) == 0, TRIDA_ERR_ALIGN, "gdn_restore: k must be 16-byte aligned");
+    RestoreArgs ra{snap_state, state, k, v, g, beta, n_keep, (int)seq_mod, (int)T, (int)Hk, (int)Hv, (int)Dv,
+                   skip_full};
+    int rc;
+    switch (Dk) {
+      case 32: rc = launch_restore<2>(ra, NB, st); break;
+      case 64: rc = launch_restore<4>(ra, NB, st); break;
+      case 128: rc = launch_restore<8>(ra, NB, st); break;
+      default: rc = launch_restore<16>(ra, NB, st); break;
+    }
+    if (rc) return rc;
+  }
+  if (snap_window || window) {
+    TRIDA_CHECK(snap_window && window && preconv, TRIDA_ERR_NULL,
+                "gdn_restore: window rollback needs snap_window, window and preconv");
+    TRIDA_CHECK(C > 0 && C % 8 == 0 && Kc >= 2 && Kc <= 8, TRIDA_ERR_ARG, "gdn_restore: bad C / Kc");
+    TRIDA_CHECK(x_st % 8 == 0 && x_sb % 8 == 0 &&
+                ((((uintptr_t)preconv) | (uintptr_t)window | (uintptr_t)snap_window) & 15) == 0,
+                TRIDA_ERR_ALIGN, "gdn_restore: window buffers must be 16-byte aligned");
+    const int64_t threads = NB * (C / 8);
+    WindowArgs wa{snap_window, window, preconv, n_keep, (int)seq_mod, (int)T, (int)C, (int)Kc, skip_full,
+                  x_sb, x_st, threads};
+    hipLaunchKernelGGL(restore_window_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, st, wa);
+    return launch_status("gdn_restore/window");
+  }
+  return TRIDA_OK;
+}

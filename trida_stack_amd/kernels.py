@@ -93,3 +93,168 @@ def greedy_accept(logits: torch.Tensor, drafts: torch.Tensor, n_live: Optional[t
         crop.data_ptr(), scr.data_ptr(), scr.numel(), splits, _stream(dev))
     _lib.check(rc, "trida_greedy_accept")
     return am, n_acc, bonus, crop
+
+
+# --------------------------------------------------------------------------------------------------
+# GDN (gated delta net) layer pieces
+def _bf16(t: torch.Tensor, name: str):
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bf16 (got {t.dtype})")
+
+
+def _f32(t: torch.Tensor, name: str):
+    if t.dtype != torch.float32:
+        raise ValueError(f"{name} must be fp32 (got {t.dtype})")
+
+
+def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+             A_log: torch.Tensor, dt_bias: torch.Tensor, *, Hk: int, Hv: int, Dk: int, Dv: int,
+             window_out: Optional[torch.Tensor] = None):
+    """Conv + SiLU + split + l2norm(q, k) + gates for a block of rows (one launch).
+
+    x [B, T, C] bf16 (last dim contiguous, C = 2*Hk*Dk + Hv*Dv; batch / row strides may be larger),
+    window [B, Kc-1, C] bf16, conv_w [C, Kc] bf16, a, b [B, T, Hv] bf16 (last dim contiguous),
+    A_log, dt_bias [Hv] fp32. Returns q, k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g, beta [B,T,Hv] fp32.
+    window_out (optional, [B, Kc-1, C], not aliasing window) receives the last Kc-1 rows of
+    [window ++ x] (the causal-prefill conv state)."""
+    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, window_out)
+    for t, n in ((x, "x"), (window, "window"), (conv_w, "conv_w"), (a, "a"), (b, "b")):
+        _bf16(t, n)
+    _f32(A_log, "A_log")
+    _f32(dt_bias, "dt_bias")
+    B, T, C = x.shape
+    Kc = conv_w.shape[1]
+    if C != 2 * Hk * Dk + Hv * Dv or conv_w.shape != (C, Kc) or not conv_w.is_contiguous():
+        raise ValueError("x / conv_w do not match the head geometry")
+    if x.stride(2) != 1 or window.shape != (B, Kc - 1, C) or not window.is_contiguous():
+        raise ValueError("x must have a contiguous last dim and window be contiguous [B, Kc-1, C]")
+    if a.shape != (B, T, Hv) or b.shape != (B, T, Hv) or a.stride() != b.stride() or a.stride(2) != 1:
+        raise ValueError("a and b must be [B, T, Hv] with identical strides and a contiguous last dim")
+    if window_out is not None and (window_out.shape != window.shape or not window_out.is_contiguous()
+                                   or window_out.data_ptr() == window.data_ptr()):
+        raise ValueError("window_out must be a separate contiguous [B, Kc-1, C] buffer")
+    q = torch.empty((B, T, Hk, Dk), dtype=torch.bfloat16, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    g = torch.empty((B, T, Hv), dtype=torch.float32, device=dev)
+    beta = torch.empty_like(g)
+    rc = _lib.load().trida_gdn_prep(
+        x.data_ptr(), window.data_ptr(), conv_w.data_ptr(), a.data_ptr(), b.data_ptr(),
+        A_log.contiguous().data_ptr(), dt_bias.contiguous().data_ptr(), q.data_ptr(), k.data_ptr(),
+        v.data_ptr(), g.data_ptr(), beta.data_ptr(), _ptr(window_out), B, T, Kc, Hk, Hv, Dk, Dv,
+        x.stride(0), x.stride(1), a.stride(0), a.stride(1), _stream(dev))
+    _lib.check(rc, "trida_gdn_prep")
+    return q, k, v, g, beta
+
+
+def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                  state: torch.Tensor, *, causal_mode: int = 1, num_clean: Optional[int] = None,
+                  state_out: Optional[torch.Tensor] = None, want_clean: bool = False,
+                  scale: Optional[float] = None):
+    """Gated delta rule over T rows with the block-causal readout (one launch).
+
+    q, k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g (log decay), beta [B,T,Hv] fp32, state [B,Hv,Dv,Dk]
+    fp32 (read only unless passed again as state_out). causal_mode 2 with num_clean: rows >= num_clean
+    read the block-end state. Returns (out [B,T,Hv,Dv] bf16, state_clean or None)."""
+    dev = _need_gpu(q, k, v, g, beta, state, state_out)
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _bf16(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    for t, n in ((g, "g"), (beta, "beta"), (state, "state")):
+        _f32(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    B, T, Hk, Dk = k.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    if q.shape != k.shape or v.shape[:2] != (B, T) or g.shape != (B, T, Hv) or beta.shape != g.shape:
+        raise ValueError("q/k/v/g/beta shapes disagree")
+    if state.shape != (B, Hv, Dv, Dk):
+        raise ValueError(f"state must be [B, Hv, Dv, Dk] = {(B, Hv, Dv, Dk)}")
+    if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
+                                  or not state_out.is_contiguous()):
+        raise ValueError("state_out must match state")
+    nc = T if num_clean is None else int(num_clean)
+    out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    clean = torch.empty_like(state) if want_clean else None
+    sc = Dk ** -0.5 if scale is None else float(scale)
+    rc = _lib.load().trida_gdr_recurrent(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), state.data_ptr(),
+        out.data_ptr(), _ptr(state_out), _ptr(clean), B, T, Hk, Hv, Dk, Dv, causal_mode, nc, sc,
+        _stream(dev))
+    _lib.check(rc, "trida_gdr_recurrent")
+    return out, clean
+
+
+def gdn_snapshot(state: torch.Tensor, snap_state: torch.Tensor, window: Optional[torch.Tensor] = None,
+                 snap_window: Optional[torch.Tensor] = None) -> None:
+    """Copies recurrent states (fp32) and conv windows (bf16) into snapshot buffers (one launch)."""
+    dev = _need_gpu(state, snap_state, window, snap_window)
+    _f32(state, "state")
+    if snap_state.shape != state.shape or snap_state.dtype != state.dtype:
+        raise ValueError("snap_state must match state")
+    if not (state.is_contiguous() and snap_state.is_contiguous()):
+        raise ValueError("state buffers must be contiguous")
+    wn = 0
+    if window is not None:
+        _bf16(window, "window")
+        if snap_window is None or snap_window.shape != window.shape or not window.is_contiguous() \
+                or not snap_window.is_contiguous():
+            raise ValueError("snap_window must match window (contiguous)")
+        wn = window.numel()
+    rc = _lib.load().trida_gdn_snapshot(state.data_ptr(), snap_state.data_ptr(), state.numel(), _ptr(window),
+                                        _ptr(snap_window), wn, _stream(dev))
+    _lib.check(rc, "trida_gdn_snapshot")
+
+
+def gdn_restore(n_keep: torch.Tensor, *, snap_state: Optional[torch.Tensor] = None,
+                state: Optional[torch.Tensor] = None, k: Optional[torch.Tensor] = None,
+                v: Optional[torch.Tensor] = None, g: Optional[torch.Tensor] = None,
+                beta: Optional[torch.Tensor] = None, snap_window: Optional[torch.Tensor] = None,
+                window: Optional[torch.Tensor] = None, preconv: Optional[torch.Tensor] = None,
+                skip_full: bool = False) -> None:
+    """Rolls GDN state and/or conv windows back to the accepted prefix n_keep (one launch each).
+
+    The leading dims of every buffer are NB slots (layers stacked on sequences: slot b uses
+    n_keep[b % len(n_keep)]). state [NB,Hv,Dv,Dk] fp32, k [NB,T,Hk,Dk], v [NB,T,Hv,Dv] bf16,
+    g, beta [NB,T,Hv] fp32, windows [NB,Kc-1,C] bf16, preconv [NB,T,C] bf16 (last dim contiguous).
+    Outputs may alias the snapshots."""
+    dev = _need_gpu(n_keep, snap_state, state, k, v, g, beta, snap_window, window, preconv)
+    if n_keep.dtype != torch.int32 or n_keep.dim() != 1 or not n_keep.is_contiguous():
+        raise ValueError("n_keep must be int32 [B]")
+    seq_mod = n_keep.shape[0]
+    NB = T = Hk = Hv = Dk = Dv = C = Kc = 0
+    x_sb = x_st = 0
+    if state is not None:
+        for t, n in ((snap_state, "snap_state"), (state, "state"), (g, "g"), (beta, "beta")):
+            _f32(t, n)
+        _bf16(k, "k")
+        _bf16(v, "v")
+        NB, Hv, Dv, Dk = state.shape
+        T, Hk = k.shape[1], k.shape[2]
+        if snap_state.shape != state.shape or k.shape != (NB, T, Hk, Dk) or v.shape != (NB, T, Hv, Dv) \
+                or g.shape != (NB, T, Hv) or beta.shape != g.shape:
+            raise ValueError("restore: state / block row shapes disagree")
+        if not all(t.is_contiguous() for t in (snap_state, state, k, v, g, beta)):
+            raise ValueError("restore: state and block rows must be contiguous")
+    if window is not None:
+        _bf16(window, "window")
+        _bf16(snap_window, "snap_window")
+        _bf16(preconv, "preconv")
+        NBw, Km1, C = window.shape
+        Kc = Km1 + 1
+        if NB and NBw != NB:
+            raise ValueError("restore: window slots differ from state slots")
+        NB = NBw
+        T = preconv.shape[1] if not T else T
+        if snap_window.shape != window.shape or preconv.shape[0] != NB or preconv.shape[2] != C \
+                or preconv.shape[1] != T or preconv.stride(2) != 1:
+            raise ValueError("restore: window / preconv shapes disagree")
+        x_sb, x_st = preconv.stride(0), preconv.stride(1)
+    if NB == 0 or NB % seq_mod:
+        raise ValueError("restore: nothing to do or slots not a multiple of len(n_keep)")
+    rc = _lib.load().trida_gdn_restore(
+        _ptr(snap_state), _ptr(state), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(snap_window), _ptr(window),
+        _ptr(preconv), n_keep.data_ptr(), NB, seq_mod, T, Hk, Hv, Dk, Dv, C, Kc, x_sb, x_st, int(skip_full),
+        _stream(dev))
+    _lib.check(rc, "trida_gdn_restore")
