@@ -124,6 +124,29 @@ int trida_gdn_restore(const float* snap_state, float* state, const uint16_t* k, 
                       int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t C, int64_t Kc, int64_t x_sb,
                       int64_t x_st, int skip_full, void* stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * Canvas attention over a bf16 KV cache, with the draft / verify / mixed masks and GQA.
+ * Replaces TridaRuntime._attention + _canvas_mask (inference/zoro-1/mlx/trida_mlx/model.py:262-280,
+ *   461-470) and the FA3 canvas call with the E3 bidirectional MASK rows
+ *   (qwen3_5_diffusion.py:2516-2578).
+ * q [B, T, Hq, D] bf16 (normalised, rotated); k_cache, v_cache [B, Hkv, Lmax, D] bf16 holding the
+ * block's own keys at [prefix_len[b], prefix_len[b] + T); prefix_len [B] int32 on the device.
+ * Row t (query head hq = hk * (Hq/Hkv) + g) sees every prefix key and, inside the block, column j when
+ *   mask_mode 0 (verify): j <= t;  1 (draft): always;  2 (canvas): j <= t for t < n_clean, else always.
+ * out [B, T, Hq, D] bf16 = softmax(scale q k^T) v, times sigmoid(gate) when gate is not NULL (gate
+ * element (b, t, h, d) at gate + (b*T + t)*gate_row_stride + h*gate_head_stride + d).
+ * KV crop after acceptance is a change of prefix_len only. D in {64, 128, 256}.
+ * max_keys: an upper bound of prefix_len + T used to plan splits (0 = Lmax); splits 0 = auto.
+ * scratch: trida_attn_canvas_scratch_bytes(B, T, Hq, Hkv, D, max_keys, splits) bytes.
+ */
+int64_t trida_attn_canvas_scratch_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                        int64_t max_keys, int64_t splits);
+int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                      const int32_t* prefix_len, const uint16_t* gate, int64_t gate_row_stride,
+                      int64_t gate_head_stride, uint16_t* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
+                      int64_t D, int64_t Lmax, int mask_mode, int64_t n_clean, float scale, int64_t max_keys,
+                      int64_t splits, void* scratch, int64_t scratch_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

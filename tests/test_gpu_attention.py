@@ -1,0 +1,76 @@
+"""GPU parity: canvas attention kernel vs the CPU oracle (tolerance 2e-2, normwise max-abs)."""
+import pytest
+import torch
+
+from oracle import attention as A
+from trida_stack_amd import kernels
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+TOL = 2e-2
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def inputs(seed, B, T, Hq, Hkv, D, L):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16)
+    return q, kc, vc
+
+
+CASES = [  # B, T, Hq, Hkv, D, L, prefixes
+    (1, 32, 16, 4, 256, 8224, [8192]),          # config 3: verify / draft over 8192 + 32
+    (1, 33, 16, 4, 256, 2400, [2100]),          # the 4B-shape canvas (132 query rows)
+    (2, 5, 4, 2, 64, 300, [0, 213]),
+    (3, 9, 8, 2, 128, 520, [1, 77, 500]),
+    (1, 40, 8, 2, 128, 200, [100]),             # 160 query rows: two query tiles
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("mode", [0, 1, 2])
+def test_attn_canvas(gpu, case, mode):
+    B, T, Hq, Hkv, D, L, prefix = case
+    q, kc, vc = inputs(B + T + D + mode, B, T, Hq, Hkv, D, L)
+    nc = T // 2
+    ref = A.canvas_attention(q, kc, vc, prefix, mode, nc)
+    out = kernels.attn_canvas(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor(prefix, dtype=torch.int32, device=DEV),
+                              mask_mode=mode, n_clean=nc)
+    assert rel(out, ref) < TOL
+
+
+@pytest.mark.parametrize("splits", [1, 3, 64, 200])
+def test_attn_split_counts(gpu, splits):
+    B, T, Hq, Hkv, D, L, prefix = 1, 33, 16, 4, 256, 1100, [1000]
+    q, kc, vc = inputs(7, B, T, Hq, Hkv, D, L)
+    ref = A.canvas_attention(q, kc, vc, prefix, 0)
+    out = kernels.attn_canvas(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor(prefix, dtype=torch.int32, device=DEV),
+                              mask_mode=0, splits=splits)
+    assert rel(out, ref) < TOL
+
+
+def test_attn_gate_and_crop(gpu):
+    """Output gate fused into the combine; a KV crop is only a prefix-length change."""
+    B, T, Hq, Hkv, D, L = 1, 8, 8, 2, 128, 64
+    q, kc, vc = inputs(3, B, T, Hq, Hkv, D, L)
+    gate = torch.randn(B, T, Hq, 2 * D).to(torch.bfloat16)[..., D:]  # interleaved [q | gate] per head
+    for prefix in (30, 21):  # second call: the cache was cropped back to 21 committed keys
+        ref = A.canvas_attention(q, kc, vc, [prefix], 0, gate=gate)
+        out = kernels.attn_canvas(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor([prefix], dtype=torch.int32, device=DEV),
+                                  mask_mode=0, gate=gate.to(DEV))
+        assert rel(out, ref) < TOL
+
+
+def test_attn_clean_rows_equal_verify_rows(gpu):
+    """Canvas clean rows (mode 2, rows < n_clean) equal the verify (causal) rows exactly."""
+    B, T, Hq, Hkv, D, L = 1, 33, 16, 4, 256, 600
+    q, kc, vc = [t.to(DEV) for t in inputs(4, B, T, Hq, Hkv, D, L)]
+    pl = torch.tensor([500], dtype=torch.int32, device=DEV)
+    o0 = kernels.attn_canvas(q, kc, vc, pl, mask_mode=0)
+    o2 = kernels.attn_canvas(q, kc, vc, pl, mask_mode=2, n_clean=17)
+    assert torch.equal(o0[:, :17], o2[:, :17])

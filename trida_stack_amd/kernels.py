@@ -258,3 +258,51 @@ def gdn_restore(n_keep: torch.Tensor, *, snap_state: Optional[torch.Tensor] = No
         _ptr(preconv), n_keep.data_ptr(), NB, seq_mod, T, Hk, Hv, Dk, Dv, C, Kc, x_sb, x_st, int(skip_full),
         _stream(dev))
     _lib.check(rc, "trida_gdn_restore")
+
+
+# --------------------------------------------------------------------------------------------------
+# attention
+MASK_VERIFY, MASK_DRAFT, MASK_CANVAS = 0, 1, 2
+
+
+def attn_canvas(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, prefix_len: torch.Tensor, *,
+                mask_mode: int, n_clean: int = 0, scale: Optional[float] = None,
+                gate: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                max_keys: int = 0, splits: int = 0) -> torch.Tensor:
+    """Canvas attention of a block of T rows against a bf16 KV cache (split-K, MFMA).
+
+    q [B, T, Hq, D] bf16 contiguous; k_cache, v_cache [B, Hkv, Lmax, D] bf16 contiguous with the
+    block's keys already at [prefix_len, prefix_len + T); prefix_len [B] int32 on the device.
+    mask_mode: MASK_VERIFY (causal), MASK_DRAFT (bidirectional block) or MASK_CANVAS (rows < n_clean
+    causal). gate (optional) is [B, T, Hq, D]-indexable with a contiguous last dim: the output is
+    multiplied by sigmoid(gate). Returns out [B, T, Hq, D] bf16."""
+    dev = _need_gpu(q, k_cache, v_cache, prefix_len, gate, out)
+    for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _bf16(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    B, T, Hq, D = q.shape
+    _, Hkv, Lmax, Dk = k_cache.shape
+    if k_cache.shape[0] != B or v_cache.shape != k_cache.shape or Dk != D or Hq % Hkv:
+        raise ValueError("q / cache shapes disagree")
+    if prefix_len.dtype != torch.int32 or prefix_len.shape != (B,) or not prefix_len.is_contiguous():
+        raise ValueError("prefix_len must be int32 [B]")
+    g_row = g_head = 0
+    if gate is not None:
+        _bf16(gate, "gate")
+        if gate.shape != (B, T, Hq, D) or gate.stride(3) != 1 or gate.stride(0) != T * gate.stride(1):
+            raise ValueError("gate must be [B, T, Hq, D] with a contiguous last dim and packed batch rows")
+        g_row, g_head = gate.stride(1), gate.stride(2)
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 tensor shaped like q")
+    lib = _lib.load()
+    mk = max_keys if max_keys > 0 else Lmax
+    scr = workspaces.get(dev, "attn_canvas", lib.trida_attn_canvas_scratch_bytes(B, T, Hq, Hkv, D, mk, splits))
+    sc = D ** -0.5 if scale is None else float(scale)
+    rc = lib.trida_attn_canvas(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), prefix_len.data_ptr(),
+                               _ptr(gate), g_row, g_head, out.data_ptr(), B, T, Hq, Hkv, D, Lmax, mask_mode,
+                               n_clean, sc, mk, splits, scr.data_ptr(), scr.numel(), _stream(dev))
+    _lib.check(rc, "trida_attn_canvas")
+    return out
