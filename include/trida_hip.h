@@ -40,24 +40,34 @@ const char* trida_last_error(void);
  *   (inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:906-914)
  * and the greedy verify of selfspec_generate (inference/zoro-1/mlx/trida_mlx/decode.py:323-332).
  *
- * logits   [B, R, V] fp32, row r of sequence b at logits + b*batch_stride + r*row_stride.
- *          Row j (j < K) verifies draft j; row n_acc gives the bonus token (shift readout).
+ * logits   [B, R, V], dtype 0 = fp32 or 1 = bf16, element (b, r, x) at
+ *          logits + b*batch_stride + r*row_stride + x (strides in elements). Row j (j < K) verifies
+ *          draft j; row n_acc gives the bonus token (shift readout).
  * drafts   [B, K] int64 (row stride draft_stride); n_live [B] int32 or NULL (= K): draft j only counts
  *          when j < n_live[b]. ctx_len [B] int64 or NULL (= 0).
  * Outputs: argmax_out [B, R] int64 (or NULL), n_acc [B] int32, bonus [B] int64,
  *          crop [B] int64 = ctx_len + 1 + n_acc (KV entries kept: prefix + pending + accepted).
- * argmax is exact on fp32 with the first index winning ties and NaN ranking above every number.
- * Requires R >= K + 1, V < 2^31, R <= 1024. Two launches: a split-V argmax (each split of each row
- * to scratch), then one block per sequence reduces the splits and runs a wave ballot prefix scan.
- * splits = 0 picks the split count. scratch: trida_greedy_accept_scratch_bytes(B, R, V, splits) bytes,
- * no initialisation needed.
+ * argmax is exact with the first index winning ties and NaN ranking above every number (bf16 values
+ * compare as their exact fp32 widening). Requires R >= K + 1, V < 2^31, R <= 1024.
+ * Two launches: a split-V argmax (each split of each row to scratch), then one block per sequence
+ * reduces the splits and runs a wave ballot prefix scan. splits = 0 picks the split count.
+ * scratch: trida_greedy_accept_scratch_bytes(B, R, V, dtype, splits) bytes, no initialisation needed.
  */
-int64_t trida_greedy_accept_scratch_bytes(int64_t B, int64_t R, int64_t V, int64_t splits);
-int trida_greedy_accept(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+int64_t trida_greedy_accept_scratch_bytes(int64_t B, int64_t R, int64_t V, int dtype, int64_t splits);
+int trida_greedy_accept(const void* logits, int dtype, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
                         int64_t row_stride, const int64_t* drafts, int64_t K, int64_t draft_stride,
                         const int32_t* n_live, const int64_t* ctx_len, int64_t* argmax_out,
                         int32_t* n_acc, int64_t* bonus, int64_t* crop, void* scratch,
                         int64_t scratch_bytes, int64_t splits, void* stream);
+
+/* Row argmax (first index on ties) and, when conf is not NULL, the softmax probability of the argmax
+ * (the confidence the denoising passes rank MASK slots by). Replaces the argmax / max-softmax readout
+ * of the block-diffusion denoise step (_shifted_conf_pred, qwen3_5_diffusion.py:446-467).
+ * logits [rows, V] (dtype 0 fp32 / 1 bf16, row stride in elements); argmax [rows] int64; conf [rows]
+ * fp32. scratch: trida_row_argmax_scratch_bytes(rows, V, dtype, splits). */
+int64_t trida_row_argmax_scratch_bytes(int64_t rows, int64_t V, int dtype, int64_t splits);
+int trida_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, int64_t* argmax,
+                     float* conf, void* scratch, int64_t scratch_bytes, int64_t splits, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * GDN layer front half: depthwise causal conv (width Kc in 2..4) over [window ++ x] + SiLU, split into
@@ -146,6 +156,31 @@ int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t
                       int64_t gate_head_stride, uint16_t* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
                       int64_t D, int64_t Lmax, int mask_mode, int64_t n_clean, float scale, int64_t max_keys,
                       int64_t splits, void* scratch, int64_t scratch_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
+ * Row-wise decoder kernels around the GEMMs (bf16 storage, fp32 arithmetic). They replace the torch
+ * elementwise ops of the Qwen3.5 decoder layer the reference runtime calls through mlx-lm / vLLM
+ * (TridaRuntime._forward, inference/zoro-1/mlx/trida_mlx/model.py:337-364).
+ * add_rmsnorm: x = x + r (in place, r may be NULL), out = x * rsqrt(mean(x^2) + eps) * (1 + w)
+ *   (zero_centred = 1, Qwen3.5 RMSNorm) or * w (zero_centred = 0). Row strides in elements.
+ * silu_mul: out = silu(gu[:, :inter]) * gu[:, inter:2*inter] (SwiGLU).
+ * gated_rmsnorm: per value head, out = bf16(o * rsqrt(mean(o^2) + eps)) * w * silu(z)
+ *   (Qwen3.5 RMSNormGated); o, out [rows, H, Dv] contiguous, z row stride z_st.
+ * attn_prep: one canvas block of full-attention rows. qkv rows hold [Hq x (q | gate)] [Hkv x k] [Hkv x v]
+ *   (each D wide); q and k get a per-head zero-centred RMSNorm and rotate-half RoPE on the first
+ *   rot_dim dims at position pos0[b] + t (inv_freq_i = theta^(-2i/rot_dim)); q goes to q_out
+ *   [B, T, Hq, D], k and v to the caches [B, Hkv, Lmax, D] at slot slot0[b] + t.
+ */
+int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim,
+                      int64_t x_st, int64_t r_st, int64_t o_st, float eps, int zero_centred, void* stream);
+int trida_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter, int64_t g_st, int64_t o_st,
+                   void* stream);
+int trida_gated_rmsnorm(const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out, int64_t rows,
+                        int64_t H, int64_t Dv, int64_t z_st, float eps, void* stream);
+int trida_attn_prep(const uint16_t* qkv, int64_t qkv_row_stride, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
+                    const int32_t* pos0, const int32_t* slot0, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                    int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax, int64_t rot_dim,
+                    float rope_theta, float eps, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,276 @@
+"""CPU oracle: the hybrid decoder and the self-spec decode loops. Test infrastructure only (and the
+bench's timed CPU baseline).
+
+Follows the reference runtime inference/zoro-1/mlx/trida_mlx/model.py (forwards, canvas, commit) and
+decode.py (ar_generate, selfspec_generate), one sequence at a time, in fp32 arithmetic with bf16
+rounding where the model stores bf16 (GEMM outputs, residual stream, normalised activations). The
+layer math is the Qwen3.5 decoder layer ([tf]:420-760): zero-centred RMSNorm, GDN layer (oracle.gdn),
+full attention with per-head q/k RMSNorm, rotate-half partial RoPE, GQA and a sigmoid output gate,
+SwiGLU MLP, tied LM head.
+
+Weights use the dict layout of trida_stack_amd.model.init_weights ([out, in] projections; the GDN
+in-projection stacks [qkv | z | b | a] rows, the attention one [Hq x (q | gate) | k | v]).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import attention as OA
+from . import gdn as OG
+
+
+def bf(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, zero_centred: bool = True) -> torch.Tensor:
+    y = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps)
+    return bf(y * ((1.0 + w) if zero_centred else w))
+
+
+def rope(x: torch.Tensor, pos: torch.Tensor, rot: int, theta: float) -> torch.Tensor:
+    """Rotate-half RoPE on the first `rot` dims. x [T, H, D], pos [T]."""
+    half = rot // 2
+    i = torch.arange(half, dtype=torch.float32)
+    inv = theta ** (-2.0 * i / rot)
+    ang = pos.float()[:, None] * inv[None, :]                      # [T, half]
+    cs, sn = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+    x1, x2 = x[..., :half], x[..., half:rot]
+    out = x.clone()
+    out[..., :half] = x1 * cs - x2 * sn
+    out[..., half:rot] = x2 * cs + x1 * sn
+    return out
+
+
+@dataclass
+class CpuCache:
+    kv: Dict[int, tuple] = field(default_factory=dict)       # attention layer -> (K [Hkv, L, D], V)
+    state: Dict[int, torch.Tensor] = field(default_factory=dict)   # GDN layer -> [1, Hv, Dv, Dk]
+    window: Dict[int, torch.Tensor] = field(default_factory=dict)  # GDN layer -> [1, Kc-1, C]
+    tokens: List[int] = field(default_factory=list)
+    pending: Optional[dict] = None
+
+    @property
+    def length(self) -> int:
+        return len(self.tokens)
+
+
+class CpuHybrid:
+    def __init__(self, cfg, weights: Dict[str, torch.Tensor]):
+        self.cfg = cfg
+        self.w = {k: v.detach().to("cpu", torch.float32) for k, v in weights.items()}
+        self.mask_id = cfg.mask_id
+
+    def make_cache(self) -> CpuCache:
+        c = self.cfg
+        cache = CpuCache()
+        for i in range(c.n_layers):
+            if c.is_attention(i):
+                cache.kv[i] = (torch.zeros(c.n_kv_heads, 0, c.head_dim), torch.zeros(c.n_kv_heads, 0, c.head_dim))
+            else:
+                cache.state[i] = torch.zeros(1, c.lin_v_heads, c.lin_v_dim, c.lin_k_dim)
+                cache.window[i] = torch.zeros(1, c.conv_kernel - 1, c.conv_dim)
+        return cache
+
+    # ------------------------------------------------------------------ layers
+    def _attention(self, i, x, cache: CpuCache, mode: int, n_clean: int, persist: bool):
+        c, w = self.cfg, self.w
+        p = f"l{i}."
+        T = x.shape[0]
+        D, Hq, Hkv = c.head_dim, c.n_heads, c.n_kv_heads
+        qkv = bf(x @ w[p + "w_qkv"].t())
+        qg = qkv[:, : 2 * Hq * D].reshape(T, Hq, 2 * D)
+        q, gate = qg[..., :D], qg[..., D:]
+        k = qkv[:, 2 * Hq * D: 2 * Hq * D + Hkv * D].reshape(T, Hkv, D)
+        v = qkv[:, 2 * Hq * D + Hkv * D:].reshape(T, Hkv, D)
+        pos = torch.arange(cache.length, cache.length + T)
+        q = bf(rope(rmsnorm(q, w[p + "q_norm"], c.rms_eps), pos, c.rot_dim, c.rope_theta))
+        k = bf(rope(rmsnorm(k, w[p + "k_norm"], c.rms_eps), pos, c.rot_dim, c.rope_theta))
+        K0, V0 = cache.kv[i]
+        Kc = torch.cat([K0, k.transpose(0, 1)], dim=1)
+        Vc = torch.cat([V0, v.transpose(0, 1)], dim=1)
+        if persist:
+            cache.kv[i] = (Kc, Vc)
+        o = OA.canvas_attention(q[None], Kc[None], Vc[None], [cache.length], mode, n_clean, gate=gate[None])[0]
+        return bf(bf(o).reshape(T, -1) @ w[p + "w_o"].t()), (k, v)
+
+    def _gdn(self, i, x, cache: CpuCache, gdn_mode: int, n_clean: int, persist: bool):
+        c, w = self.cfg, self.w
+        p = f"l{i}."
+        T = x.shape[0]
+        C, VD, Hv = c.conv_dim, c.value_dim, c.lin_v_heads
+        proj = bf(x @ w[p + "w_in"].t())
+        xpre = proj[None, :, :C]
+        z = proj[:, C: C + VD]
+        b_in = proj[None, :, C + VD: C + VD + Hv]
+        a_in = proj[None, :, C + VD + Hv: C + VD + 2 * Hv]
+        q, k, v, g, beta, new_win = OG.prep(xpre, cache.window[i], w[p + "conv_w"], a_in, b_in, w[p + "A_log"],
+                                            w[p + "dt_bias"], c.lin_k_heads, Hv, c.lin_k_dim, c.lin_v_dim)
+        if persist:
+            o, s_end, _ = OG.recurrent(q, k, v, g, beta, cache.state[i])
+            cache.state[i] = s_end
+            cache.window[i] = new_win
+            rec = None
+        else:
+            o, _, _ = OG.canvas(q, k, v, g, beta, cache.state[i], n_clean, causal_mode=gdn_mode)
+            rec = (k, v, g, beta, xpre)
+        y = bf(o)[0]                                                   # [T, Hv, Dv]
+        yn = bf(y * torch.rsqrt((y * y).mean(-1, keepdim=True) + c.rms_eps))
+        yn = bf(yn * w[p + "gnorm"] * F.silu(z.reshape(T, Hv, c.lin_v_dim)))
+        return bf(yn.reshape(T, -1) @ w[p + "w_out"].t()), rec
+
+    def forward(self, tokens: List[int], cache: CpuCache, mode: str, n_clean: int = 0) -> torch.Tensor:
+        """mode: causal (persist), verify, canvas (n_clean) or draft. Returns bf16-valued fp32 logits [T, V]."""
+        c, w = self.cfg, self.w
+        persist = mode == "causal"
+        T = len(tokens)
+        att_mode, gdn_mode, nc = {"causal": (0, 1, T), "verify": (0, 1, T), "canvas": (2, 2, n_clean),
+                                  "draft": (1, 2, 1)}[mode]
+        h = w["embed"][torch.as_tensor(tokens)]
+        recs = {}
+        for i in range(c.n_layers):
+            p = f"l{i}."
+            x = rmsnorm(h, w[p + "in_norm"], c.rms_eps)
+            if c.is_attention(i):
+                r, rec = self._attention(i, x, cache, att_mode, nc, persist)
+            else:
+                r, rec = self._gdn(i, x, cache, gdn_mode, nc, persist)
+            recs[i] = rec
+            h = bf(h + r)
+            x = rmsnorm(h, w[p + "post_norm"], c.rms_eps)
+            gu = bf(x @ w[p + "w_gu"].t())
+            I = c.intermediate
+            act = bf(F.silu(gu[:, :I]) * gu[:, I:])
+            h = bf(h + bf(act @ w[p + "w_down"].t()))
+        x = rmsnorm(h, w["final_norm"], c.rms_eps)
+        logits = bf(x @ w["embed"].t())
+        if persist:
+            cache.tokens.extend(tokens)
+        else:
+            cache.pending = {"recs": recs, "tokens": list(tokens)}
+        return logits
+
+    # ------------------------------------------------------------------ reference runtime API
+    def prefill(self, cache: CpuCache, tokens: List[int]) -> torch.Tensor:
+        return self.forward(tokens, cache, "causal")[-1]
+
+    def ar_step(self, cache: CpuCache, tok: int) -> torch.Tensor:
+        return self.forward([tok], cache, "causal")[-1]
+
+    def canvas(self, cache: CpuCache, tokens: List[int], n_clean: int) -> torch.Tensor:
+        return self.forward(tokens, cache, "canvas", n_clean)
+
+    def commit(self, cache: CpuCache, adv: int) -> None:
+        """Keep the first adv rows of the pending block (model.py:486-507)."""
+        rec = cache.pending
+        assert rec is not None and 1 <= adv <= len(rec["tokens"])
+        c = self.cfg
+        for i, r in rec["recs"].items():
+            if c.is_attention(i):
+                k, v = r
+                K0, V0 = cache.kv[i]
+                cache.kv[i] = (torch.cat([K0, k[:adv].transpose(0, 1)], 1), torch.cat([V0, v[:adv].transpose(0, 1)], 1))
+            else:
+                k, v, g, beta, xpre = r
+                st, win = OG.restore(cache.state[i], cache.window[i], k, v, g, beta, xpre, [adv])
+                cache.state[i], cache.window[i] = st, win
+        cache.tokens.extend(rec["tokens"][:adv])
+        cache.pending = None
+
+
+# ---------------------------------------------------------------------- decode loops (greedy)
+def argmax(x: torch.Tensor) -> int:
+    return int(torch.argmax(x))
+
+
+def ar_generate(m: CpuHybrid, prompt: List[int], max_new: int) -> List[int]:
+    """Greedy AR decode (decode.py:273-293)."""
+    cache = m.make_cache()
+    logits = m.prefill(cache, prompt)
+    out = []
+    while True:
+        tok = argmax(logits)
+        out.append(tok)
+        if len(out) >= max_new:
+            return out
+        logits = m.ar_step(cache, tok)
+
+
+def selfspec_generate(m: CpuHybrid, prompt: List[int], max_new: int, n: int = 4):
+    """Greedy self-spec with the bd_bidir_shift canvas (decode.py:297-387): cold start [t0, MASK x 2n-2],
+    verify round [pending, specs, MASK x n-1] with n_clean = n. Returns (tokens, forwards)."""
+    cache = m.make_cache()
+    logits = m.prefill(cache, prompt)
+    blk, K = 2 * n - 1, n - 1
+    t0 = argmax(logits)
+    out, fwd = [], 0
+    t0_emitted = False
+    pending = specs = None
+    while len(out) < max_new:
+        if specs is not None:
+            L = m.canvas(cache, [pending] + specs + [m.mask_id] * (n - 1), n)
+            fwd += 1
+            vals = L.argmax(-1).tolist()
+            acc = 0
+            while acc < K and vals[acc] == specs[acc]:
+                acc += 1
+            if acc < K:
+                m.commit(cache, 1 + acc)
+                out += specs[:acc] + [vals[acc]]
+                t0, t0_emitted, pending, specs = vals[acc], True, None, None
+            else:
+                m.commit(cache, n)
+                out += specs + [vals[n - 1]]
+                pending, specs = vals[n - 1], vals[n:blk]
+        else:
+            L = m.canvas(cache, [t0] + [m.mask_id] * (blk - 1), n)
+            fwd += 1
+            vals = L[:n].argmax(-1).tolist()
+            m.commit(cache, 1)
+            out += ([] if t0_emitted else [t0]) + [vals[0]]
+            t0_emitted = True
+            pending, specs = vals[0], vals[1:n]
+    return out[:max_new], fwd
+
+
+def blockspec_step(m: CpuHybrid, cache: CpuCache, t0: int, block: int, denoise: int):
+    """One draft-then-verify step: `denoise` block-diffusion passes over [t0, MASK x block] (each unmasks
+    the block/denoise most confident MASK slots, shift readout), a token-causal verify pass over
+    [t0, d_1..d_block], greedy acceptance and rollback. Returns (emitted tokens, next t0, n_acc)."""
+    canvas = [t0] + [m.mask_id] * block
+    masked = [True] * block
+    per = [block // denoise + (1 if p < block % denoise else 0) for p in range(denoise)]
+    for p in range(denoise):
+        L = m.forward(canvas, cache, "draft")
+        cache.pending = None
+        probs = torch.softmax(L[:block], dim=-1)
+        conf, am = probs.max(dim=-1)
+        cand = [(float(conf[j]), j) for j in range(block) if masked[j]]
+        cand.sort(key=lambda x: (-x[0], x[1]))
+        for _, j in cand[: per[p]]:
+            canvas[1 + j] = int(am[j])
+            masked[j] = False
+    L = m.forward(canvas, cache, "verify")
+    vals = L.argmax(-1).tolist()
+    acc = 0
+    while acc < block and vals[acc] == canvas[1 + acc]:
+        acc += 1
+    m.commit(cache, 1 + acc)
+    return canvas[1: 1 + acc] + [vals[acc]], vals[acc], acc
+
+
+def blockspec_generate(m: CpuHybrid, prompt: List[int], max_new: int, block: int = 32, denoise: int = 4):
+    """Greedy draft-then-verify decode. The first token comes from the prompt logits; each step emits
+    the accepted drafts plus the bonus token. Returns (tokens, steps)."""
+    cache = m.make_cache()
+    t0 = argmax(m.prefill(cache, prompt))
+    out, steps = [t0], 0
+    while len(out) < max_new:
+        emit, t0, _ = blockspec_step(m, cache, t0, block, denoise)
+        out += emit
+        steps += 1
+    return out[:max_new], steps

@@ -1,0 +1,206 @@
+"""GPU parity of the end-to-end hybrid runtime (tiny config) and of its row-wise kernels against the
+CPU oracle; greedy self-spec == greedy AR on the GPU (lossless property)."""
+import random
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model as OM
+from trida_stack_amd import kernels as K
+from trida_stack_amd.decode import DecodeStats, SamplingParams, ar_generate, selfspec_generate
+from trida_stack_amd.model import HybridConfig, TridaRuntime, build_runtime, init_weights
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+CFG = HybridConfig.tiny()
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def prompt(n, seed=1):
+    rng = random.Random(seed)
+    return [rng.randrange(0, CFG.vocab - 10) for _ in range(n)]
+
+
+# ------------------------------------------------------------------------------ row-wise kernels
+def test_add_rmsnorm(gpu):
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(7, 2560, generator=g).to(torch.bfloat16)
+    r = torch.randn(7, 2560, generator=g).to(torch.bfloat16)
+    w = (torch.randn(2560, generator=g) * 0.1).to(torch.bfloat16)
+    h_ref = OM.bf(x.float() + r.float())
+    y_ref = OM.rmsnorm(h_ref, w.float(), 1e-6)
+    xd, out = x.to(DEV), torch.empty(7, 2560, dtype=torch.bfloat16, device=DEV)
+    K.add_rmsnorm(xd, r.to(DEV), w.to(DEV), out)
+    assert torch.equal(xd.cpu().float(), h_ref)
+    assert rel(out, y_ref) < 1e-2
+
+
+def test_silu_mul_and_gated_norm(gpu):
+    g = torch.Generator().manual_seed(1)
+    gu = torch.randn(5, 2 * 96, generator=g).to(torch.bfloat16)
+    out = torch.empty(5, 96, dtype=torch.bfloat16, device=DEV)
+    K.silu_mul(gu.to(DEV), out)
+    ref = F.silu(gu[:, :96].float()) * gu[:, 96:].float()
+    assert rel(out, ref) < 1e-2
+    o = torch.randn(6, 4, 128, generator=g).to(torch.bfloat16)
+    z = torch.randn(6, 4 * 128 + 16, generator=g).to(torch.bfloat16)
+    w = torch.rand(128, generator=g).to(torch.bfloat16)
+    y = torch.empty_like(o, device=DEV)
+    K.gated_rmsnorm(o.to(DEV), z.to(DEV), w.to(DEV), y)
+    of = o.float()
+    ref = OM.bf(of * torch.rsqrt((of * of).mean(-1, keepdim=True) + 1e-6)) * w.float() * \
+        F.silu(z[:, :512].float().reshape(6, 4, 128))
+    assert rel(y, ref) < 1e-2
+
+
+def test_attn_prep_rope_and_cache_write(gpu):
+    B, T, Hq, Hkv, D, L = 2, 5, 4, 2, 256, 40
+    g = torch.Generator().manual_seed(2)
+    qkv = torch.randn(B, T, (2 * Hq + 2 * Hkv) * D, generator=g).to(torch.bfloat16)
+    qn = (torch.randn(D, generator=g) * 0.1).to(torch.bfloat16)
+    kn = (torch.randn(D, generator=g) * 0.1).to(torch.bfloat16)
+    pos0 = torch.tensor([3, 17], dtype=torch.int32)
+    kc = torch.zeros(B, Hkv, L, D, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    q_out = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=DEV)
+    K.attn_prep(qkv.to(DEV), qn.to(DEV), kn.to(DEV), pos0.to(DEV), pos0.to(DEV), q_out, kc, vc, Hq=Hq, Hkv=Hkv, D=D,
+                rot_dim=64, rope_theta=1e7)
+    for b in range(B):
+        pos = torch.arange(int(pos0[b]), int(pos0[b]) + T)
+        row = qkv[b].float()
+        q = row[:, : 2 * Hq * D].reshape(T, Hq, 2 * D)[..., :D]
+        k = row[:, 2 * Hq * D: 2 * Hq * D + Hkv * D].reshape(T, Hkv, D)
+        v = row[:, 2 * Hq * D + Hkv * D:].reshape(T, Hkv, D)
+        q_ref = OM.rope(OM.rmsnorm(q, qn.float(), 1e-6), pos, 64, 1e7)
+        k_ref = OM.rope(OM.rmsnorm(k, kn.float(), 1e-6), pos, 64, 1e7)
+        p0 = int(pos0[b])
+        assert rel(q_out[b], q_ref) < 1e-2
+        assert rel(kc[b, :, p0: p0 + T].transpose(0, 1), k_ref) < 1e-2
+        assert torch.equal(vc[b, :, p0: p0 + T].transpose(0, 1).cpu().float(), v)
+
+
+@pytest.mark.parametrize("V,dtype", [(248320, torch.bfloat16), (151936, torch.float32), (300, torch.bfloat16)])
+def test_row_argmax_conf(gpu, V, dtype):
+    g = torch.Generator().manual_seed(V)
+    x = (torch.randn(33, V, generator=g) * 3).to(dtype)
+    am, conf = K.row_argmax(x.to(DEV))
+    xf = x.float()
+    assert torch.equal(am.cpu(), xf.argmax(-1))
+    assert rel(conf, torch.softmax(xf, -1).max(-1).values) < 1e-4
+
+
+def test_greedy_accept_bf16_logits(gpu):
+    from oracle import accept as A
+    g = torch.Generator().manual_seed(4)
+    x = (torch.randn(2, 33, 248320, generator=g) * 2).to(torch.bfloat16)
+    am = torch.from_numpy(A.argmax_first(x.float().numpy()))
+    drafts = am[:, :32].clone()
+    drafts[1, 5] = (drafts[1, 5] + 1) % 248320
+    _, n_acc, bonus, _ = K.greedy_accept(x.to(DEV), drafts.to(DEV))
+    ref = A.greedy_accept(x.float().numpy(), drafts.numpy())
+    assert n_acc.cpu().tolist() == ref[1].tolist() == [32, 5]
+    assert bonus.cpu().tolist() == ref[2].tolist()
+
+
+# ------------------------------------------------------------------------------ tiny model
+@pytest.fixture(scope="module")
+def pair():
+    w = init_weights(CFG, seed=0, embed_scale=4.0)
+    return TridaRuntime(CFG, w, device=DEV), OM.CpuHybrid(CFG, w)
+
+
+def test_prefill_and_canvas_match_oracle(gpu, pair):
+    rt, m = pair
+    p = prompt(29)
+    c, co = rt.make_cache(max_len=128), m.make_cache()
+    lg = rt.prefill(c, p)
+    lo = m.prefill(co, p)
+    assert rel(lg, lo) < 2e-2
+    n = 4
+    canvas = prompt(n, seed=5) + [CFG.mask_id] * (n - 1)
+    for mode in ("canvas", "draft", "verify"):
+        ids = torch.tensor([canvas], device=DEV)
+        g = rt.forward(ids, c, mode, n_clean=n)[0]
+        o = m.forward(canvas, co, mode, n_clean=n)
+        co.pending = None
+        assert rel(g, o) < 2e-2, mode
+
+
+def test_commit_matches_ar_state(gpu, pair):
+    rt, _ = pair
+    n = 4
+    p = prompt(17)
+    cont = prompt(n, seed=9)
+    for adv in (1, 3, 4):
+        c = rt.make_cache(max_len=128)
+        rt.prefill(c, p)
+        rt.canvas(c, cont + [CFG.mask_id] * (n - 1), n)
+        rt.commit(c, adv)
+        got = rt.ar_step(c, 42)
+        c2 = rt.make_cache(max_len=128)
+        rt.prefill(c2, p + cont[:adv])
+        ref = rt.ar_step(c2, 42)
+        assert rel(got, ref) < 2e-2, adv
+        assert c.tokens[0] == p + cont[:adv] + [42]
+
+
+def collect(gen):
+    out = []
+    for ch in gen:
+        out.extend(ch)
+    return out
+
+
+def test_greedy_selfspec_equals_ar_gpu(gpu, pair):
+    rt, _ = pair
+    sp = SamplingParams(temperature=0.0)
+    for seed in range(2):
+        p = prompt(25, seed=seed + 10)
+        ar = collect(ar_generate(rt, rt.make_cache(max_len=256), p, max_new_tokens=60, eos_ids=set(), sp=sp))
+        st = DecodeStats()
+        ss = collect(selfspec_generate(rt, rt.make_cache(max_len=256), p, max_new_tokens=60, eos_ids=set(), sp=sp,
+                                       mask_id=CFG.mask_id, n=4, stats=st))
+        assert ss == ar, f"seed {seed}"
+        st2 = DecodeStats()
+        bs = collect(selfspec_generate(rt, rt.make_cache(max_len=256), p, max_new_tokens=60, eos_ids=set(), sp=sp,
+                                       mask_id=CFG.mask_id, n=8, denoise_steps=2, stats=st2))
+        assert bs == ar, f"seed {seed} block"
+
+
+def test_gpu_greedy_tokens_follow_oracle(gpu, pair):
+    """Teacher-forced: the GPU AR logits along the oracle's greedy path stay within tolerance, and the
+    GPU argmax equals the oracle's wherever the oracle's top-2 margin is not a near-tie."""
+    rt, m = pair
+    p = prompt(21, seed=3)
+    toks = OM.ar_generate(m, p, 24)
+    c = rt.make_cache(max_len=128)
+    co = m.make_cache()
+    lg, lo = rt.prefill(c, p), m.prefill(co, p)
+    for t in toks:
+        assert rel(lg, lo) < 3e-2
+        top2 = torch.topk(lo, 2).values
+        if float(top2[0] - top2[1]) > 0.05:
+            assert int(lg.argmax()) == int(lo.argmax())
+        lg, lo = rt.ar_step(c, t), m.ar_step(co, t)
+
+
+def test_four_b_block_step_runs(gpu):
+    """The benchmark model shape: one draft-then-verify step after a short prefill."""
+    from trida_stack_amd.decode import BlockSpecStep
+    cfg = HybridConfig.four_b()
+    rt = build_runtime(cfg, seed=0, device=DEV)
+    c = rt.make_cache(max_len=256)
+    lg = rt.prefill(c, list(range(100, 164)))
+    assert lg.shape == (cfg.vocab,) and torch.isfinite(lg).all()
+    step = BlockSpecStep(rt, c, block=32, denoise=4)
+    step.t0.fill_(int(lg.argmax()))
+    step.run()
+    n = int(step.n_acc[0])
+    assert 0 <= n <= 32 and int(c.length[0]) == 64 + 1 + n
+    del rt
+    torch.cuda.empty_cache()

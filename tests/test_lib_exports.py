@@ -37,9 +37,9 @@ def test_binding_covers_header():
 def test_host_only_entry_points():
     lib = _lib.load()
     assert lib.trida_version() >= 100
-    n = lib.trida_greedy_accept_scratch_bytes(1, 33, 151936, 0)
+    n = lib.trida_greedy_accept_scratch_bytes(1, 33, 151936, 0, 0)
     assert n > 0
     # argument validation happens before any launch: R < K + 1 is rejected with TRIDA_ERR_ARG
-    rc = lib.trida_greedy_accept(1, 1, 4, 10, 40, 10, 1, 4, 4, None, None, None, 1, 1, 1, 1, n, 0, None)
+    rc = lib.trida_greedy_accept(1, 0, 1, 4, 10, 40, 10, 1, 4, 4, None, None, None, 1, 1, 1, 1, n, 0, None)
     assert rc == _lib.TRIDA_ERR_ARG
     assert b"R >= K + 1" in lib.trida_last_error()

@@ -27,8 +27,14 @@ F32 = C.c_float
 SIGNATURES = {
     "trida_version": (C.c_int, []),
     "trida_last_error": (C.c_char_p, []),
-    "trida_greedy_accept_scratch_bytes": (I64, [I64, I64, I64, I64]),
-    "trida_greedy_accept": (C.c_int, [P, I64, I64, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, P, I64, I64, P]),
+    "trida_greedy_accept_scratch_bytes": (I64, [I64, I64, I64, C.c_int, I64]),
+    "trida_greedy_accept": (C.c_int, [P, C.c_int, I64, I64, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, P, I64, I64, P]),
+    "trida_row_argmax_scratch_bytes": (I64, [I64, I64, C.c_int, I64]),
+    "trida_row_argmax": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P, I64, I64, P]),
+    "trida_add_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, I64, F32, C.c_int, P]),
+    "trida_silu_mul": (C.c_int, [P, P, I64, I64, I64, I64, P]),
+    "trida_gated_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, F32, P]),
+    "trida_attn_prep": (C.c_int, [P, I64, P, P, P, P, P, P, P] + [I64] * 7 + [F32, F32, P]),
     "trida_gdn_prep": (C.c_int, [P] * 13 + [I64] * 11 + [P]),
     "trida_gdr_recurrent": (C.c_int, [P] * 9 + [I64] * 6 + [C.c_int, I64, F32, P]),
     "trida_gdn_snapshot": (C.c_int, [P, P, I64, P, P, I64, P]),

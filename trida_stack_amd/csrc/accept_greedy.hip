@@ -49,54 +49,120 @@ __device__ __forceinline__ void take(float x, int ix, bool valid, float& v, int&
 }
 
 struct SplitArgs {
-  const float* logits;
-  int64_t batch_stride, row_stride;
+  const void* logits;
+  int64_t batch_stride, row_stride;  // elements
   int V, R, S, chunk;
   float* pval;
   int* pidx;
+  float* psum;  // sum of exp(x - split max), or null
 };
 
-template <int U, bool kVec>
+template <typename TIn>
+struct Vec;  // one 16-byte load
+template <>
+struct Vec<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void get(const u32x4 w, float* f) {
+    f[0] = __uint_as_float(w.x);
+    f[1] = __uint_as_float(w.y);
+    f[2] = __uint_as_float(w.z);
+    f[3] = __uint_as_float(w.w);
+  }
+  __device__ __forceinline__ static float one(const void* p, int64_t i) { return static_cast<const float*>(p)[i]; }
+};
+template <>
+struct Vec<uint16_t> {  // bf16
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void get(const u32x4 w, float* f) {
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      f[2 * j] = __uint_as_float(ws[j] << 16);
+      f[2 * j + 1] = __uint_as_float(ws[j] & 0xffff0000u);
+    }
+  }
+  __device__ __forceinline__ static float one(const void* p, int64_t i) {
+    return bf2f(static_cast<const uint16_t*>(p)[i]);
+  }
+};
+
+// Online softmax denominator over the elements a thread has seen: s = sum exp(x - m).
+__device__ __forceinline__ void acc_exp(float x, bool valid, float& m, float& s) {
+  if (!valid || x != x) return;
+  if (x > m) {
+    s = s * __expf(m - x) + 1.f;
+    m = x;
+  } else {
+    s += __expf(x - m);
+  }
+}
+
+template <int U, bool kVec, typename TIn, bool kConf>
 __global__ __launch_bounds__(kThreads) void split_argmax_kernel(SplitArgs a) {
+  constexpr int N = Vec<TIn>::N;
   const int s = blockIdx.x, r = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
-  const float* row = a.logits + (int64_t)b * a.batch_stride + (int64_t)r * a.row_stride;
+  const int64_t row_off = (int64_t)b * a.batch_stride + (int64_t)r * a.row_stride;
+  const TIn* row = static_cast<const TIn*>(a.logits) + row_off;
   const int lo = s * a.chunk;
   const int hi = min(a.V, lo + a.chunk);
 
-  float best = -INFINITY;
+  float best = -INFINITY, sm = -INFINITY, ss = 0.f;
   int bi = INT_MAX;
   if (kVec) {
-    // lo is a multiple of 4 and the row start is 16-byte aligned (checked on the host)
-    const f32x4* row4 = reinterpret_cast<const f32x4*>(row + lo);
-    const int n4 = (hi - lo) >> 2;
+    // lo is a multiple of N and the row start is 16-byte aligned (checked on the host)
+    const u32x4* row4 = reinterpret_cast<const u32x4*>(row + lo);
+    const int n4 = (hi - lo) / N;
     for (int base = 0; base < n4; base += kThreads * U) {
-      f32x4 x[U];
+      u32x4 x[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) x[u] = __builtin_nontemporal_load(row4 + min(base + u * kThreads + tid, n4 - 1));
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int j = base + u * kThreads + tid;
         const bool ok = j < n4;
-        const int ix = lo + 4 * j;
-        take(x[u].x, ix, ok, best, bi);
-        take(x[u].y, ix + 1, ok, best, bi);
-        take(x[u].z, ix + 2, ok, best, bi);
-        take(x[u].w, ix + 3, ok, best, bi);
+        const int ix = lo + N * j;
+        float f[N];
+        Vec<TIn>::get(x[u], f);
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          take(f[e], ix + e, ok, best, bi);
+          if (kConf) acc_exp(f[e], ok, sm, ss);
+        }
       }
     }
-    for (int ix = lo + 4 * n4 + tid; ix < hi; ix += kThreads) take(row[ix], ix, true, best, bi);
+    for (int ix = lo + N * n4 + tid; ix < hi; ix += kThreads) {
+      const float f = Vec<TIn>::one(row, ix);
+      take(f, ix, true, best, bi);
+      if (kConf) acc_exp(f, true, sm, ss);
+    }
   } else {
-    for (int ix = lo + tid; ix < hi; ix += kThreads) take(row[ix], ix, true, best, bi);
+    for (int ix = lo + tid; ix < hi; ix += kThreads) {
+      const float f = Vec<TIn>::one(row, ix);
+      take(f, ix, true, best, bi);
+      if (kConf) acc_exp(f, true, sm, ss);
+    }
   }
 
-  __shared__ float sv[kThreads / kWave];
+  __shared__ float sv[kThreads / kWave], sx[kThreads / kWave], sy[kThreads / kWave];
   __shared__ int si[kThreads / kWave];
   wave_argbest(best, bi);
+  if (kConf) {
+    // merge (m, s) pairs across the wave
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float om = __shfl_xor(sm, off, kWave), os = __shfl_xor(ss, off, kWave);
+      const float nm = fmaxf(sm, om);
+      ss = (nm == -INFINITY) ? 0.f : ss * __expf(sm - nm) + os * __expf(om - nm);
+      sm = nm;
+    }
+  }
   const int wave = tid / kWave, lane = tid % kWave;
   if (lane == 0) {
     sv[wave] = best;
     si[wave] = bi;
+    sx[wave] = sm;
+    sy[wave] = ss;
   }
   __syncthreads();
   if (tid == 0) {
@@ -110,6 +176,16 @@ __global__ __launch_bounds__(kThreads) void split_argmax_kernel(SplitArgs a) {
     const int64_t slot = ((int64_t)b * a.R + r) * a.S + s;
     a.pval[slot] = v;
     a.pidx[slot] = i;
+    if (kConf) {
+      float m = sx[0], sum = sy[0];
+      for (int w = 1; w < kThreads / kWave; ++w) {
+        const float nm = fmaxf(m, sx[w]);
+        sum = (nm == -INFINITY) ? 0.f : sum * __expf(m - nm) + sy[w] * __expf(sx[w] - nm);
+        m = nm;
+      }
+      // stored relative to the split's argmax value (the row max is found among these)
+      a.psum[slot] = (m == -INFINITY || v != v) ? 0.f : sum * __expf(m - v);
+    }
   }
 }
 
@@ -202,16 +278,38 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalArgs a) {
   }
 }
 
+// one thread per row: argmax over the splits and the softmax probability of the argmax
+__global__ __launch_bounds__(256) void row_finalize_kernel(const float* pval, const int* pidx, const float* psum,
+                                                           int rows, int S, int64_t* argmax, float* conf) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int64_t base = (int64_t)r * S;
+  float v = pval[base];
+  int i = pidx[base];
+  for (int s = 1; s < S; ++s)
+    if (better(pval[base + s], pidx[base + s], v, i)) {
+      v = pval[base + s];
+      i = pidx[base + s];
+    }
+  if (i == INT_MAX) i = 0;
+  argmax[r] = i;
+  if (conf) {
+    float sum = 0.f;
+    for (int s = 0; s < S; ++s) sum += psum[base + s] * __expf(pval[base + s] - v);
+    conf[r] = sum > 0.f ? 1.f / sum : 0.f;
+  }
+}
+
 // Split a row into chunks of one tile each (kThreads * U float4), U in {4, 8, 16}: the largest U
 // that still gives at least ~512 blocks; callers may force the split count.
-void plan(int64_t B, int64_t R, int64_t V, int64_t splits_req, int64_t* S, int64_t* chunk) {
+void plan(int64_t B, int64_t R, int64_t V, int64_t splits_req, int elems, int64_t* S, int64_t* chunk) {
   int64_t c;
   if (splits_req > 0) {
-    c = align_up(cdiv(V, splits_req), 4);
+    c = align_up(cdiv(V, splits_req), 8);
   } else {
-    c = 4 * kThreads * 4;
+    c = (int64_t)elems * kThreads * 4;
     for (int u = 16; u >= 4; u /= 2) {
-      c = 4 * kThreads * u;
+      c = (int64_t)elems * kThreads * u;
       if (B * R * cdiv(V, c) >= 512) break;
     }
   }
@@ -219,26 +317,69 @@ void plan(int64_t B, int64_t R, int64_t V, int64_t splits_req, int64_t* S, int64
   *S = cdiv(V, c);
 }
 
-int pick_unroll(int64_t chunk) {
-  const int64_t per_thread = cdiv(chunk / 4, kThreads);
+int pick_unroll(int64_t chunk, int elems) {
+  const int64_t per_thread = cdiv(chunk / elems, kThreads);
   return per_thread <= 4 ? 4 : (per_thread <= 8 ? 8 : 16);
 }
 
-int64_t scratch_bytes(int64_t B, int64_t R, int64_t S) { return align_up(B * R * S * 4, 256) * 2; }
+int64_t scratch_bytes(int64_t B, int64_t R, int64_t S) { return align_up(B * R * S * 4, 256) * 3; }
+
+int elems_of(int dtype) { return dtype == 1 ? 8 : 4; }
+
+template <typename TIn, bool kConf>
+int launch_split(const SplitArgs& sa, dim3 grid, bool vec, int64_t chunk, hipStream_t st) {
+  if (!vec) {
+    hipLaunchKernelGGL((split_argmax_kernel<4, false, TIn, kConf>), grid, dim3(kThreads), 0, st, sa);
+  } else {
+    switch (pick_unroll(chunk, Vec<TIn>::N)) {
+      case 4: hipLaunchKernelGGL((split_argmax_kernel<4, true, TIn, kConf>), grid, dim3(kThreads), 0, st, sa); break;
+      case 8: hipLaunchKernelGGL((split_argmax_kernel<8, true, TIn, kConf>), grid, dim3(kThreads), 0, st, sa); break;
+      default: hipLaunchKernelGGL((split_argmax_kernel<16, true, TIn, kConf>), grid, dim3(kThreads), 0, st, sa); break;
+    }
+  }
+  return launch_status("split_argmax");
+}
+
+// shared planning + first launch of greedy_accept and row_argmax
+int run_split(const void* logits, int dtype, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+              int64_t row_stride, bool conf, void* scratch, int64_t scratch_bytes_, int64_t splits, hipStream_t st,
+              int64_t* S_out, float** pval, int** pidx, float** psum) {
+  TRIDA_CHECK(dtype == 0 || dtype == 1, TRIDA_ERR_ARG, "logits dtype must be 0 (fp32) or 1 (bf16)");
+  int64_t S, chunk;
+  plan(B, R, V, splits, elems_of(dtype), &S, &chunk);
+  TRIDA_CHECK(S <= kStage && S <= 65535, TRIDA_ERR_ARG, "at most %d splits per row", kStage);
+  TRIDA_CHECK(scratch_bytes_ >= scratch_bytes(B, R, S), TRIDA_ERR_WORKSPACE, "scratch %lld < %lld bytes",
+              (long long)scratch_bytes_, (long long)scratch_bytes(B, R, S));
+  char* ws = static_cast<char*>(scratch);
+  const int64_t part = align_up(B * R * S * 4, 256);
+  *pval = reinterpret_cast<float*>(ws);
+  *pidx = reinterpret_cast<int*>(ws + part);
+  *psum = reinterpret_cast<float*>(ws + 2 * part);
+  *S_out = S;
+  SplitArgs sa{logits, batch_stride, row_stride, (int)V, (int)R, (int)S, (int)chunk, *pval, *pidx,
+               conf ? *psum : nullptr};
+  const int align = elems_of(dtype);
+  const bool vec = ((reinterpret_cast<uintptr_t>(logits) & 15) == 0) && (row_stride % align == 0) &&
+                   (batch_stride % align == 0) && (chunk % align == 0);
+  const dim3 grid((unsigned)S, (unsigned)R, (unsigned)B);
+  if (dtype == 0)
+    return conf ? launch_split<float, true>(sa, grid, vec, chunk, st) : launch_split<float, false>(sa, grid, vec, chunk, st);
+  return conf ? launch_split<uint16_t, true>(sa, grid, vec, chunk, st) : launch_split<uint16_t, false>(sa, grid, vec, chunk, st);
+}
 
 }  // namespace
 }  // namespace trida
 
 using namespace trida;
 
-extern "C" int64_t trida_greedy_accept_scratch_bytes(int64_t B, int64_t R, int64_t V, int64_t splits) {
+extern "C" int64_t trida_greedy_accept_scratch_bytes(int64_t B, int64_t R, int64_t V, int dtype, int64_t splits) {
   if (B <= 0 || R <= 0 || V <= 0) return 0;
   int64_t S, chunk;
-  plan(B, R, V, splits, &S, &chunk);
+  plan(B, R, V, splits, elems_of(dtype), &S, &chunk);
   return scratch_bytes(B, R, S);
 }
 
-extern "C" int trida_greedy_accept(const float* logits, int64_t B, int64_t R, int64_t V,
+extern "C" int trida_greedy_accept(const void* logits, int dtype, int64_t B, int64_t R, int64_t V,
                                    int64_t batch_stride, int64_t row_stride, const int64_t* drafts,
                                    int64_t K, int64_t draft_stride, const int32_t* n_live,
                                    const int64_t* ctx_len, int64_t* argmax_out, int32_t* n_acc,
@@ -254,34 +395,37 @@ extern "C" int trida_greedy_accept(const float* logits, int64_t B, int64_t R, in
   TRIDA_CHECK(R <= 1024 && B <= 65535, TRIDA_ERR_ARG, "greedy_accept: R <= 1024 and B <= 65535 supported");
   TRIDA_CHECK(K == 0 || drafts, TRIDA_ERR_NULL, "greedy_accept: drafts is NULL with K > 0");
   TRIDA_CHECK(row_stride >= V && batch_stride >= 0, TRIDA_ERR_ARG, "greedy_accept: bad strides");
-  int64_t S, chunk;
-  plan(B, R, V, splits, &S, &chunk);
-  TRIDA_CHECK(S <= kStage && S <= 65535, TRIDA_ERR_ARG, "greedy_accept: at most %d splits per row", kStage);
-  TRIDA_CHECK(scratch_bytes_ >= scratch_bytes(B, R, S), TRIDA_ERR_WORKSPACE,
-              "greedy_accept: scratch %lld < %lld bytes", (long long)scratch_bytes_,
-              (long long)scratch_bytes(B, R, S));
-  char* ws = static_cast<char*>(scratch);
-  float* pval = reinterpret_cast<float*>(ws);
-  int* pidx = reinterpret_cast<int*>(ws + align_up(B * R * S * 4, 256));
   hipStream_t st = static_cast<hipStream_t>(stream);
-
-  SplitArgs sa{logits, batch_stride, row_stride, (int)V, (int)R, (int)S, (int)chunk, pval, pidx};
-  const bool vec = ((reinterpret_cast<uintptr_t>(logits) & 15) == 0) && (row_stride % 4 == 0) &&
-                   (batch_stride % 4 == 0);
-  dim3 grid((unsigned)S, (unsigned)R, (unsigned)B);
-  if (!vec) {
-    hipLaunchKernelGGL((split_argmax_kernel<4, false>), grid, dim3(kThreads), 0, st, sa);
-  } else {
-    switch (pick_unroll(chunk)) {
-      case 4: hipLaunchKernelGGL((split_argmax_kernel<4, true>), grid, dim3(kThreads), 0, st, sa); break;
-      case 8: hipLaunchKernelGGL((split_argmax_kernel<8, true>), grid, dim3(kThreads), 0, st, sa); break;
-      default: hipLaunchKernelGGL((split_argmax_kernel<16, true>), grid, dim3(kThreads), 0, st, sa); break;
-    }
-  }
-  int rc = launch_status("greedy_accept/split_argmax");
+  int64_t S;
+  float *pval, *psum;
+  int* pidx;
+  int rc = run_split(logits, dtype, B, R, V, batch_stride, row_stride, false, scratch, scratch_bytes_, splits, st,
+                     &S, &pval, &pidx, &psum);
   if (rc) return rc;
   FinalArgs fa{pval, pidx, (int)R, (int)S, drafts, draft_stride, (int)K, n_live, ctx_len,
                argmax_out, n_acc, bonus, crop};
   hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)B), dim3(kThreads), 0, st, fa);
   return launch_status("greedy_accept/finalize");
+}
+
+extern "C" int64_t trida_row_argmax_scratch_bytes(int64_t rows, int64_t V, int dtype, int64_t splits) {
+  return trida_greedy_accept_scratch_bytes(1, rows, V, dtype, splits);
+}
+
+extern "C" int trida_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride,
+                                int64_t* argmax, float* conf, void* scratch, int64_t scratch_bytes_, int64_t splits,
+                                void* stream) {
+  TRIDA_CHECK(logits && argmax && scratch, TRIDA_ERR_NULL, "row_argmax: logits, argmax and scratch are required");
+  TRIDA_CHECK(rows > 0 && rows <= 65535 && V > 0 && V < INT_MAX && row_stride >= V, TRIDA_ERR_ARG,
+              "row_argmax: bad sizes");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int64_t S;
+  float *pval, *psum;
+  int* pidx;
+  int rc = run_split(logits, dtype, 1, rows, V, 0, row_stride, conf != nullptr, scratch, scratch_bytes_, splits, st,
+                     &S, &pval, &pidx, &psum);
+  if (rc) return rc;
+  hipLaunchKernelGGL(row_finalize_kernel, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, st, pval, pidx, psum,
+                     (int)rows, (int)S, argmax, conf);
+  return launch_status("row_argmax/finalize");
 }

@@ -1,0 +1,272 @@
+"""Decoders on MI355X: autoregressive baseline and self-speculative decoding.
+
+Mirrors inference/zoro-1/mlx/trida_mlx/decode.py (SamplingParams, DecodeStats, ar_generate,
+selfspec_generate; decode.py:35-387) over the GPU runtime of trida_stack_amd.model:
+
+  selfspec_generate(..., n, denoise_steps=0)   the reference canvas algorithm (bd_bidir_shift):
+      cold start [t0, MASK x (2n-2)]; verify round [pending, spec_1..spec_{n-1}, MASK x (n-1)] with
+      n_clean = n; spec_i verified against row i; all accepted -> clean = row n-1, new specs = rows
+      n..2n-2; reject at i -> emit the accepted specs + correction, next step cold.
+  selfspec_generate(..., n, denoise_steps=D)   draft-then-verify over a block of n: D block-diffusion
+      passes over [t0, MASK x n] (each unmasks the most confident MASK slots, shift readout), then a
+      token-causal verify pass over [t0, d_1..d_n], greedy acceptance and rollback of the hybrid state
+      (KV crop + GDN restore to 1 + n_acc rows).
+
+Acceptance runs in the fused gfx950 kernels (greedy: split-V argmax + wave prefix scan); the host
+syncs once per step to emit tokens. Greedy decoding is lossless w.r.t. ar_generate up to bf16
+numerics (the verify rows are the AR computation).
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Iterator, List, Optional
+
+import torch
+
+from . import kernels as K
+from .model import SeqCache, TridaRuntime
+
+
+@dataclass
+class SamplingParams:
+    temperature: float = 1.0
+    top_k: int = 50
+    top_p: float = 0.95
+    seed: Optional[int] = None
+
+    @property
+    def greedy(self) -> bool:
+        return self.temperature <= 0
+
+
+@dataclass
+class DecodeStats:
+    mode: str = ""
+    prompt_tokens: int = 0
+    reused_tokens: int = 0
+    new_tokens: int = 0
+    forwards: int = 0
+    cold_forwards: int = 0
+    steps: int = 0
+    accept_hist: list = field(default_factory=list)
+    prefill_s: float = 0.0
+    decode_s: float = 0.0
+    finish_reason: str = "length"
+    stop_token: Optional[int] = None
+
+    @property
+    def tokens_per_forward(self) -> float:
+        return self.new_tokens / self.forwards if self.forwards else 0.0
+
+    @property
+    def decode_tps(self) -> float:
+        return self.new_tokens / self.decode_s if self.decode_s else 0.0
+
+    def as_dict(self) -> dict:
+        return {"mode": self.mode, "prompt_tokens": self.prompt_tokens, "reused_tokens": self.reused_tokens,
+                "new_tokens": self.new_tokens, "forwards": self.forwards, "cold_forwards": self.cold_forwards,
+                "steps": self.steps, "tokens_per_forward": round(self.tokens_per_forward, 3),
+                "accept_hist": self.accept_hist, "prefill_s": round(self.prefill_s, 4),
+                "decode_s": round(self.decode_s, 4), "decode_tok_s": round(self.decode_tps, 2),
+                "finish_reason": self.finish_reason}
+
+
+class _Emitter:
+    """Applies max_new_tokens / EOS to emitted chunks and records stats (decode.py:228-257)."""
+
+    def __init__(self, stats: DecodeStats, max_new: int, eos: set):
+        self.stats, self.max_new, self.eos, self.done = stats, max_new, eos, False
+
+    def __call__(self, toks: list) -> list:
+        out = []
+        for t in toks:
+            if t in self.eos:
+                self.done = True
+                self.stats.finish_reason = "stop"
+                self.stats.stop_token = t
+                break
+            out.append(t)
+            if self.stats.new_tokens + len(out) >= self.max_new:
+                self.done = True
+                self.stats.finish_reason = "length"
+                break
+        self.stats.new_tokens += len(out)
+        return out
+
+
+def _argmax1(logits: torch.Tensor) -> int:
+    am, _ = K.row_argmax(logits.reshape(1, -1), want_conf=False)
+    return int(am[0])
+
+
+def _prefill(rt: TridaRuntime, cache: SeqCache, prompt: list, stats: DecodeStats) -> torch.Tensor:
+    t = time.perf_counter()
+    todo = prompt[len(cache.tokens[0]):]
+    stats.prompt_tokens, stats.reused_tokens = len(prompt), len(cache.tokens[0])
+    if not todo:
+        raise ValueError("prompt fully cached; callers must leave at least one token to prefill")
+    logits = rt.prefill(cache, todo)
+    torch.cuda.synchronize(rt.dev)
+    stats.prefill_s = time.perf_counter() - t
+    return logits
+
+
+def _need_greedy(sp: SamplingParams) -> None:
+    if not sp.greedy:
+        raise NotImplementedError("sampled decoding runs through trida_stack_amd.sampling.spec_sample_generate")
+
+
+# ----------------------------------------------------------------------------- AR
+def ar_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
+                sp: SamplingParams, stats: Optional[DecodeStats] = None) -> Iterator[list]:
+    """Greedy causal decoding (decode.py:273-293)."""
+    _need_greedy(sp)
+    stats = stats or DecodeStats()
+    stats.mode = "causal"
+    logits = _prefill(rt, cache, prompt, stats)
+    emit = _Emitter(stats, max_new_tokens, eos_ids)
+    t = time.perf_counter()
+    while True:
+        tok = _argmax1(logits)
+        out = emit([tok])
+        if out:
+            yield out
+        if emit.done:
+            break
+        logits = rt.ar_step(cache, tok)
+        stats.forwards += 1
+    stats.decode_s = time.perf_counter() - t
+
+
+# ----------------------------------------------------------------------------- self-spec
+def selfspec_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
+                      sp: SamplingParams, mask_id: int, n: int = 4, stats: Optional[DecodeStats] = None,
+                      denoise_steps: int = 0) -> Iterator[list]:
+    """Self-speculative decoding (decode.py:297-387); see the module docstring for the two variants."""
+    _need_greedy(sp)
+    if denoise_steps > 0:
+        yield from _blockspec(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids, mask_id=mask_id,
+                              block=n, denoise=denoise_steps, stats=stats)
+        return
+    stats = stats or DecodeStats()
+    stats.mode = f"self-spec(N={n})"
+    stats.accept_hist = [0] * n
+    blk, Kd = 2 * n - 1, n - 1
+    logits = _prefill(rt, cache, prompt, stats)
+    emit = _Emitter(stats, max_new_tokens, eos_ids)
+    t_start = time.perf_counter()
+    t0 = _argmax1(logits)
+    t0_emitted = False
+    pending = specs = None
+    dev = rt.dev
+    while not emit.done:
+        if specs is not None:  # ---- verify round
+            L = rt.canvas(cache, [pending] + specs + [mask_id] * (n - 1), n, as_float=False)
+            stats.forwards += 1
+            drafts = torch.as_tensor([specs], dtype=torch.int64, device=dev)
+            am, n_acc, _, _ = K.greedy_accept(L[None], drafts)
+            vals = am[0].tolist()
+            acc = int(n_acc[0])
+            if acc < Kd:  # rejected at spec `acc`: emit accepted specs + correction, next step cold
+                rt.commit(cache, 1 + acc)
+                stats.accept_hist[acc] += 1
+                out = emit(specs[:acc] + [vals[acc]])
+                t0, t0_emitted = vals[acc], True
+                pending = specs = None
+            else:  # all accepted: n tokens this forward
+                rt.commit(cache, n)
+                stats.accept_hist[Kd] += 1
+                out = emit(specs + [vals[n - 1]])
+                pending, specs = vals[n - 1], vals[n:blk]
+        else:  # ---- cold start
+            L = rt.canvas(cache, [t0] + [mask_id] * (blk - 1), n, rows=n if rt.skip_rows else None, as_float=False)
+            stats.forwards += 1
+            stats.cold_forwards += 1
+            am, _ = K.row_argmax(L[:n], want_conf=False)
+            vals = am.tolist()
+            rt.commit(cache, 1)
+            out = emit(([] if t0_emitted else [t0]) + [vals[0]])
+            t0_emitted = True
+            pending, specs = vals[0], vals[1:n]
+        if out:
+            yield out
+    stats.decode_s = time.perf_counter() - t_start
+
+
+class BlockSpecStep:
+    """One batched draft-then-verify step on device buffers of fixed shape (so a whole step can be
+    replayed from a HIP graph): denoise passes, verify, greedy acceptance, rollback.
+
+    Inputs: t0 [B] int64 (the pending token, already emitted). Outputs after run(): canvas [B, block+1]
+    (row 0 = t0, rows 1.. = drafts), n_acc [B] int32, bonus [B] int64 (next t0)."""
+
+    def __init__(self, rt: TridaRuntime, cache: SeqCache, block: int, denoise: int):
+        self.rt, self.cache, self.block, self.denoise = rt, cache, block, denoise
+        B = cache.B
+        dev = rt.dev
+        self.per = [block // denoise + (1 if p < block % denoise else 0) for p in range(denoise)]
+        self.t0 = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.canvas = torch.full((B, block + 1), rt.mask_id, dtype=torch.int64, device=dev)
+        self.masked = torch.ones(B, block, dtype=torch.bool, device=dev)
+        self.ctx = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.n_keep = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.am = torch.empty(B, block + 1, dtype=torch.int64, device=dev)
+        self.n_acc = torch.empty(B, dtype=torch.int32, device=dev)
+        self.bonus = torch.empty(B, dtype=torch.int64, device=dev)
+        self.crop = torch.empty(B, dtype=torch.int64, device=dev)
+        self.d_am = torch.empty(B, block + 1, dtype=torch.int64, device=dev)
+        self.d_conf = torch.empty(B, block + 1, dtype=torch.float32, device=dev)
+        self.neg = torch.full((B, block), float("-inf"), dtype=torch.float32, device=dev)
+
+    def run(self) -> None:
+        rt, cache, blk = self.rt, self.cache, self.block
+        self.canvas.fill_(rt.mask_id)
+        self.canvas[:, 0] = self.t0
+        self.masked.fill_(True)
+        for p in range(self.denoise):
+            L = rt.forward(self.canvas, cache, "draft")
+            # row j predicts slot j + 1 (shift readout); the last row is not used
+            K.row_argmax(L, out=(self.d_am, self.d_conf))
+            score = torch.where(self.masked, self.d_conf[:, :blk], self.neg)
+            # the per[p] most confident MASK slots (ties: the lower slot first)
+            pos = torch.sort(score, dim=1, descending=True, stable=True).indices[:, : self.per[p]]
+            self.canvas.scatter_(1, pos + 1, self.d_am[:, :blk].gather(1, pos))
+            self.masked.scatter_(1, pos, False)
+        L = rt.forward(self.canvas, cache, "verify")
+        self.ctx.copy_(cache.length)
+        K.greedy_accept(L, self.canvas[:, 1:], ctx_len=self.ctx, out=(self.am, self.n_acc, self.bonus, self.crop))
+        torch.add(self.n_acc, 1, out=self.n_keep)
+        cache.pending = {"T": blk + 1}
+        rt.commit(cache, self.n_keep)
+        self.t0.copy_(self.bonus)
+
+
+def _blockspec(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
+               mask_id: int, block: int, denoise: int, stats: Optional[DecodeStats]) -> Iterator[list]:
+    stats = stats or DecodeStats()
+    stats.mode = f"self-spec(block={block}, denoise={denoise})"
+    stats.accept_hist = [0] * (block + 1)
+    logits = _prefill(rt, cache, prompt, stats)
+    emit = _Emitter(stats, max_new_tokens, eos_ids)
+    t_start = time.perf_counter()
+    step = BlockSpecStep(rt, cache, block, denoise)
+    t0 = _argmax1(logits)
+    out = emit([t0])
+    if out:
+        yield out
+    step.t0.fill_(t0)
+    while not emit.done:
+        step.run()
+        stats.forwards += denoise + 1
+        stats.steps += 1
+        packed = torch.cat([step.canvas[0, 1:], step.bonus[:1], step.n_acc[:1].to(torch.int64)]).tolist()
+        acc = packed[-1]
+        cache.tokens[0].extend([t0] + packed[:acc])  # the committed rows: pending token + accepted drafts
+        stats.accept_hist[acc] += 1
+        chunk = packed[:acc] + [packed[block]]
+        t0 = packed[block]
+        out = emit(chunk)
+        if out:
+            yield out
+    stats.decode_s = time.perf_counter() - t_start

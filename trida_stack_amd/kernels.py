@@ -56,8 +56,17 @@ workspaces = _Workspaces()
 
 
 # --------------------------------------------------------------------------------------------------
+def _logit_dtype(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return 0
+    if t.dtype == torch.bfloat16:
+        return 1
+    raise ValueError(f"logits must be fp32 or bf16 (got {t.dtype})")
+
+
 def greedy_accept(logits: torch.Tensor, drafts: torch.Tensor, n_live: Optional[torch.Tensor] = None,
-                  ctx_len: Optional[torch.Tensor] = None, *, want_argmax: bool = True, splits: int = 0):
+                  ctx_len: Optional[torch.Tensor] = None, *, want_argmax: bool = True, splits: int = 0,
+                  out=None):
     """Greedy acceptance over verify logits (split-V argmax + per-sequence scan, one call).
 
     Semantics of TridaDiffusionSampler._selfspec_step's greedy branch
@@ -65,12 +74,14 @@ def greedy_accept(logits: torch.Tensor, drafts: torch.Tensor, n_live: Optional[t
     (first index on ties), ``match = (am[:, :K] == drafts) & (j < n_live)``, ``n_acc`` = length of the
     leading run of matches, ``bonus = am[n_acc]`` and ``crop = ctx_len + 1 + n_acc``.
 
-    logits [B, R, V] fp32 (last dim contiguous), drafts [B, K] int64 with R >= K + 1.
-    Returns (argmax [B, R] int64 or None, n_acc [B] int32, bonus [B] int64, crop [B] int64).
+    logits [B, R, V] fp32 or bf16 (last dim contiguous), drafts [B, K] int64 with R >= K + 1.
+    out: optional preallocated (argmax [B,R] int64 or None, n_acc [B] int32, bonus [B] int64,
+    crop [B] int64). Returns that tuple.
     """
     dev = _need_gpu(logits, drafts, n_live, ctx_len)
-    if logits.dtype != torch.float32 or logits.dim() != 3 or logits.stride(2) != 1:
-        raise ValueError("logits must be fp32 [B, R, V] with a contiguous last dim")
+    dt = _logit_dtype(logits)
+    if logits.dim() != 3 or logits.stride(2) != 1:
+        raise ValueError("logits must be [B, R, V] with a contiguous last dim")
     B, R, V = logits.shape
     if drafts.dtype != torch.int64 or drafts.dim() != 2 or drafts.shape[0] != B or drafts.stride(1) != 1:
         raise ValueError("drafts must be int64 [B, K] with a contiguous last dim")
@@ -82,17 +93,40 @@ def greedy_accept(logits: torch.Tensor, drafts: torch.Tensor, n_live: Optional[t
     if ctx_len is not None and (ctx_len.dtype != torch.int64 or ctx_len.shape != (B,) or not ctx_len.is_contiguous()):
         raise ValueError("ctx_len must be int64 [B]")
     lib = _lib.load()
-    am = torch.empty((B, R), dtype=torch.int64, device=dev) if want_argmax else None
-    n_acc = torch.empty(B, dtype=torch.int32, device=dev)
-    bonus = torch.empty(B, dtype=torch.int64, device=dev)
-    crop = torch.empty(B, dtype=torch.int64, device=dev)
-    scr = workspaces.get(dev, "greedy_accept", lib.trida_greedy_accept_scratch_bytes(B, R, V, splits))
+    if out is None:
+        am = torch.empty((B, R), dtype=torch.int64, device=dev) if want_argmax else None
+        out = (am, torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
+               torch.empty(B, dtype=torch.int64, device=dev))
+    am, n_acc, bonus, crop = out
+    scr = workspaces.get(dev, "argmax", lib.trida_greedy_accept_scratch_bytes(B, R, V, dt, splits))
     rc = lib.trida_greedy_accept(
-        logits.data_ptr(), B, R, V, logits.stride(0), logits.stride(1), _ptr(drafts), K,
+        logits.data_ptr(), dt, B, R, V, logits.stride(0), logits.stride(1), _ptr(drafts), K,
         drafts.stride(0), _ptr(n_live), _ptr(ctx_len), _ptr(am), n_acc.data_ptr(), bonus.data_ptr(),
         crop.data_ptr(), scr.data_ptr(), scr.numel(), splits, _stream(dev))
     _lib.check(rc, "trida_greedy_accept")
-    return am, n_acc, bonus, crop
+    return out
+
+
+def row_argmax(logits: torch.Tensor, *, want_conf: bool = True, splits: int = 0, out=None):
+    """Per-row argmax (first index on ties) and softmax probability of the argmax.
+    logits [..., V] fp32 or bf16 with contiguous rows. Returns (argmax int64, conf fp32 or None)."""
+    dev = _need_gpu(logits)
+    dt = _logit_dtype(logits)
+    V = logits.shape[-1]
+    x = logits.reshape(-1, V)
+    if x.stride(1) != 1:
+        raise ValueError("logits rows must be contiguous")
+    rows = x.shape[0]
+    lib = _lib.load()
+    if out is None:
+        out = (torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev),
+               torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev) if want_conf else None)
+    am, conf = out
+    scr = workspaces.get(dev, "argmax", lib.trida_row_argmax_scratch_bytes(rows, V, dt, splits))
+    rc = lib.trida_row_argmax(x.data_ptr(), dt, rows, V, x.stride(0), am.data_ptr(), _ptr(conf), scr.data_ptr(),
+                              scr.numel(), splits, _stream(dev))
+    _lib.check(rc, "trida_row_argmax")
+    return out
 
 
 # --------------------------------------------------------------------------------------------------
@@ -109,7 +143,7 @@ def _f32(t: torch.Tensor, name: str):
 
 def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
              A_log: torch.Tensor, dt_bias: torch.Tensor, *, Hk: int, Hv: int, Dk: int, Dv: int,
-             window_out: Optional[torch.Tensor] = None):
+             window_out: Optional[torch.Tensor] = None, out=None):
     """Conv + SiLU + split + l2norm(q, k) + gates for a block of rows (one launch).
 
     x [B, T, C] bf16 (last dim contiguous, C = 2*Hk*Dk + Hv*Dv; batch / row strides may be larger),
@@ -133,11 +167,17 @@ def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: tor
     if window_out is not None and (window_out.shape != window.shape or not window_out.is_contiguous()
                                    or window_out.data_ptr() == window.data_ptr()):
         raise ValueError("window_out must be a separate contiguous [B, Kc-1, C] buffer")
-    q = torch.empty((B, T, Hk, Dk), dtype=torch.bfloat16, device=dev)
-    k = torch.empty_like(q)
-    v = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
-    g = torch.empty((B, T, Hv), dtype=torch.float32, device=dev)
-    beta = torch.empty_like(g)
+    if out is None:
+        q = torch.empty((B, T, Hk, Dk), dtype=torch.bfloat16, device=dev)
+        k = torch.empty_like(q)
+        v = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+        g = torch.empty((B, T, Hv), dtype=torch.float32, device=dev)
+        beta = torch.empty_like(g)
+    else:
+        q, k, v, g, beta = out
+        if q.shape != (B, T, Hk, Dk) or k.shape != q.shape or v.shape != (B, T, Hv, Dv) or g.shape != (B, T, Hv) \
+                or beta.shape != g.shape or not all(t.is_contiguous() for t in out):
+            raise ValueError("gdn_prep: out buffers have the wrong shape")
     rc = _lib.load().trida_gdn_prep(
         x.data_ptr(), window.data_ptr(), conv_w.data_ptr(), a.data_ptr(), b.data_ptr(),
         A_log.contiguous().data_ptr(), dt_bias.contiguous().data_ptr(), q.data_ptr(), k.data_ptr(),
@@ -150,7 +190,7 @@ def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: tor
 def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                   state: torch.Tensor, *, causal_mode: int = 1, num_clean: Optional[int] = None,
                   state_out: Optional[torch.Tensor] = None, want_clean: bool = False,
-                  scale: Optional[float] = None):
+                  scale: Optional[float] = None, out: Optional[torch.Tensor] = None):
     """Gated delta rule over T rows with the block-causal readout (one launch).
 
     q, k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g (log decay), beta [B,T,Hv] fp32, state [B,Hv,Dv,Dk]
@@ -175,7 +215,10 @@ def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                                   or not state_out.is_contiguous()):
         raise ValueError("state_out must match state")
     nc = T if num_clean is None else int(num_clean)
-    out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    if out is None:
+        out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    elif out.shape != (B, T, Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("gdr_recurrent: out must be contiguous bf16 [B, T, Hv, Dv]")
     clean = torch.empty_like(state) if want_clean else None
     sc = Dk ** -0.5 if scale is None else float(scale)
     rc = _lib.load().trida_gdr_recurrent(
@@ -306,3 +349,55 @@ def attn_canvas(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, p
                                n_clean, sc, mk, splits, scr.data_ptr(), scr.numel(), _stream(dev))
     _lib.check(rc, "trida_attn_canvas")
     return out
+
+
+# --------------------------------------------------------------------------------------------------
+# row-wise decoder kernels
+def add_rmsnorm(x: torch.Tensor, r: Optional[torch.Tensor], w: torch.Tensor, out: torch.Tensor, *,
+                eps: float = 1e-6, zero_centred: bool = True) -> torch.Tensor:
+    """x += r (in place, bf16 residual stream; r may be None), out = rmsnorm(x) * (1 + w) (or * w).
+    x, r, out: [rows, dim] bf16 with contiguous rows; w [dim] bf16."""
+    dev = _need_gpu(x, r, w, out)
+    rows, dim = x.shape
+    rc = _lib.load().trida_add_rmsnorm(x.data_ptr(), _ptr(r), w.data_ptr(), out.data_ptr(), rows, dim, x.stride(0),
+                                       r.stride(0) if r is not None else 0, out.stride(0), eps, int(zero_centred),
+                                       _stream(dev))
+    _lib.check(rc, "trida_add_rmsnorm")
+    return out
+
+
+def silu_mul(gu: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out = silu(gu[:, :I]) * gu[:, I:] for gu [rows, 2I] bf16."""
+    dev = _need_gpu(gu, out)
+    rows, two_i = gu.shape
+    rc = _lib.load().trida_silu_mul(gu.data_ptr(), out.data_ptr(), rows, two_i // 2, gu.stride(0), out.stride(0),
+                                    _stream(dev))
+    _lib.check(rc, "trida_silu_mul")
+    return out
+
+
+def gated_rmsnorm(o: torch.Tensor, z: torch.Tensor, w: torch.Tensor, out: torch.Tensor, *, eps: float = 1e-6):
+    """Per value head: out = bf16(rmsnorm(o)) * w * silu(z). o, out [rows, H, Dv] contiguous bf16;
+    z [rows, >= H*Dv] bf16 with contiguous rows; w [Dv] bf16."""
+    dev = _need_gpu(o, z, w, out)
+    rows, H, Dv = o.shape
+    rc = _lib.load().trida_gated_rmsnorm(o.data_ptr(), z.data_ptr(), w.data_ptr(), out.data_ptr(), rows, H, Dv,
+                                         z.stride(0), eps, _stream(dev))
+    _lib.check(rc, "trida_gated_rmsnorm")
+    return out
+
+
+def attn_prep(qkv: torch.Tensor, q_norm_w: torch.Tensor, k_norm_w: torch.Tensor, pos0: torch.Tensor,
+              slot0: torch.Tensor, q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *,
+              Hq: int, Hkv: int, D: int, rot_dim: int, rope_theta: float, eps: float = 1e-6) -> None:
+    """Per-head q/k RMSNorm + partial RoPE; q to q_out [B, T, Hq, D], k / v into the caches
+    [B, Hkv, Lmax, D] at slots slot0[b] + t. qkv [B, T, >= (2Hq + 2Hkv) D] bf16 with packed rows."""
+    dev = _need_gpu(qkv, q_norm_w, k_norm_w, pos0, slot0, q_out, k_cache, v_cache)
+    B, T = qkv.shape[0], qkv.shape[1]
+    if qkv.stride(0) != T * qkv.stride(1) or qkv.stride(2) != 1:
+        raise ValueError("qkv rows must be packed")
+    rc = _lib.load().trida_attn_prep(qkv.data_ptr(), qkv.stride(1), q_norm_w.data_ptr(), k_norm_w.data_ptr(),
+                                     pos0.data_ptr(), slot0.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(),
+                                     v_cache.data_ptr(), B, T, Hq, Hkv, D, k_cache.shape[2], rot_dim, rope_theta,
+                                     eps, _stream(dev))
+    _lib.check(rc, "trida_attn_prep")

@@ -1,0 +1,403 @@
+"""Hybrid Qwen3.5-style decoder (gated-delta + full attention) on MI355X, with the forwards the
+self-speculative decoder needs.
+
+Mirrors the reference runtime API of inference/zoro-1/mlx/trida_mlx/model.py:
+  make_cache() / prefill(cache, tokens) / ar_step(cache, tok) / canvas(cache, tokens, n_clean, rows)
+  / commit(cache, adv)                                                          (model.py:245-507)
+plus draft(cache, tokens), the block-diffusion denoising pass (MASK rows see the whole block).
+
+Every hot op runs in a gfx950 kernel of libtrida_hip.so (attention, GDN conv/prep/recurrence/readout,
+rollback, norms, SwiGLU, acceptance); the projections, MLP and LM head are torch GEMMs (hipBLASLt).
+Caches are batched device tensors: KV [A, B, Hkv, Lmax, D] bf16, GDN state [L, B, Hv, Dv, Dk] fp32 and
+conv window [L, B, Kc-1, C] bf16 (A / L = number of attention / GDN layers). Per-sequence lengths and
+RoPE positions live on the device, so every forward of a given (B, T, mode) has fixed launch shapes
+and can be captured in a HIP graph.
+
+Forward modes (reference semantics):
+  causal  token-causal rows, state persisted (prefill / AR step)
+  verify  token-causal rows, nothing persisted; commit(adv) keeps the first adv rows
+  canvas  rows < n_clean token-causal, later rows see the whole block (attention) and read the
+          block-end GDN state (causal_mode 2, num_clean)                        (model.py:461-484)
+  draft   the denoising pass: every row sees the whole block in attention, GDN rows >= 1 read the
+          block-end state (causal_mode 2, num_clean 1)
+"""
+from __future__ import annotations
+
+import json
+import math
+from dataclasses import asdict, dataclass, field
+from typing import Dict, List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import kernels as K
+
+DEFAULT_MASK_ID = 248077
+
+
+@dataclass
+class HybridConfig:
+    hidden: int = 2560
+    n_layers: int = 32
+    full_attention_interval: int = 4     # layer i is full attention when (i + 1) % interval == 0
+    intermediate: int = 9728
+    vocab: int = 248320
+    lin_k_heads: int = 16
+    lin_v_heads: int = 16
+    lin_k_dim: int = 128
+    lin_v_dim: int = 128
+    conv_kernel: int = 4
+    n_heads: int = 16
+    n_kv_heads: int = 4
+    head_dim: int = 256
+    rotary_frac: float = 0.25
+    rope_theta: float = 1.0e7
+    rms_eps: float = 1e-6
+    mask_id: int = DEFAULT_MASK_ID
+    tie_embeddings: bool = True
+
+    @property
+    def conv_dim(self) -> int:
+        return 2 * self.lin_k_heads * self.lin_k_dim + self.lin_v_heads * self.lin_v_dim
+
+    @property
+    def value_dim(self) -> int:
+        return self.lin_v_heads * self.lin_v_dim
+
+    @property
+    def rot_dim(self) -> int:
+        return int(self.head_dim * self.rotary_frac)
+
+    def is_attention(self, i: int) -> bool:
+        return (i + 1) % self.full_attention_interval == 0
+
+    @classmethod
+    def four_b(cls) -> "HybridConfig":
+        """The 4B-shape hybrid of the end-to-end benchmark: hidden 2560, 32 layers (24 GDN + 8 attention),
+        GDN 16 key / 16 value heads of 128, attention 16 q / 4 kv heads of 256, FFN 9728, vocab 248320."""
+        return cls()
+
+    @classmethod
+    def tiny(cls, vocab: int = 300) -> "HybridConfig":
+        """A small configuration for tests (kernel-supported head sizes)."""
+        return cls(hidden=128, n_layers=8, intermediate=256, vocab=vocab, lin_k_heads=2, lin_v_heads=4,
+                   lin_k_dim=32, lin_v_dim=64, n_heads=4, n_kv_heads=2, head_dim=64, rope_theta=10000.0,
+                   mask_id=vocab - 1)
+
+    def n_params(self) -> int:
+        h, I = self.hidden, self.intermediate
+        gdn = h * (self.conv_dim + self.value_dim + 2 * self.lin_v_heads) + self.value_dim * h
+        attn = h * (2 * self.n_heads + 2 * self.n_kv_heads) * self.head_dim + self.n_heads * self.head_dim * h
+        mlp = 3 * h * I
+        n_attn = sum(self.is_attention(i) for i in range(self.n_layers))
+        return self.vocab * h + (self.n_layers - n_attn) * gdn + n_attn * attn + self.n_layers * mlp
+
+
+def init_weights(cfg: HybridConfig, seed: int = 0, device="cpu", dtype=torch.bfloat16,
+                 embed_scale: float = 1.0) -> Dict[str, torch.Tensor]:
+    """Random weights of the hybrid architecture (normal(0, 0.02) projections, zero-centred norms at 0,
+    gated norm at 1, A_log = log U(1, 16), dt_bias = 1), in the [out, in] layout of torch Linear.
+    embed_scale sharpens the tied embedding (tests use it to give greedy decoding structure)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    h, I = cfg.hidden, cfg.intermediate
+
+    def nrm(*shape, std=0.02):
+        return (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std).to(dtype)
+
+    w: Dict[str, torch.Tensor] = {"embed": (nrm(cfg.vocab, h).float() * embed_scale).to(dtype),
+                                  "final_norm": torch.zeros(h, device=device, dtype=dtype)}
+    for i in range(cfg.n_layers):
+        p = f"l{i}."
+        w[p + "in_norm"] = torch.zeros(h, device=device, dtype=dtype)
+        w[p + "post_norm"] = torch.zeros(h, device=device, dtype=dtype)
+        w[p + "w_gu"] = nrm(2 * I, h)
+        w[p + "w_down"] = nrm(h, I)
+        if cfg.is_attention(i):
+            w[p + "w_qkv"] = nrm((2 * cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim, h)
+            w[p + "q_norm"] = torch.zeros(cfg.head_dim, device=device, dtype=dtype)
+            w[p + "k_norm"] = torch.zeros(cfg.head_dim, device=device, dtype=dtype)
+            w[p + "w_o"] = nrm(h, cfg.n_heads * cfg.head_dim)
+        else:
+            w[p + "w_in"] = nrm(cfg.conv_dim + cfg.value_dim + 2 * cfg.lin_v_heads, h)
+            bound = 1.0 / math.sqrt(cfg.conv_kernel)
+            w[p + "conv_w"] = ((torch.rand(cfg.conv_dim, cfg.conv_kernel, generator=g, device=device) * 2 - 1)
+                               * bound).to(dtype)
+            w[p + "A_log"] = torch.log(torch.rand(cfg.lin_v_heads, generator=g, device=device) * 15 + 1)
+            w[p + "dt_bias"] = torch.ones(cfg.lin_v_heads, device=device, dtype=torch.float32)
+            w[p + "gnorm"] = torch.ones(cfg.lin_v_dim, device=device, dtype=dtype)
+            w[p + "w_out"] = nrm(h, cfg.value_dim)
+    return w
+
+
+@dataclass
+class SeqCache:
+    """Batched decode state: KV caches, GDN states and conv windows, per-sequence committed length
+    and RoPE position on the device, and the committed token ids on the host (what the state
+    encodes). `pending` holds the record of a verify/canvas/draft forward until commit."""
+    kv_k: torch.Tensor
+    kv_v: torch.Tensor
+    state: torch.Tensor
+    window: torch.Tensor
+    length: torch.Tensor         # [B] int32: committed tokens (KV entries)
+    pos: torch.Tensor            # [B] int32: RoPE position of the next token
+    tokens: List[List[int]] = field(default_factory=list)
+    pending: Optional[dict] = None
+
+    @property
+    def B(self) -> int:
+        return self.length.shape[0]
+
+    @property
+    def Lmax(self) -> int:
+        return self.kv_k.shape[3]
+
+    def snapshot(self):
+        """Copy of the recurrent state, conv windows and lengths (KV entries are append-only, so the
+        length is enough for them) — SeqCache.snapshot of the reference (model.py:184-190)."""
+        assert self.pending is None
+        st, win = torch.empty_like(self.state), torch.empty_like(self.window)
+        K.gdn_snapshot(self.state, st, self.window, win)
+        return st, win, self.length.clone(), self.pos.clone(), [list(t) for t in self.tokens]
+
+    def restore(self, snap) -> None:
+        st, win, length, pos, tokens = snap
+        assert self.pending is None
+        K.gdn_snapshot(st, self.state, win, self.window)
+        self.length.copy_(length)
+        self.pos.copy_(pos)
+        self.tokens = [list(t) for t in tokens]
+
+
+class _Scratch:
+    """Per-(B, T) activation buffers, reused across forwards (fixed addresses for graph capture)."""
+
+    def __init__(self, cfg: HybridConfig, B: int, T: int, n_gdn: int, dev):
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        f32 = dict(dtype=torch.float32, device=dev)
+        N = B * T
+        h = cfg.hidden
+        self.h = torch.empty(N, h, **bf)
+        self.x = torch.empty(N, h, **bf)
+        self.r = torch.empty(N, h, **bf)
+        self.gu = torch.empty(N, 2 * cfg.intermediate, **bf)
+        self.act = torch.empty(N, cfg.intermediate, **bf)
+        self.proj = torch.empty(B, T, cfg.conv_dim + cfg.value_dim + 2 * cfg.lin_v_heads, **bf)
+        self.qkv = torch.empty(B, T, (2 * cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim, **bf)
+        self.q_att = torch.empty(B, T, cfg.n_heads, cfg.head_dim, **bf)
+        self.o_att = torch.empty(B, T, cfg.n_heads, cfg.head_dim, **bf)
+        self.y = torch.empty(B, T, cfg.lin_v_heads, cfg.lin_v_dim, **bf)
+        self.yn = torch.empty(N, cfg.lin_v_heads, cfg.lin_v_dim, **bf)
+        self.q = torch.empty(B, T, cfg.lin_k_heads, cfg.lin_k_dim, **bf)
+        self.win_tmp = torch.empty(B, cfg.conv_kernel - 1, cfg.conv_dim, **bf)
+        # per-GDN-layer block rows kept for commit (stacked so one restore launch covers every layer)
+        self.k_rec = torch.empty(n_gdn, B, T, cfg.lin_k_heads, cfg.lin_k_dim, **bf)
+        self.v_rec = torch.empty(n_gdn, B, T, cfg.lin_v_heads, cfg.lin_v_dim, **bf)
+        self.g_rec = torch.empty(n_gdn, B, T, cfg.lin_v_heads, **f32)
+        self.b_rec = torch.empty(n_gdn, B, T, cfg.lin_v_heads, **f32)
+        self.pre_rec = torch.empty(n_gdn, B, T, cfg.conv_dim, **bf)
+
+
+class TridaRuntime:
+    """The self-spec runtime over one model (see the module docstring for the mode semantics)."""
+
+    def __init__(self, cfg: HybridConfig, weights: Dict[str, torch.Tensor], device="cuda:0",
+                 prefill_chunk: int = 512):
+        self.cfg = cfg
+        self.dev = torch.device(device)
+        self.w = {k: v.to(self.dev) for k, v in weights.items()}
+        self.prefill_chunk = prefill_chunk
+        self.attn_layers = [i for i in range(cfg.n_layers) if cfg.is_attention(i)]
+        self.gdn_layers = [i for i in range(cfg.n_layers) if not cfg.is_attention(i)]
+        self._slot = {}
+        for j, i in enumerate(self.attn_layers):
+            self._slot[i] = j
+        for j, i in enumerate(self.gdn_layers):
+            self._slot[i] = j
+        self._scratch: Dict[tuple, _Scratch] = {}
+        self.skip_rows = False
+        self.mask_id = cfg.mask_id
+
+    # ---------------------------------------------------------------- cache
+    def make_cache(self, batch: int = 1, max_len: int = 4096) -> SeqCache:
+        c = self.cfg
+        bf = dict(dtype=torch.bfloat16, device=self.dev)
+        A, L = len(self.attn_layers), len(self.gdn_layers)
+        return SeqCache(
+            kv_k=torch.zeros(A, batch, c.n_kv_heads, max_len, c.head_dim, **bf),
+            kv_v=torch.zeros(A, batch, c.n_kv_heads, max_len, c.head_dim, **bf),
+            state=torch.zeros(L, batch, c.lin_v_heads, c.lin_v_dim, c.lin_k_dim, dtype=torch.float32, device=self.dev),
+            window=torch.zeros(L, batch, c.conv_kernel - 1, c.conv_dim, **bf),
+            length=torch.zeros(batch, dtype=torch.int32, device=self.dev),
+            pos=torch.zeros(batch, dtype=torch.int32, device=self.dev),
+            tokens=[[] for _ in range(batch)])
+
+    def scratch(self, B: int, T: int) -> _Scratch:
+        key = (B, T)
+        s = self._scratch.get(key)
+        if s is None:
+            s = self._scratch[key] = _Scratch(self.cfg, B, T, len(self.gdn_layers), self.dev)
+        return s
+
+    # ---------------------------------------------------------------- forward
+    def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
+                rows: Optional[int] = None, seq: Optional[slice] = None) -> torch.Tensor:
+        """One forward of a [B, T] block of token ids (device int64) on top of the cache.
+        Returns bf16 logits [B, rows or T, V]. seq restricts the forward to a contiguous range of the
+        cache's sequences (used by per-sequence prefill of ragged prompts)."""
+        c, w = self.cfg, self.w
+        B, T = ids.shape
+        sq = seq if seq is not None else slice(0, cache.B)
+        kv_k, kv_v = cache.kv_k[:, sq], cache.kv_v[:, sq]
+        state, window = cache.state[:, sq], cache.window[:, sq]
+        length, pos = cache.length[sq], cache.pos[sq]
+        persist = mode == "causal"
+        if mode in ("causal", "verify"):
+            att_mask, gdn_mode, nc = K.MASK_VERIFY, 1, T
+        elif mode == "canvas":
+            att_mask, gdn_mode, nc = K.MASK_CANVAS, 2, n_clean
+        elif mode == "draft":
+            att_mask, gdn_mode, nc = K.MASK_DRAFT, 2, 1
+        else:
+            raise ValueError(f"unknown forward mode {mode!r}")
+        s = self.scratch(B, T)
+        N = B * T
+        torch.index_select(w["embed"], 0, ids.reshape(-1), out=s.h)
+        first = True
+        for i in range(c.n_layers):
+            p = f"l{i}."
+            K.add_rmsnorm(s.h, None if first else s.r, w[p + "in_norm"], s.x, eps=c.rms_eps)
+            first = False
+            j = self._slot[i]
+            if c.is_attention(i):
+                torch.matmul(s.x, w[p + "w_qkv"].t(), out=s.qkv.view(N, -1))
+                K.attn_prep(s.qkv, w[p + "q_norm"], w[p + "k_norm"], pos, length, s.q_att, kv_k[j], kv_v[j],
+                            Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, rot_dim=c.rot_dim,
+                            rope_theta=c.rope_theta, eps=c.rms_eps)
+                # the q projection interleaves [q | gate] per head: gate (b, t, h, d) at h * 2D + D + d
+                Wq = s.qkv.shape[2]
+                gate = s.qkv.as_strided((B, T, c.n_heads, c.head_dim), (T * Wq, Wq, 2 * c.head_dim, 1),
+                                        s.qkv.storage_offset() + c.head_dim)
+                K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
+                              out=s.o_att, max_keys=cache.Lmax)
+                torch.matmul(s.o_att.view(N, -1), w[p + "w_o"].t(), out=s.r)
+            else:
+                torch.matmul(s.x, w[p + "w_in"].t(), out=s.proj.view(N, -1))
+                xv = s.proj[..., : c.conv_dim]
+                off = c.conv_dim + c.value_dim
+                b_in = s.proj[..., off: off + c.lin_v_heads]
+                a_in = s.proj[..., off + c.lin_v_heads: off + 2 * c.lin_v_heads]
+                rec = (s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j])
+                K.gdn_prep(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"], w[p + "dt_bias"],
+                           Hk=c.lin_k_heads, Hv=c.lin_v_heads, Dk=c.lin_k_dim, Dv=c.lin_v_dim,
+                           window_out=s.win_tmp if persist else None, out=rec)
+                K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
+                                causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
+                                out=s.y)
+                if persist:
+                    window[j].copy_(s.win_tmp)
+                elif mode != "draft":  # a draft pass is never committed
+                    s.pre_rec[j].copy_(xv)
+                z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
+                K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
+                torch.matmul(s.yn.view(N, -1), w[p + "w_out"].t(), out=s.r)
+            K.add_rmsnorm(s.h, s.r, w[p + "post_norm"], s.x, eps=c.rms_eps)
+            torch.matmul(s.x, w[p + "w_gu"].t(), out=s.gu)
+            K.silu_mul(s.gu, s.act)
+            torch.matmul(s.act, w[p + "w_down"].t(), out=s.r)
+        K.add_rmsnorm(s.h, s.r, w["final_norm"], s.x, eps=c.rms_eps)
+        x = s.x.view(B, T, -1)
+        if rows is not None:
+            x = x[:, :rows]
+        logits = torch.matmul(x, w["embed"].t())
+        if persist:
+            length += T
+            pos += T
+        return logits
+
+    # ---------------------------------------------------------------- reference API (batch 1 lists)
+    def _ids(self, tokens, B: int = 1) -> torch.Tensor:
+        t = torch.as_tensor(tokens, dtype=torch.int64)
+        return t.reshape(B, -1).to(self.dev)
+
+    def prefill(self, cache: SeqCache, tokens: list, seq: int = 0) -> torch.Tensor:
+        """Causal prefill of `tokens` for sequence `seq` (chunked). Returns fp32 logits [V] of the last
+        token (model.py:398-453)."""
+        assert cache.pending is None and tokens
+        logits = None
+        sl = slice(seq, seq + 1)
+        for s0 in range(0, len(tokens), self.prefill_chunk):
+            chunk = tokens[s0: s0 + self.prefill_chunk]
+            logits = self.forward(self._ids(chunk), cache, "causal", seq=sl)
+            cache.tokens[seq].extend(chunk)
+        return logits[0, -1].float()
+
+    def ar_step(self, cache: SeqCache, token: int) -> torch.Tensor:
+        logits = self.forward(self._ids([token]), cache, "causal")
+        cache.tokens[0].append(token)
+        return logits[0, -1].float()
+
+    def canvas(self, cache: SeqCache, canvas_tokens: list, n_clean: int, rows: Optional[int] = None,
+               as_float: bool = True) -> torch.Tensor:
+        """One self-spec canvas forward (model.py:472-484): rows < n_clean token-causal, MASK rows see
+        the block. Returns logits [rows or blk, V] (shift readout). Call commit() afterwards."""
+        assert cache.pending is None
+        ids = self._ids(canvas_tokens)
+        logits = self.forward(ids, cache, "canvas", n_clean=n_clean, rows=rows)
+        cache.pending = {"tokens": [list(canvas_tokens)], "T": ids.shape[1]}
+        return logits[0].float() if as_float else logits[0]
+
+    def verify(self, cache: SeqCache, ids: torch.Tensor) -> torch.Tensor:
+        """Token-causal pass over a [B, T] block (nothing persisted); commit() keeps a prefix."""
+        assert cache.pending is None
+        logits = self.forward(ids, cache, "verify")
+        cache.pending = {"ids": ids, "T": ids.shape[1]}
+        return logits
+
+    def draft(self, cache: SeqCache, ids: torch.Tensor) -> torch.Tensor:
+        """Block-diffusion denoising pass over a [B, T] block (nothing persisted, no commit)."""
+        assert cache.pending is None
+        return self.forward(ids, cache, "draft")
+
+    def commit(self, cache: SeqCache, adv, tokens_host: Optional[list] = None) -> None:
+        """Keep the first adv canvas rows (model.py:486-507): KV crop by length, GDN state advanced
+        from the block-entry state by those rows, conv window rebuilt. adv: int (same for every
+        sequence) or an int32 device tensor [B]. tokens_host: committed ids per sequence (host lists)
+        when the caller already has them."""
+        rec = cache.pending
+        assert rec is not None
+        T = rec["T"]
+        B = cache.B
+        if isinstance(adv, int):
+            assert 1 <= adv <= T
+            n_keep = torch.full((B,), adv, dtype=torch.int32, device=self.dev)
+        else:
+            n_keep = adv
+        s = self.scratch(B, T)
+        L = len(self.gdn_layers)
+        if L:
+            st = cache.state.view(L * B, *cache.state.shape[2:])
+            win = cache.window.view(L * B, *cache.window.shape[2:])
+            K.gdn_restore(n_keep, snap_state=st, state=st, k=s.k_rec.view(L * B, *s.k_rec.shape[2:]),
+                          v=s.v_rec.view(L * B, *s.v_rec.shape[2:]), g=s.g_rec.view(L * B, *s.g_rec.shape[2:]),
+                          beta=s.b_rec.view(L * B, *s.b_rec.shape[2:]), snap_window=win, window=win,
+                          preconv=s.pre_rec.view(L * B, *s.pre_rec.shape[2:]))
+        cache.length += n_keep
+        cache.pos += n_keep
+        if tokens_host is not None:
+            for b in range(B):
+                cache.tokens[b].extend(tokens_host[b])
+        elif "tokens" in rec and isinstance(adv, int):
+            for b in range(B):
+                cache.tokens[b].extend(rec["tokens"][b][:adv])
+        cache.pending = None
+
+
+def build_runtime(cfg: HybridConfig, seed: int = 0, device="cuda:0", embed_scale: float = 1.0) -> TridaRuntime:
+    """Random-init runtime: weights drawn on the device (no host copy of the 4B parameters)."""
+    w = init_weights(cfg, seed=seed, device=device, embed_scale=embed_scale)
+    return TridaRuntime(cfg, w, device=device)
+
+
+def config_json(cfg: HybridConfig) -> str:
+    return json.dumps(asdict(cfg))
