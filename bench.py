@@ -96,20 +96,139 @@ def bench_accept(args):
     }
 
 
+# ------------------------------------------------------------------------------ end-to-end (config 4)
+PROMPT_LEN, BLOCK, DENOISE = 2048, 32, 4
+
+
+def _cpu_baseline_e2e(rt, cfg, prompt_tail, args):
+    """The oracle's draft-then-verify step on the host cores, over a synthetic 2048-token context
+    (random KV entries and GDN states of the real shapes instead of a CPU prefill)."""
+    import torch
+
+    from oracle import model as OM
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    m = OM.CpuHybrid(cfg, rt.w)
+    cache = m.make_cache()
+    g = torch.Generator().manual_seed(1)
+    for i in range(cfg.n_layers):
+        if cfg.is_attention(i):
+            shape = (cfg.n_kv_heads, PROMPT_LEN, cfg.head_dim)
+            cache.kv[i] = (torch.randn(*shape, generator=g).bfloat16().float(),
+                           torch.randn(*shape, generator=g).bfloat16().float())
+        else:
+            cache.state[i] = torch.randn(1, cfg.lin_v_heads, cfg.lin_v_dim, cfg.lin_k_dim, generator=g) * 0.05
+            cache.window[i] = torch.randn(1, cfg.conv_kernel - 1, cfg.conv_dim, generator=g).bfloat16().float()
+    cache.tokens = list(prompt_tail) * (PROMPT_LEN // len(prompt_tail))
+    t0 = int(prompt_tail[-1])
+    steps, acc_tokens = 0, 0
+    t = time.perf_counter()
+    while steps < args.cpu_steps:
+        _, t0, acc = OM.blockspec_step(m, cache, t0, BLOCK, DENOISE)
+        acc_tokens += 1 + acc
+        steps += 1
+    dt = time.perf_counter() - t
+    return {"value": round(acc_tokens / dt, 4), "unit": "accepted tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{steps} draft-then-verify step(s) (4 denoising passes + verify + greedy acceptance + "
+                      f"rollback) of the CPU oracle on the same random-init 4B-shape weights (fp32 arithmetic), "
+                      f"synthetic {PROMPT_LEN}-token context; {dt:.1f} s"}
+
+
+def bench_e2e(args):
+    import torch
+
+    from trida_stack_amd import kernels as K
+    from trida_stack_amd.decode import BlockSpecStep
+    from trida_stack_amd.model import HybridConfig, build_runtime
+
+    cfg = HybridConfig.four_b()
+    rt = build_runtime(cfg, seed=0)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab - 1024, (PROMPT_LEN,), generator=g).tolist()
+    total = args.warmup + args.steps
+    cache = rt.make_cache(1, max_len=PROMPT_LEN + (BLOCK + 1) * (total + 2) + 64)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    logits = rt.prefill(cache, prompt)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t
+    step = BlockSpecStep(rt, cache, BLOCK, DENOISE)
+    step.t0.fill_(int(logits.argmax()))
+    for _ in range(args.warmup):
+        step.run()
+        int(step.n_acc[0])
+    torch.cuda.synchronize()
+    K.TIMERS = {} if not args.no_events else None
+    acc_tokens, hist = 0, [0] * (BLOCK + 1)
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        step.run()
+        n = int(step.n_acc[0])  # the host reads the accepted length each step to emit tokens
+        acc_tokens += 1 + n
+        hist[n] += 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    timers = K.timer_means_us(K.TIMERS) if K.TIMERS is not None else {}
+    K.TIMERS = None
+    ctx = int(cache.length[0])
+
+    # roofline of the decoder forward: every weight byte is read once per forward (bf16), plus the KV
+    # cache of the 8 attention layers and the 24 fp32 GDN states
+    weight_bytes = cfg.n_params() * 2
+    kv_bytes = 8 * 2 * cfg.n_kv_heads * ctx * cfg.head_dim * 2
+    state_bytes = 24 * cfg.lin_v_heads * cfg.lin_v_dim * cfg.lin_k_dim * 4
+    fwd_bytes = weight_bytes + kv_bytes + state_bytes
+    fwd_us = timers.get("forward")
+    roof = None
+    if fwd_us:
+        ach = fwd_bytes / (fwd_us * 1e-6) / 1e9
+        roof = {"bound": "hbm", "kernel": "decoder forward (33 canvas rows, every layer)", "achieved": round(ach, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                "algorithmic_bytes": fwd_bytes, "avg_us": round(fwd_us, 1)}
+    cpu = None if args.no_cpu else _cpu_baseline_e2e(rt, cfg, prompt[-64:], args)
+    value = acc_tokens / elapsed
+    return {
+        "metric": METRIC, "value": round(value, 2), "unit": "accepted tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init weights, random prompt ids)",
+        "config": {"workload": "end-to-end self-spec decode, random-init 4B-shape hybrid (hidden 2560, 24 GDN + 8 "
+                               "attention layers, FFN 9728, vocab 248320), batch 1, 2048-token prompt, block 32 "
+                               "with 4 denoising passes + verify, greedy acceptance and hybrid rollback",
+                   "batch": 1, "prompt_len": PROMPT_LEN, "block": BLOCK, "denoise_passes": DENOISE,
+                   "generated_tokens": acc_tokens, "tokens_per_step": round(acc_tokens / args.steps, 3),
+                   "accept_hist": hist, "params": cfg.n_params()},
+        "verify_step_us": round(timers["verify_step"], 1) if "verify_step" in timers else None,
+        "prefill_s": round(prefill_s, 3),
+        "kernel_avg_us": {k: round(v, 2) for k, v in timers.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
+    }
+
+
+WORKLOADS = {"e2e": (bench_e2e, 256, 8), "accept": (bench_accept, 100, 10)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="accept", choices=["accept"])
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="e2e", choices=sorted(WORKLOADS))
     ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--cpu-steps", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-events", action="store_true", help="skip the live per-kernel event timers")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the step shards by "
               "sequence; see the sharding notes)", file=sys.stderr)
         sys.exit(2)
-    res = {"accept": bench_accept}[args.workload](args)
+    fn, steps, warmup = WORKLOADS[args.workload]
+    args.steps = steps if args.steps is None else args.steps
+    args.warmup = warmup if args.warmup is None else args.warmup
+    res = fn(args)
     print(json.dumps(res), flush=True)
 
 

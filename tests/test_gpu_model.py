@@ -204,3 +204,20 @@ def test_four_b_block_step_runs(gpu):
     assert 0 <= n <= 32 and int(c.length[0]) == 64 + 1 + n
     del rt
     torch.cuda.empty_cache()
+
+
+def test_engine_modes_agree(gpu, pair):
+    """Engine drop-in: --mode causal and --mode self-spec (both variants) yield the same greedy ids."""
+    from trida_stack_amd.engine import Engine
+
+    rt, _ = pair
+    p = prompt(19, seed=21)
+    outs = []
+    for mode, n, d in (("causal", None, 0), ("self-spec", 4, 0), ("self-spec", 8, 2)):
+        eng = Engine(rt, mode=mode, gen_block=n, denoise_steps=d)
+        toks = []
+        for ch in eng.generate_ids(p, max_tokens=40):
+            toks.extend(ch)
+        outs.append(toks)
+        assert eng.last_stats["new_tokens"] == 40
+    assert outs[0] == outs[1] == outs[2]

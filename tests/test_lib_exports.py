@@ -43,3 +43,14 @@ def test_host_only_entry_points():
     rc = lib.trida_greedy_accept(1, 0, 1, 4, 10, 40, 10, 1, 4, 4, None, None, None, 1, 1, 1, 1, n, 0, None)
     assert rc == _lib.TRIDA_ERR_ARG
     assert b"R >= K + 1" in lib.trida_last_error()
+
+
+def test_mode_registry_matches_reference_launcher():
+    """The --mode values of the reference launcher (inference/zoro-1/serve.py:55-58)."""
+    from trida_stack_amd.engine import MODES
+    from trida_stack_amd import cli
+
+    assert set(MODES) == {"causal", "self-spec"}
+    import pytest as _p
+    with _p.raises(SystemExit):
+        cli.main(["--mode", "decide"])

@@ -106,6 +106,15 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   const int kmax = (a.mask_mode == 1 || (a.mask_mode == 2 && t_last >= a.n_clean)) ? nk : min(nk, prefix + t_last + 1);
 
   const int64_t pbase = ((((int64_t)b * a.Hkv + hk) * a.QT + qt) * a.S + s);
+  if (kb0 >= kb1 || kb0 * kKB >= kmax) {
+    // no key of this split is visible to the tile: only the (empty) row stats are written and the
+    // combine skips the split without reading its O
+    for (int r = tid; r < rows; r += kNW * kWave) {
+      a.mpart[pbase * kMT + r] = -INFINITY;
+      a.lpart[pbase * kMT + r] = 0.f;
+    }
+    return;
+  }
   // ---- stage Q rows (zero padding rows) and init running stats
   for (int p = tid; p < kMT * (D / 8); p += kNW * kWave) {
     const int r = p / (D / 8), c = (p % (D / 8)) * 8;
@@ -293,7 +302,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float lsum = 0.f;
   for (int s = 0; s < a.S; ++s) {
-    const float wgt = exp2f(a.mpart[(base + s) * kMT + r] - m_use);
+    const float ms = a.mpart[(base + s) * kMT + r];
+    if (ms == -INFINITY) continue;  // a split without visible keys (its O was never written)
+    const float wgt = exp2f(ms - m_use);
     lsum += wgt * a.lpart[(base + s) * kMT + r];
     const f32x4* op = reinterpret_cast<const f32x4*>(a.opart + ((base + s) * kMT + r) * a.D + c);
     const f32x4 x0 = op[0], x1 = op[1];

@@ -227,18 +227,22 @@ class BlockSpecStep:
         for p in range(self.denoise):
             L = rt.forward(self.canvas, cache, "draft")
             # row j predicts slot j + 1 (shift readout); the last row is not used
-            K.row_argmax(L, out=(self.d_am, self.d_conf))
+            with K.timed("row_argmax"):
+                K.row_argmax(L, out=(self.d_am, self.d_conf))
             score = torch.where(self.masked, self.d_conf[:, :blk], self.neg)
             # the per[p] most confident MASK slots (ties: the lower slot first)
             pos = torch.sort(score, dim=1, descending=True, stable=True).indices[:, : self.per[p]]
             self.canvas.scatter_(1, pos + 1, self.d_am[:, :blk].gather(1, pos))
             self.masked.scatter_(1, pos, False)
+        vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
         self.ctx.copy_(cache.length)
-        K.greedy_accept(L, self.canvas[:, 1:], ctx_len=self.ctx, out=(self.am, self.n_acc, self.bonus, self.crop))
+        with K.timed("greedy_accept"):
+            K.greedy_accept(L, self.canvas[:, 1:], ctx_len=self.ctx, out=(self.am, self.n_acc, self.bonus, self.crop))
         torch.add(self.n_acc, 1, out=self.n_keep)
         cache.pending = {"T": blk + 1}
         rt.commit(cache, self.n_keep)
+        vt.__exit__(None, None, None)
         self.t0.copy_(self.bonus)
 
 

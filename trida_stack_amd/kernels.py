@@ -54,6 +54,33 @@ class _Workspaces:
 
 workspaces = _Workspaces()
 
+# Optional live timing: while TIMERS is a dict, the wrappers (and the runtime's forward) record a pair
+# of events on the launching stream around their launches, keyed by name. Eager execution only.
+TIMERS: Optional[dict] = None
+
+
+class timed:
+    def __init__(self, name: str):
+        self.name = name
+        self.ev = None
+
+    def __enter__(self):
+        if TIMERS is not None:
+            self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            self.ev[0].record()
+        return self
+
+    def __exit__(self, *exc):
+        if self.ev is not None:
+            self.ev[1].record()
+            TIMERS.setdefault(self.name, []).append(self.ev)
+        return False
+
+
+def timer_means_us(timers: dict) -> dict:
+    """Mean duration (us) per timer name (call after a device synchronize)."""
+    return {k: sum(a.elapsed_time(b) for a, b in v) * 1e3 / len(v) for k, v in timers.items() if v}
+
 
 # --------------------------------------------------------------------------------------------------
 def _logit_dtype(t: torch.Tensor) -> int:

@@ -262,6 +262,7 @@ class TridaRuntime:
             raise ValueError(f"unknown forward mode {mode!r}")
         s = self.scratch(B, T)
         N = B * T
+        fwd_timer = K.timed("forward").__enter__()
         torch.index_select(w["embed"], 0, ids.reshape(-1), out=s.h)
         first = True
         for i in range(c.n_layers):
@@ -271,15 +272,17 @@ class TridaRuntime:
             j = self._slot[i]
             if c.is_attention(i):
                 torch.matmul(s.x, w[p + "w_qkv"].t(), out=s.qkv.view(N, -1))
-                K.attn_prep(s.qkv, w[p + "q_norm"], w[p + "k_norm"], pos, length, s.q_att, kv_k[j], kv_v[j],
-                            Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, rot_dim=c.rot_dim,
-                            rope_theta=c.rope_theta, eps=c.rms_eps)
+                with K.timed("attn_prep"):
+                    K.attn_prep(s.qkv, w[p + "q_norm"], w[p + "k_norm"], pos, length, s.q_att, kv_k[j], kv_v[j],
+                                Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, rot_dim=c.rot_dim,
+                                rope_theta=c.rope_theta, eps=c.rms_eps)
                 # the q projection interleaves [q | gate] per head: gate (b, t, h, d) at h * 2D + D + d
                 Wq = s.qkv.shape[2]
                 gate = s.qkv.as_strided((B, T, c.n_heads, c.head_dim), (T * Wq, Wq, 2 * c.head_dim, 1),
                                         s.qkv.storage_offset() + c.head_dim)
-                K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
-                              out=s.o_att, max_keys=cache.Lmax)
+                with K.timed("attn_canvas"):
+                    K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
+                                  out=s.o_att, max_keys=cache.Lmax)
                 torch.matmul(s.o_att.view(N, -1), w[p + "w_o"].t(), out=s.r)
             else:
                 torch.matmul(s.x, w[p + "w_in"].t(), out=s.proj.view(N, -1))
@@ -288,12 +291,14 @@ class TridaRuntime:
                 b_in = s.proj[..., off: off + c.lin_v_heads]
                 a_in = s.proj[..., off + c.lin_v_heads: off + 2 * c.lin_v_heads]
                 rec = (s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j])
-                K.gdn_prep(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"], w[p + "dt_bias"],
-                           Hk=c.lin_k_heads, Hv=c.lin_v_heads, Dk=c.lin_k_dim, Dv=c.lin_v_dim,
-                           window_out=s.win_tmp if persist else None, out=rec)
-                K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
-                                causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
-                                out=s.y)
+                with K.timed("gdn_prep"):
+                    K.gdn_prep(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"], w[p + "dt_bias"],
+                               Hk=c.lin_k_heads, Hv=c.lin_v_heads, Dk=c.lin_k_dim, Dv=c.lin_v_dim,
+                               window_out=s.win_tmp if persist else None, out=rec)
+                with K.timed("gdr_recurrent"):
+                    K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
+                                    causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
+                                    out=s.y)
                 if persist:
                     window[j].copy_(s.win_tmp)
                 elif mode != "draft":  # a draft pass is never committed
@@ -309,7 +314,9 @@ class TridaRuntime:
         x = s.x.view(B, T, -1)
         if rows is not None:
             x = x[:, :rows]
-        logits = torch.matmul(x, w["embed"].t())
+        with K.timed("lm_head"):
+            logits = torch.matmul(x, w["embed"].t())
+        fwd_timer.__exit__(None, None, None)
         if persist:
             length += T
             pos += T
@@ -378,10 +385,11 @@ class TridaRuntime:
         if L:
             st = cache.state.view(L * B, *cache.state.shape[2:])
             win = cache.window.view(L * B, *cache.window.shape[2:])
-            K.gdn_restore(n_keep, snap_state=st, state=st, k=s.k_rec.view(L * B, *s.k_rec.shape[2:]),
-                          v=s.v_rec.view(L * B, *s.v_rec.shape[2:]), g=s.g_rec.view(L * B, *s.g_rec.shape[2:]),
-                          beta=s.b_rec.view(L * B, *s.b_rec.shape[2:]), snap_window=win, window=win,
-                          preconv=s.pre_rec.view(L * B, *s.pre_rec.shape[2:]))
+            with K.timed("gdn_restore"):
+                K.gdn_restore(n_keep, snap_state=st, state=st, k=s.k_rec.view(L * B, *s.k_rec.shape[2:]),
+                              v=s.v_rec.view(L * B, *s.v_rec.shape[2:]), g=s.g_rec.view(L * B, *s.g_rec.shape[2:]),
+                              beta=s.b_rec.view(L * B, *s.b_rec.shape[2:]), snap_window=win, window=win,
+                              preconv=s.pre_rec.view(L * B, *s.pre_rec.shape[2:]))
         cache.length += n_keep
         cache.pos += n_keep
         if tokens_host is not None:
