@@ -171,6 +171,17 @@ int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t
  *   rot_dim dims at position pos0[b] + t (inv_freq_i = theta^(-2i/rot_dim)); q goes to q_out
  *   [B, T, Hq, D], k and v to the caches [B, Hkv, Lmax, D] at slot slot0[b] + t.
  */
+/* Skinny bf16 GEMM for canvas-sized activations: Y[M, N] = X[M, K] W[N, K]^T (torch Linear weight
+ * layout), fp32 accumulation, bf16 output, 1 <= M <= 64, N % 16 == 0, K % 32 == 0. It replaces the
+ * projection / MLP / LM-head matmuls of the decoder forward at decode-step sizes
+ * (TridaRuntime._forward, inference/zoro-1/mlx/trida_mlx/model.py:337-364), which are bound by the
+ * weight stream. Row strides in elements. splits = 0 picks the K split; scratch:
+ * trida_skinny_gemm_scratch_bytes(M, N, K, splits) bytes (0 when no split is used). */
+int64_t trida_skinny_gemm_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t splits);
+int trida_skinny_gemm(const uint16_t* X, int64_t x_row_stride, const uint16_t* W, int64_t w_row_stride, uint16_t* Y,
+                      int64_t y_row_stride, int64_t M, int64_t N, int64_t K, void* scratch, int64_t scratch_bytes,
+                      int64_t splits, void* stream);
+
 int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim,
                       int64_t x_st, int64_t r_st, int64_t o_st, float eps, int zero_centred, void* stream);
 int trida_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter, int64_t g_st, int64_t o_st,

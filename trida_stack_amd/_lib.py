@@ -31,6 +31,8 @@ SIGNATURES = {
     "trida_greedy_accept": (C.c_int, [P, C.c_int, I64, I64, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, P, I64, I64, P]),
     "trida_row_argmax_scratch_bytes": (I64, [I64, I64, C.c_int, I64]),
     "trida_row_argmax": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P, I64, I64, P]),
+    "trida_skinny_gemm_scratch_bytes": (I64, [I64, I64, I64, I64]),
+    "trida_skinny_gemm": (C.c_int, [P, I64, P, I64, P, I64, I64, I64, I64, P, I64, I64, P]),
     "trida_add_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, I64, F32, C.c_int, P]),
     "trida_silu_mul": (C.c_int, [P, P, I64, I64, I64, I64, P]),
     "trida_gated_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, F32, P]),

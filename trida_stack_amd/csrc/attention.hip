@@ -286,32 +286,73 @@ struct CombineArgs {
   int64_t gate_st, gate_hs;
 };
 
-// one thread per (row, 8 output columns)
+// Block = a group of RB rows of one (sequence, KV head); thread = (row, 8 output columns). The split
+// weights exp2(m_s - max) / sum of the group's rows are computed once into LDS; each thread then sums
+// the O rows of the non-empty splits.
+constexpr int kMaxSplits = 256;
+
 __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
+  __shared__ float s_w[32][kMaxSplits];  // rows of the group x listed splits
+  __shared__ float s_inv[32];
+  __shared__ int s_list[kMaxSplits];
+  __shared__ int s_cnt[4];
   const int M = a.T * a.G;
   const int per_row = a.D / 8;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)M * per_row) return;
-  const int m = (int)(gid / per_row), c = (int)(gid % per_row) * 8;
+  const int rb = 256 / per_row;  // rows per block: 8 (D=256), 16 (D=128), 32 (D=64)
   const int b = blockIdx.y / a.Hkv, hk = blockIdx.y % a.Hkv;
-  const int qt = m / kMT, r = m % kMT;
-  const int64_t base = (((int64_t)b * a.Hkv + hk) * a.QT + qt) * a.S;
-  float mx = -INFINITY;
-  for (int s = 0; s < a.S; ++s) mx = fmaxf(mx, a.mpart[(base + s) * kMT + r]);
-  const float m_use = mx == -INFINITY ? 0.f : mx;
+  const int m0 = blockIdx.x * rb;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  // list, in split order, the splits with a visible key for some row of the group (one split per
+  // thread, S <= 256; wave ballots give each listed split its position)
+  bool any = false;
+  if (tid < a.S) {
+    for (int i = 0; i < rb && m0 + i < M; ++i) {
+      const int m = m0 + i;
+      const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
+      any |= a.mpart[(bs + tid) * kMT + m % kMT] != -INFINITY;
+    }
+  }
+  const unsigned long long mask = __ballot(any);
+  if (lane == 0) s_cnt[wave] = __popcll(mask);
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wave; ++w) off += s_cnt[w];
+  if (any) s_list[off + __popcll(mask & ((1ull << lane) - 1ull))] = tid;
+  const int ns = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+  __syncthreads();
+  // per row: max, weights and 1 / sum
+  if (tid < rb && m0 + tid < M) {
+    const int m = m0 + tid;
+    const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
+    const int r = m % kMT;
+    float mx = -INFINITY;
+    for (int j = 0; j < ns; ++j) mx = fmaxf(mx, a.mpart[(bs + s_list[j]) * kMT + r]);
+    const float m_use = mx == -INFINITY ? 0.f : mx;
+    float lsum = 0.f;
+    for (int j = 0; j < ns; ++j) {
+      const float w = exp2f(a.mpart[(bs + s_list[j]) * kMT + r] - m_use);
+      s_w[tid][j] = w;
+      lsum += w * a.lpart[(bs + s_list[j]) * kMT + r];
+    }
+    s_inv[tid] = lsum > 0.f ? 1.f / lsum : 0.f;
+  }
+  __syncthreads();
+  const int i = tid / per_row;
+  const int m = m0 + i;
+  if (i >= rb || m >= M) return;
+  const int c = (tid % per_row) * 8;
+  const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
+  const int r = m % kMT;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  for (int s = 0; s < a.S; ++s) {
-    const float ms = a.mpart[(base + s) * kMT + r];
-    if (ms == -INFINITY) continue;  // a split without visible keys (its O was never written)
-    const float wgt = exp2f(ms - m_use);
-    lsum += wgt * a.lpart[(base + s) * kMT + r];
-    const f32x4* op = reinterpret_cast<const f32x4*>(a.opart + ((base + s) * kMT + r) * a.D + c);
+#pragma unroll 4
+  for (int j = 0; j < ns; ++j) {
+    const float wgt = s_w[i][j];
+    const f32x4* op = reinterpret_cast<const f32x4*>(a.opart + ((bs + s_list[j]) * kMT + r) * a.D + c);
     const f32x4 x0 = op[0], x1 = op[1];
     acc[0] += wgt * x0.x; acc[1] += wgt * x0.y; acc[2] += wgt * x0.z; acc[3] += wgt * x0.w;
     acc[4] += wgt * x1.x; acc[5] += wgt * x1.y; acc[6] += wgt * x1.z; acc[7] += wgt * x1.w;
   }
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const float inv = s_inv[i];
   const int t = m / a.G, g = m % a.G, hq = hk * a.G + g;
   uint32_t packed[4];
 #pragma unroll
@@ -329,11 +370,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
       u32x4{packed[0], packed[1], packed[2], packed[3]};
 }
 
+// Splits per (sequence, KV head, query tile): enough workgroups to cover the CUs (~512 in all), but
+// at least 4 key blocks per split so one split's O partial (rows x D fp32) stays small next to the
+// keys it reads.
 int64_t plan_splits(int64_t B, int64_t Hkv, int64_t QT, int64_t max_keys, int64_t splits) {
   if (splits > 0) return splits;
   const int64_t nblk = cdiv(max_keys, kKB);
   int64_t s = cdiv(512, B * Hkv * QT);
-  if (s > nblk) s = nblk;
+  const int64_t by_len = cdiv(nblk, 4);
+  if (s > by_len) s = by_len;
+  if (s > kMaxSplits) s = kMaxSplits;
   return s < 1 ? 1 : s;
 }
 
@@ -370,6 +416,7 @@ extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, con
   const int64_t G = Hq / Hkv;
   const int64_t QT = cdiv(T * G, kMT);
   const int64_t S = plan_splits(B, Hkv, QT, max_keys > 0 ? max_keys : Lmax, splits);
+  TRIDA_CHECK(S >= 1 && S <= kMaxSplits, TRIDA_ERR_ARG, "attn_canvas: 1..%d key splits", kMaxSplits);
   const int64_t need = trida_attn_canvas_scratch_bytes(B, T, Hq, Hkv, D, max_keys > 0 ? max_keys : Lmax, S);
   TRIDA_CHECK(scratch_bytes >= need, TRIDA_ERR_WORKSPACE, "attn_canvas: scratch %lld < %lld bytes",
               (long long)scratch_bytes, (long long)need);
@@ -392,8 +439,8 @@ extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, con
   if (rc) return rc;
   CombineArgs c{opart, mpart, lpart, gate, out, (int)T, (int)Hq, (int)Hkv, (int)G, (int)D, (int)S, (int)QT,
                 gate_row_stride, gate_head_stride};
-  const int64_t threads = T * G * (D / 8);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)cdiv(threads, 256), (unsigned)(B * Hkv)), dim3(256), 0,
-                     st, c);
+  const int64_t rows_per_block = 256 / (D / 8);
+  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv)), dim3(256),
+                     0, st, c);
   return launch_status("attn_canvas/combine");
 }

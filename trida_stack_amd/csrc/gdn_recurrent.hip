@@ -18,7 +18,7 @@ namespace {
 
 constexpr int kLanesPerV = 16;
 constexpr int kVPerWave = kWave / kLanesPerV;  // 4
-constexpr int kTC = 32;                        // rows staged per LDS chunk
+constexpr int kTC = 64;                        // rows staged per LDS chunk (a canvas block fits in one)
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -112,6 +112,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     }
     __syncthreads();
 
+#pragma unroll 2
     for (int r = 0; r < tn; ++r) {
       const int t = t0 + r;
       float kk[KPL], qq[KPL];

@@ -267,6 +267,7 @@ def _blockspec(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_token
         packed = torch.cat([step.canvas[0, 1:], step.bonus[:1], step.n_acc[:1].to(torch.int64)]).tolist()
         acc = packed[-1]
         cache.tokens[0].extend([t0] + packed[:acc])  # the committed rows: pending token + accepted drafts
+        cache.ctx_hint = len(cache.tokens[0])
         stats.accept_hist[acc] += 1
         chunk = packed[:acc] + [packed[block]]
         t0 = packed[block]

@@ -379,6 +379,32 @@ def attn_canvas(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, p
 
 
 # --------------------------------------------------------------------------------------------------
+# skinny GEMM
+SKINNY_MAX_M = 64
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None, *, splits: int = 0) -> torch.Tensor:
+    """y = x @ w.T for bf16 x [M, K] (M <= 64, contiguous rows) and w [N, K] (torch Linear layout);
+    fp32 accumulation, bf16 out [M, N]."""
+    dev = _need_gpu(x, w, out)
+    _bf16(x, "x")
+    _bf16(w, "w")
+    M, Kd = x.shape
+    N = w.shape[0]
+    if w.shape[1] != Kd or x.stride(1) != 1 or w.stride(1) != 1:
+        raise ValueError("linear: shapes / strides")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    nbytes = lib.trida_skinny_gemm_scratch_bytes(M, N, Kd, splits)
+    scr = workspaces.get(dev, "skinny_gemm", nbytes) if nbytes else None
+    rc = lib.trida_skinny_gemm(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
+                               M, N, Kd, _ptr(scr), scr.numel() if scr is not None else 0, splits, _stream(dev))
+    _lib.check(rc, "trida_skinny_gemm")
+    return out
+
+
+# --------------------------------------------------------------------------------------------------
 # row-wise decoder kernels
 def add_rmsnorm(x: torch.Tensor, r: Optional[torch.Tensor], w: torch.Tensor, out: torch.Tensor, *,
                 eps: float = 1e-6, zero_centred: bool = True) -> torch.Tensor:

@@ -143,6 +143,10 @@ class SeqCache:
     pos: torch.Tensor            # [B] int32: RoPE position of the next token
     tokens: List[List[int]] = field(default_factory=list)
     pending: Optional[dict] = None
+    # host-side upper bound of the committed length of every sequence (plans attention key splits;
+    # exact after prefill / integer commits, conservative after device-side commits until the decode
+    # loop settles it)
+    ctx_hint: int = 0
 
     @property
     def B(self) -> int:
@@ -240,6 +244,19 @@ class TridaRuntime:
         return s
 
     # ---------------------------------------------------------------- forward
+    use_skinny_gemm = False  # the skinny kernel is slower than hipBLASLt at these shapes so far
+
+    def _mm(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x @ w.T: the skinny weight-streaming kernel for canvas-sized x (<= 64 rows), hipBLASLt
+        (torch.matmul) for prefill chunks."""
+        if self.use_skinny_gemm and x.shape[0] <= K.SKINNY_MAX_M and w.shape[0] % 16 == 0 and w.shape[1] % 32 == 0:
+            with K.timed("skinny_gemm"):
+                return K.linear(x, w, out=out)
+        with K.timed("gemm"):
+            if out is None:
+                return torch.matmul(x, w.t())
+            return torch.matmul(x, w.t(), out=out)
+
     def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
                 rows: Optional[int] = None, seq: Optional[slice] = None) -> torch.Tensor:
         """One forward of a [B, T] block of token ids (device int64) on top of the cache.
@@ -262,6 +279,7 @@ class TridaRuntime:
             raise ValueError(f"unknown forward mode {mode!r}")
         s = self.scratch(B, T)
         N = B * T
+        max_keys = min(cache.Lmax, cache.ctx_hint + T)
         fwd_timer = K.timed("forward").__enter__()
         torch.index_select(w["embed"], 0, ids.reshape(-1), out=s.h)
         first = True
@@ -271,7 +289,7 @@ class TridaRuntime:
             first = False
             j = self._slot[i]
             if c.is_attention(i):
-                torch.matmul(s.x, w[p + "w_qkv"].t(), out=s.qkv.view(N, -1))
+                self._mm(s.x, w[p + "w_qkv"], s.qkv.view(N, -1))
                 with K.timed("attn_prep"):
                     K.attn_prep(s.qkv, w[p + "q_norm"], w[p + "k_norm"], pos, length, s.q_att, kv_k[j], kv_v[j],
                                 Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, rot_dim=c.rot_dim,
@@ -282,10 +300,10 @@ class TridaRuntime:
                                         s.qkv.storage_offset() + c.head_dim)
                 with K.timed("attn_canvas"):
                     K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
-                                  out=s.o_att, max_keys=cache.Lmax)
-                torch.matmul(s.o_att.view(N, -1), w[p + "w_o"].t(), out=s.r)
+                                  out=s.o_att, max_keys=max_keys)
+                self._mm(s.o_att.view(N, -1), w[p + "w_o"], s.r)
             else:
-                torch.matmul(s.x, w[p + "w_in"].t(), out=s.proj.view(N, -1))
+                self._mm(s.x, w[p + "w_in"], s.proj.view(N, -1))
                 xv = s.proj[..., : c.conv_dim]
                 off = c.conv_dim + c.value_dim
                 b_in = s.proj[..., off: off + c.lin_v_heads]
@@ -305,21 +323,25 @@ class TridaRuntime:
                     s.pre_rec[j].copy_(xv)
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
                 K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
-                torch.matmul(s.yn.view(N, -1), w[p + "w_out"].t(), out=s.r)
+                self._mm(s.yn.view(N, -1), w[p + "w_out"], s.r)
             K.add_rmsnorm(s.h, s.r, w[p + "post_norm"], s.x, eps=c.rms_eps)
-            torch.matmul(s.x, w[p + "w_gu"].t(), out=s.gu)
+            self._mm(s.x, w[p + "w_gu"], s.gu)
             K.silu_mul(s.gu, s.act)
-            torch.matmul(s.act, w[p + "w_down"].t(), out=s.r)
+            self._mm(s.act, w[p + "w_down"], s.r)
         K.add_rmsnorm(s.h, s.r, w["final_norm"], s.x, eps=c.rms_eps)
         x = s.x.view(B, T, -1)
         if rows is not None:
             x = x[:, :rows]
         with K.timed("lm_head"):
-            logits = torch.matmul(x, w["embed"].t())
+            logits = self._mm(x.reshape(-1, x.shape[-1]), w["embed"]).view(B, x.shape[1], -1)
         fwd_timer.__exit__(None, None, None)
         if persist:
             length += T
             pos += T
+            if seq is None or cache.B == 1:
+                cache.ctx_hint += T
+            else:
+                cache.ctx_hint = max(cache.ctx_hint, len(cache.tokens[sq.start]) + T)
         return logits
 
     # ---------------------------------------------------------------- reference API (batch 1 lists)
@@ -392,6 +414,7 @@ class TridaRuntime:
                               preconv=s.pre_rec.view(L * B, *s.pre_rec.shape[2:]))
         cache.length += n_keep
         cache.pos += n_keep
+        cache.ctx_hint += adv if isinstance(adv, int) else T
         if tokens_host is not None:
             for b in range(B):
                 cache.tokens[b].extend(tokens_host[b])
