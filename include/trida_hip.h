@@ -70,6 +70,53 @@ int trida_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int
                      float* conf, void* scratch, int64_t scratch_bytes, int64_t splits, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Sampled self-spec acceptance (speculative rejection sampling).
+ * Replaces the sampled verify of selfspec_generate (inference/zoro-1/mlx/trida_mlx/decode.py:333-354)
+ * with truncated_probs (decode.py:102-130), the role of _ss_sample_verify
+ *   (inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:787-880).
+ *
+ * P_i = truncated distribution of verify row i: y = logit / T (fp32 division) with ban_id at -inf;
+ * top-k keeps y >= the k-th largest (0 < top_k < V, top_k <= 4096); the nucleus (top_p < 1) is taken
+ * over those k largest values (or the whole row) in descending order and keeps every value whose
+ * preceding mass is < top_p; the kept set is every y >= the last kept value (ties kept).
+ * Draft i (i < min(K, n_live)) is accepted iff ratio >= 1 or u_accept[i] < ratio, ratio = P_i(d_i) /
+ * q_i(d_i) (0 where q = 0); n_acc = leading accepted drafts. token = the correction drawn from
+ * max(0, P_a - q_a) normalised (P_a if that mass is 0), a = n_acc < K, or the bonus from P_K when
+ * every draft is accepted; the draw is the inverse CDF in vocabulary order at u_sample[b]
+ * (token = min{x : cdf(x) > u * total}). crop = ctx_len + 1 + n_acc.
+ * p_logits [B, R, V] fp32 (R >= K + 1), q_probs [B, K, V] fp32 probabilities the drafts were drawn
+ * from, drafts [B, K] int64, n_live [B] int32 or NULL, u_accept [B, K] fp32 (row stride u_stride),
+ * u_sample [B] fp32, ctx_len [B] int64 or NULL. Outputs n_acc [B] int32, token [B] int64, crop [B]
+ * int64, ratio [B, K] fp64 or NULL, status [B] int32 (nonzero: a NaN / +inf logit or a row with no
+ * finite logit among rows 0..K; the outputs of that sequence are then undefined). K <= 64.
+ * scratch: trida_sample_accept_scratch_bytes(B, R, V, K) bytes, 256-byte aligned, no initialisation.
+ */
+int64_t trida_sample_accept_scratch_bytes(int64_t B, int64_t R, int64_t V, int64_t K);
+int trida_sample_accept(const float* p_logits, int64_t B, int64_t R, int64_t V, int64_t p_batch_stride,
+                        int64_t p_row_stride, const float* q_probs, int64_t q_batch_stride, int64_t q_row_stride,
+                        const int64_t* drafts, int64_t K, int64_t draft_stride, const int32_t* n_live,
+                        const float* u_accept, int64_t u_stride, const float* u_sample, const int64_t* ctx_len,
+                        float temperature, int64_t top_k, float top_p, int64_t ban_id, int32_t* n_acc,
+                        int64_t* token, int64_t* crop, double* ratio, int32_t* status, void* scratch,
+                        int64_t scratch_bytes, void* stream);
+
+/* Truncation statistics of rows [B, R, V] fp32 (the statistics of truncated_probs, decode.py:102-130):
+ * m = max y, thr = smallest kept y (-inf: nothing truncated), zk = sum over kept y of exp(y - m), so
+ * P(x) = [y_x >= thr] exp(y_x - m) / zk. status 1 = NaN / +inf logit, 2 = no finite logit. flags bit 0
+ * skips the one-pass window path (exact radix select only); passes [B*R] (or NULL) reports how many
+ * streaming passes each row took. Outputs are [B*R], row-major. */
+int trida_truncate_stats(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                         int64_t row_stride, float temperature, int64_t top_k, float top_p, int64_t ban_id, int flags,
+                         float* m, float* thr, double* zk, int32_t* status, int32_t* passes, void* stream);
+
+/* Writes the truncated distributions P [B, R, V] fp32 from the statistics above (the probability rows
+ * selfspec_generate keeps as the next step's draft distributions, decode.py:354, 378). */
+int trida_truncated_probs(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                          int64_t row_stride, float temperature, int64_t ban_id, const float* m, const float* thr,
+                          const double* zk, float* probs, int64_t out_batch_stride, int64_t out_row_stride,
+                          void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * GDN layer front half: depthwise causal conv (width Kc in 2..4) over [window ++ x] + SiLU, split into
  * q / k / v, per-head l2norm of q and k (eps 1e-6), gates g = -exp(A_log) * softplus(a + dt_bias) and
  * beta = sigmoid(b). Replaces the conv / split / normalise / gate steps of TridaRuntime._gdn

@@ -76,9 +76,12 @@ def truncated_probs(logits: np.ndarray, temperature: float, top_k: int = 0, top_
 
     The logits are divided by the temperature in fp32 (as the reference does); the softmax, the
     nucleus cumulative mass and the renormalisation are done in float64 here, so this is the exact
-    distribution up to the fp32 temperature division. Kept set: with top-k, the k largest (ties at
-    the k-th value kept); then the nucleus keeps the sorted prefix whose mass *before* each token is
-    < top_p (the token that crosses top_p stays), i.e. every x with l(x) >= the last kept value.
+    distribution up to the fp32 temperature division. Kept set: with top-k, every x >= the k-th
+    largest value (ties kept, decode.py:114-116); the nucleus is then computed on exactly the k
+    largest values (the sorted mx.topk list, decode.py:117-122), or on the whole sorted row without
+    top-k (decode.py:123-128), keeping the sorted prefix whose mass *before* each value is < top_p
+    (the value that crosses top_p stays); the final kept set is every x >= the last kept value, so
+    ties at that value are all kept.
     """
     x = np.asarray(logits, dtype=np.float32).copy()
     if mask_id >= 0:
@@ -98,7 +101,7 @@ def truncated_probs(logits: np.ndarray, temperature: float, top_k: int = 0, top_
         if 0 < top_k < V:
             thr = s[top_k - 1]
         if top_p < 1.0:
-            cand = s[s >= thr] if np.isfinite(thr) else s
+            cand = s[:top_k] if 0 < top_k < V else s
             m = cand[0]
             e = np.exp(cand - m)
             ps = e / e.sum()
@@ -119,7 +122,8 @@ def truncated_probs(logits: np.ndarray, temperature: float, top_k: int = 0, top_
 
 def sample_inverse_cdf(weights: np.ndarray, u: float) -> tuple[int, float]:
     """token = min{x : sum_{y<=x} w(y) > u * sum(w)} (vocabulary order). Returns (token, gap), gap
-    being the distance of u*total to the nearest cdf step (for tie tolerance in tests)."""
+    being the distance of u*total to the nearest cdf step in the units of ``weights`` (probabilities
+    here), for the tie tolerance of tests."""
     w = np.asarray(weights, dtype=np.float64)
     c = np.cumsum(w)
     tot = c[-1]
@@ -129,7 +133,7 @@ def sample_inverse_cdf(weights: np.ndarray, u: float) -> tuple[int, float]:
     # skip zero-weight tokens the search could land on at the very end
     while w[tok] <= 0 and tok > 0:
         tok -= 1
-    gap = float(np.min(np.abs(c - t)) / max(tot, 1e-300))
+    gap = float(np.min(np.abs(c - t)))
     return tok, gap
 
 

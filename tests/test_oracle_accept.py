@@ -179,3 +179,20 @@ def test_rejection_accept_closed_forms():
     q3[0, 0, 0] = 0
     r = A.rejection_accept(logits, q3, drafts, np.zeros((1, K)), np.array([0.0]), temperature=1.0)
     assert r["n_acc"].tolist() == [0]
+
+
+def test_truncated_probs_top_k_ties_follow_topk_list():
+    """With top-k the nucleus runs over exactly the k largest values (decode.py:117-122): ties at the
+    k-th value beyond k do not enter the nucleus mass, but every x >= the final threshold is kept."""
+    x = np.array([[3.0, 2.0, 2.0, 2.0, 0.0]], np.float32)
+    # top = [3, 2]: softmax [0.731, 0.269]; mass before the 2 is 0.731 >= 0.6 -> only the 3 stays
+    P = A.truncated_probs(x, 1.0, 2, 0.6)
+    assert np.nonzero(P[0])[0].tolist() == [0]
+    # top_p 0.8 keeps both listed values, so the threshold is 2 and all three 2s are kept
+    P = A.truncated_probs(x, 1.0, 2, 0.8)
+    assert np.nonzero(P[0])[0].tolist() == [0, 1, 2, 3]
+    e = np.exp(np.array([3.0, 2, 2, 2]) - 3)
+    assert np.allclose(P[0, :4], e / e.sum(), atol=1e-15)
+    # top-k alone keeps the ties at the k-th value as well
+    P = A.truncated_probs(x, 1.0, 2, 1.0)
+    assert np.nonzero(P[0])[0].tolist() == [0, 1, 2, 3]

@@ -1,0 +1,1062 @@
+// Sampled self-spec acceptance (speculative rejection sampling with top-k / top-p truncation).
+//
+// Three launches on the caller's stream:
+//   truncate (grid rows): one 512-thread block per verify row finds the truncated distribution's
+//       statistics: m = max y (y = logit / T, the banned id at -inf), thr = the smallest kept y and
+//       Zk = sum over kept y of exp(y - m), so that P(x) = [y_x >= thr] exp(y_x - m) / Zk.
+//       A sorted, evenly spaced 2048-element sample of the row places a window that should hold the
+//       truncation boundary; ONE streaming pass then accumulates the row max, the total mass, the mass
+//       above the window, and collects the window's values into LDS, where a bitonic sort and an fp64
+//       prefix scan resolve thr exactly. When the window misses (a few heavy tokens outside the
+//       sample, massive ties, |y| large enough to overflow the sample-relative exponentials) the block
+//       falls back to an exact radix select over the order-preserving keys of y, 8 bits per pass.
+//   resid_sums (grid NC x B): every block re-derives its sequence's accepted length from the drafted
+//       tokens' ratios P_i(d_i) / q_i(d_i), then sums the correction weights max(0, P_a - q_a) (P_K
+//       when every draft is accepted) and P_a over its chunk of the vocabulary, in fp64.
+//   resid_pick (grid B): inverse CDF in vocabulary order with one uniform: the chunk where the
+//       cumulative weight first exceeds u * total, then the token inside it.
+// Nothing allocates; scratch holds the per-row statistics and the chunk sums.
+#include <limits.h>
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace trida {
+namespace {
+
+constexpr int kT = 512;  // threads of the truncation block
+constexpr int kTW = kT / kWave;
+constexpr int kSample = 2048;
+constexpr int kCap = 8192;  // LDS collection capacity (values)
+constexpr int kBins = 256;  // digits of one radix pass
+constexpr int kMaxTopK = 4096;
+constexpr uint32_t kKeyLo = 0x00800000u;  // smallest finite key (key(-inf) + 1)
+constexpr uint32_t kKeyHi = 0xff7fffffu;  // largest finite key (key(+inf) - 1)
+constexpr int kRT = 256;                  // threads of the residual kernels
+
+// Order-preserving map float -> uint32 (larger value, larger key) and its inverse.
+__device__ __forceinline__ uint32_t fkey(float y) {
+  const uint32_t u = __float_as_uint(y);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float kval(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// y = logit / T rounded to fp32 exactly as an IEEE fp32 division (the reference divides the fp32
+// logits by the temperature), -0 folded into +0 so that equal values have equal keys, the banned id at
+// -inf. rt = 1/T in fp64: the fp64 product is within 2^-52 (relative) of x/T, while x/T is never within
+// 2^-48 of a midpoint between two floats unless it is one exactly, which needs T's odd significand
+// times a 25-bit odd significand to fit 24 bits, i.e. T a power of two, where the product is exact.
+// So rounding the fp64 product to fp32 gives the correctly rounded quotient, in three instructions.
+template <bool kDiv>
+__device__ __forceinline__ float make_y(float x, int ix, double rt, int64_t ban) {
+  float y = kDiv ? (float)((double)x * rt) : x;
+  y = (y == 0.f) ? 0.f : y;
+  return (ix == ban) ? -INFINITY : y;
+}
+
+__device__ __forceinline__ int next_pow2(int n) {
+  int p = 1;
+  while (p < n) p <<= 1;
+  return p;
+}
+
+// ---------------------------------------------------------------- block reductions (512 threads)
+__device__ __forceinline__ double block_sum(double v, double* sh) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) sh[threadIdx.x / kWave] = v;
+  __syncthreads();
+  double t = 0.0;
+#pragma unroll
+  for (int w = 0; w < kTW; ++w) t += sh[w];
+  return t;
+}
+__device__ __forceinline__ float block_max(float v, double* sh) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) sh[threadIdx.x / kWave] = v;
+  __syncthreads();
+  float t = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kTW; ++w) t = fmaxf(t, (float)sh[w]);
+  return t;
+}
+__device__ __forceinline__ int block_isum(int v, double* sh) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) sh[threadIdx.x / kWave] = (double)v;
+  __syncthreads();
+  int t = 0;
+#pragma unroll
+  for (int w = 0; w < kTW; ++w) t += (int)sh[w];
+  return t;
+}
+// Exclusive prefix sum over the block in thread order; *total gets the block total.
+__device__ __forceinline__ double block_excl_scan(double v, double* sh, double* total) {
+  const int lane = threadIdx.x % kWave, w = threadIdx.x / kWave;
+  double inc = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const double o = __shfl_up(inc, off, kWave);
+    if (lane >= off) inc += o;
+  }
+  double ex = __shfl_up(inc, 1, kWave);
+  if (lane == 0) ex = 0.0;
+  __syncthreads();
+  if (lane == kWave - 1) sh[w] = inc;
+  __syncthreads();
+  double base = 0.0, tot = 0.0;
+#pragma unroll
+  for (int i = 0; i < kTW; ++i) {
+    base += (i < w) ? sh[i] : 0.0;
+    tot += sh[i];
+  }
+  *total = tot;
+  return base + ex;
+}
+
+// Bitonic sort, descending, of s[0..n) (n a power of two); starts and ends with a barrier.
+__device__ void sort_desc(float* s, int n) {
+  __syncthreads();
+  for (int k = 2; k <= n; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int i = threadIdx.x; i < (n >> 1); i += kT) {
+        const int lo = ((i & ~(j - 1)) << 1) | (i & (j - 1));
+        const int hi = lo + j;
+        const float a = s[lo], b = s[hi];
+        const bool desc = (lo & k) == 0;
+        if (desc ? (a < b) : (a > b)) {
+          s[lo] = b;
+          s[hi] = a;
+        }
+      }
+      __syncthreads();
+    }
+}
+
+// Appends y (where pred) to s_coll through one LDS counter bump per wave; the counter keeps counting
+// past kCap so that an overflow is visible. Called by every lane of the wave.
+__device__ __forceinline__ void append(float y, bool pred, float* s_coll, int* s_n) {
+  const uint64_t bal = __ballot(pred);
+  if (bal == 0) return;
+  const int lane = threadIdx.x % kWave;
+  int base = 0;
+  if (lane == 0) base = atomicAdd(s_n, __popcll(bal));
+  base = __shfl(base, 0, kWave);
+  const int slot = base + __popcll(bal & ((1ull << lane) - 1ull));
+  if (pred && slot < kCap) s_coll[slot] = y;
+}
+
+// Calls f(y, ix, valid) for every element of a row; U 16-byte loads in flight per thread.
+template <bool kDiv, bool kVec, bool kNT, int U = 4, typename F>
+__device__ __forceinline__ void for_each_y(const float* row, int V, double rt, int64_t ban, F&& f) {
+  const int tid = threadIdx.x;
+  int done = 0;
+  if (kVec) {
+    const u32x4* row4 = reinterpret_cast<const u32x4*>(row);
+    const int n4 = V >> 2;
+    for (int base = 0; base < n4; base += kT * U) {
+      u32x4 x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const u32x4* p = row4 + min(base + u * kT + tid, n4 - 1);
+        x[u] = kNT ? __builtin_nontemporal_load(p) : *p;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = base + u * kT + tid;
+        const bool ok = j < n4;
+        const float xs[4] = {__uint_as_float(x[u].x), __uint_as_float(x[u].y), __uint_as_float(x[u].z),
+                             __uint_as_float(x[u].w)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) f(make_y<kDiv>(xs[e], 4 * j + e, rt, ban), 4 * j + e, ok);
+      }
+    }
+    done = n4 << 2;
+  }
+  for (int base = done; base < V; base += kT) {
+    const int ix = base + tid;
+    const bool ok = ix < V;
+    f(make_y<kDiv>(row[ok ? ix : V - 1], ix, rt, ban), ix, ok);
+  }
+}
+
+struct TruncArgs {
+  const float* logits;
+  int64_t batch_stride, row_stride;  // elements
+  int R, V;
+  double rt;    // 1 / temperature
+  int top_k;    // active when 0 < top_k < V
+  float top_p;  // active when < 1
+  int64_t ban;
+  int flags;    // bit 0: skip the window pass (exact radix select only)
+  float* m_out;
+  float* thr_out;
+  double* zk_out;
+  int* status_out;
+  int* passes_out;
+};
+
+// Value histogram of the streaming pass: 1024 bins of 1/16 nat over d = y - mref in (-24, 40]
+// (mref = the sample max); bin 0 holds the largest values. Entries below the range are summed in
+// registers; entries above it (d > 40) send the row to the radix select.
+constexpr int kNB = 1024;
+constexpr float kTop = 40.f;
+constexpr float kPerNat = 16.f;
+__device__ __forceinline__ int bin_of(float d) {
+  return (int)fminf(fmaxf(fmaf(d, -kPerNat, kTop * kPerNat), 0.f), 2048.f);
+}
+
+struct Shared {
+  float coll[kCap];
+  unsigned cnt[kNB];  // histogram bins (the radix select uses the first kBins)
+  double mass[kNB];
+  double red[kTW];
+  int n;
+  int ipar[4];
+  float fpar[4];
+  double dpar[4];
+};
+
+// Count of j < lim with base + sum_{i<j} e_i < target, e_i = exp(s_i - m) in fp64 (a prefix, since
+// the partial sums only grow); *tot = sum_{j<lim} e_j.
+__device__ int count_below(const float* s, int lim, double m, double base, double target, double* tot,
+                           double* sh) {
+  const int L = (lim + kT - 1) / kT;
+  const int j0 = min(lim, (int)threadIdx.x * L), j1 = min(lim, j0 + L);
+  double loc = 0.0;
+  for (int j = j0; j < j1; ++j) loc += exp((double)s[j] - m);
+  const double ex = block_excl_scan(loc, sh, tot);
+  int c = 0;
+  double run = base + ex;
+  for (int j = j0; j < j1; ++j) {
+    c += run < target;
+    run += exp((double)s[j] - m);
+  }
+  return block_isum(c, sh);
+}
+
+// sum over j < n with s_j >= thr of exp(s_j - m)
+__device__ double mass_at_least(const float* s, int n, float thr, double m, double* sh) {
+  double loc = 0.0;
+  for (int j = threadIdx.x; j < n; j += kT) loc += (s[j] >= thr) ? exp((double)s[j] - m) : 0.0;
+  return block_sum(loc, sh);
+}
+
+__device__ int count_cmp(const float* s, int n, float v, bool strictly_greater, double* sh) {
+  int c = 0;
+  for (int j = threadIdx.x; j < n; j += kT) c += strictly_greater ? (s[j] > v) : (s[j] == v);
+  return block_isum(c, sh);
+}
+
+// Pads the collection to a power of two with -inf and sorts it (descending).
+__device__ void sort_collection(Shared& sh, int n) {
+  const int np = next_pow2(max(n, 2));
+  for (int j = n + threadIdx.x; j < np; j += kT) sh.coll[j] = -INFINITY;
+  sort_desc(sh.coll, np);
+}
+
+// One fallback pass over the keys: counts/mass (relative to the exact max m) above khi, and either a
+// histogram of [klo, khi] in digits of 2^shift keys or a collection of that range. On want_z it also
+// sums the whole row's mass and counts its finite entries.
+template <bool kDiv, bool kVec, bool kHist>
+__device__ void range_pass(const float* row, const TruncArgs& a, float m, uint32_t klo, uint32_t khi, int shift,
+                           bool want_z, Shared& sh, int* ca_out, double* ma_out, double* z_out, int* cf_out) {
+  if (kHist)
+    for (int j = threadIdx.x; j < kBins; j += kT) {
+      sh.cnt[j] = 0u;
+      sh.mass[j] = 0.0;
+    }
+  if (threadIdx.x == 0) sh.n = 0;
+  __syncthreads();
+  int ca = 0, cf = 0;
+  double ma = 0.0, z = 0.0;
+  for_each_y<kDiv, kVec, false, 2>(row, a.V, a.rt, a.ban, [&](float y, int ix, bool ok) {
+    const bool fin = ok && (y > -INFINITY);
+    const uint32_t key = fkey(y);
+    const float e = __expf(y - m);
+    const bool above = fin && key > khi;
+    const bool in = fin && key >= klo && key <= khi;
+    ca += above;
+    ma += above ? e : 0.f;
+    if (want_z) {
+      z += fin ? e : 0.f;
+      cf += fin;
+    }
+    if (kHist) {
+      if (in) {
+        const int bin = (int)((key - klo) >> shift);
+        atomicAdd(&sh.cnt[bin], 1u);
+        atomicAdd(&sh.mass[bin], (double)e);
+      }
+    } else {
+      append(y, in, sh.coll, &sh.n);
+    }
+  });
+  *ca_out = block_isum(ca, sh.red);
+  *ma_out = block_sum(ma, sh.red);
+  if (want_z) {
+    *z_out = block_sum(z, sh.red);
+    *cf_out = block_isum(cf, sh.red);
+  }
+  __syncthreads();
+}
+
+// Exact radix select with the exact row max m. Count mode (use_k): the top_k-th largest value; mass
+// mode: the smallest y whose strictly-greater mass is < top_p * Z. Writes thr / Zk (relative to m).
+template <bool kDiv, bool kVec>
+__device__ void radix_resolve(const float* row, const TruncArgs& a, float m, bool use_k, bool use_p, Shared& sh,
+                              float* thr_out, double* zk_out, int* passes) {
+  const double md = (double)m;
+  uint32_t klo = kKeyLo, khi = kKeyHi;
+  int shift = 24;
+  int ca = 0, cf = 0;
+  double ma = 0.0, Z = 0.0, z = 0.0;
+  bool count_mode = use_k;
+  const int k = a.top_k;
+  double tp = 0.0;
+  // results of the select
+  float v = -INFINITY;  // count mode: kth; mass mode: thr
+  int c_gt = 0, c_eq = 0;
+  double zk = 0.0;
+  bool resolved = false;
+  for (int it = 0; !resolved; ++it) {
+    range_pass<kDiv, kVec, true>(row, a, m, klo, khi, shift, it == 0, sh, &ca, &ma, &z, &cf);
+    ++*passes;
+    if (it == 0) {
+      Z = z;
+      if (count_mode && cf <= k) count_mode = false;  // fewer finite entries than k: top-k keeps them all
+      if (!count_mode && !use_p) {                    // nothing left to select
+        *thr_out = -INFINITY;
+        *zk_out = Z;
+        return;
+      }
+      tp = (double)a.top_p * Z;
+    }
+    if (threadIdx.x == 0) {
+      const int nb = (int)(((uint64_t)khi - klo) >> shift) + 1;
+      double cum = count_mode ? (double)ca : ma;
+      int pick = -1, last = -1;
+      double cum_last = cum;
+      for (int bin = nb - 1; bin >= 0; --bin) {
+        if (sh.cnt[bin] == 0u) continue;
+        const double add = count_mode ? (double)sh.cnt[bin] : sh.mass[bin];
+        if ((count_mode && cum + add >= (double)k) || (!count_mode && cum + add >= tp)) {
+          pick = bin;
+          break;
+        }
+        last = bin;
+        cum_last = cum;
+        cum += add;
+      }
+      if (pick < 0) {  // mass mode: every entry qualifies, so the smallest one is the threshold
+        pick = max(last, 0);
+        cum = cum_last;
+      }
+      sh.ipar[0] = pick;
+      sh.dpar[0] = cum;  // count or mass strictly above the picked digit
+    }
+    __syncthreads();
+    const int pick = sh.ipar[0];
+    const double cum = sh.dpar[0];
+    const uint32_t nlo = klo + ((uint32_t)pick << shift);
+    const uint32_t nhi = (uint32_t)min((uint64_t)khi, (uint64_t)nlo + (1ull << shift) - 1ull);
+    const unsigned cnt = sh.cnt[pick];
+    const double bmass = sh.mass[pick];
+    __syncthreads();
+    if (nlo == nhi) {  // one key: every entry of the digit has the same value
+      v = kval(nlo);
+      if (count_mode) {
+        c_gt = (int)cum;
+        c_eq = (int)cnt;
+      } else {
+        zk = cum + bmass;
+      }
+      resolved = true;
+    } else if (cnt <= (unsigned)kCap) {
+      klo = nlo;
+      khi = nhi;
+      int ca2 = 0, cf2 = 0;
+      double ma2 = 0.0, z2 = 0.0;
+      range_pass<kDiv, kVec, false>(row, a, m, klo, khi, 0, false, sh, &ca2, &ma2, &z2, &cf2);
+      ++*passes;
+      const int n = min(sh.n, kCap);
+      sort_collection(sh, n);
+      if (count_mode) {
+        v = sh.coll[min(max(k - 1 - ca2, 0), max(n - 1, 0))];
+        c_gt = ca2 + count_cmp(sh.coll, n, v, true, sh.red);
+        c_eq = count_cmp(sh.coll, n, v, false, sh.red);
+      } else {
+        double tot = 0.0;
+        int nk = count_below(sh.coll, n, md, ma2, tp, &tot, sh.red);
+        nk = min(max(nk, 1), n);
+        v = sh.coll[nk - 1];
+        zk = ma2 + mass_at_least(sh.coll, n, v, md, sh.red);
+      }
+      resolved = true;
+    } else {
+      klo = nlo;
+      khi = nhi;
+      shift = shift >= 8 ? shift - 8 : 0;
+    }
+  }
+  if (!count_mode) {
+    *thr_out = v;
+    *zk_out = zk;
+    return;
+  }
+  // top-k: the values above kth (fewer than k <= kMaxTopK, so they fit), then the nucleus over the
+  // k-value list {values > kth} + (k - c_gt) copies of kth
+  const float kth = v;
+  int ca2 = 0, cf2 = 0;
+  double ma2 = 0.0, z2 = 0.0;
+  const uint32_t kk = fkey(kth);
+  range_pass<kDiv, kVec, false>(row, a, m, kk + 1u, kKeyHi, 0, false, sh, &ca2, &ma2, &z2, &cf2);
+  ++*passes;
+  const int n = min(sh.n, kCap);
+  sort_collection(sh, n);
+  const double e_k = exp((double)kth - md);
+  double s_gt = 0.0;
+  const double copies = (double)(k - c_gt);
+  if (use_p) {
+    double tot = 0.0;
+    // total first: S = sum_{coll} e + copies * e_k
+    (void)count_below(sh.coll, n, md, 0.0, -1.0, &tot, sh.red);
+    s_gt = tot;
+    const double target = (double)a.top_p * (s_gt + copies * e_k);
+    int nk = count_below(sh.coll, n, md, 0.0, target, &tot, sh.red);
+    int ncp = 0;
+    for (int i = threadIdx.x; i < k - c_gt; i += kT) ncp += (s_gt + (double)i * e_k) < target;
+    ncp = block_isum(ncp, sh.red);
+    nk = max(nk + ncp, 1);
+    if (nk <= c_gt) {
+      const float thr = sh.coll[nk - 1];
+      *thr_out = thr;
+      *zk_out = mass_at_least(sh.coll, n, thr, md, sh.red);
+      return;
+    }
+  } else {
+    double tot = 0.0;
+    (void)count_below(sh.coll, n, md, 0.0, -1.0, &tot, sh.red);
+    s_gt = tot;
+  }
+  *thr_out = kth;
+  *zk_out = s_gt + (double)c_eq * e_k;
+}
+
+// Keeps the collected values whose histogram bin lies in [lo, hi], packed at the front of sh.coll;
+// returns how many.
+__device__ int compact_bins(Shared& sh, int n, float mref, int lo, int hi) {
+  constexpr int kPer = kCap / kT;
+  float v[kPer];
+  int keep = 0;
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = (int)threadIdx.x * kPer + u;
+    v[u] = j < n ? sh.coll[j] : -INFINITY;
+    const int bin = bin_of(v[u] - mref);
+    keep += (j < n) && bin >= lo && bin <= hi;
+  }
+  double tot = 0.0;
+  int w = (int)block_excl_scan((double)keep, sh.red, &tot);  // every read of sh.coll precedes its barriers
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = (int)threadIdx.x * kPer + u;
+    const int bin = bin_of(v[u] - mref);
+    if ((j < n) && bin >= lo && bin <= hi) sh.coll[w++] = v[u];
+  }
+  __syncthreads();
+  return (int)tot;
+}
+
+// A second streaming pass that collects the row's values whose histogram bin lies in [lo, hi].
+template <bool kDiv, bool kVec>
+__device__ int collect_bins(const float* row, const TruncArgs& a, float mref, int lo, int hi, Shared& sh) {
+  __syncthreads();
+  if (threadIdx.x == 0) sh.n = 0;
+  __syncthreads();
+  for_each_y<kDiv, kVec, false, 2>(row, a.V, a.rt, a.ban, [&](float y, int ix, bool ok) {
+    const int bin = bin_of((ok ? y : -INFINITY) - mref);
+    append(y, ok && bin >= lo && bin <= hi, sh.coll, &sh.n);
+  });
+  __syncthreads();
+  return sh.n;
+}
+
+template <bool kDiv, bool kVec>
+__global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
+  __shared__ Shared sh;
+  const int r = blockIdx.x;
+  const int b = r / a.R, i = r % a.R;
+  const float* row = a.logits + (int64_t)b * a.batch_stride + (int64_t)i * a.row_stride;
+  const int V = a.V, tid = threadIdx.x;
+  const bool use_k = a.top_k > 0 && a.top_k < V;
+  const bool use_p = a.top_p < 1.f;
+  const bool collect = use_k || use_p;
+  int passes = 0;
+
+  // ---- sample: evenly spaced entries, sorted; their max is the exponent reference of the pass
+  const int ns = min(kSample, V);
+  const int nsp = next_pow2(max(ns, 2));
+  for (int j = tid; j < nsp; j += kT) {
+    float y = -INFINITY;
+    if (j < ns) {
+      const int ix = (int)((int64_t)j * V / ns);
+      y = make_y<kDiv>(row[ix], ix, a.rt, a.ban);
+      if (!(y < INFINITY)) y = -INFINITY;  // NaN / +inf rows are reported by the pass
+    }
+    sh.coll[j] = y;
+  }
+  sort_desc(sh.coll, nsp);
+  const float mref = sh.coll[0];
+  // the window of bins collected by the pass, placed from the sample; about 0.4 * kCap entries of
+  // the row per side of the sample's estimate
+  int w_lo = 1, w_hi = 0;
+  const int spare = (int)min(0.4 * kCap * (double)ns / V, (double)ns);
+  if (use_k) {
+    const double est = (double)a.top_k * ns / V;
+    const int rk = max((int)(est + 4.0 * sqrt(est) + 4.0), spare);
+    w_lo = 0;
+    w_hi = rk < ns ? bin_of(sh.coll[rk] - mref) : kNB - 1;
+  } else if (use_p) {
+    // the sample's own nucleus boundary j*, widened by kW sample ranks on each side
+    const int kW = max(12, spare);
+    const int L = nsp / kT > 0 ? nsp / kT : 1;
+    const int j0 = min(nsp, tid * L), j1 = min(nsp, j0 + L);
+    double loc = 0.0;
+    for (int j = j0; j < j1; ++j) loc += (double)__expf(sh.coll[j] - mref);
+    double W = 0.0;
+    const double ex = block_excl_scan(loc, sh.red, &W);
+    if (tid == 0) sh.ipar[1] = ns - 1;
+    __syncthreads();
+    const double target = (double)a.top_p * W;
+    double run = ex;
+    for (int j = j0; j < j1; ++j) {
+      const double e = (double)__expf(sh.coll[j] - mref);
+      if (run < target && run + e >= target) sh.ipar[1] = j;
+      run += e;
+    }
+    __syncthreads();
+    const int js = sh.ipar[1];
+    w_lo = js - kW >= 0 ? bin_of(sh.coll[js - kW] - mref) : 0;
+    w_hi = js + kW < ns ? bin_of(sh.coll[js + kW] - mref) : kNB - 1;
+  }
+  w_lo = min(w_lo, kNB - 1);
+  w_hi = min(w_hi, kNB - 1);
+  __syncthreads();  // the sample is dead; the collection reuses its LDS
+  for (int j = tid; j < kNB; j += kT) {
+    sh.cnt[j] = 0u;
+    sh.mass[j] = 0.0;
+  }
+  if (tid == 0) sh.n = 0;
+  __syncthreads();
+
+  // ---- the streaming pass: max, histogram, collection of the window
+  float mx = -INFINITY;
+  int bad = 0, big = 0;
+  double mb = 0.0;  // mass below the histogram's range
+  const bool window = !(a.flags & 1);
+  if (window) {
+    for_each_y<kDiv, kVec, true>(row, V, a.rt, a.ban, [&](float y, int ix, bool ok) {
+      const float yy = ok ? y : -INFINITY;
+      bad |= ok && !(y < INFINITY);
+      mx = fmaxf(mx, yy);
+      const float d = yy - mref;
+      big |= d > kTop;
+      const float e = __expf(d);
+      const int bin = bin_of(d);
+      if (bin < kNB) {
+        atomicAdd(&sh.cnt[bin], 1u);
+        atomicAdd(&sh.mass[bin], (double)e);
+      } else {
+        mb += e;
+      }
+      if (collect) append(yy, bin >= w_lo && bin <= w_hi, sh.coll, &sh.n);
+    });
+  } else {
+    for_each_y<kDiv, kVec, true>(row, V, a.rt, a.ban, [&](float y, int ix, bool ok) {
+      bad |= ok && !(y < INFINITY);
+      mx = fmaxf(mx, ok ? y : -INFINITY);
+    });
+  }
+  ++passes;
+  mx = block_max(mx, sh.red);
+  bad = block_isum(bad, sh.red);
+  float thr = -INFINITY;
+  double zk = 0.0;
+  int status = 0;
+  if (bad) {
+    status = 1;
+  } else if (!(mx > -INFINITY)) {
+    status = 2;
+  } else {
+    bool ok = window && (mref > -INFINITY) && !block_isum(big, sh.red);
+    mb = block_sum(mb, sh.red);
+    __syncthreads();
+    const int n = sh.n;
+    const double md = (double)mx;
+    const double scale = exp((double)mref - md);
+    if (ok) {
+      // each thread owns kNB / kT consecutive bins; exclusive scans give the mass / count above each
+      constexpr int kBPT = kNB / kT;
+      double lm = 0.0, lc = 0.0;
+#pragma unroll
+      for (int u = 0; u < kBPT; ++u) {
+        lm += sh.mass[tid * kBPT + u];
+        lc += (double)sh.cnt[tid * kBPT + u];
+      }
+      double zb = 0.0, cbins = 0.0;
+      const double exm = block_excl_scan(lm, sh.red, &zb);
+      const double exc = block_excl_scan(lc, sh.red, &cbins);
+      const double Z = zb + mb;
+      if (!collect) {
+        zk = Z * scale;
+      } else {
+        // the bin holding the k-th largest value (top-k) or the nucleus boundary (top-p)
+        const double tgt = use_k ? (double)a.top_k : (double)a.top_p * Z;
+        if (tid == 0) sh.ipar[0] = INT_MAX;
+        __syncthreads();
+        double run = use_k ? exc : exm;
+#pragma unroll
+        for (int u = 0; u < kBPT; ++u) {
+          const int bin = tid * kBPT + u;
+          const double add = use_k ? (double)sh.cnt[bin] : sh.mass[bin];
+          if (run < tgt && run + add >= tgt) atomicMin(&sh.ipar[0], bin);
+          run += add;
+        }
+        __syncthreads();
+        const int B = sh.ipar[0];
+        if (B != INT_MAX && tid == B / kBPT) {  // the owner publishes the count / mass above the bin
+          double cum = use_k ? exc : exm;
+          for (int u = 0; u < B % kBPT; ++u)
+            cum += use_k ? (double)sh.cnt[tid * kBPT + u] : sh.mass[tid * kBPT + u];
+          sh.dpar[0] = cum;
+        }
+        __syncthreads();
+        if (B == INT_MAX) {
+          ok = false;  // the target lies below the histogram's range
+        } else {
+          const double cum = sh.dpar[0];
+          const int c_lo = use_k ? 0 : B;
+          const int need = (int)((use_k ? cum : 0.0) + (double)sh.cnt[B]);
+          if (need > kCap) {
+            ok = false;
+          } else {
+            int n2;
+            if (c_lo >= w_lo && B <= w_hi && n <= kCap) {
+              n2 = compact_bins(sh, n, mref, c_lo, B);
+            } else {
+              n2 = collect_bins<kDiv, kVec>(row, a, mref, c_lo, B, sh);
+              ++passes;
+            }
+            n2 = min(n2, kCap);
+            sort_collection(sh, n2);
+            if (use_k) {
+              const int k = min(a.top_k, n2);
+              thr = sh.coll[k - 1];
+              if (use_p) {
+                double Sk = 0.0, tot = 0.0;
+                (void)count_below(sh.coll, k, md, 0.0, -1.0, &Sk, sh.red);
+                const int nk = max(count_below(sh.coll, k, md, 0.0, (double)a.top_p * Sk, &tot, sh.red), 1);
+                thr = sh.coll[nk - 1];
+              }
+              zk = mass_at_least(sh.coll, n2, thr, md, sh.red);
+            } else {
+              const double base = cum * scale, target = tgt * scale;
+              double tot = 0.0;
+              const int nk = min(max(count_below(sh.coll, n2, md, base, target, &tot, sh.red), 1), max(n2, 1));
+              thr = sh.coll[nk - 1];
+              zk = base + mass_at_least(sh.coll, n2, thr, md, sh.red);
+            }
+          }
+        }
+      }
+    }
+    if (!ok) radix_resolve<kDiv, kVec>(row, a, mx, use_k, use_p, sh, &thr, &zk, &passes);
+  }
+  if (tid == 0) {
+    a.m_out[r] = mx;
+    a.thr_out[r] = thr;
+    a.zk_out[r] = zk;
+    a.status_out[r] = status;
+    if (a.passes_out) a.passes_out[r] = passes;
+  }
+}
+
+// ---------------------------------------------------------------- acceptance and correction
+struct AcceptArgs {
+  const float* p;
+  int64_t p_bs, p_rs;
+  const float* q;
+  int64_t q_bs, q_rs;
+  const int64_t* drafts;
+  int64_t d_st;
+  const int32_t* n_live;
+  const float* u_acc;
+  int64_t u_st;
+  const float* u_samp;
+  const int64_t* ctx;
+  int B, V, K;
+  double rt;  // 1 / temperature
+  int64_t ban;
+  const float* m;  // [B * (K + 1)] row statistics
+  const float* thr;
+  const double* zk;
+  const int* status;
+  int NC, chunk;
+  double* sums;  // [B][NC][2]: correction weight, P
+  int32_t* n_acc;
+  int64_t* token;
+  int64_t* crop;
+  double* ratio;  // [B, K] or null
+  int32_t* status_out;
+};
+
+// P_row(x) in fp64 from the row statistics (0 outside the kept set).
+__device__ __forceinline__ double prob_of(const AcceptArgs& a, int srow, float x, int ix) {
+  const float y = make_y<true>(x, ix, a.rt, a.ban);  // the product with rt = 1 is exact
+  if (!(y > -INFINITY) || !(y >= a.thr[srow])) return 0.0;
+  return exp((double)y - (double)a.m[srow]) / a.zk[srow];
+}
+
+// Weight of token ix in the correction draw of sequence b at row r (r < K: residual, r == K: P_K).
+__device__ __forceinline__ void weights_of(const AcceptArgs& a, int b, int r, int ix, double* w, double* pp) {
+  const int srow = b * (a.K + 1) + r;
+  const double P = prob_of(a, srow, a.p[(int64_t)b * a.p_bs + (int64_t)r * a.p_rs + ix], ix);
+  *pp = P;
+  if (r < a.K) {
+    const double q = (double)a.q[(int64_t)b * a.q_bs + (int64_t)r * a.q_rs + ix];
+    *w = fmax(P - q, 0.0);
+  } else {
+    *w = P;
+  }
+}
+
+__device__ __forceinline__ double rblock_sum(double v, double* sh) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  __syncthreads();
+  if (threadIdx.x % kWave == 0) sh[threadIdx.x / kWave] = v;
+  __syncthreads();
+  double t = 0.0;
+#pragma unroll
+  for (int w = 0; w < kRT / kWave; ++w) t += sh[w];
+  return t;
+}
+
+__global__ __launch_bounds__(kRT) void resid_sums_kernel(AcceptArgs a) {
+  const int c = blockIdx.x, b = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  __shared__ int s_nacc;
+  __shared__ double s_red[kRT / kWave];
+  if (tid < kWave) {
+    const int i = lane;
+    const int live = a.n_live ? min(max((int)a.n_live[b], 0), a.K) : a.K;
+    bool acc = false;
+    double ratio = 0.0;
+    if (i < a.K) {
+      const int64_t d = a.drafts[(int64_t)b * a.d_st + i];
+      if (d >= 0 && d < a.V) {
+        const int srow = b * (a.K + 1) + i;
+        const double P = prob_of(a, srow, a.p[(int64_t)b * a.p_bs + (int64_t)i * a.p_rs + d], (int)d);
+        const double q = (double)a.q[(int64_t)b * a.q_bs + (int64_t)i * a.q_rs + d];
+        ratio = q > 0.0 ? P / fmax(q, 1e-30) : 0.0;
+        acc = (i < live) && (ratio >= 1.0 || (double)a.u_acc[(int64_t)b * a.u_st + i] < ratio);
+      }
+    }
+    const uint64_t lead = ~__ballot(acc);
+    const int n = lead == 0ull ? kWave : __builtin_ctzll(lead);
+    const int n_acc = min(n, a.K);
+    // any invalid row among 0..K
+    int st = 0;
+    for (int r = lane; r <= a.K; r += kWave) st |= a.status[b * (a.K + 1) + r];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) st |= __shfl_xor(st, off, kWave);
+    if (lane == 0) s_nacc = n_acc;
+    if (c == 0) {
+      if (a.ratio && i < a.K) a.ratio[(int64_t)b * a.K + i] = ratio;
+      if (lane == 0) {
+        a.n_acc[b] = n_acc;
+        a.crop[b] = (a.ctx ? a.ctx[b] : 0) + 1 + n_acc;
+        a.status_out[b] = st;
+      }
+    }
+  }
+  __syncthreads();
+  const int r = s_nacc;
+  const int lo = c * a.chunk, hi = min(a.V, lo + a.chunk);
+  double sw = 0.0, sp = 0.0;
+  for (int ix = lo + tid; ix < hi; ix += kRT) {
+    double w, pp;
+    weights_of(a, b, r, ix, &w, &pp);
+    sw += w;
+    sp += pp;
+  }
+  sw = rblock_sum(sw, s_red);
+  sp = rblock_sum(sp, s_red);
+  if (tid == 0) {
+    a.sums[((int64_t)b * a.NC + c) * 2 + 0] = sw;
+    a.sums[((int64_t)b * a.NC + c) * 2 + 1] = sp;
+  }
+}
+
+__global__ __launch_bounds__(kRT) void resid_pick_kernel(AcceptArgs a) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int lane = tid % kWave, w = tid / kWave;
+  __shared__ int s_chunk, s_last, s_tok, s_sel;
+  __shared__ double s_t;
+  __shared__ double s_red[kRT / kWave];
+  const int r = a.n_acc[b];
+  if (tid == 0) {
+    const double* s = a.sums + (int64_t)b * a.NC * 2;
+    double tw = 0.0, tp = 0.0;
+    for (int c = 0; c < a.NC; ++c) {
+      tw += s[2 * c];
+      tp += s[2 * c + 1];
+    }
+    const int sel = tw > 0.0 ? 0 : 1;  // an empty residual draws from P itself
+    const double total = sel ? tp : tw;
+    const double t = (double)a.u_samp[b] * total;
+    double cum = 0.0;
+    int pick = -1, lastpos = -1;
+    for (int c = 0; c < a.NC; ++c) {
+      const double v = s[2 * c + sel];
+      if (v > 0.0) lastpos = c;
+      if (pick < 0 && cum + v > t) {
+        pick = c;
+        break;
+      }
+      cum += v;
+    }
+    s_last = pick < 0;
+    s_chunk = pick < 0 ? max(lastpos, 0) : pick;
+    s_t = t - cum;
+    s_tok = INT_MAX;
+    s_sel = sel;
+  }
+  __syncthreads();
+  const int c = s_chunk, sel = s_sel;
+  const bool last = s_last;
+  const double t = s_t;
+  const int lo = c * a.chunk, hi = min(a.V, lo + a.chunk);
+  const int L = (hi - lo + kRT - 1) / kRT;
+  const int j0 = min(hi, lo + tid * L), j1 = min(hi, j0 + L);
+  double loc = 0.0;
+  int lastpos = -1;
+  for (int ix = j0; ix < j1; ++ix) {
+    double wt, pp;
+    weights_of(a, b, r, ix, &wt, &pp);
+    const double v = sel ? pp : wt;
+    loc += v;
+    if (v > 0.0) lastpos = ix;
+  }
+  // exclusive scan over the block (thread order = vocabulary order)
+  double inc = loc;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const double o = __shfl_up(inc, off, kWave);
+    if (lane >= off) inc += o;
+  }
+  double ex = __shfl_up(inc, 1, kWave);
+  if (lane == 0) ex = 0.0;
+  if (lane == kWave - 1) s_red[w] = inc;
+  __syncthreads();
+  for (int i = 0; i < w; ++i) ex += s_red[i];
+  int found = INT_MAX;
+  if (!last && ex <= t && t < ex + loc) {
+    double run = ex;
+    for (int ix = j0; ix < j1; ++ix) {
+      double wt, pp;
+      weights_of(a, b, r, ix, &wt, &pp);
+      run += sel ? pp : wt;
+      if (run > t) {
+        found = ix;
+        break;
+      }
+    }
+  }
+  if (found != INT_MAX) atomicMin(&s_tok, found);
+  // the last positive-weight token of the chunk: used when u * total lands past the summed weight
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) lastpos = max(lastpos, __shfl_xor(lastpos, off, kWave));
+  __syncthreads();
+  if (lane == 0) s_red[w] = (double)lastpos;
+  __syncthreads();
+  if (tid == 0) {
+    int lp = -1;
+    for (int i = 0; i < kRT / kWave; ++i) lp = max(lp, (int)s_red[i]);
+    const int tok = s_tok != INT_MAX ? s_tok : max(lp, 0);
+    a.token[b] = tok;
+  }
+}
+
+bool vec_ok(const void* p, int64_t V, int64_t bs, int64_t rs) {
+  return ((uintptr_t)p % 16 == 0) && V % 4 == 0 && bs % 4 == 0 && rs % 4 == 0;
+}
+
+int launch_truncate(const TruncArgs& ta, int rows, bool vec, hipStream_t st) {
+  const bool div = ta.rt != 1.0;
+  if (div && vec) hipLaunchKernelGGL((truncate_kernel<true, true>), dim3(rows), dim3(kT), 0, st, ta);
+  else if (div) hipLaunchKernelGGL((truncate_kernel<true, false>), dim3(rows), dim3(kT), 0, st, ta);
+  else if (vec) hipLaunchKernelGGL((truncate_kernel<false, true>), dim3(rows), dim3(kT), 0, st, ta);
+  else hipLaunchKernelGGL((truncate_kernel<false, false>), dim3(rows), dim3(kT), 0, st, ta);
+  return launch_status("truncate_kernel");
+}
+
+int check_trunc_params(int64_t V, float temperature, int64_t top_k, float top_p) {
+  TRIDA_CHECK(V > 0 && V < INT_MAX / 2, TRIDA_ERR_ARG, "V=%lld out of range", (long long)V);
+  TRIDA_CHECK(temperature > 0.f && temperature < INFINITY, TRIDA_ERR_ARG,
+              "temperature must be positive and finite (greedy decoding has its own entry point)");
+  TRIDA_CHECK(top_p > 0.f && top_p <= 1.f, TRIDA_ERR_ARG, "top_p must lie in (0, 1]");
+  TRIDA_CHECK(top_k >= 0, TRIDA_ERR_ARG, "top_k must be >= 0 (0 disables it)");
+  TRIDA_CHECK(top_k == 0 || top_k >= V || top_k <= kMaxTopK, TRIDA_ERR_ARG, "top_k=%lld above the supported %d",
+              (long long)top_k, kMaxTopK);
+  return TRIDA_OK;
+}
+
+void plan_chunks(int64_t B, int64_t V, int* NC, int* chunk) {
+  int nc = (int)std::min<int64_t>(64, std::max<int64_t>(1, cdiv(1024, B)));
+  nc = (int)std::min<int64_t>(nc, std::max<int64_t>(1, cdiv(V, 1024)));
+  *chunk = (int)cdiv(V, nc);
+  *NC = (int)cdiv(V, *chunk);
+}
+
+struct ScratchLayout {
+  int64_t m, thr, zk, status, sums, total;
+};
+ScratchLayout layout(int64_t B, int64_t K, int64_t V) {
+  int NC, chunk;
+  plan_chunks(B, V, &NC, &chunk);
+  const int64_t rows = B * (K + 1);
+  ScratchLayout L;
+  L.m = 0;
+  L.thr = L.m + align_up(rows * 4, 256);
+  L.zk = L.thr + align_up(rows * 4, 256);
+  L.status = L.zk + align_up(rows * 8, 256);
+  L.sums = L.status + align_up(rows * 4, 256);
+  L.total = L.sums + align_up(B * NC * 2 * 8, 256);
+  return L;
+}
+
+}  // namespace
+}  // namespace trida
+
+using namespace trida;
+
+extern "C" int trida_truncate_stats(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                                    int64_t row_stride, float temperature, int64_t top_k, float top_p,
+                                    int64_t ban_id, int flags, float* m_out, float* thr_out, double* zk_out,
+                                    int32_t* status_out, int32_t* passes_out, void* stream) {
+  TRIDA_CHECK(logits && m_out && thr_out && zk_out && status_out, TRIDA_ERR_NULL, "null pointer argument");
+  TRIDA_CHECK(B > 0 && R > 0 && B * R < INT_MAX, TRIDA_ERR_ARG, "bad B=%lld R=%lld", (long long)B, (long long)R);
+  const int rc = check_trunc_params(V, temperature, top_k, top_p);
+  if (rc != TRIDA_OK) return rc;
+  TRIDA_CHECK(row_stride >= V && (B == 1 || batch_stride >= (R - 1) * row_stride + V), TRIDA_ERR_ARG,
+              "strides too small");
+  TruncArgs ta{logits, batch_stride, row_stride, (int)R, (int)V, 1.0 / (double)temperature, (int)top_k, top_p, ban_id, flags,
+               m_out, thr_out, zk_out, status_out, passes_out};
+  return launch_truncate(ta, (int)(B * R), vec_ok(logits, V, batch_stride, row_stride),
+                         static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t trida_sample_accept_scratch_bytes(int64_t B, int64_t R, int64_t V, int64_t K) {
+  (void)R;
+  if (B <= 0 || V <= 0 || K < 0) return -1;
+  return layout(B, K, V).total;
+}
+
+extern "C" int trida_sample_accept(const float* p_logits, int64_t B, int64_t R, int64_t V, int64_t p_batch_stride,
+                                   int64_t p_row_stride, const float* q_probs, int64_t q_batch_stride,
+                                   int64_t q_row_stride, const int64_t* drafts, int64_t K, int64_t draft_stride,
+                                   const int32_t* n_live, const float* u_accept, int64_t u_stride,
+                                   const float* u_sample, const int64_t* ctx_len, float temperature, int64_t top_k,
+                                   float top_p, int64_t ban_id, int32_t* n_acc, int64_t* token, int64_t* crop,
+                                   double* ratio, int32_t* status, void* scratch, int64_t scratch_bytes,
+                                   void* stream_) {
+  hipStream_t stream = static_cast<hipStream_t>(stream_);
+  TRIDA_CHECK(p_logits && u_sample && n_acc && token && crop && status && scratch, TRIDA_ERR_NULL,
+              "null pointer argument");
+  TRIDA_CHECK(K == 0 || (q_probs && drafts && u_accept), TRIDA_ERR_NULL, "q_probs, drafts and u_accept are needed when K > 0");
+  TRIDA_CHECK(B > 0 && B <= 65535 && K >= 0 && K <= kWave && R >= K + 1, TRIDA_ERR_ARG,
+              "need 0 < B <= 65535, 0 <= K <= 64 and R >= K + 1 (B=%lld K=%lld R=%lld)", (long long)B, (long long)K,
+              (long long)R);
+  const int rc = check_trunc_params(V, temperature, top_k, top_p);
+  if (rc != TRIDA_OK) return rc;
+  TRIDA_CHECK(p_row_stride >= V && (B == 1 || p_batch_stride >= (R - 1) * p_row_stride + V), TRIDA_ERR_ARG,
+              "p strides too small");
+  TRIDA_CHECK(K == 0 || (q_row_stride >= V && (B == 1 || (q_batch_stride >= (K - 1) * q_row_stride + V &&
+                                                          draft_stride >= K && u_stride >= K))),
+              TRIDA_ERR_ARG, "q / draft / uniform strides too small");
+  const ScratchLayout L = layout(B, K, V);
+  TRIDA_CHECK(scratch_bytes >= L.total, TRIDA_ERR_WORKSPACE, "scratch of %lld bytes, need %lld",
+              (long long)scratch_bytes, (long long)L.total);
+  TRIDA_CHECK((uintptr_t)scratch % 256 == 0, TRIDA_ERR_ALIGN, "scratch must be 256-byte aligned");
+  char* s = static_cast<char*>(scratch);
+  float* m = reinterpret_cast<float*>(s + L.m);
+  float* thr = reinterpret_cast<float*>(s + L.thr);
+  double* zk = reinterpret_cast<double*>(s + L.zk);
+  int* st = reinterpret_cast<int*>(s + L.status);
+  double* sums = reinterpret_cast<double*>(s + L.sums);
+
+  // statistics of rows 0..K of every sequence (the rows past K are not needed)
+  TruncArgs ta{p_logits, p_batch_stride, p_row_stride, (int)(K + 1), (int)V, 1.0 / (double)temperature, (int)top_k,
+               top_p, ban_id,
+               0, m, thr, zk, st, nullptr};
+  int r = launch_truncate(ta, (int)(B * (K + 1)), vec_ok(p_logits, V, p_batch_stride, p_row_stride), stream);
+  if (r != TRIDA_OK) return r;
+
+  int NC, chunk;
+  plan_chunks(B, V, &NC, &chunk);
+  AcceptArgs aa{p_logits, p_batch_stride, p_row_stride, q_probs, q_batch_stride, q_row_stride, drafts, draft_stride,
+                n_live, u_accept, u_stride, u_sample, ctx_len, (int)B, (int)V, (int)K, 1.0 / (double)temperature, ban_id,
+                m, thr,
+                zk, st, NC, chunk, sums, n_acc, token, crop, ratio, status};
+  hipLaunchKernelGGL(resid_sums_kernel, dim3(NC, B), dim3(kRT), 0, stream, aa);
+  r = launch_status("resid_sums_kernel");
+  if (r != TRIDA_OK) return r;
+  hipLaunchKernelGGL(resid_pick_kernel, dim3(B), dim3(kRT), 0, stream, aa);
+  return launch_status("resid_pick_kernel");
+}
+
+namespace trida {
+namespace {
+__global__ __launch_bounds__(256) void probs_kernel(const float* logits, int64_t bs, int64_t rs, int R, int V,
+                                                    double rt, int64_t ban, const float* m, const float* thr,
+                                                    const double* zk, float* out, int64_t obs, int64_t ors) {
+  const int r = blockIdx.y;
+  const int b = r / R, i = r % R;
+  const float* row = logits + (int64_t)b * bs + (int64_t)i * rs;
+  float* o = out + (int64_t)b * obs + (int64_t)i * ors;
+  const float mm = m[r], t = thr[r];
+  const float inv = (float)(1.0 / zk[r]);
+  for (int ix = blockIdx.x * 256 + threadIdx.x; ix < V; ix += gridDim.x * 256) {
+    const float y = make_y<true>(row[ix], ix, rt, ban);
+    o[ix] = (y > -INFINITY && y >= t) ? __expf(y - mm) * inv : 0.f;
+  }
+}
+}  // namespace
+}  // namespace trida
+
+extern "C" int trida_truncated_probs(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                                     int64_t row_stride, float temperature, int64_t ban_id, const float* m,
+                                     const float* thr, const double* zk, float* probs, int64_t out_batch_stride,
+                                     int64_t out_row_stride, void* stream) {
+  TRIDA_CHECK(logits && m && thr && zk && probs, TRIDA_ERR_NULL, "null pointer argument");
+  TRIDA_CHECK(B > 0 && R > 0 && B * R <= 65535 && V > 0 && V < INT_MAX / 2, TRIDA_ERR_ARG, "bad shape");
+  TRIDA_CHECK(temperature > 0.f && temperature < INFINITY, TRIDA_ERR_ARG, "temperature must be positive");
+  TRIDA_CHECK(row_stride >= V && out_row_stride >= V &&
+                  (B == 1 || (batch_stride >= (R - 1) * row_stride + V &&
+                              out_batch_stride >= (R - 1) * out_row_stride + V)),
+              TRIDA_ERR_ARG, "strides too small");
+  const int gx = (int)std::min<int64_t>(cdiv(V, 256 * 8), 256);
+  hipLaunchKernelGGL(probs_kernel, dim3(gx, B * R), dim3(256), 0, static_cast<hipStream_t>(stream), logits, batch_stride, row_stride, (int)R,
+                     (int)V, 1.0 / (double)temperature, ban_id, m, thr, zk, probs, out_batch_stride, out_row_stride);
+  return launch_status("probs_kernel");
+}

@@ -157,6 +157,110 @@ def row_argmax(logits: torch.Tensor, *, want_conf: bool = True, splits: int = 0,
 
 
 # --------------------------------------------------------------------------------------------------
+# Sampled acceptance (temperature / top-k / top-p, speculative rejection sampling)
+MAX_TOP_K = 4096
+
+
+def _f32_rows(t: torch.Tensor, name: str, dims: int = 3):
+    if t.dtype != torch.float32 or t.dim() != dims or t.stride(-1) != 1:
+        raise ValueError(f"{name} must be fp32 with {dims} dims and a contiguous last dim")
+
+
+def truncate_stats(logits: torch.Tensor, *, temperature: float, top_k: int = 0, top_p: float = 1.0,
+                   ban_id: int = -1, radix_only: bool = False, want_passes: bool = False):
+    """Statistics of truncated_probs (inference/zoro-1/mlx/trida_mlx/decode.py:102-130) per row of
+    logits [B, R, V] fp32: m = max y (y = logit / T, ban_id at -inf), thr = smallest kept y, zk = sum of
+    exp(y - m) over the kept set. Returns (m [B,R] fp32, thr [B,R] fp32, zk [B,R] fp64, status [B,R]
+    int32[, passes [B,R] int32])."""
+    dev = _need_gpu(logits)
+    _f32_rows(logits, "logits")
+    B, R, V = logits.shape
+    m = torch.empty((B, R), dtype=torch.float32, device=dev)
+    thr = torch.empty_like(m)
+    zk = torch.empty((B, R), dtype=torch.float64, device=dev)
+    st = torch.empty((B, R), dtype=torch.int32, device=dev)
+    passes = torch.empty((B, R), dtype=torch.int32, device=dev) if want_passes else None
+    rc = _lib.load().trida_truncate_stats(
+        logits.data_ptr(), B, R, V, logits.stride(0), logits.stride(1), float(temperature), int(top_k),
+        float(top_p), int(ban_id), 1 if radix_only else 0, m.data_ptr(), thr.data_ptr(), zk.data_ptr(),
+        st.data_ptr(), _ptr(passes), _stream(dev))
+    _lib.check(rc, "trida_truncate_stats")
+    return (m, thr, zk, st, passes) if want_passes else (m, thr, zk, st)
+
+
+def truncated_probs(logits: torch.Tensor, stats, *, temperature: float, ban_id: int = -1,
+                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Truncated distributions P [B, R, V] fp32 from ``truncate_stats`` output (the probability rows the
+    reference keeps as the next step's draft distributions, decode.py:354, 378)."""
+    dev = _need_gpu(logits)
+    _f32_rows(logits, "logits")
+    B, R, V = logits.shape
+    m, thr, zk = stats[0], stats[1], stats[2]
+    for t, dt in ((m, torch.float32), (thr, torch.float32), (zk, torch.float64)):
+        if t.dtype != dt or t.shape != (B, R) or not t.is_contiguous():
+            raise ValueError("stats must be the (m, thr, zk) tensors of truncate_stats for these logits")
+    if out is None:
+        out = torch.empty((B, R, V), dtype=torch.float32, device=dev)
+    _f32_rows(out, "out")
+    rc = _lib.load().trida_truncated_probs(
+        logits.data_ptr(), B, R, V, logits.stride(0), logits.stride(1), float(temperature), int(ban_id),
+        m.data_ptr(), thr.data_ptr(), zk.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1), _stream(dev))
+    _lib.check(rc, "trida_truncated_probs")
+    return out
+
+
+def sample_accept(p_logits: torch.Tensor, q_probs: Optional[torch.Tensor], drafts: torch.Tensor,
+                  u_accept: Optional[torch.Tensor], u_sample: torch.Tensor, *, temperature: float,
+                  top_k: int = 0, top_p: float = 1.0, ban_id: int = -1, n_live: Optional[torch.Tensor] = None,
+                  ctx_len: Optional[torch.Tensor] = None, want_ratio: bool = False, out=None):
+    """Sampled acceptance of a verify pass (selfspec_generate's sampled verify,
+    inference/zoro-1/mlx/trida_mlx/decode.py:333-354): per draft ratio P_i(d_i) / q_i(d_i), accepted while
+    ``ratio >= 1 or u < ratio``; the correction (or, when every draft is accepted, the bonus) is drawn by
+    inverse CDF at ``u_sample`` from max(0, P_a - q_a) (P_a when that is empty) or P_K.
+
+    p_logits [B, R, V] fp32, q_probs [B, K, V] fp32, drafts [B, K] int64, u_accept [B, K] fp32,
+    u_sample [B] fp32. Returns (n_acc [B] int32, token [B] int64, crop [B] int64, ratio [B, K] fp64 or
+    None, status [B] int32)."""
+    dev = _need_gpu(p_logits, q_probs, drafts, u_accept, u_sample, n_live, ctx_len)
+    _f32_rows(p_logits, "p_logits")
+    B, R, V = p_logits.shape
+    if drafts.dtype != torch.int64 or drafts.dim() != 2 or drafts.shape[0] != B or (
+            drafts.shape[1] > 0 and drafts.stride(1) != 1):
+        raise ValueError("drafts must be int64 [B, K] with a contiguous last dim")
+    K = drafts.shape[1]
+    if K:
+        _f32_rows(q_probs, "q_probs")
+        if q_probs.shape != (B, K, V):
+            raise ValueError(f"q_probs must be [B, K, V] = {(B, K, V)}")
+        _f32_rows(u_accept, "u_accept", 2)
+        if u_accept.shape != (B, K):
+            raise ValueError("u_accept must be [B, K]")
+    if u_sample.dtype != torch.float32 or u_sample.shape != (B,) or not u_sample.is_contiguous():
+        raise ValueError("u_sample must be fp32 [B]")
+    if n_live is not None and (n_live.dtype != torch.int32 or n_live.shape != (B,) or not n_live.is_contiguous()):
+        raise ValueError("n_live must be int32 [B]")
+    if ctx_len is not None and (ctx_len.dtype != torch.int64 or ctx_len.shape != (B,) or not ctx_len.is_contiguous()):
+        raise ValueError("ctx_len must be int64 [B]")
+    lib = _lib.load()
+    if out is None:
+        out = (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
+               torch.empty(B, dtype=torch.int64, device=dev),
+               torch.empty((B, K), dtype=torch.float64, device=dev) if want_ratio else None,
+               torch.empty(B, dtype=torch.int32, device=dev))
+    n_acc, token, crop, ratio, status = out
+    scr = workspaces.get(dev, "sample", lib.trida_sample_accept_scratch_bytes(B, R, V, K))
+    rc = lib.trida_sample_accept(
+        p_logits.data_ptr(), B, R, V, p_logits.stride(0), p_logits.stride(1), _ptr(q_probs),
+        q_probs.stride(0) if K else 0, q_probs.stride(1) if K else 0, drafts.data_ptr(), K,
+        drafts.stride(0) if K else 0,
+        _ptr(n_live), _ptr(u_accept), u_accept.stride(0) if K else 0, u_sample.data_ptr(), _ptr(ctx_len),
+        float(temperature), int(top_k), float(top_p), int(ban_id), n_acc.data_ptr(), token.data_ptr(),
+        crop.data_ptr(), _ptr(ratio), status.data_ptr(), scr.data_ptr(), scr.numel(), _stream(dev))
+    _lib.check(rc, "trida_sample_accept")
+    return out
+
+
+# --------------------------------------------------------------------------------------------------
 # GDN (gated delta net) layer pieces
 def _bf16(t: torch.Tensor, name: str):
     if t.dtype != torch.bfloat16:
