@@ -1,6 +1,6 @@
 """Benchmark of the MI355X self-speculative decode step.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload accept]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|accept|sample|gemm]
 
 Prints ONE JSON line (rank 0). One GPU only: --gpus above 1 exits with a message.
 """
@@ -90,6 +90,80 @@ def bench_accept(args):
         "data": "synthetic",
         "config": {"workload": "greedy acceptance, batch 1, block 32, vocab 151936, ctx 4096",
                    "n_acc": n_acc},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
+# ------------------------------------------------------------------------------ sampled acceptance
+def bench_sample(args):
+    """Rejection-sampling acceptance of one bs64 verify step: p logits [64, 33, 248320] fp32 ~ N(0, 4),
+    draft distributions q [64, 32, 248320] fp32 (truncated probabilities of perturbed logits), drafts
+    drawn from q, temperature 0.7, top-p 0.95, seeded uniforms."""
+    import torch
+
+    from trida_stack_amd import kernels
+
+    dev = torch.device("cuda:0")
+    B, K, V, T, TOP_P = 64, 32, 248320, 0.7, 0.95
+    g = torch.Generator(device=dev).manual_seed(0)
+    pl = torch.randn(B, K + 1, V, generator=g, device=dev) * 2
+    ql = pl[:, :K] + torch.randn(B, K, V, generator=g, device=dev) * 0.3
+    q = kernels.truncated_probs(ql, kernels.truncate_stats(ql, temperature=T, top_p=TOP_P), temperature=T)
+    del ql
+    drafts = torch.multinomial(q.reshape(-1, V), 1, generator=g).reshape(B, K)
+    ua = torch.rand(B, K, generator=g, device=dev)
+    us = torch.rand(B, generator=g, device=dev)
+    ctx = torch.full((B,), 4096, dtype=torch.int64, device=dev)
+    out = [torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
+           torch.empty(B, dtype=torch.int64, device=dev), None, torch.empty(B, dtype=torch.int32, device=dev)]
+    fn = lambda: kernels.sample_accept(pl, q, drafts, ua, us, temperature=T, top_p=TOP_P, ctx_len=ctx, out=out)
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fn()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    kern_ms = _events_time_ms(fn, 20)
+    passes = kernels.truncate_stats(pl, temperature=T, top_p=TOP_P, want_passes=True)[4]
+    one_pass = float((passes == 4).float().mean())  # 4 streamed quarter-rows = one pass
+    mean_passes = float(passes.float().mean()) / 4
+    n_acc = out[0].cpu()
+    # Bytes this algorithm must read: the verify rows it evaluates (the first group of G0 rows of every
+    # sequence, all K + 1 rows of the sequences that accept past it), then the correction row of p and
+    # q per sequence. The reference evaluates every verify row (B * (K + 1) * V * 4 bytes + the
+    # correction rows); that figure is reported alongside.
+    G0 = min(K + 1, max(8, -(-512 // B)))
+    rows_read = int(sum(G0 if int(n) < G0 else K + 1 for n in n_acc))
+    nbytes = rows_read * V * 4 + B * 2 * V * 4
+    ref_bytes = B * (K + 1) * V * 4 + B * 2 * V * 4
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        from oracle import accept as A
+
+        ns = 2
+        p_np, q_np = pl[:ns].cpu().numpy(), q[:ns].cpu().numpy()
+        d_np, ua_np, us_np = drafts[:ns].cpu().numpy(), ua[:ns].cpu().numpy(), us[:ns].cpu().numpy()
+        t = time.perf_counter()
+        A.rejection_accept(p_np, q_np, d_np, ua_np, us_np, temperature=T, top_p=TOP_P)
+        per_seq = (time.perf_counter() - t) / ns
+        cpu = {"value": round(per_seq * B * 1e3, 1), "unit": "ms per bs64 verify step (extrapolated)", "cores": 1,
+               "kind": "port", "sample": f"oracle rejection_accept on {ns} of the 64 sequences (33 x 248320 fp32 "
+                                         f"rows each, numpy float64), x {B // ns}"}
+    return {
+        "metric": METRIC, "value": round(kern_ms * 1e3, 1), "unit": "us per bs64 sampled verify step (kernels)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "sampled acceptance, batch 64, block 32 (33 verify rows), vocab 248320, temperature "
+                               "0.7, top-p 0.95, q as full-vocabulary fp32 probabilities",
+                   "one_pass_rows": round(one_pass, 3), "mean_passes_per_row": round(mean_passes, 3),
+                   "mean_n_acc": round(float(n_acc.float().mean()), 2), "verify_rows_read": rows_read,
+                   "bytes_read": nbytes, "reference_bytes": ref_bytes,
+                   "reference_equivalent_GBps": round(ref_bytes / (kern_ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
@@ -241,7 +315,8 @@ def bench_gemm(args):
             "cpu_baseline": None}
 
 
-WORKLOADS = {"e2e": (bench_e2e, 256, 8), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1)}
+WORKLOADS = {"e2e": (bench_e2e, 256, 8), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
+             "sample": (bench_sample, 20, 3)}
 
 
 def main():

@@ -87,8 +87,10 @@ int trida_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int
  * p_logits [B, R, V] fp32 (R >= K + 1), q_probs [B, K, V] fp32 probabilities the drafts were drawn
  * from, drafts [B, K] int64, n_live [B] int32 or NULL, u_accept [B, K] fp32 (row stride u_stride),
  * u_sample [B] fp32, ctx_len [B] int64 or NULL. Outputs n_acc [B] int32, token [B] int64, crop [B]
- * int64, ratio [B, K] fp64 or NULL, status [B] int32 (nonzero: a NaN / +inf logit or a row with no
- * finite logit among rows 0..K; the outputs of that sequence are then undefined). K <= 64.
+ * int64, ratio [B, K] fp64 or NULL (rows up to the first rejection; 0 after it), status [B] int32
+ * (nonzero: a NaN / +inf logit or a row with no finite logit among the rows evaluated; the outputs of
+ * that sequence are then undefined). K <= 64. Rows past a sequence's first rejection are never read:
+ * the rows are evaluated in groups, each followed by a per-sequence accept scan.
  * scratch: trida_sample_accept_scratch_bytes(B, R, V, K) bytes, 256-byte aligned, no initialisation.
  */
 int64_t trida_sample_accept_scratch_bytes(int64_t B, int64_t R, int64_t V, int64_t K);

@@ -44,10 +44,11 @@ def check_stats(logits, T, k, p, ban=-1, radix_only=False, expect_one_pass=None,
             assert (kept_ref == kept_gpu).all(), (b, r, int(kept_ref.sum()), int(kept_gpu.sum()))
             zref = np.exp(row[kept_ref] - row.max()).sum()
             assert abs(zk[b, r] / zref - 1) < 1e-6, (b, r, zk[b, r], zref)
+    # passes counts streamed quarter-rows: 4 = one pass over the row
     if expect_one_pass is not None:
-        assert (passes == 1).mean() >= expect_one_pass, passes
+        assert (passes == 4).mean() >= expect_one_pass, passes
     if max_passes is not None:
-        assert passes.max() <= max_passes, passes
+        assert passes.max() <= 4 * max_passes, passes
     return passes
 
 
@@ -156,9 +157,12 @@ def test_sample_accept_vs_oracle(gpu, T, k, p):
     assert (n_acc[ok] == ref["n_acc"][ok]).all()
     assert (tok[ok] == ref["token"][ok]).all()
     assert (crop[ok] == ref["crop"][ok]).all()
-    nz = ref["ratio"] > 0
+    # ratios of the rows the decision used (up to the first rejection); the rows after it are never
+    # evaluated and read 0
+    used = np.arange(K)[None, :] <= n_acc[:, None]
+    nz = used & (ref["ratio"] > 0)
     assert np.allclose(ratio[nz], ref["ratio"][nz], rtol=1e-5)
-    assert (ratio[~nz] == 0).all()
+    assert (ratio[used & ~nz] == 0).all() and (ratio[~used] == 0).all()
     # the cases cover early rejections and full acceptance
     assert len(set(n_acc.tolist())) >= 3
 

@@ -45,6 +45,31 @@ def test_host_only_entry_points():
     assert b"R >= K + 1" in lib.trida_last_error()
 
 
+def test_sampling_argument_checks():
+    """The sampled-acceptance entry points reject bad sampling parameters before touching memory
+    (dummy non-null pointers; nothing is launched)."""
+    lib = _lib.load()
+    n = lib.trida_sample_accept_scratch_bytes(64, 33, 248320, 32)
+    assert n > 64 * 33 * 20
+    P = 256  # a dummy, aligned, non-null address
+
+    def stats(T=0.7, k=0, p=0.95, V=1000):
+        return lib.trida_truncate_stats(P, 1, 2, V, 2 * V, V, T, k, p, -1, 0, P, P, P, P, None, None)
+
+    for kw, text in [(dict(T=0.0), b"temperature"), (dict(T=float("inf")), b"temperature"),
+                     (dict(p=0.0), b"top_p"), (dict(p=1.5), b"top_p"), (dict(k=-1), b"top_k"),
+                     (dict(k=5000, V=10000), b"top_k")]:
+        assert stats(**kw) == _lib.TRIDA_ERR_ARG, kw
+        assert text in lib.trida_last_error(), (kw, lib.trida_last_error())
+    # top_k >= V disables top-k, so it is not an error; K above one wave is
+    rc = lib.trida_sample_accept(P, 1, 66, 100, 6600, 100, P, 6500, 100, P, 65, 65, None, P, 65, P, None,
+                                 0.7, 0, 0.9, -1, P, P, P, None, P, P, n, None)
+    assert rc == _lib.TRIDA_ERR_ARG and b"K <= 64" in lib.trida_last_error()
+    rc = lib.trida_sample_accept(P, 1, 33, 100, 3300, 100, P, 3200, 100, P, 32, 32, None, P, 32, P, None,
+                                 0.7, 0, 0.9, -1, P, P, P, None, P, P, 16, None)
+    assert rc == _lib.TRIDA_ERR_WORKSPACE
+
+
 def test_mode_registry_matches_reference_launcher():
     """The --mode values of the reference launcher (inference/zoro-1/serve.py:55-58)."""
     from trida_stack_amd.engine import MODES

@@ -52,10 +52,13 @@ __device__ __forceinline__ float kval(uint32_t k) {
 // times a 25-bit odd significand to fit 24 bits, i.e. T a power of two, where the product is exact.
 // So rounding the fp64 product to fp32 gives the correctly rounded quotient, in three instructions.
 template <bool kDiv>
-__device__ __forceinline__ float make_y(float x, int ix, double rt, int64_t ban) {
-  float y = kDiv ? (float)((double)x * rt) : x;
-  y = (y == 0.f) ? 0.f : y;
-  return (ix == ban) ? -INFINITY : y;
+__device__ __forceinline__ float exact_y(float x, double rt) {
+  const float y = kDiv ? (float)((double)x * rt) : x;
+  return y + 0.f;  // -0 + 0 = +0; every other value is unchanged
+}
+template <bool kDiv>
+__device__ __forceinline__ float make_y(float x, int ix, double rt, int ban) {
+  return (ix == ban) ? -INFINITY : exact_y<kDiv>(x, rt);
 }
 
 __device__ __forceinline__ int next_pow2(int n) {
@@ -156,7 +159,7 @@ __device__ __forceinline__ void append(float y, bool pred, float* s_coll, int* s
 
 // Calls f(y, ix, valid) for every element of a row; U 16-byte loads in flight per thread.
 template <bool kDiv, bool kVec, bool kNT, int U = 4, typename F>
-__device__ __forceinline__ void for_each_y(const float* row, int V, double rt, int64_t ban, F&& f) {
+__device__ __forceinline__ void for_each_y(const float* row, int V, double rt, int ban, F&& f) {
   const int tid = threadIdx.x;
   int done = 0;
   if (kVec) {
@@ -195,8 +198,10 @@ struct TruncArgs {
   double rt;    // 1 / temperature
   int top_k;    // active when 0 < top_k < V
   float top_p;  // active when < 1
-  int64_t ban;
+  int ban;      // banned id (-1: none)
   int flags;    // bit 0: skip the window pass (exact radix select only)
+  int G, first;       // row group: block j of sequence b handles row first + j (rows >= R are skipped)
+  const int* state;   // per sequence: -1 = every row so far accepted; >= 0 = decided (skip); null: none
   float* m_out;
   float* thr_out;
   double* zk_out;
@@ -205,24 +210,47 @@ struct TruncArgs {
 };
 
 // Value histogram of the streaming pass: 1024 bins of 1/16 nat over d = y - mref in (-24, 40]
-// (mref = the sample max); bin 0 holds the largest values. Entries below the range are summed in
-// registers; entries above it (d > 40) send the row to the radix select.
+// (mref = the sample max); bin 0 holds the largest values. Bin kNB is the spare bin: entries with
+// d <= -24, -inf entries, the banned id and padding lanes land there (its mass still counts towards
+// the total). d > 40 is caught afterwards from the row max and sends the row to the radix select.
+// Each bin is one 64-bit LDS word: the count in bits 46..63 and, below, the sum of r * 2^26 with
+// r = exp(d - top of the bin) in (e^-1/16, 1]: one integer LDS atomic per element (fp64 and fp32 LDS
+// atomics measured several times slower on gfx950). Rows need V < 2^18 for the count field.
 constexpr int kNB = 1024;
 constexpr float kTop = 40.f;
 constexpr float kPerNat = 16.f;
-__device__ __forceinline__ int bin_of(float d) {
-  return (int)fminf(fmaxf(fmaf(d, -kPerNat, kTop * kPerNat), 0.f), 2048.f);
+constexpr int kSeg = 4;  // the streaming pass re-places its collection window between segments
+constexpr int kCountShift = 46;
+constexpr unsigned long long kMassMask = (1ull << kCountShift) - 1ull;
+constexpr int kMaxPackedV = (1 << 18) - 1;
+
+// Bin of an element from its raw logit x: t = 16 (40 - d) with d = x / T - mref, as one fma whose
+// coefficients the block derives once (tA = -16 / T, tB = 16 (40 + mref)). Monotone in x.
+__device__ __forceinline__ unsigned bin_of_t(float t) {
+  return min((unsigned)(int)__builtin_amdgcn_fmed3f(t, -1.f, 2048.f), (unsigned)kNB);
 }
+__device__ __forceinline__ double bin_mass(unsigned long long h, int bin) {  // relative to exp(mref)
+  return ldexp((double)(h & kMassMask), -26) * exp((double)kTop - (double)bin / kPerNat);
+}
+
+struct BinMap {  // the per-row coefficients of the element -> bin / exponent maps
+  float tA, tB;  // t = fma(x, tA, tB)
+  float rf, nm;  // d = fma(x, rf, nm) = x / T - mref
+  __device__ unsigned bin(float x) const { return bin_of_t(fmaf(x, tA, tB)); }
+};
 
 struct Shared {
   float coll[kCap];
-  unsigned cnt[kNB];  // histogram bins (the radix select uses the first kBins)
-  double mass[kNB];
+  unsigned long long hist[kNB + 1];
+  unsigned cnt[kBins];  // radix-select digits
+  double mass[kBins];
   double red[kTW];
   int n;
   int ipar[4];
-  float fpar[4];
+  int wlo[kSeg], whi[kSeg];  // the window each segment collected (bins, inclusive)
+  int nseg[kSeg];            // collection fill after each segment
   double dpar[4];
+  unsigned umax;
 };
 
 // Count of j < lim with base + sum_{i<j} e_i < target, e_i = exp(s_i - m) in fp64 (a prefix, since
@@ -451,171 +479,328 @@ __device__ void radix_resolve(const float* row, const TruncArgs& a, float m, boo
   *zk_out = s_gt + (double)c_eq * e_k;
 }
 
-// Keeps the collected values whose histogram bin lies in [lo, hi], packed at the front of sh.coll;
-// returns how many.
-__device__ int compact_bins(Shared& sh, int n, float mref, int lo, int hi) {
+// Keeps the collected logits whose bin lies in [lo, hi] and that came from a segment in the bit set
+// `segs` (entry j came from segment s when nseg[s-1] <= j < nseg[s]), packed at the front of
+// sh.coll; returns how many.
+__device__ int compact_bins(Shared& sh, const BinMap& bm, int n, int lo, int hi, unsigned segs) {
   constexpr int kPer = kCap / kT;
   float v[kPer];
+  bool kp[kPer];
   int keep = 0;
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
     const int j = (int)threadIdx.x * kPer + u;
     v[u] = j < n ? sh.coll[j] : -INFINITY;
-    const int bin = bin_of(v[u] - mref);
-    keep += (j < n) && bin >= lo && bin <= hi;
+    const int bin = (int)bm.bin(v[u]);
+    int s = 0;
+    while (s < kSeg - 1 && j >= sh.nseg[s]) ++s;
+    kp[u] = (j < n) && bin >= lo && bin <= hi && ((segs >> s) & 1u);
+    keep += kp[u];
   }
   double tot = 0.0;
   int w = (int)block_excl_scan((double)keep, sh.red, &tot);  // every read of sh.coll precedes its barriers
 #pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const int j = (int)threadIdx.x * kPer + u;
-    const int bin = bin_of(v[u] - mref);
-    if ((j < n) && bin >= lo && bin <= hi) sh.coll[w++] = v[u];
-  }
+  for (int u = 0; u < kPer; ++u)
+    if (kp[u]) sh.coll[w++] = v[u];
   __syncthreads();
   return (int)tot;
 }
 
-// A second streaming pass that collects the row's values whose histogram bin lies in [lo, hi].
-template <bool kDiv, bool kVec>
-__device__ int collect_bins(const float* row, const TruncArgs& a, float mref, int lo, int hi, Shared& sh) {
+// Appends the values of xv whose bit is set in mask (one LDS counter bump per thread).
+template <int N>
+__device__ __forceinline__ void append_batch(const float (&xv)[N], unsigned mask, Shared& sh) {
+  const int c = __popc(mask);
+  int pos = 0;
+  if (c) pos = atomicAdd(&sh.n, c);
+#pragma unroll
+  for (int e = 0; e < N; ++e)
+    if ((mask >> e) & 1u) {
+      if (pos < kCap) sh.coll[pos] = xv[e];
+      ++pos;
+    }
+}
+
+// Streams the row's elements [e0, e1) (e0 and e1 multiples of 4 on the vector path, except e1 = V),
+// in the logits' own units: the division by the temperature is folded into the bin / exponent maps,
+// and the exact y = x / T is only formed for the few collected values.
+// kHist: histogram every element, track the max and the NaN flag, collect the bins [wlo, whi].
+// Otherwise only collect the bins [wlo, whi]. The element body is branch-free; the banned id and the
+// padding lanes of a last partial tile take a separate path for that tile only.
+template <bool kVec, bool kHist>
+__device__ void stream_segment(const float* row, const TruncArgs& a, const BinMap& bm, int e0, int e1, int wlo,
+                               int whi, Shared& sh, float& mx, unsigned& nanbits) {
+  constexpr int U = 4;
+  const int tid = threadIdx.x;
+  const unsigned wspan = (unsigned)(whi - wlo);
+  auto one = [&](float x, unsigned& mask, int e) {
+    const unsigned bin = bm.bin(x);
+    if (kHist) {
+      const float d = fmaf(x, bm.rf, bm.nm);
+      const float top = fmaf((float)bin, -1.f / kPerNat, kTop);
+      const float r = __builtin_amdgcn_exp2f(fmaf(d - top, 1.44269504f, 26.f));  // r * 2^26
+      atomicAdd(&sh.hist[bin], (1ull << kCountShift) | (unsigned long long)(unsigned)r);
+      mx = fmaxf(mx, x);
+      nanbits = max(nanbits, __float_as_uint(x) << 1);  // a NaN sorts above +-inf here
+    }
+    mask |= (unsigned)((unsigned)((int)bin - wlo) <= wspan) << e;
+  };
+  int t0 = e0;
+  if (kVec) {
+    const u32x4* row4 = reinterpret_cast<const u32x4*>(row);
+    const int v0 = e0 >> 2, v1 = (e1 == a.V) ? (a.V >> 2) : (e1 >> 2);
+    const int vb = a.ban >= 0 ? (a.ban >> 2) : -1;
+    for (int base = v0; base < v1; base += kT * U) {
+      u32x4 x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const u32x4* p = row4 + min(base + u * kT + tid, v1 - 1);
+        x[u] = kHist ? __builtin_nontemporal_load(p) : *p;
+      }
+      float xv[4 * U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        xv[4 * u + 0] = __uint_as_float(x[u].x);
+        xv[4 * u + 1] = __uint_as_float(x[u].y);
+        xv[4 * u + 2] = __uint_as_float(x[u].z);
+        xv[4 * u + 3] = __uint_as_float(x[u].w);
+      }
+      // wave-uniform: does this tile hold the banned id or padding lanes?
+      if (base + kT * U > v1 || (unsigned)(vb - base) < (unsigned)(kT * U)) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int j = base + u * kT + tid;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (j >= v1 || 4 * j + e == a.ban) xv[4 * u + e] = -INFINITY;
+        }
+      }
+      unsigned mask = 0u;
+#pragma unroll
+      for (int e = 0; e < 4 * U; ++e) one(xv[e], mask, e);
+      append_batch(xv, mask, sh);
+    }
+    t0 = max(e0, v1 << 2);
+  }
+  for (int base = t0; base < e1; base += kT) {
+    const int ix = base + tid;
+    float xv[1];
+    xv[0] = (ix < e1 && ix != a.ban) ? row[ix < e1 ? ix : e1 - 1] : -INFINITY;
+    unsigned mask = 0u;
+    one(xv[0], mask, 0);
+    append_batch(xv, mask, sh);
+  }
+}
+
+// Element bounds of segment s of the streaming pass.
+template <bool kVec>
+__device__ __forceinline__ void seg_bounds(int V, int s, int* e0, int* e1) {
+  if (kVec) {
+    const int n4 = V >> 2;
+    *e0 = 4 * (int)((int64_t)n4 * s / kSeg);
+    *e1 = s == kSeg - 1 ? V : 4 * (int)((int64_t)n4 * (s + 1) / kSeg);
+  } else {
+    *e0 = (int)((int64_t)V * s / kSeg);
+    *e1 = (int)((int64_t)V * (s + 1) / kSeg);
+  }
+}
+
+// Places a collection window from a histogram of part of the row (the sample, or the segments seen
+// so far): the bin where that histogram's own boundary falls (the k_seen-th largest for top-k, the
+// top_p mass point for top-p), widened to about `budget` entries of the next segment; `scale` =
+// entries of the next segment per counted entry.
+__device__ void place_window(Shared& sh, bool use_k, float top_p, double k_seen, double scale, double budget,
+                             int* wlo, int* whi) {
+  constexpr int kBPT = kNB / kT;
+  const int tid = threadIdx.x;
+  double lm = 0.0, lc = 0.0;
+  double bm[kBPT], bc[kBPT];
+#pragma unroll
+  for (int u = 0; u < kBPT; ++u) {
+    const unsigned long long h = sh.hist[tid * kBPT + u];
+    bc[u] = (double)(h >> kCountShift);
+    bm[u] = (double)(float)bin_mass(h, tid * kBPT + u);
+    lm += bm[u];
+    lc += bc[u];
+  }
+  double zb = 0.0, cbins = 0.0;
+  const double exm = block_excl_scan(lm, sh.red, &zb);
+  const double exc = block_excl_scan(lc, sh.red, &cbins);
+  if (tid == 0) {
+    sh.ipar[0] = INT_MAX;
+    sh.ipar[1] = INT_MAX;
+    sh.ipar[2] = -1;
+  }
   __syncthreads();
-  if (threadIdx.x == 0) sh.n = 0;
+  const double tgt = use_k ? k_seen : (double)top_p * (zb + bin_mass(sh.hist[kNB], kNB));
+  double run = use_k ? exc : exm;
+#pragma unroll
+  for (int u = 0; u < kBPT; ++u) {
+    const double add = use_k ? bc[u] : bm[u];
+    if (run < tgt && run + add >= tgt) atomicMin(&sh.ipar[0], tid * kBPT + u);
+    run += add;
+  }
   __syncthreads();
-  for_each_y<kDiv, kVec, false, 2>(row, a.V, a.rt, a.ban, [&](float y, int ix, bool ok) {
-    const int bin = bin_of((ok ? y : -INFINITY) - mref);
-    append(y, ok && bin >= lo && bin <= hi, sh.coll, &sh.n);
-  });
+  int B = sh.ipar[0];
+  if (B == INT_MAX) B = kNB - 1;
+  if (tid == B / kBPT) {
+    double c = exc;
+    for (int u = 0; u < B % kBPT; ++u) c += bc[u];
+    sh.dpar[1] = c;                                                 // count above B
+    sh.dpar[2] = (double)(sh.hist[B] >> kCountShift);                // count in B
+  }
   __syncthreads();
-  return sh.n;
+  const double cB = sh.dpar[1], nB = sh.dpar[2];
+  const double half = budget / scale / 2.0;  // in counted entries
+  const double lo_c = use_k ? -1.0 : cB - half, hi_c = use_k ? budget / scale : cB + nB + half;
+  double c = exc;
+#pragma unroll
+  for (int u = 0; u < kBPT; ++u) {
+    const int bin = tid * kBPT + u;
+    if (c + bc[u] > lo_c) atomicMin(&sh.ipar[1], bin);
+    if (c < hi_c) atomicMax(&sh.ipar[2], bin);
+    c += bc[u];
+  }
+  __syncthreads();
+  *wlo = use_k ? 0 : min(sh.ipar[1], B);
+  *whi = min(max(sh.ipar[2], B) + 1, kNB - 1);  // one bin of slack below: values tied across a bin edge
+  __syncthreads();
+}
+
+// Exact y = x / T of the collected logits, in place.
+template <bool kDiv>
+__device__ void collected_to_y(Shared& sh, int n, double rt) {
+  for (int j = threadIdx.x; j < n; j += kT) sh.coll[j] = exact_y<kDiv>(sh.coll[j], rt);
+  __syncthreads();
 }
 
 template <bool kDiv, bool kVec>
 __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
   __shared__ Shared sh;
-  const int r = blockIdx.x;
-  const int b = r / a.R, i = r % a.R;
+  const int b = blockIdx.x / a.G, i = a.first + (int)(blockIdx.x % a.G);
+  if (i >= a.R || (a.state && a.state[b] >= 0)) return;  // block-uniform: past the rows, or decided
+  const int r = b * a.R + i;
   const float* row = a.logits + (int64_t)b * a.batch_stride + (int64_t)i * a.row_stride;
   const int V = a.V, tid = threadIdx.x;
   const bool use_k = a.top_k > 0 && a.top_k < V;
   const bool use_p = a.top_p < 1.f;
   const bool collect = use_k || use_p;
-  int passes = 0;
+  const bool window = !(a.flags & 1) && V <= kMaxPackedV;
+  int passes = 0;  // segments streamed (kSeg = one pass over the row)
 
-  // ---- sample: evenly spaced entries, sorted; their max is the exponent reference of the pass
-  const int ns = min(kSample, V);
-  const int nsp = next_pow2(max(ns, 2));
-  for (int j = tid; j < nsp; j += kT) {
-    float y = -INFINITY;
-    if (j < ns) {
-      const int ix = (int)((int64_t)j * V / ns);
-      y = make_y<kDiv>(row[ix], ix, a.rt, a.ban);
-      if (!(y < INFINITY)) y = -INFINITY;  // NaN / +inf rows are reported by the pass
-    }
-    sh.coll[j] = y;
-  }
-  sort_desc(sh.coll, nsp);
-  const float mref = sh.coll[0];
-  // the window of bins collected by the pass, placed from the sample; about 0.4 * kCap entries of
-  // the row per side of the sample's estimate
-  int w_lo = 1, w_hi = 0;
-  const int spare = (int)min(0.4 * kCap * (double)ns / V, (double)ns);
-  if (use_k) {
-    const double est = (double)a.top_k * ns / V;
-    const int rk = max((int)(est + 4.0 * sqrt(est) + 4.0), spare);
-    w_lo = 0;
-    w_hi = rk < ns ? bin_of(sh.coll[rk] - mref) : kNB - 1;
-  } else if (use_p) {
-    // the sample's own nucleus boundary j*, widened by kW sample ranks on each side
-    const int kW = max(12, spare);
-    const int L = nsp / kT > 0 ? nsp / kT : 1;
-    const int j0 = min(nsp, tid * L), j1 = min(nsp, j0 + L);
-    double loc = 0.0;
-    for (int j = j0; j < j1; ++j) loc += (double)__expf(sh.coll[j] - mref);
-    double W = 0.0;
-    const double ex = block_excl_scan(loc, sh.red, &W);
-    if (tid == 0) sh.ipar[1] = ns - 1;
-    __syncthreads();
-    const double target = (double)a.top_p * W;
-    double run = ex;
-    for (int j = j0; j < j1; ++j) {
-      const double e = (double)__expf(sh.coll[j] - mref);
-      if (run < target && run + e >= target) sh.ipar[1] = j;
-      run += e;
-    }
-    __syncthreads();
-    const int js = sh.ipar[1];
-    w_lo = js - kW >= 0 ? bin_of(sh.coll[js - kW] - mref) : 0;
-    w_hi = js + kW < ns ? bin_of(sh.coll[js + kW] - mref) : kNB - 1;
-  }
-  w_lo = min(w_lo, kNB - 1);
-  w_hi = min(w_hi, kNB - 1);
-  __syncthreads();  // the sample is dead; the collection reuses its LDS
-  for (int j = tid; j < kNB; j += kT) {
-    sh.cnt[j] = 0u;
-    sh.mass[j] = 0.0;
-  }
-  if (tid == 0) sh.n = 0;
-  __syncthreads();
-
-  // ---- the streaming pass: max, histogram, collection of the window
-  float mx = -INFINITY;
-  int bad = 0, big = 0;
-  double mb = 0.0;  // mass below the histogram's range
-  const bool window = !(a.flags & 1);
+  float mx = -INFINITY;  // max logit (the banned id excluded)
+  unsigned nanbits = 0u;
+  float mref = 0.f;
+  BinMap bm{};
   if (window) {
-    for_each_y<kDiv, kVec, true>(row, V, a.rt, a.ban, [&](float y, int ix, bool ok) {
-      const float yy = ok ? y : -INFINITY;
-      bad |= ok && !(y < INFINITY);
-      mx = fmaxf(mx, yy);
-      const float d = yy - mref;
-      big |= d > kTop;
-      const float e = __expf(d);
-      const int bin = bin_of(d);
-      if (bin < kNB) {
-        atomicAdd(&sh.cnt[bin], 1u);
-        atomicAdd(&sh.mass[bin], (double)e);
-      } else {
-        mb += e;
+    // ---- sample: evenly spaced entries; their max is the exponent reference of the pass, their
+    // histogram places the first segment's window
+    const int ns = min(kSample, V);
+    float xs[kSample / kT];
+    float smax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kSample / kT; ++u) {
+      const int j = u * kT + tid;
+      const int ix = (int)((int64_t)min(j, ns - 1) * V / ns);
+      const float x = row[ix];
+      xs[u] = (j < ns && ix != a.ban && x == x) ? x : -INFINITY;
+      smax = xs[u] < INFINITY ? fmaxf(smax, xs[u]) : smax;
+    }
+    smax = block_max(smax, sh.red);
+    mref = smax > -INFINITY ? exact_y<kDiv>(smax, a.rt) : 0.f;
+    const float rf = (float)a.rt;
+    bm.tA = -kPerNat * rf;
+    bm.tB = kPerNat * (kTop + mref);
+    bm.rf = rf;
+    bm.nm = -mref;
+    for (int j = tid; j <= kNB; j += kT) sh.hist[j] = 0ull;
+    __syncthreads();
+    int w_lo = kNB + 1, w_hi = kNB + 1;  // empty
+    if (collect) {
+#pragma unroll
+      for (int u = 0; u < kSample / kT; ++u) {
+        const float x = xs[u] < INFINITY ? xs[u] : -INFINITY;
+        const unsigned bin = bm.bin(x);
+        const float d = fmaf(x, bm.rf, bm.nm);
+        const float top = fmaf((float)bin, -1.f / kPerNat, kTop);
+        const float rr = __builtin_amdgcn_exp2f(fmaf(d - top, 1.44269504f, 26.f));
+        atomicAdd(&sh.hist[bin], (1ull << kCountShift) | (unsigned long long)(unsigned)rr);
       }
-      if (collect) append(yy, bin >= w_lo && bin <= w_hi, sh.coll, &sh.n);
-    });
+      __syncthreads();
+      int s0, s1;
+      seg_bounds<kVec>(V, 0, &s0, &s1);
+      place_window(sh, use_k, a.top_p, (double)a.top_k * ns / V, (double)(s1 - s0) / ns, 0.2 * kCap, &w_lo, &w_hi);
+      for (int j = tid; j <= kNB; j += kT) sh.hist[j] = 0ull;
+    }
+    if (tid == 0) sh.n = 0;
+    __syncthreads();
+
+    // ---- the streaming pass, kSeg segments: max, histogram, collection of a window re-placed from the
+    // exact histogram after every segment
+    for (int s = 0; s < kSeg; ++s) {
+      int e0, e1;
+      seg_bounds<kVec>(V, s, &e0, &e1);
+      if (tid == 0) {
+        sh.wlo[s] = w_lo;
+        sh.whi[s] = w_hi;
+      }
+      stream_segment<kVec, true>(row, a, bm, e0, e1, w_lo, w_hi, sh, mx, nanbits);
+      ++passes;
+      __syncthreads();
+      if (tid == 0) sh.nseg[s] = sh.n;
+      if (collect && s + 1 < kSeg) {
+        __syncthreads();
+        int n0, n1;
+        seg_bounds<kVec>(V, s + 1, &n0, &n1);
+        const double seen = (double)e1, next = (double)(n1 - n0);
+        const double room = max(0.6 * kCap - (double)min(sh.n, kCap), 0.0);
+        place_window(sh, use_k, a.top_p, (double)a.top_k * seen / V, next / seen, room / (kSeg - 1 - s), &w_lo,
+                     &w_hi);
+      }
+    }
   } else {
     for_each_y<kDiv, kVec, true>(row, V, a.rt, a.ban, [&](float y, int ix, bool ok) {
-      bad |= ok && !(y < INFINITY);
       mx = fmaxf(mx, ok ? y : -INFINITY);
+      nanbits = max(nanbits, ok ? __float_as_uint(y) << 1 : 0u);
     });
+    passes += kSeg;
   }
-  ++passes;
   mx = block_max(mx, sh.red);
-  bad = block_isum(bad, sh.red);
+  if (tid == 0) sh.umax = 0u;
+  __syncthreads();
+  atomicMax(&sh.umax, nanbits);
+  __syncthreads();
+  const bool bad = sh.umax > 0xff000000u || mx == INFINITY;  // a NaN, or a +inf logit
+  // the exact row max of y (the window path tracked the raw logits; y = x / T is monotone in x)
+  const float ymax = window ? exact_y<kDiv>(mx, a.rt) : mx;
   float thr = -INFINITY;
   double zk = 0.0;
   int status = 0;
   if (bad) {
     status = 1;
-  } else if (!(mx > -INFINITY)) {
+  } else if (!(ymax > -INFINITY)) {
     status = 2;
   } else {
-    bool ok = window && (mref > -INFINITY) && !block_isum(big, sh.red);
-    mb = block_sum(mb, sh.red);
-    __syncthreads();
+    bool ok = window && !(ymax - mref > kTop);
     const int n = sh.n;
-    const double md = (double)mx;
+    const double md = (double)ymax;
     const double scale = exp((double)mref - md);
     if (ok) {
       // each thread owns kNB / kT consecutive bins; exclusive scans give the mass / count above each
       constexpr int kBPT = kNB / kT;
       double lm = 0.0, lc = 0.0;
+      double bms[kBPT], bcs[kBPT];
 #pragma unroll
       for (int u = 0; u < kBPT; ++u) {
-        lm += sh.mass[tid * kBPT + u];
-        lc += (double)sh.cnt[tid * kBPT + u];
+        const unsigned long long h = sh.hist[tid * kBPT + u];
+        bcs[u] = (double)(h >> kCountShift);
+        bms[u] = bin_mass(h, tid * kBPT + u);
+        lm += bms[u];
+        lc += bcs[u];
       }
       double zb = 0.0, cbins = 0.0;
       const double exm = block_excl_scan(lm, sh.red, &zb);
       const double exc = block_excl_scan(lc, sh.red, &cbins);
-      const double Z = zb + mb;
+      const double Z = zb + bin_mass(sh.hist[kNB], kNB);
       if (!collect) {
         zk = Z * scale;
       } else {
@@ -626,37 +811,49 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
         double run = use_k ? exc : exm;
 #pragma unroll
         for (int u = 0; u < kBPT; ++u) {
-          const int bin = tid * kBPT + u;
-          const double add = use_k ? (double)sh.cnt[bin] : sh.mass[bin];
-          if (run < tgt && run + add >= tgt) atomicMin(&sh.ipar[0], bin);
+          const double add = use_k ? bcs[u] : bms[u];
+          if (run < tgt && run + add >= tgt) atomicMin(&sh.ipar[0], tid * kBPT + u);
           run += add;
         }
         __syncthreads();
         const int B = sh.ipar[0];
         if (B != INT_MAX && tid == B / kBPT) {  // the owner publishes the count / mass above the bin
           double cum = use_k ? exc : exm;
-          for (int u = 0; u < B % kBPT; ++u)
-            cum += use_k ? (double)sh.cnt[tid * kBPT + u] : sh.mass[tid * kBPT + u];
+          for (int u = 0; u < B % kBPT; ++u) cum += use_k ? bcs[u] : bms[u];
           sh.dpar[0] = cum;
         }
         __syncthreads();
         if (B == INT_MAX) {
           ok = false;  // the target lies below the histogram's range
         } else {
+          // values tied in y may straddle a bin edge (the bins come from the logits), so the
+          // candidate set takes one more bin below the boundary bin
           const double cum = sh.dpar[0];
-          const int c_lo = use_k ? 0 : B;
-          const int need = (int)((use_k ? cum : 0.0) + (double)sh.cnt[B]);
+          const int c_lo = use_k ? 0 : B, c_hi = min(B + 1, kNB - 1);
+          double need = use_k ? cum : 0.0;
+          for (int bb = B; bb <= c_hi; ++bb) need += (double)(sh.hist[bb] >> kCountShift);
           if (need > kCap) {
             ok = false;
           } else {
-            int n2;
-            if (c_lo >= w_lo && B <= w_hi && n <= kCap) {
-              n2 = compact_bins(sh, n, mref, c_lo, B);
-            } else {
-              n2 = collect_bins<kDiv, kVec>(row, a, mref, c_lo, B, sh);
+            // keep what the segments whose window held [c_lo, c_hi] collected (and that fit the
+            // collection); stream the others again
+            unsigned complete = 0u;
+            for (int s = 0; s < kSeg; ++s)
+              complete |= (unsigned)(c_lo >= sh.wlo[s] && c_hi <= sh.whi[s] && sh.nseg[s] <= kCap) << s;
+            int n2 = compact_bins(sh, bm, min(n, kCap), c_lo, c_hi, complete);
+            __syncthreads();
+            if (tid == 0) sh.n = n2;
+            __syncthreads();
+            for (int s = 0; s < kSeg; ++s) {
+              if ((complete >> s) & 1u) continue;
+              int e0, e1;
+              seg_bounds<kVec>(V, s, &e0, &e1);
+              stream_segment<kVec, false>(row, a, bm, e0, e1, c_lo, c_hi, sh, mx, nanbits);
               ++passes;
             }
-            n2 = min(n2, kCap);
+            __syncthreads();
+            n2 = min(sh.n, kCap);
+            collected_to_y<kDiv>(sh, n2, a.rt);
             sort_collection(sh, n2);
             if (use_k) {
               const int k = min(a.top_k, n2);
@@ -679,10 +876,14 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
         }
       }
     }
-    if (!ok) radix_resolve<kDiv, kVec>(row, a, mx, use_k, use_p, sh, &thr, &zk, &passes);
+    if (!ok) {
+      int rp = 0;
+      radix_resolve<kDiv, kVec>(row, a, ymax, use_k, use_p, sh, &thr, &zk, &rp);
+      passes += rp * kSeg;
+    }
   }
   if (tid == 0) {
-    a.m_out[r] = mx;
+    a.m_out[r] = ymax;
     a.thr_out[r] = thr;
     a.zk_out[r] = zk;
     a.status_out[r] = status;
@@ -705,11 +906,13 @@ struct AcceptArgs {
   const int64_t* ctx;
   int B, V, K;
   double rt;  // 1 / temperature
-  int64_t ban;
+  int ban;
   const float* m;  // [B * (K + 1)] row statistics
   const float* thr;
   const double* zk;
   const int* status;
+  int* state;    // per sequence: -1 while every verified draft was accepted, else the accepted length
+  int* rstatus;  // per sequence: OR of the row statuses seen
   int NC, chunk;
   double* sums;  // [B][NC][2]: correction weight, P
   int32_t* n_acc;
@@ -719,24 +922,40 @@ struct AcceptArgs {
   int32_t* status_out;
 };
 
-// P_row(x) in fp64 from the row statistics (0 outside the kept set).
-__device__ __forceinline__ double prob_of(const AcceptArgs& a, int srow, float x, int ix) {
+// P_row(x) exactly (fp64 exponential) from the row statistics, 0 outside the kept set: the drafted
+// tokens' probabilities in the accept test.
+__device__ __forceinline__ double prob_exact(const AcceptArgs& a, int srow, float x, int ix) {
   const float y = make_y<true>(x, ix, a.rt, a.ban);  // the product with rt = 1 is exact
   if (!(y > -INFINITY) || !(y >= a.thr[srow])) return 0.0;
   return exp((double)y - (double)a.m[srow]) / a.zk[srow];
 }
 
-// Weight of token ix in the correction draw of sequence b at row r (r < K: residual, r == K: P_K).
-__device__ __forceinline__ void weights_of(const AcceptArgs& a, int b, int r, int ix, double* w, double* pp) {
-  const int srow = b * (a.K + 1) + r;
-  const double P = prob_of(a, srow, a.p[(int64_t)b * a.p_bs + (int64_t)r * a.p_rs + ix], ix);
-  *pp = P;
-  if (r < a.K) {
-    const double q = (double)a.q[(int64_t)b * a.q_bs + (int64_t)r * a.q_rs + ix];
-    *w = fmax(P - q, 0.0);
-  } else {
-    *w = P;
+// The correction draw's weights over a row (fp32 exponential: a relative error of ~1e-7 per entry,
+// so the cumulative weight is off by at most ~1e-7 in probability units).
+struct RowW {
+  const float* p;
+  const float* q;  // null: weights are P_K itself
+  float m, thr, inv_zk;
+  double rt;
+  int ban;
+  __device__ __forceinline__ void at(int ix, float* w, float* pp) const {
+    const float y = make_y<true>(p[ix], ix, rt, ban);
+    const float P = (y > -INFINITY && y >= thr) ? __expf(y - m) * inv_zk : 0.f;
+    *pp = P;
+    *w = q ? fmaxf(P - q[ix], 0.f) : P;
   }
+};
+__device__ __forceinline__ RowW row_weights(const AcceptArgs& a, int b, int r) {
+  const int srow = b * (a.K + 1) + r;
+  RowW w;
+  w.p = a.p + (int64_t)b * a.p_bs + (int64_t)r * a.p_rs;
+  w.q = r < a.K ? a.q + (int64_t)b * a.q_bs + (int64_t)r * a.q_rs : nullptr;
+  w.m = a.m[srow];
+  w.thr = a.thr[srow];
+  w.inv_zk = (float)(1.0 / a.zk[srow]);
+  w.rt = a.rt;
+  w.ban = a.ban;
+  return w;
 }
 
 __device__ __forceinline__ double rblock_sum(double v, double* sh) {
@@ -751,51 +970,67 @@ __device__ __forceinline__ double rblock_sum(double v, double* sh) {
   return t;
 }
 
+// The accept test of the row group [first, first + G) of sequence b, one wave: the drafted token's
+// ratio P_i(d_i) / q_i(d_i) per row, accepted while ratio >= 1 or u_i < ratio (and i < n_live). Decides
+// the sequence at its first rejection, or once row K (the bonus row) has been reached.
+__global__ __launch_bounds__(kWave) void accept_scan_kernel(AcceptArgs a, int first, int G) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  if (first > 0 && a.state[b] >= 0) return;
+  const int i = first + lane;
+  const bool row_here = lane < G && i <= a.K;
+  const bool draft_here = lane < G && i < a.K;
+  const int live = a.n_live ? min(max((int)a.n_live[b], 0), a.K) : a.K;
+  bool acc = false;
+  double ratio = 0.0;
+  if (draft_here) {
+    const int64_t d = a.drafts[(int64_t)b * a.d_st + i];
+    if (d >= 0 && d < a.V) {
+      const int srow = b * (a.K + 1) + i;
+      const double P = prob_exact(a, srow, a.p[(int64_t)b * a.p_bs + (int64_t)i * a.p_rs + d], (int)d);
+      const double q = (double)a.q[(int64_t)b * a.q_bs + (int64_t)i * a.q_rs + d];
+      ratio = q > 0.0 ? P / fmax(q, 1e-30) : 0.0;
+      acc = (i < live) && (ratio >= 1.0 || (double)a.u_acc[(int64_t)b * a.u_st + i] < ratio);
+    }
+  }
+  const uint64_t drafts = __ballot(draft_here);
+  const uint64_t rej = drafts & ~__ballot(acc);
+  int n = -1;  // still open
+  if (rej) n = first + __builtin_ctzll(rej);
+  else if (first + G > a.K) n = a.K;  // this group holds row K: every draft accepted
+  int st = row_here ? a.status[b * (a.K + 1) + i] : 0;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) st |= __shfl_xor(st, off, kWave);
+  if (a.ratio && draft_here && (n < 0 || i <= n)) a.ratio[(int64_t)b * a.K + i] = ratio;
+  if (lane == 0) {
+    a.state[b] = n;
+    a.rstatus[b] = (first > 0 ? a.rstatus[b] : 0) | st;
+  }
+}
+
 __global__ __launch_bounds__(kRT) void resid_sums_kernel(AcceptArgs a) {
   const int c = blockIdx.x, b = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid % kWave;
+  const int tid = threadIdx.x;
   __shared__ int s_nacc;
   __shared__ double s_red[kRT / kWave];
-  if (tid < kWave) {
-    const int i = lane;
-    const int live = a.n_live ? min(max((int)a.n_live[b], 0), a.K) : a.K;
-    bool acc = false;
-    double ratio = 0.0;
-    if (i < a.K) {
-      const int64_t d = a.drafts[(int64_t)b * a.d_st + i];
-      if (d >= 0 && d < a.V) {
-        const int srow = b * (a.K + 1) + i;
-        const double P = prob_of(a, srow, a.p[(int64_t)b * a.p_bs + (int64_t)i * a.p_rs + d], (int)d);
-        const double q = (double)a.q[(int64_t)b * a.q_bs + (int64_t)i * a.q_rs + d];
-        ratio = q > 0.0 ? P / fmax(q, 1e-30) : 0.0;
-        acc = (i < live) && (ratio >= 1.0 || (double)a.u_acc[(int64_t)b * a.u_st + i] < ratio);
-      }
-    }
-    const uint64_t lead = ~__ballot(acc);
-    const int n = lead == 0ull ? kWave : __builtin_ctzll(lead);
-    const int n_acc = min(n, a.K);
-    // any invalid row among 0..K
-    int st = 0;
-    for (int r = lane; r <= a.K; r += kWave) st |= a.status[b * (a.K + 1) + r];
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) st |= __shfl_xor(st, off, kWave);
-    if (lane == 0) s_nacc = n_acc;
-    if (c == 0) {
-      if (a.ratio && i < a.K) a.ratio[(int64_t)b * a.K + i] = ratio;
-      if (lane == 0) {
-        a.n_acc[b] = n_acc;
-        a.crop[b] = (a.ctx ? a.ctx[b] : 0) + 1 + n_acc;
-        a.status_out[b] = st;
-      }
+  if (tid == 0) s_nacc = min(max(a.state[b], 0), a.K);
+  __syncthreads();
+  if (c == 0) {  // the per-sequence outputs; ratios past the first rejection are 0
+    const int n_acc = s_nacc;
+    if (a.ratio)
+      for (int i = n_acc + 1 + tid; i < a.K; i += kRT) a.ratio[(int64_t)b * a.K + i] = 0.0;
+    if (tid == 0) {
+      a.n_acc[b] = n_acc;
+      a.crop[b] = (a.ctx ? a.ctx[b] : 0) + 1 + n_acc;
+      a.status_out[b] = a.rstatus[b];
     }
   }
   __syncthreads();
-  const int r = s_nacc;
+  const RowW rw = row_weights(a, b, s_nacc);
   const int lo = c * a.chunk, hi = min(a.V, lo + a.chunk);
   double sw = 0.0, sp = 0.0;
   for (int ix = lo + tid; ix < hi; ix += kRT) {
-    double w, pp;
-    weights_of(a, b, r, ix, &w, &pp);
+    float w, pp;
+    rw.at(ix, &w, &pp);
     sw += w;
     sp += pp;
   }
@@ -807,12 +1042,15 @@ __global__ __launch_bounds__(kRT) void resid_sums_kernel(AcceptArgs a) {
   }
 }
 
+constexpr int kPickChunk = 4096;  // the largest chunk: its weights fit the pick kernel's LDS
+
 __global__ __launch_bounds__(kRT) void resid_pick_kernel(AcceptArgs a) {
   const int b = blockIdx.x, tid = threadIdx.x;
   const int lane = tid % kWave, w = tid / kWave;
   __shared__ int s_chunk, s_last, s_tok, s_sel;
   __shared__ double s_t;
   __shared__ double s_red[kRT / kWave];
+  __shared__ float s_w[kPickChunk];
   const int r = a.n_acc[b];
   if (tid == 0) {
     const double* s = a.sums + (int64_t)b * a.NC * 2;
@@ -845,17 +1083,22 @@ __global__ __launch_bounds__(kRT) void resid_pick_kernel(AcceptArgs a) {
   const int c = s_chunk, sel = s_sel;
   const bool last = s_last;
   const double t = s_t;
-  const int lo = c * a.chunk, hi = min(a.V, lo + a.chunk);
-  const int L = (hi - lo + kRT - 1) / kRT;
-  const int j0 = min(hi, lo + tid * L), j1 = min(hi, j0 + L);
+  const int lo = c * a.chunk, hi = min(a.V, lo + a.chunk), len = hi - lo;
+  // stage the chunk's weights in LDS with coalesced loads, then scan contiguous runs per thread
+  const RowW rw = row_weights(a, b, r);
+  for (int j = tid; j < len; j += kRT) {
+    float wt, pp;
+    rw.at(lo + j, &wt, &pp);
+    s_w[j] = sel ? pp : wt;
+  }
+  __syncthreads();
+  const int L = (len + kRT - 1) / kRT;
+  const int j0 = min(len, tid * L), j1 = min(len, j0 + L);
   double loc = 0.0;
   int lastpos = -1;
-  for (int ix = j0; ix < j1; ++ix) {
-    double wt, pp;
-    weights_of(a, b, r, ix, &wt, &pp);
-    const double v = sel ? pp : wt;
-    loc += v;
-    if (v > 0.0) lastpos = ix;
+  for (int j = j0; j < j1; ++j) {
+    loc += (double)s_w[j];
+    if (s_w[j] > 0.f) lastpos = lo + j;
   }
   // exclusive scan over the block (thread order = vocabulary order)
   double inc = loc;
@@ -872,12 +1115,10 @@ __global__ __launch_bounds__(kRT) void resid_pick_kernel(AcceptArgs a) {
   int found = INT_MAX;
   if (!last && ex <= t && t < ex + loc) {
     double run = ex;
-    for (int ix = j0; ix < j1; ++ix) {
-      double wt, pp;
-      weights_of(a, b, r, ix, &wt, &pp);
-      run += sel ? pp : wt;
+    for (int j = j0; j < j1; ++j) {
+      run += (double)s_w[j];
       if (run > t) {
-        found = ix;
+        found = lo + j;
         break;
       }
     }
@@ -896,6 +1137,8 @@ __global__ __launch_bounds__(kRT) void resid_pick_kernel(AcceptArgs a) {
     a.token[b] = tok;
   }
 }
+
+int ban_of(int64_t ban_id, int64_t V) { return (ban_id >= 0 && ban_id < V) ? (int)ban_id : -1; }
 
 bool vec_ok(const void* p, int64_t V, int64_t bs, int64_t rs) {
   return ((uintptr_t)p % 16 == 0) && V % 4 == 0 && bs % 4 == 0 && rs % 4 == 0;
@@ -922,14 +1165,15 @@ int check_trunc_params(int64_t V, float temperature, int64_t top_k, float top_p)
 }
 
 void plan_chunks(int64_t B, int64_t V, int* NC, int* chunk) {
-  int nc = (int)std::min<int64_t>(64, std::max<int64_t>(1, cdiv(1024, B)));
-  nc = (int)std::min<int64_t>(nc, std::max<int64_t>(1, cdiv(V, 1024)));
+  int64_t nc = std::min<int64_t>(64, std::max<int64_t>(1, cdiv(1024, B)));
+  nc = std::min<int64_t>(nc, std::max<int64_t>(1, cdiv(V, 1024)));
+  nc = std::max<int64_t>(nc, cdiv(V, kPickChunk));  // a chunk's weights fit the pick kernel's LDS
   *chunk = (int)cdiv(V, nc);
   *NC = (int)cdiv(V, *chunk);
 }
 
 struct ScratchLayout {
-  int64_t m, thr, zk, status, sums, total;
+  int64_t m, thr, zk, status, state, rstatus, sums, total;
 };
 ScratchLayout layout(int64_t B, int64_t K, int64_t V) {
   int NC, chunk;
@@ -940,7 +1184,9 @@ ScratchLayout layout(int64_t B, int64_t K, int64_t V) {
   L.thr = L.m + align_up(rows * 4, 256);
   L.zk = L.thr + align_up(rows * 4, 256);
   L.status = L.zk + align_up(rows * 8, 256);
-  L.sums = L.status + align_up(rows * 4, 256);
+  L.state = L.status + align_up(rows * 4, 256);
+  L.rstatus = L.state + align_up(B * 4, 256);
+  L.sums = L.rstatus + align_up(B * 4, 256);
   L.total = L.sums + align_up(B * NC * 2 * 8, 256);
   return L;
 }
@@ -960,7 +1206,8 @@ extern "C" int trida_truncate_stats(const float* logits, int64_t B, int64_t R, i
   if (rc != TRIDA_OK) return rc;
   TRIDA_CHECK(row_stride >= V && (B == 1 || batch_stride >= (R - 1) * row_stride + V), TRIDA_ERR_ARG,
               "strides too small");
-  TruncArgs ta{logits, batch_stride, row_stride, (int)R, (int)V, 1.0 / (double)temperature, (int)top_k, top_p, ban_id, flags,
+  TruncArgs ta{logits, batch_stride, row_stride, (int)R, (int)V, 1.0 / (double)temperature, (int)top_k, top_p,
+               ban_of(ban_id, V), flags, (int)R, 0, nullptr,
                m_out, thr_out, zk_out, status_out, passes_out};
   return launch_truncate(ta, (int)(B * R), vec_ok(logits, V, batch_stride, row_stride),
                          static_cast<hipStream_t>(stream));
@@ -1005,19 +1252,33 @@ extern "C" int trida_sample_accept(const float* p_logits, int64_t B, int64_t R, 
   int* st = reinterpret_cast<int*>(s + L.status);
   double* sums = reinterpret_cast<double*>(s + L.sums);
 
-  // statistics of rows 0..K of every sequence (the rows past K are not needed)
-  TruncArgs ta{p_logits, p_batch_stride, p_row_stride, (int)(K + 1), (int)V, 1.0 / (double)temperature, (int)top_k,
-               top_p, ban_id,
-               0, m, thr, zk, st, nullptr};
-  int r = launch_truncate(ta, (int)(B * (K + 1)), vec_ok(p_logits, V, p_batch_stride, p_row_stride), stream);
-  if (r != TRIDA_OK) return r;
-
+  int* state = reinterpret_cast<int*>(s + L.state);
+  int* rstatus = reinterpret_cast<int*>(s + L.rstatus);
   int NC, chunk;
   plan_chunks(B, V, &NC, &chunk);
   AcceptArgs aa{p_logits, p_batch_stride, p_row_stride, q_probs, q_batch_stride, q_row_stride, drafts, draft_stride,
-                n_live, u_accept, u_stride, u_sample, ctx_len, (int)B, (int)V, (int)K, 1.0 / (double)temperature, ban_id,
-                m, thr,
-                zk, st, NC, chunk, sums, n_acc, token, crop, ratio, status};
+                n_live, u_accept, u_stride, u_sample, ctx_len, (int)B, (int)V, (int)K, 1.0 / (double)temperature,
+                ban_of(ban_id, V), m, thr, zk, st, state, rstatus, NC, chunk, sums, n_acc, token, crop, ratio, status};
+
+  // Only rows up to a sequence's first rejection decide anything. Rows 0..G0-1 of every sequence go
+  // first (G0 sized so that this group alone fills the GPU, ~512 blocks); a one-wave scan per
+  // sequence then settles the sequences it can, and one more group evaluates all the remaining rows
+  // of the rest at once (decided sequences' blocks exit at once), followed by the final scan.
+  const int R1 = (int)K + 1;
+  const int G0 = (int)std::min<int64_t>(R1, std::max<int64_t>(8, cdiv(512, B)));
+  const bool vec = vec_ok(p_logits, V, p_batch_stride, p_row_stride);
+  int r = TRIDA_OK;
+  for (int g = 0; g < 2; ++g) {
+    const int first = g == 0 ? 0 : G0, cnt = g == 0 ? G0 : R1 - G0;
+    if (cnt <= 0) break;
+    TruncArgs ta{p_logits, p_batch_stride, p_row_stride, R1, (int)V, 1.0 / (double)temperature, (int)top_k, top_p,
+                 ban_of(ban_id, V), 0, cnt, first, g > 0 ? state : nullptr, m, thr, zk, st, nullptr};
+    r = launch_truncate(ta, (int)(B * cnt), vec, stream);
+    if (r != TRIDA_OK) return r;
+    hipLaunchKernelGGL(accept_scan_kernel, dim3(B), dim3(kWave), 0, stream, aa, first, cnt);
+    r = launch_status("accept_scan_kernel");
+    if (r != TRIDA_OK) return r;
+  }
   hipLaunchKernelGGL(resid_sums_kernel, dim3(NC, B), dim3(kRT), 0, stream, aa);
   r = launch_status("resid_sums_kernel");
   if (r != TRIDA_OK) return r;
@@ -1028,7 +1289,7 @@ extern "C" int trida_sample_accept(const float* p_logits, int64_t B, int64_t R, 
 namespace trida {
 namespace {
 __global__ __launch_bounds__(256) void probs_kernel(const float* logits, int64_t bs, int64_t rs, int R, int V,
-                                                    double rt, int64_t ban, const float* m, const float* thr,
+                                                    double rt, int ban, const float* m, const float* thr,
                                                     const double* zk, float* out, int64_t obs, int64_t ors) {
   const int r = blockIdx.y;
   const int b = r / R, i = r % R;
@@ -1057,6 +1318,6 @@ extern "C" int trida_truncated_probs(const float* logits, int64_t B, int64_t R, 
               TRIDA_ERR_ARG, "strides too small");
   const int gx = (int)std::min<int64_t>(cdiv(V, 256 * 8), 256);
   hipLaunchKernelGGL(probs_kernel, dim3(gx, B * R), dim3(256), 0, static_cast<hipStream_t>(stream), logits, batch_stride, row_stride, (int)R,
-                     (int)V, 1.0 / (double)temperature, ban_id, m, thr, zk, probs, out_batch_stride, out_row_stride);
+                     (int)V, 1.0 / (double)temperature, ban_of(ban_id, V), m, thr, zk, probs, out_batch_stride, out_row_stride);
   return launch_status("probs_kernel");
 }
