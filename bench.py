@@ -1,6 +1,6 @@
 """Benchmark of the MI355X self-speculative decode step.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|accept|sample|gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|accept|sample|attn|gemm]
 
 Prints ONE JSON line (rank 0). One GPU only: --gpus above 1 exits with a message.
 """
@@ -170,6 +170,73 @@ def bench_sample(args):
     }
 
 
+# ------------------------------------------------------------------------------ canvas attention
+def bench_attn(args):
+    """Canvas attention of one verify block: q [1, 32, 16, 256] bf16 against a bf16 KV cache of 8192
+    prefix + 32 block keys per kv head (4 kv heads), verify (causal block) and draft (bidirectional
+    block) masks, then the crop to 8192 + a."""
+    import torch
+
+    from trida_stack_amd import kernels
+
+    dev = torch.device("cuda:0")
+    B, T, Hq, Hkv, D, P = 1, 32, 16, 4, 256, 8192
+    L = P + T
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, T, Hq, D, generator=g, device=dev).to(torch.bfloat16)
+    kc = torch.randn(B, Hkv, L, D, generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn(B, Hkv, L, D, generator=g, device=dev).to(torch.bfloat16)
+    plen = torch.full((B,), P, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+    res = {}
+    for name, mode in (("verify", kernels.MASK_VERIFY), ("draft", kernels.MASK_DRAFT)):
+        fn = lambda: kernels.attn_canvas(q, kc, vc, plen, mask_mode=mode, out=out, max_keys=L, splits=args.splits)
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            fn()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        res[name] = (_events_time_ms(fn, 200), wall_ms)
+    # crop to 8192 + a: a device-side length update (the cache keeps its memory)
+    a = 17
+    crop = lambda: plen.fill_(P + a)
+    crop_ms = _events_time_ms(crop, 200)
+    plen.fill_(P)
+    nbytes = 2 * L * Hkv * D * 2 + 2 * B * T * Hq * D * 2
+    flops = 4 * Hq * T * L * D
+    kern_ms = res["verify"][0]
+    achieved = nbytes / (kern_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        from oracle import attention as OA
+
+        qc, kk, vv = q.float().cpu(), kc.float().cpu(), vc.float().cpu()
+        pl = [P]
+        OA.canvas_attention(qc, kk, vv, pl, kernels.MASK_VERIFY)
+        t = time.perf_counter()
+        reps = 0
+        while time.perf_counter() - t < 3.0:
+            OA.canvas_attention(qc, kk, vv, pl, kernels.MASK_VERIFY)
+            reps += 1
+        cpu = {"value": round((time.perf_counter() - t) / reps * 1e6, 1), "unit": "us per verify attention",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{reps} oracle canvas_attention calls (torch fp32 on the host) on the same inputs"}
+    return {
+        "metric": METRIC, "value": round(kern_ms * 1e3, 2), "unit": "us per verify-block attention (kernels)",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["verify"][1], 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "canvas attention, 32 block rows, 16 q / 4 kv heads, d 256, ctx 8192 + 32",
+                   "draft_us": round(res["draft"][0] * 1e3, 2), "crop_us": round(crop_ms * 1e3, 2),
+                   "tflops": round(flops / (kern_ms * 1e-3) / 1e12, 1)},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+
+
 # ------------------------------------------------------------------------------ end-to-end (config 4)
 PROMPT_LEN, BLOCK, DENOISE = 2048, 32, 4
 
@@ -316,7 +383,7 @@ def bench_gemm(args):
 
 
 WORKLOADS = {"e2e": (bench_e2e, 256, 8), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
-             "sample": (bench_sample, 20, 3)}
+             "sample": (bench_sample, 20, 3), "attn": (bench_attn, 100, 10)}
 
 
 def main():

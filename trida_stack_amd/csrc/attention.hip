@@ -7,11 +7,10 @@
 //   mask 1 (draft, bidirectional) always
 //   mask 2 (canvas, mixed)        j <= t for t < n_clean, always for t >= n_clean
 //
-// attn_partial: workgroup = (sequence, KV head, query tile of <= 144 rows, key split), 4 waves.
-//   Per block of 64 keys: each wave computes S = Q K^T for its 16 keys and all rows of the tile with
-//   v_mfma_f32_16x16x32_bf16 (K fragments straight from global memory into registers, Q from LDS),
-//   the online-softmax statistics are combined across the 4 waves through LDS, P is written to LDS in
-//   bf16, and each wave accumulates O[:, its D/4 columns] += P V with V staged transposed in LDS.
+// attn_partial: workgroup = (sequence, KV head, query tile of <= 128 rows, key split), 8 waves of 16
+//   rows each. Per 64-key step, K and V^T are staged in LDS (XOR-swizzled) while the next step is
+//   loaded into registers; every wave computes S = Q K^T for its rows with v_mfma_f32_16x16x32_bf16 (Q
+//   fragments in registers), runs the online softmax within the wave, and accumulates O += P V.
 //   Writes the unnormalised O, row max and row sum of its split.
 // attn_combine: merges the splits per row (log-sum-exp weights), applies the optional output gate
 //   sigmoid(gate) and writes bf16.
@@ -24,11 +23,10 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-constexpr int kNW = 4;
-constexpr int kMT = 144;        // query rows per workgroup (9 MFMA row tiles)
-constexpr int kRT = kMT / 16;
-constexpr int kKB = 64;         // keys per block
-constexpr int kKP = kKB + 8;    // padded LDS row of P / V^T (elements)
+constexpr int kNW = 8;              // waves per workgroup
+constexpr int kWR = 16;             // query rows per wave (one MFMA row tile)
+constexpr int kMT = kNW * kWR;      // query rows per workgroup
+constexpr int kKB = 64;             // keys per step
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int CTRL>
@@ -72,17 +70,35 @@ __device__ __forceinline__ bool visible(int p, int prefix, int t, int mode, int 
   return j <= t;
 }
 
+// LDS tiles of one 64-key step, 16-byte groups XOR-swizzled so that both the staging writes and the
+// MFMA fragment reads touch 8 distinct bank groups per 8 lanes:
+//   K   [key][D]   group g of key k stored at g ^ (k & 7)
+//   V^T [d][key]   key group g of column d stored at g ^ (d & 7)
+//   P   [row][key] (per wave) key group g of row r stored at g ^ (r & 7)
+template <int D>
+__device__ __forceinline__ int k_off(int key, int grp) { return key * D + ((grp ^ (key & 7)) << 3); }
+__device__ __forceinline__ int vt_off(int d, int kgrp) { return d * kKB + ((kgrp ^ (d & 7)) << 3); }
+__device__ __forceinline__ int p_off(int r, int kgrp) { return r * kKB + ((kgrp ^ (r & 7)) << 3); }
+
+// Workgroup = (sequence, KV head, query tile of kMT rows, key split); 8 waves, wave w owns rows
+// [16 w, 16 w + 16) of the tile, so the online softmax of a row lives in one wave (DPP row
+// reductions, no cross-wave statistics). Per 64-key step: K and V^T are staged in LDS (the next
+// step's K / V are loaded into registers meanwhile), S = Q K^T from LDS fragments, P goes through
+// the wave's LDS slice into the A layout, and O += P V accumulates in registers; O is rescaled only
+// when a row's running max moved. Writes the unnormalised O, the row max (log2 domain) and the row
+// sum of its split.
 template <int D>
 __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
-  constexpr int DP = D + 8;       // padded LDS row of Q (elements)
-  constexpr int KC = D / 32;      // MFMA k-chunks over the head dim
-  constexpr int CPW = D / kNW;    // O columns per wave
-  constexpr int CT = CPW / 16;    // O column tiles per wave
-  __shared__ __align__(16) uint16_t sQ[kMT * DP];
-  __shared__ __align__(16) uint16_t sVt[D * kKP];
-  __shared__ __align__(16) uint16_t sP[kMT * kKP];
-  __shared__ float sMax[kNW][kMT], sSum[kNW][kMT];
-  __shared__ float sM[kMT], sL[kMT];
+  constexpr int KC = D / 32;         // 32-wide k-chunks of the head dim (QK^T)
+  constexpr int CT = D / 16;         // 16-column tiles of O
+  constexpr int GPR = D / 8;         // 16-byte groups per K row
+  constexpr int NT = kNW * kWave;
+  constexpr int NKG = kKB * GPR / NT;  // K groups staged per thread
+  constexpr int NVP = (kKB / 8) * (D / 4);  // V pieces of 8 keys x 4 columns per step
+  __shared__ __align__(16) uint16_t sQ[kMT * D];  // [row][D], groups swizzled by row & 7 (as K)
+  __shared__ __align__(16) uint16_t sK[kKB * D];
+  __shared__ __align__(16) uint16_t sVt[D * kKB];
+  __shared__ __align__(16) uint16_t sP[kNW][kWR * kKB];
 
   int idx = blockIdx.x;
   const int s = idx % a.S;
@@ -97,182 +113,176 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   const int rows = min(kMT, M - m0);
   const int prefix = a.prefix[b];
   const int nk = prefix + a.T;
-  // key range of this split: whole blocks of 64
   const int nblk = (nk + kKB - 1) / kKB;
   const int bps = (nblk + a.S - 1) / a.S;
-  const int kb0 = s * bps, kb1 = min(nblk, kb0 + bps);
+  const int kb0 = s * bps;
   // the last query row of the tile bounds the keys any row can see under the causal masks
   const int t_last = (m0 + rows - 1) / a.G;
   const int kmax = (a.mask_mode == 1 || (a.mask_mode == 2 && t_last >= a.n_clean)) ? nk : min(nk, prefix + t_last + 1);
+  const int kb1 = min(min(nblk, kb0 + bps), (kmax + kKB - 1) / kKB);
 
   const int64_t pbase = ((((int64_t)b * a.Hkv + hk) * a.QT + qt) * a.S + s);
-  if (kb0 >= kb1 || kb0 * kKB >= kmax) {
+  if (kb0 >= kb1) {
     // no key of this split is visible to the tile: only the (empty) row stats are written and the
     // combine skips the split without reading its O
-    for (int r = tid; r < rows; r += kNW * kWave) {
+    for (int r = tid; r < rows; r += NT) {
       a.mpart[pbase * kMT + r] = -INFINITY;
       a.lpart[pbase * kMT + r] = 0.f;
     }
     return;
   }
-  // ---- stage Q rows (zero padding rows) and init running stats
-  for (int p = tid; p < kMT * (D / 8); p += kNW * kWave) {
-    const int r = p / (D / 8), c = (p % (D / 8)) * 8;
-    u32x4 val = {0u, 0u, 0u, 0u};
-    if (r < rows) {
-      const int m = m0 + r, t = m / a.G, g = m % a.G;
-      val = *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + c);
-    }
-    *reinterpret_cast<u32x4*>(&sQ[r * DP + c]) = val;
-  }
-  for (int r = tid; r < kMT; r += kNW * kWave) {
-    sM[r] = -INFINITY;
-    sL[r] = 0.f;
-  }
-  f32x4 o[kRT][CT];
-#pragma unroll
-  for (int rt = 0; rt < kRT; ++rt)
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) o[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   const uint16_t* kh = a.k_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
   const uint16_t* vh = a.v_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
 
-  for (int kb = kb0; kb < kb1 && kb * kKB < kmax; ++kb) {
+  // ---- the tile's Q rows into LDS (padding rows zero); read back as A fragments every step
+  for (int gi = tid; gi < kMT * GPR; gi += NT) {
+    const int r = gi / GPR, grp = gi % GPR;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (r < rows) {
+      const int m = m0 + r, t = m / a.G, g = m % a.G;
+      v = *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + grp * 8);
+    }
+    *reinterpret_cast<u32x4*>(&sQ[k_off<D>(r, grp)]) = v;
+  }
+
+  // ---- prefetch registers: K groups (coalesced rows) and one V piece (8 keys x 4 columns)
+  u32x4 kreg[NKG];
+  u32x2 vreg[8];
+  const int vp_kg = tid % 8, vp_cq = tid / 8;  // V piece: keys vp_kg*8.., columns vp_cq*4..
+  auto load_step = [&](int kb) {
     const int key0 = kb * kKB;
-    __syncthreads();  // previous block's P / V^T fully consumed (and Q / stats staged)
-    // ---- K fragments for this wave's 16 keys: B operand, col = key (l % 16), k = head dim
-    const int my_key = key0 + w * 16 + (l % 16);
-    const int kclamp = min(my_key, nk - 1);
-    u32x4 kf[KC];
 #pragma unroll
-    for (int kc = 0; kc < KC; ++kc)
-      kf[kc] = *reinterpret_cast<const u32x4*>(kh + (int64_t)kclamp * D + kc * 32 + (l / 16) * 8);
-    // ---- V block transposed into LDS: each thread moves one 8 keys x 8 columns square
-    for (int p = tid; p < (kKB / 8) * (D / 8); p += kNW * kWave) {
-      const int kg = p / (D / 8), cg = (p % (D / 8)) * 8;
-      u32x4 rowv[8];
+    for (int j = 0; j < NKG; ++j) {
+      const int gi = tid + j * NT;
+      const int key = min(key0 + gi / GPR, nk - 1);
+      kreg[j] = *reinterpret_cast<const u32x4*>(kh + (int64_t)key * D + (gi % GPR) * 8);
+    }
+    if (tid < NVP) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int key = min(key0 + kg * 8 + j, nk - 1);
-        rowv[j] = *reinterpret_cast<const u32x4*>(vh + (int64_t)key * D + cg);
+        const int key = min(key0 + vp_kg * 8 + j, nk - 1);
+        vreg[j] = *reinterpret_cast<const u32x2*>(vh + (int64_t)key * D + vp_cq * 4);
       }
-      const uint32_t* rw = reinterpret_cast<const uint32_t*>(rowv);
+    }
+  };
+  auto stage_step = [&]() {
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        // column c of the square: element c of each of the 8 key rows
+    for (int j = 0; j < NKG; ++j) {
+      const int gi = tid + j * NT;
+      *reinterpret_cast<u32x4*>(&sK[k_off<D>(gi / GPR, gi % GPR)]) = kreg[j];
+    }
+    if (tid < NVP) {
+      const uint32_t* rw = reinterpret_cast<const uint32_t*>(vreg);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {  // column vp_cq*4 + c: element c of each of the 8 key rows
         uint32_t e[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const uint32_t word = rw[j * 4 + c / 2];
+          const uint32_t word = rw[j * 2 + c / 2];
           e[j] = (c & 1) ? (word >> 16) : (word & 0xffffu);
         }
-        u32x4 packed;
-        packed.x = e[0] | (e[1] << 16);
-        packed.y = e[2] | (e[3] << 16);
-        packed.z = e[4] | (e[5] << 16);
-        packed.w = e[6] | (e[7] << 16);
-        *reinterpret_cast<u32x4*>(&sVt[(cg + c) * kKP + kg * 8]) = packed;
+        const u32x4 packed = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
+        *reinterpret_cast<u32x4*>(&sVt[vt_off(vp_cq * 4 + c, vp_kg)]) = packed;
       }
     }
-    // ---- S = Q K^T for this wave's 16 keys, all row tiles; mask; per-row block max
-    float sv[kRT][4];
-    const bool key_ok = my_key < nk;
+  };
+
+  f32x4 o[CT];
 #pragma unroll
-    for (int rt = 0; rt < kRT; ++rt) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+  for (int ct = 0; ct < CT; ++ct) o[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run[4], l_run[4];
 #pragma unroll
-      for (int kc = 0; kc < KC; ++kc) {
-        const u32x4 af = *reinterpret_cast<const u32x4*>(&sQ[(rt * 16 + (l % 16)) * DP + kc * 32 + (l / 16) * 8]);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(kf[kc]), c, 0, 0, 0);
-      }
+  for (int i = 0; i < 4; ++i) {
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.f;
+  }
+  uint16_t* pw = sP[w];
+
+  load_step(kb0);
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int key0 = kb * kKB;
+    __syncthreads();  // the previous step's tiles are consumed
+    stage_step();
+    __syncthreads();
+    if (kb + 1 < kb1) load_step(kb + 1);  // in flight during this step's MFMAs
+    // ---- S = Q K^T: this wave's 16 rows x 64 keys (4 key tiles)
+    f32x4 sacc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = rt * 16 + (l / 16) * 4 + i;  // row within the tile
-        const int t = (m0 + r) / a.G;
-        const bool ok = key_ok && r < rows && visible(my_key, prefix, t, a.mask_mode, a.n_clean);
-        sv[rt][i] = ok ? c[i] * a.scale_log2 : -INFINITY;
+    for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const bf16x8 qf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sQ[k_off<D>(w * kWR + (l % 16), kc * 4 + l / 16)]));
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const bf16x8 kf =
+            as_bf16x8(*reinterpret_cast<const u32x4*>(&sK[k_off<D>(kt * 16 + (l % 16), kc * 4 + l / 16)]));
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf, kf, sacc[kt], 0, 0, 0);
       }
     }
+    // ---- mask, scale, online softmax (rows (l/16)*4+i; a row's keys across 16 lanes x 4 tiles)
+    const bool edge = key0 + kKB > prefix || key0 + kKB > nk;  // block keys or the cache end
+    float alpha[4];
+    bool moved = false;
 #pragma unroll
-    for (int rt = 0; rt < kRT; ++rt)
+    for (int i = 0; i < 4; ++i) {
+      const int rr = (l / 16) * 4 + i;  // row within the wave
+      const int t = (m0 + w * kWR + rr) / a.G;
+      float mx = -INFINITY;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float mx = row16_max(sv[rt][i]);
-        if ((l % 16) == 0) sMax[w][rt * 16 + (l / 16) * 4 + i] = mx;
+      for (int kt = 0; kt < 4; ++kt) {
+        const int key = key0 + kt * 16 + (l % 16);
+        float v = sacc[kt][i] * a.scale_log2;
+        if (edge && !(key < nk && visible(key, prefix, t, a.mask_mode, a.n_clean))) v = -INFINITY;
+        sacc[kt][i] = v;
+        mx = fmaxf(mx, v);
       }
-    __syncthreads();
-    // ---- P = exp2(S - m_new) (bf16 to LDS), partial row sums, rescale factors
-    float alpha[kRT][4];
-#pragma unroll
-    for (int rt = 0; rt < kRT; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = rt * 16 + (l / 16) * 4 + i;
-        const float m_old = sM[r];
-        float bm = sMax[0][r];
-#pragma unroll
-        for (int ww = 1; ww < kNW; ++ww) bm = fmaxf(bm, sMax[ww][r]);
-        const float m_new = fmaxf(m_old, bm);
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        alpha[rt][i] = exp2f(m_old - m_use);
-        const float p = exp2f(sv[rt][i] - m_use);
-        sP[r * kKP + w * 16 + (l % 16)] = f2bf(p);
-        const float ps = row16_sum(p);
-        if ((l % 16) == 0) sSum[w][r] = ps;
-      }
-    __syncthreads();
-    // ---- running stats (one thread per row) and O rescale
-    for (int r = tid; r < kMT; r += kNW * kWave) {
-      const float m_old = sM[r];
-      float bm = sMax[0][r], ps = sSum[0][r];
-#pragma unroll
-      for (int ww = 1; ww < kNW; ++ww) {
-        bm = fmaxf(bm, sMax[ww][r]);
-        ps += sSum[ww][r];
-      }
-      const float m_new = fmaxf(m_old, bm);
+      mx = row16_max(mx);
+      const float m_new = fmaxf(m_run[i], mx);
       const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      sL[r] = sL[r] * exp2f(m_old - m_use) + ps;
-      sM[r] = m_new;
-    }
+      alpha[i] = exp2f(m_run[i] - m_use);
+      moved |= alpha[i] != 1.f;
+      float ps = 0.f;
 #pragma unroll
-    for (int rt = 0; rt < kRT; ++rt)
+      for (int kt = 0; kt < 4; ++kt) {
+        const float p = exp2f(sacc[kt][i] - m_use);
+        ps += p;
+        const int kk = kt * 16 + (l % 16);
+        pw[p_off(rr, kk >> 3) + (kk & 7)] = f2bf(p);
+      }
+      l_run[i] = l_run[i] * alpha[i] + row16_sum(ps);
+      m_run[i] = m_new;
+    }
+    // rescale O only when some row's running max moved (rare once the max settles)
+    if (__ballot(moved)) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[rt][ct][i] *= alpha[rt][i];
-    // ---- O[:, wave columns] += P V: A = P (rows x keys), B = V^T fragment (col, 8 keys)
+        for (int i = 0; i < 4; ++i) o[ct][i] *= alpha[i];
+    }
+    // ---- O += P V (P from this wave's LDS slice in the A layout, V^T fragments from LDS)
 #pragma unroll
     for (int kk = 0; kk < kKB / 32; ++kk) {
-      bf16x8 bfr[CT];
+      const bf16x8 pf = as_bf16x8(*reinterpret_cast<const u32x4*>(&pw[p_off(l % 16, kk * 4 + l / 16)]));
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-        bfr[ct] = as_bf16x8(*reinterpret_cast<const u32x4*>(
-            &sVt[(w * CPW + ct * 16 + (l % 16)) * kKP + kk * 32 + (l / 16) * 8]));
-#pragma unroll
-      for (int rt = 0; rt < kRT; ++rt) {
-        const bf16x8 af = as_bf16x8(*reinterpret_cast<const u32x4*>(&sP[(rt * 16 + (l % 16)) * kKP + kk * 32 + (l / 16) * 8]));
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) o[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[ct], o[rt][ct], 0, 0, 0);
+      for (int ct = 0; ct < CT; ++ct) {
+        const bf16x8 vf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sVt[vt_off(ct * 16 + (l % 16), kk * 4 + l / 16)]));
+        o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, vf, o[ct], 0, 0, 0);
       }
     }
   }
-  __syncthreads();
-  // ---- write this split's unnormalised O and row stats (fp32)
+  // ---- write this split's unnormalised O and row stats
   float* op = a.opart + pbase * kMT * D;
 #pragma unroll
-  for (int rt = 0; rt < kRT; ++rt)
+  for (int i = 0; i < 4; ++i) {
+    const int r = w * kWR + (l / 16) * 4 + i;
+    if (r < rows) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = rt * 16 + (l / 16) * 4 + i;
-        if (r < rows) op[(int64_t)r * D + w * CPW + ct * 16 + (l % 16)] = o[rt][ct][i];
+      for (int ct = 0; ct < CT; ++ct) op[(int64_t)r * D + ct * 16 + (l % 16)] = o[ct][i];
+      if ((l % 16) == 0) {
+        a.mpart[pbase * kMT + r] = m_run[i];
+        a.lpart[pbase * kMT + r] = l_run[i];
       }
-  for (int r = tid; r < rows; r += kNW * kWave) {
-    a.mpart[pbase * kMT + r] = sM[r];
-    a.lpart[pbase * kMT + r] = sL[r];
+    }
   }
 }
 
@@ -286,19 +296,20 @@ struct CombineArgs {
   int64_t gate_st, gate_hs;
 };
 
-// Block = a group of RB rows of one (sequence, KV head); thread = (row, 8 output columns). The split
-// weights exp2(m_s - max) / sum of the group's rows are computed once into LDS; each thread then sums
-// the O rows of the non-empty splits.
+// Block = a group of RB = 1024 / D rows of one (sequence, KV head); thread = (row, 4 output columns).
+// The split weights exp2(m_s - max) / sum of the group's rows are computed once into LDS; each
+// thread then sums the O rows of the non-empty splits, four splits' loads in flight at a time.
 constexpr int kMaxSplits = 256;
+constexpr int kCRB = 16;  // the most rows a combine block holds (D = 64)
 
 __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
-  __shared__ float s_w[32][kMaxSplits];  // rows of the group x listed splits
-  __shared__ float s_inv[32];
+  __shared__ float s_w[kCRB][kMaxSplits];  // rows of the group x listed splits
+  __shared__ float s_inv[kCRB];
   __shared__ int s_list[kMaxSplits];
   __shared__ int s_cnt[4];
   const int M = a.T * a.G;
-  const int per_row = a.D / 8;
-  const int rb = 256 / per_row;  // rows per block: 8 (D=256), 16 (D=128), 32 (D=64)
+  const int per_row = a.D / 4;
+  const int rb = 256 / per_row;  // rows per block: 4 (D=256), 8 (D=128), 16 (D=64)
   const int b = blockIdx.y / a.Hkv, hk = blockIdx.y % a.Hkv;
   const int m0 = blockIdx.x * rb;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -320,54 +331,57 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
   if (any) s_list[off + __popcll(mask & ((1ull << lane) - 1ull))] = tid;
   const int ns = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
   __syncthreads();
-  // per row: max, weights and 1 / sum
-  if (tid < rb && m0 + tid < M) {
-    const int m = m0 + tid;
+  // per row: max, weights and 1 / sum (one wave per row, lanes over the listed splits)
+  for (int i = wave; i < rb; i += 4) {
+    const int m = m0 + i;
+    if (m >= M) break;
     const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
     const int r = m % kMT;
     float mx = -INFINITY;
-    for (int j = 0; j < ns; ++j) mx = fmaxf(mx, a.mpart[(bs + s_list[j]) * kMT + r]);
+    for (int j = lane; j < ns; j += kWave) mx = fmaxf(mx, a.mpart[(bs + s_list[j]) * kMT + r]);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
     const float m_use = mx == -INFINITY ? 0.f : mx;
     float lsum = 0.f;
-    for (int j = 0; j < ns; ++j) {
+    for (int j = lane; j < ns; j += kWave) {
       const float w = exp2f(a.mpart[(bs + s_list[j]) * kMT + r] - m_use);
-      s_w[tid][j] = w;
+      s_w[i][j] = w;
       lsum += w * a.lpart[(bs + s_list[j]) * kMT + r];
     }
-    s_inv[tid] = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, kWave);
+    if (lane == 0) s_inv[i] = lsum > 0.f ? 1.f / lsum : 0.f;
   }
   __syncthreads();
   const int i = tid / per_row;
   const int m = m0 + i;
   if (i >= rb || m >= M) return;
-  const int c = (tid % per_row) * 8;
+  const int c = (tid % per_row) * 4;
   const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
   const int r = m % kMT;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int j = 0; j < ns; ++j) {
-    const float wgt = s_w[i][j];
-    const f32x4* op = reinterpret_cast<const f32x4*>(a.opart + ((bs + s_list[j]) * kMT + r) * a.D + c);
-    const f32x4 x0 = op[0], x1 = op[1];
-    acc[0] += wgt * x0.x; acc[1] += wgt * x0.y; acc[2] += wgt * x0.z; acc[3] += wgt * x0.w;
-    acc[4] += wgt * x1.x; acc[5] += wgt * x1.y; acc[6] += wgt * x1.z; acc[7] += wgt * x1.w;
+  const float* obase = a.opart + (int64_t)r * a.D + c;
+  const int64_t sstride = (int64_t)kMT * a.D;  // floats between consecutive splits
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  int j = 0;
+  for (; j + 4 <= ns; j += 4) {
+    f32x4 x[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const f32x4*>(obase + (bs + s_list[j + u]) * sstride);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += s_w[i][j + u] * x[u];
   }
+  for (; j < ns; ++j) acc += s_w[i][j] * *reinterpret_cast<const f32x4*>(obase + (bs + s_list[j]) * sstride);
   const float inv = s_inv[i];
   const int t = m / a.G, g = m % a.G, hq = hk * a.G + g;
-  uint32_t packed[4];
+  float y[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
+  if (a.gate) {
+    const uint16_t* gp = a.gate + ((int64_t)b * a.T + t) * a.gate_st + (int64_t)hq * a.gate_hs + c;
 #pragma unroll
-  for (int j = 0; j < 8; j += 2) {
-    float y0 = acc[j] * inv, y1 = acc[j + 1] * inv;
-    if (a.gate) {
-      const uint16_t* gp = a.gate + ((int64_t)b * a.T + t) * a.gate_st + (int64_t)hq * a.gate_hs + c + j;
-      // the attention output is rounded to bf16 before the gate, as the torch path does
-      y0 = bf2f(f2bf(y0)) * (1.f / (1.f + __expf(-bf2f(gp[0]))));
-      y1 = bf2f(f2bf(y1)) * (1.f / (1.f + __expf(-bf2f(gp[1]))));
-    }
-    packed[j / 2] = (uint32_t)f2bf(y0) | ((uint32_t)f2bf(y1) << 16);
+    for (int u = 0; u < 4; ++u)  // the attention output is rounded to bf16 before the gate, as torch does
+      y[u] = bf2f(f2bf(y[u])) * (1.f / (1.f + __expf(-bf2f(gp[u]))));
   }
-  *reinterpret_cast<u32x4*>(a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * a.D + c) =
-      u32x4{packed[0], packed[1], packed[2], packed[3]};
+  *reinterpret_cast<u32x2*>(a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * a.D + c) =
+      u32x2{(uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16), (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16)};
 }
 
 // Splits per (sequence, KV head, query tile): enough workgroups to cover the CUs (~512 in all), but
@@ -439,7 +453,7 @@ extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, con
   if (rc) return rc;
   CombineArgs c{opart, mpart, lpart, gate, out, (int)T, (int)Hq, (int)Hkv, (int)G, (int)D, (int)S, (int)QT,
                 gate_row_stride, gate_head_stride};
-  const int64_t rows_per_block = 256 / (D / 8);
+  const int64_t rows_per_block = 256 / (D / 4);
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv)), dim3(256),
                      0, st, c);
   return launch_status("attn_canvas/combine");
