@@ -1,6 +1,6 @@
 """Benchmark of the MI355X self-speculative decode step.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|accept|sample|attn|gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|e2e64|accept|sample|attn|gemm]
 
 Prints ONE JSON line (rank 0). One GPU only: --gpus above 1 exits with a message.
 """
@@ -241,26 +241,36 @@ def bench_attn(args):
 PROMPT_LEN, BLOCK, DENOISE = 2048, 32, 4
 
 
+def _cpu_cache(cfg, ctx: int, prompt_tail, seed: int = 1):
+    """An oracle cache holding a synthetic ctx-token context: random KV entries and GDN states of the
+    real shapes instead of a CPU prefill (which would take minutes at 4B scale)."""
+    import torch
+
+    from oracle import model as OM
+
+    cache = OM.CpuCache()
+    g = torch.Generator().manual_seed(seed)
+    for i in range(cfg.n_layers):
+        if cfg.is_attention(i):
+            shape = (cfg.n_kv_heads, ctx, cfg.head_dim)
+            cache.kv[i] = (torch.randn(*shape, generator=g).bfloat16().float(),
+                           torch.randn(*shape, generator=g).bfloat16().float())
+        else:
+            cache.state[i] = torch.randn(1, cfg.lin_v_heads, cfg.lin_v_dim, cfg.lin_k_dim, generator=g) * 0.05
+            cache.window[i] = torch.randn(1, cfg.conv_kernel - 1, cfg.conv_dim, generator=g).bfloat16().float()
+    cache.tokens = (list(prompt_tail) * (ctx // len(prompt_tail) + 1))[:ctx]
+    return cache
+
+
 def _cpu_baseline_e2e(rt, cfg, prompt_tail, args):
-    """The oracle's draft-then-verify step on the host cores, over a synthetic 2048-token context
-    (random KV entries and GDN states of the real shapes instead of a CPU prefill)."""
+    """The oracle's draft-then-verify step on the host cores, over a synthetic 2048-token context."""
     import torch
 
     from oracle import model as OM
 
     torch.set_num_threads(os.cpu_count() or 1)
     m = OM.CpuHybrid(cfg, rt.w)
-    cache = m.make_cache()
-    g = torch.Generator().manual_seed(1)
-    for i in range(cfg.n_layers):
-        if cfg.is_attention(i):
-            shape = (cfg.n_kv_heads, PROMPT_LEN, cfg.head_dim)
-            cache.kv[i] = (torch.randn(*shape, generator=g).bfloat16().float(),
-                           torch.randn(*shape, generator=g).bfloat16().float())
-        else:
-            cache.state[i] = torch.randn(1, cfg.lin_v_heads, cfg.lin_v_dim, cfg.lin_k_dim, generator=g) * 0.05
-            cache.window[i] = torch.randn(1, cfg.conv_kernel - 1, cfg.conv_dim, generator=g).bfloat16().float()
-    cache.tokens = list(prompt_tail) * (PROMPT_LEN // len(prompt_tail))
+    cache = _cpu_cache(cfg, PROMPT_LEN, prompt_tail)
     t0 = int(prompt_tail[-1])
     steps, acc_tokens = 0, 0
     t = time.perf_counter()
@@ -349,6 +359,124 @@ def bench_e2e(args):
     }
 
 
+# ------------------------------------------------------------------------------ batch-64 sampled (config 5)
+B64, PMIN, PMAX, TEMP, TOP_P = 64, 512, 4096, 0.7, 0.95
+
+
+def _cpu_baseline_e2e64(rt, cfg, prompts, args):
+    """The oracle's sampled draft-then-verify step on the host cores for the first sequence(s) of the
+    batch (sequences are independent; the oracle runs them one at a time), over a synthetic context of
+    that sequence's prompt length."""
+    import numpy as np
+    import torch
+
+    from oracle import model as OM
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    m = OM.CpuHybrid(cfg, rt.w)
+    rng = np.random.default_rng(0)
+    acc_tokens, steps, seqs = 0, 0, 0
+    t = time.perf_counter()
+    for b in range(max(1, args.cpu_steps)):
+        cache = _cpu_cache(cfg, len(prompts[b]), prompts[b][-64:], seed=1 + b)
+        _, _, acc = OM.blockspec_sample_step(m, cache, int(prompts[b][-1]), BLOCK, DENOISE, temperature=TEMP,
+                                             top_k=0, top_p=TOP_P, rng=rng)
+        acc_tokens += 1 + acc
+        steps += 1
+        seqs += 1
+    dt = time.perf_counter() - t
+    return {"value": round(acc_tokens / dt, 4), "unit": "accepted tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{steps} sampled draft-then-verify step(s) (4 denoising passes + verify + rejection-sampling "
+                      f"acceptance + rollback, temperature {TEMP}, top-p {TOP_P}) of the CPU oracle for {seqs} "
+                      f"sequence(s) of the batch, one at a time (fp32 arithmetic, float64 sampling), synthetic "
+                      f"contexts of the prompt lengths {[len(p) for p in prompts[:seqs]]}; {dt:.1f} s"}
+
+
+def bench_e2e64(args):
+    import torch
+
+    from trida_stack_amd import kernels as K
+    from trida_stack_amd.decode import SamplingParams
+    from trida_stack_amd.model import HybridConfig, build_runtime
+    from trida_stack_amd.sampling import SampledBlockSpecStep, Sampler, prefill_batch
+
+    cfg = HybridConfig.four_b()
+    rt = build_runtime(cfg, seed=0)
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(PMIN, PMAX + 1, (B64,), generator=g).tolist()
+    prompts = [torch.randint(0, cfg.vocab - 1024, (n,), generator=g).tolist() for n in lens]
+    total = args.warmup + args.steps
+    cache = rt.make_cache(B64, max_len=max(lens) + (BLOCK + 1) * (total + 2) + 64)
+    smp = Sampler(SamplingParams(temperature=TEMP, top_k=0, top_p=TOP_P, seed=0), rt.dev, ban_id=rt.mask_id)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    logits = prefill_batch(rt, cache, prompts)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t
+    print(f"[bench] e2e64: prefill of {sum(lens)} prompt tokens in {prefill_s:.1f} s", file=sys.stderr, flush=True)
+    step = SampledBlockSpecStep(rt, cache, BLOCK, DENOISE, smp)
+    step.t0.copy_(smp.draw(logits))
+    host_len = list(lens)
+
+    def one():
+        step.run()
+        n = step.n_acc.tolist()  # the host reads the accepted lengths each step to emit tokens
+        for b in range(B64):
+            host_len[b] += 1 + n[b]
+        cache.ctx_hint = max(host_len)
+        return n
+
+    for _ in range(args.warmup):
+        one()
+    torch.cuda.synchronize()
+    K.TIMERS = {} if not args.no_events else None
+    acc_tokens, hist = 0, [0] * (BLOCK + 1)
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        for n in one():
+            acc_tokens += 1 + n
+            hist[n] += 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    smp.check()
+    timers = K.timer_means_us(K.TIMERS) if K.TIMERS is not None else {}
+    K.TIMERS = None
+    rows = B64 * (BLOCK + 1)
+    ctx_avg = sum(host_len) / B64
+    # roofline of the decoder forward at 64 x 33 rows: the GEMMs make it MFMA-bound
+    flops = 2 * cfg.n_params() * rows + 8 * 4 * cfg.n_heads * (BLOCK + 1) * ctx_avg * cfg.head_dim * B64
+    fwd_us = timers.get("forward")
+    roof = None
+    if fwd_us:
+        ach = flops / (fwd_us * 1e-6) / 1e12
+        roof = {"bound": "mfma", "kernel": "decoder forward (64 x 33 canvas rows, every layer)",
+                "achieved": round(ach, 1), "peak": 2500.0, "unit": "TFLOP/s", "frac": round(ach / 2500.0, 4),
+                "traffic": None, "algorithmic_flops": round(flops), "avg_us": round(fwd_us, 1)}
+    cpu = None if args.no_cpu else _cpu_baseline_e2e64(rt, cfg, prompts, args)
+    value = acc_tokens / elapsed
+    return {
+        "metric": METRIC, "value": round(value, 2), "unit": "accepted tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init weights, random prompt ids)",
+        "config": {"workload": "batched sampled self-spec decode, random-init 4B-shape hybrid, batch 64, ragged "
+                               "prompts of 512-4096 tokens, block 32 with 4 denoising passes + verify, temperature "
+                               "0.7, top-p 0.95, rejection sampling of the causal-head p against the draft q, "
+                               "per-sequence KV crops and GDN restores",
+                   "batch": B64, "prompt_lens": [min(lens), max(lens), round(sum(lens) / B64, 1)], "block": BLOCK,
+                   "denoise_passes": DENOISE, "temperature": TEMP, "top_p": TOP_P,
+                   "generated_tokens": acc_tokens, "tokens_per_seq_step": round(acc_tokens / args.steps / B64, 3),
+                   "accept_hist": hist, "params": cfg.n_params()},
+        "verify_step_us": round(timers["verify_step"], 1) if "verify_step" in timers else None,
+        "prefill_s": round(prefill_s, 3),
+        "kernel_avg_us": {k: round(v, 2) for k, v in timers.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
+    }
+
+
+
 def bench_gemm(args):
     """The decode-step projection GEMMs (M = 33 rows) of the 4B-shape model: skinny kernel vs hipBLASLt."""
     import torch
@@ -382,7 +510,7 @@ def bench_gemm(args):
             "cpu_baseline": None}
 
 
-WORKLOADS = {"e2e": (bench_e2e, 256, 8), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
+WORKLOADS = {"e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
              "sample": (bench_sample, 20, 3), "attn": (bench_attn, 100, 10)}
 
 

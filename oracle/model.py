@@ -274,3 +274,43 @@ def blockspec_generate(m: CpuHybrid, prompt: List[int], max_new: int, block: int
         out += emit
         steps += 1
     return out[:max_new], steps
+
+
+# ---------------------------------------------------------------------- sampled draft-then-verify
+def blockspec_sample_step(m: CpuHybrid, cache: CpuCache, t0: int, block: int, denoise: int, *, temperature: float,
+                          top_k: int, top_p: float, rng):
+    """One sampled draft-then-verify step (the rejection-sampling counterpart of blockspec_step):
+    `denoise` passes over [t0, MASK x block]; in each, every slot's candidate is drawn by inverse CDF
+    from its truncated distribution P_j (decode.py:102-130; MASK banned, qwen3_5_diffusion.py:820) and
+    the per-pass quota of MASK slots with the most probable draws (P_j(x_j), ties to the lower slot)
+    is unmasked, keeping P_j as the slot's q row (the draft distribution, qwen3_5_diffusion.py:779).
+    Then a token-causal verify pass, rejection-sampling acceptance (oracle.accept.rejection_accept,
+    decode.py:333-354) and the rollback to 1 + n_acc rows. Uniforms come from the numpy Generator rng.
+    Returns (emitted tokens, next t0, n_acc)."""
+    import numpy as np
+
+    from . import accept as A
+
+    mask = m.mask_id
+    canvas = [t0] + [mask] * block
+    masked = [True] * block
+    per = [block // denoise + (1 if p < block % denoise else 0) for p in range(denoise)]
+    V = m.cfg.vocab
+    q = np.zeros((block, V))
+    for p in range(denoise):
+        L = m.forward(canvas, cache, "draft")
+        cache.pending = None
+        P = A.truncated_probs(L[:block].numpy(), temperature, top_k, top_p, mask)
+        u = rng.random(block)
+        x = [A.sample_inverse_cdf(P[j], float(u[j]))[0] for j in range(block)]
+        cand = sorted((j for j in range(block) if masked[j]), key=lambda j: (-P[j, x[j]], j))
+        for j in cand[: per[p]]:
+            canvas[1 + j] = x[j]
+            masked[j] = False
+            q[j] = P[j]
+    L = m.forward(canvas, cache, "verify")
+    res = A.rejection_accept(L[None].numpy(), q[None], np.asarray([canvas[1:]], np.int64), rng.random((1, block)),
+                             rng.random(1), temperature=temperature, top_k=top_k, top_p=top_p, mask_id=mask)
+    acc, tok = int(res["n_acc"][0]), int(res["token"][0])
+    m.commit(cache, 1 + acc)
+    return canvas[1: 1 + acc] + [tok], tok, acc

@@ -12,8 +12,8 @@ selfspec_generate; decode.py:35-387) over the GPU runtime of trida_stack_amd.mod
       token-causal verify pass over [t0, d_1..d_n], greedy acceptance and rollback of the hybrid state
       (KV crop + GDN restore to 1 + n_acc rows).
 
-Acceptance runs in the fused gfx950 kernels (greedy: split-V argmax + wave prefix scan); the host
-syncs once per step to emit tokens. Greedy decoding is lossless w.r.t. ar_generate up to bf16
+Acceptance runs in the fused gfx950 kernels (greedy: split-V argmax + wave prefix scan; temperature > 0:
+speculative rejection sampling, trida_stack_amd.sampling); the host syncs once per step to emit tokens. Greedy decoding is lossless w.r.t. ar_generate up to bf16
 numerics (the verify rows are the AR computation).
 """
 from __future__ import annotations
@@ -112,17 +112,17 @@ def _prefill(rt: TridaRuntime, cache: SeqCache, prompt: list, stats: DecodeStats
     return logits
 
 
-def _need_greedy(sp: SamplingParams) -> None:
-    if not sp.greedy:
-        raise NotImplementedError("sampled decoding runs through trida_stack_amd.sampling.spec_sample_generate")
-
-
 # ----------------------------------------------------------------------------- AR
 def ar_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
                 sp: SamplingParams, stats: Optional[DecodeStats] = None) -> Iterator[list]:
-    """Greedy causal decoding (decode.py:273-293)."""
-    _need_greedy(sp)
+    """Causal decoding (decode.py:273-293): greedy, or sampled through trida_stack_amd.sampling."""
     stats = stats or DecodeStats()
+    if not sp.greedy:
+        from .sampling import ar_sample_generate
+
+        yield from ar_sample_generate(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids, sp=sp,
+                                      stats=stats)
+        return
     stats.mode = "causal"
     logits = _prefill(rt, cache, prompt, stats)
     emit = _Emitter(stats, max_new_tokens, eos_ids)
@@ -143,8 +143,21 @@ def ar_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_toke
 def selfspec_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
                       sp: SamplingParams, mask_id: int, n: int = 4, stats: Optional[DecodeStats] = None,
                       denoise_steps: int = 0) -> Iterator[list]:
-    """Self-speculative decoding (decode.py:297-387); see the module docstring for the two variants."""
-    _need_greedy(sp)
+    """Self-speculative decoding (decode.py:297-387); see the module docstring for the two variants.
+    Sampling parameters with temperature > 0 run the rejection-sampling versions of both variants
+    (trida_stack_amd.sampling)."""
+    if not sp.greedy:
+        from . import sampling as S
+
+        stats = stats or DecodeStats()
+        if denoise_steps > 0:
+            yield from S.blockspec_sample_generate(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids,
+                                                   sp=sp, mask_id=mask_id, block=n, denoise=denoise_steps,
+                                                   stats=stats)
+        else:
+            yield from S.selfspec_sample_generate(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids,
+                                                  sp=sp, mask_id=mask_id, n=n, stats=stats)
+        return
     if denoise_steps > 0:
         yield from _blockspec(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids, mask_id=mask_id,
                               block=n, denoise=denoise_steps, stats=stats)

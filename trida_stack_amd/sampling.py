@@ -1,0 +1,311 @@
+"""Sampled decoding on MI355X: temperature / top-k / top-p sampling for the AR baseline and speculative
+rejection sampling for self-spec (the canvas algorithm and the batched draft-then-verify step).
+
+Mirrors the sampled branches of inference/zoro-1/mlx/trida_mlx/decode.py:
+  ar_generate         tok ~ truncated_probs(logits)                                   (decode.py:283)
+  selfspec_generate   verify round: ratio p(d)/q(d), accept while ratio >= 1 or u < ratio, correction
+                      from norm(max(0, P - q)), clean + new specs drawn from P[n-1:blk], new q = P[n:blk];
+                      cold start: clean + specs drawn from P[:n], q = P[1:n]        (decode.py:333-387)
+  truncated_probs     temperature, top-k, top-p                                    (decode.py:102-130)
+and the role of the vLLM plugin's sampled self-spec step (_ss_sample_verify, _ss_draft_gumbel_kernel:
+inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:250-285, 787-880), whose q rows are
+full-vocabulary fp32 distributions kept per draft slot (qwen3_5_diffusion.py:779).
+
+Token draws. The reference draws with an RNG (mx.random.categorical / Gumbel noise) that has no
+uniform -> token contract. Here every draw is the inverse CDF in vocabulary order at one seeded uniform,
+token = min{x : cdf(x) > u * mass}, computed on the GPU by the sampled-acceptance kernel (a verify
+with no drafts draws from P_0). The MASK id is banned from every sampled row, drafts and verify alike
+(qwen3_5_diffusion.py:820), so the AR baseline and self-spec share one target distribution.
+"""
+from __future__ import annotations
+
+import time
+from typing import Iterator, List, Optional
+
+import torch
+
+from . import kernels as K
+from .model import SeqCache, TridaRuntime
+
+
+class Sampler:
+    """Seeded sampling of truncated distributions on the device (one generator per decode)."""
+
+    def __init__(self, sp, device: torch.device, ban_id: int = -1):
+        if sp.temperature <= 0:
+            raise ValueError("Sampler needs temperature > 0 (temperature 0 is greedy decoding)")
+        if sp.top_k > K.MAX_TOP_K:
+            raise ValueError(f"top_k <= {K.MAX_TOP_K} is supported (got {sp.top_k})")
+        self.T, self.top_k, self.top_p = float(sp.temperature), int(max(sp.top_k, 0)), float(sp.top_p)
+        self.ban = int(ban_id)
+        self.dev = torch.device(device)
+        self.gen = torch.Generator(device=self.dev)
+        if sp.seed is None:
+            self.gen.seed()
+        else:
+            self.gen.manual_seed(int(sp.seed))
+        self.bad = torch.zeros(1, dtype=torch.int32, device=self.dev)  # any nonzero kernel status so far
+
+    def uniform(self, *shape) -> torch.Tensor:
+        return torch.rand(shape, generator=self.gen, device=self.dev, dtype=torch.float32)
+
+    def _note(self, status: torch.Tensor) -> None:
+        self.bad |= (status != 0).any().to(torch.int32)
+
+    def check(self) -> None:
+        """Raises when any sampled row so far had a NaN / +inf logit or no finite logit."""
+        if int(self.bad):
+            raise FloatingPointError("sampled decoding met a NaN / +inf logit or a row with no finite logit")
+
+    def draw(self, logits: torch.Tensor, u: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """One token per row of logits [..., V] (bf16 or fp32) from the truncated distribution."""
+        V = logits.shape[-1]
+        x = logits.reshape(-1, V)
+        if x.dtype != torch.float32 or x.stride(1) != 1:
+            x = x.float().contiguous()
+        n = x.shape[0]
+        u = self.uniform(n) if u is None else u
+        none = torch.empty((n, 0), dtype=torch.int64, device=self.dev)
+        _, tok, _, _, st = K.sample_accept(x.view(n, 1, V), None, none, None, u, temperature=self.T,
+                                           top_k=self.top_k, top_p=self.top_p, ban_id=self.ban)
+        self._note(st)
+        return tok.view(logits.shape[:-1])
+
+    def stats(self, lf: torch.Tensor):
+        m, thr, zk, st = K.truncate_stats(lf, temperature=self.T, top_k=self.top_k, top_p=self.top_p,
+                                          ban_id=self.ban)
+        self._note(st)
+        return m, thr, zk
+
+    def probs(self, lf: torch.Tensor, stats=None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """Truncated distributions P [B, R, V] fp32 of fp32 logits [B, R, V]."""
+        stats = self.stats(lf) if stats is None else stats
+        return K.truncated_probs(lf, stats, temperature=self.T, ban_id=self.ban, out=out)
+
+    def prob_of(self, lf: torch.Tensor, stats, tok: torch.Tensor) -> torch.Tensor:
+        """P(tok) per row: [y >= thr] exp(y - m) / zk with y = logit / T (the kept-set formula)."""
+        m, thr, zk = stats
+        y = lf.gather(-1, tok.unsqueeze(-1)).squeeze(-1)
+        if self.T != 1.0:
+            y = y / self.T
+        p = torch.exp((y - m).double()) / zk
+        return torch.where(y >= thr, p, torch.zeros_like(p)).float()
+
+    def accept(self, pf: torch.Tensor, q: torch.Tensor, drafts: torch.Tensor, *, ctx_len=None, n_live=None,
+               u_accept: Optional[torch.Tensor] = None, u_sample: Optional[torch.Tensor] = None, out=None):
+        """Rejection-sampling acceptance of a verify pass (fp32 logits [B, R, V], q [B, K, V])."""
+        B, Kd = drafts.shape
+        ua = self.uniform(B, Kd) if u_accept is None else u_accept
+        us = self.uniform(B) if u_sample is None else u_sample
+        res = K.sample_accept(pf, q, drafts, ua, us, temperature=self.T, top_k=self.top_k, top_p=self.top_p,
+                              ban_id=self.ban, ctx_len=ctx_len, n_live=n_live, out=out)
+        self._note(res[4])
+        return res
+
+
+# ----------------------------------------------------------------------------- AR (sampled)
+def ar_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
+                       sp, stats) -> Iterator[list]:
+    """Sampled causal decoding (decode.py:273-293, the sampled branch at :283)."""
+    from .decode import _Emitter, _prefill
+
+    stats.mode = "causal"
+    smp = Sampler(sp, rt.dev, ban_id=rt.mask_id)
+    logits = _prefill(rt, cache, prompt, stats)
+    emit = _Emitter(stats, max_new_tokens, eos_ids)
+    t = time.perf_counter()
+    while True:
+        tok = int(smp.draw(logits.reshape(1, -1))[0])
+        smp.check()
+        out = emit([tok])
+        if out:
+            yield out
+        if emit.done:
+            break
+        logits = rt.ar_step(cache, tok)
+        stats.forwards += 1
+    stats.decode_s = time.perf_counter() - t
+
+
+# ----------------------------------------------------------------------------- self-spec (sampled)
+def selfspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int,
+                             eos_ids: set, sp, mask_id: int, n: int, stats) -> Iterator[list]:
+    """Sampled self-spec with the bd_bidir_shift canvas (decode.py:297-387, sampled branches): one
+    host read per forward (acceptance, correction or clean token, and the next specs together)."""
+    from .decode import _Emitter, _prefill
+
+    stats.mode = f"self-spec(N={n})"
+    stats.accept_hist = [0] * n
+    smp = Sampler(sp, rt.dev, ban_id=mask_id)
+    blk, Kd = 2 * n - 1, n - 1
+    logits = _prefill(rt, cache, prompt, stats)
+    emit = _Emitter(stats, max_new_tokens, eos_ids)
+    t_start = time.perf_counter()
+    t0 = int(smp.draw(logits.reshape(1, -1))[0])
+    t0_emitted = False
+    pending = specs = spec_q = None
+    dev = rt.dev
+    while not emit.done:
+        if specs is not None:  # ---- verify round
+            L = rt.canvas(cache, [pending] + specs + [mask_id] * (n - 1), n, as_float=False)
+            stats.forwards += 1
+            pf = L.float()[None]                                       # [1, blk, V]
+            drafts = torch.as_tensor([specs], dtype=torch.int64, device=dev)
+            n_acc, tok, _, _, _ = smp.accept(pf, spec_q, drafts)
+            new = smp.draw(pf[0, n:blk])                                # next specs (used when all accepted)
+            vals = torch.cat([n_acc.to(torch.int64), tok, new]).tolist()
+            smp.check()
+            acc, tk, new_specs = vals[0], vals[1], vals[2:]
+            if acc < Kd:  # rejected at spec `acc`: tk is the correction, next step cold
+                rt.commit(cache, 1 + acc)
+                stats.accept_hist[acc] += 1
+                out = emit(specs[:acc] + [tk])
+                t0, t0_emitted = tk, True
+                pending = specs = spec_q = None
+            else:  # all accepted: tk is the clean token drawn from P[n-1]
+                rt.commit(cache, n)
+                stats.accept_hist[Kd] += 1
+                out = emit(specs + [tk])
+                pending, specs = tk, new_specs
+                spec_q = smp.probs(pf[:, n:blk].contiguous())
+        else:  # ---- cold start
+            L = rt.canvas(cache, [t0] + [mask_id] * (blk - 1), n, rows=n if rt.skip_rows else None, as_float=False)
+            stats.forwards += 1
+            stats.cold_forwards += 1
+            pf = L[:n].float()[None]                                   # [1, n, V]
+            vals = smp.draw(pf[0]).tolist()
+            smp.check()
+            spec_q = smp.probs(pf[:, 1:n].contiguous())
+            rt.commit(cache, 1)
+            out = emit(([] if t0_emitted else [t0]) + [vals[0]])
+            t0_emitted = True
+            pending, specs = vals[0], vals[1:n]
+        if out:
+            yield out
+    stats.decode_s = time.perf_counter() - t_start
+
+
+class SampledBlockSpecStep:
+    """One batched draft-then-verify step with speculative rejection sampling, on device buffers of fixed
+    shape: `denoise` block-diffusion passes over [t0, MASK x block] (each draws a candidate for every
+    slot from its truncated distribution and unmasks the slots whose draw is most probable, keeping that
+    slot's distribution as its q row), a token-causal verify pass, rejection-sampling acceptance (the
+    correction, or the bonus when every draft is accepted, becomes the next t0) and the hybrid rollback
+    to 1 + n_acc rows per sequence (ragged KV crops and GDN restores).
+
+    Inputs: t0 [B] int64. Outputs after run(): canvas [B, block+1] (row 0 = t0, rows 1.. = drafts),
+    n_acc [B] int32, token [B] int64 (next t0). q rows: [B, block, V] fp32 (the reference layout).
+    trace: a list to which run() appends the pass inputs (for parity tests), or None."""
+
+    def __init__(self, rt: TridaRuntime, cache: SeqCache, block: int, denoise: int, sampler: Sampler):
+        self.rt, self.cache, self.block, self.denoise, self.smp = rt, cache, block, denoise, sampler
+        B, V = cache.B, rt.cfg.vocab
+        dev = rt.dev
+        self.per = [block // denoise + (1 if p < block % denoise else 0) for p in range(denoise)]
+        self.t0 = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.canvas = torch.full((B, block + 1), rt.mask_id, dtype=torch.int64, device=dev)
+        self.masked = torch.ones(B, block, dtype=torch.bool, device=dev)
+        self.ctx = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.n_keep = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.out = (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
+                    torch.empty(B, dtype=torch.int64, device=dev), None, torch.empty(B, dtype=torch.int32, device=dev))
+        self.lf = torch.empty(B, block, V, dtype=torch.float32, device=dev)      # draft rows 0..block-1
+        self.pt = torch.empty(B, block, V, dtype=torch.float32, device=dev)      # their truncated P
+        self.q = torch.zeros(B, block, V, dtype=torch.float32, device=dev)       # q row per draft slot
+        self.pf = torch.empty(B, block + 1, V, dtype=torch.float32, device=dev)  # verify rows
+        self.neg = torch.full((B, block), float("-inf"), dtype=torch.float32, device=dev)
+        self.trace: Optional[list] = None
+
+    @property
+    def n_acc(self) -> torch.Tensor:
+        return self.out[0]
+
+    @property
+    def token(self) -> torch.Tensor:
+        return self.out[1]
+
+    def run(self) -> None:
+        rt, cache, blk, smp = self.rt, self.cache, self.block, self.smp
+        B, V = cache.B, rt.cfg.vocab
+        self.canvas.fill_(rt.mask_id)
+        self.canvas[:, 0] = self.t0
+        self.masked.fill_(True)
+        for p in range(self.denoise):
+            L = rt.forward(self.canvas, cache, "draft")
+            # row j predicts slot j + 1 (shift readout); the last row is not used
+            self.lf.copy_(L[:, :blk])
+            with K.timed("draft_sample"):
+                st = smp.stats(self.lf)
+                u = smp.uniform(B * blk)
+                x = smp.draw(self.lf, u)                                 # [B, blk]
+                conf = smp.prob_of(self.lf, st, x)
+            score = torch.where(self.masked, conf, self.neg)
+            # the per[p] most probable MASK-slot draws (ties: the lower slot first)
+            pos = torch.sort(score, dim=1, descending=True, stable=True).indices[:, : self.per[p]]
+            if self.trace is not None:
+                self.trace.append({"lf": self.lf.clone(), "u": u.clone(), "x": x.clone(),
+                                   "masked": self.masked.clone(), "pos": pos.clone()})
+            self.canvas.scatter_(1, pos + 1, x.gather(1, pos))
+            self.masked.scatter_(1, pos, False)
+            with K.timed("draft_q"):
+                smp.probs(self.lf, st, out=self.pt)
+                idx = pos[:, :, None].expand(-1, -1, V)
+                self.q.scatter_(1, idx, self.pt.gather(1, idx))
+        vt = K.timed("verify_step").__enter__()
+        L = rt.forward(self.canvas, cache, "verify")
+        self.pf.copy_(L)
+        self.ctx.copy_(cache.length)
+        with K.timed("sample_accept"):
+            ua, us = smp.uniform(B, blk), smp.uniform(B)
+            smp.accept(self.pf, self.q, self.canvas[:, 1:], ctx_len=self.ctx, u_accept=ua, u_sample=us, out=self.out)
+        if self.trace is not None:
+            self.trace.append({"pf": self.pf.clone(), "q": self.q.clone(), "drafts": self.canvas[:, 1:].clone(),
+                               "ua": ua.clone(), "us": us.clone()})
+        torch.add(self.n_acc, 1, out=self.n_keep)
+        cache.pending = {"T": blk + 1}
+        rt.commit(cache, self.n_keep)
+        vt.__exit__(None, None, None)
+        self.t0.copy_(self.token)
+
+
+def blockspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int,
+                              eos_ids: set, sp, mask_id: int, block: int, denoise: int, stats) -> Iterator[list]:
+    """Sampled draft-then-verify decode of one sequence over SampledBlockSpecStep."""
+    from .decode import _Emitter, _prefill
+
+    stats.mode = f"self-spec(block={block}, denoise={denoise})"
+    stats.accept_hist = [0] * (block + 1)
+    smp = Sampler(sp, rt.dev, ban_id=mask_id)
+    logits = _prefill(rt, cache, prompt, stats)
+    emit = _Emitter(stats, max_new_tokens, eos_ids)
+    t_start = time.perf_counter()
+    step = SampledBlockSpecStep(rt, cache, block, denoise, smp)
+    t0 = int(smp.draw(logits.reshape(1, -1))[0])
+    out = emit([t0])
+    if out:
+        yield out
+    step.t0.fill_(t0)
+    while not emit.done:
+        step.run()
+        stats.forwards += denoise + 1
+        stats.steps += 1
+        packed = torch.cat([step.canvas[0, 1:], step.token[:1], step.n_acc[:1].to(torch.int64)]).tolist()
+        smp.check()
+        acc = packed[-1]
+        cache.tokens[0].extend([t0] + packed[:acc])
+        cache.ctx_hint = len(cache.tokens[0])
+        stats.accept_hist[acc] += 1
+        t0 = packed[block]
+        out = emit(packed[:acc] + [t0])
+        if out:
+            yield out
+    stats.decode_s = time.perf_counter() - t_start
+
+
+def prefill_batch(rt: TridaRuntime, cache: SeqCache, prompts: List[List[int]]) -> torch.Tensor:
+    """Per-sequence causal prefill of ragged prompts into a batched cache. Returns the fp32 last-token
+    logits [B, V]."""
+    assert len(prompts) == cache.B
+    rows = [rt.prefill(cache, p, seq=b) for b, p in enumerate(prompts)]
+    cache.ctx_hint = max(len(p) for p in prompts)
+    return torch.stack(rows)
