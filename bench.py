@@ -1,6 +1,6 @@
 """Benchmark of the MI355X self-speculative decode step.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|e2e64|accept|sample|attn|gemm]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload e2e|e2e64|gdr|accept|sample|attn|gemm]
 
 Prints ONE JSON line (rank 0). One GPU only: --gpus above 1 exits with a message.
 """
@@ -298,7 +298,7 @@ def bench_e2e(args):
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab - 1024, (PROMPT_LEN,), generator=g).tolist()
     total = args.warmup + args.steps
-    cache = rt.make_cache(1, max_len=PROMPT_LEN + (BLOCK + 1) * (total + 2) + 64)
+    cache = rt.make_cache(1, max_len=PROMPT_LEN + (BLOCK + 1) * (total + 8) + 64)
     torch.cuda.synchronize()
     t = time.perf_counter()
     logits = rt.prefill(cache, prompt)
@@ -310,7 +310,7 @@ def bench_e2e(args):
         step.run()
         cache.ctx_hint += int(step.n_acc[0]) - BLOCK
     torch.cuda.synchronize()
-    K.TIMERS = {} if not args.no_events else None
+    K.TIMERS, K.TIMER_ONLY = ({}, {"forward", "verify_step"}) if not args.no_events else (None, None)
     acc_tokens, hist = 0, [0] * (BLOCK + 1)
     t = time.perf_counter()
     for _ in range(args.steps):
@@ -322,7 +322,7 @@ def bench_e2e(args):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t
     timers = K.timer_means_us(K.TIMERS) if K.TIMERS is not None else {}
-    K.TIMERS = None
+    kern = _kernel_breakdown(step, cache, BLOCK, args)
     ctx = int(cache.length[0])
 
     # roofline of the decoder forward: every weight byte is read once per forward (bf16), plus the KV
@@ -352,11 +352,31 @@ def bench_e2e(args):
                    "accept_hist": hist, "params": cfg.n_params()},
         "verify_step_us": round(timers["verify_step"], 1) if "verify_step" in timers else None,
         "prefill_s": round(prefill_s, 3),
-        "kernel_avg_us": {k: round(v, 2) for k, v in timers.items()},
+        "kernel_avg_us": kern,
         "roofline": roof,
         "cpu_baseline": cpu,
         "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
     }
+
+
+def _kernel_breakdown(step, cache, block, args, steps: int = 4) -> dict:
+    """Per-kernel average durations (HIP events around every launch) over a few extra steps after the
+    timed region, so the event records do not slow the timed steps."""
+    from trida_stack_amd import kernels as K
+
+    if args.no_events:
+        return {}
+    import torch
+
+    K.TIMERS, K.TIMER_ONLY = {}, None
+    for _ in range(steps):
+        step.run()
+        n = step.n_acc.tolist()
+        cache.ctx_hint = max(cache.ctx_hint, int(cache.length.max()))
+    torch.cuda.synchronize()
+    out = {k: round(v, 2) for k, v in K.timer_means_us(K.TIMERS).items()}
+    K.TIMERS = None
+    return out
 
 
 # ------------------------------------------------------------------------------ batch-64 sampled (config 5)
@@ -407,7 +427,7 @@ def bench_e2e64(args):
     lens = torch.randint(PMIN, PMAX + 1, (B64,), generator=g).tolist()
     prompts = [torch.randint(0, cfg.vocab - 1024, (n,), generator=g).tolist() for n in lens]
     total = args.warmup + args.steps
-    cache = rt.make_cache(B64, max_len=max(lens) + (BLOCK + 1) * (total + 2) + 64)
+    cache = rt.make_cache(B64, max_len=max(lens) + (BLOCK + 1) * (total + 8) + 64)
     smp = Sampler(SamplingParams(temperature=TEMP, top_k=0, top_p=TOP_P, seed=0), rt.dev, ban_id=rt.mask_id)
     torch.cuda.synchronize()
     t = time.perf_counter()
@@ -430,7 +450,7 @@ def bench_e2e64(args):
     for _ in range(args.warmup):
         one()
     torch.cuda.synchronize()
-    K.TIMERS = {} if not args.no_events else None
+    K.TIMERS, K.TIMER_ONLY = ({}, {"forward", "verify_step"}) if not args.no_events else (None, None)
     acc_tokens, hist = 0, [0] * (BLOCK + 1)
     t = time.perf_counter()
     for _ in range(args.steps):
@@ -441,7 +461,7 @@ def bench_e2e64(args):
     elapsed = time.perf_counter() - t
     smp.check()
     timers = K.timer_means_us(K.TIMERS) if K.TIMERS is not None else {}
-    K.TIMERS = None
+    kern = _kernel_breakdown(step, cache, BLOCK, args, steps=2)
     rows = B64 * (BLOCK + 1)
     ctx_avg = sum(host_len) / B64
     # roofline of the decoder forward at 64 x 33 rows: the GEMMs make it MFMA-bound
@@ -469,10 +489,104 @@ def bench_e2e64(args):
                    "accept_hist": hist, "params": cfg.n_params()},
         "verify_step_us": round(timers["verify_step"], 1) if "verify_step" in timers else None,
         "prefill_s": round(prefill_s, 3),
-        "kernel_avg_us": {k: round(v, 2) for k, v in timers.items()},
+        "kernel_avg_us": kern,
         "roofline": roof,
         "cpu_baseline": cpu,
         "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
+    }
+
+
+
+# ------------------------------------------------------------------------------ chunked GDR (config 2)
+def bench_gdr(args):
+    """Chunked gated-delta rule of one GDN layer: a 4096-row prefix from a zero state (batch 1, 16 heads,
+    d_k = d_v = 128, chunks of 64), a snapshot of the recurrent state [16, 128, 128] fp32 and the conv
+    window [3, 8192] bf16, a 32-row verify block on top of the prefix state, and the rollback to a seeded
+    accepted length a in [0, 32] (state advanced a rows from the snapshot, window rebuilt)."""
+    import torch
+    import torch.nn.functional as F
+
+    from trida_stack_amd import kernels as K
+
+    dev = torch.device("cuda:0")
+    B, T, H, D, BLK, CH = 1, 4096, 16, 128, 32, 8192
+    g0 = torch.Generator(device=dev).manual_seed(0)
+    l2 = lambda x: x * torch.rsqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    rn = lambda *sh: torch.randn(*sh, generator=g0, device=dev)
+
+    def rows(n):
+        return (l2(rn(B, n, H, D)).bfloat16(), l2(rn(B, n, H, D)).bfloat16(), rn(B, n, H, D).bfloat16(),
+                (-F.softplus(rn(B, n, H))).contiguous(), torch.sigmoid(rn(B, n, H)).contiguous())
+
+    q, k, v, g, beta = rows(T)
+    qb, kb, vb, gb, bb = rows(BLK)
+    s0 = torch.zeros(B, H, D, D, device=dev)
+    s1, snap = torch.empty_like(s0), torch.empty_like(s0)
+    o, ob = torch.empty_like(v), torch.empty_like(vb)
+    win, snap_win = rn(B, 3, CH).bfloat16(), torch.empty(B, 3, CH, dtype=torch.bfloat16, device=dev)
+    pre = rn(B, BLK, CH).bfloat16()
+    a = int(torch.randint(0, BLK + 1, (1,), generator=torch.Generator().manual_seed(0)))
+    n_keep = torch.tensor([a], dtype=torch.int32, device=dev)
+
+    prefix = lambda: K.gdr_chunk(q, k, v, g, beta, s0, state_out=s1, out=o)
+    snapshot = lambda: K.gdn_snapshot(s1, snap, win, snap_win)
+    block = lambda: K.gdr_chunk(qb, kb, vb, gb, bb, s1, causal_mode=1, out=ob)
+
+    def restore():
+        K.gdr_chunk(None, kb, vb, gb, bb, snap, state_out=s1, n_keep=n_keep, want_out=False)
+        K.gdn_restore(n_keep, snap_window=snap_win, window=win, preconv=pre)
+
+    prefix()
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        prefix(), snapshot(), block(), restore()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        prefix(), snapshot(), block(), restore()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    us = {name: _events_time_ms(fn, 50) * 1e3 for name, fn in
+          (("prefix", prefix), ("snapshot", snapshot), ("block", block), ("restore", restore))}
+    # the token-recurrent kernel over the same prefix, for reference
+    rec = lambda: K.gdr_recurrent(q, k, v, g, beta, s0, state_out=s1, out=o)
+    us["prefix_token_recurrent"] = _events_time_ms(rec, 3) * 1e3
+    C = 64
+    flops = (T // C) * H * (C * C * (6 * D + 4 * D) + 6 * C * D * D + 2 * C ** 3 / 3)
+    prefix_bytes = 3 * B * T * H * D * 2 + B * T * H * D * 2 + 2 * B * T * H * 4 + 2 * B * H * D * D * 4
+    snap_bytes = 2 * (B * H * D * D * 4 + B * 3 * CH * 2)
+    total = us["prefix"] + us["snapshot"] + us["block"] + us["restore"]
+    tflops = flops / (us["prefix"] * 1e-6) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        from oracle import gdn as OG
+
+        torch.set_num_threads(os.cpu_count() or 1)
+        hc = [t.float().cpu() for t in (q, k, v, g, beta)]
+        hb = [t.float().cpu() for t in (qb, kb, vb, gb, bb)]
+        tt = time.perf_counter()
+        _, sT = OG.chunked(*hc, torch.zeros(B, H, D, D))
+        snap_h = sT.clone()
+        OG.canvas(*hb, sT, num_clean=BLK, causal_mode=1)
+        OG.restore(snap_h, win.float().cpu(), *hb[1:], pre.float().cpu(), [a])
+        cpu_s = time.perf_counter() - tt
+        cpu = {"value": round(cpu_s * 1e6, 1), "unit": "us per prefix + snapshot + block + rollback",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": "one pass of the oracle (torch fp32 on the host): chunked form over the 4096-row prefix, "
+                         "snapshot copy, 32-row block, rollback to the same a"}
+    return {
+        "metric": METRIC, "value": round(total, 2), "unit": "us per prefix (4096 rows) + snapshot + 32-row block + rollback",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16 in / fp32 state",
+        "data": "synthetic",
+        "config": {"workload": "chunked gated-delta rule, batch 1, 16 heads, d_k = d_v = 128, chunk 64, 4096-row "
+                               "prefix then 32-row block, snapshot and rollback", "accepted_len": a,
+                   "kernel_us": {kk: round(vv, 2) for kk, vv in us.items()},
+                   "prefix_gflop": round(flops / 1e9, 3), "prefix_hbm_GBps": round(prefix_bytes / us["prefix"] / 1e3, 1),
+                   "snapshot_GBps": round(snap_bytes / us["snapshot"] / 1e3, 1)},
+        "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (prep + scan)", "achieved": round(tflops, 1),
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None},
+        "cpu_baseline": cpu,
     }
 
 
@@ -510,7 +624,7 @@ def bench_gemm(args):
             "cpu_baseline": None}
 
 
-WORKLOADS = {"e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
+WORKLOADS = {"e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "gdr": (bench_gdr, 20, 3), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
              "sample": (bench_sample, 20, 3), "attn": (bench_attn, 100, 10)}
 
 

@@ -156,6 +156,33 @@ int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         int64_t Dv, int causal_mode, int64_t num_clean, float scale, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Gated delta rule, chunked WY / UT form on MFMA (v_mfma_f32_16x16x32_bf16), same recurrence and
+ * readout as trida_gdr_recurrent. Replaces chunk_gated_delta_rule(q, k, v, g, beta, chunk_size=64,
+ *   initial_state, output_final_state) (transformers modeling_qwen3_5.py torch_chunk_gated_delta_rule,
+ *   the reference's declared CPU path, train/models/hybrid.py:31-35; FLA / HybridDiffusion
+ *   chunk_block_causal_gated_delta_rule, train/models/hybrid.py:271-281) and, for blocks of T <= 64 rows,
+ *   fused_recurrent_block_causal_gated_delta_rule(..., causal_mode, num_clean)
+ *   (inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:2408-2415).
+ * Per chunk of 64 rows: T = (I + strict_lower(beta K K^T e^{G_t - G_s}))^{-1},
+ *   v_new = T diag(beta) (V - e^G K S^T), o = scale (e^G Q S^T + (Q K^T e^{G_t - G_s})_{s<=t} v_new),
+ *   S^T' = e^{G_last} S^T + K^T diag(e^{G_last - G}) v_new, with G the in-chunk cumulative log decay.
+ * Layouts as trida_gdr_recurrent: q, k [B, T, Hk, Dk] bf16, v [B, T, Hv, Dv] bf16, g, beta [B, T, Hv]
+ * fp32, state_in [B, Hv, Dv, Dk] fp32 (row v = column v of S^T), out [B, T, Hv, Dv] bf16.
+ * out may be NULL (no readout; q may then be NULL). state_out (NULL, or may alias state_in): the state
+ * after the first n rows, n = T, or n = n_keep[b % seq_mod] clamped to [0, T] when n_keep is not NULL
+ * (the rollback of TridaRuntime.commit, inference/zoro-1/mlx/trida_mlx/model.py:486-507).
+ * causal_mode 2 (rows >= num_clean read the block-end state) needs T <= 64 and no n_keep.
+ * Dk in {32, 64, 128}, Dv % 16 == 0. T <= 64: one launch (prep and scan fused per workgroup); T > 64:
+ * a chunk-parallel prep launch then a sequential scan launch, with a workspace of
+ * trida_gdr_chunk_workspace_bytes(B, T, Hv) bytes (0 for T <= 64), 16-byte aligned, no initialisation.
+ */
+int64_t trida_gdr_chunk_workspace_bytes(int64_t B, int64_t T, int64_t Hv);
+int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g, const float* beta,
+                    const float* state_in, uint16_t* out, float* state_out, const int32_t* n_keep, int64_t seq_mod,
+                    int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int causal_mode,
+                    int64_t num_clean, float scale, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * GDN state snapshot: one coalesced copy of state_elems fp32 recurrent-state values and window_elems
  * bf16 conv-window values (any number of layers and sequences laid out contiguously).
  * Replaces the GDN backup before a draft/verify block (SGLang patch

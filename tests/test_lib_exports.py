@@ -79,3 +79,40 @@ def test_mode_registry_matches_reference_launcher():
     import pytest as _p
     with _p.raises(SystemExit):
         cli.main(["--mode", "decide"])
+
+
+def declared_param_counts():
+    """name -> number of parameters of each declaration in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(trida_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+def test_binding_arity_matches_header():
+    """Every ctypes signature has exactly the header's parameter count (a miscount would shift every
+    argument after it)."""
+    counts = declared_param_counts()
+    assert counts, "no declarations parsed"
+    bad = {n: (counts[n], len(_lib.SIGNATURES[n][1])) for n in counts if counts[n] != len(_lib.SIGNATURES[n][1])}
+    assert not bad, bad
+
+
+def test_gdr_chunk_argument_checks():
+    """The chunked GDR entry point rejects bad shapes and modes before launching (dummy pointers)."""
+    lib = _lib.load()
+    P = 256
+    assert lib.trida_gdr_chunk_workspace_bytes(1, 64, 16) == 0
+    assert lib.trida_gdr_chunk_workspace_bytes(1, 4096, 16) == 64 * 16 * 3 * 64 * 64 * 2
+
+    def call(T=100, Dk=128, Dv=128, mode=1, ws=None, ws_bytes=0, n_keep=None):
+        return lib.trida_gdr_chunk(P, P, P, P, P, P, P, P, n_keep, 1, 1, T, 16, 16, Dk, Dv, mode, 0, 0.1, ws,
+                                   ws_bytes, None)
+
+    assert call(Dk=256) == _lib.TRIDA_ERR_ARG and b"Dk" in lib.trida_last_error()
+    assert call(Dv=24) == _lib.TRIDA_ERR_ARG
+    assert call(mode=2) == _lib.TRIDA_ERR_ARG and b"causal_mode 2" in lib.trida_last_error()
+    assert call(T=64, mode=2, n_keep=P) == _lib.TRIDA_ERR_ARG
+    assert call(T=100) == _lib.TRIDA_ERR_WORKSPACE

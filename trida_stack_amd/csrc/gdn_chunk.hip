@@ -1,0 +1,773 @@
+// Gated delta rule, chunked WY / UT form on MFMA (gfx950), with the block-causal canvas readout and the
+// rollback to an accepted prefix of the block.
+//
+// Per value head, one chunk of C = 16 * NB rows with cumulative log decay G_t = sum_{s<=t} g_s inside the
+// chunk and St = S^T [Dk, Dv] at the chunk start (S as stored: [Dv, Dk], row v = column v of St):
+//   A[t][s]   = beta_t (k_t . k_s) e^{G_t - G_s}   (s < t)        T = (I + A)^{-1}
+//   Aqk[t][s] = (q_t . k_s) e^{G_t - G_s}           (s <= t)
+//   v_new     = T diag(beta) (V - e^{G} (K St))     the delta of every row against the chunk-start state
+//   o         = scale (e^{G} (Q St) + Aqk v_new)
+//   St'       = e^{G_{n-1}} St + K^T diag(e^{G_{n-1} - G}) v_new[:n]    (the first n rows absorbed)
+// the chunk-parallel form of S = e^g S; S += beta (v - S k) k^T; o = S q. Every exponent is <= 0, so
+// nothing overflows under strong decay.
+//
+// T is inverted in 16 x 16 blocks: D_i = (I + A_ii)^{-1} by forward substitution (one lane per column),
+// N_ik = D_i A_ik, then block rows T_ij = -sum_{k=j}^{i-1} N_ik T_kj (T_ii = D_i).
+//
+// Precision: products that feed the state (K St, T diag(beta) R, K^T v', and the inverse) split their
+// fp32 operands into bf16 hi + lo parts and sum hi*hi + hi*lo + lo*hi on v_mfma_f32_16x16x32_bf16 /
+// 16x16x16 (about 16 mantissa bits, fp32 accumulation); products that only feed the bf16 output (Q St,
+// Aqk v_new) use the hi parts. Keys, queries and values are bf16 inputs and enter exactly.
+//
+// MFMA lane layouts (wave64): 16x16x32 A fragment = row (l % 16), k = 8 (l / 16) .. + 7; B fragment =
+// column (l % 16), same k; 16x16x16 uses k = 4 (l / 16) .. + 3; the accumulator holds rows
+// 4 (l / 16) .. + 3 of column (l % 16).
+//
+// Kernels:
+//   gdr_chunk_prep   (sequence, chunk of 64 rows, value head): T diag(beta) (hi / lo) and Aqk (hi) of the
+//                    chunk into a workspace, in the swizzled LDS layout the scan copies back verbatim.
+//   gdr_chunk_scan   (sequence, value head, Dv slice): the chunks in order; the state slice stays in MFMA
+//                    accumulators from the first chunk to the last.
+//   gdr_chunk_fused  (sequence, value head, Dv slice): one chunk of T <= 64 rows (a canvas block) with
+//                    prep and scan in one launch; causal_mode 2 rows read the block-end state; without
+//                    an output it is the rollback (state after n_keep rows).
+#include <math.h>
+
+#include "common.h"
+
+namespace trida {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kNT = 256;  // 4 waves
+constexpr int kNW = kNT / kWave;
+constexpr int kChunk = 64;  // rows per chunk of the multi-chunk path
+
+__device__ __forceinline__ f32x4 mfma32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void split(float x, uint16_t& hi, uint16_t& lo) {
+  hi = f2bf(x);
+  lo = f2bf(x - bf2f(hi));
+}
+__device__ __forceinline__ void split4(const float* x, s16x4& hi, s16x4& lo) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    uint16_t h, l;
+    split(x[r], h, l);
+    hi[r] = (short)h;
+    lo[r] = (short)l;
+  }
+}
+// hi*hi + hi*lo + lo*hi of two fp32 16x16 blocks given as 4-element fragments
+__device__ __forceinline__ f32x4 mm3(const float* a, const float* b, f32x4 c) {
+  s16x4 ah, al, bh, bl;
+  split4(a, ah, al);
+  split4(b, bh, bl);
+  c = mfma16(ah, bh, c);
+  c = mfma16(ah, bl, c);
+  return mfma16(al, bh, c);
+}
+
+// bf16 matrix [rows][COLS] in LDS, 16-byte groups XOR-swizzled by the row so that the 8-element fragment
+// reads of 16 consecutive rows (and the 4-element writes from accumulator layouts) spread over banks.
+template <int COLS>
+__device__ __forceinline__ int sw(int r, int c) {
+  constexpr int G = COLS / 8;
+  constexpr int M = (G >= 8 ? 8 : G) - 1;
+  return r * COLS + ((((c >> 3) ^ (r & M))) << 3) + (c & 7);
+}
+template <int COLS>
+__device__ __forceinline__ u32x4 frag8(const uint16_t* m, int r, int c) {
+  return *reinterpret_cast<const u32x4*>(&m[sw<COLS>(r, c)]);
+}
+// 4 bf16 (hi or lo of 4 fp32 values) at row r, columns c .. c + 3 (c % 4 == 0)
+template <int COLS>
+__device__ __forceinline__ void put4(uint16_t* m, int r, int c, const uint16_t* v) {
+  u32x2 w;
+  w.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+  w.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+  *reinterpret_cast<u32x2*>(&m[sw<COLS>(r, c)]) = w;
+}
+template <int COLS>
+__device__ __forceinline__ void put4_split(uint16_t* mh, uint16_t* ml, int r, int c, const float* x) {
+  uint16_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) split(x[i], h[i], l[i]);
+  put4<COLS>(mh, r, c, h);
+  if (ml) put4<COLS>(ml, r, c, l);
+}
+
+// LDS plan of one workgroup (bytes). The prep's fp32 scratch (A then N in place, T) overlays the
+// scan-only buffers, which are first written after the prep is done.
+template <int DK, int NB, int DVS>
+struct Lay {
+  static constexpr int C = 16 * NB;
+  static constexpr int PS = C + 4;  // fp32 row stride of the prep matrices
+  static constexpr int kK = 0;                         // K   [C][DK]  bf16 (A operand, rows = t)
+  static constexpr int kKt = kK + C * DK * 2;          // K^T [DK][C]  bf16 (A operand, rows = dk)
+  static constexpr int kQ = kKt + DK * C * 2;          // Q   [C][DK]  bf16
+  static constexpr int kV = kQ + C * DK * 2;           // V   [C][DVS] fp32 (this workgroup's columns)
+  static constexpr int kG = kV + C * DVS * 4;          // G   [C] fp32 (cumulative log decay)
+  static constexpr int kBeta = kG + C * 4;             // beta [C] fp32
+  static constexpr int kTbH = kBeta + C * 4;           // T diag(beta) [C][C] bf16 hi / lo
+  static constexpr int kTbL = kTbH + C * C * 2;
+  static constexpr int kAq = kTbL + C * C * 2;         // Aqk [C][C] bf16 hi
+  static constexpr int kSH = kAq + C * C * 2;          // St slice as [DVS][DK] bf16 hi / lo (B operand)
+  static constexpr int kSL = kSH + DVS * DK * 2;
+  static constexpr int kRH = kSL + DVS * DK * 2;       // R, v_new, v' as [DVS][C] bf16 (B operands)
+  static constexpr int kRL = kRH + DVS * C * 2;
+  static constexpr int kVn = kRL + DVS * C * 2;
+  static constexpr int kVpH = kVn + DVS * C * 2;
+  static constexpr int kVpL = kVpH + DVS * C * 2;
+  static constexpr int kEnd = kVpL + DVS * C * 2;
+  static constexpr int kPA = kSH;                      // prep: A, then N in place   [C][PS] fp32
+  static constexpr int kPT = kPA + C * PS * 4;         // prep: T                    [C][PS] fp32
+  static constexpr int kPEnd = kPT + C * PS * 4;
+  static constexpr int BYTES = kPEnd > kEnd ? kPEnd : kEnd;
+  static_assert(BYTES <= 160 * 1024, "LDS plan exceeds 160 KiB");
+};
+
+struct ChunkArgs {
+  const uint16_t* q;       // [B, T, Hk, DK]
+  const uint16_t* k;       // [B, T, Hk, DK]
+  const uint16_t* v;       // [B, T, Hv, Dv]
+  const float* g;          // [B, T, Hv]
+  const float* beta;       // [B, T, Hv]
+  const float* state_in;   // [B, Hv, Dv, DK]
+  uint16_t* out;           // [B, T, Hv, Dv] or null (no readout)
+  float* state_out;        // [B, Hv, Dv, DK] or null
+  const int32_t* n_keep;   // [seq_mod] or null: rows absorbed into state_out
+  uint16_t* ws;            // prep workspace: [B, nchunks, Hv][3][64 x 64] bf16
+  int T, Hk, Hv, Dv, nc, seq_mod, nchunks;
+  float scale;
+};
+
+// ---------------------------------------------------------------------------------------------- staging
+// Rows [t0, t0 + cc) of sequence b into LDS (rows cc..C-1 zero): K (row-major and transposed), Q when
+// WANT_Q, the V slice [dv0, dv0 + DVS) when WANT_V, G (inclusive cumsum of g) and beta.
+template <int DK, int NB, int DVS, bool WANT_Q, bool WANT_KT, bool WANT_V>
+__device__ void stage_rows(unsigned char* smem, const ChunkArgs& a, int b, int h, int hk, int dv0, int t0, int cc) {
+  using L = Lay<DK, NB, DVS>;
+  constexpr int C = L::C;
+  uint16_t* sK = reinterpret_cast<uint16_t*>(smem + L::kK);
+  uint16_t* sKt = reinterpret_cast<uint16_t*>(smem + L::kKt);
+  uint16_t* sQ = reinterpret_cast<uint16_t*>(smem + L::kQ);
+  float* sV = reinterpret_cast<float*>(smem + L::kV);
+  float* sG = reinterpret_cast<float*>(smem + L::kG);
+  float* sBeta = reinterpret_cast<float*>(smem + L::kBeta);
+  const int tid = threadIdx.x;
+  const int64_t qk_row = (int64_t)a.Hk * DK;
+  const uint16_t* kb = a.k + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK;
+  const uint16_t* qb = a.q ? a.q + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK : nullptr;
+  // K: 8 x 8 squares, written row-major and transposed
+  constexpr int KSQ = (C / 8) * (DK / 8);
+  for (int sq = tid; sq < KSQ; sq += kNT) {
+    const int rb = sq / (DK / 8), cb = sq % (DK / 8);
+    u32x4 rows[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int t = rb * 8 + r;
+      rows[r] = t < cc ? *reinterpret_cast<const u32x4*>(kb + (int64_t)t * qk_row + cb * 8) : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&sK[sw<DK>(t, cb * 8)]) = rows[r];
+    }
+    if (WANT_KT) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {  // column dk = cb * 8 + j of the 8 rows
+        uint16_t e[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const uint32_t w = rows[r][j >> 1];
+          e[r] = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
+        }
+        u32x4 o;
+        o.x = (uint32_t)e[0] | ((uint32_t)e[1] << 16);
+        o.y = (uint32_t)e[2] | ((uint32_t)e[3] << 16);
+        o.z = (uint32_t)e[4] | ((uint32_t)e[5] << 16);
+        o.w = (uint32_t)e[6] | ((uint32_t)e[7] << 16);
+        *reinterpret_cast<u32x4*>(&sKt[sw<C>(cb * 8 + j, rb * 8)]) = o;
+      }
+    }
+  }
+  if (WANT_Q) {
+    constexpr int QP = C * (DK / 8);
+    for (int p = tid; p < QP; p += kNT) {
+      const int t = p / (DK / 8), c = (p % (DK / 8)) * 8;
+      *reinterpret_cast<u32x4*>(&sQ[sw<DK>(t, c)]) =
+          t < cc ? *reinterpret_cast<const u32x4*>(qb + (int64_t)t * qk_row + c) : u32x4{0, 0, 0, 0};
+    }
+  }
+  if (WANT_V) {
+    const int64_t v_row = (int64_t)a.Hv * a.Dv;
+    const uint16_t* vb = a.v + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0;
+    constexpr int VP = C * (DVS / 8);
+    for (int p = tid; p < VP; p += kNT) {
+      const int t = p / (DVS / 8), c = (p % (DVS / 8)) * 8;
+      const u32x4 w = t < cc ? *reinterpret_cast<const u32x4*>(vb + (int64_t)t * v_row + c) : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sV[t * DVS + c + 2 * i] = bf2f((uint16_t)(w[i] & 0xffffu));
+        sV[t * DVS + c + 2 * i + 1] = bf2f((uint16_t)(w[i] >> 16));
+      }
+    }
+  }
+  if (tid < kWave) {  // G = inclusive cumsum of g over the chunk (rows past cc carry the last value)
+    const int t = tid;
+    const int64_t gi = ((int64_t)b * a.T + t0 + t) * a.Hv + h;
+    float gv = (t < cc && t < C) ? a.g[gi] : 0.f;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const float o = __shfl_up(gv, off, kWave);
+      if (t >= off) gv += o;
+    }
+    if (t < C) {
+      sG[t] = gv;
+      sBeta[t] = t < cc ? a.beta[gi] : 0.f;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- prep
+// From sK, sQ, sG, sBeta: T diag(beta) (hi / lo) into sTbH / sTbL and Aqk (hi) into sAq (when WANT_Q).
+// Uses and ends with __syncthreads; the caller synchronises after staging.
+template <int DK, int NB, int DVS, bool WANT_Q>
+__device__ void prep_chunk(unsigned char* smem) {
+  using L = Lay<DK, NB, DVS>;
+  constexpr int C = L::C, PS = L::PS;
+  const uint16_t* sK = reinterpret_cast<const uint16_t*>(smem + L::kK);
+  const uint16_t* sQ = reinterpret_cast<const uint16_t*>(smem + L::kQ);
+  const float* sG = reinterpret_cast<const float*>(smem + L::kG);
+  const float* sBeta = reinterpret_cast<const float*>(smem + L::kBeta);
+  uint16_t* sTbH = reinterpret_cast<uint16_t*>(smem + L::kTbH);
+  uint16_t* sTbL = reinterpret_cast<uint16_t*>(smem + L::kTbL);
+  uint16_t* sAq = reinterpret_cast<uint16_t*>(smem + L::kAq);
+  float* pA = reinterpret_cast<float*>(smem + L::kPA);
+  float* pT = reinterpret_cast<float*>(smem + L::kPT);
+  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+  const int lr = l % 16, lg = l / 16;
+
+  // zero T diag(beta) and Aqk (their upper blocks stay zero)
+  for (int p = tid; p < C * C / 8; p += kNT) {
+    reinterpret_cast<u32x4*>(sTbH)[p] = u32x4{0, 0, 0, 0};
+    reinterpret_cast<u32x4*>(sTbL)[p] = u32x4{0, 0, 0, 0};
+    if (WANT_Q) reinterpret_cast<u32x4*>(sAq)[p] = u32x4{0, 0, 0, 0};
+  }
+  __syncthreads();
+  // P1: K K^T and Q K^T on the lower block tiles (i >= j)
+  constexpr int NTL = NB * (NB + 1) / 2;
+  for (int tile = w; tile < NTL; tile += kNW) {
+    int i = 0, rem = tile;
+    while (rem > i) {
+      rem -= i + 1;
+      ++i;
+    }
+    const int j = rem;
+    f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < DK / 32; ++kc) {
+      const u32x4 bf = frag8<DK>(sK, 16 * j + lr, 32 * kc + 8 * lg);
+      kk = mfma32(frag8<DK>(sK, 16 * i + lr, 32 * kc + 8 * lg), bf, kk);
+      if (WANT_Q) qk = mfma32(frag8<DK>(sQ, 16 * i + lr, 32 * kc + 8 * lg), bf, qk);
+    }
+    const int s = 16 * j + lr;
+    const float gs = sG[s];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = 16 * i + 4 * lg + r;
+      const float dec = __expf(sG[t] - gs);
+      pA[t * PS + s] = s < t ? sBeta[t] * kk[r] * dec : 0.f;
+      if (WANT_Q) sAq[sw<C>(t, s)] = f2bf(s <= t ? qk[r] * dec : 0.f);
+    }
+  }
+  __syncthreads();
+  // P2: diagonal blocks D_i = (I + A_ii)^{-1}, one lane per column (wave 0, block = lane / 16)
+  if (w == 0 && lg < NB) {
+    const int o = 16 * lg;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = (i == lr) ? 1.f : 0.f;
+      const float* arow = pA + (o + i) * PS + o;
+#pragma unroll
+      for (int j = 0; j < i; ++j) s = fmaf(-arow[j], x[j], s);
+      x[i] = s;
+    }
+    const float bs = sBeta[o + lr];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      pT[(o + i) * PS + o + lr] = x[i];
+      uint16_t hi, lo;
+      split(x[i] * bs, hi, lo);
+      sTbH[sw<C>(o + i, o + lr)] = hi;
+      sTbL[sw<C>(o + i, o + lr)] = lo;
+    }
+  }
+  if (NB == 1) {
+    __syncthreads();
+    return;
+  }
+  __syncthreads();
+  // P3: N_ik = D_i A_ik (i > k), in place over A_ik
+  constexpr int NOFF = NB * (NB - 1) / 2;
+  for (int tile = w; tile < NOFF; tile += kNW) {
+    int i = 1, rem = tile;
+    while (rem >= i) {
+      rem -= i;
+      ++i;
+    }
+    const int kb = rem;
+    float af[4], bfv[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      af[r] = pT[(16 * i + lr) * PS + 16 * i + 4 * lg + r];     // D_i [row lr][k]
+      bfv[r] = pA[(16 * i + 4 * lg + r) * PS + 16 * kb + lr];   // A_ik [k][col lr]
+    }
+    const f32x4 n = mm3(af, bfv, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pA[(16 * i + 4 * lg + r) * PS + 16 * kb + lr] = n[r];
+  }
+  // P4: block rows T_ij = -sum_{k=j}^{i-1} N_ik T_kj
+#pragma unroll
+  for (int i = 1; i < NB; ++i) {
+    __syncthreads();
+    if (w < i) {
+      const int j = w;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int kb = j; kb < i; ++kb) {
+        float af[4], bfv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          af[r] = pA[(16 * i + lr) * PS + 16 * kb + 4 * lg + r];   // N_ik [row lr][k]
+          bfv[r] = pT[(16 * kb + 4 * lg + r) * PS + 16 * j + lr];  // T_kj [k][col lr]
+        }
+        acc = mm3(af, bfv, acc);
+      }
+      const int s = 16 * j + lr;
+      const float bs = sBeta[s];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * i + 4 * lg + r;
+        const float tv = -acc[r];
+        pT[t * PS + s] = tv;
+        uint16_t hi, lo;
+        split(tv * bs, hi, lo);
+        sTbH[sw<C>(t, s)] = hi;
+        sTbL[sw<C>(t, s)] = lo;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------------- scan
+// State slice registers: wave w owns the dk row tiles w, w + 4, ... (< DK / 16) and every dv column tile.
+template <int DK>
+struct StTiles {
+  static constexpr int NMT = DK / 16;
+  static constexpr int PER = (NMT + kNW - 1) / kNW;
+};
+
+template <int DK, int DVS>
+__device__ __forceinline__ void load_state(f32x4 (&st)[StTiles<DK>::PER][DVS / 16], const float* sp, int w, int l) {
+#pragma unroll
+  for (int m = 0; m < StTiles<DK>::PER; ++m) {
+    const int mt = w + kNW * m;
+#pragma unroll
+    for (int ct = 0; ct < DVS / 16; ++ct) {
+      if (mt < StTiles<DK>::NMT)
+        st[m][ct] = *reinterpret_cast<const f32x4*>(sp + (int64_t)(16 * ct + l % 16) * DK + 16 * mt + 4 * (l / 16));
+      else
+        st[m][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+}
+template <int DK, int DVS>
+__device__ __forceinline__ void store_state(const f32x4 (&st)[StTiles<DK>::PER][DVS / 16], float* sp, int w, int l) {
+#pragma unroll
+  for (int m = 0; m < StTiles<DK>::PER; ++m) {
+    const int mt = w + kNW * m;
+    if (mt >= StTiles<DK>::NMT) continue;
+#pragma unroll
+    for (int ct = 0; ct < DVS / 16; ++ct)
+      *reinterpret_cast<f32x4*>(sp + (int64_t)(16 * ct + l % 16) * DK + 16 * mt + 4 * (l / 16)) = st[m][ct];
+  }
+}
+// St (hi / lo) into sSH / sSL as [dv][dk]
+template <int DK, int NB, int DVS>
+__device__ __forceinline__ void put_state(unsigned char* smem, const f32x4 (&st)[StTiles<DK>::PER][DVS / 16], int w,
+                                          int l) {
+  using L = Lay<DK, NB, DVS>;
+  uint16_t* sSH = reinterpret_cast<uint16_t*>(smem + L::kSH);
+  uint16_t* sSL = reinterpret_cast<uint16_t*>(smem + L::kSL);
+#pragma unroll
+  for (int m = 0; m < StTiles<DK>::PER; ++m) {
+    const int mt = w + kNW * m;
+    if (mt >= StTiles<DK>::NMT) continue;
+#pragma unroll
+    for (int ct = 0; ct < DVS / 16; ++ct) {
+      float x[4] = {st[m][ct][0], st[m][ct][1], st[m][ct][2], st[m][ct][3]};
+      put4_split<DK>(sSH, sSL, 16 * ct + l % 16, 16 * mt + 4 * (l / 16), x);
+    }
+  }
+}
+
+// One chunk (LDS staged and prepped): rows t < cc; the first n_abs rows are absorbed into the state;
+// rows t < n_out get the chunk readout written to out_rows (row t at out_rows + t * out_stride), when
+// out_rows is not null. Ends with the state updated in registers.
+template <int DK, int NB, int DVS>
+__device__ void scan_chunk(unsigned char* smem, f32x4 (&st)[StTiles<DK>::PER][DVS / 16], int cc, int n_abs,
+                           int n_out, uint16_t* out_rows, int64_t out_stride, float scale) {
+  using L = Lay<DK, NB, DVS>;
+  constexpr int C = L::C, NCT = DVS / 16;
+  const uint16_t* sK = reinterpret_cast<const uint16_t*>(smem + L::kK);
+  const uint16_t* sKt = reinterpret_cast<const uint16_t*>(smem + L::kKt);
+  const uint16_t* sQ = reinterpret_cast<const uint16_t*>(smem + L::kQ);
+  const float* sV = reinterpret_cast<const float*>(smem + L::kV);
+  const float* sG = reinterpret_cast<const float*>(smem + L::kG);
+  const uint16_t* sTbH = reinterpret_cast<const uint16_t*>(smem + L::kTbH);
+  const uint16_t* sTbL = reinterpret_cast<const uint16_t*>(smem + L::kTbL);
+  const uint16_t* sAq = reinterpret_cast<const uint16_t*>(smem + L::kAq);
+  uint16_t* sSH = reinterpret_cast<uint16_t*>(smem + L::kSH);
+  uint16_t* sSL = reinterpret_cast<uint16_t*>(smem + L::kSL);
+  uint16_t* sRH = reinterpret_cast<uint16_t*>(smem + L::kRH);
+  uint16_t* sRL = reinterpret_cast<uint16_t*>(smem + L::kRL);
+  uint16_t* sVn = reinterpret_cast<uint16_t*>(smem + L::kVn);
+  uint16_t* sVpH = reinterpret_cast<uint16_t*>(smem + L::kVpH);
+  uint16_t* sVpL = reinterpret_cast<uint16_t*>(smem + L::kVpL);
+  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+  const int lr = l % 16, lg = l / 16;
+  const bool want_out = out_rows != nullptr && n_out > 0;
+  const bool row_wave = w < NB;  // wave w owns chunk rows [16 w, 16 w + 16)
+
+  put_state<DK, NB, DVS>(smem, st, w, l);
+  __syncthreads();
+  // K St (hi + lo) and Q St (hi); R = V - e^G K St
+  f32x4 qs[NCT];
+  if (row_wave) {
+    f32x4 ks[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) ks[ct] = qs[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < DK / 32; ++kc) {
+      const u32x4 af = frag8<DK>(sK, 16 * w + lr, 32 * kc + 8 * lg);
+      u32x4 qf;
+      if (want_out) qf = frag8<DK>(sQ, 16 * w + lr, 32 * kc + 8 * lg);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const u32x4 sh = frag8<DK>(sSH, 16 * ct + lr, 32 * kc + 8 * lg);
+        const u32x4 sl = frag8<DK>(sSL, 16 * ct + lr, 32 * kc + 8 * lg);
+        ks[ct] = mfma32(af, sh, ks[ct]);
+        ks[ct] = mfma32(af, sl, ks[ct]);
+        if (want_out) qs[ct] = mfma32(qf, sh, qs[ct]);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      float r[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * lg + i;
+        const float eg = __expf(sG[t]);
+        r[i] = sV[t * DVS + 16 * ct + lr] - eg * ks[ct][i];
+        qs[ct][i] *= eg;
+      }
+      put4_split<C>(sRH, sRL, 16 * ct + lr, 16 * w + 4 * lg, r);
+    }
+  }
+  __syncthreads();
+  // v_new = T diag(beta) R (hi*hi + hi*lo + lo*hi); v' = e^{G_{n-1} - G} v_new on the absorbed rows
+  const float gl = n_abs > 0 ? sG[n_abs - 1] : 0.f;
+  if (row_wave) {
+    f32x4 vn[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) vn[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < C / 32; ++kc) {
+      if (32 * kc > 16 * w + 15) break;  // T is lower triangular
+      const u32x4 th = frag8<C>(sTbH, 16 * w + lr, 32 * kc + 8 * lg);
+      const u32x4 tl = frag8<C>(sTbL, 16 * w + lr, 32 * kc + 8 * lg);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        const u32x4 rh = frag8<C>(sRH, 16 * ct + lr, 32 * kc + 8 * lg);
+        const u32x4 rl = frag8<C>(sRL, 16 * ct + lr, 32 * kc + 8 * lg);
+        vn[ct] = mfma32(th, rh, vn[ct]);
+        vn[ct] = mfma32(th, rl, vn[ct]);
+        vn[ct] = mfma32(tl, rh, vn[ct]);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      float x[4], vp[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * w + 4 * lg + i;
+        x[i] = vn[ct][i];
+        vp[i] = t < n_abs ? __expf(gl - sG[t]) * vn[ct][i] : 0.f;
+      }
+      if (want_out) put4_split<C>(sVn, nullptr, 16 * ct + lr, 16 * w + 4 * lg, x);
+      put4_split<C>(sVpH, sVpL, 16 * ct + lr, 16 * w + 4 * lg, vp);
+    }
+  }
+  __syncthreads();
+  // o = scale (e^G Q St + Aqk v_new)
+  if (want_out && row_wave) {
+#pragma unroll
+    for (int kc = 0; kc < C / 32; ++kc) {
+      if (32 * kc > 16 * w + 15) break;
+      const u32x4 aq = frag8<C>(sAq, 16 * w + lr, 32 * kc + 8 * lg);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) qs[ct] = mfma32(aq, frag8<C>(sVn, 16 * ct + lr, 32 * kc + 8 * lg), qs[ct]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * lg + i;
+      if (t < n_out && t < cc) {
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) out_rows[(int64_t)t * out_stride + 16 * ct + lr] = f2bf(scale * qs[ct][i]);
+      }
+    }
+  }
+  // St = e^{G_{n-1}} St + K^T v' (hi + lo)
+  if (n_abs > 0) {
+    const float dl = __expf(gl);
+#pragma unroll
+    for (int m = 0; m < StTiles<DK>::PER; ++m) {
+      const int mt = w + kNW * m;
+      if (mt >= StTiles<DK>::NMT) continue;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[m][ct][i] *= dl;
+#pragma unroll
+      for (int kc = 0; kc < C / 32; ++kc) {
+        const u32x4 kt = frag8<C>(sKt, 16 * mt + lr, 32 * kc + 8 * lg);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          st[m][ct] = mfma32(kt, frag8<C>(sVpH, 16 * ct + lr, 32 * kc + 8 * lg), st[m][ct]);
+          st[m][ct] = mfma32(kt, frag8<C>(sVpL, 16 * ct + lr, 32 * kc + 8 * lg), st[m][ct]);
+        }
+      }
+    }
+  }
+}
+
+// MASK rows of a canvas block: rows t in [nc, cc) read the block-end state St: o_t = scale q_t . St.
+template <int DK, int NB, int DVS>
+__device__ void mask_rows(unsigned char* smem, const f32x4 (&st)[StTiles<DK>::PER][DVS / 16], int nc, int cc,
+                          uint16_t* out_rows, int64_t out_stride, float scale) {
+  using L = Lay<DK, NB, DVS>;
+  constexpr int NCT = DVS / 16;
+  const uint16_t* sQ = reinterpret_cast<const uint16_t*>(smem + L::kQ);
+  const uint16_t* sSH = reinterpret_cast<const uint16_t*>(smem + L::kSH);
+  const uint16_t* sSL = reinterpret_cast<const uint16_t*>(smem + L::kSL);
+  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+  const int lr = l % 16, lg = l / 16;
+  __syncthreads();  // every wave is done reading sSH / sSL of the scan
+  put_state<DK, NB, DVS>(smem, st, w, l);
+  __syncthreads();
+  if (w < NB && 16 * w + 15 >= nc && 16 * w < cc) {
+    f32x4 qs[NCT];
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) qs[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < DK / 32; ++kc) {
+      const u32x4 qf = frag8<DK>(sQ, 16 * w + lr, 32 * kc + 8 * lg);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        qs[ct] = mfma32(qf, frag8<DK>(sSH, 16 * ct + lr, 32 * kc + 8 * lg), qs[ct]);
+        qs[ct] = mfma32(qf, frag8<DK>(sSL, 16 * ct + lr, 32 * kc + 8 * lg), qs[ct]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = 16 * w + 4 * lg + i;
+      if (t >= nc && t < cc) {
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) out_rows[(int64_t)t * out_stride + 16 * ct + lr] = f2bf(scale * qs[ct][i]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------- kernels
+// Workspace block of one (sequence, chunk, value head): T diag(beta) hi, lo and Aqk hi, 64 x 64 bf16 each.
+constexpr int kWsElems = 3 * kChunk * kChunk;
+
+template <int DK>
+__global__ __launch_bounds__(kNT) void gdr_chunk_prep_kernel(ChunkArgs a) {
+  using L = Lay<DK, 4, 16>;
+  __shared__ __align__(16) unsigned char smem[L::BYTES];
+  int idx = blockIdx.x;
+  const int h = idx % a.Hv;
+  idx /= a.Hv;
+  const int c = idx % a.nchunks;
+  const int b = idx / a.nchunks;
+  const int hk = h / (a.Hv / a.Hk);
+  const int t0 = c * kChunk;
+  const int cc = min(kChunk, a.T - t0);
+  if (a.out) {
+    stage_rows<DK, 4, 16, true, false, false>(smem, a, b, h, hk, 0, t0, cc);
+    __syncthreads();
+    prep_chunk<DK, 4, 16, true>(smem);
+  } else {
+    stage_rows<DK, 4, 16, false, false, false>(smem, a, b, h, hk, 0, t0, cc);
+    __syncthreads();
+    prep_chunk<DK, 4, 16, false>(smem);
+  }
+  u32x4* dst = reinterpret_cast<u32x4*>(a.ws + (((int64_t)b * a.nchunks + c) * a.Hv + h) * kWsElems);
+  const u32x4* src = reinterpret_cast<const u32x4*>(smem + L::kTbH);  // TbH, TbL, Aq are contiguous
+  for (int p = threadIdx.x; p < kWsElems / 8; p += kNT) dst[p] = src[p];
+}
+
+template <int DK, int DVS>
+__global__ __launch_bounds__(kNT) void gdr_chunk_scan_kernel(ChunkArgs a) {
+  using L = Lay<DK, 4, DVS>;
+  __shared__ __align__(16) unsigned char smem[L::BYTES];
+  const int slices = a.Dv / DVS;
+  int idx = blockIdx.x;
+  const int sl = idx % slices;
+  idx /= slices;
+  const int h = idx % a.Hv;
+  const int b = idx / a.Hv;
+  const int hk = h / (a.Hv / a.Hk);
+  const int dv0 = sl * DVS;
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  const int n_tot = a.n_keep ? min(max(a.n_keep[b % a.seq_mod], 0), a.T) : a.T;
+  f32x4 st[StTiles<DK>::PER][DVS / 16];
+  const int64_t soff = (((int64_t)b * a.Hv + h) * a.Dv + dv0) * DK;
+  load_state<DK, DVS>(st, a.state_in + soff, w, l);
+  const int64_t v_row = (int64_t)a.Hv * a.Dv;
+  for (int c = 0; c < a.nchunks; ++c) {
+    const int t0 = c * kChunk;
+    const int cc = min(kChunk, a.T - t0);
+    const int n_abs = min(max(n_tot - t0, 0), cc);
+    if (!a.out && n_abs == 0) break;  // nothing more to absorb and nothing to read out
+    __syncthreads();  // the previous chunk's LDS reads are done
+    if (a.out) stage_rows<DK, 4, DVS, true, true, true>(smem, a, b, h, hk, dv0, t0, cc);
+    else stage_rows<DK, 4, DVS, false, true, true>(smem, a, b, h, hk, dv0, t0, cc);
+    const u32x4* src = reinterpret_cast<const u32x4*>(a.ws + (((int64_t)b * a.nchunks + c) * a.Hv + h) * kWsElems);
+    u32x4* dst = reinterpret_cast<u32x4*>(smem + L::kTbH);
+    for (int p = threadIdx.x; p < kWsElems / 8; p += kNT) dst[p] = src[p];
+    __syncthreads();
+    uint16_t* orow = a.out ? a.out + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
+    scan_chunk<DK, 4, DVS>(smem, st, cc, n_abs, cc, orow, v_row, a.scale);
+  }
+  if (a.state_out) store_state<DK, DVS>(st, a.state_out + soff, w, l);
+}
+
+template <int DK, int NB, int DVS>
+__global__ __launch_bounds__(kNT) void gdr_chunk_fused_kernel(ChunkArgs a) {
+  using L = Lay<DK, NB, DVS>;
+  __shared__ __align__(16) unsigned char smem[L::BYTES];
+  const int slices = a.Dv / DVS;
+  int idx = blockIdx.x;
+  const int sl = idx % slices;
+  idx /= slices;
+  const int h = idx % a.Hv;
+  const int b = idx / a.Hv;
+  const int hk = h / (a.Hv / a.Hk);
+  const int dv0 = sl * DVS;
+  const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+  const int cc = a.T;
+  const int n_abs = a.n_keep ? min(max(a.n_keep[b % a.seq_mod], 0), cc) : cc;
+  if (a.out) {
+    stage_rows<DK, NB, DVS, true, true, true>(smem, a, b, h, hk, dv0, 0, cc);
+    __syncthreads();
+    prep_chunk<DK, NB, DVS, true>(smem);
+  } else {
+    stage_rows<DK, NB, DVS, false, true, true>(smem, a, b, h, hk, dv0, 0, cc);
+    __syncthreads();
+    prep_chunk<DK, NB, DVS, false>(smem);
+  }
+  f32x4 st[StTiles<DK>::PER][DVS / 16];
+  const int64_t soff = (((int64_t)b * a.Hv + h) * a.Dv + dv0) * DK;
+  load_state<DK, DVS>(st, a.state_in + soff, w, l);
+  const int64_t v_row = (int64_t)a.Hv * a.Dv;
+  uint16_t* orow = a.out ? a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
+  const int n_out = min(a.nc, cc);
+  scan_chunk<DK, NB, DVS>(smem, st, cc, n_abs, n_out, orow, v_row, a.scale);
+  if (a.out && n_out < cc) mask_rows<DK, NB, DVS>(smem, st, n_out, cc, orow, v_row, a.scale);
+  if (a.state_out) store_state<DK, DVS>(st, a.state_out + soff, w, l);
+}
+
+template <int DK>
+int launch_dk(ChunkArgs& a, int B, hipStream_t stream) {
+  const bool fused = a.T <= kChunk;
+  // Dv slices: 32 columns when the grid is already wide, else 16
+  const int64_t wide = (int64_t)B * a.Hv * (a.Dv / 32);
+  const int dvs = (a.Dv % 32 == 0 && wide >= 512) ? 32 : 16;
+  const unsigned grid = (unsigned)((int64_t)B * a.Hv * (a.Dv / dvs));
+  if (fused) {
+    const bool nb2 = a.T <= 32;
+    if (dvs == 32) {
+      if (nb2) hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 2, 32>), dim3(grid), dim3(kNT), 0, stream, a);
+      else hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 4, 32>), dim3(grid), dim3(kNT), 0, stream, a);
+    } else {
+      if (nb2) hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 2, 16>), dim3(grid), dim3(kNT), 0, stream, a);
+      else hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 4, 16>), dim3(grid), dim3(kNT), 0, stream, a);
+    }
+    return launch_status("gdr_chunk (single chunk)");
+  }
+  const unsigned pgrid = (unsigned)((int64_t)B * a.nchunks * a.Hv);
+  hipLaunchKernelGGL((gdr_chunk_prep_kernel<DK>), dim3(pgrid), dim3(kNT), 0, stream, a);
+  if (dvs == 32) hipLaunchKernelGGL((gdr_chunk_scan_kernel<DK, 32>), dim3(grid), dim3(kNT), 0, stream, a);
+  else hipLaunchKernelGGL((gdr_chunk_scan_kernel<DK, 16>), dim3(grid), dim3(kNT), 0, stream, a);
+  return launch_status("gdr_chunk (prep + scan)");
+}
+
+}  // namespace
+}  // namespace trida
+
+using namespace trida;
+
+extern "C" int64_t trida_gdr_chunk_workspace_bytes(int64_t B, int64_t T, int64_t Hv) {
+  if (B <= 0 || T <= kChunk || Hv <= 0) return 0;
+  return B * cdiv(T, kChunk) * Hv * (int64_t)kWsElems * 2;
+}
+
+extern "C" int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                               const float* beta, const float* state_in, uint16_t* out, float* state_out,
+                               const int32_t* n_keep, int64_t seq_mod, int64_t B, int64_t T, int64_t Hk, int64_t Hv,
+                               int64_t Dk, int64_t Dv, int causal_mode, int64_t num_clean, float scale,
+                               void* workspace, int64_t workspace_bytes, void* stream) {
+  TRIDA_CHECK(k && v && g && beta && state_in, TRIDA_ERR_NULL, "gdr_chunk: k, v, g, beta and state_in are required");
+  TRIDA_CHECK(out || state_out, TRIDA_ERR_ARG, "gdr_chunk: nothing to compute (out and state_out are both NULL)");
+  TRIDA_CHECK(!out || q, TRIDA_ERR_NULL, "gdr_chunk: q is required with out");
+  TRIDA_CHECK(B > 0 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, TRIDA_ERR_ARG,
+              "gdr_chunk: bad sizes B=%lld T=%lld Hk=%lld Hv=%lld", (long long)B, (long long)T, (long long)Hk,
+              (long long)Hv);
+  TRIDA_CHECK(Dk == 32 || Dk == 64 || Dk == 128, TRIDA_ERR_ARG, "gdr_chunk: Dk must be 32, 64 or 128 (got %lld)",
+              (long long)Dk);
+  TRIDA_CHECK(Dv > 0 && Dv % 16 == 0, TRIDA_ERR_ARG, "gdr_chunk: Dv must be a multiple of 16 (got %lld)",
+              (long long)Dv);
+  TRIDA_CHECK(causal_mode == 1 || causal_mode == 2, TRIDA_ERR_ARG, "gdr_chunk: causal_mode is 1 or 2");
+  TRIDA_CHECK(causal_mode == 1 || T <= kChunk, TRIDA_ERR_ARG,
+              "gdr_chunk: causal_mode 2 (canvas readout) needs T <= %d rows", kChunk);
+  TRIDA_CHECK(causal_mode == 1 || !n_keep, TRIDA_ERR_ARG, "gdr_chunk: n_keep needs causal_mode 1");
+  TRIDA_CHECK(num_clean >= 0, TRIDA_ERR_ARG, "gdr_chunk: num_clean >= 0");
+  TRIDA_CHECK(!n_keep || seq_mod > 0, TRIDA_ERR_ARG, "gdr_chunk: seq_mod > 0 with n_keep");
+  TRIDA_CHECK(((uintptr_t)k & 15) == 0 && (!q || ((uintptr_t)q & 15) == 0) && ((uintptr_t)v & 15) == 0 &&
+                  ((uintptr_t)state_in & 15) == 0 && (!state_out || ((uintptr_t)state_out & 15) == 0),
+              TRIDA_ERR_ALIGN, "gdr_chunk: q, k, v and the states must be 16-byte aligned");
+  TRIDA_CHECK(B * T * Hv < INT32_MAX && B * Hv * Dv < INT32_MAX, TRIDA_ERR_ARG, "gdr_chunk: problem too large");
+  const int64_t nchunks = cdiv(T, kChunk);
+  const int64_t need = trida_gdr_chunk_workspace_bytes(B, T, Hv);
+  TRIDA_CHECK(need == 0 || (workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0),
+              TRIDA_ERR_WORKSPACE, "gdr_chunk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  ChunkArgs a{q,        k,   v,       g,         beta,       state_in,      out,
+              state_out, n_keep, static_cast<uint16_t*>(workspace), (int)T, (int)Hk, (int)Hv, (int)Dv,
+              causal_mode == 2 ? (int)(num_clean < T ? num_clean : T) : (int)T, n_keep ? (int)seq_mod : 1, (int)nchunks,
+              scale};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (Dk) {
+    case 32: return launch_dk<32>(a, (int)B, st);
+    case 64: return launch_dk<64>(a, (int)B, st);
+    default: return launch_dk<128>(a, (int)B, st);
+  }
+}

@@ -57,6 +57,8 @@ workspaces = _Workspaces()
 # Optional live timing: while TIMERS is a dict, the wrappers (and the runtime's forward) record a pair
 # of events on the launching stream around their launches, keyed by name. Eager execution only.
 TIMERS: Optional[dict] = None
+# when not None, only these timer names record events (the rest cost nothing)
+TIMER_ONLY: Optional[set] = None
 
 
 class timed:
@@ -65,7 +67,7 @@ class timed:
         self.ev = None
 
     def __enter__(self):
-        if TIMERS is not None:
+        if TIMERS is not None and (TIMER_ONLY is None or self.name in TIMER_ONLY):
             self.ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             self.ev[0].record()
         return self
@@ -358,6 +360,60 @@ def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         _stream(dev))
     _lib.check(rc, "trida_gdr_recurrent")
     return out, clean
+
+
+def gdr_chunk(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+              state: torch.Tensor, *, causal_mode: int = 1, num_clean: Optional[int] = None,
+              state_out: Optional[torch.Tensor] = None, n_keep: Optional[torch.Tensor] = None,
+              want_out: bool = True, scale: Optional[float] = None, out: Optional[torch.Tensor] = None):
+    """Gated delta rule in the chunked WY / UT form on MFMA (chunks of 64 rows; one fused launch for
+    T <= 64). Same shapes and readout as gdr_recurrent. n_keep (int32 [B] or [seq_mod] with B a multiple):
+    state_out holds the state after the first n_keep[b] rows (the rollback). want_out=False skips the
+    readout (q may be None). Returns out (or None)."""
+    dev = _need_gpu(q, k, v, g, beta, state, state_out, n_keep, out)
+    for t, n in ((k, "k"), (v, "v")) + (((q, "q"),) if q is not None else ()):
+        _bf16(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    for t, n in ((g, "g"), (beta, "beta"), (state, "state")):
+        _f32(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    B, T, Hk, Dk = k.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    if (q is not None and q.shape != k.shape) or v.shape[:2] != (B, T) or g.shape != (B, T, Hv) \
+            or beta.shape != g.shape:
+        raise ValueError("q/k/v/g/beta shapes disagree")
+    if state.shape != (B, Hv, Dv, Dk):
+        raise ValueError(f"state must be [B, Hv, Dv, Dk] = {(B, Hv, Dv, Dk)}")
+    if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
+                                  or not state_out.is_contiguous()):
+        raise ValueError("state_out must match state")
+    seq_mod = 0
+    if n_keep is not None:
+        if n_keep.dtype != torch.int32 or n_keep.dim() != 1 or not n_keep.is_contiguous() or B % n_keep.shape[0]:
+            raise ValueError("n_keep must be int32 [seq_mod] with B a multiple of seq_mod")
+        seq_mod = n_keep.shape[0]
+    if want_out:
+        if q is None:
+            raise ValueError("q is required for the readout")
+        if out is None:
+            out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+        elif out.shape != (B, T, Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+            raise ValueError("gdr_chunk: out must be contiguous bf16 [B, T, Hv, Dv]")
+    else:
+        out = None
+    nc = T if num_clean is None else int(num_clean)
+    sc = Dk ** -0.5 if scale is None else float(scale)
+    lib = _lib.load()
+    nbytes = lib.trida_gdr_chunk_workspace_bytes(B, T, Hv)
+    ws = workspaces.get(dev, "gdr_chunk", nbytes) if nbytes else None
+    rc = lib.trida_gdr_chunk(
+        _ptr(q), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), state.data_ptr(), _ptr(out),
+        _ptr(state_out), _ptr(n_keep), seq_mod, B, T, Hk, Hv, Dk, Dv, causal_mode, nc, sc, _ptr(ws),
+        ws.numel() if ws is not None else 0, _stream(dev))
+    _lib.check(rc, "trida_gdr_chunk")
+    return out
 
 
 def gdn_snapshot(state: torch.Tensor, snap_state: torch.Tensor, window: Optional[torch.Tensor] = None,

@@ -245,6 +245,20 @@ class TridaRuntime:
 
     # ---------------------------------------------------------------- forward
     use_skinny_gemm = False  # the skinny kernel is slower than hipBLASLt at these shapes so far
+    # GDN recurrence form: "chunked" (WY / UT chunks on MFMA, trida_gdr_chunk), "recurrent" (token by
+    # token, trida_gdr_recurrent) or "auto" (chunked over more than one chunk of rows, i.e. prefill;
+    # recurrent for canvas blocks and the rollback, where it measures faster). Both kernels follow the
+    # same recurrence; only "recurrent" makes the rows of a verify block bitwise equal to the same rows
+    # decoded one AR step at a time.
+    gdr_form = "auto"
+
+    def _chunked_gdr(self, T: int, gdn_mode: int) -> bool:
+        c = self.cfg
+        if self.gdr_form == "recurrent" or c.lin_k_dim not in (32, 64, 128) or c.lin_v_dim % 16:
+            return False
+        if self.gdr_form == "auto":
+            return gdn_mode == 1 and T > 64
+        return gdn_mode == 1 or T <= 64
 
     def _mm(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x @ w.T: the skinny weight-streaming kernel for canvas-sized x (<= 64 rows), hipBLASLt
@@ -313,10 +327,16 @@ class TridaRuntime:
                     K.gdn_prep(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"], w[p + "dt_bias"],
                                Hk=c.lin_k_heads, Hv=c.lin_v_heads, Dk=c.lin_k_dim, Dv=c.lin_v_dim,
                                window_out=s.win_tmp if persist else None, out=rec)
-                with K.timed("gdr_recurrent"):
-                    K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
+                if self._chunked_gdr(T, gdn_mode):
+                    with K.timed("gdr_chunk"):
+                        K.gdr_chunk(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
                                     causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
                                     out=s.y)
+                else:
+                    with K.timed("gdr_recurrent"):
+                        K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
+                                        causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
+                                        out=s.y)
                 if persist:
                     window[j].copy_(s.win_tmp)
                 elif mode != "draft":  # a draft pass is never committed
@@ -407,11 +427,17 @@ class TridaRuntime:
         if L:
             st = cache.state.view(L * B, *cache.state.shape[2:])
             win = cache.window.view(L * B, *cache.window.shape[2:])
+            rows = (s.k_rec.view(L * B, *s.k_rec.shape[2:]), s.v_rec.view(L * B, *s.v_rec.shape[2:]),
+                    s.g_rec.view(L * B, *s.g_rec.shape[2:]), s.b_rec.view(L * B, *s.b_rec.shape[2:]))
+            pre = s.pre_rec.view(L * B, *s.pre_rec.shape[2:])
             with K.timed("gdn_restore"):
-                K.gdn_restore(n_keep, snap_state=st, state=st, k=s.k_rec.view(L * B, *s.k_rec.shape[2:]),
-                              v=s.v_rec.view(L * B, *s.v_rec.shape[2:]), g=s.g_rec.view(L * B, *s.g_rec.shape[2:]),
-                              beta=s.b_rec.view(L * B, *s.b_rec.shape[2:]), snap_window=win, window=win,
-                              preconv=s.pre_rec.view(L * B, *s.pre_rec.shape[2:]))
+                if self._chunked_gdr(T, 1):
+                    # every (layer, sequence) slot: the block-entry state advanced by its n_keep rows
+                    K.gdr_chunk(None, *rows, st, state_out=st, n_keep=n_keep, want_out=False)
+                    K.gdn_restore(n_keep, snap_window=win, window=win, preconv=pre)
+                else:
+                    K.gdn_restore(n_keep, snap_state=st, state=st, k=rows[0], v=rows[1], g=rows[2], beta=rows[3],
+                                  snap_window=win, window=win, preconv=pre)
         cache.length += n_keep
         cache.pos += n_keep
         cache.ctx_hint += adv if isinstance(adv, int) else T
