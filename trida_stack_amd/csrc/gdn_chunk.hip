@@ -150,40 +150,106 @@ struct ChunkArgs {
 };
 
 // ---------------------------------------------------------------------------------------------- staging
-// Rows [t0, t0 + cc) of sequence b into LDS (rows cc..C-1 zero): K (row-major and transposed), Q when
-// WANT_Q, the V slice [dv0, dv0 + DVS) when WANT_V, G (inclusive cumsum of g) and beta.
-template <int DK, int NB, int DVS, bool WANT_Q, bool WANT_KT, bool WANT_V>
-__device__ void stage_rows(unsigned char* smem, const ChunkArgs& a, int b, int h, int hk, int dv0, int t0, int cc) {
+// Workspace block of one (sequence, chunk, value head): T diag(beta) hi, lo and Aqk hi, 64 x 64 bf16 each.
+constexpr int kWsElems = 3 * kChunk * kChunk;
+
+// Rows [t0, t0 + cc) of one chunk (rows cc..C-1 read as zero), staged in two steps so that every global
+// load of a chunk is in flight at once: load() issues them into registers, store() writes LDS (K
+// row-major and transposed, Q, the V slice as fp32, G = inclusive cumsum of g, beta and, with WS, the
+// chunk's prep block from the workspace). The multi-chunk scan loads chunk c + 1 while computing c.
+template <int DK, int NB, int DVS, bool WANT_Q, bool WANT_V, bool WS>
+struct Stage {
   using L = Lay<DK, NB, DVS>;
-  constexpr int C = L::C;
-  uint16_t* sK = reinterpret_cast<uint16_t*>(smem + L::kK);
-  uint16_t* sKt = reinterpret_cast<uint16_t*>(smem + L::kKt);
-  uint16_t* sQ = reinterpret_cast<uint16_t*>(smem + L::kQ);
-  float* sV = reinterpret_cast<float*>(smem + L::kV);
-  float* sG = reinterpret_cast<float*>(smem + L::kG);
-  float* sBeta = reinterpret_cast<float*>(smem + L::kBeta);
-  const int tid = threadIdx.x;
-  const int64_t qk_row = (int64_t)a.Hk * DK;
-  const uint16_t* kb = a.k + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK;
-  const uint16_t* qb = a.q ? a.q + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK : nullptr;
-  // K: 8 x 8 squares, written row-major and transposed
-  constexpr int KSQ = (C / 8) * (DK / 8);
-  for (int sq = tid; sq < KSQ; sq += kNT) {
-    const int rb = sq / (DK / 8), cb = sq % (DK / 8);
-    u32x4 rows[8];
+  static constexpr int C = L::C;
+  static constexpr int KSQ = (C / 8) * (DK / 8);  // 8 x 8 squares of K (rows t, columns dk)
+  static constexpr int KSQ_PT = (KSQ + kNT - 1) / kNT;
+  static constexpr int QP = C * DK / 8;           // 16-byte pieces of Q
+  static constexpr int QP_PT = WANT_Q ? (QP + kNT - 1) / kNT : 0;
+  static constexpr int VP = C * DVS / 8;          // 16-byte pieces of the V slice
+  static constexpr int VP_PT = WANT_V ? (VP + kNT - 1) / kNT : 0;
+  static constexpr int WP = kWsElems / 8;
+  static constexpr int WP_PT = WS ? (WP + kNT - 1) / kNT : 0;
+  u32x4 k[KSQ_PT][8];
+  u32x4 q[QP_PT > 0 ? QP_PT : 1];
+  u32x4 v[VP_PT > 0 ? VP_PT : 1];
+  u32x4 ws[WP_PT > 0 ? WP_PT : 1];
+  float g, beta;
+
+  __device__ __forceinline__ void load(const ChunkArgs& a, int b, int h, int hk, int dv0, int t0, int cc,
+                                       int chunk) {
+    const int tid = threadIdx.x;
+    const int64_t qk_row = (int64_t)a.Hk * DK;
+    const uint16_t* kb = a.k + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK;
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const int t = rb * 8 + r;
-      rows[r] = t < cc ? *reinterpret_cast<const u32x4*>(kb + (int64_t)t * qk_row + cb * 8) : u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(&sK[sw<DK>(t, cb * 8)]) = rows[r];
+    for (int i = 0; i < KSQ_PT; ++i) {
+      const int sq = tid + i * kNT;
+      const int rb = sq / (DK / 8), cb = sq % (DK / 8);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int t = rb * 8 + r;
+        k[i][r] = (sq < KSQ && t < cc) ? *reinterpret_cast<const u32x4*>(kb + (int64_t)t * qk_row + cb * 8)
+                                       : u32x4{0, 0, 0, 0};
+      }
     }
-    if (WANT_KT) {
+    if (WANT_Q) {
+      const uint16_t* qb = a.q + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK;
+#pragma unroll
+      for (int i = 0; i < QP_PT; ++i) {
+        const int p = tid + i * kNT;
+        const int t = p / (DK / 8), c = (p % (DK / 8)) * 8;
+        q[i] = (p < QP && t < cc) ? *reinterpret_cast<const u32x4*>(qb + (int64_t)t * qk_row + c)
+                                  : u32x4{0, 0, 0, 0};
+      }
+    }
+    if (WANT_V) {
+      const int64_t v_row = (int64_t)a.Hv * a.Dv;
+      const uint16_t* vb = a.v + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0;
+#pragma unroll
+      for (int i = 0; i < VP_PT; ++i) {
+        const int p = tid + i * kNT;
+        const int t = p / (DVS / 8), c = (p % (DVS / 8)) * 8;
+        v[i] = (p < VP && t < cc) ? *reinterpret_cast<const u32x4*>(vb + (int64_t)t * v_row + c)
+                                  : u32x4{0, 0, 0, 0};
+      }
+    }
+    if (WS) {
+      const u32x4* src =
+          reinterpret_cast<const u32x4*>(a.ws + (((int64_t)b * a.nchunks + chunk) * a.Hv + h) * kWsElems);
+#pragma unroll
+      for (int i = 0; i < WP_PT; ++i) {
+        const int p = tid + i * kNT;
+        ws[i] = p < WP ? src[p] : u32x4{0, 0, 0, 0};
+      }
+    }
+    if (tid < kWave) {
+      const int64_t gi = ((int64_t)b * a.T + t0 + tid) * a.Hv + h;
+      const bool in = tid < cc && tid < C;
+      g = in ? a.g[gi] : 0.f;
+      beta = in ? a.beta[gi] : 0.f;
+    }
+  }
+
+  __device__ __forceinline__ void store(unsigned char* smem) {
+    uint16_t* sK = reinterpret_cast<uint16_t*>(smem + L::kK);
+    uint16_t* sKt = reinterpret_cast<uint16_t*>(smem + L::kKt);
+    uint16_t* sQ = reinterpret_cast<uint16_t*>(smem + L::kQ);
+    float* sV = reinterpret_cast<float*>(smem + L::kV);
+    float* sG = reinterpret_cast<float*>(smem + L::kG);
+    float* sBeta = reinterpret_cast<float*>(smem + L::kBeta);
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < KSQ_PT; ++i) {
+      const int sq = tid + i * kNT;
+      if (sq >= KSQ) continue;
+      const int rb = sq / (DK / 8), cb = sq % (DK / 8);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) *reinterpret_cast<u32x4*>(&sK[sw<DK>(rb * 8 + r, cb * 8)]) = k[i][r];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {  // column dk = cb * 8 + j of the 8 rows
         uint16_t e[8];
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-          const uint32_t w = rows[r][j >> 1];
+          const uint32_t w = k[i][r][j >> 1];
           e[r] = (uint16_t)((j & 1) ? (w >> 16) : (w & 0xffffu));
         }
         u32x4 o;
@@ -194,44 +260,53 @@ __device__ void stage_rows(unsigned char* smem, const ChunkArgs& a, int b, int h
         *reinterpret_cast<u32x4*>(&sKt[sw<C>(cb * 8 + j, rb * 8)]) = o;
       }
     }
-  }
-  if (WANT_Q) {
-    constexpr int QP = C * (DK / 8);
-    for (int p = tid; p < QP; p += kNT) {
-      const int t = p / (DK / 8), c = (p % (DK / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&sQ[sw<DK>(t, c)]) =
-          t < cc ? *reinterpret_cast<const u32x4*>(qb + (int64_t)t * qk_row + c) : u32x4{0, 0, 0, 0};
-    }
-  }
-  if (WANT_V) {
-    const int64_t v_row = (int64_t)a.Hv * a.Dv;
-    const uint16_t* vb = a.v + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0;
-    constexpr int VP = C * (DVS / 8);
-    for (int p = tid; p < VP; p += kNT) {
-      const int t = p / (DVS / 8), c = (p % (DVS / 8)) * 8;
-      const u32x4 w = t < cc ? *reinterpret_cast<const u32x4*>(vb + (int64_t)t * v_row + c) : u32x4{0, 0, 0, 0};
+    if (WANT_Q) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sV[t * DVS + c + 2 * i] = bf2f((uint16_t)(w[i] & 0xffffu));
-        sV[t * DVS + c + 2 * i + 1] = bf2f((uint16_t)(w[i] >> 16));
+      for (int i = 0; i < QP_PT; ++i) {
+        const int p = tid + i * kNT;
+        if (p < QP) *reinterpret_cast<u32x4*>(&sQ[sw<DK>(p / (DK / 8), (p % (DK / 8)) * 8)]) = q[i];
+      }
+    }
+    if (WANT_V) {
+#pragma unroll
+      for (int i = 0; i < VP_PT; ++i) {
+        const int p = tid + i * kNT;
+        if (p >= VP) continue;
+        const int t = p / (DVS / 8), c = (p % (DVS / 8)) * 8;
+        f32x4 lo, hi;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          lo[2 * e] = bf2f((uint16_t)(v[i][e] & 0xffffu));
+          lo[2 * e + 1] = bf2f((uint16_t)(v[i][e] >> 16));
+          hi[2 * e] = bf2f((uint16_t)(v[i][2 + e] & 0xffffu));
+          hi[2 * e + 1] = bf2f((uint16_t)(v[i][2 + e] >> 16));
+        }
+        *reinterpret_cast<f32x4*>(&sV[t * DVS + c]) = lo;
+        *reinterpret_cast<f32x4*>(&sV[t * DVS + c + 4]) = hi;
+      }
+    }
+    if (WS) {
+      u32x4* dst = reinterpret_cast<u32x4*>(smem + L::kTbH);  // TbH, TbL, Aq are contiguous
+#pragma unroll
+      for (int i = 0; i < WP_PT; ++i) {
+        const int p = tid + i * kNT;
+        if (p < WP) dst[p] = ws[i];
+      }
+    }
+    if (tid < kWave) {  // G = inclusive cumsum of g over the chunk (rows past cc carry the last value)
+      float gv = g;
+#pragma unroll
+      for (int off = 1; off < kWave; off <<= 1) {
+        const float o = __shfl_up(gv, off, kWave);
+        if (tid >= off) gv += o;
+      }
+      if (tid < C) {
+        sG[tid] = gv;
+        sBeta[tid] = beta;
       }
     }
   }
-  if (tid < kWave) {  // G = inclusive cumsum of g over the chunk (rows past cc carry the last value)
-    const int t = tid;
-    const int64_t gi = ((int64_t)b * a.T + t0 + t) * a.Hv + h;
-    float gv = (t < cc && t < C) ? a.g[gi] : 0.f;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const float o = __shfl_up(gv, off, kWave);
-      if (t >= off) gv += o;
-    }
-    if (t < C) {
-      sG[t] = gv;
-      sBeta[t] = t < cc ? a.beta[gi] : 0.f;
-    }
-  }
-}
+};
 
 // ---------------------------------------------------------------------------------------------- prep
 // From sK, sQ, sG, sBeta: T diag(beta) (hi / lo) into sTbH / sTbL and Aqk (hi) into sAq (when WANT_Q).
@@ -596,10 +671,8 @@ __device__ void mask_rows(unsigned char* smem, const f32x4 (&st)[StTiles<DK>::PE
 }
 
 // ---------------------------------------------------------------------------------------------- kernels
-// Workspace block of one (sequence, chunk, value head): T diag(beta) hi, lo and Aqk hi, 64 x 64 bf16 each.
-constexpr int kWsElems = 3 * kChunk * kChunk;
 
-template <int DK>
+template <int DK, bool OUT>
 __global__ __launch_bounds__(kNT) void gdr_chunk_prep_kernel(ChunkArgs a) {
   using L = Lay<DK, 4, 16>;
   __shared__ __align__(16) unsigned char smem[L::BYTES];
@@ -611,21 +684,19 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_prep_kernel(ChunkArgs a) {
   const int hk = h / (a.Hv / a.Hk);
   const int t0 = c * kChunk;
   const int cc = min(kChunk, a.T - t0);
-  if (a.out) {
-    stage_rows<DK, 4, 16, true, false, false>(smem, a, b, h, hk, 0, t0, cc);
-    __syncthreads();
-    prep_chunk<DK, 4, 16, true>(smem);
-  } else {
-    stage_rows<DK, 4, 16, false, false, false>(smem, a, b, h, hk, 0, t0, cc);
-    __syncthreads();
-    prep_chunk<DK, 4, 16, false>(smem);
+  {
+    Stage<DK, 4, 16, OUT, false, false> st;
+    st.load(a, b, h, hk, 0, t0, cc, c);
+    st.store(smem);
   }
+  __syncthreads();
+  prep_chunk<DK, 4, 16, OUT>(smem);
   u32x4* dst = reinterpret_cast<u32x4*>(a.ws + (((int64_t)b * a.nchunks + c) * a.Hv + h) * kWsElems);
   const u32x4* src = reinterpret_cast<const u32x4*>(smem + L::kTbH);  // TbH, TbL, Aq are contiguous
   for (int p = threadIdx.x; p < kWsElems / 8; p += kNT) dst[p] = src[p];
 }
 
-template <int DK, int DVS>
+template <int DK, int DVS, bool OUT>
 __global__ __launch_bounds__(kNT) void gdr_chunk_scan_kernel(ChunkArgs a) {
   using L = Lay<DK, 4, DVS>;
   __shared__ __align__(16) unsigned char smem[L::BYTES];
@@ -639,29 +710,29 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_scan_kernel(ChunkArgs a) {
   const int dv0 = sl * DVS;
   const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
   const int n_tot = a.n_keep ? min(max(a.n_keep[b % a.seq_mod], 0), a.T) : a.T;
+  // chunks to visit: all of them with a readout, else those holding absorbed rows
+  const int nch = OUT ? a.nchunks : (n_tot + kChunk - 1) / kChunk;
   f32x4 st[StTiles<DK>::PER][DVS / 16];
   const int64_t soff = (((int64_t)b * a.Hv + h) * a.Dv + dv0) * DK;
   load_state<DK, DVS>(st, a.state_in + soff, w, l);
   const int64_t v_row = (int64_t)a.Hv * a.Dv;
-  for (int c = 0; c < a.nchunks; ++c) {
+  Stage<DK, 4, DVS, OUT, true, true> nx;
+  if (nch > 0) nx.load(a, b, h, hk, dv0, 0, min(kChunk, a.T), 0);
+  for (int c = 0; c < nch; ++c) {
     const int t0 = c * kChunk;
     const int cc = min(kChunk, a.T - t0);
     const int n_abs = min(max(n_tot - t0, 0), cc);
-    if (!a.out && n_abs == 0) break;  // nothing more to absorb and nothing to read out
     __syncthreads();  // the previous chunk's LDS reads are done
-    if (a.out) stage_rows<DK, 4, DVS, true, true, true>(smem, a, b, h, hk, dv0, t0, cc);
-    else stage_rows<DK, 4, DVS, false, true, true>(smem, a, b, h, hk, dv0, t0, cc);
-    const u32x4* src = reinterpret_cast<const u32x4*>(a.ws + (((int64_t)b * a.nchunks + c) * a.Hv + h) * kWsElems);
-    u32x4* dst = reinterpret_cast<u32x4*>(smem + L::kTbH);
-    for (int p = threadIdx.x; p < kWsElems / 8; p += kNT) dst[p] = src[p];
+    nx.store(smem);
     __syncthreads();
-    uint16_t* orow = a.out ? a.out + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
+    if (c + 1 < nch) nx.load(a, b, h, hk, dv0, t0 + kChunk, min(kChunk, a.T - t0 - kChunk), c + 1);
+    uint16_t* orow = OUT ? a.out + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
     scan_chunk<DK, 4, DVS>(smem, st, cc, n_abs, cc, orow, v_row, a.scale);
   }
   if (a.state_out) store_state<DK, DVS>(st, a.state_out + soff, w, l);
 }
 
-template <int DK, int NB, int DVS>
+template <int DK, int NB, int DVS, bool OUT>
 __global__ __launch_bounds__(kNT) void gdr_chunk_fused_kernel(ChunkArgs a) {
   using L = Lay<DK, NB, DVS>;
   __shared__ __align__(16) unsigned char smem[L::BYTES];
@@ -676,24 +747,33 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_fused_kernel(ChunkArgs a) {
   const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
   const int cc = a.T;
   const int n_abs = a.n_keep ? min(max(a.n_keep[b % a.seq_mod], 0), cc) : cc;
-  if (a.out) {
-    stage_rows<DK, NB, DVS, true, true, true>(smem, a, b, h, hk, dv0, 0, cc);
-    __syncthreads();
-    prep_chunk<DK, NB, DVS, true>(smem);
-  } else {
-    stage_rows<DK, NB, DVS, false, true, true>(smem, a, b, h, hk, dv0, 0, cc);
-    __syncthreads();
-    prep_chunk<DK, NB, DVS, false>(smem);
-  }
   f32x4 st[StTiles<DK>::PER][DVS / 16];
   const int64_t soff = (((int64_t)b * a.Hv + h) * a.Dv + dv0) * DK;
-  load_state<DK, DVS>(st, a.state_in + soff, w, l);
+  {
+    Stage<DK, NB, DVS, OUT, true, false> sg;
+    sg.load(a, b, h, hk, dv0, 0, cc, 0);
+    load_state<DK, DVS>(st, a.state_in + soff, w, l);
+    sg.store(smem);
+  }
+  __syncthreads();
+  prep_chunk<DK, NB, DVS, OUT>(smem);
   const int64_t v_row = (int64_t)a.Hv * a.Dv;
-  uint16_t* orow = a.out ? a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
+  uint16_t* orow = OUT ? a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
   const int n_out = min(a.nc, cc);
   scan_chunk<DK, NB, DVS>(smem, st, cc, n_abs, n_out, orow, v_row, a.scale);
-  if (a.out && n_out < cc) mask_rows<DK, NB, DVS>(smem, st, n_out, cc, orow, v_row, a.scale);
+  if (OUT && n_out < cc) mask_rows<DK, NB, DVS>(smem, st, n_out, cc, orow, v_row, a.scale);
   if (a.state_out) store_state<DK, DVS>(st, a.state_out + soff, w, l);
+}
+
+template <int DK, int NB, int DVS>
+void launch_fused(const ChunkArgs& a, unsigned grid, hipStream_t stream) {
+  if (a.out) hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, NB, DVS, true>), dim3(grid), dim3(kNT), 0, stream, a);
+  else hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, NB, DVS, false>), dim3(grid), dim3(kNT), 0, stream, a);
+}
+template <int DK, int DVS>
+void launch_scan(const ChunkArgs& a, unsigned grid, hipStream_t stream) {
+  if (a.out) hipLaunchKernelGGL((gdr_chunk_scan_kernel<DK, DVS, true>), dim3(grid), dim3(kNT), 0, stream, a);
+  else hipLaunchKernelGGL((gdr_chunk_scan_kernel<DK, DVS, false>), dim3(grid), dim3(kNT), 0, stream, a);
 }
 
 template <int DK>
@@ -706,18 +786,19 @@ int launch_dk(ChunkArgs& a, int B, hipStream_t stream) {
   if (fused) {
     const bool nb2 = a.T <= 32;
     if (dvs == 32) {
-      if (nb2) hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 2, 32>), dim3(grid), dim3(kNT), 0, stream, a);
-      else hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 4, 32>), dim3(grid), dim3(kNT), 0, stream, a);
+      if (nb2) launch_fused<DK, 2, 32>(a, grid, stream);
+      else launch_fused<DK, 4, 32>(a, grid, stream);
     } else {
-      if (nb2) hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 2, 16>), dim3(grid), dim3(kNT), 0, stream, a);
-      else hipLaunchKernelGGL((gdr_chunk_fused_kernel<DK, 4, 16>), dim3(grid), dim3(kNT), 0, stream, a);
+      if (nb2) launch_fused<DK, 2, 16>(a, grid, stream);
+      else launch_fused<DK, 4, 16>(a, grid, stream);
     }
     return launch_status("gdr_chunk (single chunk)");
   }
   const unsigned pgrid = (unsigned)((int64_t)B * a.nchunks * a.Hv);
-  hipLaunchKernelGGL((gdr_chunk_prep_kernel<DK>), dim3(pgrid), dim3(kNT), 0, stream, a);
-  if (dvs == 32) hipLaunchKernelGGL((gdr_chunk_scan_kernel<DK, 32>), dim3(grid), dim3(kNT), 0, stream, a);
-  else hipLaunchKernelGGL((gdr_chunk_scan_kernel<DK, 16>), dim3(grid), dim3(kNT), 0, stream, a);
+  if (a.out) hipLaunchKernelGGL((gdr_chunk_prep_kernel<DK, true>), dim3(pgrid), dim3(kNT), 0, stream, a);
+  else hipLaunchKernelGGL((gdr_chunk_prep_kernel<DK, false>), dim3(pgrid), dim3(kNT), 0, stream, a);
+  if (dvs == 32) launch_scan<DK, 32>(a, grid, stream);
+  else launch_scan<DK, 16>(a, grid, stream);
   return launch_status("gdr_chunk (prep + scan)");
 }
 
