@@ -118,6 +118,20 @@ int trida_truncated_probs(const float* logits, int64_t B, int64_t R, int64_t V, 
                           const double* zk, float* probs, int64_t out_batch_stride, int64_t out_row_stride,
                           void* stream);
 
+/* Draws one token per row from the truncated distribution of statistics (m, thr, zk) given by
+ * trida_truncate_stats: the inverse CDF in vocabulary order of P(x) = [y_x >= thr] exp(y_x - m) / zk at
+ * u[r] (token = min{x : cdf(x) > u * total}), the draw the sampled acceptance makes for its bonus token.
+ * It is the proposal draw of the draft pass (sample_from_probs(truncated_probs(...)),
+ * inference/zoro-1/mlx/trida_mlx/decode.py:133-134, 374-378; _ss_draft_gumbel_kernel,
+ * inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:250-285), with the row statistics
+ * computed once and shared with the q rows. logits [rows, V] fp32 (row stride in elements), m, thr,
+ * zk, u [rows]; token [rows] int64. rows <= 65535. scratch: trida_sample_rows_scratch_bytes(rows, V)
+ * bytes, 256-byte aligned, no initialisation. */
+int64_t trida_sample_rows_scratch_bytes(int64_t rows, int64_t V);
+int trida_sample_rows(const float* logits, int64_t rows, int64_t V, int64_t row_stride, float temperature,
+                      int64_t ban_id, const float* m, const float* thr, const double* zk, const float* u,
+                      int64_t* token, void* scratch, int64_t scratch_bytes, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * GDN layer front half: depthwise causal conv (width Kc in 2..4) over [window ++ x] + SiLU, split into
  * q / k / v, per-head l2norm of q and k (eps 1e-6), gates g = -exp(A_log) * softplus(a + dt_bias) and

@@ -280,8 +280,8 @@ def blockspec_generate(m: CpuHybrid, prompt: List[int], max_new: int, block: int
 def blockspec_sample_step(m: CpuHybrid, cache: CpuCache, t0: int, block: int, denoise: int, *, temperature: float,
                           top_k: int, top_p: float, rng):
     """One sampled draft-then-verify step (the rejection-sampling counterpart of blockspec_step):
-    `denoise` passes over [t0, MASK x block]; in each, every slot's candidate is drawn by inverse CDF
-    from its truncated distribution P_j (decode.py:102-130; MASK banned, qwen3_5_diffusion.py:820) and
+    `denoise` passes over [t0, MASK x block]; in each, every still-masked slot's candidate is drawn by
+    inverse CDF from its truncated distribution P_j (decode.py:102-130; MASK banned, qwen3_5_diffusion.py:820) and
     the per-pass quota of MASK slots with the most probable draws (P_j(x_j), ties to the lower slot)
     is unmasked, keeping P_j as the slot's q row (the draft distribution, qwen3_5_diffusion.py:779).
     Then a token-causal verify pass, rejection-sampling acceptance (oracle.accept.rejection_accept,
@@ -300,14 +300,16 @@ def blockspec_sample_step(m: CpuHybrid, cache: CpuCache, t0: int, block: int, de
     for p in range(denoise):
         L = m.forward(canvas, cache, "draft")
         cache.pending = None
-        P = A.truncated_probs(L[:block].numpy(), temperature, top_k, top_p, mask)
-        u = rng.random(block)
-        x = [A.sample_inverse_cdf(P[j], float(u[j]))[0] for j in range(block)]
-        cand = sorted((j for j in range(block) if masked[j]), key=lambda j: (-P[j, x[j]], j))
+        live = [j for j in range(block) if masked[j]]
+        P = A.truncated_probs(L[live].numpy(), temperature, top_k, top_p, mask)
+        u = rng.random(len(live))
+        x = {j: A.sample_inverse_cdf(P[i], float(u[i]))[0] for i, j in enumerate(live)}
+        prob = {j: P[i, x[j]] for i, j in enumerate(live)}
+        cand = sorted(live, key=lambda j: (-prob[j], j))
         for j in cand[: per[p]]:
             canvas[1 + j] = x[j]
             masked[j] = False
-            q[j] = P[j]
+            q[j] = P[live.index(j)]
     L = m.forward(canvas, cache, "verify")
     res = A.rejection_accept(L[None].numpy(), q[None], np.asarray([canvas[1:]], np.int64), rng.random((1, block)),
                              rng.random(1), temperature=temperature, top_k=top_k, top_p=top_p, mask_id=mask)

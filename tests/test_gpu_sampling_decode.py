@@ -37,30 +37,34 @@ def collect(gen):
 
 
 def check_step_trace(trace, block, per, T, k, p, mask):
-    """Replays one SampledBlockSpecStep on the oracle from the tensors the GPU step used."""
+    """Replays one SampledBlockSpecStep on the oracle from the tensors the GPU step used: the draws of
+    the still-masked slots, the choice of the slots to unmask, their q rows and the acceptance."""
     passes, ver = trace[:-1], trace[-1]
-    B = passes[0]["lf"].shape[0]
-    q_ref = np.zeros((B, block, passes[0]["lf"].shape[2]))
+    B, _, V = passes[0]["lf"].shape
+    q_ref = np.zeros((B, block, V))
     skipped = 0
     for pi, tr in enumerate(passes):
         lf, u, x = tr["lf"].cpu().numpy(), tr["u"].cpu().numpy(), tr["x"].cpu().numpy()
-        masked, pos = tr["masked"].cpu().numpy(), tr["pos"].cpu().numpy()
+        midx, slots = tr["midx"].cpu().numpy(), tr["slots"].cpu().numpy()
+        n = lf.shape[1]
         P, info = A.truncated_probs(lf, T, k, p, mask, return_info=True)
         for b in range(B):
-            for j in range(block):
-                tok, gap = A.sample_inverse_cdf(P[b, j], float(u[b * block + j]))
-                if gap > 1e-6 and info.boundary_gap[b, j] > 1e-6:
-                    assert x[b, j] == tok, (pi, b, j)
+            assert (np.diff(midx[b]) > 0).all()  # the masked slots, ascending
+            for i in range(n):
+                tok, gap = A.sample_inverse_cdf(P[b, i], float(u[b * n + i]))
+                if gap > 1e-6 and info.boundary_gap[b, i] > 1e-6:
+                    assert x[b, i] == tok, (pi, b, i)
                 else:
                     skipped += 1
-            conf = np.array([P[b, j, x[b, j]] for j in range(block)])
-            cand = sorted((j for j in range(block) if masked[b, j]), key=lambda j: (-conf[j], j))
-            chosen = cand[: per[pi]]
-            border = [conf[j] for j in cand[per[pi] - 1: per[pi] + 1]]
+            conf = np.array([P[b, i, x[b, i]] for i in range(n)])
+            order = sorted(range(n), key=lambda i: (-conf[i], midx[b, i]))
+            chosen = [int(midx[b, i]) for i in order[: per[pi]]]
+            border = [conf[i] for i in order[per[pi] - 1: per[pi] + 1]]
             if len(border) < 2 or abs(border[0] - border[1]) > 1e-6:
-                assert sorted(pos[b].tolist()) == sorted(chosen), (pi, b)
-            for j in pos[b].tolist():
-                q_ref[b, j] = P[b, j]
+                assert sorted(slots[b].tolist()) == sorted(chosen), (pi, b)
+            for i in range(n):
+                if midx[b, i] in slots[b]:
+                    q_ref[b, midx[b, i]] = P[b, i]
     q = ver["q"].cpu().numpy()
     assert np.abs(q - q_ref).max() < 2e-6
     res = A.rejection_accept(ver["pf"].cpu().numpy(), q, ver["drafts"].cpu().numpy(), ver["ua"].cpu().numpy(),
@@ -90,6 +94,26 @@ def test_sampled_blockspec_step_vs_oracle(gpu, T, k, p):
         assert torch.equal(cache.length.cpu(), (length_before + 1 + step.n_acc).cpu())
         assert (tok != rt.mask_id).all()
     smp.check()
+
+
+def test_sample_rows_vs_oracle(gpu):
+    """Draws from given truncation statistics: the inverse CDF at each row's uniform (near-ties skipped)."""
+    from trida_stack_amd import kernels as TK
+
+    rng = np.random.default_rng(3)
+    for T, k, p in [(0.7, 0, 0.95), (1.0, 20, 0.9), (1.3, 0, 1.0)]:
+        lf = (rng.normal(size=(3, 7, 5000)) * 3).astype(np.float32)
+        u = rng.random(21).astype(np.float32)
+        x = torch.from_numpy(lf).to(DEV)
+        st = TK.truncate_stats(x, temperature=T, top_k=k, top_p=p, ban_id=11)
+        tok = TK.sample_rows(x, st, torch.from_numpy(u).to(DEV), temperature=T, ban_id=11).cpu().numpy()
+        P, info = A.truncated_probs(lf, T, k, p, 11, return_info=True)
+        for r in range(21):
+            b, i = divmod(r, 7)
+            ref, gap = A.sample_inverse_cdf(P[b, i], float(u[r]))
+            if gap > 1e-6 and info.boundary_gap[b, i] > 1e-6:
+                assert tok[b, i] == ref, (T, k, p, r)
+            assert tok[b, i] != 11 and P[b, i, tok[b, i]] > 0
 
 
 def test_sampled_generate_runs(gpu):

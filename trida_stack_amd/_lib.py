@@ -35,6 +35,8 @@ SIGNATURES = {
     "trida_sample_accept": (C.c_int, [P, I64, I64, I64, I64, I64, P, I64, I64, P, I64, I64, P, P, I64, P, P,
                                       F32, I64, F32, I64, P, P, P, P, P, P, I64, P]),
     "trida_truncate_stats": (C.c_int, [P, I64, I64, I64, I64, I64, F32, I64, F32, I64, C.c_int, P, P, P, P, P, P]),
+    "trida_sample_rows_scratch_bytes": (I64, [I64, I64]),
+    "trida_sample_rows": (C.c_int, [P, I64, I64, I64, F32, I64, P, P, P, P, P, P, I64, P]),
     "trida_truncated_probs": (C.c_int, [P, I64, I64, I64, I64, I64, F32, I64, P, P, P, P, I64, I64, P]),
     "trida_skinny_gemm_scratch_bytes": (I64, [I64, I64, I64, I64]),
     "trida_skinny_gemm": (C.c_int, [P, I64, P, I64, P, I64, I64, I64, I64, P, I64, I64, P]),

@@ -1321,3 +1321,61 @@ extern "C" int trida_truncated_probs(const float* logits, int64_t B, int64_t R, 
                      (int)V, 1.0 / (double)temperature, ban_of(ban_id, V), m, thr, zk, probs, out_batch_stride, out_row_stride);
   return launch_status("probs_kernel");
 }
+
+// ---------------------------------------------------------------- draws from given truncation statistics
+// The residual kernels with no drafts: per row, the inverse CDF in vocabulary order of
+// P(x) = [y_x >= thr] exp(y_x - m) / zk at one uniform. Scratch: the per-row bookkeeping those kernels
+// read and write, then the chunk sums.
+namespace trida {
+namespace {
+struct DrawScratch {
+  int64_t state, rstatus, status, n_acc, crop, sums, total;
+};
+DrawScratch draw_layout(int64_t rows, int64_t V) {
+  int NC, chunk;
+  plan_chunks(rows, V, &NC, &chunk);
+  DrawScratch L;
+  L.state = 0;
+  L.rstatus = L.state + align_up(rows * 4, 256);
+  L.status = L.rstatus + align_up(rows * 4, 256);
+  L.n_acc = L.status + align_up(rows * 4, 256);
+  L.crop = L.n_acc + align_up(rows * 4, 256);
+  L.sums = L.crop + align_up(rows * 8, 256);
+  L.total = L.sums + align_up(rows * NC * 2 * 8, 256);
+  return L;
+}
+}  // namespace
+}  // namespace trida
+
+extern "C" int64_t trida_sample_rows_scratch_bytes(int64_t rows, int64_t V) {
+  if (rows <= 0 || V <= 0) return 0;
+  return draw_layout(rows, V).total;
+}
+
+extern "C" int trida_sample_rows(const float* logits, int64_t rows, int64_t V, int64_t row_stride, float temperature,
+                                 int64_t ban_id, const float* m, const float* thr, const double* zk, const float* u,
+                                 int64_t* token, void* scratch, int64_t scratch_bytes, void* stream) {
+  TRIDA_CHECK(logits && m && thr && zk && u && token && scratch, TRIDA_ERR_NULL, "null pointer argument");
+  TRIDA_CHECK(rows > 0 && rows <= 65535 && V > 0 && V < INT_MAX / 2, TRIDA_ERR_ARG, "bad shape rows=%lld V=%lld",
+              (long long)rows, (long long)V);
+  TRIDA_CHECK(temperature > 0.f && temperature < INFINITY, TRIDA_ERR_ARG, "temperature must be positive");
+  TRIDA_CHECK(row_stride >= V, TRIDA_ERR_ARG, "row_stride too small");
+  const DrawScratch L = draw_layout(rows, V);
+  TRIDA_CHECK(scratch_bytes >= L.total, TRIDA_ERR_WORKSPACE, "scratch of %lld bytes, need %lld",
+              (long long)scratch_bytes, (long long)L.total);
+  TRIDA_CHECK((uintptr_t)scratch % 256 == 0, TRIDA_ERR_ALIGN, "scratch must be 256-byte aligned");
+  char* s = static_cast<char*>(scratch);
+  int NC, chunk;
+  plan_chunks(rows, V, &NC, &chunk);
+  AcceptArgs aa{logits, row_stride, 0, nullptr, 0, 0, nullptr, 0, nullptr, nullptr, 0, u, nullptr, (int)rows, (int)V, 0,
+                1.0 / (double)temperature, ban_of(ban_id, V), m, thr, zk, nullptr,
+                reinterpret_cast<int*>(s + L.state), reinterpret_cast<int*>(s + L.rstatus), NC, chunk,
+                reinterpret_cast<double*>(s + L.sums), reinterpret_cast<int32_t*>(s + L.n_acc), token,
+                reinterpret_cast<int64_t*>(s + L.crop), nullptr, reinterpret_cast<int32_t*>(s + L.status)};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(resid_sums_kernel, dim3(NC, rows), dim3(kRT), 0, st, aa);
+  const int r = launch_status("resid_sums_kernel (draw)");
+  if (r != TRIDA_OK) return r;
+  hipLaunchKernelGGL(resid_pick_kernel, dim3(rows), dim3(kRT), 0, st, aa);
+  return launch_status("resid_pick_kernel (draw)");
+}

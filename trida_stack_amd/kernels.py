@@ -211,6 +211,33 @@ def truncated_probs(logits: torch.Tensor, stats, *, temperature: float, ban_id: 
     return out
 
 
+def sample_rows(logits: torch.Tensor, stats, u: torch.Tensor, *, temperature: float, ban_id: int = -1,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One token per row of logits [..., V] fp32 (contiguous rows) from the truncated distribution of
+    ``truncate_stats`` output (inverse CDF in vocabulary order at u, one uniform per row)."""
+    dev = _need_gpu(logits, u, out)
+    V = logits.shape[-1]
+    x = logits.reshape(-1, V)
+    if x.dtype != torch.float32 or x.stride(1) != 1:
+        raise ValueError("logits must be fp32 with contiguous rows")
+    rows = x.shape[0]
+    m, thr, zk = (t.reshape(-1) for t in stats[:3])
+    for t, dt in ((m, torch.float32), (thr, torch.float32), (zk, torch.float64)):
+        if t.dtype != dt or t.numel() != rows or not t.is_contiguous():
+            raise ValueError("stats must be the (m, thr, zk) tensors of truncate_stats for these rows")
+    if u.dtype != torch.float32 or u.numel() != rows or not u.is_contiguous():
+        raise ValueError("u must be fp32 with one uniform per row")
+    if out is None:
+        out = torch.empty(logits.shape[:-1], dtype=torch.int64, device=dev)
+    lib = _lib.load()
+    scr = workspaces.get(dev, "draw", lib.trida_sample_rows_scratch_bytes(rows, V))
+    rc = lib.trida_sample_rows(x.data_ptr(), rows, V, x.stride(0), float(temperature), int(ban_id), m.data_ptr(),
+                               thr.data_ptr(), zk.data_ptr(), u.data_ptr(), out.data_ptr(), scr.data_ptr(), scr.numel(),
+                               _stream(dev))
+    _lib.check(rc, "trida_sample_rows")
+    return out
+
+
 def sample_accept(p_logits: torch.Tensor, q_probs: Optional[torch.Tensor], drafts: torch.Tensor,
                   u_accept: Optional[torch.Tensor], u_sample: torch.Tensor, *, temperature: float,
                   top_k: int = 0, top_p: float = 1.0, ban_id: int = -1, n_live: Optional[torch.Tensor] = None,

@@ -13,8 +13,8 @@ full-vocabulary fp32 distributions kept per draft slot (qwen3_5_diffusion.py:779
 
 Token draws. The reference draws with an RNG (mx.random.categorical / Gumbel noise) that has no
 uniform -> token contract. Here every draw is the inverse CDF in vocabulary order at one seeded uniform,
-token = min{x : cdf(x) > u * mass}, computed on the GPU by the sampled-acceptance kernel (a verify
-with no drafts draws from P_0). The MASK id is banned from every sampled row, drafts and verify alike
+token = min{x : cdf(x) > u * mass}, computed on the GPU by the sampled-acceptance kernels (a verify
+with no drafts draws from P_0; the draft passes draw from row statistics computed once, trida_sample_rows). The MASK id is banned from every sampled row, drafts and verify alike
 (qwen3_5_diffusion.py:820), so the AR baseline and self-spec share one target distribution.
 """
 from __future__ import annotations
@@ -70,6 +70,11 @@ class Sampler:
                                            top_k=self.top_k, top_p=self.top_p, ban_id=self.ban)
         self._note(st)
         return tok.view(logits.shape[:-1])
+
+    def draw_given(self, lf: torch.Tensor, stats, u: torch.Tensor) -> torch.Tensor:
+        """One token per row of fp32 logits [B, R, V] from their truncated distributions, given the
+        statistics of `stats` (no second truncation pass)."""
+        return K.sample_rows(lf, stats, u, temperature=self.T, ban_id=self.ban)
 
     def stats(self, lf: torch.Tensor):
         m, thr, zk, st = K.truncate_stats(lf, temperature=self.T, top_k=self.top_k, top_p=self.top_p,
@@ -188,10 +193,10 @@ def selfspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *,
 class SampledBlockSpecStep:
     """One batched draft-then-verify step with speculative rejection sampling, on device buffers of fixed
     shape: `denoise` block-diffusion passes over [t0, MASK x block] (each draws a candidate for every
-    slot from its truncated distribution and unmasks the slots whose draw is most probable, keeping that
-    slot's distribution as its q row), a token-causal verify pass, rejection-sampling acceptance (the
-    correction, or the bonus when every draft is accepted, becomes the next t0) and the hybrid rollback
-    to 1 + n_acc rows per sequence (ragged KV crops and GDN restores).
+    still-masked slot from its truncated distribution and unmasks the slots whose draw is most probable,
+    keeping that slot's distribution as its q row), a token-causal verify pass, rejection-sampling
+    acceptance (the correction, or the bonus when every draft is accepted, becomes the next t0) and the
+    hybrid rollback to 1 + n_acc rows per sequence (ragged KV crops and GDN restores).
 
     Inputs: t0 [B] int64. Outputs after run(): canvas [B, block+1] (row 0 = t0, rows 1.. = drafts),
     n_acc [B] int32, token [B] int64 (next t0). q rows: [B, block, V] fp32 (the reference layout).
@@ -209,11 +214,10 @@ class SampledBlockSpecStep:
         self.n_keep = torch.zeros(B, dtype=torch.int32, device=dev)
         self.out = (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
                     torch.empty(B, dtype=torch.int64, device=dev), None, torch.empty(B, dtype=torch.int32, device=dev))
-        self.lf = torch.empty(B, block, V, dtype=torch.float32, device=dev)      # draft rows 0..block-1
-        self.pt = torch.empty(B, block, V, dtype=torch.float32, device=dev)      # their truncated P
+        self.lf = torch.empty(B * block * V, dtype=torch.float32, device=dev)   # masked draft rows, fp32
+        self.pt = torch.empty(B * max(self.per) * V, dtype=torch.float32, device=dev)  # unmasked slots' P
         self.q = torch.zeros(B, block, V, dtype=torch.float32, device=dev)       # q row per draft slot
         self.pf = torch.empty(B, block + 1, V, dtype=torch.float32, device=dev)  # verify rows
-        self.neg = torch.full((B, block), float("-inf"), dtype=torch.float32, device=dev)
         self.trace: Optional[list] = None
 
     @property
@@ -230,27 +234,33 @@ class SampledBlockSpecStep:
         self.canvas.fill_(rt.mask_id)
         self.canvas[:, 0] = self.t0
         self.masked.fill_(True)
+        left = blk
         for p in range(self.denoise):
             L = rt.forward(self.canvas, cache, "draft")
-            # row j predicts slot j + 1 (shift readout); the last row is not used
-            self.lf.copy_(L[:, :blk])
+            # the still-masked slots in ascending order (every sequence has `left` of them); row s of the
+            # draft logits predicts slot s (shift readout)
+            midx = torch.sort(self.masked.to(torch.int8), dim=1, descending=True, stable=True).indices[:, :left]
+            lf = self.lf[: B * left * V].view(B, left, V)
             with K.timed("draft_sample"):
-                st = smp.stats(self.lf)
-                u = smp.uniform(B * blk)
-                x = smp.draw(self.lf, u)                                 # [B, blk]
-                conf = smp.prob_of(self.lf, st, x)
-            score = torch.where(self.masked, conf, self.neg)
-            # the per[p] most probable MASK-slot draws (ties: the lower slot first)
-            pos = torch.sort(score, dim=1, descending=True, stable=True).indices[:, : self.per[p]]
+                lf.copy_(L.gather(1, midx[:, :, None].expand(B, left, V)))
+                st = smp.stats(lf)
+                u = smp.uniform(B * left)
+                x = smp.draw_given(lf, st, u)                            # [B, left]
+                conf = smp.prob_of(lf, st, x)
+            # the per[p] most probable draws (ties: the lower slot first)
+            k = self.per[p]
+            sel = torch.sort(conf, dim=1, descending=True, stable=True).indices[:, :k]
+            slots = midx.gather(1, sel)
             if self.trace is not None:
-                self.trace.append({"lf": self.lf.clone(), "u": u.clone(), "x": x.clone(),
-                                   "masked": self.masked.clone(), "pos": pos.clone()})
-            self.canvas.scatter_(1, pos + 1, x.gather(1, pos))
-            self.masked.scatter_(1, pos, False)
+                self.trace.append({"lf": lf.clone(), "u": u.clone(), "x": x.clone(), "midx": midx.clone(),
+                                   "slots": slots.clone()})
+            self.canvas.scatter_(1, slots + 1, x.gather(1, sel))
+            self.masked.scatter_(1, slots, False)
             with K.timed("draft_q"):
-                smp.probs(self.lf, st, out=self.pt)
-                idx = pos[:, :, None].expand(-1, -1, V)
-                self.q.scatter_(1, idx, self.pt.gather(1, idx))
+                lq = lf.gather(1, sel[:, :, None].expand(B, k, V))
+                P = smp.probs(lq, tuple(t.gather(1, sel) for t in st), out=self.pt[: B * k * V].view(B, k, V))
+                self.q.scatter_(1, slots[:, :, None].expand(B, k, V), P)
+            left -= k
         vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
         self.pf.copy_(L)
