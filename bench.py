@@ -310,11 +310,15 @@ def bench_e2e(args):
         step.run()
         cache.ctx_hint += int(step.n_acc[0]) - BLOCK
     torch.cuda.synchronize()
-    K.TIMERS, K.TIMER_ONLY = ({}, {"forward", "verify_step"}) if not args.no_events else (None, None)
+    graph = not args.no_graph
+    if graph:
+        step.capture()  # the whole step as one HIP graph (the decode loop's default)
+    fwd_us = _forward_event_us(rt, cache, step, args) if graph else None
+    K.TIMERS, K.TIMER_ONLY = ({}, {"forward", "verify_step"}) if not (args.no_events or graph) else (None, None)
     acc_tokens, hist = 0, [0] * (BLOCK + 1)
     t = time.perf_counter()
     for _ in range(args.steps):
-        step.run()
+        step.replay() if graph else step.run()
         n = int(step.n_acc[0])  # the host reads the accepted length each step to emit tokens
         cache.ctx_hint += n - BLOCK  # commit counted the whole block; keep the exact length
         acc_tokens += 1 + n
@@ -322,6 +326,9 @@ def bench_e2e(args):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t
     timers = K.timer_means_us(K.TIMERS) if K.TIMERS is not None else {}
+    if fwd_us is not None:
+        timers["forward"] = fwd_us
+    K.TIMERS = None
     kern = _kernel_breakdown(step, cache, BLOCK, args)
     ctx = int(cache.length[0])
 
@@ -350,13 +357,42 @@ def bench_e2e(args):
                    "batch": 1, "prompt_len": PROMPT_LEN, "block": BLOCK, "denoise_passes": DENOISE,
                    "generated_tokens": acc_tokens, "tokens_per_step": round(acc_tokens / args.steps, 3),
                    "accept_hist": hist, "params": cfg.n_params()},
-        "verify_step_us": round(timers["verify_step"], 1) if "verify_step" in timers else None,
+        "verify_step_us": round(timers.get("verify_step", kern.get("verify_step", 0.0)), 1) or None,
+        "hip_graph": graph,
         "prefill_s": round(prefill_s, 3),
         "kernel_avg_us": kern,
         "roofline": roof,
         "cpu_baseline": cpu,
         "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
     }
+
+
+def _forward_event_us(rt, cache, step, args, reps: int = 5) -> float:
+    """Average duration of one verify forward replayed from its own HIP graph (HIP events on the
+    capture stream around the replays), on the live cache: the decoder forward with no launch gaps.
+    The forwards only read the cache (a verify pass persists nothing)."""
+    import torch
+
+    ids = step.canvas.clone()
+    fwd = lambda: rt.forward(ids, cache, "verify")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fwd()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fwd()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
 
 
 def _kernel_breakdown(step, cache, block, args, steps: int = 4) -> dict:
@@ -638,6 +674,7 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-events", action="store_true", help="skip the live per-kernel event timers")
+    ap.add_argument("--no-graph", action="store_true", help="e2e: launch the step eagerly instead of from a HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (the step shards by "

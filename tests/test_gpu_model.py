@@ -252,3 +252,34 @@ def test_engine_modes_agree(gpu, pair):
         assert eng.last_stats["new_tokens"] == 40
     rt.gdr_form = old_form
     assert outs[0] == outs[1] == outs[2]
+
+
+def test_block_step_graph_replay_matches_eager(gpu, pair):
+    """A whole draft-then-verify step captured in a HIP graph and replayed: every replay (with eager
+    work between replays) gives the eager step's drafts, accepted length, bonus and cache lengths."""
+    from trida_stack_amd.decode import BlockSpecStep
+
+    rt, _ = pair
+    p = prompt(23, seed=31)
+
+    def fresh():
+        c = rt.make_cache(max_len=256)
+        lg = rt.prefill(c, p)
+        c.ctx_hint = c.Lmax  # the graph plans attention splits for the capacity; the eager run does too
+        st = BlockSpecStep(rt, c, block=8, denoise=2)
+        st.t0.fill_(int(lg.argmax()))
+        return c, st
+
+    c1, s1 = fresh()
+    ref = []
+    for _ in range(4):
+        s1.run()
+        ref.append((s1.canvas.cpu().clone(), int(s1.n_acc[0]), int(s1.bonus[0]), int(c1.length[0])))
+    c2, s2 = fresh()
+    s2.capture()
+    assert int(c2.length[0]) == len(p), "capture must leave the cache as it was"
+    for i in range(4):
+        s2.replay()
+        torch.matmul(torch.randn(64, 64, device=DEV), torch.randn(64, 64, device=DEV))  # eager work between
+        got = (s2.canvas.cpu().clone(), int(s2.n_acc[0]), int(s2.bonus[0]), int(c2.length[0]))
+        assert torch.equal(got[0], ref[i][0]) and got[1:] == ref[i][1:], i

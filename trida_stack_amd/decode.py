@@ -258,9 +258,41 @@ class BlockSpecStep:
         vt.__exit__(None, None, None)
         self.t0.copy_(self.bonus)
 
+    # ---------------------------------------------------------------- HIP-graph replay
+    graph = None
+
+    def capture(self) -> None:
+        """Records one whole step (every kernel of the denoise and verify forwards, the acceptance and the
+        rollback) into a HIP graph; replay() then launches it with one call. The step reads lengths and
+        positions on the device, so one graph serves every step; the attention key splits are planned for
+        the cache capacity (splits past a sequence's keys exit at once). The warm-up runs that precede the
+        capture are undone (cache state, lengths and t0 restored), so the cache is left as it was."""
+        rt, cache = self.rt, self.cache
+        cache.ctx_hint = max(cache.ctx_hint, cache.Lmax)
+        snap, t0 = cache.snapshot(), self.t0.clone()
+        side = torch.cuda.Stream(rt.dev)
+        side.wait_stream(torch.cuda.current_stream(rt.dev))
+        with torch.cuda.stream(side):
+            for _ in range(2):  # workspaces, allocator pools and library handles exist before capture
+                self.run()
+                cache.restore(snap)
+                self.t0.copy_(t0)
+        torch.cuda.current_stream(rt.dev).wait_stream(side)
+        torch.cuda.synchronize(rt.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.run()
+        torch.cuda.synchronize(rt.dev)
+        self.graph = g
+
+    def replay(self) -> None:
+        """One step from the captured graph (capture() first)."""
+        self.graph.replay()
+
 
 def _blockspec(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
-               mask_id: int, block: int, denoise: int, stats: Optional[DecodeStats]) -> Iterator[list]:
+               mask_id: int, block: int, denoise: int, stats: Optional[DecodeStats],
+               graph: bool = True) -> Iterator[list]:
     stats = stats or DecodeStats()
     stats.mode = f"self-spec(block={block}, denoise={denoise})"
     stats.accept_hist = [0] * (block + 1)
@@ -273,8 +305,14 @@ def _blockspec(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_token
     if out:
         yield out
     step.t0.fill_(t0)
+    use_graph = graph and rt.dev.type == "cuda"
     while not emit.done:
-        step.run()
+        if use_graph and step.graph is None and stats.steps >= 1:
+            step.capture()
+        if step.graph is not None:
+            step.replay()
+        else:
+            step.run()
         stats.forwards += denoise + 1
         stats.steps += 1
         packed = torch.cat([step.canvas[0, 1:], step.bonus[:1], step.n_acc[:1].to(torch.int64)]).tolist()

@@ -42,11 +42,15 @@ class _Workspaces:
 
     def __init__(self):
         self._bufs = {}
+        # buffers replaced by larger ones stay alive: a captured HIP graph may still launch kernels on them
+        self._retired = []
 
     def get(self, dev: torch.device, name: str, nbytes: int) -> torch.Tensor:
         key = (dev.index, name)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._retired.append(buf)
             buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=dev)
             self._bufs[key] = buf
         return buf
