@@ -169,6 +169,16 @@ int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         float* state_clean, int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk,
                         int64_t Dv, int causal_mode, int64_t num_clean, float scale, void* stream);
 
+/* Block-bidirectional gated delta rule: the training research path _block_bidirectional_gdr
+ *   (train/models/hybrid.py:461-536) for blocks of block_size consecutive rows (the last block may be
+ *   shorter). Per block with causal entry state E: out_f = the causal readout (forward sub-scan from E),
+ *   out_b = the readout of a sub-scan over the block's rows in reverse order from E, out =
+ *   (out_f + out_b) / 2. state_out (NULL or may alias state_in) = the causal state after all T rows.
+ *   Layouts and Dk / Dv limits as trida_gdr_recurrent; 1 <= block_size <= 64. */
+int trida_gdr_block_bidir(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g, const float* beta,
+                          const float* state_in, uint16_t* out, float* state_out, int64_t B, int64_t T, int64_t Hk,
+                          int64_t Hv, int64_t Dk, int64_t Dv, int64_t block_size, float scale, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Gated delta rule, chunked WY / UT form on MFMA (v_mfma_f32_16x16x32_bf16), same recurrence and
  * readout as trida_gdr_recurrent. Replaces chunk_gated_delta_rule(q, k, v, g, beta, chunk_size=64,

@@ -14,6 +14,8 @@ Restated from:
                   s_clean = state after the clean rows  (causal_mode 2)  inference/zoro-1/mlx/trida_mlx/kernels.py:19-97
   restore/commit  state after the first `a` block rows from the block-entry snapshot;
                   conv window = last K-1 rows of (snapshot window ++ pre-conv rows[:a])  model.py:486-507
+  block-bidir     per block, mean of the causal readout and a reversed within-block scan from the
+                  block-entry state; state carried on causally          train/models/hybrid.py:461-536
 ([tf] = transformers/models/qwen3_5/modeling_qwen3_5.py, the reference's declared CPU fallback for
 these layers, train/models/hybrid.py:31-35.)
 """
@@ -185,3 +187,24 @@ def restore(snap_state, snap_window, k, v, g, beta, preconv, n_keep):
         full = torch.cat([snap_window[b].float(), preconv[b, :a].float()], dim=0)
         windows.append(full[-Km1:])
     return torch.cat(states), torch.stack(windows)
+
+
+def block_bidirectional(q, k, v, g, beta, state: Optional[torch.Tensor], block_size: int,
+                        scale: Optional[float] = None):
+    """Block-local-bidirectional readout (train/models/hybrid.py:461-536, _block_bidirectional_gdr), blocks
+    of block_size consecutive rows (the last may be shorter). For a block with causal entry state E:
+    out_f = the causal readout, out_b = the readout of a scan over the block's rows in reverse order
+    starting from E, out = (out_f + out_b) / 2; the state carried to the next block (and returned) is
+    the causal one. Returns (o fp32 [B,T,Hv,Dv], final state)."""
+    T = k.shape[1]
+    B, Hv, Dv, Dk = v.shape[0], v.shape[2], v.shape[3], k.shape[3]
+    S = torch.zeros(B, Hv, Dv, Dk) if state is None else state.float().clone()
+    out = torch.zeros(B, T, Hv, Dv)
+    for t0 in range(0, T, block_size):
+        t1 = min(T, t0 + block_size)
+        o_f, S_next, _ = recurrent(q[:, t0:t1], k[:, t0:t1], v[:, t0:t1], g[:, t0:t1], beta[:, t0:t1], S, scale)
+        rev = torch.arange(t1 - 1, t0 - 1, -1)
+        o_b, _, _ = recurrent(q[:, rev], k[:, rev], v[:, rev], g[:, rev], beta[:, rev], S, scale)
+        out[:, t0:t1] = 0.5 * (o_f + o_b.flip(1))
+        S = S_next
+    return out, S

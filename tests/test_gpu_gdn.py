@@ -174,3 +174,18 @@ def test_restore_stacked_layers_in_place(gpu):
                         window=win, preconv=pre)
     assert rel(s, ref_s) < TOL_F32
     assert torch.equal(win.cpu().float(), ref_w.float())
+
+
+@pytest.mark.parametrize("bs,shape", [(1, (2, 7, 2, 4, 32, 16)), (8, (1, 33, 16, 16, 128, 128)),
+                                      (5, (3, 40, 2, 4, 64, 32)), (32, (1, 70, 2, 2, 128, 64)),
+                                      (64, (1, 130, 2, 2, 64, 32))])
+def test_gdr_block_bidir(gpu, bs, shape):
+    """Block-bidirectional readout (train/models/hybrid.py:461-536) vs the oracle; the carried state is
+    the causal one."""
+    inp = gdr_inputs(60 + bs, *shape)
+    o_ref, s_ref = G.block_bidirectional(*inp, block_size=bs)
+    q, k, v, g, beta, s0 = to_dev(*inp)
+    s_out = torch.empty_like(s0)
+    o = kernels.gdr_block_bidir(q, k, v, g, beta, s0, block_size=bs, state_out=s_out)
+    assert rel(o, o_ref) < TOL_BF16, rel(o, o_ref)
+    assert rel(s_out, s_ref) < TOL_F32

@@ -173,3 +173,52 @@ def test_prep_matches_pieces():
     assert torch.allclose(q.norm(dim=-1), torch.ones(B, T, Hk), atol=1e-2)
     assert torch.equal(v.reshape(B, T, -1), y[..., 2 * Hk * Dk:])
     assert torch.equal(nw, torch.cat([win, x], 1)[:, -3:])
+
+
+# ------------------------------------------------------------------ block-bidirectional readout
+def _bidir_inputs(seed, B=2, T=11, Hk=2, Hv=4, Dk=8, Dv=4):
+    g0 = torch.Generator().manual_seed(seed)
+    q = G.l2norm(torch.randn(B, T, Hk, Dk, generator=g0))
+    k = G.l2norm(torch.randn(B, T, Hk, Dk, generator=g0))
+    v = torch.randn(B, T, Hv, Dv, generator=g0)
+    g = -torch.nn.functional.softplus(torch.randn(B, T, Hv, generator=g0))
+    beta = torch.sigmoid(torch.randn(B, T, Hv, generator=g0))
+    s0 = torch.randn(B, Hv, Dv, Dk, generator=g0) * 0.1
+    return q, k, v, g, beta, s0
+
+
+def test_block_bidir_single_token_blocks_are_causal():
+    """Blocks of one row: the reversed within-block scan from the entry state is the forward step
+    itself, so the readout reduces to the causal recurrence."""
+    inp = _bidir_inputs(1)
+    o_ref, s_ref, _ = G.recurrent(*inp)
+    o, s = G.block_bidirectional(*inp, block_size=1)
+    assert torch.allclose(o, o_ref, atol=1e-6) and torch.allclose(s, s_ref, atol=1e-6)
+
+
+def test_block_bidir_state_is_causal():
+    inp = _bidir_inputs(2)
+    _, s_ref, _ = G.recurrent(*inp)
+    for bs in (2, 3, 5, 11, 64):
+        _, s = G.block_bidirectional(*inp, block_size=bs)
+        assert torch.allclose(s, s_ref, atol=1e-6), bs
+
+
+def test_block_bidir_hand_case():
+    """Scalar state (Dk = Dv = 1, k = q = 1, scale 1, no decay, beta 1/2, zero state), two rows in one
+    block. Forward: o0 = v0/2, o1 = v0/4 + v1/2. Reversed from the entry state: ob1 = v1/2, ob0 =
+    v0/2 + v1/4. Mean: (v0/2 + v1/8, v0/8 + v1/2)."""
+    v0, v1 = 3.0, -5.0
+    one = torch.ones(1, 2, 1, 1)
+    v = torch.tensor([v0, v1]).reshape(1, 2, 1, 1)
+    g = torch.zeros(1, 2, 1)
+    beta = torch.full((1, 2, 1), 0.5)
+    o, s = G.block_bidirectional(one, one, v, g, beta, torch.zeros(1, 1, 1, 1), block_size=2, scale=1.0)
+    assert torch.allclose(o.flatten(), torch.tensor([v0 / 2 + v1 / 8, v0 / 8 + v1 / 2]))
+    assert torch.allclose(s.flatten(), torch.tensor([v0 / 4 + v1 / 2]))
+    # a second block starts from the causal state after the first (the state carried on is forward)
+    v4 = torch.tensor([v0, v1, v0, v1]).reshape(1, 4, 1, 1)
+    o4, _ = G.block_bidirectional(torch.ones(1, 4, 1, 1), torch.ones(1, 4, 1, 1), v4, torch.zeros(1, 4, 1),
+                                  torch.full((1, 4, 1), 0.5), torch.zeros(1, 1, 1, 1), block_size=2, scale=1.0)
+    assert torch.allclose(o4[0, :2].flatten(), o.flatten())
+    assert not torch.allclose(o4[0, 2:].flatten(), o.flatten())

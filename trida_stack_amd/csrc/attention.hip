@@ -62,14 +62,6 @@ struct AttnArgs {
   float scale_log2;         // softmax scale * log2(e)
 };
 
-__device__ __forceinline__ bool visible(int p, int prefix, int t, int mode, int n_clean) {
-  const int j = p - prefix;
-  if (j < 0) return true;
-  if (mode == 1) return true;
-  if (mode == 2 && t >= n_clean) return true;
-  return j <= t;
-}
-
 // LDS tiles of one 64-key step, 16-byte groups XOR-swizzled so that both the staging writes and the
 // MFMA fragment reads touch 8 distinct bank groups per 8 lanes:
 //   K   [key][D]   group g of key k stored at g ^ (k & 7)
@@ -134,15 +126,24 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   const uint16_t* kh = a.k_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
   const uint16_t* vh = a.v_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
 
-  // ---- the tile's Q rows into LDS (padding rows zero); read back as A fragments every step
-  for (int gi = tid; gi < kMT * GPR; gi += NT) {
-    const int r = gi / GPR, grp = gi % GPR;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (r < rows) {
-      const int m = m0 + r, t = m / a.G, g = m % a.G;
-      v = *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + grp * 8);
+  // ---- the tile's Q rows into LDS (padding rows zero); read back as A fragments every step. Every
+  // load of the tile is issued before the first store, so the staging costs one memory latency.
+  {
+    constexpr int QPT = kMT * GPR / NT;  // 16-byte pieces per thread
+    u32x4 qv[QPT];
+#pragma unroll
+    for (int j = 0; j < QPT; ++j) {
+      const int gi = tid + j * NT;
+      const int r = gi / GPR, grp = gi % GPR;
+      const int m = m0 + min(r, rows - 1), t = m / a.G, g = m % a.G;
+      qv[j] = *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + grp * 8);
     }
-    *reinterpret_cast<u32x4*>(&sQ[k_off<D>(r, grp)]) = v;
+#pragma unroll
+    for (int j = 0; j < QPT; ++j) {
+      const int gi = tid + j * NT;
+      const int r = gi / GPR, grp = gi % GPR;
+      *reinterpret_cast<u32x4*>(&sQ[k_off<D>(r, grp)]) = r < rows ? qv[j] : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   // ---- prefetch registers: K groups (coalesced rows) and one V piece (8 keys x 4 columns)
@@ -197,6 +198,15 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     l_run[i] = 0.f;
   }
   uint16_t* pw = sP[w];
+  // the keys each of this lane's 4 rows sees are exactly [0, klim): the whole prefix, then the block keys
+  // its mask allows (a prefix of the block for the causal rows, all of it for the others)
+  int klim[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = (m0 + w * kWR + (l / 16) * 4 + i) / a.G;
+    const bool all = a.mask_mode == 1 || (a.mask_mode == 2 && t >= a.n_clean);
+    klim[i] = all ? nk : min(nk, prefix + t + 1);
+  }
 
   load_step(kb0);
   for (int kb = kb0; kb < kb1; ++kb) {
@@ -226,13 +236,12 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int rr = (l / 16) * 4 + i;  // row within the wave
-      const int t = (m0 + w * kWR + rr) / a.G;
       float mx = -INFINITY;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         const int key = key0 + kt * 16 + (l % 16);
         float v = sacc[kt][i] * a.scale_log2;
-        if (edge && !(key < nk && visible(key, prefix, t, a.mask_mode, a.n_clean))) v = -INFINITY;
+        if (edge) v = key < klim[i] ? v : -INFINITY;
         sacc[kt][i] = v;
         mx = fmaxf(mx, v);
       }

@@ -4,6 +4,9 @@
 //   S = e^{g_t} S;  kv = S k_t;  delta = beta_t (v_t - kv);  S += delta k_t^T;  o_t = S q_t
 // causal_mode 1: every row reads its own state. causal_mode 2: rows t < num_clean read their own
 // state, rows t >= num_clean read the block-end state (the state after all T rows).
+// Block-bidirectional readout (trida_gdr_block_bidir): per block of `bidir` rows, a backward sub-scan
+// over the block's rows in reverse from the block-entry state, then the causal forward sub-scan; each
+// row reads out the mean of the two; the state carried on is the forward one.
 //
 // Launch: block = (sequence b, value head h, v-tile). Each wave owns 4 value columns; the 16 lanes of
 // a column each hold KPL = Dk/16 consecutive k entries of that column's state in registers, so the
@@ -56,6 +59,7 @@ struct RecArgs {
   int T, Hk, Hv, Dk, Dv;
   int causal_mode, num_clean;
   float scale;
+  int bidir;  // > 0: block-bidirectional readout over blocks of this many rows (causal_mode 1)
 };
 
 template <int KPL, int NW>
@@ -76,6 +80,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   __shared__ __align__(16) uint16_t s_k[kTC][Dk];
   __shared__ float s_v[kTC][VPB];
   __shared__ float s_g[kTC], s_b[kTC];
+  __shared__ float s_ob[kTC][VPB];  // backward sub-scan outputs of the block-bidirectional readout
 
   const int64_t st_off = (((int64_t)b * a.Hv + h) * a.Dv + v) * Dk + kl * KPL;
   float s[KPL];
@@ -92,8 +97,34 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   const float* gb = a.g + (int64_t)b * a.T * a.Hv + h;
   const float* bb = a.beta + (int64_t)b * a.T * a.Hv + h;
 
-  for (int t0 = 0; t0 < a.T; t0 += kTC) {
-    const int tn = min(kTC, a.T - t0);
+  // rows staged per chunk: whole blocks when the readout is block-bidirectional
+  const int tcn = a.bidir > 0 ? (kTC / a.bidir) * a.bidir : kTC;
+  // one step of the recurrence on state st with staged row r; returns the row's readout S'q
+  auto step = [&](float (&st)[KPL], int r) -> float {
+    float kk[KPL], qq[KPL];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      kk[i] = bf2f(s_k[r][kl * KPL + i]);
+      qq[i] = bf2f(s_q[r][kl * KPL + i]) * a.scale;
+    }
+    const float eg = s_g[r];
+    float kv = 0.f, sq = 0.f, kq = 0.f;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      st[i] *= eg;
+      kv = fmaf(st[i], kk[i], kv);
+      sq = fmaf(st[i], qq[i], sq);
+      kq = fmaf(kk[i], qq[i], kq);
+    }
+    row16_sum2(kv, sq);
+    kq = row16_sum(kq);
+    const float delta = (s_v[r][vl] - kv) * s_b[r];
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) st[i] = fmaf(kk[i], delta, st[i]);
+    return fmaf(delta, kq, sq);
+  };
+  for (int t0 = 0; t0 < a.T; t0 += tcn) {
+    const int tn = min(tcn, a.T - t0);
     __syncthreads();  // previous chunk fully consumed
     // stage q, k rows (16-byte pieces), v tile, g, beta
     constexpr int kPieces = Dk / 8;
@@ -112,30 +143,30 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     }
     __syncthreads();
 
+    if (a.bidir > 0) {
+      // each block: a backward sub-scan from the block-entry state (a register copy), then the causal
+      // forward sub-scan; a row reads out the mean of the two
+      for (int r0 = 0; r0 < tn; r0 += a.bidir) {
+        const int r1 = min(r0 + a.bidir, tn);
+        float sb[KPL];
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) sb[i] = s[i];
+        for (int r = r1 - 1; r >= r0; --r) {
+          const float o = step(sb, r);
+          if (kl == 0) s_ob[r][vl] = o;
+        }
+        for (int r = r0; r < r1; ++r) {
+          const float o = step(s, r);
+          if (kl == 0) ob[(int64_t)(t0 + r) * v_row] = f2bf(0.5f * (o + s_ob[r][vl]));
+        }
+      }
+      continue;
+    }
 #pragma unroll 2
     for (int r = 0; r < tn; ++r) {
       const int t = t0 + r;
-      float kk[KPL], qq[KPL];
-#pragma unroll
-      for (int i = 0; i < KPL; ++i) {
-        kk[i] = bf2f(s_k[r][kl * KPL + i]);
-        qq[i] = bf2f(s_q[r][kl * KPL + i]) * a.scale;
-      }
-      const float eg = s_g[r];
-      float kv = 0.f, sq = 0.f, kq = 0.f;
-#pragma unroll
-      for (int i = 0; i < KPL; ++i) {
-        s[i] *= eg;
-        kv = fmaf(s[i], kk[i], kv);
-        sq = fmaf(s[i], qq[i], sq);
-        kq = fmaf(kk[i], qq[i], kq);
-      }
-      row16_sum2(kv, sq);
-      kq = row16_sum(kq);
-      const float delta = (s_v[r][vl] - kv) * s_b[r];
-#pragma unroll
-      for (int i = 0; i < KPL; ++i) s[i] = fmaf(kk[i], delta, s[i]);
-      if (t < nc && kl == 0) ob[(int64_t)t * v_row] = f2bf(fmaf(delta, kq, sq));
+      const float o = step(s, r);
+      if (t < nc && kl == 0) ob[(int64_t)t * v_row] = f2bf(o);
       if (t == nc - 1 && a.state_clean) {
 #pragma unroll
         for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = s[i];
@@ -210,7 +241,32 @@ extern "C" int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const u
               "gdr_recurrent: q and k must be 16-byte aligned");
   TRIDA_CHECK(B * T * Hv < INT32_MAX, TRIDA_ERR_ARG, "gdr_recurrent: problem too large");
   RecArgs a{q, k, v, g, beta, state_in, out, state_out, state_clean, (int)T, (int)Hk, (int)Hv, (int)Dk,
-            (int)Dv, causal_mode, (int)num_clean, scale};
+            (int)Dv, causal_mode, (int)num_clean, scale, 0};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (Dk) {
+    case 32: return launch_kpl<2>(a, (int)B, st);
+    case 64: return launch_kpl<4>(a, (int)B, st);
+    case 128: return launch_kpl<8>(a, (int)B, st);
+    default: return launch_kpl<16>(a, (int)B, st);
+  }
+}
+
+extern "C" int trida_gdr_block_bidir(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                                     const float* beta, const float* state_in, uint16_t* out, float* state_out,
+                                     int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv,
+                                     int64_t block_size, float scale, void* stream) {
+  TRIDA_CHECK(q && k && v && g && beta && state_in && out, TRIDA_ERR_NULL,
+              "gdr_block_bidir: q, k, v, g, beta, state_in and out are required");
+  TRIDA_CHECK(B > 0 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, TRIDA_ERR_ARG, "gdr_block_bidir: bad sizes");
+  TRIDA_CHECK(Dk == 32 || Dk == 64 || Dk == 128 || Dk == 256, TRIDA_ERR_ARG,
+              "gdr_block_bidir: Dk must be 32, 64, 128 or 256 (got %lld)", (long long)Dk);
+  TRIDA_CHECK(Dv > 0 && Dv % 4 == 0, TRIDA_ERR_ARG, "gdr_block_bidir: Dv must be a multiple of 4");
+  TRIDA_CHECK(block_size >= 1 && block_size <= kTC, TRIDA_ERR_ARG, "gdr_block_bidir: block_size in [1, %d]", kTC);
+  TRIDA_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0, TRIDA_ERR_ALIGN,
+              "gdr_block_bidir: q and k must be 16-byte aligned");
+  TRIDA_CHECK(B * T * Hv < INT32_MAX, TRIDA_ERR_ARG, "gdr_block_bidir: problem too large");
+  RecArgs a{q, k, v, g, beta, state_in, out, state_out, nullptr, (int)T, (int)Hk, (int)Hv, (int)Dk,
+            (int)Dv, 1, (int)T, scale, (int)block_size};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (Dk) {
     case 32: return launch_kpl<2>(a, (int)B, st);

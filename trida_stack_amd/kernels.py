@@ -393,6 +393,41 @@ def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     return out, clean
 
 
+def gdr_block_bidir(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                    state: torch.Tensor, *, block_size: int, state_out: Optional[torch.Tensor] = None,
+                    scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Block-bidirectional gated delta rule (the training research readout of
+    train/models/hybrid.py:461-536) over blocks of block_size rows: each row reads out the mean of the
+    causal readout and a reversed within-block scan from the block-entry state. Same shapes as
+    gdr_recurrent. Returns out [B, T, Hv, Dv] bf16."""
+    dev = _need_gpu(q, k, v, g, beta, state, state_out, out)
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _bf16(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    for t, n in ((g, "g"), (beta, "beta"), (state, "state")):
+        _f32(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    B, T, Hk, Dk = k.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    if q.shape != k.shape or v.shape[:2] != (B, T) or g.shape != (B, T, Hv) or beta.shape != g.shape:
+        raise ValueError("q/k/v/g/beta shapes disagree")
+    if state.shape != (B, Hv, Dv, Dk):
+        raise ValueError(f"state must be [B, Hv, Dv, Dk] = {(B, Hv, Dv, Dk)}")
+    if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
+                                  or not state_out.is_contiguous()):
+        raise ValueError("state_out must match state")
+    if out is None:
+        out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    sc = Dk ** -0.5 if scale is None else float(scale)
+    rc = _lib.load().trida_gdr_block_bidir(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                                           state.data_ptr(), out.data_ptr(), _ptr(state_out), B, T, Hk, Hv, Dk, Dv,
+                                           int(block_size), sc, _stream(dev))
+    _lib.check(rc, "trida_gdr_block_bidir")
+    return out
+
+
 def gdr_chunk(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
               state: torch.Tensor, *, causal_mode: int = 1, num_clean: Optional[int] = None,
               state_out: Optional[torch.Tensor] = None, n_keep: Optional[torch.Tensor] = None,
