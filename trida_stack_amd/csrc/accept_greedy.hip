@@ -2,7 +2,7 @@
 //
 // Two launches on the caller's stream, no atomics:
 //   split_argmax (grid S x R x B): block (s, r, b) reduces split s of row r of sequence b to an
-//       (argmax value, index) pair in scratch. Each thread issues U 16-byte nontemporal loads per tile
+//       (argmax value, index) pair in scratch. Each thread issues U 16-byte loads per tile
 //       back to back (indices clamped in bounds, compares masked), so a block has U * 4 KiB in flight.
 //   finalize (grid B): stages the split results and the drafts through LDS (one memory latency per
 //       pass), reduces each row with one thread per row, then one wave ballots draft matches and
@@ -116,7 +116,7 @@ __global__ __launch_bounds__(kThreads) void split_argmax_kernel(SplitArgs a) {
     for (int base = 0; base < n4; base += kThreads * U) {
       u32x4 x[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) x[u] = __builtin_nontemporal_load(row4 + min(base + u * kThreads + tid, n4 - 1));
+      for (int u = 0; u < U; ++u) x[u] = row4[min(base + u * kThreads + tid, n4 - 1)];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int j = base + u * kThreads + tid;

@@ -158,7 +158,7 @@ __device__ __forceinline__ void append(float y, bool pred, float* s_coll, int* s
 }
 
 // Calls f(y, ix, valid) for every element of a row; U 16-byte loads in flight per thread.
-template <bool kDiv, bool kVec, bool kNT, int U = 4, typename F>
+template <bool kDiv, bool kVec, int U = 4, typename F>
 __device__ __forceinline__ void for_each_y(const float* row, int V, double rt, int ban, F&& f) {
   const int tid = threadIdx.x;
   int done = 0;
@@ -170,7 +170,7 @@ __device__ __forceinline__ void for_each_y(const float* row, int V, double rt, i
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const u32x4* p = row4 + min(base + u * kT + tid, n4 - 1);
-        x[u] = kNT ? __builtin_nontemporal_load(p) : *p;
+        x[u] = *p;
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -306,7 +306,7 @@ __device__ void range_pass(const float* row, const TruncArgs& a, float m, uint32
   __syncthreads();
   int ca = 0, cf = 0;
   double ma = 0.0, z = 0.0;
-  for_each_y<kDiv, kVec, false, 2>(row, a.V, a.rt, a.ban, [&](float y, int ix, bool ok) {
+  for_each_y<kDiv, kVec, 2>(row, a.V, a.rt, a.ban, [&](float y, int ix, bool ok) {
     const bool fin = ok && (y > -INFINITY);
     const uint32_t key = fkey(y);
     const float e = __expf(y - m);
@@ -554,7 +554,7 @@ __device__ void stream_segment(const float* row, const TruncArgs& a, const BinMa
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const u32x4* p = row4 + min(base + u * kT + tid, v1 - 1);
-        x[u] = kHist ? __builtin_nontemporal_load(p) : *p;
+        x[u] = *p;
       }
       float xv[4 * U];
 #pragma unroll
@@ -758,7 +758,7 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
       }
     }
   } else {
-    for_each_y<kDiv, kVec, true>(row, V, a.rt, a.ban, [&](float y, int ix, bool ok) {
+    for_each_y<kDiv, kVec>(row, V, a.rt, a.ban, [&](float y, int ix, bool ok) {
       mx = fmaxf(mx, ok ? y : -INFINITY);
       nanbits = max(nanbits, ok ? __float_as_uint(y) << 1 : 0u);
     });

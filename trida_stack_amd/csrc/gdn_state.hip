@@ -35,14 +35,14 @@ __global__ __launch_bounds__(256) void copy2_kernel(const u32x4* __restrict__ s0
   int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   // 4 independent 16-byte copies in flight per thread per iteration
   for (; i + 3 * stride < n0; i += 4 * stride) {
-    const u32x4 a = __builtin_nontemporal_load(s0 + i), b = __builtin_nontemporal_load(s0 + i + stride);
-    const u32x4 c = __builtin_nontemporal_load(s0 + i + 2 * stride), d = __builtin_nontemporal_load(s0 + i + 3 * stride);
+    const u32x4 a = s0[i], b = s0[i + stride];
+    const u32x4 c = s0[i + 2 * stride], d = s0[i + 3 * stride];
     d0[i] = a;
     d0[i + stride] = b;
     d0[i + 2 * stride] = c;
     d0[i + 3 * stride] = d;
   }
-  for (; i < n0; i += stride) d0[i] = __builtin_nontemporal_load(s0 + i);
+  for (; i < n0; i += stride) d0[i] = s0[i];
   for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n1; j += stride) d1[j] = s1[j];
 }
 
