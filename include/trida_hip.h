@@ -169,6 +169,26 @@ int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                         float* state_clean, int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk,
                         int64_t Dv, int causal_mode, int64_t num_clean, float scale, void* stream);
 
+/* Fused self-spec GDN layer, one launch for a block of T <= 64 rows: depthwise causal conv over
+ * [window ++ x] + SiLU, split, l2norm(q, k), gates, then the recurrence and readout of
+ * trida_gdr_recurrent. Replaces fused_selfspec_gdn_layer(mixed_qkv, a, b, A_log, dt_bias, conv_weight,
+ *   win, ssm_states, block_size, num_clean, out, pre_out) (inference/zoro-1/vllm/vllm_native_diffusion/
+ *   qwen3_5_diffusion.py:2207-2221) and the Metal canvas_gdn_fused front half
+ *   (inference/zoro-1/mlx/trida_mlx/kernels.py:118-131, model.py:289-303).
+ * Inputs as trida_gdn_prep (x, window, conv_w, a, b, A_log, dt_bias, strides) plus state_in; outputs as
+ * trida_gdr_recurrent (out, state_out, state_clean) and, each optional (NULL = not written), the rows a
+ * rollback needs: k_out [B, T, Hk, Dk] bf16, v_out [B, T, Hv, Dv] bf16, g_out, beta_out [B, T, Hv] fp32
+ * (given together), pre_out [B, T, C] bf16 raw pre-conv rows, window_out [B, Kc-1, C] (must not alias
+ * window). Results are bit-identical to trida_gdn_prep followed by trida_gdr_recurrent.
+ * Dk in {32, 64, 128}, Dv % 8 == 0, 2 <= Kc <= 4. */
+int trida_gdn_fused_layer(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w, const uint16_t* a,
+                          const uint16_t* b, const float* A_log, const float* dt_bias, const float* state_in,
+                          uint16_t* out, float* state_out, float* state_clean, uint16_t* k_out, uint16_t* v_out,
+                          float* g_out, float* beta_out, uint16_t* pre_out, uint16_t* window_out, int64_t B,
+                          int64_t T, int64_t Kc, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb,
+                          int64_t x_st, int64_t ab_sb, int64_t ab_st, int causal_mode, int64_t num_clean,
+                          float scale, void* stream);
+
 /* Block-bidirectional gated delta rule: the training research path _block_bidirectional_gdr
  *   (train/models/hybrid.py:461-536) for blocks of block_size consecutive rows (the last block may be
  *   shorter). Per block with causal entry state E: out_f = the causal readout (forward sub-scan from E),

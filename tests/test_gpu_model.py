@@ -283,3 +283,34 @@ def test_block_step_graph_replay_matches_eager(gpu, pair):
         torch.matmul(torch.randn(64, 64, device=DEV), torch.randn(64, 64, device=DEV))  # eager work between
         got = (s2.canvas.cpu().clone(), int(s2.n_acc[0]), int(s2.bonus[0]), int(c2.length[0]))
         assert torch.equal(got[0], ref[i][0]) and got[1:] == ref[i][1:], i
+
+
+def test_fused_gdn_layer_matches_two_launch_forward(gpu, pair):
+    """The runtime's fused GDN layer path gives the same logits and the same committed cache as the
+    two-launch path (gdn_prep + gdr_recurrent), bit for bit, in every forward mode."""
+    rt, _ = pair
+    n = 4
+    p = prompt(21, seed=3)
+    canvas = prompt(n, seed=4) + [CFG.mask_id] * (n - 1)
+    outs = {}
+    old = rt.fused_gdn
+    try:
+        for fused in (True, False):
+            rt.fused_gdn = fused
+            c = rt.make_cache(max_len=128)
+            rt.prefill(c, p)
+            lg = [rt.ar_step(c, 7)]
+            ids = torch.tensor([canvas], device=DEV)
+            lg.append(rt.forward(ids, c, "draft")[0])
+            lg.append(rt.canvas(c, canvas, n))
+            rt.commit(c, 3)
+            lg.append(rt.verify(c, ids)[0])
+            rt.commit(c, 2)
+            lg.append(rt.ar_step(c, 9))
+            outs[fused] = (lg, c.state.clone(), c.window.clone())
+    finally:
+        rt.fused_gdn = old
+    (la, sa, wa), (lb, sb, wb) = outs[True], outs[False]
+    for i, (x, y) in enumerate(zip(la, lb)):
+        assert torch.equal(x, y), i
+    assert torch.equal(sa, sb) and torch.equal(wa, wb)

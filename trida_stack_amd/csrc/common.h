@@ -10,11 +10,12 @@ namespace trida {
 
 // ---------------------------------------------------------------- bf16 storage (uint16 bits)
 // Round-to-nearest-even, quiet NaN preserved: the same rounding torch applies on fp32 -> bf16.
+// Branch-free (a select, not a divergent branch around the NaN case).
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (u >> 16) | 0x0040u;
+  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
 }
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 

@@ -8,6 +8,12 @@
 // over the block's rows in reverse from the block-entry state, then the causal forward sub-scan; each
 // row reads out the mean of the two; the state carried on is the forward one.
 //
+// Fused layer (trida_gdn_fused_layer, blocks of <= 64 rows): the block first runs the layer's front
+// half itself -- depthwise causal conv over [window ++ x] + SiLU, l2norm of its q / k head, the gates
+// g and beta -- from the pre-conv rows, staging the head's source rows in LDS, with the arithmetic of
+// trida_gdn_prep in the same order (so the results are bit-identical to the two-kernel path). It
+// writes the rows a rollback needs (k, v, g, beta, raw pre-conv rows, new window) only when asked.
+//
 // Launch: block = (sequence b, value head h, v-tile). Each wave owns 4 value columns; the 16 lanes of
 // a column each hold KPL = Dk/16 consecutive k entries of that column's state in registers, so the
 // two dot products of a step reduce over one 16-lane DPP row (no LDS round trip). The rows of q, k,
@@ -35,6 +41,17 @@ __device__ __forceinline__ float row16_sum(float v) {
   v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
   return v;
 }
+// Four independent 16-lane row sums, interleaved so the DPP latencies overlap.
+__device__ __forceinline__ void row16_sum4(float (&v)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp<0x128>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp<0x124>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp<0x4E>(v[j]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) v[j] += dpp<0xB1>(v[j]);
+}
 __device__ __forceinline__ void row16_sum2(float& a, float& b) {
   a += dpp<0x128>(a);
   b += dpp<0x128>(b);
@@ -45,6 +62,27 @@ __device__ __forceinline__ void row16_sum2(float& a, float& b) {
   a += dpp<0xB1>(a);
   b += dpp<0xB1>(b);
 }
+
+constexpr int kMaxKc = 4;
+
+// the fused layer's front half
+struct PrepIn {
+  const uint16_t* x;       // [B, T, C] pre-conv rows (batch stride x_sb, row stride x_st)
+  const uint16_t* window;  // [B, Kc-1, C]
+  const uint16_t* conv_w;  // [C, Kc]
+  const uint16_t* a_in;    // [B, T, Hv] (batch stride ab_sb, row stride ab_st)
+  const uint16_t* b_in;
+  const float* A_log;  // [Hv]
+  const float* dt_bias;
+  uint16_t* k_out;  // [B, T, Hk, Dk] or null (rows kept for a rollback)
+  uint16_t* v_out;  // [B, T, Hv, Dv] or null
+  float* g_out;     // [B, T, Hv] or null (log decay)
+  float* beta_out;
+  uint16_t* pre_out;     // [B, T, C] raw pre-conv rows or null
+  uint16_t* window_out;  // [B, Kc-1, C] new window or null
+  int64_t x_sb, x_st, ab_sb, ab_st;
+  int Kc;
+};
 
 struct RecArgs {
   const uint16_t* q;  // [B, T, Hk, Dk]
@@ -60,9 +98,58 @@ struct RecArgs {
   int causal_mode, num_clean;
   float scale;
   int bidir;  // > 0: block-bidirectional readout over blocks of this many rows (causal_mode 1)
+  PrepIn p;   // fused layer only
 };
 
-template <int KPL, int NW>
+__device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
+  f[0] = bf2f((uint16_t)(w.x & 0xffff));
+  f[1] = bf2f((uint16_t)(w.x >> 16));
+  f[2] = bf2f((uint16_t)(w.y & 0xffff));
+  f[3] = bf2f((uint16_t)(w.y >> 16));
+  f[4] = bf2f((uint16_t)(w.z & 0xffff));
+  f[5] = bf2f((uint16_t)(w.z >> 16));
+  f[6] = bf2f((uint16_t)(w.w & 0xffff));
+  f[7] = bf2f((uint16_t)(w.w >> 16));
+}
+__device__ __forceinline__ u32x4 pack8(const float* f) {
+  u32x4 w;
+  w.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+  w.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+  w.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
+  w.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+  return w;
+}
+__device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
+// torch.nn.functional.softplus with beta 1 and threshold 20
+__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+// Sum over aligned groups of W lanes (W = 4, 8 or 16); every lane receives its group's total.
+template <int W>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  if (W == 16) {
+    v += dpp<0x128>(v);
+    v += dpp<0x124>(v);
+  } else if (W == 8) {
+    v += __shfl_xor(v, 4, kWave);
+  }
+  v += dpp<0x4E>(v);
+  v += dpp<0xB1>(v);
+  return v;
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+// Copies n items of SZ bytes (4 or 16) to LDS, item i at dst + i * SZ, from the global address src(i),
+// with direct-to-LDS loads: every load of the block stays in flight at once and no register holds the
+// data. The caller waits for vmcnt(0), then a barrier, before reading dst.
+template <int SZ, typename F>
+__device__ __forceinline__ void lds_gather(void* dst, int n, F&& src, int nthreads) {
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave), lane = (int)threadIdx.x % kWave;
+  for (int base = wave * kWave; base < n; base += nthreads)  // base is uniform over the wave
+    if (base + lane < n)
+      __builtin_amdgcn_global_load_lds(src(base + lane), (lds_void*)(static_cast<char*>(dst) + base * SZ), SZ, 0, 0);
+}
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+template <int KPL, int NW, bool PREP>
 __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   constexpr int Dk = KPL * kLanesPerV;
   constexpr int VPB = NW * kVPerWave;
@@ -78,7 +165,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
 
   __shared__ __align__(16) uint16_t s_q[kTC][Dk];
   __shared__ __align__(16) uint16_t s_k[kTC][Dk];
-  __shared__ float s_v[kTC][VPB];
+  __shared__ __align__(16) uint16_t s_v[kTC][VPB];
   __shared__ float s_g[kTC], s_b[kTC];
   __shared__ float s_ob[kTC][VPB];  // backward sub-scan outputs of the block-bidirectional readout
 
@@ -118,31 +205,191 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     }
     row16_sum2(kv, sq);
     kq = row16_sum(kq);
-    const float delta = (s_v[r][vl] - kv) * s_b[r];
+    const float delta = (bf2f(s_v[r][vl]) - kv) * s_b[r];
 #pragma unroll
     for (int i = 0; i < KPL; ++i) st[i] = fmaf(kk[i], delta, st[i]);
     return fmaf(delta, kq, sq);
   };
-  for (int t0 = 0; t0 < a.T; t0 += tcn) {
-    const int tn = min(tcn, a.T - t0);
-    __syncthreads();  // previous chunk fully consumed
-    // stage q, k rows (16-byte pieces), v tile, g, beta
-    constexpr int kPieces = Dk / 8;
-    for (int p = tid; p < tn * kPieces; p += NW * kWave) {
-      const int r = p / kPieces, c = (p % kPieces) * 8;
-      *reinterpret_cast<u32x4*>(&s_q[r][c]) = *reinterpret_cast<const u32x4*>(qb + (int64_t)(t0 + r) * qk_row + c);
-      *reinterpret_cast<u32x4*>(&s_k[r][c]) = *reinterpret_cast<const u32x4*>(kb + (int64_t)(t0 + r) * qk_row + c);
+  if constexpr (PREP) {
+    // ---- front half: conv + SiLU + l2norm + gates for this block's head, all T (<= kTC) rows ----
+    constexpr int NT = NW * kWave;
+    constexpr int GW = Dk / 8;    // 8-channel pieces per q or k head
+    constexpr int QKP = 2 * GW;   // q pieces then k pieces
+    __shared__ __align__(16) uint16_t s_src[kTC + kMaxKc - 1][2 * Dk];  // [window ++ x] rows, q|k channels
+    __shared__ __align__(16) uint16_t s_vsrc[kTC + kMaxKc - 1][VPB];
+    __shared__ __align__(16) uint16_t s_qkw[2][Dk * kMaxKc];  // conv weights [channel][tap], q then k head
+    __shared__ __align__(16) uint16_t s_vw[VPB * kMaxKc];
+    const PrepIn& p = a.p;
+    const int Kc = p.Kc, W = Kc - 1, nsrc = a.T + W;
+    const int key_dim = a.Hk * Dk, C = 2 * key_dim + a.Hv * a.Dv;
+    const uint16_t* xs = p.x + (int64_t)b * p.x_sb;
+    const uint16_t* ws = p.window + (int64_t)b * W * C;
+    auto src_row = [&](int i) { return i < W ? ws + (int64_t)i * C : xs + (int64_t)(i - W) * p.x_st; };
+    auto qk_chan = [&](int pc) { return (pc < GW ? hk * Dk : key_dim + hk * Dk - GW * 8) + pc * 8; };
+    const int vc0 = 2 * key_dim + h * a.Dv + vt * VPB;  // this block's first v channel
+    // every input of the front half in one round trip: rows and weights straight to LDS, the gate
+    // inputs into registers (T <= kTC <= NT: one row per thread)
+    lds_gather<16>(&s_src[0][0], nsrc * QKP, [&](int i) { return (const void*)(src_row(i / QKP) + qk_chan(i % QKP)); }, NT);
+    lds_gather<4>(&s_vsrc[0][0], nsrc * (VPB / 2),
+                  [&](int i) { return (const void*)(src_row(i / (VPB / 2)) + vc0 + (i % (VPB / 2)) * 2); }, NT);
+    lds_gather<16>(&s_qkw[0][0], Dk * Kc / 8, [&](int i) { return (const void*)(p.conv_w + (int64_t)hk * Dk * Kc + i * 8); }, NT);
+    lds_gather<16>(&s_qkw[1][0], Dk * Kc / 8,
+                   [&](int i) { return (const void*)(p.conv_w + (int64_t)(key_dim + hk * Dk) * Kc + i * 8); }, NT);
+    lds_gather<4>(&s_vw[0], VPB * Kc / 2, [&](int i) { return (const void*)(p.conv_w + (int64_t)vc0 * Kc + i * 2); }, NT);
+    const bool grow = tid < a.T;
+    float av = 0.f, bv = 0.f;
+    if (grow) {
+      av = bf2f(p.a_in[(int64_t)b * p.ab_sb + (int64_t)tid * p.ab_st + h]);
+      bv = bf2f(p.b_in[(int64_t)b * p.ab_sb + (int64_t)tid * p.ab_st + h]);
     }
-    for (int p = tid; p < tn * VPB; p += NW * kWave) {
-      const int r = p / VPB, c = p % VPB;
-      s_v[r][c] = bf2f(vb[(int64_t)(t0 + r) * v_row + c]);
-    }
-    for (int p = tid; p < tn; p += NW * kWave) {
-      s_g[p] = __expf(gb[(int64_t)(t0 + p) * a.Hv]);
-      s_b[p] = bb[(int64_t)(t0 + p) * a.Hv];
+    const float alog = p.A_log[h], dtb = p.dt_bias[h];
+    wait_vmem();
+    // one block per q/k head (and per value head for g, beta) writes the shared rows
+    const bool qk_writer = vt == 0 && h % (a.Hv / a.Hk) == 0;
+    if (grow) {
+      const float gl = -__expf(alog) * softplus(av + dtb);
+      const float be = 1.f / (1.f + __expf(-bv));
+      s_g[tid] = __expf(gl);
+      s_b[tid] = be;
+      if (vt == 0 && p.g_out) {
+        const int64_t o = ((int64_t)b * a.T + tid) * a.Hv + h;
+        p.g_out[o] = gl;
+        p.beta_out[o] = be;
+      }
     }
     __syncthreads();
-
+    // q / k: a thread owns one piece; the GW lanes of a head reduce its sum of squares together, so
+    // every lane of a group walks the same rows (rows past T are computed and dropped)
+    {
+      const int pc = tid % QKP, part = tid / QKP, nparts = NT / QKP;
+      float w[8][kMaxKc];
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+        for (int j = 0; j < kMaxKc; ++j)
+          w[ch][j] = j < Kc ? bf2f(s_qkw[pc < GW ? 0 : 1][((pc % GW) * 8 + ch) * Kc + j]) : 0.f;
+      const int tpad = (a.T + nparts - 1) / nparts * nparts;
+      for (int t = part; t < tpad; t += nparts) {
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < kMaxKc; ++j) {
+          if (j < Kc) {
+            float f[8];
+            unpack8(*reinterpret_cast<const u32x4*>(&s_src[t + j][pc * 8]), f);
+#pragma unroll
+            for (int ch = 0; ch < 8; ++ch) acc[ch] = fmaf(w[ch][j], f[ch], acc[ch]);
+          }
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) {
+          acc[ch] = bf2f(f2bf(silu(acc[ch])));
+          ss = fmaf(acc[ch], acc[ch], ss);
+        }
+        ss = lane_group_sum<GW>(ss);
+        const float inv = rsqrtf(ss + 1e-6f);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) acc[ch] *= inv;
+        if (t < a.T) {
+          const u32x4 pk = pack8(acc);
+          if (pc < GW) {
+            *reinterpret_cast<u32x4*>(&s_q[t][pc * 8]) = pk;
+          } else {
+            *reinterpret_cast<u32x4*>(&s_k[t][(pc - GW) * 8]) = pk;
+            if (qk_writer && p.k_out)
+              *reinterpret_cast<u32x4*>(p.k_out + (((int64_t)b * a.T + t) * a.Hk + hk) * Dk + (pc - GW) * 8) = pk;
+          }
+        }
+      }
+    }
+    // v: one (row, column) per thread
+    for (int e = tid; e < a.T * VPB; e += NT) {
+      const int t = e / VPB, cc = e % VPB;
+      float acc = 0.f;
+      for (int j = 0; j < Kc; ++j) acc = fmaf(bf2f(s_vw[cc * Kc + j]), bf2f(s_vsrc[t + j][cc]), acc);
+      const uint16_t vb16 = f2bf(silu(acc));
+      s_v[t][cc] = vb16;
+      if (p.v_out) p.v_out[((int64_t)b * a.T + t) * a.Hv * a.Dv + h * a.Dv + vt * VPB + cc] = vb16;
+    }
+    // raw pre-conv rows and the new window (last Kc-1 rows of [window ++ x]) of this block's channels
+    if (p.pre_out || p.window_out) {
+      for (int e = tid; e < nsrc * QKP; e += NT) {
+        const int i = e / QKP, pc = e % QKP;
+        if (!qk_writer) break;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(&s_src[i][pc * 8]);
+        if (p.pre_out && i >= W)
+          *reinterpret_cast<u32x4*>(p.pre_out + ((int64_t)b * a.T + (i - W)) * C + qk_chan(pc)) = val;
+        if (p.window_out && i >= nsrc - W)
+          *reinterpret_cast<u32x4*>(p.window_out + ((int64_t)b * W + (i - (nsrc - W))) * C + qk_chan(pc)) = val;
+      }
+      for (int e = tid; e < nsrc * VPB; e += NT) {
+        const int i = e / VPB, cc = e % VPB;
+        const uint16_t val = s_vsrc[i][cc];
+        if (p.pre_out && i >= W) p.pre_out[((int64_t)b * a.T + (i - W)) * C + vc0 + cc] = val;
+        if (p.window_out && i >= nsrc - W) p.window_out[((int64_t)b * W + (i - (nsrc - W))) * C + vc0 + cc] = val;
+      }
+    }
+    __syncthreads();
+  }
+  // a row's operands in registers, and the step on them (the same arithmetic as step())
+  struct Row {
+    float kk[KPL], qq[KPL];
+    float eg, vv, be;
+  };
+  auto fetch = [&](Row& R, int r) {
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      R.kk[i] = bf2f(s_k[r][kl * KPL + i]);
+      R.qq[i] = bf2f(s_q[r][kl * KPL + i]) * a.scale;
+    }
+    R.eg = s_g[r];
+    R.vv = bf2f(s_v[r][vl]);
+    R.be = s_b[r];
+  };
+  auto apply = [&](float (&st)[KPL], const Row& R) -> float {
+    float kv = 0.f, sq = 0.f, kq = 0.f;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) {
+      st[i] *= R.eg;
+      kv = fmaf(st[i], R.kk[i], kv);
+      sq = fmaf(st[i], R.qq[i], sq);
+      kq = fmaf(R.kk[i], R.qq[i], kq);
+    }
+    row16_sum2(kv, sq);
+    kq = row16_sum(kq);
+    const float delta = (R.vv - kv) * R.be;
+#pragma unroll
+    for (int i = 0; i < KPL; ++i) st[i] = fmaf(R.kk[i], delta, st[i]);
+    return fmaf(delta, kq, sq);
+  };
+  for (int t0 = 0; t0 < a.T; t0 += tcn) {
+    const int tn = min(tcn, a.T - t0);
+    if constexpr (!PREP) {
+    __syncthreads();  // previous chunk fully consumed
+    // stage q, k rows (16-byte pieces) and the v tile straight to LDS, g and beta through registers
+    // (tn <= kTC <= block size: one row per thread), all in one round trip
+    constexpr int kPieces = Dk / 8;
+    lds_gather<16>(&s_q[0][0], tn * kPieces,
+                   [&](int i) { return (const void*)(qb + (int64_t)(t0 + i / kPieces) * qk_row + (i % kPieces) * 8); },
+                   NW * kWave);
+    lds_gather<16>(&s_k[0][0], tn * kPieces,
+                   [&](int i) { return (const void*)(kb + (int64_t)(t0 + i / kPieces) * qk_row + (i % kPieces) * 8); },
+                   NW * kWave);
+    lds_gather<4>(&s_v[0][0], tn * (VPB / 2),
+                  [&](int i) { return (const void*)(vb + (int64_t)(t0 + i / (VPB / 2)) * v_row + (i % (VPB / 2)) * 2); },
+                  NW * kWave);
+    float gv = 0.f, bv = 0.f;
+    if (tid < tn) {
+      gv = gb[(int64_t)(t0 + tid) * a.Hv];
+      bv = bb[(int64_t)(t0 + tid) * a.Hv];
+    }
+    wait_vmem();
+    if (tid < tn) {
+      s_g[tid] = __expf(gv);
+      s_b[tid] = bv;
+    }
+    __syncthreads();
+    }
     if (a.bidir > 0) {
       // each block: a backward sub-scan from the block-entry state (a register copy), then the causal
       // forward sub-scan; a row reads out the mean of the two
@@ -162,37 +409,47 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       }
       continue;
     }
-#pragma unroll 2
-    for (int r = 0; r < tn; ++r) {
+    // the next row's operands are read from LDS while the current row computes (two register sets,
+    // unconditional reads of a clamped row, so the waits are the same on every path)
+    auto emit = [&](int r, float o) {
       const int t = t0 + r;
-      const float o = step(s, r);
       if (t < nc && kl == 0) ob[(int64_t)t * v_row] = f2bf(o);
       if (t == nc - 1 && a.state_clean) {
 #pragma unroll
         for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = s[i];
       }
+    };
+    Row ra, rb;
+    fetch(ra, 0);
+    int r = 0;
+    for (; r + 1 < tn; r += 2) {
+      fetch(rb, r + 1);
+      emit(r, apply(s, ra));
+      fetch(ra, min(r + 2, tn - 1));
+      emit(r + 1, apply(s, rb));
     }
+    if (r < tn) emit(r, apply(s, ra));
   }
   if (nc == 0 && a.state_clean) {
 #pragma unroll
     for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = a.state_in[st_off + i];
   }
-  // MASK rows (causal_mode 2): read the block-end state
-  for (int t = nc; t < a.T; ++t) {
-    const u32x4* qp = reinterpret_cast<const u32x4*>(qb + (int64_t)t * qk_row + kl * KPL);
-    float o = 0.f;
+  // MASK rows (causal_mode 2): read the block-end state, four rows at a time
+  for (int t = nc; t < a.T; t += 4) {
+    float o[4];
 #pragma unroll
-    for (int i = 0; i < KPL; i += 8) {
-      const u32x4 w = qp[i / 8];
-      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    for (int j = 0; j < 4; ++j) {
+      const int tt = min(t + j, a.T - 1);
+      // the lane's KPL entries of q row tt: from LDS when the whole block was staged
+      const uint16_t* qr = ((PREP || a.T <= tcn) ? &s_q[tt][0] : qb + (int64_t)tt * qk_row) + kl * KPL;
+      o[j] = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4 && i + 2 * j < KPL; ++j) {
-        o = fmaf(s[i + 2 * j], bf2f((uint16_t)(ws[j] & 0xffff)) * a.scale, o);
-        o = fmaf(s[i + 2 * j + 1], bf2f((uint16_t)(ws[j] >> 16)) * a.scale, o);
-      }
+      for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], bf2f(qr[i]) * a.scale, o[j]);
     }
-    o = row16_sum(o);
-    if (kl == 0) ob[(int64_t)t * v_row] = f2bf(o);
+    row16_sum4(o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (t + j < a.T && kl == 0) ob[(int64_t)(t + j) * v_row] = f2bf(o[j]);
   }
   if (a.state_out) {
 #pragma unroll
@@ -200,7 +457,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   }
 }
 
-template <int KPL>
+template <int KPL, bool PREP = false>
 int launch_kpl(const RecArgs& a, int B, hipStream_t st) {
   // widest block whose v-tile divides Dv; more, narrower blocks when the grid would be small
   int nw = 4;
@@ -208,11 +465,11 @@ int launch_kpl(const RecArgs& a, int B, hipStream_t st) {
   if (a.Dv % (nw * kVPerWave) != 0) return TRIDA_ERR_ARG;
   const unsigned grid = (unsigned)((int64_t)B * a.Hv * (a.Dv / (nw * kVPerWave)));
   switch (nw) {
-    case 4: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 4>), dim3(grid), dim3(4 * kWave), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 2>), dim3(grid), dim3(2 * kWave), 0, st, a); break;
-    default: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 1>), dim3(grid), dim3(kWave), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 4, PREP>), dim3(grid), dim3(4 * kWave), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 2, PREP>), dim3(grid), dim3(2 * kWave), 0, st, a); break;
+    default: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 1, PREP>), dim3(grid), dim3(kWave), 0, st, a); break;
   }
-  return launch_status("gdr_recurrent");
+  return launch_status(PREP ? "gdn_fused_layer" : "gdr_recurrent");
 }
 
 }  // namespace
@@ -237,11 +494,11 @@ extern "C" int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const u
   TRIDA_CHECK(num_clean >= 0, TRIDA_ERR_ARG, "gdr_recurrent: num_clean >= 0");
   TRIDA_CHECK(state_clean == nullptr || (state_clean != state_in && state_clean != state_out), TRIDA_ERR_ARG,
               "gdr_recurrent: state_clean must not alias state_in or state_out");
-  TRIDA_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0, TRIDA_ERR_ALIGN,
-              "gdr_recurrent: q and k must be 16-byte aligned");
+  TRIDA_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 3) == 0, TRIDA_ERR_ALIGN,
+              "gdr_recurrent: q and k must be 16-byte aligned, v 4-byte aligned");
   TRIDA_CHECK(B * T * Hv < INT32_MAX, TRIDA_ERR_ARG, "gdr_recurrent: problem too large");
   RecArgs a{q, k, v, g, beta, state_in, out, state_out, state_clean, (int)T, (int)Hk, (int)Hv, (int)Dk,
-            (int)Dv, causal_mode, (int)num_clean, scale, 0};
+            (int)Dv, causal_mode, (int)num_clean, scale, 0, PrepIn{}};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (Dk) {
     case 32: return launch_kpl<2>(a, (int)B, st);
@@ -262,16 +519,57 @@ extern "C" int trida_gdr_block_bidir(const uint16_t* q, const uint16_t* k, const
               "gdr_block_bidir: Dk must be 32, 64, 128 or 256 (got %lld)", (long long)Dk);
   TRIDA_CHECK(Dv > 0 && Dv % 4 == 0, TRIDA_ERR_ARG, "gdr_block_bidir: Dv must be a multiple of 4");
   TRIDA_CHECK(block_size >= 1 && block_size <= kTC, TRIDA_ERR_ARG, "gdr_block_bidir: block_size in [1, %d]", kTC);
-  TRIDA_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0, TRIDA_ERR_ALIGN,
-              "gdr_block_bidir: q and k must be 16-byte aligned");
+  TRIDA_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 3) == 0, TRIDA_ERR_ALIGN,
+              "gdr_block_bidir: q and k must be 16-byte aligned, v 4-byte aligned");
   TRIDA_CHECK(B * T * Hv < INT32_MAX, TRIDA_ERR_ARG, "gdr_block_bidir: problem too large");
   RecArgs a{q, k, v, g, beta, state_in, out, state_out, nullptr, (int)T, (int)Hk, (int)Hv, (int)Dk,
-            (int)Dv, 1, (int)T, scale, (int)block_size};
+            (int)Dv, 1, (int)T, scale, (int)block_size, PrepIn{}};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (Dk) {
     case 32: return launch_kpl<2>(a, (int)B, st);
     case 64: return launch_kpl<4>(a, (int)B, st);
     case 128: return launch_kpl<8>(a, (int)B, st);
     default: return launch_kpl<16>(a, (int)B, st);
+  }
+}
+
+extern "C" int trida_gdn_fused_layer(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w,
+                                     const uint16_t* a_in, const uint16_t* b_in, const float* A_log,
+                                     const float* dt_bias, const float* state_in, uint16_t* out, float* state_out,
+                                     float* state_clean, uint16_t* k_out, uint16_t* v_out, float* g_out,
+                                     float* beta_out, uint16_t* pre_out, uint16_t* window_out, int64_t B,
+                                     int64_t T, int64_t Kc, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv,
+                                     int64_t x_sb, int64_t x_st, int64_t ab_sb, int64_t ab_st, int causal_mode,
+                                     int64_t num_clean, float scale, void* stream) {
+  TRIDA_CHECK(x && window && conv_w && a_in && b_in && A_log && dt_bias && state_in && out, TRIDA_ERR_NULL,
+              "gdn_fused_layer: x, window, conv_w, a, b, A_log, dt_bias, state_in and out are required");
+  TRIDA_CHECK(B > 0 && T > 0 && T <= kTC && Hk > 0 && Hv > 0 && Hv % Hk == 0 && Kc >= 2 && Kc <= kMaxKc,
+              TRIDA_ERR_ARG, "gdn_fused_layer: bad sizes B=%lld T=%lld (<= %d) Hk=%lld Hv=%lld Kc=%lld",
+              (long long)B, (long long)T, kTC, (long long)Hk, (long long)Hv, (long long)Kc);
+  TRIDA_CHECK(Dk == 32 || Dk == 64 || Dk == 128, TRIDA_ERR_ARG, "gdn_fused_layer: Dk must be 32, 64 or 128");
+  TRIDA_CHECK(Dv > 0 && Dv % 8 == 0, TRIDA_ERR_ARG, "gdn_fused_layer: Dv must be a multiple of 8");
+  TRIDA_CHECK(causal_mode == 1 || causal_mode == 2, TRIDA_ERR_ARG, "gdn_fused_layer: causal_mode is 1 or 2");
+  TRIDA_CHECK(num_clean >= 0, TRIDA_ERR_ARG, "gdn_fused_layer: num_clean >= 0");
+  TRIDA_CHECK((g_out == nullptr) == (beta_out == nullptr), TRIDA_ERR_ARG,
+              "gdn_fused_layer: g_out and beta_out are given together");
+  TRIDA_CHECK(state_clean == nullptr || (state_clean != state_in && state_clean != state_out), TRIDA_ERR_ARG,
+              "gdn_fused_layer: state_clean must not alias state_in or state_out");
+  TRIDA_CHECK(window_out == nullptr || window_out != window, TRIDA_ERR_ARG,
+              "gdn_fused_layer: window_out must not alias window");
+  const int64_t C = 2 * Hk * Dk + Hv * Dv;
+  TRIDA_CHECK(x_st >= C && x_st % 8 == 0 && x_sb % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)window & 15) == 0 &&
+                  ((uintptr_t)conv_w & 15) == 0 && ((uintptr_t)k_out & 15) == 0 && ((uintptr_t)pre_out & 15) == 0 &&
+                  ((uintptr_t)window_out & 15) == 0,
+              TRIDA_ERR_ALIGN, "gdn_fused_layer: x, window, conv_w, k_out, pre_out, window_out 16-byte aligned, x strides in multiples of 8");
+  TRIDA_CHECK(B * T * Hv < INT32_MAX && B * T * C < INT32_MAX * 8LL, TRIDA_ERR_ARG, "gdn_fused_layer: problem too large");
+  RecArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, state_in, out, state_out, state_clean, (int)T, (int)Hk,
+            (int)Hv, (int)Dk, (int)Dv, causal_mode, (int)num_clean, scale, 0,
+            PrepIn{x, window, conv_w, a_in, b_in, A_log, dt_bias, k_out, v_out, g_out, beta_out, pre_out, window_out,
+                   x_sb, x_st, ab_sb, ab_st, (int)Kc}};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (Dk) {
+    case 32: return launch_kpl<2, true>(a, (int)B, st);
+    case 64: return launch_kpl<4, true>(a, (int)B, st);
+    default: return launch_kpl<8, true>(a, (int)B, st);
   }
 }

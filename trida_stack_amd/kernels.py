@@ -393,6 +393,66 @@ def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     return out, clean
 
 
+def gdn_fused_layer(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+                    A_log: torch.Tensor, dt_bias: torch.Tensor, state: torch.Tensor, *, Hk: int, Hv: int, Dk: int,
+                    Dv: int, causal_mode: int = 1, num_clean: Optional[int] = None,
+                    state_out: Optional[torch.Tensor] = None, want_clean: bool = False,
+                    rows_out: Optional[tuple] = None, pre_out: Optional[torch.Tensor] = None,
+                    window_out: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                    out: Optional[torch.Tensor] = None):
+    """The GDN layer's conv + prep + recurrence + readout for a block of T <= 64 rows in one launch
+    (fused_selfspec_gdn_layer, qwen3_5_diffusion.py:2207-2221); bit-identical to gdn_prep followed by
+    gdr_recurrent. Inputs as gdn_prep plus state [B, Hv, Dv, Dk] fp32. Optional outputs:
+    rows_out = (k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g, beta [B,T,Hv] fp32) for a rollback,
+    pre_out [B, T, C] bf16 (raw pre-conv rows), window_out [B, Kc-1, C] (not aliasing window).
+    Returns (out [B,T,Hv,Dv] bf16, state_clean or None)."""
+    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, state, state_out, out, pre_out, window_out)
+    for t, n in ((x, "x"), (window, "window"), (conv_w, "conv_w"), (a, "a"), (b, "b")):
+        _bf16(t, n)
+    for t, n in ((A_log, "A_log"), (dt_bias, "dt_bias"), (state, "state")):
+        _f32(t, n)
+    B, T, C = x.shape
+    Kc = conv_w.shape[1]
+    if C != 2 * Hk * Dk + Hv * Dv or conv_w.shape != (C, Kc) or not conv_w.is_contiguous():
+        raise ValueError("x / conv_w do not match the head geometry")
+    if x.stride(2) != 1 or window.shape != (B, Kc - 1, C) or not window.is_contiguous():
+        raise ValueError("x must have a contiguous last dim and window be contiguous [B, Kc-1, C]")
+    if a.shape != (B, T, Hv) or b.shape != (B, T, Hv) or a.stride() != b.stride() or a.stride(2) != 1:
+        raise ValueError("a and b must be [B, T, Hv] with identical strides and a contiguous last dim")
+    if state.shape != (B, Hv, Dv, Dk) or not state.is_contiguous():
+        raise ValueError(f"state must be contiguous [B, Hv, Dv, Dk] = {(B, Hv, Dv, Dk)}")
+    if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
+                                  or not state_out.is_contiguous()):
+        raise ValueError("state_out must match state")
+    if window_out is not None and (window_out.shape != window.shape or not window_out.is_contiguous()
+                                   or window_out.data_ptr() == window.data_ptr()):
+        raise ValueError("window_out must be a separate contiguous [B, Kc-1, C] buffer")
+    if pre_out is not None and (pre_out.shape != (B, T, C) or pre_out.dtype != torch.bfloat16
+                                or not pre_out.is_contiguous()):
+        raise ValueError("pre_out must be contiguous bf16 [B, T, C]")
+    kr = vr = gr = br = None
+    if rows_out is not None:
+        kr, vr, gr, br = rows_out
+        if kr.shape != (B, T, Hk, Dk) or vr.shape != (B, T, Hv, Dv) or gr.shape != (B, T, Hv) \
+                or br.shape != gr.shape or not all(t.is_contiguous() for t in rows_out):
+            raise ValueError("gdn_fused_layer: rows_out buffers have the wrong shape")
+    nc = T if num_clean is None else int(num_clean)
+    if out is None:
+        out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    elif out.shape != (B, T, Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("gdn_fused_layer: out must be contiguous bf16 [B, T, Hv, Dv]")
+    clean = torch.empty_like(state) if want_clean else None
+    sc = Dk ** -0.5 if scale is None else float(scale)
+    rc = _lib.load().trida_gdn_fused_layer(
+        x.data_ptr(), window.data_ptr(), conv_w.data_ptr(), a.data_ptr(), b.data_ptr(),
+        A_log.contiguous().data_ptr(), dt_bias.contiguous().data_ptr(), state.data_ptr(), out.data_ptr(),
+        _ptr(state_out), _ptr(clean), _ptr(kr), _ptr(vr), _ptr(gr), _ptr(br), _ptr(pre_out), _ptr(window_out),
+        B, T, Kc, Hk, Hv, Dk, Dv, x.stride(0), x.stride(1), a.stride(0), a.stride(1), causal_mode, nc, sc,
+        _stream(dev))
+    _lib.check(rc, "trida_gdn_fused_layer")
+    return out, clean
+
+
 def gdr_block_bidir(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                     state: torch.Tensor, *, block_size: int, state_out: Optional[torch.Tensor] = None,
                     scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -251,6 +251,11 @@ class TridaRuntime:
     # same recurrence; only "recurrent" makes the rows of a verify block bitwise equal to the same rows
     # decoded one AR step at a time.
     gdr_form = "auto"
+    # recurrent blocks of <= 64 rows may run conv + prep + recurrence as one launch
+    # (trida_gdn_fused_layer, bit-identical to trida_gdn_prep then trida_gdr_recurrent). Off: each
+    # recurrence block would redo its head's q/k front half (16x at batch 1), which measures slower
+    # than the separate prep launch (27 vs 23 us per layer at batch 1, 407 vs 236 us at batch 64).
+    fused_gdn = False
 
     def _chunked_gdr(self, T: int, gdn_mode: int) -> bool:
         c = self.cfg
@@ -323,24 +328,36 @@ class TridaRuntime:
                 b_in = s.proj[..., off: off + c.lin_v_heads]
                 a_in = s.proj[..., off + c.lin_v_heads: off + 2 * c.lin_v_heads]
                 rec = (s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j])
-                with K.timed("gdn_prep"):
-                    K.gdn_prep(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"], w[p + "dt_bias"],
-                               Hk=c.lin_k_heads, Hv=c.lin_v_heads, Dk=c.lin_k_dim, Dv=c.lin_v_dim,
-                               window_out=s.win_tmp if persist else None, out=rec)
-                if self._chunked_gdr(T, gdn_mode):
-                    with K.timed("gdr_chunk"):
-                        K.gdr_chunk(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
-                                    causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
-                                    out=s.y)
+                chunked = self._chunked_gdr(T, gdn_mode)
+                keep = mode != "draft"  # a draft pass is never committed
+                if not chunked and self.fused_gdn and T <= 64 and c.lin_k_dim in (32, 64, 128):
+                    with K.timed("gdn_fused"):
+                        K.gdn_fused_layer(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"],
+                                          w[p + "dt_bias"], state[j], Hk=c.lin_k_heads, Hv=c.lin_v_heads,
+                                          Dk=c.lin_k_dim, Dv=c.lin_v_dim, causal_mode=gdn_mode, num_clean=nc,
+                                          state_out=state[j] if persist else None,
+                                          rows_out=rec[1:] if keep else None,
+                                          pre_out=s.pre_rec[j] if keep and not persist else None,
+                                          window_out=s.win_tmp if persist else None, out=s.y)
                 else:
-                    with K.timed("gdr_recurrent"):
-                        K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
+                    with K.timed("gdn_prep"):
+                        K.gdn_prep(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"], w[p + "dt_bias"],
+                                   Hk=c.lin_k_heads, Hv=c.lin_v_heads, Dk=c.lin_k_dim, Dv=c.lin_v_dim,
+                                   window_out=s.win_tmp if persist else None, out=rec)
+                    if chunked:
+                        with K.timed("gdr_chunk"):
+                            K.gdr_chunk(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
                                         causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
                                         out=s.y)
+                    else:
+                        with K.timed("gdr_recurrent"):
+                            K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
+                                            causal_mode=gdn_mode, num_clean=nc,
+                                            state_out=state[j] if persist else None, out=s.y)
+                    if keep and not persist:
+                        s.pre_rec[j].copy_(xv)
                 if persist:
                     window[j].copy_(s.win_tmp)
-                elif mode != "draft":  # a draft pass is never committed
-                    s.pre_rec[j].copy_(xv)
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
                 K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
                 self._mm(s.yn.view(N, -1), w[p + "w_out"], s.r)
