@@ -8,6 +8,9 @@ layer math is the Qwen3.5 decoder layer ([tf]:420-760): zero-centred RMSNorm, GD
 full attention with per-head q/k RMSNorm, rotate-half partial RoPE, GQA and a sigmoid output gate,
 SwiGLU MLP, tied LM head.
 
+Also restates the vLLM plugin's greedy block-diffusion loop (qwen3_5_diffusion.py:449-632, 1180-1270):
+shift_conf_pred, denoise_round, diffusion_generate.
+
 Weights use the dict layout of trida_stack_amd.model.init_weights ([out, in] projections; the GDN
 in-projection stacks [qkv | z | b | a] rows, the attention one [Hq x (q | gate) | k | v]).
 """
@@ -147,7 +150,7 @@ class CpuHybrid:
             act = bf(F.silu(gu[:, :I]) * gu[:, I:])
             h = bf(h + bf(act @ w[p + "w_down"].t()))
         x = rmsnorm(h, w["final_norm"], c.rms_eps)
-        logits = bf(x @ w["embed"].t())
+        logits = bf(x @ w.get("lm_head", w["embed"]).t())
         if persist:
             cache.tokens.extend(tokens)
         else:
@@ -316,3 +319,54 @@ def blockspec_sample_step(m: CpuHybrid, cache: CpuCache, t0: int, block: int, de
     acc, tok = int(res["n_acc"][0]), int(res["token"][0])
     m.commit(cache, 1 + acc)
     return canvas[1: 1 + acc] + [tok], tok, acc
+
+
+# ---------------------------------------------------------------------- pure block diffusion (greedy)
+def shift_conf_pred(logits: torch.Tensor, mask_id: int):
+    """Shifted readout of a canvas forward (qwen3_5_diffusion.py:449-466): position i >= 1 is
+    predicted by the logits of position i-1, with its fp32 softmax maximum as the confidence; position
+    0 (the seed) gets -inf / mask_id. logits [CL, V]. Returns (conf [CL] fp32, pred [CL] int64)."""
+    probs = torch.softmax(logits[:-1].float(), dim=-1)
+    c, p = probs.max(dim=-1)
+    conf = torch.cat([torch.tensor([float("-inf")]), c])
+    pred = torch.cat([torch.tensor([mask_id]), p])
+    return conf, pred
+
+
+def denoise_round(canvas: List[int], logits: torch.Tensor, mask_id: int, threshold: float) -> List[int]:
+    """One LowConfidenceShift round (qwen3_5_diffusion.py:476-524, 596-600): every still-masked position
+    (never position 0) whose confidence exceeds `threshold` takes its prediction; when masks remain but
+    none passes, only the most confident masked position (first on ties) does."""
+    conf, pred = shift_conf_pred(logits, mask_id)
+    masked = [i >= 1 and t == mask_id for i, t in enumerate(canvas)]
+    score = [float(conf[i]) if masked[i] else float("-inf") for i in range(len(canvas))]
+    take = [s > threshold for s in score]
+    if any(masked) and not any(take):
+        best = max(range(len(canvas)), key=lambda i: (score[i], -i))
+        take[best] = True
+    return [int(pred[i]) if take[i] else t for i, t in enumerate(canvas)]
+
+
+def diffusion_generate(m: CpuHybrid, prompt: List[int], max_new: int, canvas: int = 32, threshold: float = 0.9,
+                       max_steps: Optional[int] = None) -> List[int]:
+    """Greedy block diffusion (qwen3_5_diffusion.py:1180-1270): each block [seed, MASK x (canvas-1)] is
+    denoised with draft passes (prefix + whole block visible, MASK rows read the block-end GDN state)
+    until no mask is left or max_steps rounds ran; a causal forward then commits the block, every
+    position of it is emitted, and the argmax of its last logit seeds the next block. The first seed
+    is the argmax of the prompt's last logit."""
+    max_steps = canvas if max_steps is None else max_steps
+    cache = m.make_cache()
+    seed = argmax(m.prefill(cache, prompt))
+    out: List[int] = []
+    while True:
+        blk = [seed] + [m.mask_id] * (canvas - 1)
+        for _ in range(max_steps):
+            blk = denoise_round(blk, m.forward(blk, cache, "draft"), m.mask_id, threshold)
+            cache.pending = None
+            if m.mask_id not in blk[1:]:
+                break
+        logits = m.forward(blk, cache, "causal")
+        out.extend(blk)
+        if len(out) >= max_new:
+            return out[:max_new]
+        seed = argmax(logits[-1])

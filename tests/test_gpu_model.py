@@ -314,3 +314,39 @@ def test_fused_gdn_layer_matches_two_launch_forward(gpu, pair):
     for i, (x, y) in enumerate(zip(la, lb)):
         assert torch.equal(x, y), i
     assert torch.equal(sa, sb) and torch.equal(wa, wb)
+
+
+def test_engine_from_checkpoint_directory(gpu, tmp_path):
+    """Engine(checkpoint_dir) generates exactly what an engine over the same weights in memory does, and
+    takes the eos ids of generation_config.json."""
+    from trida_stack_amd import checkpoint as CK
+    from trida_stack_amd.engine import Engine
+
+    w = init_weights(CFG, seed=0, embed_scale=4.0)
+    CK.save_checkpoint(tmp_path, CFG, w, eos_ids={CFG.vocab - 2})
+    e1 = Engine(str(tmp_path), mode="self-spec", gen_block=4)
+    e2 = Engine(TridaRuntime(CFG, w, device=DEV), mode="self-spec", gen_block=4)
+    assert e1.eos_ids == {CFG.vocab - 2} and e1.mask_id == CFG.mask_id
+    p = prompt(19, seed=12)
+    a = collect(e1.generate_ids(p, max_tokens=40, stop_ids=set()))
+    b = collect(e2.generate_ids(p, max_tokens=40, stop_ids=e1.eos_ids))
+    assert a == b
+
+
+@pytest.mark.parametrize("threshold,canvas", [(0.9, 8), (0.3, 8), (0.9, 16)])
+def test_diffusion_mode_follows_oracle(gpu, threshold, canvas):
+    """Greedy block diffusion (confidence-threshold commit gate) on the GPU == the CPU oracle's loop,
+    token for token (first divergence allowed only at a near-tie of the AR logits)."""
+    from trida_stack_amd.engine import Engine
+
+    w = init_weights(CFG, seed=0, embed_scale=1.0)
+    w["embed"][CFG.mask_id] = 0  # a MASK input does not predict MASK (a random model otherwise would)
+    rt, m = TridaRuntime(CFG, w, device=DEV), OM.CpuHybrid(CFG, w)
+    eng = Engine(rt, mode="diffusion", canvas=canvas, threshold=threshold)
+    for seed in range(2):
+        p = prompt(20, seed=seed + 30)
+        st = DecodeStats()
+        got = collect(eng.generate_ids(p, max_tokens=40, stats=st))
+        ref = OM.diffusion_generate(m, p, 40, canvas=canvas, threshold=threshold)
+        assert len(got) == 40 and st.mode == "diffusion" and st.steps == -(-40 // canvas)
+        assert got == ref or same_or_near_tie(rt, p, ref, got), (seed, got, ref)

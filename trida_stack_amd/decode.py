@@ -139,6 +139,59 @@ def ar_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_toke
     stats.decode_s = time.perf_counter() - t
 
 
+# ----------------------------------------------------------------------------- pure block diffusion
+def diffusion_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
+                       mask_id: int, canvas: int = 32, threshold: float = 0.9, max_steps: Optional[int] = None,
+                       stats: Optional[DecodeStats] = None) -> Iterator[list]:
+    """Greedy block diffusion with the LowConfidenceShift commit gate (qwen3_5_diffusion.py:449-632,
+    1180-1270). A block [seed, MASK x (canvas - 1)] is denoised by draft passes (prefix plus the whole
+    block visible; MASK rows read the block-end GDN state): position i takes the prediction of the
+    logits of position i - 1 when its softmax confidence exceeds `threshold`, or, when no masked
+    position passes, only the most confident one does (first on ties); rounds repeat until no mask is
+    left or `max_steps` (default: canvas) ran. A causal forward then commits the block; the whole
+    block is emitted and the argmax of its last logit seeds the next one."""
+    stats = stats or DecodeStats()
+    stats.mode = "diffusion"
+    CL = int(canvas)
+    if CL < 2:
+        raise ValueError("canvas must hold the seed and at least one masked position")
+    max_steps = CL if max_steps is None else int(max_steps)
+    seed = _argmax1(_prefill(rt, cache, prompt, stats))
+    emit = _Emitter(stats, max_new_tokens, eos_ids)
+    dev = rt.dev
+    ids = torch.full((1, CL), mask_id, dtype=torch.int64, device=dev)
+    neg = torch.tensor(float("-inf"), device=dev)
+    t = time.perf_counter()
+    while True:
+        ids.fill_(mask_id)
+        ids[0, 0] = seed
+        for _ in range(max_steps):
+            logits = rt.draft(cache, ids)[0]
+            stats.forwards += 1
+            pred, conf = K.row_argmax(logits[: CL - 1])  # row i - 1 predicts position i
+            cur = ids[0, 1:]
+            masked = cur == mask_id
+            score = torch.where(masked, conf, neg)
+            take = score > threshold
+            if not bool(take.any()):
+                best = int(torch.nonzero(score == score.max())[0])  # first most confident masked position
+                take[best] = True
+            ids[0, 1:] = torch.where(take, pred, cur)
+            if not bool((ids[0, 1:] == mask_id).any()):
+                break
+        block = ids[0].tolist()
+        logits = rt.prefill(cache, block)  # the causal commit forward (state and KV persisted)
+        stats.forwards += 1
+        stats.steps += 1
+        out = emit(block)
+        if out:
+            yield out
+        if emit.done:
+            break
+        seed = _argmax1(logits)
+    stats.decode_s = time.perf_counter() - t
+
+
 # ----------------------------------------------------------------------------- self-spec
 def selfspec_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
                       sp: SamplingParams, mask_id: int, n: int = 4, stats: Optional[DecodeStats] = None,

@@ -26,7 +26,7 @@ from __future__ import annotations
 import json
 import math
 from dataclasses import asdict, dataclass, field
-from typing import Dict, List, Optional
+from typing import Dict, List, Optional, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -56,6 +56,9 @@ class HybridConfig:
     rms_eps: float = 1e-6
     mask_id: int = DEFAULT_MASK_ID
     tie_embeddings: bool = True
+    # per-layer "linear_attention" / "full_attention" (a checkpoint's config.json layer_types); when
+    # None, layer i is full attention iff (i + 1) % full_attention_interval == 0
+    layer_types: Optional[Tuple[str, ...]] = None
 
     @property
     def conv_dim(self) -> int:
@@ -70,6 +73,8 @@ class HybridConfig:
         return int(self.head_dim * self.rotary_frac)
 
     def is_attention(self, i: int) -> bool:
+        if self.layer_types is not None:
+            return self.layer_types[i] == "full_attention"
         return (i + 1) % self.full_attention_interval == 0
 
     @classmethod
@@ -370,7 +375,7 @@ class TridaRuntime:
         if rows is not None:
             x = x[:, :rows]
         with K.timed("lm_head"):
-            logits = self._mm(x.reshape(-1, x.shape[-1]), w["embed"]).view(B, x.shape[1], -1)
+            logits = self._mm(x.reshape(-1, x.shape[-1]), w.get("lm_head", w["embed"])).view(B, x.shape[1], -1)
         fwd_timer.__exit__(None, None, None)
         if persist:
             length += T
