@@ -71,11 +71,12 @@ def test_sampling_argument_checks():
 
 
 def test_mode_registry_matches_reference_launcher():
-    """The --mode values of the reference launcher (inference/zoro-1/serve.py:55-58)."""
+    """The --mode values of the reference launcher (inference/zoro-1/serve.py:55-58), plus "diffusion",
+    the vLLM plugin's pure block-diffusion decode (qwen3_5_diffusion.py:1180-1270)."""
     from trida_stack_amd.engine import MODES
     from trida_stack_amd import cli
 
-    assert set(MODES) == {"causal", "self-spec"}
+    assert {"causal", "self-spec"} <= set(MODES) and set(MODES) - {"causal", "self-spec"} == {"diffusion"}
     import pytest as _p
     with _p.raises(SystemExit):
         cli.main(["--mode", "decide"])
