@@ -84,6 +84,7 @@ def bench_accept(args):
         cpu = {"value": round(cpu_us, 2), "unit": "us per verify step", "cores": 1, "kind": "port",
                "sample": f"{reps} oracle greedy_accept calls on the same [1,33,151936] fp32 logits (numpy)"}
     n_acc = int(out[1][0])
+    at_scale = _greedy_accept_at_scale(dev, K)
     return {
         "metric": METRIC, "value": round(kern_ms * 1e3, 3), "unit": "us per greedy verify step (kernel)",
         "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall_ms, 5),
@@ -93,8 +94,36 @@ def bench_accept(args):
                    "n_acc": n_acc},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "at_scale": at_scale,
         "cpu_baseline": cpu,
     }
+
+
+def _greedy_accept_at_scale(dev, K):
+    """The same two kernels at batch 64 over the 4B-shape vocabulary (248320): the verify logits in the
+    runtime's bf16 layout (1.05 GB) and in fp32 (2.1 GB). At 20 MB (batch 1) a launch is latency-bound;
+    here the HBM stream dominates."""
+    import torch
+
+    from trida_stack_amd import kernels
+
+    B, V = 64, 248320
+    g = torch.Generator(device=dev).manual_seed(1)
+    drafts = torch.randint(0, V, (B, K), generator=g, device=dev)
+    ctx = torch.full((B,), 4096, dtype=torch.int64, device=dev)
+    res = {}
+    for dt, esz in ((torch.bfloat16, 2), (torch.float32, 4)):
+        lg = (torch.randn(B, K + 1, V, generator=g, device=dev) * 2).to(dt)
+        fn = lambda: kernels.greedy_accept(lg, drafts, ctx_len=ctx)
+        for _ in range(3):
+            fn()
+        us = _events_time_ms(fn, 20) * 1e3
+        nbytes = B * (K + 1) * V * esz
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[str(dt).replace("torch.", "")] = {"us": round(us, 1), "bytes": nbytes, "GBps": round(gbs, 1),
+                                              "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del lg
+    return {"workload": f"greedy acceptance, batch {B}, {K + 1} verify rows, vocab {V}", **res}
 
 
 # ------------------------------------------------------------------------------ sampled acceptance
@@ -623,8 +652,52 @@ def bench_gdr(args):
                    "snapshot_GBps": round(snap_bytes / us["snapshot"] / 1e3, 1)},
         "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (prep + scan)", "achieved": round(tflops, 1),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None},
+        "at_scale": _snapshot_restore_at_scale(dev, H, D, CH),
         "cpu_baseline": cpu,
     }
+
+
+def _snapshot_restore_at_scale(dev, H, D, CH, L=24, B=64, T=33):
+    """Snapshot and rollback over every GDN layer of a batch-64 decode step: L * B state slots
+    [H, D, D] fp32 (1.61 GB) and conv windows [3, CH] bf16. The rollback advances each slot from its
+    snapshot by that sequence's kept rows (1 + accepted, seeded in [1, T]) and rebuilds the window from
+    the block's pre-conv rows; its algorithmic bytes are the state read + write, the kept k / v / g /
+    beta rows, the window written and the rows it is rebuilt from."""
+    import torch
+    import torch.nn.functional as F
+
+    from trida_stack_amd import kernels as K
+
+    NB = L * B
+    g = torch.Generator(device=dev).manual_seed(2)
+    rn = lambda *sh: torch.randn(*sh, generator=g, device=dev)
+    st = rn(NB, H, D, D) * 0.1
+    sn = torch.empty_like(st)
+    win = rn(NB, 3, CH).bfloat16()
+    snw = torch.empty_like(win)
+    kb = rn(NB, T, H, D)
+    kb = (kb * torch.rsqrt((kb * kb).sum(-1, keepdim=True) + 1e-6)).bfloat16()
+    vb = rn(NB, T, H, D).bfloat16()
+    gb, bb = (-F.softplus(rn(NB, T, H))).contiguous(), torch.sigmoid(rn(NB, T, H)).contiguous()
+    pre = rn(NB, T, CH).bfloat16()
+    n_keep = torch.randint(1, T + 1, (B,), generator=g, device=dev, dtype=torch.int32)
+    snapshot = lambda: K.gdn_snapshot(st, sn, win, snw)
+    restore = lambda: K.gdn_restore(n_keep, snap_state=sn, state=st, k=kb, v=vb, g=gb, beta=bb, snap_window=snw,
+                                    window=win, preconv=pre)
+    snapshot(), restore()
+    torch.cuda.synchronize()
+    state_b, win_b = NB * H * D * D * 4, NB * 3 * CH * 2
+    kept = int(n_keep.sum()) * L  # kept rows over all slots
+    row_b = H * D * 2 * 2 + H * 4 * 2
+    snap_bytes = 2 * (state_b + win_b)
+    rest_bytes = 2 * state_b + kept * row_b + 2 * win_b
+    res = {"workload": f"{L} GDN layers x batch {B}: state [{H}, {D}, {D}] fp32 + window [3, {CH}] bf16 per slot"}
+    for name, fn, nb in (("snapshot", snapshot, snap_bytes), ("restore", restore, rest_bytes)):
+        us = _events_time_ms(fn, 10) * 1e3
+        gbs = nb / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 1), "bytes": nb, "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del st, sn, win, snw, kb, vb, gb, bb, pre
+    return res
 
 
 

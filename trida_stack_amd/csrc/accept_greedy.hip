@@ -3,7 +3,9 @@
 // Two launches on the caller's stream, no atomics:
 //   split_argmax (grid S x R x B): block (s, r, b) reduces split s of row r of sequence b to an
 //       (argmax value, index) pair in scratch. Each thread issues U 16-byte loads per tile
-//       back to back (indices clamped in bounds, compares masked), so a block has U * 4 KiB in flight.
+//       back to back (indices clamped in bounds, loads past the split set to -inf), so a block has
+//       U * 4 KiB in flight, and folds the tile as a max first and an index search only when the
+//       tile's max beats the thread's best.
 //   finalize (grid B): stages the split results and the drafts through LDS (one memory latency per
 //       pass), reduces each row with one thread per row, then one wave ballots draft matches and
 //       takes the accepted length as the count of leading ones.
@@ -97,6 +99,93 @@ __device__ __forceinline__ void acc_exp(float x, bool valid, float& m, float& s)
   }
 }
 
+// Element e of load u of a tile, as fp32.
+template <typename TIn>
+__device__ __forceinline__ float elem(const u32x4 w, int e) {
+  const uint32_t word = w[Vec<TIn>::N == 4 ? e : e >> 1];
+  if (Vec<TIn>::N == 4) return __uint_as_float(word);
+  return __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+}
+
+// Folds one tile (U loads of N elements per thread; row4 + j0 + u * kThreads is load u) into the
+// thread's running (best, bi), with take()'s result: per load the max m_u, then the tile max m; only
+// when m beats best does the thread find the first load holding m and the first element of it equal
+// to m (+-inf need nothing more: -inf never beats best, and the first +inf is the first element equal
+// to m). A NaN is flagged from the raw words (|x| above inf, i.e. x << 1 above inf << 1 per element)
+// and such a tile (rare) is read again and taken element by element. Loads at or past n4 hold -inf;
+// element e of load u has index ix0 + u * N * kThreads + e.
+// kConf: the tile's softmax partial sum(exp(x - m)) is folded into the thread's (sm, ss) once per tile;
+// a tile whose max is +inf is also taken element by element (acc_exp's order for infinities).
+template <int U, typename TIn, bool kConf>
+__device__ __forceinline__ void fold_tile(const u32x4 (&x)[U], const u32x4* row4, int j0, int n4, int ix0,
+                                          float& best, int& bi, float& sm, float& ss) {
+  constexpr int N = Vec<TIn>::N;
+  constexpr float kLog2e = 1.44269504f;
+  float mu[U];
+  uint32_t nb = 0u;
+  float pm = -INFINITY, ps[4] = {0.f, 0.f, 0.f, 0.f};  // kConf: the tile's running (max, sum exp(x - max))
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float m = elem<TIn>(x[u], 0);
+#pragma unroll
+    for (int e = 1; e < N; ++e) m = fmaxf(m, elem<TIn>(x[u], e));
+    mu[u] = m;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)  // bf16: both halves' magnitudes at the top of a word
+      nb = N == 8 ? max(nb, max(x[u][k] << 1, x[u][k] << 17)) : max(nb, x[u][k] << 1);
+    if (kConf) {  // rescale to the new max, then add this load's terms while its elements are live
+      const float nm = fmaxf(pm, m);
+      const float sc = pm > -INFINITY ? __builtin_amdgcn_exp2f((pm - nm) * kLog2e) : 0.f;
+      const float ml = nm > -INFINITY ? nm * kLog2e : 0.f;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) ps[k] *= sc;
+#pragma unroll
+      for (int e = 0; e < N; ++e) ps[e & 3] += __builtin_amdgcn_exp2f(fmaf(elem<TIn>(x[u], e), kLog2e, -ml));
+      pm = nm;
+    }
+  }
+  float m = mu[0];
+#pragma unroll
+  for (int u = 1; u < U; ++u) m = fmaxf(m, mu[u]);
+  if (nb > (N == 8 ? 0xff01ffffu : 0xff000000u) || (kConf && m == INFINITY)) {  // a NaN (or +inf) in the tile
+#pragma unroll 1
+    for (int u = 0; u < U; ++u) {
+      const int j = j0 + u * kThreads;
+      if (j >= n4) break;
+      const u32x4 w = row4[j];
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        const float f = elem<TIn>(w, e);
+        take(f, ix0 + u * N * kThreads + e, true, best, bi);
+        if (kConf) acc_exp(f, true, sm, ss);
+      }
+    }
+    return;
+  }
+  if (kConf && m > -INFINITY) {  // pm == m
+    const float st = (ps[0] + ps[1]) + (ps[2] + ps[3]);
+    if (m > sm) {
+      ss = ss * __expf(sm - m) + st;
+      sm = m;
+    } else {
+      ss += st * __expf(m - sm);
+    }
+  }
+  if (!(m > best)) return;  // also keeps a NaN best
+  const int ustride = N * kThreads;
+  int us = U - 1;
+#pragma unroll
+  for (int u = U - 2; u >= 0; --u) us = mu[u] == m ? u : us;
+  u32x4 w = x[U - 1];
+#pragma unroll
+  for (int u = U - 2; u >= 0; --u) w = u == us ? x[u] : w;
+  int es = N - 1;
+#pragma unroll
+  for (int e = N - 2; e >= 0; --e) es = elem<TIn>(w, e) == m ? e : es;
+  best = m;
+  bi = ix0 + us * ustride + es;
+}
+
 template <int U, bool kVec, typename TIn, bool kConf>
 __global__ __launch_bounds__(kThreads) void split_argmax_kernel(SplitArgs a) {
   constexpr int N = Vec<TIn>::N;
@@ -117,19 +206,13 @@ __global__ __launch_bounds__(kThreads) void split_argmax_kernel(SplitArgs a) {
       u32x4 x[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) x[u] = row4[min(base + u * kThreads + tid, n4 - 1)];
+      if (base + U * kThreads > n4) {  // the split's last tile: loads past it become -inf
+        const uint32_t ninf = N == 4 ? 0xff800000u : 0xff80ff80u;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int j = base + u * kThreads + tid;
-        const bool ok = j < n4;
-        const int ix = lo + N * j;
-        float f[N];
-        Vec<TIn>::get(x[u], f);
-#pragma unroll
-        for (int e = 0; e < N; ++e) {
-          take(f[e], ix + e, ok, best, bi);
-          if (kConf) acc_exp(f[e], ok, sm, ss);
-        }
+        for (int u = 0; u < U; ++u)
+          if (base + u * kThreads + tid >= n4) x[u] = u32x4{ninf, ninf, ninf, ninf};
       }
+      fold_tile<U, TIn, kConf>(x, row4, base + tid, n4, lo + N * (base + tid), best, bi, sm, ss);
     }
     for (int ix = lo + N * n4 + tid; ix < hi; ix += kThreads) {
       const float f = Vec<TIn>::one(row, ix);

@@ -29,21 +29,31 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 // ------------------------------------------------------------------ snapshot (flat copy)
+// Each block copies one contiguous chunk of one of the two regions (blocks [0, nb0) the states, the
+// rest the windows), kCopyD 16-byte loads per thread in flight per step. Contiguous per-block chunks
+// stream about 17 % faster than a grid-stride copy at decode scale (1.6 GB of states).
+constexpr int kCopyD = 8;
+constexpr int kCopyStep = 256 * kCopyD;  // vectors per block step
+
 __global__ __launch_bounds__(256) void copy2_kernel(const u32x4* __restrict__ s0, u32x4* __restrict__ d0, int64_t n0,
-                                                    const u32x4* __restrict__ s1, u32x4* __restrict__ d1, int64_t n1) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  // 4 independent 16-byte copies in flight per thread per iteration
-  for (; i + 3 * stride < n0; i += 4 * stride) {
-    const u32x4 a = s0[i], b = s0[i + stride];
-    const u32x4 c = s0[i + 2 * stride], d = s0[i + 3 * stride];
-    d0[i] = a;
-    d0[i + stride] = b;
-    d0[i + 2 * stride] = c;
-    d0[i + 3 * stride] = d;
+                                                    const u32x4* __restrict__ s1, u32x4* __restrict__ d1, int64_t n1,
+                                                    int64_t chunk, int64_t nb0) {
+  const bool second = (int64_t)blockIdx.x >= nb0;  // block-uniform
+  const u32x4* __restrict__ s = second ? s1 : s0;
+  u32x4* __restrict__ d = second ? d1 : d0;
+  const int64_t n = second ? n1 : n0;
+  const int64_t b0 = (second ? (int64_t)blockIdx.x - nb0 : (int64_t)blockIdx.x) * chunk;
+  const int64_t b1 = min(n, b0 + chunk);  // b0 < n: the host sizes each region's blocks to it
+  for (int64_t base = b0; base < b1; base += kCopyStep) {
+    u32x4 a[kCopyD];
+#pragma unroll
+    for (int k = 0; k < kCopyD; ++k) a[k] = s[min(base + k * 256 + (int64_t)threadIdx.x, b1 - 1)];
+#pragma unroll
+    for (int k = 0; k < kCopyD; ++k) {
+      const int64_t j = base + k * 256 + threadIdx.x;
+      if (j < b1) d[j] = a[k];
+    }
   }
-  for (; i < n0; i += stride) d0[i] = s0[i];
-  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < n1; j += stride) d1[j] = s1[j];
 }
 
 // ------------------------------------------------------------------ restore: recurrent state
@@ -194,12 +204,15 @@ extern "C" int trida_gdn_snapshot(const float* state, float* snap_state, int64_t
               TRIDA_ERR_ALIGN, "gdn_snapshot: buffers must be 16-byte aligned");
   const int64_t n0 = state_elems / 4, n1 = window_elems / 8;
   if (n0 + n1 == 0) return TRIDA_OK;
-  // enough blocks for every CU, at most ~8 KiB per thread-row pass
-  int64_t blocks = cdiv(n0 > n1 ? n0 : n1, 256 * 4);
-  blocks = blocks < 1 ? 1 : (blocks > 4096 ? 4096 : blocks);
+  // chunks of 1..4 block steps: small copies keep many blocks in flight, large ones stream 128 KiB each
+  int64_t steps = cdiv(n0 + n1, (int64_t)kCopyStep * 1024);
+  steps = steps < 1 ? 1 : (steps > 4 ? 4 : steps);
+  const int64_t chunk = steps * kCopyStep;
+  const int64_t nb0 = cdiv(n0, chunk), blocks = nb0 + cdiv(n1, chunk);
+  TRIDA_CHECK(blocks <= INT32_MAX, TRIDA_ERR_ARG, "gdn_snapshot: too large");
   hipLaunchKernelGGL(copy2_kernel, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      reinterpret_cast<const u32x4*>(state), reinterpret_cast<u32x4*>(snap_state), n0,
-                     reinterpret_cast<const u32x4*>(window), reinterpret_cast<u32x4*>(snap_window), n1);
+                     reinterpret_cast<const u32x4*>(window), reinterpret_cast<u32x4*>(snap_window), n1, chunk, nb0);
   return launch_status("gdn_snapshot");
 }
 
