@@ -209,28 +209,31 @@ struct TruncArgs {
   int* passes_out;
 };
 
-// Value histogram of the streaming pass: 1024 bins of 1/16 nat over d = y - mref in (-24, 40]
+// Value histogram of the streaming pass: 2048 bins of 1/32 nat over d = y - mref in (-24, 40]
 // (mref = the sample max); bin 0 holds the largest values. Bin kNB is the spare bin: entries with
 // d <= -24, -inf entries, the banned id and padding lanes land there (its mass still counts towards
 // the total). d > 40 is caught afterwards from the row max and sends the row to the radix select.
 // Each bin is one 64-bit LDS word: the count in bits 46..63 and, below, the sum of r * 2^26 with
-// r = exp(d - top of the bin) in (e^-1/16, 1]: one integer LDS atomic per element (fp64 and fp32 LDS
+// r = exp(d - top of the bin) in (e^-1/32, 1]: one integer LDS atomic per element (fp64 and fp32 LDS
 // atomics measured several times slower on gfx950). Rows need V < 2^18 for the count field.
-constexpr int kNB = 1024;
+constexpr int kNB = 2048;
 constexpr float kTop = 40.f;
-constexpr float kPerNat = 16.f;
+constexpr float kPerNat = 32.f;
+constexpr double kBinRatio = 0x1.f03f56a88b5d8p-1;  // exp(-1 / kPerNat): the scale of bin b + 1 over bin b
 constexpr int kSeg = 4;  // the streaming pass re-places its collection window between segments
 constexpr int kCountShift = 46;
 constexpr unsigned long long kMassMask = (1ull << kCountShift) - 1ull;
 constexpr int kMaxPackedV = (1 << 18) - 1;
 
-// Bin of an element from its raw logit x: t = 16 (40 - d) with d = x / T - mref, as one fma whose
-// coefficients the block derives once (tA = -16 / T, tB = 16 (40 + mref)). Monotone in x.
+// Bin of an element from its raw logit x: t = 32 (40 - d) with d = x / T - mref, as one fma whose
+// coefficients the block derives once (tA = -32 / T, tB = 32 (40 + mref)). Monotone in x.
 __device__ __forceinline__ unsigned bin_of_t(float t) {
-  return min((unsigned)(int)__builtin_amdgcn_fmed3f(t, -1.f, 2048.f), (unsigned)kNB);
+  return min((unsigned)(int)__builtin_amdgcn_fmed3f(t, -1.f, (float)kNB), (unsigned)kNB);
 }
-__device__ __forceinline__ double bin_mass(unsigned long long h, int bin) {  // relative to exp(mref)
-  return ldexp((double)(h & kMassMask), -26) * exp((double)kTop - (double)bin / kPerNat);
+// exp(top of the bin) relative to exp(mref); consecutive bins scale by kBinRatio
+__device__ __forceinline__ double bin_scale(int bin) { return exp((double)kTop - (double)bin / kPerNat); }
+__device__ __forceinline__ double bin_mass(unsigned long long h, double scale) {  // relative to exp(mref)
+  return ldexp((double)(h & kMassMask), -26) * scale;
 }
 
 struct BinMap {  // the per-row coefficients of the element -> bin / exponent maps
@@ -614,11 +617,13 @@ __device__ void place_window(Shared& sh, bool use_k, float top_p, double k_seen,
   const int tid = threadIdx.x;
   double lm = 0.0, lc = 0.0;
   double bm[kBPT], bc[kBPT];
+  double sc = bin_scale(tid * kBPT);
 #pragma unroll
   for (int u = 0; u < kBPT; ++u) {
     const unsigned long long h = sh.hist[tid * kBPT + u];
     bc[u] = (double)(h >> kCountShift);
-    bm[u] = (double)(float)bin_mass(h, tid * kBPT + u);
+    bm[u] = (double)(float)bin_mass(h, sc);
+    sc *= kBinRatio;
     lm += bm[u];
     lc += bc[u];
   }
@@ -631,7 +636,7 @@ __device__ void place_window(Shared& sh, bool use_k, float top_p, double k_seen,
     sh.ipar[2] = -1;
   }
   __syncthreads();
-  const double tgt = use_k ? k_seen : (double)top_p * (zb + bin_mass(sh.hist[kNB], kNB));
+  const double tgt = use_k ? k_seen : (double)top_p * (zb + bin_mass(sh.hist[kNB], bin_scale(kNB)));
   double run = use_k ? exc : exm;
 #pragma unroll
   for (int u = 0; u < kBPT; ++u) {
@@ -789,18 +794,20 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
       constexpr int kBPT = kNB / kT;
       double lm = 0.0, lc = 0.0;
       double bms[kBPT], bcs[kBPT];
+      double sc = bin_scale(tid * kBPT);
 #pragma unroll
       for (int u = 0; u < kBPT; ++u) {
         const unsigned long long h = sh.hist[tid * kBPT + u];
         bcs[u] = (double)(h >> kCountShift);
-        bms[u] = bin_mass(h, tid * kBPT + u);
+        bms[u] = bin_mass(h, sc);
+        sc *= kBinRatio;
         lm += bms[u];
         lc += bcs[u];
       }
       double zb = 0.0, cbins = 0.0;
       const double exm = block_excl_scan(lm, sh.red, &zb);
       const double exc = block_excl_scan(lc, sh.red, &cbins);
-      const double Z = zb + bin_mass(sh.hist[kNB], kNB);
+      const double Z = zb + bin_mass(sh.hist[kNB], bin_scale(kNB));
       if (!collect) {
         zk = Z * scale;
       } else {
