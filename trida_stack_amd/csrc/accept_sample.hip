@@ -230,6 +230,10 @@ constexpr int kMaxPackedV = (1 << 18) - 1;
 __device__ __forceinline__ unsigned bin_of_t(float t) {
   return min((unsigned)(int)__builtin_amdgcn_fmed3f(t, -1.f, (float)kNB), (unsigned)kNB);
 }
+// c ? x : y on values: a conditional over two array elements (lvalues) selects their addresses, which
+// sends register arrays to scratch memory
+__device__ __forceinline__ double pick(bool c, double x, double y) { return c ? x : y; }
+
 // exp(top of the bin) relative to exp(mref); consecutive bins scale by kBinRatio
 __device__ __forceinline__ double bin_scale(int bin) { return exp((double)kTop - (double)bin / kPerNat); }
 __device__ __forceinline__ double bin_mass(unsigned long long h, double scale) {  // relative to exp(mref)
@@ -275,7 +279,7 @@ __device__ int count_below(const float* s, int lim, double m, double base, doubl
 }
 
 // sum over j < n with s_j >= thr of exp(s_j - m)
-__device__ double mass_at_least(const float* s, int n, float thr, double m, double* sh) {
+__device__ __forceinline__ double mass_at_least(const float* s, int n, float thr, double m, double* sh) {
   double loc = 0.0;
   for (int j = threadIdx.x; j < n; j += kT) loc += (s[j] >= thr) ? exp((double)s[j] - m) : 0.0;
   return block_sum(loc, sh);
@@ -485,7 +489,7 @@ __device__ void radix_resolve(const float* row, const TruncArgs& a, float m, boo
 // Keeps the collected logits whose bin lies in [lo, hi] and that came from a segment in the bit set
 // `segs` (entry j came from segment s when nseg[s-1] <= j < nseg[s]), packed at the front of
 // sh.coll; returns how many.
-__device__ int compact_bins(Shared& sh, const BinMap& bm, int n, int lo, int hi, unsigned segs) {
+__device__ __forceinline__ int compact_bins(Shared& sh, const BinMap& bm, int n, int lo, int hi, unsigned segs) {
   constexpr int kPer = kCap / kT;
   float v[kPer];
   bool kp[kPer];
@@ -640,7 +644,7 @@ __device__ void place_window(Shared& sh, bool use_k, float top_p, double k_seen,
   double run = use_k ? exc : exm;
 #pragma unroll
   for (int u = 0; u < kBPT; ++u) {
-    const double add = use_k ? bc[u] : bm[u];
+    const double add = pick(use_k, bc[u], bm[u]);
     if (run < tgt && run + add >= tgt) atomicMin(&sh.ipar[0], tid * kBPT + u);
     run += add;
   }
@@ -649,7 +653,8 @@ __device__ void place_window(Shared& sh, bool use_k, float top_p, double k_seen,
   if (B == INT_MAX) B = kNB - 1;
   if (tid == B / kBPT) {
     double c = exc;
-    for (int u = 0; u < B % kBPT; ++u) c += bc[u];
+#pragma unroll
+    for (int u = 0; u < kBPT; ++u) c += u < B % kBPT ? bc[u] : 0.0;  // unrolled: bc stays in registers
     sh.dpar[1] = c;                                                 // count above B
     sh.dpar[2] = (double)(sh.hist[B] >> kCountShift);                // count in B
   }
@@ -818,7 +823,7 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
         double run = use_k ? exc : exm;
 #pragma unroll
         for (int u = 0; u < kBPT; ++u) {
-          const double add = use_k ? bcs[u] : bms[u];
+          const double add = pick(use_k, bcs[u], bms[u]);
           if (run < tgt && run + add >= tgt) atomicMin(&sh.ipar[0], tid * kBPT + u);
           run += add;
         }
@@ -826,7 +831,8 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
         const int B = sh.ipar[0];
         if (B != INT_MAX && tid == B / kBPT) {  // the owner publishes the count / mass above the bin
           double cum = use_k ? exc : exm;
-          for (int u = 0; u < B % kBPT; ++u) cum += use_k ? bcs[u] : bms[u];
+#pragma unroll
+          for (int u = 0; u < kBPT; ++u) cum += u < B % kBPT ? pick(use_k, bcs[u], bms[u]) : 0.0;
           sh.dpar[0] = cum;
         }
         __syncthreads();
