@@ -92,11 +92,12 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t sVt[D * kKB];
   __shared__ __align__(16) uint16_t sP[kNW][kWR * kKB];
 
-  int idx = blockIdx.x;
-  const int s = idx % a.S;
-  idx /= a.S;
+  // query tiles of one (split, kv head) read the same keys: innermost, and on one XCD
+  int idx = xcd_major(blockIdx.x, gridDim.x);
   const int qt = idx % a.QT;
   idx /= a.QT;
+  const int s = idx % a.S;
+  idx /= a.S;
   const int hk = idx % a.Hkv;
   const int b = idx / a.Hkv;
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;

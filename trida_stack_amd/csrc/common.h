@@ -57,6 +57,15 @@ __device__ __forceinline__ void reset_counter(unsigned* counter) {
   __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin (block i runs on XCD i % 8), each XCD with its
+// own L2. xcd_major(i, n) renumbers the n blocks of a grid so that logical ids [x n/8, (x + 1) n/8)
+// all run on XCD x: neighbouring logical units, which read the same operands, then share one L2.
+// A bijection on [0, n); the identity unless n is a multiple of 8.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_major(int i, int n) {
+  return (n % kXcds) ? i : (i % kXcds) * (n / kXcds) + i / kXcds;
+}
+
 // ---------------------------------------------------------------- host error plumbing
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);

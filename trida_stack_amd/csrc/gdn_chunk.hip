@@ -701,7 +701,7 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_scan_kernel(ChunkArgs a) {
   using L = Lay<DK, 4, DVS>;
   __shared__ __align__(16) unsigned char smem[L::BYTES];
   const int slices = a.Dv / DVS;
-  int idx = blockIdx.x;
+  int idx = xcd_major(blockIdx.x, gridDim.x);  // a head's Dv slices (same chunk rows) on one XCD
   const int sl = idx % slices;
   idx /= slices;
   const int h = idx % a.Hv;
@@ -737,7 +737,7 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_fused_kernel(ChunkArgs a) {
   using L = Lay<DK, NB, DVS>;
   __shared__ __align__(16) unsigned char smem[L::BYTES];
   const int slices = a.Dv / DVS;
-  int idx = blockIdx.x;
+  int idx = xcd_major(blockIdx.x, gridDim.x);  // a head's Dv slices (same chunk rows) on one XCD
   const int sl = idx % slices;
   idx /= slices;
   const int h = idx % a.Hv;

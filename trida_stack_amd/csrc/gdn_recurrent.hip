@@ -154,9 +154,10 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   constexpr int Dk = KPL * kLanesPerV;
   constexpr int VPB = NW * kVPerWave;
   const int tiles = a.Dv / VPB;
-  const int vt = blockIdx.x % tiles;
-  const int h = (blockIdx.x / tiles) % a.Hv;
-  const int b = blockIdx.x / (tiles * a.Hv);
+  const int bid = xcd_major(blockIdx.x, gridDim.x);  // a head's value tiles (same q / k rows) on one XCD
+  const int vt = bid % tiles;
+  const int h = (bid / tiles) % a.Hv;
+  const int b = bid / (tiles * a.Hv);
   const int hk = h / (a.Hv / a.Hk);
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int vl = wave * kVPerWave + lane / kLanesPerV;  // value column within the tile

@@ -73,9 +73,11 @@ __global__ __launch_bounds__(NW* kWave) void restore_state_kernel(RestoreArgs a)
   constexpr int Dk = KPL * kLanesPerV;
   constexpr int VPB = NW * kVPerWave;
   const int tiles = a.Dv / VPB;
-  const int vt = blockIdx.x % tiles;
-  const int h = (blockIdx.x / tiles) % a.Hv;
-  const int b = blockIdx.x / (tiles * a.Hv);
+  // the value tiles of one head (which all read the head's k rows) run on one XCD
+  const int bid = xcd_major(blockIdx.x, gridDim.x);
+  const int vt = bid % tiles;
+  const int h = (bid / tiles) % a.Hv;
+  const int b = bid / (tiles * a.Hv);
   const int hk = h / (a.Hv / a.Hk);
   const int n = min(max(a.n_keep[b % a.seq_mod], 0), a.T);
   if (a.skip_full && n == a.T) return;  // the state already holds the whole block
