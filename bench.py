@@ -21,6 +21,27 @@ METRIC = "accepted tok/s (bs1, bs64) on 4B-shape hybrid; verify-step µs; % HBM 
 HBM_PEAK_GBS = 8000.0
 
 
+def _measured_traffic(*keys):
+    """HBM bytes per call: the sum over `keys` of the calibrated rocprofv3 FETCH_SIZE / WRITE_SIZE bytes
+    per dispatch in profiles/hbm_traffic.md (measured on MI355X by two counter passes over this
+    bench), or None when that table or a key is missing."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "hbm_traffic.md")
+    try:
+        with open(path) as f:
+            lines = f.read().splitlines()
+    except OSError:
+        return None
+    vals = {}
+    for ln in lines:
+        parts = [p.strip() for p in ln.split("|")]
+        if len(parts) > 6 and parts[5].isdigit():
+            vals[parts[1]] = int(parts[5])
+    try:
+        return sum(vals[k] for k in keys)
+    except KeyError:
+        return None
+
+
 def _events_time_ms(fn, iters: int) -> float:
     """Average ms per call of fn, from HIP events on the current stream, with the calls captured in
     one HIP graph so the launch gaps of a host loop do not count."""
@@ -93,7 +114,8 @@ def bench_accept(args):
         "config": {"workload": "greedy acceptance, batch 1, block 32, vocab 151936, ctx 4096",
                    "n_acc": n_acc},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _measured_traffic("accept_split_argmax", "accept_finalize")},
         "at_scale": at_scale,
         "cpu_baseline": cpu,
     }
@@ -195,7 +217,8 @@ def bench_sample(args):
                    "bytes_read": nbytes, "reference_bytes": ref_bytes,
                    "reference_equivalent_GBps": round(ref_bytes / (kern_ms * 1e-3) / 1e9, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _measured_traffic("sample_truncate_g0", "sample_truncate_g1", "sample_resid_sums")},
         "cpu_baseline": cpu,
     }
 
@@ -262,7 +285,8 @@ def bench_attn(args):
                    "draft_us": round(res["draft"][0] * 1e3, 2), "crop_us": round(crop_ms * 1e3, 2),
                    "tflops": round(flops / (kern_ms * 1e-3) / 1e12, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": _measured_traffic("attn_partial", "attn_combine")},
         "cpu_baseline": cpu,
     }
 
@@ -651,7 +675,8 @@ def bench_gdr(args):
                    "prefix_gflop": round(flops / 1e9, 3), "prefix_hbm_GBps": round(prefix_bytes / us["prefix"] / 1e3, 1),
                    "snapshot_GBps": round(snap_bytes / us["snapshot"] / 1e3, 1)},
         "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (prep + scan)", "achieved": round(tflops, 1),
-                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None},
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
+                     "traffic": _measured_traffic("gdr_chunk_prep", "gdr_chunk_scan")},
         "at_scale": _snapshot_restore_at_scale(dev, H, D, CH),
         "cpu_baseline": cpu,
     }
