@@ -54,16 +54,27 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, cons
   __shared__ float red[kThreads / kWave];
   const int64_t row = blockIdx.x;
   const int pieces = dim / 8;
+  // every load (x, residual, weight) is issued before the reduction: one memory round trip per row
+  u32x4 xr[kMaxPieces], rr[kMaxPieces], wr[kMaxPieces];
+#pragma unroll
+  for (int u = 0; u < kMaxPieces; ++u) {
+    const int p = threadIdx.x + u * kThreads;
+    if (p < pieces) {
+      xr[u] = *reinterpret_cast<const u32x4*>(x + row * x_st + p * 8);
+      if (r) rr[u] = *reinterpret_cast<const u32x4*>(r + row * r_st + p * 8);
+      wr[u] = *reinterpret_cast<const u32x4*>(w + p * 8);
+    }
+  }
   float v[kMaxPieces][8];
   float ss = 0.f;
 #pragma unroll
   for (int u = 0; u < kMaxPieces; ++u) {
     const int p = threadIdx.x + u * kThreads;
     if (p < pieces) {
-      unpack8(*reinterpret_cast<const u32x4*>(x + row * x_st + p * 8), v[u]);
+      unpack8(xr[u], v[u]);
       if (r) {
         float rv[8];
-        unpack8(*reinterpret_cast<const u32x4*>(r + row * r_st + p * 8), rv);
+        unpack8(rr[u], rv);
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[u][j] = bf2f(f2bf(v[u][j] + rv[j]));  // the residual stream is bf16
         *reinterpret_cast<u32x4*>(x + row * x_st + p * 8) = pack8(v[u]);
@@ -78,7 +89,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, cons
     const int p = threadIdx.x + u * kThreads;
     if (p < pieces) {
       float wv[8], y[8];
-      unpack8(*reinterpret_cast<const u32x4*>(w + p * 8), wv);
+      unpack8(wr[u], wv);
 #pragma unroll
       for (int j = 0; j < 8; ++j) y[j] = v[u][j] * inv * (zero_centred ? 1.f + wv[j] : wv[j]);
       *reinterpret_cast<u32x4*>(out + row * o_st + p * 8) = pack8(y);
@@ -112,19 +123,30 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
   const int64_t row = gw / H;
   const int h = (int)(gw % H);
   const int per = Dv / kWave;  // elements per lane (Dv in {64, 128, 256})
-  float v[4];
-  float ss = 0.f;
   const uint16_t* op = o + (row * H + h) * Dv + l * per;
-  for (int j = 0; j < per; ++j) {
-    v[j] = bf2f(op[j]);
-    ss = fmaf(v[j], v[j], ss);
-  }
-  const float inv = rsqrtf(wave_sum(ss) / Dv + eps);
   const uint16_t* zp = z + row * z_st + (int64_t)h * Dv + l * per;
+  // o, gate and weight are all loaded before the reduction: one memory round trip
+  float v[4], zv[4], wv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j < per) {
+      v[j] = bf2f(op[j]);
+      zv[j] = bf2f(zp[j]);
+      wv[j] = bf2f(w[l * per + j]);
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (j < per) ss = fmaf(v[j], v[j], ss);
+  const float inv = rsqrtf(wave_sum(ss) / Dv + eps);
   uint16_t* dst = out + (row * H + h) * Dv + l * per;
-  for (int j = 0; j < per; ++j) {
-    const float nrm = bf2f(f2bf(v[j] * inv));  // normalised value in the input dtype, then weight and gate
-    dst[j] = f2bf(nrm * bf2f(w[l * per + j]) * silu(bf2f(zp[j])));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j < per) {
+      const float nrm = bf2f(f2bf(v[j] * inv));  // normalised value in the input dtype, then weight and gate
+      dst[j] = f2bf(nrm * wv[j] * silu(zv[j]));
+    }
   }
 }
 
@@ -169,8 +191,12 @@ __global__ __launch_bounds__(kThreads) void attn_prep_kernel(AttnPrepArgs a) {
     h = hh - a.Hq - a.Hkv;
     src = row + (int64_t)a.Hq * 2 * a.D + (int64_t)a.Hkv * a.D + (int64_t)h * a.D;
   }
-  float v[kMaxPer];
-  for (int j = 0; j < per; ++j) v[j] = bf2f(src[l * per + j]);
+  float v[kMaxPer], wnv[kMaxPer];
+  const uint16_t* wn = kind == 0 ? a.qn_w : a.kn_w;  // loaded with the row: one memory round trip
+  for (int j = 0; j < per; ++j) {
+    v[j] = bf2f(src[l * per + j]);
+    wnv[j] = bf2f(wn[l * per + j]);
+  }
   const int64_t slot = (int64_t)a.slot0[bb] + t;
   if (kind == 2) {
     uint16_t* dst = a.v_cache + (((int64_t)bb * a.Hkv + h) * a.Lmax + slot) * a.D + l * per;
@@ -180,8 +206,7 @@ __global__ __launch_bounds__(kThreads) void attn_prep_kernel(AttnPrepArgs a) {
   float ss = 0.f;
   for (int j = 0; j < per; ++j) ss = fmaf(v[j], v[j], ss);
   const float inv = rsqrtf(wave_sum(ss) / a.D + a.eps);
-  const uint16_t* wn = kind == 0 ? a.qn_w : a.kn_w;
-  for (int j = 0; j < per; ++j) v[j] = bf2f(f2bf(v[j] * inv * (1.f + bf2f(wn[l * per + j]))));
+  for (int j = 0; j < per; ++j) v[j] = bf2f(f2bf(v[j] * inv * (1.f + wnv[j])));
   // partial rotary (rotate-half over the first `rot` dims): x1 = [0, rot/2), x2 = [rot/2, rot).
   // half is a multiple of the per-lane width, so a lane's partner values sit in one other lane.
   const int half = a.rot / 2;
