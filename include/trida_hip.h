@@ -118,6 +118,25 @@ int trida_truncated_probs(const float* logits, int64_t B, int64_t R, int64_t V, 
                           const double* zk, float* probs, int64_t out_batch_stride, int64_t out_row_stride,
                           void* stream);
 
+/* Row-mapped truncated distributions: for sequence b and j < K, row out_rows[b*K + j] of probs[b] (Ro
+ * rows) = P of logits row in_rows[b*K + j] (R rows; its statistics at [b, in_rows[b*K + j]]). It writes
+ * the q rows of the slots a draft pass unmasks straight from the pass's rows (the q-row write of the draft
+ * proposal, qwen3_5_diffusion.py:250-285; decode.py:376-378 keeps the P rows as q) in one launch. An index
+ * outside its range skips that row (the maps are device data). */
+int trida_truncated_probs_rows(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                               int64_t row_stride, float temperature, int64_t ban_id, const float* m,
+                               const float* thr, const double* zk, const int64_t* in_rows, const int64_t* out_rows,
+                               int64_t K, float* probs, int64_t Ro, int64_t out_batch_stride,
+                               int64_t out_row_stride, void* stream);
+
+/* dst[b, k, :] = fp32(src[b, rows[b*K + k], :]) for bf16 (dtype 1) or fp32 (dtype 0) logits [B, R, V]:
+ * the still-masked rows of a draft pass's logits (the rows the draft proposal reads,
+ * qwen3_5_diffusion.py:250-285) gathered and widened in one pass. A row index outside [0, R) skips that
+ * row. */
+int trida_gather_rows(const void* src, int dtype, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                      int64_t row_stride, const int64_t* rows, int64_t K, float* dst, int64_t out_batch_stride,
+                      int64_t out_row_stride, void* stream);
+
 /* Draws one token per row from the truncated distribution of statistics (m, thr, zk) given by
  * trida_truncate_stats: the inverse CDF in vocabulary order of P(x) = [y_x >= thr] exp(y_x - m) / zk at
  * u[r] (token = min{x : cdf(x) > u * total}), the draw the sampled acceptance makes for its bonus token.

@@ -119,6 +119,46 @@ def test_truncated_probs(gpu):
         assert (P[..., 3] == 0).all()
 
 
+@pytest.mark.parametrize("V", [3000, 3001])
+def test_truncated_probs_rows_equals_gather_then_scatter(gpu, V):
+    """Row-mapped P rows (vector path V % 4 == 0, scalar otherwise) == truncated_probs of the gathered
+    rows, written at the mapped output rows, bit for bit; other rows and out-of-range indices untouched."""
+    rng = np.random.default_rng(3)
+    B, R, Ro, T = 3, 5, 7, 0.8
+    x = torch.from_numpy((rng.normal(size=(B, R, V)) * 3).astype(np.float32)).to(DEV)
+    stats = TK.truncate_stats(x, temperature=T, top_k=0, top_p=0.9, ban_id=2)[:3]
+    full = TK.truncated_probs(x, stats, temperature=T, ban_id=2)
+    in_rows = torch.tensor([[4, 0], [1, 1], [2, R]], dtype=torch.int64, device=DEV)  # (2, 1) out of range
+    out_rows = torch.tensor([[6, 2], [0, 5], [3, 4]], dtype=torch.int64, device=DEV)
+    out = torch.full((B, Ro, V), -1.0, device=DEV)
+    TK.truncated_probs_rows(x, stats, in_rows, out_rows, out, temperature=T, ban_id=2)
+    ref = torch.full_like(out, -1.0)
+    for b in range(B):
+        for j in range(2):
+            i, o = int(in_rows[b, j]), int(out_rows[b, j])
+            if i < R:
+                ref[b, o] = full[b, i]
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.bfloat16, 4096), (torch.bfloat16, 4099), (torch.float32, 4096),
+                                     (torch.float32, 4099)])
+def test_gather_rows_widens_exactly(gpu, dtype, V):
+    g = torch.Generator(device=DEV).manual_seed(4)
+    B, R, Kr = 2, 6, 4
+    src = torch.randn(B, R, V, generator=g, device=DEV).to(dtype)
+    rows = torch.tensor([[5, 0, 3, 3], [1, 6, 2, -1]], dtype=torch.int64, device=DEV)  # 6 and -1 skip
+    out = torch.full((B, Kr, V), 7.0, device=DEV)
+    TK.gather_rows(src, rows, out=out)
+    ref = torch.full_like(out, 7.0)
+    for b in range(B):
+        for k in range(Kr):
+            i = int(rows[b, k])
+            if 0 <= i < R:
+                ref[b, k] = src[b, i].float()
+    assert torch.equal(out, ref)
+
+
 def make_case(seed, B, K, V, T, k, p, accept_bias=2.0):
     """Verify logits and draft distributions q that overlap P (so drafts are often accepted)."""
     rng = np.random.default_rng(seed)

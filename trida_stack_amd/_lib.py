@@ -38,6 +38,9 @@ SIGNATURES = {
     "trida_sample_rows_scratch_bytes": (I64, [I64, I64]),
     "trida_sample_rows": (C.c_int, [P, I64, I64, I64, F32, I64, P, P, P, P, P, P, I64, P]),
     "trida_truncated_probs": (C.c_int, [P, I64, I64, I64, I64, I64, F32, I64, P, P, P, P, I64, I64, P]),
+    "trida_truncated_probs_rows": (C.c_int, [P, I64, I64, I64, I64, I64, F32, I64, P, P, P, P, P, I64, P, I64, I64,
+                                             I64, P]),
+    "trida_gather_rows": (C.c_int, [P, C.c_int, I64, I64, I64, I64, I64, P, I64, P, I64, I64, P]),
     "trida_skinny_gemm_scratch_bytes": (I64, [I64, I64, I64, I64]),
     "trida_skinny_gemm": (C.c_int, [P, I64, P, I64, P, I64, I64, I64, I64, P, I64, I64, P]),
     "trida_add_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, I64, F32, C.c_int, P]),

@@ -1315,8 +1315,150 @@ __global__ __launch_bounds__(256) void probs_kernel(const float* logits, int64_t
     o[ix] = (y > -INFINITY && y >= t) ? __expf(y - mm) * inv : 0.f;
   }
 }
+// Row-mapped form: out row out_rows[b K + j] of sequence b = P of logits row in_rows[b K + j] (whose
+// statistics are at [b, in_rows[..]]). An index outside its range skips the row: the maps are device
+// data the host cannot check. Four elements per thread per step (16-byte loads and stores) when vec.
+template <bool kVec>
+__global__ __launch_bounds__(256) void probs_rows_kernel(const float* logits, int64_t bs, int64_t rs, int R, int V,
+                                                         double rt, int ban, const float* m, const float* thr,
+                                                         const double* zk, const int64_t* in_rows,
+                                                         const int64_t* out_rows, int K, int Ro, float* out,
+                                                         int64_t obs, int64_t ors) {
+  const int r = blockIdx.y;
+  const int b = r / K;
+  const int64_t i = in_rows[r], o = out_rows[r];
+  if (i < 0 || i >= R || o < 0 || o >= Ro) return;  // block-uniform
+  const float* row = logits + (int64_t)b * bs + i * rs;
+  float* dst = out + (int64_t)b * obs + o * ors;
+  const int64_t si = (int64_t)b * R + i;
+  const float mm = m[si], t = thr[si];
+  const float inv = (float)(1.0 / zk[si]);
+  auto p_of = [&](float x, int ix) {
+    const float y = make_y<true>(x, ix, rt, ban);
+    return (y > -INFINITY && y >= t) ? __expf(y - mm) * inv : 0.f;
+  };
+  if (kVec) {
+    const int n4 = V >> 2;
+    for (int j = blockIdx.x * 256 + threadIdx.x; j < n4; j += gridDim.x * 256) {
+      const u32x4 w = reinterpret_cast<const u32x4*>(row)[j];
+      float4 y;
+      y.x = p_of(__uint_as_float(w.x), 4 * j);
+      y.y = p_of(__uint_as_float(w.y), 4 * j + 1);
+      y.z = p_of(__uint_as_float(w.z), 4 * j + 2);
+      y.w = p_of(__uint_as_float(w.w), 4 * j + 3);
+      reinterpret_cast<float4*>(dst)[j] = y;
+    }
+  } else {
+    for (int ix = blockIdx.x * 256 + threadIdx.x; ix < V; ix += gridDim.x * 256) dst[ix] = p_of(row[ix], ix);
+  }
+}
+
+// dst[b, k, :] = fp32(src[b, rows[b, k], :]) for bf16 (kBf16) or fp32 sources; a row index outside
+// [0, R) skips the row. 16-byte loads and stores when vec (8 bf16 or 4 fp32 elements a load).
+template <bool kBf16, bool kVec>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const void* src, int64_t sbs, int64_t srs, int R, int V,
+                                                          const int64_t* rows, int K, float* dst, int64_t dbs,
+                                                          int64_t drs) {
+  const int r = blockIdx.y;
+  const int b = r / K, k = r % K;
+  const int64_t i = rows[r];
+  if (i < 0 || i >= R) return;  // block-uniform
+  float* d = dst + (int64_t)b * dbs + (int64_t)k * drs;
+  const int64_t off = (int64_t)b * sbs + i * srs;
+  if (kBf16) {
+    const uint16_t* s = static_cast<const uint16_t*>(src) + off;
+    if (kVec) {
+      for (int j = blockIdx.x * 256 + threadIdx.x; j < (V >> 3); j += gridDim.x * 256) {
+        const u32x4 w = reinterpret_cast<const u32x4*>(s)[j];
+        float4 lo, hi;
+        lo.x = __uint_as_float(w.x << 16);
+        lo.y = __uint_as_float(w.x & 0xffff0000u);
+        lo.z = __uint_as_float(w.y << 16);
+        lo.w = __uint_as_float(w.y & 0xffff0000u);
+        hi.x = __uint_as_float(w.z << 16);
+        hi.y = __uint_as_float(w.z & 0xffff0000u);
+        hi.z = __uint_as_float(w.w << 16);
+        hi.w = __uint_as_float(w.w & 0xffff0000u);
+        reinterpret_cast<float4*>(d)[2 * j] = lo;
+        reinterpret_cast<float4*>(d)[2 * j + 1] = hi;
+      }
+    } else {
+      for (int ix = blockIdx.x * 256 + threadIdx.x; ix < V; ix += gridDim.x * 256) d[ix] = bf2f(s[ix]);
+    }
+  } else {
+    const float* s = static_cast<const float*>(src) + off;
+    if (kVec) {
+      for (int j = blockIdx.x * 256 + threadIdx.x; j < (V >> 2); j += gridDim.x * 256)
+        reinterpret_cast<float4*>(d)[j] = reinterpret_cast<const float4*>(s)[j];
+    } else {
+      for (int ix = blockIdx.x * 256 + threadIdx.x; ix < V; ix += gridDim.x * 256) d[ix] = s[ix];
+    }
+  }
+}
 }  // namespace
 }  // namespace trida
+
+extern "C" int trida_truncated_probs_rows(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                                          int64_t row_stride, float temperature, int64_t ban_id, const float* m,
+                                          const float* thr, const double* zk, const int64_t* in_rows,
+                                          const int64_t* out_rows, int64_t K, float* probs, int64_t Ro,
+                                          int64_t out_batch_stride, int64_t out_row_stride, void* stream) {
+  TRIDA_CHECK(logits && m && thr && zk && in_rows && out_rows && probs, TRIDA_ERR_NULL, "null pointer argument");
+  TRIDA_CHECK(B > 0 && R > 0 && K >= 0 && Ro > 0 && B * K <= 65535 && V > 0 && V < INT_MAX / 2, TRIDA_ERR_ARG,
+              "bad shape");
+  TRIDA_CHECK(temperature > 0.f && temperature < INFINITY, TRIDA_ERR_ARG, "temperature must be positive");
+  TRIDA_CHECK(row_stride >= V && out_row_stride >= V &&
+                  (B == 1 || (batch_stride >= (R - 1) * row_stride + V &&
+                              out_batch_stride >= (Ro - 1) * out_row_stride + V)),
+              TRIDA_ERR_ARG, "strides too small");
+  if (K == 0) return TRIDA_OK;
+  const bool vec = V % 4 == 0 && row_stride % 4 == 0 && batch_stride % 4 == 0 && out_row_stride % 4 == 0 &&
+                   out_batch_stride % 4 == 0 && (((uintptr_t)logits | (uintptr_t)probs) & 15) == 0;
+  const int gx = (int)std::min<int64_t>(cdiv(V, 256 * (vec ? 4 : 1)), 256);
+  const dim3 grid(gx, (unsigned)(B * K));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (vec)
+    hipLaunchKernelGGL((probs_rows_kernel<true>), grid, dim3(256), 0, st, logits, batch_stride, row_stride, (int)R,
+                       (int)V, 1.0 / (double)temperature, ban_of(ban_id, V), m, thr, zk, in_rows, out_rows, (int)K,
+                       (int)Ro, probs, out_batch_stride, out_row_stride);
+  else
+    hipLaunchKernelGGL((probs_rows_kernel<false>), grid, dim3(256), 0, st, logits, batch_stride, row_stride, (int)R,
+                       (int)V, 1.0 / (double)temperature, ban_of(ban_id, V), m, thr, zk, in_rows, out_rows, (int)K,
+                       (int)Ro, probs, out_batch_stride, out_row_stride);
+  return launch_status("probs_rows_kernel");
+}
+
+extern "C" int trida_gather_rows(const void* src, int dtype, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                                 int64_t row_stride, const int64_t* rows, int64_t K, float* dst,
+                                 int64_t out_batch_stride, int64_t out_row_stride, void* stream) {
+  TRIDA_CHECK(src && rows && dst, TRIDA_ERR_NULL, "null pointer argument");
+  TRIDA_CHECK(dtype == 0 || dtype == 1, TRIDA_ERR_ARG, "dtype must be 0 (fp32) or 1 (bf16)");
+  TRIDA_CHECK(B > 0 && R > 0 && K >= 0 && B * K <= 65535 && V > 0 && V < INT_MAX / 2, TRIDA_ERR_ARG, "bad shape");
+  TRIDA_CHECK(row_stride >= V && out_row_stride >= V &&
+                  (B == 1 || (batch_stride >= (R - 1) * row_stride + V &&
+                              out_batch_stride >= (K - 1) * out_row_stride + V)),
+              TRIDA_ERR_ARG, "strides too small");
+  if (K == 0) return TRIDA_OK;
+  const int e = dtype == 1 ? 8 : 4;  // elements per 16-byte load
+  const bool vec = V % e == 0 && row_stride % e == 0 && batch_stride % e == 0 && out_row_stride % 4 == 0 &&
+                   out_batch_stride % 4 == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15) == 0;
+  const int gx = (int)std::min<int64_t>(cdiv(V, 256 * (vec ? e : 1)), 256);
+  const dim3 grid(gx, (unsigned)(B * K));
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == 1 && vec)
+    hipLaunchKernelGGL((gather_rows_kernel<true, true>), grid, dim3(256), 0, st, src, batch_stride, row_stride, (int)R,
+                       (int)V, rows, (int)K, dst, out_batch_stride, out_row_stride);
+  else if (dtype == 1)
+    hipLaunchKernelGGL((gather_rows_kernel<true, false>), grid, dim3(256), 0, st, src, batch_stride, row_stride,
+                       (int)R, (int)V, rows, (int)K, dst, out_batch_stride, out_row_stride);
+  else if (vec)
+    hipLaunchKernelGGL((gather_rows_kernel<false, true>), grid, dim3(256), 0, st, src, batch_stride, row_stride,
+                       (int)R, (int)V, rows, (int)K, dst, out_batch_stride, out_row_stride);
+  else
+    hipLaunchKernelGGL((gather_rows_kernel<false, false>), grid, dim3(256), 0, st, src, batch_stride, row_stride,
+                       (int)R, (int)V, rows, (int)K, dst, out_batch_stride, out_row_stride);
+  return launch_status("gather_rows_kernel");
+}
 
 extern "C" int trida_truncated_probs(const float* logits, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
                                      int64_t row_stride, float temperature, int64_t ban_id, const float* m,

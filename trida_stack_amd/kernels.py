@@ -215,6 +215,55 @@ def truncated_probs(logits: torch.Tensor, stats, *, temperature: float, ban_id: 
     return out
 
 
+def truncated_probs_rows(logits: torch.Tensor, stats, in_rows: torch.Tensor, out_rows: torch.Tensor, out: torch.Tensor,
+                         *, temperature: float, ban_id: int = -1) -> torch.Tensor:
+    """out[b, out_rows[b, j]] = truncated distribution of logits[b, in_rows[b, j]] (stats of
+    ``truncate_stats`` over logits [B, R, V] fp32), for j < K; out [B, Ro, V] fp32. One launch for the
+    gather / truncated_probs / scatter that keeps a draft pass's unmasked slots' q rows. Indices outside
+    [0, R) / [0, Ro) skip their row."""
+    dev = _need_gpu(logits, in_rows, out_rows, out)
+    _f32_rows(logits, "logits")
+    _f32_rows(out, "out")
+    B, R, V = logits.shape
+    m, thr, zk = stats[0], stats[1], stats[2]
+    for t, dt in ((m, torch.float32), (thr, torch.float32), (zk, torch.float64)):
+        if t.dtype != dt or t.shape != (B, R) or not t.is_contiguous():
+            raise ValueError("stats must be the (m, thr, zk) tensors of truncate_stats for these logits")
+    for t, n in ((in_rows, "in_rows"), (out_rows, "out_rows")):
+        if t.dtype != torch.int64 or t.dim() != 2 or t.shape[0] != B or not t.is_contiguous():
+            raise ValueError(f"{n} must be int64 [B, K] contiguous")
+    if in_rows.shape != out_rows.shape or out.shape[0] != B or out.shape[2] != V:
+        raise ValueError("in_rows / out_rows / out shapes disagree")
+    rc = _lib.load().trida_truncated_probs_rows(
+        logits.data_ptr(), B, R, V, logits.stride(0), logits.stride(1), float(temperature), int(ban_id),
+        m.data_ptr(), thr.data_ptr(), zk.data_ptr(), in_rows.data_ptr(), out_rows.data_ptr(), in_rows.shape[1],
+        out.data_ptr(), out.shape[1], out.stride(0), out.stride(1), _stream(dev))
+    _lib.check(rc, "trida_truncated_probs_rows")
+    return out
+
+
+def gather_rows(src: torch.Tensor, rows: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[b, k] = fp32(src[b, rows[b, k]]) for src [B, R, V] bf16 or fp32 (contiguous last dim), rows int64
+    [B, K]: a row gather and the widening to fp32 in one pass. Indices outside [0, R) skip their row."""
+    dev = _need_gpu(src, rows, out)
+    dt = _logit_dtype(src)
+    if src.dim() != 3 or src.stride(2) != 1:
+        raise ValueError("src must be [B, R, V] with a contiguous last dim")
+    B, R, V = src.shape
+    if rows.dtype != torch.int64 or rows.dim() != 2 or rows.shape[0] != B or not rows.is_contiguous():
+        raise ValueError("rows must be int64 [B, K] contiguous")
+    K_ = rows.shape[1]
+    if out is None:
+        out = torch.empty((B, K_, V), dtype=torch.float32, device=dev)
+    _f32_rows(out, "out")
+    if out.shape != (B, K_, V):
+        raise ValueError("out must be [B, K, V] fp32")
+    rc = _lib.load().trida_gather_rows(src.data_ptr(), dt, B, R, V, src.stride(0), src.stride(1), rows.data_ptr(),
+                                       K_, out.data_ptr(), out.stride(0), out.stride(1), _stream(dev))
+    _lib.check(rc, "trida_gather_rows")
+    return out
+
+
 def sample_rows(logits: torch.Tensor, stats, u: torch.Tensor, *, temperature: float, ban_id: int = -1,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One token per row of logits [..., V] fp32 (contiguous rows) from the truncated distribution of

@@ -215,7 +215,6 @@ class SampledBlockSpecStep:
         self.out = (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
                     torch.empty(B, dtype=torch.int64, device=dev), None, torch.empty(B, dtype=torch.int32, device=dev))
         self.lf = torch.empty(B * block * V, dtype=torch.float32, device=dev)   # masked draft rows, fp32
-        self.pt = torch.empty(B * max(self.per) * V, dtype=torch.float32, device=dev)  # unmasked slots' P
         self.q = torch.zeros(B, block, V, dtype=torch.float32, device=dev)       # q row per draft slot
         self.pf = torch.empty(B, block + 1, V, dtype=torch.float32, device=dev)  # verify rows
         self.trace: Optional[list] = None
@@ -239,27 +238,26 @@ class SampledBlockSpecStep:
             L = rt.forward(self.canvas, cache, "draft")
             # the still-masked slots in ascending order (every sequence has `left` of them); row s of the
             # draft logits predicts slot s (shift readout)
-            midx = torch.sort(self.masked.to(torch.int8), dim=1, descending=True, stable=True).indices[:, :left]
+            midx = torch.sort(self.masked.to(torch.int8), dim=1, descending=True,
+                              stable=True).indices[:, :left].contiguous()
             lf = self.lf[: B * left * V].view(B, left, V)
             with K.timed("draft_sample"):
-                lf.copy_(L.gather(1, midx[:, :, None].expand(B, left, V)))
+                K.gather_rows(L, midx, out=lf)                           # gather + widen in one pass
                 st = smp.stats(lf)
                 u = smp.uniform(B * left)
                 x = smp.draw_given(lf, st, u)                            # [B, left]
                 conf = smp.prob_of(lf, st, x)
             # the per[p] most probable draws (ties: the lower slot first)
             k = self.per[p]
-            sel = torch.sort(conf, dim=1, descending=True, stable=True).indices[:, :k]
+            sel = torch.sort(conf, dim=1, descending=True, stable=True).indices[:, :k].contiguous()
             slots = midx.gather(1, sel)
             if self.trace is not None:
                 self.trace.append({"lf": lf.clone(), "u": u.clone(), "x": x.clone(), "midx": midx.clone(),
                                    "slots": slots.clone()})
             self.canvas.scatter_(1, slots + 1, x.gather(1, sel))
             self.masked.scatter_(1, slots, False)
-            with K.timed("draft_q"):
-                lq = lf.gather(1, sel[:, :, None].expand(B, k, V))
-                P = smp.probs(lq, tuple(t.gather(1, sel) for t in st), out=self.pt[: B * k * V].view(B, k, V))
-                self.q.scatter_(1, slots[:, :, None].expand(B, k, V), P)
+            with K.timed("draft_q"):  # q[slot] = P of the drawn row, read and written in place
+                K.truncated_probs_rows(lf, st, sel, slots, self.q, temperature=smp.T, ban_id=smp.ban)
             left -= k
         vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
