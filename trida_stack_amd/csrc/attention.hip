@@ -216,6 +216,9 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     stage_step();
     __syncthreads();
     if (kb + 1 < kb1) load_step(kb + 1);  // in flight during this step's MFMAs
+    // a wave with no row of the tile (the last tile of a canvas, e.g. rows 128..131 of 33 x 4) only helps
+    // stage the keys: its fragment reads and MFMAs would be on padding (wave-uniform; no barrier inside)
+    if (w * kWR >= rows) continue;
     // ---- S = Q K^T: this wave's 16 rows x 64 keys (4 key tiles)
     f32x4 sacc[4];
 #pragma unroll
@@ -394,15 +397,17 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
       u32x2{(uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16), (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16)};
 }
 
-// Splits per (sequence, KV head, query tile): enough workgroups to cover the CUs (~512 in all), but
-// at least 4 key blocks per split so one split's O partial (rows x D fp32) stays small next to the
-// keys it reads.
+// Splits per (sequence, KV head, query tile): as many as keep the grid within one workgroup per CU
+// (a workgroup holds a CU's LDS), at least one key block each. Measured at batch 1 (33 canvas rows,
+// 16 / 4 heads, d 256): 2200 keys 30.0 -> 25 us, 8192 keys 54.2 -> 40 us against splits of >= 4 key
+// blocks; a grid just past the CU count (33 splits) runs a ragged second round and is slower. At
+// batch 64 one split per query tile is best (the grid already exceeds the CUs).
+constexpr int64_t kCUs = 256;
 int64_t plan_splits(int64_t B, int64_t Hkv, int64_t QT, int64_t max_keys, int64_t splits) {
   if (splits > 0) return splits;
   const int64_t nblk = cdiv(max_keys, kKB);
-  int64_t s = cdiv(512, B * Hkv * QT);
-  const int64_t by_len = cdiv(nblk, 4);
-  if (s > by_len) s = by_len;
+  int64_t s = kCUs / (B * Hkv * QT);
+  if (s > nblk) s = nblk;
   if (s > kMaxSplits) s = kMaxSplits;
   return s < 1 ? 1 : s;
 }
