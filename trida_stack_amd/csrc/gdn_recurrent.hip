@@ -169,6 +169,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   __shared__ __align__(16) uint16_t s_v[kTC][VPB];
   __shared__ float s_g[kTC], s_b[kTC];
   __shared__ float s_ob[kTC][VPB];  // backward sub-scan outputs of the block-bidirectional readout
+  __shared__ float s_kq[kTC];  // k . (q * scale) per staged row
 
   const int64_t st_off = (((int64_t)b * a.Hv + h) * a.Dv + v) * Dk + kl * KPL;
   float s[KPL];
@@ -196,20 +197,18 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       qq[i] = bf2f(s_q[r][kl * KPL + i]) * a.scale;
     }
     const float eg = s_g[r];
-    float kv = 0.f, sq = 0.f, kq = 0.f;
+    float kv = 0.f, sq = 0.f;
 #pragma unroll
     for (int i = 0; i < KPL; ++i) {
       st[i] *= eg;
       kv = fmaf(st[i], kk[i], kv);
       sq = fmaf(st[i], qq[i], sq);
-      kq = fmaf(kk[i], qq[i], kq);
     }
     row16_sum2(kv, sq);
-    kq = row16_sum(kq);
     const float delta = (bf2f(s_v[r][vl]) - kv) * s_b[r];
 #pragma unroll
     for (int i = 0; i < KPL; ++i) st[i] = fmaf(kk[i], delta, st[i]);
-    return fmaf(delta, kq, sq);
+    return fmaf(delta, s_kq[r], sq);
   };
   if constexpr (PREP) {
     // ---- front half: conv + SiLU + l2norm + gates for this block's head, all T (<= kTC) rows ----
@@ -335,7 +334,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   // a row's operands in registers, and the step on them (the same arithmetic as step())
   struct Row {
     float kk[KPL], qq[KPL];
-    float eg, vv, be;
+    float eg, vv, be, kq;
   };
   auto fetch = [&](Row& R, int r) {
 #pragma unroll
@@ -346,22 +345,21 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     R.eg = s_g[r];
     R.vv = bf2f(s_v[r][vl]);
     R.be = s_b[r];
+    R.kq = s_kq[r];
   };
   auto apply = [&](float (&st)[KPL], const Row& R) -> float {
-    float kv = 0.f, sq = 0.f, kq = 0.f;
+    float kv = 0.f, sq = 0.f;
 #pragma unroll
     for (int i = 0; i < KPL; ++i) {
       st[i] *= R.eg;
       kv = fmaf(st[i], R.kk[i], kv);
       sq = fmaf(st[i], R.qq[i], sq);
-      kq = fmaf(R.kk[i], R.qq[i], kq);
     }
     row16_sum2(kv, sq);
-    kq = row16_sum(kq);
     const float delta = (R.vv - kv) * R.be;
 #pragma unroll
     for (int i = 0; i < KPL; ++i) st[i] = fmaf(R.kk[i], delta, st[i]);
-    return fmaf(delta, kq, sq);
+    return fmaf(delta, R.kq, sq);
   };
   for (int t0 = 0; t0 < a.T; t0 += tcn) {
     const int tn = min(tcn, a.T - t0);
@@ -391,6 +389,19 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     }
     __syncthreads();
     }
+    // k . (q * scale) of every staged row, once per block instead of once per value column: each
+    // 16-lane group takes a row, lane j the same KPL-element slice and fma order as the column lanes'
+    // row step, then the same row16_sum, so the value is the one a row step would compute itself
+    for (int rr = tid / kLanesPerV; rr < tn; rr += NW * kVPerWave) {  // uniform within a 16-lane group
+      const int j = tid % kLanesPerV;
+      float kq = 0.f;
+#pragma unroll
+      for (int i = 0; i < KPL; ++i)
+        kq = fmaf(bf2f(s_k[rr][j * KPL + i]), bf2f(s_q[rr][j * KPL + i]) * a.scale, kq);
+      kq = row16_sum(kq);
+      if (j == 0) s_kq[rr] = kq;
+    }
+    __syncthreads();
     if (a.bidir > 0) {
       // each block: a backward sub-scan from the block-entry state (a register copy), then the causal
       // forward sub-scan; a row reads out the mean of the two
