@@ -31,7 +31,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+  // update_dpp with a defined old value and bound_ctrl: folds into the consuming add / max
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float row16_max(float v) {
   v = fmaxf(v, dpp<0x128>(v));

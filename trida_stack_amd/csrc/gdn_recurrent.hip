@@ -29,9 +29,12 @@ constexpr int kLanesPerV = 16;
 constexpr int kVPerWave = kWave / kLanesPerV;  // 4
 constexpr int kTC = 64;                        // rows staged per LDS chunk (a canvas block fits in one)
 
+// A DPP lane permutation within 16-lane rows (row_ror and quad_perm read lanes of the same row only).
+// Written as update_dpp with a defined old value and bound_ctrl so that the compiler folds it into the
+// consuming add (v_add_f32 with a DPP source: one instruction instead of a mov and an add).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 // Sum over the 16 lanes of a DPP row; every lane of the row receives the total.
 __device__ __forceinline__ float row16_sum(float v) {

@@ -18,7 +18,8 @@ constexpr int kTC = 32;
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, false));
+  // update_dpp with a defined old value and bound_ctrl: folds into the consuming add / max
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float row16_sum(float v) {
   v += dpp<0x128>(v);
