@@ -257,11 +257,14 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
       moved |= alpha[i] != 1.f;
       float ps = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const float p = exp2f(sacc[kt][i] - m_use);
-        ps += p;
-        const int kk = kt * 16 + (l % 16);
-        pw[p_off(rr, kk >> 3) + (kk & 7)] = f2bf(p);
+      for (int kt = 0; kt < 4; kt += 2) {  // two key tiles per packed conversion
+        const float p0 = exp2f(sacc[kt][i] - m_use), p1 = exp2f(sacc[kt + 1][i] - m_use);
+        ps += p0;
+        ps += p1;
+        const uint32_t w2 = f2bf2(p0, p1);
+        const int k0 = kt * 16 + (l % 16), k1 = k0 + 16;
+        pw[p_off(rr, k0 >> 3) + (k0 & 7)] = (uint16_t)w2;
+        pw[p_off(rr, k1 >> 3) + (k1 & 7)] = (uint16_t)(w2 >> 16);
       }
       l_run[i] = l_run[i] * alpha[i] + row16_sum(ps);
       m_run[i] = m_new;
@@ -395,7 +398,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
       y[u] = bf2f(f2bf(y[u])) * (1.f / (1.f + __expf(-bf2f(gp[u]))));
   }
   *reinterpret_cast<u32x2*>(a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * a.D + c) =
-      u32x2{(uint32_t)f2bf(y[0]) | ((uint32_t)f2bf(y[1]) << 16), (uint32_t)f2bf(y[2]) | ((uint32_t)f2bf(y[3]) << 16)};
+      u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
 }
 
 // Splits per (sequence, KV head, query tile): as many as keep the grid within one workgroup per CU

@@ -9,13 +9,15 @@
 namespace trida {
 
 // ---------------------------------------------------------------- bf16 storage (uint16 bits)
-// Round-to-nearest-even, quiet NaN preserved: the same rounding torch applies on fp32 -> bf16.
-// Branch-free (a select, not a divergent branch around the NaN case).
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t quiet = (u >> 16) | 0x0040u;
-  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded);
+// Round-to-nearest-even, quiet NaN preserved: the same rounding torch applies on fp32 -> bf16. gfx950's
+// v_cvt_pk_bf16_f32 does it in one instruction (two values for f2bf2); checked on every one of the 2^32
+// fp32 inputs against (u + 0x7fff + ((u >> 16) & 1)) >> 16, with NaNs quieted as (u >> 16) | 0x40.
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ uint32_t f2bf2(float lo, float hi) {  // lo in bits 0..15, hi in 16..31
+  const f32x2v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2v));
 }
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 

@@ -63,10 +63,10 @@ __device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
 }
 __device__ __forceinline__ u32x4 pack8(const float* f) {
   u32x4 w;
-  w.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
-  w.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
-  w.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
-  w.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+  w.x = f2bf2(f[0], f[1]);
+  w.y = f2bf2(f[2], f[3]);
+  w.z = f2bf2(f[4], f[5]);
+  w.w = f2bf2(f[6], f[7]);
   return w;
 }
 

@@ -111,8 +111,8 @@ __global__ __launch_bounds__(NW* kWave) void skinny_gemm_kernel(GemmArgs a) {
     const int n = n0 + r * 16 + (l / 16) * 4;
     if (a.SK == 1) {
       u32x2 packed;
-      packed.x = (uint32_t)f2bf(sum.x) | ((uint32_t)f2bf(sum.y) << 16);
-      packed.y = (uint32_t)f2bf(sum.z) | ((uint32_t)f2bf(sum.w) << 16);
+      packed.x = f2bf2(sum.x, sum.y);
+      packed.y = f2bf2(sum.z, sum.w);
       *reinterpret_cast<u32x2*>(a.Y + (int64_t)m * a.y_st + n) = packed;
     } else {
       *reinterpret_cast<f32x4*>(a.partial + ((int64_t)sk * a.M + m) * a.N + n) = sum;
@@ -128,8 +128,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* partial
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   for (int k = 0; k < SK; ++k) s += *reinterpret_cast<const f32x4*>(partial + ((int64_t)k * M + m) * N + n);
   u32x2 packed;
-  packed.x = (uint32_t)f2bf(s.x) | ((uint32_t)f2bf(s.y) << 16);
-  packed.y = (uint32_t)f2bf(s.z) | ((uint32_t)f2bf(s.w) << 16);
+  packed.x = f2bf2(s.x, s.y);
+  packed.y = f2bf2(s.z, s.w);
   *reinterpret_cast<u32x2*>(Y + (int64_t)m * y_st + n) = packed;
 }
 
