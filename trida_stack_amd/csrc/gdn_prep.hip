@@ -74,6 +74,8 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); 
 // torch.nn.functional.softplus with beta 1 and threshold 20
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
+constexpr int kMaxPasses = 4;  // channel pieces of 8 per thread: C <= 8 * 256 * 4 = 8192
+
 template <int GW, int KC>  // lanes per q/k head = Dk / 8; conv width
 __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
   const int t = blockIdx.x % a.T;
@@ -84,9 +86,36 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
   const uint16_t* xb = a.x + (int64_t)b * a.x_sb;
   const uint16_t* wb = a.window + (int64_t)b * (a.Kc - 1) * a.C;
 
+  // every load of the block first (one memory round trip): per pass, the KC source rows of the thread's
+  // 8 channels and their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces), and the
+  // gate inputs
+  u32x4 xs[kMaxPasses][KC], wsv[kMaxPasses][KC];
+#pragma unroll
+  for (int ps = 0; ps < kMaxPasses; ++ps) {
+    const int p = ps * kThreads + tid;
+    if (p < pieces) {
+      const int c = p * 8;
+#pragma unroll
+      for (int j = 0; j < KC; ++j) {
+        const int tau = t - (KC - 1) + j;  // source row; negative rows come from the window
+        const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(KC - 1 + tau) * a.C + c;
+        xs[ps][j] = *reinterpret_cast<const u32x4*>(src);
+        wsv[ps][j] = reinterpret_cast<const u32x4*>(a.conv_w + (int64_t)c * KC)[j];
+      }
+    }
+  }
+  float av = 0.f, bv = 0.f;
+  if (tid < a.Hv) {
+    av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
+    bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
+  }
+
   // the q/k pieces come first (2 * key_dim / 8 of them, a multiple of GW), so every group of GW
   // lanes of one pass belongs to one head and the whole group is active together
-  for (int p0 = 0; p0 < pieces; p0 += kThreads) {
+#pragma unroll
+  for (int ps = 0; ps < kMaxPasses; ++ps) {
+    const int p0 = ps * kThreads;
+    if (p0 >= pieces) break;  // uniform
     const int p = p0 + tid;
     const bool live = p < pieces;
     const int c = (live ? p : 0) * 8;
@@ -96,13 +125,15 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
 #pragma unroll
       for (int ch = 0; ch < 8; ++ch)
 #pragma unroll
-        for (int j = 0; j < KC; ++j) w[ch][j] = bf2f(a.conv_w[(int64_t)(c + ch) * KC + j]);
+        for (int j = 0; j < KC; ++j) {
+          const int e = ch * KC + j;  // element of the 8 x KC weight block
+          const uint32_t word = wsv[ps][e / 8][(e % 8) / 2];
+          w[ch][j] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+        }
 #pragma unroll
       for (int j = 0; j < KC; ++j) {
-        const int tau = t - (KC - 1) + j;  // source row; negative rows come from the window
-        const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(KC - 1 + tau) * a.C + c;
         float f[8];
-        unpack8(*reinterpret_cast<const u32x4*>(src), f);
+        unpack8(xs[ps][j], f);
 #pragma unroll
         for (int ch = 0; ch < 8; ++ch) acc[ch] = fmaf(w[ch][j], f[ch], acc[ch]);
       }
@@ -135,8 +166,6 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
   }
 
   if (tid < a.Hv) {
-    const float av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
-    const float bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
     const int64_t o = ((int64_t)b * a.T + t) * a.Hv + tid;
     a.g[o] = -__expf(a.A_log[tid]) * softplus(av + a.dt_bias[tid]);
     a.beta[o] = 1.f / (1.f + __expf(-bv));
@@ -176,6 +205,9 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
   TRIDA_CHECK(x_st % 8 == 0 && x_sb % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)window & 15) == 0,
               TRIDA_ERR_ALIGN, "gdn_prep: x / window must be 16-byte aligned with strides in multiples of 8");
   TRIDA_CHECK(x_st >= C, TRIDA_ERR_ARG, "gdn_prep: row stride of x smaller than conv_dim");
+  TRIDA_CHECK(C <= 8 * kThreads * kMaxPasses, TRIDA_ERR_ARG, "gdn_prep: conv_dim %lld above %d", (long long)C,
+              8 * kThreads * kMaxPasses);
+  TRIDA_CHECK(((uintptr_t)conv_w & 15) == 0, TRIDA_ERR_ALIGN, "gdn_prep: conv_w must be 16-byte aligned");
   TRIDA_CHECK(window_out == nullptr || window_out != window, TRIDA_ERR_ARG,
               "gdn_prep: window_out must not alias window");
   TRIDA_CHECK(B * T < INT32_MAX, TRIDA_ERR_ARG, "gdn_prep: too many rows");
