@@ -449,17 +449,35 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
 #pragma unroll
     for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = a.state_in[st_off + i];
   }
-  // MASK rows (causal_mode 2): read the block-end state, four rows at a time
+  // MASK rows (causal_mode 2): read the block-end state, four rows at a time. On a large grid (many
+  // sequences: issue-bound) their q * scale is formed once per block in fp32 (the same products the
+  // per-lane path forms) into the k stage, dead after the causal rows: its kTC x Dk bf16 hold kTC / 2
+  // rows of Dk fp32 (batch 64: 184 -> 170 us per layer). On a grid of a few hundred blocks (batch 1:
+  // latency-bound) the two barriers cost more than they save, so each lane converts its own q.
+  const int nm = a.T - nc;
+  const bool qf_staged = (PREP || a.T <= tcn) && nm > 0 && nm <= kTC / 2 && gridDim.x >= 1024;  // block-uniform
+  float* s_qf = reinterpret_cast<float*>(&s_k[0][0]);
+  if (qf_staged) {
+    __syncthreads();  // every wave is done with the k rows
+    for (int e = tid; e < nm * Dk; e += NW * kWave) s_qf[e] = bf2f(s_q[nc + e / Dk][e % Dk]) * a.scale;
+    __syncthreads();
+  }
   for (int t = nc; t < a.T; t += 4) {
     float o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int tt = min(t + j, a.T - 1);
-      // the lane's KPL entries of q row tt: from LDS when the whole block was staged
-      const uint16_t* qr = ((PREP || a.T <= tcn) ? &s_q[tt][0] : qb + (int64_t)tt * qk_row) + kl * KPL;
       o[j] = 0.f;
+      if (qf_staged) {
+        const float* qr = s_qf + (tt - nc) * Dk + kl * KPL;
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], bf2f(qr[i]) * a.scale, o[j]);
+        for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], qr[i], o[j]);
+      } else {
+        // the lane's KPL entries of q row tt: from LDS when the whole block was staged
+        const uint16_t* qr = ((PREP || a.T <= tcn) ? &s_q[tt][0] : qb + (int64_t)tt * qk_row) + kl * KPL;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], bf2f(qr[i]) * a.scale, o[j]);
+      }
     }
     row16_sum4(o);
 #pragma unroll
