@@ -513,12 +513,25 @@ __device__ __forceinline__ int compact_bins(Shared& sh, const BinMap& bm, int n,
   return (int)tot;
 }
 
-// Appends the values of xv whose bit is set in mask (one LDS counter bump per thread).
+// Appends the values of xv whose bit is set in mask. Called by every lane of the wave: the lanes'
+// offsets are the wave-exclusive prefix of their counts, summed from the counts' bit planes (a ballot
+// and a masked bit count each), and one LDS counter bump per wave takes the wave's total (same-address
+// LDS atomics serialise, one lane after another).
 template <int N>
 __device__ __forceinline__ void append_batch(const float (&xv)[N], unsigned mask, Shared& sh) {
+  constexpr int kPlanes = N >= 16 ? 5 : N >= 8 ? 4 : N >= 4 ? 3 : N >= 2 ? 2 : 1;  // bits of a count <= N
   const int c = __popc(mask);
-  int pos = 0;
-  if (c) pos = atomicAdd(&sh.n, c);
+  int pre = 0, tot = 0;
+#pragma unroll
+  for (int bit = 0; bit < kPlanes; ++bit) {
+    const uint64_t bb = __ballot((c >> bit) & 1);
+    pre += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bb, 0u)) << bit;
+    tot += __popcll(bb) << bit;
+  }
+  if (tot == 0) return;  // wave-uniform
+  int base = 0;
+  if (threadIdx.x % kWave == 0) base = atomicAdd(&sh.n, tot);
+  int pos = __builtin_amdgcn_readfirstlane(base) + pre;
 #pragma unroll
   for (int e = 0; e < N; ++e)
     if ((mask >> e) & 1u) {
@@ -556,13 +569,19 @@ __device__ void stream_segment(const float* row, const TruncArgs& a, const BinMa
     const u32x4* row4 = reinterpret_cast<const u32x4*>(row);
     const int v0 = e0 >> 2, v1 = (e1 == a.V) ? (a.V >> 2) : (e1 >> 2);
     const int vb = a.ban >= 0 ? (a.ban >> 2) : -1;
+    // the next tile's loads are issued before the current tile is folded, so the fold hides their
+    // latency; addresses are clamped to the last vector (the last tile's prefetch reads one line)
+    auto load = [&](u32x4 (&dst)[U], int base) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) dst[u] = row4[min(base + u * kT + tid, v1 - 1)];
+    };
+    u32x4 xn[U];
+    if (v0 < v1) load(xn, v0);
     for (int base = v0; base < v1; base += kT * U) {
       u32x4 x[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const u32x4* p = row4 + min(base + u * kT + tid, v1 - 1);
-        x[u] = *p;
-      }
+      for (int u = 0; u < U; ++u) x[u] = xn[u];
+      load(xn, base + kT * U);
       float xv[4 * U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -662,12 +681,15 @@ __device__ void place_window(Shared& sh, bool use_k, float top_p, double k_seen,
   const double cB = sh.dpar[1], nB = sh.dpar[2];
   const double half = budget / scale / 2.0;  // in counted entries
   const double lo_c = use_k ? -1.0 : cB - half, hi_c = use_k ? budget / scale : cB + nB + half;
+  // the first bin whose cumulative count passes lo_c and the last one that starts below hi_c: the
+  // cumulative count (exact in fp64) only grows with the bin, so one bin of each test sees the
+  // transition and a single atomic per test lands (same-address LDS atomics serialise)
   double c = exc;
 #pragma unroll
   for (int u = 0; u < kBPT; ++u) {
     const int bin = tid * kBPT + u;
-    if (c + bc[u] > lo_c) atomicMin(&sh.ipar[1], bin);
-    if (c < hi_c) atomicMax(&sh.ipar[2], bin);
+    if (c + bc[u] > lo_c && (bin == 0 || c <= lo_c)) atomicMin(&sh.ipar[1], bin);
+    if (c < hi_c && (bin == kNB - 1 || c + bc[u] >= hi_c)) atomicMax(&sh.ipar[2], bin);
     c += bc[u];
   }
   __syncthreads();
@@ -777,7 +799,9 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
   mx = block_max(mx, sh.red);
   if (tid == 0) sh.umax = 0u;
   __syncthreads();
-  atomicMax(&sh.umax, nanbits);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) nanbits = max(nanbits, (unsigned)__shfl_xor((int)nanbits, off, kWave));
+  if (tid % kWave == 0) atomicMax(&sh.umax, nanbits);  // one atomic per wave
   __syncthreads();
   const bool bad = sh.umax > 0xff000000u || mx == INFINITY;  // a NaN, or a +inf logit
   // the exact row max of y (the window path tracked the raw logits; y = x / T is monotone in x)
