@@ -705,6 +705,38 @@ __device__ void collected_to_y(Shared& sh, int n, double rt) {
   __syncthreads();
 }
 
+// Top-p candidates (the collected logits of the boundary bin B and of bin B + 1) to exact y, in place,
+// packed at the front; returns how many. Bins are monotone in the logit, so a value of bin B + 1 is
+// <= every value of bin B in y and can only be kept when it ties with the smallest of them: the
+// others are dropped, which about halves what is sorted.
+template <bool kDiv>
+__device__ int boundary_to_y(Shared& sh, const BinMap& bm, int n, int B, double rt) {
+  constexpr int kPer = kCap / kT;
+  float y[kPer];
+  unsigned inb = 0u;  // bit u: entry u is in bin B (then: is kept)
+  float ymin = INFINITY;
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int j = (int)threadIdx.x * kPer + u;
+    const float x = j < n ? sh.coll[j] : -INFINITY;
+    const bool in = j < n && (int)bm.bin(x) == B;
+    y[u] = j < n ? exact_y<kDiv>(x, rt) : -INFINITY;
+    ymin = in ? fminf(ymin, y[u]) : ymin;
+    inb |= (unsigned)in << u;
+  }
+  ymin = -block_max(-ymin, sh.red);
+  const int nl = max(min(n - (int)threadIdx.x * kPer, kPer), 0);  // this thread's entries
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) inb |= (unsigned)(u < nl && y[u] == ymin) << u;
+  double tot = 0.0;
+  int w = (int)block_excl_scan((double)__popc(inb), sh.red, &tot);  // every read of sh.coll precedes its barriers
+#pragma unroll
+  for (int u = 0; u < kPer; ++u)
+    if ((inb >> u) & 1u) sh.coll[w++] = y[u];
+  __syncthreads();
+  return (int)tot;
+}
+
 template <bool kDiv, bool kVec>
 __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
   __shared__ Shared sh;
@@ -729,13 +761,27 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
     const int ns = min(kSample, V);
     float xs[kSample / kT];
     float smax = -INFINITY;
+    if (kVec && V >= 4 * kSample) {
+      // kT evenly spaced 16-byte vectors of 4 adjacent entries each: a line per 4 entries (entries one
+      // by one would fetch a line each, a quarter of the row's bytes at V = 248320)
+      static_assert(kSample == 4 * kT, "one vector of the sample per thread");
+      const int jv = (int)((int64_t)tid * (V >> 2) / kT);
+      const u32x4 w = reinterpret_cast<const u32x4*>(row)[jv];
+      const float x4[4] = {__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w)};
 #pragma unroll
-    for (int u = 0; u < kSample / kT; ++u) {
-      const int j = u * kT + tid;
-      const int ix = (int)((int64_t)min(j, ns - 1) * V / ns);
-      const float x = row[ix];
-      xs[u] = (j < ns && ix != a.ban && x == x) ? x : -INFINITY;
-      smax = xs[u] < INFINITY ? fmaxf(smax, xs[u]) : smax;
+      for (int u = 0; u < 4; ++u) {
+        xs[u] = (4 * jv + u != a.ban && x4[u] == x4[u]) ? x4[u] : -INFINITY;
+        smax = xs[u] < INFINITY ? fmaxf(smax, xs[u]) : smax;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kSample / kT; ++u) {
+        const int j = u * kT + tid;
+        const int ix = (int)((int64_t)min(j, ns - 1) * V / ns);
+        const float x = row[ix];
+        xs[u] = (j < ns && ix != a.ban && x == x) ? x : -INFINITY;
+        smax = xs[u] < INFINITY ? fmaxf(smax, xs[u]) : smax;
+      }
     }
     smax = block_max(smax, sh.red);
     mref = smax > -INFINITY ? exact_y<kDiv>(smax, a.rt) : 0.f;
@@ -890,7 +936,10 @@ __global__ __launch_bounds__(kT, 4) void truncate_kernel(TruncArgs a) {
             }
             __syncthreads();
             n2 = min(sh.n, kCap);
-            collected_to_y<kDiv>(sh, n2, a.rt);
+            if (use_k)
+              collected_to_y<kDiv>(sh, n2, a.rt);
+            else
+              n2 = boundary_to_y<kDiv>(sh, bm, n2, B, a.rt);
             sort_collection(sh, n2);
             if (use_k) {
               const int k = min(a.top_k, n2);
