@@ -161,11 +161,14 @@ int trida_sample_rows(const float* logits, int64_t rows, int64_t V, int64_t row_
  * window [B, Kc-1, C] bf16; conv_w [C, Kc] bf16; a, b [B, T, Hv] bf16 (strides ab_sb, ab_st);
  * A_log, dt_bias [Hv] fp32. Outputs (contiguous): q, k [B, T, Hk, Dk] bf16 unit-norm, v [B, T, Hv, Dv]
  * bf16, g, beta [B, T, Hv] fp32, and window_out [B, Kc-1, C] (last Kc-1 rows of [window ++ x]) when
- * not NULL; window_out must not alias window. Dk in {32, 64, 128}, Dv % 8 == 0.
+ * not NULL; window_out must not alias window. pre_out [B, T, C] (contiguous, 16-byte aligned, not x)
+ * receives a copy of the pre-conv rows x when not NULL: the rows a rollback rebuilds the conv window
+ * from (the raw mixed_qkv rows that fused_selfspec_gdn_layer keeps, qwen3_5_diffusion.py:2219).
+ * Dk in {32, 64, 128}, Dv % 8 == 0.
  */
 int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w, const uint16_t* a,
                    const uint16_t* b, const float* A_log, const float* dt_bias, uint16_t* q, uint16_t* k,
-                   uint16_t* v, float* g, float* beta, uint16_t* window_out, int64_t B, int64_t T,
+                   uint16_t* v, float* g, float* beta, uint16_t* window_out, uint16_t* pre_out, int64_t B, int64_t T,
                    int64_t Kc, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb, int64_t x_st,
                    int64_t ab_sb, int64_t ab_st, void* stream);
 

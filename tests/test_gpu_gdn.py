@@ -120,12 +120,15 @@ def test_gdn_prep(gpu, shape):
     ref = G.prep(x[..., :C], win, w, a, b, A_log, dt, Hk, Hv, Dk, Dv)
     bf = lambda t: t.to(DEV, torch.bfloat16)
     wout = torch.empty(B, 3, C, dtype=torch.bfloat16, device=DEV)
-    got = kernels.gdn_prep(bf(x)[..., :C], bf(win), bf(w), bf(a), bf(b), A_log.to(DEV), dt.to(DEV),
-                           Hk=Hk, Hv=Hv, Dk=Dk, Dv=Dv, window_out=wout)
+    pre = torch.full((B, T, C), float("nan"), dtype=torch.bfloat16, device=DEV)
+    xd = bf(x)[..., :C]  # a strided view: row stride C + 8
+    got = kernels.gdn_prep(xd, bf(win), bf(w), bf(a), bf(b), A_log.to(DEV), dt.to(DEV),
+                           Hk=Hk, Hv=Hv, Dk=Dk, Dv=Dv, window_out=wout, pre_out=pre)
     for gt, rf, name in zip(got, ref[:5], "qkvgb"):
         assert rel(gt, rf) < TOL_BF16, name
     assert rel(got[3], ref[3]) < 1e-5 and rel(got[4], ref[4]) < 1e-5
     assert torch.equal(wout.cpu().float(), ref[5])
+    assert torch.equal(pre.cpu(), xd.cpu())  # the pre-conv rows, bit for bit
 
 
 def test_snapshot_restore_config2(gpu):

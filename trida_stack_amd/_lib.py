@@ -47,7 +47,7 @@ SIGNATURES = {
     "trida_silu_mul": (C.c_int, [P, P, I64, I64, I64, I64, P]),
     "trida_gated_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, F32, P]),
     "trida_attn_prep": (C.c_int, [P, I64, P, P, P, P, P, P, P] + [I64] * 7 + [F32, F32, P]),
-    "trida_gdn_prep": (C.c_int, [P] * 13 + [I64] * 11 + [P]),
+    "trida_gdn_prep": (C.c_int, [P] * 14 + [I64] * 11 + [P]),
     "trida_gdr_recurrent": (C.c_int, [P] * 9 + [I64] * 6 + [C.c_int, I64, F32, P]),
     "trida_gdn_fused_layer": (C.c_int, [P] * 17 + [I64] * 11 + [C.c_int, I64, F32, P]),
     "trida_gdr_block_bidir": (C.c_int, [P] * 8 + [I64] * 7 + [F32, P]),

@@ -47,6 +47,7 @@ struct PrepArgs {
   float* g;     // [B, T, Hv]
   float* beta;
   uint16_t* window_out;  // [B, Kc-1, C] or null
+  uint16_t* pre_out;     // [B, T, C] copy of the pre-conv rows x, or null
   int T, C, Kc, Hk, Hv, Dk, Dv;
   int64_t x_sb, x_st, ab_sb, ab_st;
 };
@@ -102,6 +103,15 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
         xs[ps][j] = *reinterpret_cast<const u32x4*>(src);
         wsv[ps][j] = reinterpret_cast<const u32x4*>(a.conv_w + (int64_t)c * KC)[j];
       }
+    }
+  }
+  // the pre-conv rows a rollback rebuilds the window from: the block's own row is its last source row
+  if (a.pre_out) {
+#pragma unroll
+    for (int ps = 0; ps < kMaxPasses; ++ps) {
+      const int p = ps * kThreads + tid;
+      if (p < pieces)
+        *reinterpret_cast<u32x4*>(a.pre_out + ((int64_t)b * a.T + t) * a.C + p * 8) = xs[ps][KC - 1];
     }
   }
   float av = 0.f, bv = 0.f;
@@ -191,7 +201,7 @@ using namespace trida;
 extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w,
                               const uint16_t* a_in, const uint16_t* b_in, const float* A_log,
                               const float* dt_bias, uint16_t* q, uint16_t* k, uint16_t* v, float* g,
-                              float* beta, uint16_t* window_out, int64_t B, int64_t T, int64_t Kc,
+                              float* beta, uint16_t* window_out, uint16_t* pre_out, int64_t B, int64_t T, int64_t Kc,
                               int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb, int64_t x_st,
                               int64_t ab_sb, int64_t ab_st, void* stream) {
   TRIDA_CHECK(x && window && conv_w && a_in && b_in && A_log && dt_bias && q && k && v && g && beta,
@@ -210,8 +220,10 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
   TRIDA_CHECK(((uintptr_t)conv_w & 15) == 0, TRIDA_ERR_ALIGN, "gdn_prep: conv_w must be 16-byte aligned");
   TRIDA_CHECK(window_out == nullptr || window_out != window, TRIDA_ERR_ARG,
               "gdn_prep: window_out must not alias window");
+  TRIDA_CHECK(pre_out == nullptr || (((uintptr_t)pre_out & 15) == 0 && pre_out != x), TRIDA_ERR_ARG,
+              "gdn_prep: pre_out must be 16-byte aligned and not alias x");
   TRIDA_CHECK(B * T < INT32_MAX, TRIDA_ERR_ARG, "gdn_prep: too many rows");
-  PrepArgs a{x, window, conv_w, a_in, b_in, A_log, dt_bias, q, k, v, g, beta, window_out,
+  PrepArgs a{x, window, conv_w, a_in, b_in, A_log, dt_bias, q, k, v, g, beta, window_out, pre_out,
              (int)T, (int)C, (int)Kc, (int)Hk, (int)Hv, (int)Dk, (int)Dv, x_sb, x_st, ab_sb, ab_st};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(B * T));

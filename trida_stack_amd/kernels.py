@@ -356,15 +356,16 @@ def _f32(t: torch.Tensor, name: str):
 
 def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
              A_log: torch.Tensor, dt_bias: torch.Tensor, *, Hk: int, Hv: int, Dk: int, Dv: int,
-             window_out: Optional[torch.Tensor] = None, out=None):
+             window_out: Optional[torch.Tensor] = None, pre_out: Optional[torch.Tensor] = None, out=None):
     """Conv + SiLU + split + l2norm(q, k) + gates for a block of rows (one launch).
 
     x [B, T, C] bf16 (last dim contiguous, C = 2*Hk*Dk + Hv*Dv; batch / row strides may be larger),
     window [B, Kc-1, C] bf16, conv_w [C, Kc] bf16, a, b [B, T, Hv] bf16 (last dim contiguous),
     A_log, dt_bias [Hv] fp32. Returns q, k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g, beta [B,T,Hv] fp32.
     window_out (optional, [B, Kc-1, C], not aliasing window) receives the last Kc-1 rows of
-    [window ++ x] (the causal-prefill conv state)."""
-    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, window_out)
+    [window ++ x] (the causal-prefill conv state). pre_out (optional, contiguous [B, T, C]) receives a
+    copy of x: the pre-conv rows a rollback rebuilds the window from."""
+    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, window_out, pre_out)
     for t, n in ((x, "x"), (window, "window"), (conv_w, "conv_w"), (a, "a"), (b, "b")):
         _bf16(t, n)
     _f32(A_log, "A_log")
@@ -380,6 +381,10 @@ def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: tor
     if window_out is not None and (window_out.shape != window.shape or not window_out.is_contiguous()
                                    or window_out.data_ptr() == window.data_ptr()):
         raise ValueError("window_out must be a separate contiguous [B, Kc-1, C] buffer")
+    if pre_out is not None:
+        _bf16(pre_out, "pre_out")
+        if pre_out.shape != (B, T, C) or not pre_out.is_contiguous() or pre_out.data_ptr() == x.data_ptr():
+            raise ValueError("pre_out must be a separate contiguous [B, T, C] buffer")
     if out is None:
         q = torch.empty((B, T, Hk, Dk), dtype=torch.bfloat16, device=dev)
         k = torch.empty_like(q)
@@ -394,7 +399,7 @@ def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: tor
     rc = _lib.load().trida_gdn_prep(
         x.data_ptr(), window.data_ptr(), conv_w.data_ptr(), a.data_ptr(), b.data_ptr(),
         A_log.contiguous().data_ptr(), dt_bias.contiguous().data_ptr(), q.data_ptr(), k.data_ptr(),
-        v.data_ptr(), g.data_ptr(), beta.data_ptr(), _ptr(window_out), B, T, Kc, Hk, Hv, Dk, Dv,
+        v.data_ptr(), g.data_ptr(), beta.data_ptr(), _ptr(window_out), _ptr(pre_out), B, T, Kc, Hk, Hv, Dk, Dv,
         x.stride(0), x.stride(1), a.stride(0), a.stride(1), _stream(dev))
     _lib.check(rc, "trida_gdn_prep")
     return q, k, v, g, beta

@@ -348,7 +348,8 @@ class TridaRuntime:
                     with K.timed("gdn_prep"):
                         K.gdn_prep(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"], w[p + "dt_bias"],
                                    Hk=c.lin_k_heads, Hv=c.lin_v_heads, Dk=c.lin_k_dim, Dv=c.lin_v_dim,
-                                   window_out=s.win_tmp if persist else None, out=rec)
+                                   window_out=s.win_tmp if persist else None,
+                                   pre_out=s.pre_rec[j] if keep and not persist else None, out=rec)
                     if chunked:
                         with K.timed("gdr_chunk"):
                             K.gdr_chunk(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
@@ -359,8 +360,6 @@ class TridaRuntime:
                             K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
                                             causal_mode=gdn_mode, num_clean=nc,
                                             state_out=state[j] if persist else None, out=s.y)
-                    if keep and not persist:
-                        s.pre_rec[j].copy_(xv)
                 if persist:
                     window[j].copy_(s.win_tmp)
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
