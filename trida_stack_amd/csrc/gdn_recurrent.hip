@@ -152,8 +152,13 @@ __device__ __forceinline__ void lds_gather(void* dst, int n, F&& src, int nthrea
 }
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
-template <int KPL, int NW, bool PREP>
+// F32 (small grids, no block-bidirectional readout): each staged chunk's k and q * scale are converted
+// to fp32 once per block, so a row step reads them ready (the bf16 unpack and the scale multiply leave
+// the per-step chain: 24 of ~80 instructions per step); chunks of 40 rows keep the fp32 stages within
+// two blocks per CU. Large grids keep the bf16 stages, whose smaller LDS footprint holds more blocks.
+template <int KPL, int NW, bool PREP, bool F32>
 __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
+  constexpr int TC = F32 ? 40 : kTC;  // rows staged per chunk
   constexpr int Dk = KPL * kLanesPerV;
   constexpr int VPB = NW * kVPerWave;
   const int tiles = a.Dv / VPB;
@@ -167,12 +172,23 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   const int v = vt * VPB + vl;
   const int kl = lane % kLanesPerV;                      // k slice [kl*KPL, kl*KPL+KPL)
 
-  __shared__ __align__(16) uint16_t s_q[kTC][Dk];
-  __shared__ __align__(16) uint16_t s_k[kTC][Dk];
-  __shared__ __align__(16) uint16_t s_v[kTC][VPB];
-  __shared__ float s_g[kTC], s_b[kTC];
-  __shared__ float s_ob[kTC][VPB];  // backward sub-scan outputs of the block-bidirectional readout
-  __shared__ float s_kq[kTC];  // k . (q * scale) per staged row
+  __shared__ __align__(16) uint16_t s_q[TC][Dk];
+  __shared__ __align__(16) uint16_t s_k[TC][Dk];
+  __shared__ __align__(16) float s_qf32[F32 ? TC : 1][F32 ? Dk : 4];  // q * scale (F32 form)
+  __shared__ __align__(16) float s_kf32[F32 ? TC : 1][F32 ? Dk : 4];  // k (F32 form)
+  __shared__ __align__(16) uint16_t s_v[TC][VPB];
+  __shared__ float s_g[TC], s_b[TC];
+  __shared__ float s_ob[TC][VPB];  // backward sub-scan outputs of the block-bidirectional readout
+  __shared__ float s_kq[TC];  // k . (q * scale) per staged row
+  // entry i of staged row r: k, and q * scale (the same product on both forms)
+  auto kval = [&](int r, int i) -> float {
+    if constexpr (F32) return s_kf32[r][i];
+    else return bf2f(s_k[r][i]);
+  };
+  auto qval = [&](int r, int i) -> float {
+    if constexpr (F32) return s_qf32[r][i];
+    else return bf2f(s_q[r][i]) * a.scale;
+  };
 
   const int64_t st_off = (((int64_t)b * a.Hv + h) * a.Dv + v) * Dk + kl * KPL;
   float s[KPL];
@@ -190,14 +206,14 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   const float* bb = a.beta + (int64_t)b * a.T * a.Hv + h;
 
   // rows staged per chunk: whole blocks when the readout is block-bidirectional
-  const int tcn = a.bidir > 0 ? (kTC / a.bidir) * a.bidir : kTC;
+  const int tcn = a.bidir > 0 ? (TC / a.bidir) * a.bidir : TC;
   // one step of the recurrence on state st with staged row r; returns the row's readout S'q
   auto step = [&](float (&st)[KPL], int r) -> float {
     float kk[KPL], qq[KPL];
 #pragma unroll
     for (int i = 0; i < KPL; ++i) {
-      kk[i] = bf2f(s_k[r][kl * KPL + i]);
-      qq[i] = bf2f(s_q[r][kl * KPL + i]) * a.scale;
+      kk[i] = kval(r, kl * KPL + i);
+      qq[i] = qval(r, kl * KPL + i);
     }
     const float eg = s_g[r];
     float kv = 0.f, sq = 0.f;
@@ -342,8 +358,8 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   auto fetch = [&](Row& R, int r) {
 #pragma unroll
     for (int i = 0; i < KPL; ++i) {
-      R.kk[i] = bf2f(s_k[r][kl * KPL + i]);
-      R.qq[i] = bf2f(s_q[r][kl * KPL + i]) * a.scale;
+      R.kk[i] = kval(r, kl * KPL + i);
+      R.qq[i] = qval(r, kl * KPL + i);
     }
     R.eg = s_g[r];
     R.vv = bf2f(s_v[r][vl]);
@@ -391,6 +407,13 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       s_b[tid] = bv;
     }
     __syncthreads();
+    if constexpr (F32) {
+      for (int e = tid; e < tn * Dk; e += NW * kWave) {
+        s_qf32[e / Dk][e % Dk] = bf2f(s_q[e / Dk][e % Dk]) * a.scale;
+        s_kf32[e / Dk][e % Dk] = bf2f(s_k[e / Dk][e % Dk]);
+      }
+      __syncthreads();
+    }
     }
     // k . (q * scale) of every staged row, once per block instead of once per value column: each
     // 16-lane group takes a row, lane j the same KPL-element slice and fma order as the column lanes'
@@ -400,7 +423,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       float kq = 0.f;
 #pragma unroll
       for (int i = 0; i < KPL; ++i)
-        kq = fmaf(bf2f(s_k[rr][j * KPL + i]), bf2f(s_q[rr][j * KPL + i]) * a.scale, kq);
+        kq = fmaf(kval(rr, j * KPL + i), qval(rr, j * KPL + i), kq);
       kq = row16_sum(kq);
       if (j == 0) s_kq[rr] = kq;
     }
@@ -455,7 +478,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   // rows of Dk fp32 (batch 64: 184 -> 170 us per layer). On a grid of a few hundred blocks (batch 1:
   // latency-bound) the two barriers cost more than they save, so each lane converts its own q.
   const int nm = a.T - nc;
-  const bool qf_staged = (PREP || a.T <= tcn) && nm > 0 && nm <= kTC / 2 && gridDim.x >= 1024;  // block-uniform
+  const bool qf_staged = !F32 && (PREP || a.T <= tcn) && nm > 0 && nm <= TC / 2 && gridDim.x >= 1024;  // block-uniform
   float* s_qf = reinterpret_cast<float*>(&s_k[0][0]);
   if (qf_staged) {
     __syncthreads();  // every wave is done with the k rows
@@ -468,7 +491,10 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     for (int j = 0; j < 4; ++j) {
       const int tt = min(t + j, a.T - 1);
       o[j] = 0.f;
-      if (qf_staged) {
+      if (F32 && a.T <= tcn) {  // the whole block is the last staged chunk
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], s_qf32[tt][kl * KPL + i], o[j]);
+      } else if (qf_staged) {
         const float* qr = s_qf + (tt - nc) * Dk + kl * KPL;
 #pragma unroll
         for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], qr[i], o[j]);
@@ -490,6 +516,15 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   }
 }
 
+template <int KPL, bool PREP, bool F32>
+void launch_nw(const RecArgs& a, int nw, unsigned grid, hipStream_t st) {
+  switch (nw) {
+    case 4: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 4, PREP, F32>), dim3(grid), dim3(4 * kWave), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 2, PREP, F32>), dim3(grid), dim3(2 * kWave), 0, st, a); break;
+    default: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 1, PREP, F32>), dim3(grid), dim3(kWave), 0, st, a); break;
+  }
+}
+
 template <int KPL, bool PREP = false>
 int launch_kpl(const RecArgs& a, int B, hipStream_t st) {
   // widest block whose v-tile divides Dv; more, narrower blocks when the grid would be small
@@ -497,11 +532,12 @@ int launch_kpl(const RecArgs& a, int B, hipStream_t st) {
   while (nw > 1 && (a.Dv % (nw * kVPerWave) != 0 || (int64_t)B * a.Hv * (a.Dv / (nw * kVPerWave)) < 256)) nw /= 2;
   if (a.Dv % (nw * kVPerWave) != 0) return TRIDA_ERR_ARG;
   const unsigned grid = (unsigned)((int64_t)B * a.Hv * (a.Dv / (nw * kVPerWave)));
-  switch (nw) {
-    case 4: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 4, PREP>), dim3(grid), dim3(4 * kWave), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 2, PREP>), dim3(grid), dim3(2 * kWave), 0, st, a); break;
-    default: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 1, PREP>), dim3(grid), dim3(kWave), 0, st, a); break;
-  }
+  // fp32 stages on grids of fewer than 1024 blocks (batch 1: 512), where a block's row chain is the
+  // critical path and two blocks per CU already hold the grid
+  if (!PREP && a.bidir == 0 && grid < 1024)
+    launch_nw<KPL, PREP, !PREP>(a, nw, grid, st);
+  else
+    launch_nw<KPL, PREP, false>(a, nw, grid, st);
   return launch_status(PREP ? "gdn_fused_layer" : "gdr_recurrent");
 }
 
