@@ -80,6 +80,26 @@ def test_gdr_canvas_clean_rows_equal_causal_rows_bitwise(gpu):
     assert torch.equal(o1[:, :17], o2[:, :17])
 
 
+@pytest.mark.parametrize("mode,nc", [(1, 33), (2, 1), (2, 17)])
+def test_gdr_small_and_large_grid_forms_bitwise(gpu, mode, nc):
+    """One sequence alone (a small grid: k and q * scale staged in fp32) and the same sequence as every
+    slot of a batch of 64 (a large grid: bf16 stages) give bit-identical rows and states: both forms
+    form the same products in the same order."""
+    inp = gdr_inputs(31 + nc, 1, 33, 16, 16, 128, 128)
+    q, k, v, g, beta, s0 = to_dev(*inp)
+    rep = lambda t: t.expand(64, *t.shape[1:]).contiguous()
+    s1 = torch.empty_like(s0)
+    o1, c1 = kernels.gdr_recurrent(q, k, v, g, beta, s0, causal_mode=mode, num_clean=nc, state_out=s1,
+                                   want_clean=mode == 2)
+    s64 = torch.empty_like(rep(s0))
+    o64, c64 = kernels.gdr_recurrent(rep(q), rep(k), rep(v), rep(g), rep(beta), rep(s0), causal_mode=mode,
+                                     num_clean=nc, state_out=s64, want_clean=mode == 2)
+    for j in (0, 17, 63):
+        assert torch.equal(o64[j], o1[0]) and torch.equal(s64[j], s1[0])
+        if mode == 2:
+            assert torch.equal(c64[j], c1[0])
+
+
 def test_gdr_state_in_place(gpu):
     inp = gdr_inputs(5, 2, 9, 2, 4, 64, 32)
     _, s_ref, _ = G.recurrent(*inp)
