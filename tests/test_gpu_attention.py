@@ -29,6 +29,9 @@ CASES = [  # B, T, Hq, Hkv, D, L, prefixes
     (2, 5, 4, 2, 64, 300, [0, 213]),
     (3, 9, 8, 2, 128, 520, [1, 77, 500]),
     (1, 40, 8, 2, 128, 200, [100]),             # 160 query rows: two query tiles
+    # ragged batches whose (sequence, KV head) pairs fill whole XCD rounds: scheduled longest-first
+    (4, 7, 8, 2, 64, 400, [5, 390, 120, 390]),
+    (8, 33, 16, 4, 256, 700, [600, 10, 333, 600, 0, 59, 512, 256]),
 ]
 
 

@@ -28,6 +28,7 @@ constexpr int kWR = 16;             // query rows per wave (one MFMA row tile)
 constexpr int kMT = kNW * kWR;      // query rows per workgroup
 constexpr int kKB = 64;             // keys per step
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kMaxLptSeqs = 256;  // batches up to this size are scheduled longest-first
 
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
@@ -93,15 +94,44 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t sVt[D * kKB];
   __shared__ __align__(16) uint16_t sP[kNW][kWR * kKB];
 
-  // query tiles of one (split, kv head) read the same keys: innermost, and on one XCD
-  int idx = xcd_major(blockIdx.x, gridDim.x);
-  const int qt = idx % a.QT;
-  idx /= a.QT;
-  const int s = idx % a.S;
-  idx /= a.S;
-  const int hk = idx % a.Hkv;
-  const int b = idx / a.Hkv;
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+  const int per_pair = a.S * a.QT;                  // workgroups per (sequence, KV head)
+  const int npair = (int)gridDim.x / per_pair, nseq = npair / a.Hkv;
+  int b, hk, s, qt;
+  if (nseq > 1 && nseq <= kMaxLptSeqs && npair % kXcds == 0) {
+    // ragged batches: longest sequences first. Workgroups reach the XCDs round-robin in block order,
+    // so (sequence, KV head) pairs are dealt to the XCDs in descending prefix length, each pair's
+    // workgroups consecutive on one XCD (its query tiles share the keys in that L2); the longest pairs
+    // start in the first wave of workgroups instead of wherever their batch index put them.
+    __shared__ int s_len[kMaxLptSeqs];
+    __shared__ int s_seq;
+    const int x = (int)blockIdx.x % kXcds, j = (int)blockIdx.x / kXcds;
+    const int pr = (j / per_pair) * kXcds + x;  // pair rank
+    const int wi = j % per_pair;
+    qt = wi % a.QT;
+    s = wi / a.QT;
+    hk = pr % a.Hkv;
+    const int r = pr / a.Hkv;  // sequence rank: prefix length descending, batch index ascending
+    for (int c = tid; c < nseq; c += kNW * kWave) s_len[c] = a.prefix[c];
+    __syncthreads();
+    for (int c = tid; c < nseq; c += kNW * kWave) {
+      const int lc = s_len[c];
+      int rank = 0;
+      for (int o = 0; o < nseq; ++o) rank += (s_len[o] > lc) | ((s_len[o] == lc) & (o < c));
+      if (rank == r) s_seq = c;
+    }
+    __syncthreads();
+    b = s_seq;
+  } else {
+    // query tiles of one (split, kv head) read the same keys: innermost, and on one XCD
+    int idx = xcd_major(blockIdx.x, gridDim.x);
+    qt = idx % a.QT;
+    idx /= a.QT;
+    s = idx % a.S;
+    idx /= a.S;
+    hk = idx % a.Hkv;
+    b = idx / a.Hkv;
+  }
   const int M = a.T * a.G;
   const int m0 = qt * kMT;
   const int rows = min(kMT, M - m0);
