@@ -66,6 +66,16 @@ int trida_greedy_accept(const void* logits, int dtype, int64_t B, int64_t R, int
  * logits [rows, V] (dtype 0 fp32 / 1 bf16, row stride in elements); argmax [rows] int64; conf [rows]
  * fp32. scratch: trida_row_argmax_scratch_bytes(rows, V, dtype, splits). */
 int64_t trida_row_argmax_scratch_bytes(int64_t rows, int64_t V, int dtype, int64_t splits);
+
+/* The unmasking of one denoise pass over a draft canvas: per sequence b, the `count` slots j < block
+ * with masked[b, j] != 0 and the highest conf[b, j] (ties: the lower slot first; unmasked slots rank
+ * last) set canvas[b, j + 1] = argmax[b, j] (the shift readout: row j predicts slot j + 1) and clear
+ * masked[b, j]. Replaces the commit of the most confident MASK positions of _denoise_shift_step
+ * (qwen3_5_diffusion.py:476-635), with a fixed number of slots per pass instead of a confidence
+ * threshold. argmax, conf: [B, >= block] (row stride row_stride), as trida_row_argmax writes them;
+ * masked [B, block] bytes; canvas [B, >= block + 1] int64 (row stride canvas_stride); block <= 1024. */
+int trida_unmask_top(const int64_t* argmax, const float* conf, int64_t row_stride, uint8_t* masked,
+                     int64_t* canvas, int64_t canvas_stride, int64_t B, int64_t block, int64_t count, void* stream);
 int trida_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, int64_t* argmax,
                      float* conf, void* scratch, int64_t scratch_bytes, int64_t splits, void* stream);
 

@@ -383,6 +383,29 @@ __global__ __launch_bounds__(256) void row_finalize_kernel(const float* pval, co
   }
 }
 
+// The unmasking of a denoise pass: per sequence, the `count` MASK slots with the highest confidence
+// (ties: the lower slot first, as a stable descending sort) take their shifted prediction (row j
+// predicts slot j + 1) and leave the mask. One block per sequence; a slot's rank is the number of
+// slots ahead of it in that order, so the chosen slots are those ranked below count.
+constexpr int kMaxUnmask = 1024;
+__global__ __launch_bounds__(256) void unmask_top_kernel(const int64_t* am, const float* conf, int64_t ac_st,
+                                                         uint8_t* masked, int64_t* canvas, int64_t cv_st, int blk,
+                                                         int count) {
+  __shared__ float s_sc[kMaxUnmask];
+  const int64_t b = blockIdx.x;
+  for (int j = threadIdx.x; j < blk; j += blockDim.x) s_sc[j] = masked[b * blk + j] ? conf[b * ac_st + j] : -INFINITY;
+  __syncthreads();
+  for (int j = threadIdx.x; j < blk; j += blockDim.x) {
+    const float sj = s_sc[j];
+    int rank = 0;
+    for (int i = 0; i < blk; ++i) rank += (s_sc[i] > sj) | ((s_sc[i] == sj) & (i < j));
+    if (rank < count) {
+      canvas[b * cv_st + j + 1] = am[b * ac_st + j];
+      masked[b * blk + j] = 0;
+    }
+  }
+}
+
 // Split a row into chunks of one tile each (kThreads * U float4), U in {4, 8, 16}: the largest U
 // that still gives at least ~512 blocks; callers may force the split count.
 void plan(int64_t B, int64_t R, int64_t V, int64_t splits_req, int elems, int64_t* S, int64_t* chunk) {
@@ -511,4 +534,17 @@ extern "C" int trida_row_argmax(const void* logits, int dtype, int64_t rows, int
   hipLaunchKernelGGL(row_finalize_kernel, dim3((unsigned)cdiv(rows, 256)), dim3(256), 0, st, pval, pidx, psum,
                      (int)rows, (int)S, argmax, conf);
   return launch_status("row_argmax/finalize");
+}
+
+extern "C" int trida_unmask_top(const int64_t* argmax, const float* conf, int64_t row_stride, uint8_t* masked,
+                                int64_t* canvas, int64_t canvas_stride, int64_t B, int64_t block, int64_t count,
+                                void* stream) {
+  TRIDA_CHECK(argmax && conf && masked && canvas, TRIDA_ERR_NULL, "unmask_top: argmax, conf, masked and canvas are required");
+  TRIDA_CHECK(B > 0 && B < INT32_MAX && block >= 1 && block <= kMaxUnmask && count >= 0 && count <= block, TRIDA_ERR_ARG,
+              "unmask_top: bad sizes B=%lld block=%lld (<= %d) count=%lld", (long long)B, (long long)block,
+              kMaxUnmask, (long long)count);
+  TRIDA_CHECK(row_stride >= block && canvas_stride >= block + 1, TRIDA_ERR_ARG, "unmask_top: strides");
+  hipLaunchKernelGGL(unmask_top_kernel, dim3((unsigned)B), dim3(256), 0, static_cast<hipStream_t>(stream), argmax, conf,
+                     row_stride, masked, canvas, canvas_stride, (int)block, (int)count);
+  return launch_status("unmask_top");
 }

@@ -283,7 +283,6 @@ class BlockSpecStep:
         self.crop = torch.empty(B, dtype=torch.int64, device=dev)
         self.d_am = torch.empty(B, block + 1, dtype=torch.int64, device=dev)
         self.d_conf = torch.empty(B, block + 1, dtype=torch.float32, device=dev)
-        self.neg = torch.full((B, block), float("-inf"), dtype=torch.float32, device=dev)
 
     def run(self) -> None:
         rt, cache, blk = self.rt, self.cache, self.block
@@ -295,11 +294,8 @@ class BlockSpecStep:
             # row j predicts slot j + 1 (shift readout); the last row is not used
             with K.timed("row_argmax"):
                 K.row_argmax(L, out=(self.d_am, self.d_conf))
-            score = torch.where(self.masked, self.d_conf[:, :blk], self.neg)
-            # the per[p] most confident MASK slots (ties: the lower slot first)
-            pos = torch.sort(score, dim=1, descending=True, stable=True).indices[:, : self.per[p]]
-            self.canvas.scatter_(1, pos + 1, self.d_am[:, :blk].gather(1, pos))
-            self.masked.scatter_(1, pos, False)
+            # the per[p] most confident MASK slots (ties: the lower slot first) take their predictions
+            K.unmask_top(self.d_am, self.d_conf, self.masked, self.canvas, self.per[p])
         vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
         self.ctx.copy_(cache.length)

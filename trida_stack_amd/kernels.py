@@ -162,6 +162,29 @@ def row_argmax(logits: torch.Tensor, *, want_conf: bool = True, splits: int = 0,
     return out
 
 
+def unmask_top(argmax: torch.Tensor, conf: torch.Tensor, masked: torch.Tensor, canvas: torch.Tensor,
+               count: int) -> None:
+    """One denoise pass's unmasking, in place: per sequence, the `count` masked slots with the highest
+    conf (ties: the lower slot first) take canvas[:, j + 1] = argmax[:, j] and leave `masked`
+    (_denoise_shift_step, qwen3_5_diffusion.py:476-635, with a fixed count per pass).
+    argmax [B, >= n] int64 and conf [B, >= n] fp32 with the same row stride, masked [B, n] bool,
+    canvas [B, >= n + 1] int64."""
+    dev = _need_gpu(argmax, conf, masked, canvas)
+    B, n = masked.shape
+    if masked.dtype != torch.bool or not masked.is_contiguous():
+        raise ValueError("masked must be a contiguous [B, n] bool tensor")
+    if argmax.dtype != torch.int64 or conf.dtype != torch.float32 or canvas.dtype != torch.int64:
+        raise ValueError("argmax / canvas must be int64 and conf fp32")
+    if argmax.shape[0] != B or conf.shape[0] != B or canvas.shape[0] != B or argmax.shape[1] < n \
+            or conf.shape[1] < n or canvas.shape[1] < n + 1:
+        raise ValueError("unmask_top: shapes do not match masked [B, n]")
+    if argmax.stride() != conf.stride() or argmax.stride(1) != 1 or canvas.stride(1) != 1:
+        raise ValueError("argmax and conf need the same strides and contiguous rows; canvas contiguous rows")
+    rc = _lib.load().trida_unmask_top(argmax.data_ptr(), conf.data_ptr(), argmax.stride(0), masked.data_ptr(),
+                                      canvas.data_ptr(), canvas.stride(0), B, n, int(count), _stream(dev))
+    _lib.check(rc, "trida_unmask_top")
+
+
 # --------------------------------------------------------------------------------------------------
 # Sampled acceptance (temperature / top-k / top-p, speculative rejection sampling)
 MAX_TOP_K = 4096
