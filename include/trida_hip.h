@@ -60,6 +60,22 @@ int trida_greedy_accept(const void* logits, int dtype, int64_t B, int64_t R, int
                         int32_t* n_acc, int64_t* bonus, int64_t* crop, void* scratch,
                         int64_t scratch_bytes, int64_t splits, void* stream);
 
+/* Allocation-free greedy acceptance. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, kernels and results as trida_greedy_accept without the scratch
+ * arguments: the split results go to a fixed device array of TRIDA_GREEDY_ACCEPT_NOALLOC_SCRATCH_BYTES
+ * bytes that the library holds on every GPU it runs on until the process ends (its address is looked
+ * up once per device, on the first call there). Shapes whose scratch
+ * (trida_greedy_accept_scratch_bytes) exceeds that size are rejected with TRIDA_ERR_WORKSPACE; 1 MiB
+ * covers e.g. B = 64 sequences of 33 rows over V = 248320 bf16 or fp32 at the default split count.
+ * Calls that overlap in time on one GPU share the array and race; serialise them (one stream, or
+ * events). The entry point calls no allocating routine. */
+#define TRIDA_GREEDY_ACCEPT_NOALLOC_SCRATCH_BYTES (1 << 20)
+int trida_greedy_accept_noalloc(const void* logits, int dtype, int64_t B, int64_t R, int64_t V, int64_t batch_stride,
+                                int64_t row_stride, const int64_t* drafts, int64_t K, int64_t draft_stride,
+                                const int32_t* n_live, const int64_t* ctx_len, int64_t* argmax_out, int32_t* n_acc,
+                                int64_t* bonus, int64_t* crop, int64_t splits, void* stream);
+
 /* Row argmax (first index on ties) and, when conf is not NULL, the softmax probability of the argmax
  * (the confidence the denoising passes rank MASK slots by). Replaces the argmax / max-softmax readout
  * of the block-diffusion denoise step (_shifted_conf_pred, qwen3_5_diffusion.py:446-467).

@@ -29,6 +29,8 @@ SIGNATURES = {
     "trida_last_error": (C.c_char_p, []),
     "trida_greedy_accept_scratch_bytes": (I64, [I64, I64, I64, C.c_int, I64]),
     "trida_greedy_accept": (C.c_int, [P, C.c_int, I64, I64, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, P, I64, I64, P]),
+    "trida_greedy_accept_noalloc": (C.c_int, [P, C.c_int, I64, I64, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, I64,
+                                              P]),
     "trida_row_argmax_scratch_bytes": (I64, [I64, I64, C.c_int, I64]),
     "trida_row_argmax": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P, I64, I64, P]),
     "trida_unmask_top": (C.c_int, [P, P, I64, P, P, I64, I64, I64, I64, P]),

@@ -15,9 +15,22 @@
 #include <limits.h>
 #include <math.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace trida {
+
+// Scratch of the allocation-free entry point (trida_greedy_accept_noalloc): the split results of the
+// streaming pass, in a file-scope device array. Every GPU the library runs on holds its own copy at its
+// own address until the process ends; host code reaches it only through the address that
+// hipGetSymbolAddress returns for that GPU (the array's name is a host-side stand-in). The split
+// results are written before they are read, so nothing in it needs clearing between calls.
+namespace noalloc {
+constexpr int64_t kScratchBytes = TRIDA_GREEDY_ACCEPT_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+}  // namespace noalloc
+
 namespace {
 
 constexpr int kThreads = 256;
@@ -512,6 +525,63 @@ extern "C" int trida_greedy_accept(const void* logits, int dtype, int64_t B, int
                argmax_out, n_acc, bonus, crop};
   hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)B), dim3(kThreads), 0, st, fa);
   return launch_status("greedy_accept/finalize");
+}
+
+namespace {
+// Device address of noalloc::scratch per GPU, looked up once per device (with that device current)
+// on the first call that runs there.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int noalloc_scratch(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipStreamGetDevice(st, &dev);
+  TRIDA_CHECK(e == hipSuccess, TRIDA_ERR_LAUNCH, "greedy_accept_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+  TRIDA_CHECK(dev >= 0 && dev < kMaxDevices, TRIDA_ERR_ARG, "greedy_accept_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    TRIDA_CHECK(e == hipSuccess, TRIDA_ERR_LAUNCH, "greedy_accept_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    if (cur != dev) {
+      e = hipSetDevice(dev);
+      TRIDA_CHECK(e == hipSuccess, TRIDA_ERR_LAUNCH, "greedy_accept_noalloc: hipSetDevice: %s", hipGetErrorString(e));
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(noalloc::scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      TRIDA_CHECK(e2 == hipSuccess, TRIDA_ERR_LAUNCH, "greedy_accept_noalloc: hipSetDevice: %s",
+                  hipGetErrorString(e2));
+    }
+    TRIDA_CHECK(e == hipSuccess && p, TRIDA_ERR_LAUNCH, "greedy_accept_noalloc: hipGetSymbolAddress: %s",
+                hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return TRIDA_OK;
+}
+}  // namespace
+
+extern "C" int trida_greedy_accept_noalloc(const void* logits, int dtype, int64_t B, int64_t R, int64_t V,
+                                           int64_t batch_stride, int64_t row_stride, const int64_t* drafts,
+                                           int64_t K, int64_t draft_stride, const int32_t* n_live,
+                                           const int64_t* ctx_len, int64_t* argmax_out, int32_t* n_acc,
+                                           int64_t* bonus, int64_t* crop, int64_t splits, void* stream) {
+  TRIDA_CHECK(dtype == 0 || dtype == 1, TRIDA_ERR_ARG, "greedy_accept_noalloc: logits dtype must be 0 (fp32) or 1 (bf16)");
+  TRIDA_CHECK(B > 0 && R > 0 && V > 0 && V < INT_MAX, TRIDA_ERR_ARG, "greedy_accept_noalloc: bad sizes B=%lld R=%lld V=%lld",
+              (long long)B, (long long)R, (long long)V);
+  const int64_t need = trida_greedy_accept_scratch_bytes(B, R, V, dtype, splits);
+  TRIDA_CHECK(need <= noalloc::kScratchBytes, TRIDA_ERR_WORKSPACE,
+              "greedy_accept_noalloc: B=%lld R=%lld V=%lld needs %lld scratch bytes, above the fixed %lld",
+              (long long)B, (long long)R, (long long)V, (long long)need, (long long)noalloc::kScratchBytes);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(st, &ws);
+  if (rc) return rc;
+  return trida_greedy_accept(logits, dtype, B, R, V, batch_stride, row_stride, drafts, K, draft_stride, n_live,
+                             ctx_len, argmax_out, n_acc, bonus, crop, ws, noalloc::kScratchBytes, splits, stream);
 }
 
 extern "C" int64_t trida_row_argmax_scratch_bytes(int64_t rows, int64_t V, int dtype, int64_t splits) {
