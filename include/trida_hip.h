@@ -96,6 +96,21 @@ int trida_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int
                      float* conf, void* scratch, int64_t scratch_bytes, int64_t splits, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
+ * Banned and gated tokens, in place on logit rows before an argmax or a sampling entry point reads
+ * them. Replaces apply_ban (inference/zoro-1/mlx/trida_mlx/decode.py:76-99), which the reference applies
+ * to greedy and sampled rows, drafts and verify alike.
+ * logits [rows, V] (dtype 0 fp32 / 1 bf16, row stride in elements).
+ * trida_ban_tokens: x[r, ids[j]] = -inf for j < n_ids (ids outside [0, V) are skipped); rows <= 65535.
+ * trida_gate_tokens: per row, lse = logsumexp of the row; for gate g, p = exp(x[r, ids[g]] - lse)
+ *   (written to raw_p [rows, n_gate] fp32 when not NULL; 0 for an id outside [0, V) or a row with no
+ *   finite value), and x[r, ids[g]] = -inf where thr[g] > 0 and p < thr[g]. Every p of a row is taken
+ *   before any gate writes. Apply the ban first (the reference's order). n_gate <= 512. */
+int trida_ban_tokens(void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, const int64_t* ids,
+                     int64_t n_ids, void* stream);
+int trida_gate_tokens(void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, const int64_t* ids,
+                      const float* thr, int64_t n_gate, float* raw_p, void* stream);
+
+/* ------------------------------------------------------------------------------------------------
  * Sampled self-spec acceptance (speculative rejection sampling).
  * Replaces the sampled verify of selfspec_generate (inference/zoro-1/mlx/trida_mlx/decode.py:333-354)
  * with truncated_probs (decode.py:102-130), the role of _ss_sample_verify
@@ -313,7 +328,8 @@ int trida_gdn_restore(const float* snap_state, float* state, const uint16_t* k, 
  *   mask_mode 0 (verify): j <= t;  1 (draft): always;  2 (canvas): j <= t for t < n_clean, else always.
  * out [B, T, Hq, D] bf16 = softmax(scale q k^T) v, times sigmoid(gate) when gate is not NULL (gate
  * element (b, t, h, d) at gate + (b*T + t)*gate_row_stride + h*gate_head_stride + d).
- * KV crop after acceptance is a change of prefix_len only. D in {64, 128, 256}.
+ * KV crop after acceptance is a change of prefix_len only (a prefix_len above Lmax - T is read as
+ * Lmax - T, so keys stay inside the cache). D in {64, 128, 256}.
  * max_keys: an upper bound of prefix_len + T used to plan splits (0 = Lmax); splits 0 = auto.
  * scratch: trida_attn_canvas_scratch_bytes(B, T, Hq, Hkv, D, max_keys, splits) bytes.
  */
@@ -337,7 +353,8 @@ int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t
  * attn_prep: one canvas block of full-attention rows. qkv rows hold [Hq x (q | gate)] [Hkv x k] [Hkv x v]
  *   (each D wide); q and k get a per-head zero-centred RMSNorm and rotate-half RoPE on the first
  *   rot_dim dims at position pos0[b] + t (inv_freq_i = theta^(-2i/rot_dim)); q goes to q_out
- *   [B, T, Hq, D], k and v to the caches [B, Hkv, Lmax, D] at slot slot0[b] + t.
+ *   [B, T, Hq, D], k and v to the caches [B, Hkv, Lmax, D] at slot slot0[b] + t (rows whose slot is
+ *   outside [0, Lmax) write no K / V).
  */
 /* Skinny bf16 GEMM for canvas-sized activations: Y[M, N] = X[M, K] W[N, K]^T (torch Linear weight
  * layout), fp32 accumulation, bf16 output, 1 <= M <= 64, N % 16 == 0, K % 32 == 0. It replaces the

@@ -62,6 +62,42 @@ def greedy_accept(logits: np.ndarray, drafts: np.ndarray, n_live: Optional[np.nd
     return am, n_acc.astype(np.int32), bonus.astype(np.int64), ctx + 1 + n_acc
 
 
+# ------------------------------------------------------------------------------------------ bans
+def apply_ban(x: np.ndarray, banned=(), gate=()) -> np.ndarray:
+    """apply_ban (inference/zoro-1/mlx/trida_mlx/decode.py:76-99) over the last axis: fp32 copy of x with
+    every banned id at -inf, then for each gate (id, thr) with 0 <= id < V and thr > 0, x[..., id] = -inf
+    where the id's probability under the softmax of the banned row, exp(x_id - logsumexp(x)), is below
+    thr. The logsumexp is taken once, before the gates (decode.py:89); ``gate_probs`` gives those raw
+    probabilities."""
+    x = np.array(x, dtype=np.float32, copy=True)
+    V = x.shape[-1]
+    for i in banned:
+        if 0 <= int(i) < V:
+            x[..., int(i)] = -np.inf
+    if gate:
+        p_all = gate_probs(x, gate)
+        for g, (tid, thr) in enumerate(gate):
+            if 0 <= int(tid) < V and thr > 0:
+                x[..., int(tid)] = np.where(p_all[..., g] < thr, np.float32(-np.inf), x[..., int(tid)])
+    return x
+
+
+def gate_probs(x: np.ndarray, gate) -> np.ndarray:
+    """[..., n_gate] float64: exp(x[..., id] - logsumexp(x)) per gate (0 for an id outside [0, V) or a
+    row with no finite value): the raw probability apply_ban compares with each gate's threshold."""
+    x64 = np.asarray(x, np.float64)
+    V = x64.shape[-1]
+    m = np.max(x64, axis=-1, keepdims=True)
+    finite = np.isfinite(m)
+    mm = np.where(finite, m, 0.0)
+    lse = (mm + np.log(np.sum(np.exp(x64 - mm), axis=-1, keepdims=True)))[..., 0]
+    out = np.zeros(x64.shape[:-1] + (len(gate),))
+    for g, (tid, _) in enumerate(gate):
+        if 0 <= int(tid) < V:
+            out[..., g] = np.where(finite[..., 0], np.exp(x64[..., int(tid)] - lse), 0.0)
+    return out
+
+
 # ------------------------------------------------------------------------------------------ sampling
 @dataclass
 class TruncInfo:

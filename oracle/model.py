@@ -283,12 +283,17 @@ def blockspec_generate(m: CpuHybrid, prompt: List[int], max_new: int, block: int
 def blockspec_sample_step(m: CpuHybrid, cache: CpuCache, t0: int, block: int, denoise: int, *, temperature: float,
                           top_k: int, top_p: float, rng):
     """One sampled draft-then-verify step (the rejection-sampling counterpart of blockspec_step):
-    `denoise` passes over [t0, MASK x block]; in each, every still-masked slot's candidate is drawn by
-    inverse CDF from its truncated distribution P_j (decode.py:102-130; MASK banned, qwen3_5_diffusion.py:820) and
-    the per-pass quota of MASK slots with the most probable draws (P_j(x_j), ties to the lower slot)
-    is unmasked, keeping P_j as the slot's q row (the draft distribution, qwen3_5_diffusion.py:779).
-    Then a token-causal verify pass, rejection-sampling acceptance (oracle.accept.rejection_accept,
-    decode.py:333-354) and the rollback to 1 + n_acc rows. Uniforms come from the numpy Generator rng.
+    `denoise` passes over [t0, MASK x block] that unmask the block in ascending slot order. Pass p
+    takes the per[p] lowest still-masked slots; each slot j is drawn by inverse CDF from the truncated
+    distribution P_j (decode.py:102-130; MASK banned, qwen3_5_diffusion.py:820) of its row of that pass's
+    logits (row j predicts slot j), and P_j is kept as the slot's q row (the draft distribution,
+    qwen3_5_diffusion.py:779). The slots a pass takes are fixed before the draws and each q depends only
+    on lower slots, so every draft follows its q given the drafts before it, which is what makes the
+    rejection sampling of the verify pass (oracle.accept.rejection_accept, decode.py:333-354) reproduce
+    the causal distribution; the reference's canvas algorithm has the same property (its specs come
+    from rows that see only lower positions, decode.py:361-378). Then a token-causal verify pass, the
+    acceptance, and the rollback to 1 + n_acc rows. Uniforms come from the numpy Generator rng, in the
+    order: per pass, one per drawn slot; then block acceptance uniforms and one correction/bonus uniform.
     Returns (emitted tokens, next t0, n_acc)."""
     import numpy as np
 
@@ -296,23 +301,20 @@ def blockspec_sample_step(m: CpuHybrid, cache: CpuCache, t0: int, block: int, de
 
     mask = m.mask_id
     canvas = [t0] + [mask] * block
-    masked = [True] * block
     per = [block // denoise + (1 if p < block % denoise else 0) for p in range(denoise)]
     V = m.cfg.vocab
     q = np.zeros((block, V))
+    s0 = 0
     for p in range(denoise):
         L = m.forward(canvas, cache, "draft")
         cache.pending = None
-        live = [j for j in range(block) if masked[j]]
-        P = A.truncated_probs(L[live].numpy(), temperature, top_k, top_p, mask)
-        u = rng.random(len(live))
-        x = {j: A.sample_inverse_cdf(P[i], float(u[i]))[0] for i, j in enumerate(live)}
-        prob = {j: P[i, x[j]] for i, j in enumerate(live)}
-        cand = sorted(live, key=lambda j: (-prob[j], j))
-        for j in cand[: per[p]]:
-            canvas[1 + j] = x[j]
-            masked[j] = False
-            q[j] = P[live.index(j)]
+        slots = list(range(s0, s0 + per[p]))
+        P = A.truncated_probs(L[slots].numpy(), temperature, top_k, top_p, mask)
+        u = rng.random(len(slots))
+        for i, j in enumerate(slots):
+            canvas[1 + j] = A.sample_inverse_cdf(P[i], float(u[i]))[0]
+            q[j] = P[i]
+        s0 += per[p]
     L = m.forward(canvas, cache, "verify")
     res = A.rejection_accept(L[None].numpy(), q[None], np.asarray([canvas[1:]], np.int64), rng.random((1, block)),
                              rng.random(1), temperature=temperature, top_k=top_k, top_p=top_p, mask_id=mask)

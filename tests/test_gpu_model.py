@@ -246,7 +246,7 @@ def test_engine_modes_agree(gpu, pair):
     for mode, n, d in (("causal", None, 0), ("self-spec", 4, 0), ("self-spec", 8, 2)):
         eng = Engine(rt, mode=mode, gen_block=n, denoise_steps=d)
         toks = []
-        for ch in eng.generate_ids(p, max_tokens=40):
+        for ch in eng.generate_ids(p, max_tokens=40, sampling=SamplingParams(temperature=0.0)):
             toks.extend(ch)
         outs.append(toks)
         assert eng.last_stats["new_tokens"] == 40
@@ -328,8 +328,9 @@ def test_engine_from_checkpoint_directory(gpu, tmp_path):
     e2 = Engine(TridaRuntime(CFG, w, device=DEV), mode="self-spec", gen_block=4)
     assert e1.eos_ids == {CFG.vocab - 2} and e1.mask_id == CFG.mask_id
     p = prompt(19, seed=12)
-    a = collect(e1.generate_ids(p, max_tokens=40, stop_ids=set()))
-    b = collect(e2.generate_ids(p, max_tokens=40, stop_ids=e1.eos_ids))
+    g = SamplingParams(temperature=0.0)
+    a = collect(e1.generate_ids(p, max_tokens=40, stop_ids=set(), sampling=g))
+    b = collect(e2.generate_ids(p, max_tokens=40, stop_ids=e1.eos_ids, sampling=g))
     assert a == b
 
 

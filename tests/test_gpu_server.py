@@ -8,6 +8,7 @@ import threading
 import pytest
 
 from trida_stack_amd import server as S
+from trida_stack_amd.decode import SamplingParams
 from trida_stack_amd.engine import Engine
 from trida_stack_amd.model import HybridConfig, TridaRuntime, init_weights
 
@@ -30,7 +31,7 @@ def test_served_tokens_equal_engine_output(gpu):
     rng = random.Random(5)
     prompt = [rng.randrange(0, cfg.vocab - 10) for _ in range(23)]
     ref = []
-    for ch in eng.generate_ids(prompt, max_tokens=30):
+    for ch in eng.generate_ids(prompt, max_tokens=30, sampling=SamplingParams(temperature=0.0)):
         ref.extend(ch)
     st = S.ServerState(eng, None, model_name="random-tiny")
     srv = S.make_server(st, "127.0.0.1", 0)
@@ -42,13 +43,13 @@ def test_served_tokens_equal_engine_output(gpu):
         r = json.loads(data)
         assert r["choices"][0]["token_ids"] == ref
         assert r["usage"]["completion_tokens"] == len(ref) and r["usage"]["trida"]["forwards"] > 0
-        code, data = post(port, "/v1/completions", {"prompt": prompt, "max_tokens": 30, "stream": True})
+        code, data = post(port, "/v1/completions", {"prompt": prompt, "max_tokens": 30, "stream": True, "temperature": 0})
         ids = []
         for block in data.split("\n\n"):
             if block.startswith("data: {"):
                 ids.extend(json.loads(block[6:])["choices"][0].get("token_ids", []))
         assert code == 200 and ids == ref
-        code, data = post(port, "/v1/completions", {"prompt": prompt, "max_tokens": 30, "mode": "causal"})
+        code, data = post(port, "/v1/completions", {"prompt": prompt, "max_tokens": 30, "mode": "causal", "temperature": 0})
         assert code == 200 and json.loads(data)["choices"][0]["token_ids"] == ref  # greedy AR == greedy self-spec
     finally:
         srv.shutdown()

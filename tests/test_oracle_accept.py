@@ -196,3 +196,33 @@ def test_truncated_probs_top_k_ties_follow_topk_list():
     # top-k alone keeps the ties at the k-th value as well
     P = A.truncated_probs(x, 1.0, 2, 1.0)
     assert np.nonzero(P[0])[0].tolist() == [0, 1, 2, 3]
+
+
+def test_apply_ban_hand_case():
+    """apply_ban (decode.py:76-99): the gate compares against the probability under the *banned* row.
+    p = (0.5, 0.3, 0.2); banning token 2 makes token 1's probability 0.3 / 0.8 = 0.375, so a gate of
+    0.35 keeps it (taken before the ban, 0.3 < 0.35 would drop it), and a gate of 0.4 drops it."""
+    x = np.log(np.array([[0.5, 0.3, 0.2]], np.float32))
+    y = A.apply_ban(x, banned=(2,), gate=((1, 0.35),))
+    assert np.isneginf(y[0, 2]) and np.isfinite(y[0, 1]) and y[0, 0] == x[0, 0]
+    y = A.apply_ban(x, banned=(2,), gate=((1, 0.4), (0, 0.6), (7, 0.9), (0, 0.0)))
+    assert np.isneginf(y[0, 1]) and np.isfinite(y[0, 0])  # p0 = 0.625 >= 0.6; id 7 and thr 0 are ignored
+    assert np.allclose(A.gate_probs(A.apply_ban(x, banned=(2,)), ((1, 0.4), (0, 0.6)))[0], [0.375, 0.625])
+
+
+def test_apply_ban_matches_softmax_brute_force():
+    rng = np.random.default_rng(4)
+    x = (rng.normal(size=(5, 40)) * 2).astype(np.float32)
+    gate = ((3, 0.05), (11, 0.02), (3, 0.01))
+    y = A.apply_ban(x, banned=(0, 39, 77), gate=gate)
+    for r in range(5):
+        row = x[r].astype(np.float64).copy()
+        row[[0, 39]] = -np.inf
+        p = np.exp(row - row.max())
+        p /= p.sum()
+        exp = row.copy()
+        for tid, thr in gate:
+            if p[tid] < thr:
+                exp[tid] = -np.inf
+        assert np.array_equal(np.isneginf(y[r]), np.isneginf(exp))
+        assert np.array_equal(y[r][np.isfinite(y[r])], x[r][np.isfinite(y[r])])

@@ -135,7 +135,9 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   const int M = a.T * a.G;
   const int m0 = qt * kMT;
   const int rows = min(kMT, M - m0);
-  const int prefix = a.prefix[b];
+  // a prefix past the cache capacity (a caller's overlong decode) is clamped so that every key read
+  // stays inside this sequence's [Lmax, D] rows
+  const int prefix = min(max(a.prefix[b], 0), a.Lmax - a.T);
   const int nk = prefix + a.T;
   const int nblk = (nk + kKB - 1) / kKB;
   const int bps = (nblk + a.S - 1) / a.S;

@@ -198,6 +198,9 @@ __global__ __launch_bounds__(kThreads) void attn_prep_kernel(AttnPrepArgs a) {
     wnv[j] = bf2f(wn[l * per + j]);
   }
   const int64_t slot = (int64_t)a.slot0[bb] + t;
+  // rows past the cache capacity (a caller's overlong decode) write no K / V (one (t, head) per wave,
+  // so the whole wave leaves together)
+  if (kind != 0 && (slot < 0 || slot >= a.Lmax)) return;
   if (kind == 2) {
     uint16_t* dst = a.v_cache + (((int64_t)bb * a.Hkv + h) * a.Lmax + slot) * a.D + l * per;
     for (int j = 0; j < per; ++j) dst[j] = f2bf(v[j]);

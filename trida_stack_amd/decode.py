@@ -18,6 +18,7 @@ numerics (the verify rows are the AR computation).
 """
 from __future__ import annotations
 
+import collections
 import time
 from dataclasses import dataclass, field
 from typing import Iterator, List, Optional
@@ -34,10 +35,77 @@ class SamplingParams:
     top_k: int = 50
     top_p: float = 0.95
     seed: Optional[int] = None
+    # token ids that are never produced (greedy and sampled rows, drafts and verify alike)
+    banned: tuple = ()
+    # ((token id, min raw probability), ...): the token is allowed only where its probability under the
+    # raw logits (temperature 1, no top-k / top-p, after the ban) is at least that value
+    gate: tuple = ()
+    # when a list: (raw probability, gate) of every exact causal row where a gated token was blocked
+    # although the model gave it >= GATE_NOTE_MIN
+    gate_log: Optional[list] = None
 
     @property
     def greedy(self) -> bool:
         return self.temperature <= 0
+
+
+GATE_NOTE_MIN = 0.05
+
+
+class LogitRules:
+    """SamplingParams.banned / gate in device form for one decode: apply() runs apply_ban
+    (inference/zoro-1/mlx/trida_mlx/decode.py:76-99) in place on logit rows (trida_ban_tokens, then
+    trida_gate_tokens), and note() records near-miss gate blocks of exact causal rows into
+    sp.gate_log (_gate_note, decode.py:63-73). Inactive rules cost nothing."""
+
+    def __init__(self, sp: SamplingParams, device: torch.device):
+        dev = torch.device(device)
+        ban = sorted({int(i) for i in (sp.banned or ())})
+        self.ban = torch.tensor(ban, dtype=torch.int64, device=dev) if ban else None
+        gates = [(int(t), float(th)) for t, th in (sp.gate or ())]
+        self.gates = gates
+        self.gate_ids = torch.tensor([g[0] for g in gates], dtype=torch.int64, device=dev) if gates else None
+        self.gate_thr = torch.tensor([g[1] for g in gates], dtype=torch.float32, device=dev) if gates else None
+        self.log = sp.gate_log if gates else None
+
+    @property
+    def active(self) -> bool:
+        return self.ban is not None or self.gate_ids is not None
+
+    @property
+    def n_gate(self) -> int:
+        return len(self.gates)
+
+    def apply(self, logits: torch.Tensor, raw_p: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """logits [..., V] (fp32 or bf16, evenly strided rows) with the rules applied, in place; raw_p
+        [rows, n_gate] fp32 receives the gated tokens' raw probabilities."""
+        if self.ban is not None:
+            K.ban_tokens(logits, self.ban)
+        if self.gate_ids is not None:
+            K.gate_tokens(logits, self.gate_ids, self.gate_thr, raw_p)
+        return logits
+
+    def raw_buffer(self, rows: int, device) -> Optional[torch.Tensor]:
+        """A raw-probability buffer for `rows` rows when gate notes are wanted, else None."""
+        if self.log is None:
+            return None
+        return torch.zeros(rows, self.n_gate, dtype=torch.float32, device=device)
+
+    def note(self, raw_rows) -> None:
+        """raw_rows: host lists of per-gate raw probabilities of exact causal rows."""
+        if self.log is None:
+            return
+        for row in raw_rows:
+            for (tid, thr), p in zip(self.gates, row):
+                if thr > 0 and GATE_NOTE_MIN <= p < thr:
+                    self.log.append((round(float(p), 4), thr))
+
+
+def apply_ban(x: torch.Tensor, sp: SamplingParams) -> torch.Tensor:
+    """x [..., V] on the GPU with sp.banned at -inf and sp.gate applied, in place (apply_ban,
+    decode.py:76-99; greedy and sampled alike, drafts and verify alike)."""
+    r = LogitRules(sp, x.device)
+    return r.apply(x) if r.active else x
 
 
 @dataclass
@@ -50,6 +118,8 @@ class DecodeStats:
     cold_forwards: int = 0
     steps: int = 0
     accept_hist: list = field(default_factory=list)
+    gate_blocked: list = field(default_factory=list)  # raw probabilities of blocked gated tokens (>= 0.05)
+    loop_stopped_thinking: bool = False  # the loop guard closed the thinking and the model answered after it
     prefill_s: float = 0.0
     decode_s: float = 0.0
     finish_reason: str = "length"
@@ -69,14 +139,78 @@ class DecodeStats:
                 "steps": self.steps, "tokens_per_forward": round(self.tokens_per_forward, 3),
                 "accept_hist": self.accept_hist, "prefill_s": round(self.prefill_s, 4),
                 "decode_s": round(self.decode_s, 4), "decode_tok_s": round(self.decode_tps, 2),
-                "finish_reason": self.finish_reason}
+                "finish_reason": self.finish_reason,
+                **({"gate_blocked": self.gate_blocked} if self.gate_blocked else {}),
+                **({"loop_stopped_thinking": True} if self.loop_stopped_thinking else {})}
+
+
+# ----------------------------------------------------------------------------- loop guard
+# Thresholds of the reference's loop guard (decode.py:172-217): a block repeated LOOP_MIN_REPEATS times
+# back to back spanning >= LOOP_MIN_SPAN tokens, or a LOOP_WINDOW-token window in which at least
+# LOOP_REPEAT_FRAC of the positions end a LOOP_NGRAM-token phrase seen before in the window.
+LOOP_MIN_REPEATS = 6
+LOOP_MIN_SPAN = 96
+LOOP_MAX_PERIOD = 256
+LOOP_NGRAM = 16
+LOOP_WINDOW = 1536
+LOOP_REPEAT_FRAC = 0.5
+
+
+def looping(hist: list) -> int:
+    """The period p of a block that ends `hist` repeated LOOP_MIN_REPEATS times back to back (the tail of
+    max(p * LOOP_MIN_REPEATS, LOOP_MIN_SPAN) tokens equals itself shifted by p), for the smallest such
+    p <= LOOP_MAX_PERIOD; 0 when there is none."""
+    n = len(hist)
+    for p in range(1, min(LOOP_MAX_PERIOD, n // LOOP_MIN_REPEATS) + 1):
+        span = max(p * LOOP_MIN_REPEATS, LOOP_MIN_SPAN)
+        if span > n:
+            break
+        if all(hist[i] == hist[i - p] for i in range(n - span + p, n)):
+            return p
+    return 0
+
+
+class NgramLoop:
+    """Sliding-window repeat detector (decode.py:198-225): over the last `window` positions, the count
+    of positions whose `n`-token phrase already occurred in the window."""
+
+    def __init__(self, n: int = LOOP_NGRAM, window: int = LOOP_WINDOW, frac: float = LOOP_REPEAT_FRAC):
+        self.n, self.window, self.frac = n, window, frac
+        self.seen: dict = {}
+        self.recent = collections.deque()
+        self.repeats = 0
+
+    def add(self, hist: list) -> bool:
+        """Feeds the history after one new token; True once the window is full and mostly repeats."""
+        if len(hist) < self.n:
+            return False
+        key = tuple(hist[-self.n:])
+        was = self.seen.get(key, 0) > 0
+        self.seen[key] = self.seen.get(key, 0) + 1
+        self.recent.append((key, was))
+        self.repeats += was
+        if len(self.recent) > self.window:
+            k, w = self.recent.popleft()
+            self.repeats -= w
+            left = self.seen[k] - 1
+            if left:
+                self.seen[k] = left
+            else:
+                del self.seen[k]
+        return len(self.recent) == self.window and self.repeats >= self.frac * self.window
 
 
 class _Emitter:
-    """Applies max_new_tokens / EOS to emitted chunks and records stats (decode.py:228-257)."""
+    """Applies max_new_tokens / EOS / the loop guard to emitted chunks and records stats
+    (decode.py:228-257). The loop guard is off unless the class attribute is set (the server's
+    --loop-guard)."""
+
+    loop_guard = False
 
     def __init__(self, stats: DecodeStats, max_new: int, eos: set):
         self.stats, self.max_new, self.eos, self.done = stats, max_new, eos, False
+        self.hist: list = []
+        self.ngram = NgramLoop()
 
     def __call__(self, toks: list) -> list:
         out = []
@@ -87,12 +221,25 @@ class _Emitter:
                 self.stats.stop_token = t
                 break
             out.append(t)
+            self.hist.append(t)
             if self.stats.new_tokens + len(out) >= self.max_new:
                 self.done = True
                 self.stats.finish_reason = "length"
                 break
+            if self.loop_guard and ((len(self.hist) % 8 == 0 and looping(self.hist)) or self.ngram.add(self.hist)):
+                self.done = True
+                self.stats.finish_reason = "repetition"
+                break
         self.stats.new_tokens += len(out)
         return out
+
+
+def _room(cache: SeqCache, T: int) -> None:
+    """A forward of T rows must fit every sequence's KV cache (the kernels take the committed lengths
+    from the device and would write past the capacity)."""
+    need = max(len(t) for t in cache.tokens) + T
+    if need > cache.Lmax:
+        raise ValueError(f"KV cache capacity {cache.Lmax} exceeded ({need} positions needed)")
 
 
 def _argmax1(logits: torch.Tensor) -> int:
@@ -102,14 +249,28 @@ def _argmax1(logits: torch.Tensor) -> int:
 
 def _prefill(rt: TridaRuntime, cache: SeqCache, prompt: list, stats: DecodeStats) -> torch.Tensor:
     t = time.perf_counter()
-    todo = prompt[len(cache.tokens[0]):]
-    stats.prompt_tokens, stats.reused_tokens = len(prompt), len(cache.tokens[0])
+    held = cache.tokens[0]
+    if prompt[: len(held)] != held:
+        raise ValueError("the cache holds tokens that are not a prefix of the prompt")
+    todo = prompt[len(held):]
+    stats.prompt_tokens, stats.reused_tokens = len(prompt), len(held)
     if not todo:
         raise ValueError("prompt fully cached; callers must leave at least one token to prefill")
+    _room(cache, len(todo))
     logits = rt.prefill(cache, todo)
     torch.cuda.synchronize(rt.dev)
     stats.prefill_s = time.perf_counter() - t
     return logits
+
+
+def _greedy_row(rules: LogitRules, logits: torch.Tensor, note: bool = True) -> int:
+    """The argmax of one exact causal row after the ban / gate rules (which also note gate blocks)."""
+    if rules.active:
+        raw = rules.raw_buffer(1, logits.device) if note else None
+        rules.apply(logits.reshape(1, -1), raw)
+        if raw is not None:
+            rules.note(raw.tolist())
+    return _argmax1(logits)
 
 
 # ----------------------------------------------------------------------------- AR
@@ -124,16 +285,18 @@ def ar_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_toke
                                       stats=stats)
         return
     stats.mode = "causal"
+    rules = LogitRules(sp, rt.dev)
     logits = _prefill(rt, cache, prompt, stats)
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     t = time.perf_counter()
     while True:
-        tok = _argmax1(logits)
+        tok = _greedy_row(rules, logits)
         out = emit([tok])
         if out:
             yield out
         if emit.done:
             break
+        _room(cache, 1)
         logits = rt.ar_step(cache, tok)
         stats.forwards += 1
     stats.decode_s = time.perf_counter() - t
@@ -142,33 +305,39 @@ def ar_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_toke
 # ----------------------------------------------------------------------------- pure block diffusion
 def diffusion_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
                        mask_id: int, canvas: int = 32, threshold: float = 0.9, max_steps: Optional[int] = None,
-                       stats: Optional[DecodeStats] = None) -> Iterator[list]:
+                       stats: Optional[DecodeStats] = None, sp: Optional[SamplingParams] = None) -> Iterator[list]:
     """Greedy block diffusion with the LowConfidenceShift commit gate (qwen3_5_diffusion.py:449-632,
     1180-1270). A block [seed, MASK x (canvas - 1)] is denoised by draft passes (prefix plus the whole
     block visible; MASK rows read the block-end GDN state): position i takes the prediction of the
     logits of position i - 1 when its softmax confidence exceeds `threshold`, or, when no masked
     position passes, only the most confident one does (first on ties); rounds repeat until no mask is
     left or `max_steps` (default: canvas) ran. A causal forward then commits the block; the whole
-    block is emitted and the argmax of its last logit seeds the next one."""
+    block is emitted and the argmax of its last logit seeds the next one. sp.banned / sp.gate apply to
+    every row read."""
     stats = stats or DecodeStats()
     stats.mode = "diffusion"
+    rules = LogitRules(sp or SamplingParams(temperature=0.0), rt.dev)
     CL = int(canvas)
     if CL < 2:
         raise ValueError("canvas must hold the seed and at least one masked position")
     max_steps = CL if max_steps is None else int(max_steps)
-    seed = _argmax1(_prefill(rt, cache, prompt, stats))
+    seed = _greedy_row(rules, _prefill(rt, cache, prompt, stats))
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     dev = rt.dev
     ids = torch.full((1, CL), mask_id, dtype=torch.int64, device=dev)
     neg = torch.tensor(float("-inf"), device=dev)
     t = time.perf_counter()
     while True:
+        _room(cache, CL)
         ids.fill_(mask_id)
         ids[0, 0] = seed
         for _ in range(max_steps):
             logits = rt.draft(cache, ids)[0]
             stats.forwards += 1
-            pred, conf = K.row_argmax(logits[: CL - 1])  # row i - 1 predicts position i
+            rows = logits[: CL - 1]  # row i - 1 predicts position i
+            if rules.active:
+                rules.apply(rows)
+            pred, conf = K.row_argmax(rows)
             cur = ids[0, 1:]
             masked = cur == mask_id
             score = torch.where(masked, conf, neg)
@@ -188,7 +357,7 @@ def diffusion_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_n
             yield out
         if emit.done:
             break
-        seed = _argmax1(logits)
+        seed = _greedy_row(rules, logits)
     stats.decode_s = time.perf_counter() - t
 
 
@@ -198,7 +367,7 @@ def selfspec_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_ne
                       denoise_steps: int = 0) -> Iterator[list]:
     """Self-speculative decoding (decode.py:297-387); see the module docstring for the two variants.
     Sampling parameters with temperature > 0 run the rejection-sampling versions of both variants
-    (trida_stack_amd.sampling)."""
+    (trida_stack_amd.sampling). sp.banned / sp.gate apply to every row read (drafts and verify)."""
     if not sp.greedy:
         from . import sampling as S
 
@@ -213,27 +382,34 @@ def selfspec_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_ne
         return
     if denoise_steps > 0:
         yield from _blockspec(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids, mask_id=mask_id,
-                              block=n, denoise=denoise_steps, stats=stats)
+                              block=n, denoise=denoise_steps, stats=stats, sp=sp)
         return
     stats = stats or DecodeStats()
     stats.mode = f"self-spec(N={n})"
     stats.accept_hist = [0] * n
+    rules = LogitRules(sp, rt.dev)
     blk, Kd = 2 * n - 1, n - 1
     logits = _prefill(rt, cache, prompt, stats)
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     t_start = time.perf_counter()
-    t0 = _argmax1(logits)
+    t0 = _greedy_row(rules, logits)
     t0_emitted = False
     pending = specs = None
     dev = rt.dev
+    raw = rules.raw_buffer(blk, dev)
     while not emit.done:
+        _room(cache, blk)
         if specs is not None:  # ---- verify round
             L = rt.canvas(cache, [pending] + specs + [mask_id] * (n - 1), n, as_float=False)
             stats.forwards += 1
+            if rules.active:
+                rules.apply(L, raw)
             drafts = torch.as_tensor([specs], dtype=torch.int64, device=dev)
             am, n_acc, _, _ = K.greedy_accept(L[None], drafts)
             vals = am[0].tolist()
             acc = int(n_acc[0])
+            if raw is not None:  # rows that saw real context (decode.py:358)
+                rules.note(raw[: acc + 1 if acc < Kd else n].tolist())
             if acc < Kd:  # rejected at spec `acc`: emit accepted specs + correction, next step cold
                 rt.commit(cache, 1 + acc)
                 stats.accept_hist[acc] += 1
@@ -249,6 +425,10 @@ def selfspec_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_ne
             L = rt.canvas(cache, [t0] + [mask_id] * (blk - 1), n, rows=n if rt.skip_rows else None, as_float=False)
             stats.forwards += 1
             stats.cold_forwards += 1
+            if rules.active:
+                rules.apply(L[:n], None if raw is None else raw[:n])
+                if raw is not None:
+                    rules.note(raw[:1].tolist())
             am, _ = K.row_argmax(L[:n], want_conf=False)
             vals = am.tolist()
             rt.commit(cache, 1)
@@ -265,10 +445,14 @@ class BlockSpecStep:
     replayed from a HIP graph): denoise passes, verify, greedy acceptance, rollback.
 
     Inputs: t0 [B] int64 (the pending token, already emitted). Outputs after run(): canvas [B, block+1]
-    (row 0 = t0, rows 1.. = drafts), n_acc [B] int32, bonus [B] int64 (next t0)."""
+    (row 0 = t0, rows 1.. = drafts), n_acc [B] int32, bonus [B] int64 (next t0). rules: the ban / gate
+    rules of the decode (applied to every draft and verify row), or None; with gate notes wanted,
+    raw_p [B, block+1, n_gate] holds the verify rows' raw gate probabilities."""
 
-    def __init__(self, rt: TridaRuntime, cache: SeqCache, block: int, denoise: int):
+    def __init__(self, rt: TridaRuntime, cache: SeqCache, block: int, denoise: int,
+                 rules: Optional[LogitRules] = None):
         self.rt, self.cache, self.block, self.denoise = rt, cache, block, denoise
+        self.rules = rules if rules is not None and rules.active else None
         B = cache.B
         dev = rt.dev
         self.per = [block // denoise + (1 if p < block % denoise else 0) for p in range(denoise)]
@@ -283,6 +467,9 @@ class BlockSpecStep:
         self.crop = torch.empty(B, dtype=torch.int64, device=dev)
         self.d_am = torch.empty(B, block + 1, dtype=torch.int64, device=dev)
         self.d_conf = torch.empty(B, block + 1, dtype=torch.float32, device=dev)
+        self.raw_p = None
+        if self.rules is not None and self.rules.log is not None:
+            self.raw_p = torch.zeros(B, block + 1, self.rules.n_gate, dtype=torch.float32, device=dev)
 
     def run(self) -> None:
         rt, cache, blk = self.rt, self.cache, self.block
@@ -291,6 +478,8 @@ class BlockSpecStep:
         self.masked.fill_(True)
         for p in range(self.denoise):
             L = rt.forward(self.canvas, cache, "draft")
+            if self.rules is not None:
+                self.rules.apply(L)
             # row j predicts slot j + 1 (shift readout); the last row is not used
             with K.timed("row_argmax"):
                 K.row_argmax(L, out=(self.d_am, self.d_conf))
@@ -298,6 +487,8 @@ class BlockSpecStep:
             K.unmask_top(self.d_am, self.d_conf, self.masked, self.canvas, self.per[p])
         vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
+        if self.rules is not None:
+            self.rules.apply(L, self.raw_p)
         self.ctx.copy_(cache.length)
         with K.timed("greedy_accept"):
             K.greedy_accept(L, self.canvas[:, 1:], ctx_len=self.ctx, out=(self.am, self.n_acc, self.bonus, self.crop))
@@ -341,21 +532,23 @@ class BlockSpecStep:
 
 def _blockspec(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
                mask_id: int, block: int, denoise: int, stats: Optional[DecodeStats],
-               graph: bool = True) -> Iterator[list]:
+               sp: Optional[SamplingParams] = None, graph: bool = True) -> Iterator[list]:
     stats = stats or DecodeStats()
     stats.mode = f"self-spec(block={block}, denoise={denoise})"
     stats.accept_hist = [0] * (block + 1)
+    rules = LogitRules(sp or SamplingParams(temperature=0.0), rt.dev)
     logits = _prefill(rt, cache, prompt, stats)
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     t_start = time.perf_counter()
-    step = BlockSpecStep(rt, cache, block, denoise)
-    t0 = _argmax1(logits)
+    step = BlockSpecStep(rt, cache, block, denoise, rules)
+    t0 = _greedy_row(rules, logits)
     out = emit([t0])
     if out:
         yield out
     step.t0.fill_(t0)
     use_graph = graph and rt.dev.type == "cuda"
     while not emit.done:
+        _room(cache, block + 1)
         if use_graph and step.graph is None and stats.steps >= 1:
             step.capture()
         if step.graph is not None:
@@ -366,6 +559,8 @@ def _blockspec(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_token
         stats.steps += 1
         packed = torch.cat([step.canvas[0, 1:], step.bonus[:1], step.n_acc[:1].to(torch.int64)]).tolist()
         acc = packed[-1]
+        if step.raw_p is not None:
+            rules.note(step.raw_p[0, : acc + 1].tolist())
         cache.tokens[0].extend([t0] + packed[:acc])  # the committed rows: pending token + accepted drafts
         cache.ctx_hint = len(cache.tokens[0])
         stats.accept_hist[acc] += 1

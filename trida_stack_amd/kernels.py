@@ -185,6 +185,57 @@ def unmask_top(argmax: torch.Tensor, conf: torch.Tensor, masked: torch.Tensor, c
     _lib.check(rc, "trida_unmask_top")
 
 
+def _rows2d(logits: torch.Tensor):
+    """(rows, V, row stride) of logits [..., V] whose rows are evenly strided (a row-major view)."""
+    V = logits.shape[-1]
+    if logits.stride(-1) != 1:
+        raise ValueError("logits rows must have a contiguous last dim")
+    rows, rs, expect = 1, None, None
+    for n, st in zip(reversed(logits.shape[:-1]), reversed(logits.stride()[:-1])):
+        rows *= n
+        if n == 1:
+            continue
+        if rs is None:
+            rs = st
+        elif st != expect:
+            raise ValueError("logits rows must be evenly strided")
+        expect = st * n
+    return rows, V, (rs if rs is not None else V)
+
+
+def ban_tokens(logits: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """logits[..., id] = -inf in place for every id of ids (int64 [n]), the ban of apply_ban
+    (inference/zoro-1/mlx/trida_mlx/decode.py:76-99). logits fp32 or bf16 with evenly strided rows."""
+    dev = _need_gpu(logits, ids)
+    dt = _logit_dtype(logits)
+    if ids.dtype != torch.int64 or ids.dim() != 1 or not ids.is_contiguous():
+        raise ValueError("ids must be a contiguous int64 [n] tensor")
+    rows, V, rs = _rows2d(logits)
+    rc = _lib.load().trida_ban_tokens(logits.data_ptr(), dt, rows, V, rs, ids.data_ptr(), ids.numel(), _stream(dev))
+    _lib.check(rc, "trida_ban_tokens")
+    return logits
+
+
+def gate_tokens(logits: torch.Tensor, ids: torch.Tensor, thr: torch.Tensor,
+                raw_p: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The gate of apply_ban (decode.py:88-98), in place: per row, token ids[g] is set to -inf where its
+    probability under the row's softmax, p = exp(x_id - logsumexp(x)), is below thr[g] > 0. raw_p
+    [rows, n] fp32 (optional) receives every p. ids int64 [n], thr fp32 [n]."""
+    dev = _need_gpu(logits, ids, thr, raw_p)
+    dt = _logit_dtype(logits)
+    if ids.dtype != torch.int64 or thr.dtype != torch.float32 or ids.shape != thr.shape or ids.dim() != 1 \
+            or not ids.is_contiguous() or not thr.is_contiguous():
+        raise ValueError("ids (int64 [n]) and thr (fp32 [n]) must be contiguous and of one length")
+    rows, V, rs = _rows2d(logits)
+    if raw_p is not None and (raw_p.dtype != torch.float32 or raw_p.numel() < rows * ids.numel()
+                              or not raw_p.is_contiguous()):
+        raise ValueError("raw_p must be a contiguous fp32 tensor of rows * n elements")
+    rc = _lib.load().trida_gate_tokens(logits.data_ptr(), dt, rows, V, rs, ids.data_ptr(), thr.data_ptr(), ids.numel(),
+                                       _ptr(raw_p), _stream(dev))
+    _lib.check(rc, "trida_gate_tokens")
+    return logits
+
+
 # --------------------------------------------------------------------------------------------------
 # Sampled acceptance (temperature / top-k / top-p, speculative rejection sampling)
 MAX_TOP_K = 4096

@@ -226,6 +226,7 @@ class TridaRuntime:
         self._scratch: Dict[tuple, _Scratch] = {}
         self.skip_rows = False
         self.mask_id = cfg.mask_id
+        self.progress_cb = None  # optional fn(tokens done this call) after each prefill chunk (model.py:241)
 
     # ---------------------------------------------------------------- cache
     def make_cache(self, batch: int = 1, max_len: int = 4096) -> SeqCache:
@@ -240,6 +241,19 @@ class TridaRuntime:
             length=torch.zeros(batch, dtype=torch.int32, device=self.dev),
             pos=torch.zeros(batch, dtype=torch.int32, device=self.dev),
             tokens=[[] for _ in range(batch)])
+
+    def grow_cache(self, cache: SeqCache, max_len: int) -> None:
+        """Raises the KV capacity of `cache` to max_len positions in place (the committed entries are
+        copied; the recurrent state and conv windows do not depend on the capacity)."""
+        if max_len <= cache.Lmax:
+            return
+        A = cache.kv_k.shape[0]
+        shape = (A, cache.B, self.cfg.n_kv_heads, max_len, self.cfg.head_dim)
+        for name in ("kv_k", "kv_v"):
+            old = getattr(cache, name)
+            new = torch.zeros(shape, dtype=old.dtype, device=old.device)
+            new[:, :, :, : old.shape[3]].copy_(old)
+            setattr(cache, name, new)
 
     def scratch(self, B: int, T: int) -> _Scratch:
         key = (B, T)
@@ -282,9 +296,10 @@ class TridaRuntime:
             return torch.matmul(x, w.t(), out=out)
 
     def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
-                rows: Optional[int] = None, seq: Optional[slice] = None) -> torch.Tensor:
+                rows: Optional[int] = None, seq: Optional[slice] = None, row0: int = 0) -> torch.Tensor:
         """One forward of a [B, T] block of token ids (device int64) on top of the cache.
-        Returns bf16 logits [B, rows or T, V]. seq restricts the forward to a contiguous range of the
+        Returns bf16 logits [B, rows, V] of block rows row0 .. row0 + rows - 1 (default: every row; the
+        LM head runs on those rows only). seq restricts the forward to a contiguous range of the
         cache's sequences (used by per-sequence prefill of ragged prompts)."""
         c, w = self.cfg, self.w
         B, T = ids.shape
@@ -371,8 +386,8 @@ class TridaRuntime:
             self._mm(s.act, w[p + "w_down"], s.r)
         K.add_rmsnorm(s.h, s.r, w["final_norm"], s.x, eps=c.rms_eps)
         x = s.x.view(B, T, -1)
-        if rows is not None:
-            x = x[:, :rows]
+        if rows is not None or row0:
+            x = x[:, row0: row0 + (rows if rows is not None else T - row0)]
         with K.timed("lm_head"):
             logits = self._mm(x.reshape(-1, x.shape[-1]), w.get("lm_head", w["embed"])).view(B, x.shape[1], -1)
         fwd_timer.__exit__(None, None, None)
@@ -396,10 +411,14 @@ class TridaRuntime:
         assert cache.pending is None and tokens
         logits = None
         sl = slice(seq, seq + 1)
+        if len(cache.tokens[seq]) + len(tokens) > cache.Lmax:
+            raise ValueError(f"KV cache capacity {cache.Lmax} exceeded by a prefill of {len(tokens)} tokens")
         for s0 in range(0, len(tokens), self.prefill_chunk):
             chunk = tokens[s0: s0 + self.prefill_chunk]
             logits = self.forward(self._ids(chunk), cache, "causal", seq=sl)
             cache.tokens[seq].extend(chunk)
+            if self.progress_cb is not None:
+                self.progress_cb(len(chunk))
         return logits[0, -1].float()
 
     def ar_step(self, cache: SeqCache, token: int) -> torch.Tensor:

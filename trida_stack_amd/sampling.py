@@ -32,6 +32,8 @@ class Sampler:
     """Seeded sampling of truncated distributions on the device (one generator per decode)."""
 
     def __init__(self, sp, device: torch.device, ban_id: int = -1):
+        from .decode import LogitRules
+
         if sp.temperature <= 0:
             raise ValueError("Sampler needs temperature > 0 (temperature 0 is greedy decoding)")
         if sp.top_k > K.MAX_TOP_K:
@@ -45,6 +47,12 @@ class Sampler:
         else:
             self.gen.manual_seed(int(sp.seed))
         self.bad = torch.zeros(1, dtype=torch.int32, device=self.dev)  # any nonzero kernel status so far
+        # sp.banned / sp.gate (apply_ban, decode.py:76-99), applied once to each fp32 row buffer by prepare()
+        self.rules = LogitRules(sp, self.dev)
+
+    def prepare(self, lf: torch.Tensor, raw_p: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """fp32 logit rows [..., V] with the ban / gate rules applied in place (before any statistics)."""
+        return self.rules.apply(lf, raw_p) if self.rules.active else lf
 
     def uniform(self, *shape) -> torch.Tensor:
         return torch.rand(shape, generator=self.gen, device=self.dev, dtype=torch.float32)
@@ -58,7 +66,8 @@ class Sampler:
             raise FloatingPointError("sampled decoding met a NaN / +inf logit or a row with no finite logit")
 
     def draw(self, logits: torch.Tensor, u: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """One token per row of logits [..., V] (bf16 or fp32) from the truncated distribution."""
+        """One token per row of logits [..., V] (bf16 or fp32, already prepared) from the truncated
+        distribution."""
         V = logits.shape[-1]
         x = logits.reshape(-1, V)
         if x.dtype != torch.float32 or x.stride(1) != 1:
@@ -87,15 +96,6 @@ class Sampler:
         stats = self.stats(lf) if stats is None else stats
         return K.truncated_probs(lf, stats, temperature=self.T, ban_id=self.ban, out=out)
 
-    def prob_of(self, lf: torch.Tensor, stats, tok: torch.Tensor) -> torch.Tensor:
-        """P(tok) per row: [y >= thr] exp(y - m) / zk with y = logit / T (the kept-set formula)."""
-        m, thr, zk = stats
-        y = lf.gather(-1, tok.unsqueeze(-1)).squeeze(-1)
-        if self.T != 1.0:
-            y = y / self.T
-        p = torch.exp((y - m).double()) / zk
-        return torch.where(y >= thr, p, torch.zeros_like(p)).float()
-
     def accept(self, pf: torch.Tensor, q: torch.Tensor, drafts: torch.Tensor, *, ctx_len=None, n_live=None,
                u_accept: Optional[torch.Tensor] = None, u_sample: Optional[torch.Tensor] = None, out=None):
         """Rejection-sampling acceptance of a verify pass (fp32 logits [B, R, V], q [B, K, V])."""
@@ -112,21 +112,26 @@ class Sampler:
 def ar_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
                        sp, stats) -> Iterator[list]:
     """Sampled causal decoding (decode.py:273-293, the sampled branch at :283)."""
-    from .decode import _Emitter, _prefill
+    from .decode import _Emitter, _prefill, _room
 
     stats.mode = "causal"
     smp = Sampler(sp, rt.dev, ban_id=rt.mask_id)
+    raw = smp.rules.raw_buffer(1, rt.dev)
     logits = _prefill(rt, cache, prompt, stats)
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     t = time.perf_counter()
     while True:
-        tok = int(smp.draw(logits.reshape(1, -1))[0])
+        row = smp.prepare(logits.reshape(1, -1), raw)
+        tok = int(smp.draw(row)[0])
         smp.check()
+        if raw is not None:
+            smp.rules.note(raw.tolist())
         out = emit([tok])
         if out:
             yield out
         if emit.done:
             break
+        _room(cache, 1)
         logits = rt.ar_step(cache, tok)
         stats.forwards += 1
     stats.decode_s = time.perf_counter() - t
@@ -137,30 +142,36 @@ def selfspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *,
                              eos_ids: set, sp, mask_id: int, n: int, stats) -> Iterator[list]:
     """Sampled self-spec with the bd_bidir_shift canvas (decode.py:297-387, sampled branches): one
     host read per forward (acceptance, correction or clean token, and the next specs together)."""
-    from .decode import _Emitter, _prefill
+    from .decode import _Emitter, _prefill, _room
 
     stats.mode = f"self-spec(N={n})"
     stats.accept_hist = [0] * n
     smp = Sampler(sp, rt.dev, ban_id=mask_id)
     blk, Kd = 2 * n - 1, n - 1
+    raw = smp.rules.raw_buffer(blk, rt.dev)
     logits = _prefill(rt, cache, prompt, stats)
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     t_start = time.perf_counter()
-    t0 = int(smp.draw(logits.reshape(1, -1))[0])
+    t0 = int(smp.draw(smp.prepare(logits.reshape(1, -1), None if raw is None else raw[:1]))[0])
+    if raw is not None:
+        smp.rules.note(raw[:1].tolist())
     t0_emitted = False
     pending = specs = spec_q = None
     dev = rt.dev
     while not emit.done:
+        _room(cache, blk)
         if specs is not None:  # ---- verify round
             L = rt.canvas(cache, [pending] + specs + [mask_id] * (n - 1), n, as_float=False)
             stats.forwards += 1
-            pf = L.float()[None]                                       # [1, blk, V]
+            pf = smp.prepare(L.float()[None], raw)                     # [1, blk, V]
             drafts = torch.as_tensor([specs], dtype=torch.int64, device=dev)
             n_acc, tok, _, _, _ = smp.accept(pf, spec_q, drafts)
             new = smp.draw(pf[0, n:blk])                                # next specs (used when all accepted)
             vals = torch.cat([n_acc.to(torch.int64), tok, new]).tolist()
             smp.check()
             acc, tk, new_specs = vals[0], vals[1], vals[2:]
+            if raw is not None:  # rows that saw real context (decode.py:358)
+                smp.rules.note(raw[: acc + 1 if acc < Kd else n].tolist())
             if acc < Kd:  # rejected at spec `acc`: tk is the correction, next step cold
                 rt.commit(cache, 1 + acc)
                 stats.accept_hist[acc] += 1
@@ -177,7 +188,9 @@ def selfspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *,
             L = rt.canvas(cache, [t0] + [mask_id] * (blk - 1), n, rows=n if rt.skip_rows else None, as_float=False)
             stats.forwards += 1
             stats.cold_forwards += 1
-            pf = L[:n].float()[None]                                   # [1, n, V]
+            pf = smp.prepare(L[:n].float()[None], None if raw is None else raw[:n])  # [1, n, V]
+            if raw is not None:
+                smp.rules.note(raw[:1].tolist())
             vals = smp.draw(pf[0]).tolist()
             smp.check()
             spec_q = smp.probs(pf[:, 1:n].contiguous())
@@ -192,31 +205,50 @@ def selfspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *,
 
 class SampledBlockSpecStep:
     """One batched draft-then-verify step with speculative rejection sampling, on device buffers of fixed
-    shape: `denoise` block-diffusion passes over [t0, MASK x block] (each draws a candidate for every
-    still-masked slot from its truncated distribution and unmasks the slots whose draw is most probable,
-    keeping that slot's distribution as its q row), a token-causal verify pass, rejection-sampling
-    acceptance (the correction, or the bonus when every draft is accepted, becomes the next t0) and the
-    hybrid rollback to 1 + n_acc rows per sequence (ragged KV crops and GDN restores).
+    shape: `denoise` block-diffusion passes over [t0, MASK x block], a token-causal verify pass,
+    rejection-sampling acceptance (the correction, or the bonus when every draft is accepted, becomes
+    the next t0) and the hybrid rollback to 1 + n_acc rows per sequence (ragged KV crops and GDN
+    restores).
+
+    The passes unmask the block in ascending slot order: pass p draws the `per[p]` lowest still-masked
+    slots, each from the truncated distribution of its row of that pass's logits (shift readout: row s
+    predicts slot s), and keeps that distribution as the slot's q row. Which slots a pass unmasks is
+    fixed before anything is drawn, and a slot's q depends only on lower slots' drafts, so every draft
+    is distributed exactly as its q given the drafts before it: the condition under which speculative
+    rejection sampling reproduces the verify distribution (decode.py:333-354; the reference's canvas
+    algorithm draws its specs from rows that see only lower positions, decode.py:361-378).
 
     Inputs: t0 [B] int64. Outputs after run(): canvas [B, block+1] (row 0 = t0, rows 1.. = drafts),
-    n_acc [B] int32, token [B] int64 (next t0). q rows: [B, block, V] fp32 (the reference layout).
-    trace: a list to which run() appends the pass inputs (for parity tests), or None."""
+    n_acc [B] int32, token [B] int64 (next t0). q rows: [B, block, V] fp32 (the reference layout,
+    qwen3_5_diffusion.py:779). trace: a list to which run() appends the pass inputs (for parity tests),
+    or None."""
 
     def __init__(self, rt: TridaRuntime, cache: SeqCache, block: int, denoise: int, sampler: Sampler):
+        if not 1 <= denoise <= block:
+            raise ValueError(f"need 1 <= denoise ({denoise}) <= block ({block})")
         self.rt, self.cache, self.block, self.denoise, self.smp = rt, cache, block, denoise, sampler
         B, V = cache.B, rt.cfg.vocab
         dev = rt.dev
         self.per = [block // denoise + (1 if p < block % denoise else 0) for p in range(denoise)]
+        self.start = [sum(self.per[:p]) for p in range(denoise)]
+        # per pass: the logits rows [B, per] it reads (0..per-1 of the pass's LM-head rows) and the q rows
+        # [B, per] it writes (its slots)
+        self.sel = [torch.arange(k, device=dev).repeat(B, 1).contiguous() for k in self.per]
+        self.slots = [torch.arange(s, s + k, device=dev).repeat(B, 1).contiguous()
+                      for s, k in zip(self.start, self.per)]
         self.t0 = torch.zeros(B, dtype=torch.int64, device=dev)
         self.canvas = torch.full((B, block + 1), rt.mask_id, dtype=torch.int64, device=dev)
-        self.masked = torch.ones(B, block, dtype=torch.bool, device=dev)
         self.ctx = torch.zeros(B, dtype=torch.int64, device=dev)
         self.n_keep = torch.zeros(B, dtype=torch.int32, device=dev)
         self.out = (torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
                     torch.empty(B, dtype=torch.int64, device=dev), None, torch.empty(B, dtype=torch.int32, device=dev))
-        self.lf = torch.empty(B * block * V, dtype=torch.float32, device=dev)   # masked draft rows, fp32
-        self.q = torch.zeros(B, block, V, dtype=torch.float32, device=dev)       # q row per draft slot
-        self.pf = torch.empty(B, block + 1, V, dtype=torch.float32, device=dev)  # verify rows
+        self.lf = torch.empty(B * max(self.per) * V, dtype=torch.float32, device=dev)  # a pass's rows, fp32
+        self.q = torch.zeros(B, block, V, dtype=torch.float32, device=dev)             # q row per draft slot
+        self.pf = torch.empty(B, block + 1, V, dtype=torch.float32, device=dev)        # verify rows
+        # raw gate probabilities of the verify rows, when the decode keeps gate notes
+        self.raw_p = None
+        if sampler.rules.log is not None:
+            self.raw_p = torch.zeros(B, block + 1, sampler.rules.n_gate, dtype=torch.float32, device=dev)
         self.trace: Optional[list] = None
 
     @property
@@ -232,36 +264,26 @@ class SampledBlockSpecStep:
         B, V = cache.B, rt.cfg.vocab
         self.canvas.fill_(rt.mask_id)
         self.canvas[:, 0] = self.t0
-        self.masked.fill_(True)
-        left = blk
         for p in range(self.denoise):
-            L = rt.forward(self.canvas, cache, "draft")
-            # the still-masked slots in ascending order (every sequence has `left` of them); row s of the
-            # draft logits predicts slot s (shift readout)
-            midx = torch.sort(self.masked.to(torch.int8), dim=1, descending=True,
-                              stable=True).indices[:, :left].contiguous()
-            lf = self.lf[: B * left * V].view(B, left, V)
+            k, s0 = self.per[p], self.start[p]
+            # the LM head only for the rows of the slots this pass unmasks
+            L = rt.forward(self.canvas, cache, "draft", rows=k, row0=s0)
+            lf = self.lf[: B * k * V].view(B, k, V)
             with K.timed("draft_sample"):
-                K.gather_rows(L, midx, out=lf)                           # gather + widen in one pass
+                K.gather_rows(L, self.sel[p], out=lf)                     # widen to fp32
+                smp.prepare(lf)
                 st = smp.stats(lf)
-                u = smp.uniform(B * left)
-                x = smp.draw_given(lf, st, u)                            # [B, left]
-                conf = smp.prob_of(lf, st, x)
-            # the per[p] most probable draws (ties: the lower slot first)
-            k = self.per[p]
-            sel = torch.sort(conf, dim=1, descending=True, stable=True).indices[:, :k].contiguous()
-            slots = midx.gather(1, sel)
+                u = smp.uniform(B * k)
+                x = smp.draw_given(lf, st, u)                            # [B, k]
             if self.trace is not None:
-                self.trace.append({"lf": lf.clone(), "u": u.clone(), "x": x.clone(), "midx": midx.clone(),
-                                   "slots": slots.clone()})
-            self.canvas.scatter_(1, slots + 1, x.gather(1, sel))
-            self.masked.scatter_(1, slots, False)
-            with K.timed("draft_q"):  # q[slot] = P of the drawn row, read and written in place
-                K.truncated_probs_rows(lf, st, sel, slots, self.q, temperature=smp.T, ban_id=smp.ban)
-            left -= k
+                self.trace.append({"lf": lf.clone(), "u": u.clone(), "x": x.clone(), "start": s0})
+            self.canvas[:, 1 + s0: 1 + s0 + k] = x
+            with K.timed("draft_q"):  # q[slot] = P of the slot's row, written in place
+                K.truncated_probs_rows(lf, st, self.sel[p], self.slots[p], self.q, temperature=smp.T, ban_id=smp.ban)
         vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
         self.pf.copy_(L)
+        smp.prepare(self.pf, self.raw_p)
         self.ctx.copy_(cache.length)
         with K.timed("sample_accept"):
             ua, us = smp.uniform(B, blk), smp.uniform(B)
@@ -279,7 +301,7 @@ class SampledBlockSpecStep:
 def blockspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int,
                               eos_ids: set, sp, mask_id: int, block: int, denoise: int, stats) -> Iterator[list]:
     """Sampled draft-then-verify decode of one sequence over SampledBlockSpecStep."""
-    from .decode import _Emitter, _prefill
+    from .decode import _Emitter, _prefill, _room
 
     stats.mode = f"self-spec(block={block}, denoise={denoise})"
     stats.accept_hist = [0] * (block + 1)
@@ -288,18 +310,24 @@ def blockspec_sample_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     t_start = time.perf_counter()
     step = SampledBlockSpecStep(rt, cache, block, denoise, smp)
-    t0 = int(smp.draw(logits.reshape(1, -1))[0])
+    raw = smp.rules.raw_buffer(1, rt.dev)
+    t0 = int(smp.draw(smp.prepare(logits.reshape(1, -1), raw))[0])
+    if raw is not None:
+        smp.rules.note(raw.tolist())
     out = emit([t0])
     if out:
         yield out
     step.t0.fill_(t0)
     while not emit.done:
+        _room(cache, block + 1)
         step.run()
         stats.forwards += denoise + 1
         stats.steps += 1
         packed = torch.cat([step.canvas[0, 1:], step.token[:1], step.n_acc[:1].to(torch.int64)]).tolist()
         smp.check()
         acc = packed[-1]
+        if step.raw_p is not None:
+            smp.rules.note(step.raw_p[0, : acc + 1].tolist())
         cache.tokens[0].extend([t0] + packed[:acc])
         cache.ctx_hint = len(cache.tokens[0])
         stats.accept_hist[acc] += 1

@@ -27,7 +27,7 @@ from typing import Callable, Optional
 
 from .decode import DecodeStats, SamplingParams
 
-DEFAULTS = {"temperature": 0.0, "top_k": 50, "top_p": 0.95, "max_tokens": 512, "context_length": 32768}
+DEFAULTS = {"temperature": 1.0, "top_k": 50, "top_p": 0.95, "max_tokens": 512, "context_length": 32768}
 
 
 class BadRequest(ValueError):
@@ -111,6 +111,7 @@ class Job:
         if tokenizer is not None and sent < len(text):
             self.out.put(("delta", text[sent:], []))
         if finish is None:
+            # the loop guard's cut ("repetition") is reported as a cut reply, "length" (server.py:554-555)
             finish = "stop" if stats.finish_reason == "stop" else "length"
         self.out.put(("done", text, ids, stats, finish))
 
@@ -195,7 +196,10 @@ class ServerState:
         mode = body.get("mode")
         if mode is not None and mode not in ("causal", "self-spec", "diffusion"):
             raise BadRequest("mode must be causal, self-spec or diffusion", param="mode")
-        job = Job(prompt, sampling_of(body, self.defaults), budget(prompt, body, self.defaults), stops_of(body), mode)
+        sp = sampling_of(body, self.defaults)
+        if (mode or getattr(self.engine, "mode", None)) == "diffusion" and body.get("temperature") is None:
+            sp.temperature = 0.0  # block diffusion decodes greedily
+        job = Job(prompt, sp, budget(prompt, body, self.defaults), stops_of(body), mode)
         self.worker.submit(job)
         try:
             while True:
@@ -366,11 +370,25 @@ def main(argv=None) -> int:
     ap.add_argument("--context-length", type=int, default=DEFAULTS["context_length"])
     ap.add_argument("--max-tokens", type=int, default=DEFAULTS["max_tokens"])
     ap.add_argument("--temperature", type=float, default=DEFAULTS["temperature"])
+    ap.add_argument("--top-k", type=int, default=DEFAULTS["top_k"])
+    ap.add_argument("--top-p", type=float, default=DEFAULTS["top_p"])
+    ap.add_argument("--prefill-chunk", type=int, default=512)
+    ap.add_argument("--no-prompt-cache", action="store_true")
+    ap.add_argument("--cache-slots", type=int, default=3,
+                    help="conversations whose prompt cache is kept (main loop + side requests)")
+    ap.add_argument("--loop-guard", action="store_true",
+                    help="stop replies that loop (one block repeated 6+ times, or mostly repeated 16-token "
+                         "phrases); reported as finish_reason length")
     args = ap.parse_args(argv)
-    eng = Engine(args.model, mode=args.mode, gen_block=args.gen_block, denoise_steps=args.denoise_steps)
-    state = ServerState(eng, load_tokenizer(eng.path), model_name=str(args.model).rstrip("/").split("/")[-1],
+    from . import decode as _decode
+
+    _decode._Emitter.loop_guard = args.loop_guard
+    eng = Engine(args.model, mode=args.mode, gen_block=args.gen_block, denoise_steps=args.denoise_steps,
+                 prefill_chunk=args.prefill_chunk, prompt_cache=not args.no_prompt_cache,
+                 cache_slots=args.cache_slots)
+    state = ServerState(eng, eng.tokenizer, model_name=str(args.model).rstrip("/").split("/")[-1],
                         defaults={"context_length": args.context_length, "max_tokens": args.max_tokens,
-                                  "temperature": args.temperature})
+                                  "temperature": args.temperature, "top_k": args.top_k, "top_p": args.top_p})
     srv = make_server(state, args.host, args.port)
     print(json.dumps({"listening": f"http://{args.host}:{srv.server_address[1]}", "mode": args.mode}), flush=True)
     try:
