@@ -316,8 +316,23 @@ def _cpu_cache(cfg, ctx: int, prompt_tail, seed: int = 1):
     return cache
 
 
+def _cpu_timed_steps(step_fn, reps: int):
+    """One untimed warm-up call of step_fn, then `reps` timed calls. step_fn returns the accepted tokens of
+    its step. Returns (median seconds per step, mean accepted tokens per step, per-step seconds)."""
+    import statistics
+
+    step_fn()
+    secs, toks = [], []
+    for _ in range(reps):
+        t = time.perf_counter()
+        toks.append(step_fn())
+        secs.append(time.perf_counter() - t)
+    return statistics.median(secs), sum(toks) / len(toks), secs
+
+
 def _cpu_baseline_e2e(rt, cfg, prompt_tail, args):
-    """The oracle's draft-then-verify step on the host cores, over a synthetic 2048-token context."""
+    """The oracle's draft-then-verify step on the host cores, over a synthetic 2048-token context: one
+    warm-up step, then the median of args.cpu_steps timed steps."""
     import torch
 
     from oracle import model as OM
@@ -325,22 +340,81 @@ def _cpu_baseline_e2e(rt, cfg, prompt_tail, args):
     torch.set_num_threads(os.cpu_count() or 1)
     m = OM.CpuHybrid(cfg, rt.w)
     cache = _cpu_cache(cfg, PROMPT_LEN, prompt_tail)
-    t0 = int(prompt_tail[-1])
-    steps, acc_tokens = 0, 0
-    t = time.perf_counter()
-    while steps < args.cpu_steps:
-        _, t0, acc = OM.blockspec_step(m, cache, t0, BLOCK, DENOISE)
-        acc_tokens += 1 + acc
-        steps += 1
-    dt = time.perf_counter() - t
-    return {"value": round(acc_tokens / dt, 4), "unit": "accepted tok/s", "cores": torch.get_num_threads(),
+    state = {"t0": int(prompt_tail[-1])}
+
+    def one():
+        _, state["t0"], acc = OM.blockspec_step(m, cache, state["t0"], BLOCK, DENOISE)
+        return 1 + acc
+
+    med, tok, secs = _cpu_timed_steps(one, max(3, args.cpu_steps))
+    return {"value": round(tok / med, 4), "unit": "accepted tok/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{steps} draft-then-verify step(s) (4 denoising passes + verify + greedy acceptance + "
-                      f"rollback) of the CPU oracle on the same random-init 4B-shape weights (fp32 arithmetic), "
-                      f"synthetic {PROMPT_LEN}-token context; {dt:.1f} s"}
+            "sample": f"1 warm-up + {len(secs)} timed draft-then-verify steps (4 denoising passes + verify + greedy "
+                      f"acceptance + rollback) of the CPU oracle on the same random-init 4B-shape weights (fp32 "
+                      f"arithmetic), synthetic {PROMPT_LEN}-token context; value = mean accepted tokens per step "
+                      f"({tok:.2f}) / median step time ({med:.2f} s; steps {[round(x, 2) for x in secs]} s)"}
 
 
-def bench_e2e(args):
+def _verify_graph_us(step, cache, reps: int = 5) -> float:
+    """Median duration of the verify half of a step (verify forward + acceptance + rollback) replayed from
+    its own HIP graph, with the cache and t0 restored between replays (outside the events)."""
+    import statistics
+
+    import torch
+
+    snap, t0 = cache.snapshot(), step.t0.clone()
+    hint = cache.ctx_hint
+    cache.ctx_hint = max(hint, cache.Lmax)  # attention splits planned for the capacity (as the step graph)
+
+    def undo():
+        cache.restore(snap)
+        step.t0.copy_(t0)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step.verify()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    undo()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step.verify()
+    torch.cuda.synchronize()
+    undo()
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3)
+        undo()
+    cache.ctx_hint = hint
+    del g
+    return statistics.median(times)
+
+
+GEOMETRY = ("hidden 2560; 32 layers = 24 gated-delta (16 key / 16 value heads of 128, conv 6144 channels, "
+            "kernel 4) + 8 full attention (16 q / 4 kv heads of 256, rotary 64); FFN 9728 SwiGLU; vocab 248320, "
+            "tied embedding")
+
+
+def _forward_roofline(cfg, fwd_us: float, ctx: int, traffic_key: str):
+    """HBM roofline of one decoder forward at batch 1: every weight byte once (bf16), the KV cache of the
+    8 attention layers and the 24 fp32 GDN states."""
+    weight_bytes = cfg.n_params() * 2
+    kv_bytes = 8 * 2 * cfg.n_kv_heads * ctx * cfg.head_dim * 2
+    state_bytes = 24 * cfg.lin_v_heads * cfg.lin_v_dim * cfg.lin_k_dim * 4
+    fwd_bytes = weight_bytes + kv_bytes + state_bytes
+    ach = fwd_bytes / (fwd_us * 1e-6) / 1e9
+    return {"bound": "hbm", "kernel": "decoder forward (33 canvas rows, every layer)", "achieved": round(ach, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+            "traffic": _measured_traffic(traffic_key), "algorithmic_bytes": fwd_bytes, "avg_us": round(fwd_us, 1)}
+
+
+def bench_e2e(args, rt=None):
     import torch
 
     from trida_stack_amd import kernels as K
@@ -348,11 +422,11 @@ def bench_e2e(args):
     from trida_stack_amd.model import HybridConfig, build_runtime
 
     cfg = HybridConfig.four_b()
-    rt = build_runtime(cfg, seed=0)
+    rt = rt or build_runtime(cfg, seed=0)
     g = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg.vocab - 1024, (PROMPT_LEN,), generator=g).tolist()
     total = args.warmup + args.steps
-    cache = rt.make_cache(1, max_len=PROMPT_LEN + (BLOCK + 1) * (total + 8) + 64)
+    cache = rt.make_cache(1, max_len=PROMPT_LEN + (BLOCK + 1) * (total + 12) + 64)
     torch.cuda.synchronize()
     t = time.perf_counter()
     logits = rt.prefill(cache, prompt)
@@ -370,6 +444,8 @@ def bench_e2e(args):
     fwd_us = _forward_event_us(rt, cache, step, args) if graph else None
     K.TIMERS, K.TIMER_ONLY = ({}, {"forward", "verify_step"}) if not (args.no_events or graph) else (None, None)
     acc_tokens, hist = 0, [0] * (BLOCK + 1)
+    print(f"[bench] e2e bs1: prefill {prefill_s:.2f} s, timing {args.steps} steps", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
     t = time.perf_counter()
     for _ in range(args.steps):
         step.replay() if graph else step.run()
@@ -383,35 +459,26 @@ def bench_e2e(args):
     if fwd_us is not None:
         timers["forward"] = fwd_us
     K.TIMERS = None
+    verify_us = _verify_graph_us(step, cache) if graph else timers.get("verify_step")
     kern = _kernel_breakdown(step, cache, BLOCK, args)
     ctx = int(cache.length[0])
-
-    # roofline of the decoder forward: every weight byte is read once per forward (bf16), plus the KV
-    # cache of the 8 attention layers and the 24 fp32 GDN states
-    weight_bytes = cfg.n_params() * 2
-    kv_bytes = 8 * 2 * cfg.n_kv_heads * ctx * cfg.head_dim * 2
-    state_bytes = 24 * cfg.lin_v_heads * cfg.lin_v_dim * cfg.lin_k_dim * 4
-    fwd_bytes = weight_bytes + kv_bytes + state_bytes
     fwd_us = timers.get("forward")
-    roof = None
-    if fwd_us:
-        ach = fwd_bytes / (fwd_us * 1e-6) / 1e9
-        roof = {"bound": "hbm", "kernel": "decoder forward (33 canvas rows, every layer)", "achieved": round(ach, 1),
-                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-                "algorithmic_bytes": fwd_bytes, "avg_us": round(fwd_us, 1)}
+    roof = _forward_roofline(cfg, fwd_us, ctx, "e2e_forward_bs1") if fwd_us else None
     cpu = None if args.no_cpu else _cpu_baseline_e2e(rt, cfg, prompt[-64:], args)
     value = acc_tokens / elapsed
     return {
         "metric": METRIC, "value": round(value, 2), "unit": "accepted tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic (random-init weights, random prompt ids)",
-        "config": {"workload": "end-to-end self-spec decode, random-init 4B-shape hybrid (hidden 2560, 24 GDN + 8 "
-                               "attention layers, FFN 9728, vocab 248320), batch 1, 2048-token prompt, block 32 "
-                               "with 4 denoising passes + verify, greedy acceptance and hybrid rollback",
-                   "batch": 1, "prompt_len": PROMPT_LEN, "block": BLOCK, "denoise_passes": DENOISE,
-                   "generated_tokens": acc_tokens, "tokens_per_step": round(acc_tokens / args.steps, 3),
-                   "accept_hist": hist, "params": cfg.n_params()},
-        "verify_step_us": round(timers.get("verify_step", kern.get("verify_step", 0.0)), 1) or None,
+        "config": {"workload": "end-to-end self-spec decode, random-init 4B-shape hybrid, batch 1, 2048-token prompt, "
+                               "block 32 with 4 denoising passes + verify, greedy acceptance and hybrid rollback",
+                   "model_geometry": GEOMETRY, "batch": 1, "prompt_len": PROMPT_LEN, "block": BLOCK,
+                   "denoise_passes": DENOISE, "generated_tokens": acc_tokens,
+                   "tokens_per_step": round(acc_tokens / args.steps, 3), "accept_hist": hist,
+                   "params": cfg.n_params()},
+        "verify_step_us": round(verify_us, 1) if verify_us else None,
+        "verify_step_how": ("median of 5 HIP-graph replays of the verify half of a step (verify forward + greedy "
+                            "acceptance + hybrid rollback), HIP events" if graph else "eager, HIP events"),
         "hip_graph": graph,
         "prefill_s": round(prefill_s, 3),
         "kernel_avg_us": kern,
@@ -446,6 +513,7 @@ def _forward_event_us(rt, cache, step, args, reps: int = 5) -> float:
         g.replay()
     e1.record()
     torch.cuda.synchronize()
+    cache.pending = None
     return e0.elapsed_time(e1) * 1e3 / reps
 
 
@@ -461,7 +529,6 @@ def _kernel_breakdown(step, cache, block, args, steps: int = 4) -> dict:
     K.TIMERS, K.TIMER_ONLY = {}, None
     for _ in range(steps):
         step.run()
-        n = step.n_acc.tolist()
         cache.ctx_hint = max(cache.ctx_hint, int(cache.length.max()))
     torch.cuda.synchronize()
     out = {k: round(v, 2) for k, v in K.timer_means_us(K.TIMERS).items()}
@@ -474,9 +541,9 @@ B64, PMIN, PMAX, TEMP, TOP_P = 64, 512, 4096, 0.7, 0.95
 
 
 def _cpu_baseline_e2e64(rt, cfg, prompts, args):
-    """The oracle's sampled draft-then-verify step on the host cores for the first sequence(s) of the
-    batch (sequences are independent; the oracle runs them one at a time), over a synthetic context of
-    that sequence's prompt length."""
+    """The oracle's sampled draft-then-verify step on the host cores, one sequence of the batch at a time
+    (sequences are independent): one warm-up step, then the median of args.cpu_steps timed steps, each for
+    another sequence over a synthetic context of its prompt length."""
     import numpy as np
     import torch
 
@@ -485,25 +552,30 @@ def _cpu_baseline_e2e64(rt, cfg, prompts, args):
     torch.set_num_threads(os.cpu_count() or 1)
     m = OM.CpuHybrid(cfg, rt.w)
     rng = np.random.default_rng(0)
-    acc_tokens, steps, seqs = 0, 0, 0
-    t = time.perf_counter()
-    for b in range(max(1, args.cpu_steps)):
+    seq = [0]
+    lens = []
+
+    def one():
+        b = seq[0]
+        seq[0] += 1
         cache = _cpu_cache(cfg, len(prompts[b]), prompts[b][-64:], seed=1 + b)
+        lens.append(len(prompts[b]))
         _, _, acc = OM.blockspec_sample_step(m, cache, int(prompts[b][-1]), BLOCK, DENOISE, temperature=TEMP,
                                              top_k=0, top_p=TOP_P, rng=rng)
-        acc_tokens += 1 + acc
-        steps += 1
-        seqs += 1
-    dt = time.perf_counter() - t
-    return {"value": round(acc_tokens / dt, 4), "unit": "accepted tok/s", "cores": torch.get_num_threads(),
+        return 1 + acc
+
+    med, tok, secs = _cpu_timed_steps(one, max(3, args.cpu_steps))
+    return {"value": round(tok / med, 4), "unit": "accepted tok/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{steps} sampled draft-then-verify step(s) (4 denoising passes + verify + rejection-sampling "
-                      f"acceptance + rollback, temperature {TEMP}, top-p {TOP_P}) of the CPU oracle for {seqs} "
-                      f"sequence(s) of the batch, one at a time (fp32 arithmetic, float64 sampling), synthetic "
-                      f"contexts of the prompt lengths {[len(p) for p in prompts[:seqs]]}; {dt:.1f} s"}
+            "sample": f"1 warm-up + {len(secs)} timed sampled draft-then-verify steps (4 denoising passes + verify + "
+                      f"rejection-sampling acceptance + rollback, temperature {TEMP}, top-p {TOP_P}) of the CPU oracle, "
+                      f"one sequence of the batch per step (fp32 arithmetic, float64 sampling), synthetic contexts of "
+                      f"the prompt lengths {lens}; the batch of 64 sequences would take 64 such steps; value = mean "
+                      f"accepted tokens per sequence step ({tok:.2f}) / median step time ({med:.2f} s; steps "
+                      f"{[round(x, 2) for x in secs]} s)"}
 
 
-def bench_e2e64(args):
+def bench_e2e64(args, rt=None):
     import torch
 
     from trida_stack_amd import kernels as K
@@ -512,7 +584,7 @@ def bench_e2e64(args):
     from trida_stack_amd.sampling import SampledBlockSpecStep, Sampler, prefill_batch
 
     cfg = HybridConfig.four_b()
-    rt = build_runtime(cfg, seed=0)
+    rt = rt or build_runtime(cfg, seed=0)
     g = torch.Generator().manual_seed(0)
     lens = torch.randint(PMIN, PMAX + 1, (B64,), generator=g).tolist()
     prompts = [torch.randint(0, cfg.vocab - 1024, (n,), generator=g).tolist() for n in lens]
@@ -524,7 +596,8 @@ def bench_e2e64(args):
     logits = prefill_batch(rt, cache, prompts)
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t
-    print(f"[bench] e2e64: prefill of {sum(lens)} prompt tokens in {prefill_s:.1f} s", file=sys.stderr, flush=True)
+    print(f"[bench] e2e64: prefill of {sum(lens)} prompt tokens in {prefill_s:.1f} s, timing {args.steps} steps",
+          file=sys.stderr, flush=True)
     step = SampledBlockSpecStep(rt, cache, BLOCK, DENOISE, smp)
     step.t0.copy_(smp.draw(logits))
     host_len = list(lens)
@@ -540,8 +613,9 @@ def bench_e2e64(args):
     for _ in range(args.warmup):
         one()
     torch.cuda.synchronize()
-    K.TIMERS, K.TIMER_ONLY = ({}, {"forward", "verify_step"}) if not args.no_events else (None, None)
+    fwd_us = _forward_event_us(rt, cache, step, args)
     acc_tokens, hist = 0, [0] * (BLOCK + 1)
+    torch.cuda.synchronize()
     t = time.perf_counter()
     for _ in range(args.steps):
         for n in one():
@@ -550,21 +624,21 @@ def bench_e2e64(args):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t
     smp.check()
-    timers = K.timer_means_us(K.TIMERS) if K.TIMERS is not None else {}
+    step.draw_uniforms()
+    verify_us = _verify_graph_us(step, cache, reps=3)
     kern = _kernel_breakdown(step, cache, BLOCK, args, steps=2)
     rows = B64 * (BLOCK + 1)
     ctx_avg = sum(host_len) / B64
     # roofline of the decoder forward at 64 x 33 rows: the GEMMs make it MFMA-bound
     flops = 2 * cfg.n_params() * rows + 8 * 4 * cfg.n_heads * (BLOCK + 1) * ctx_avg * cfg.head_dim * B64
-    fwd_us = timers.get("forward")
-    roof = None
-    if fwd_us:
-        ach = flops / (fwd_us * 1e-6) / 1e12
-        roof = {"bound": "mfma", "kernel": "decoder forward (64 x 33 canvas rows, every layer)",
-                "achieved": round(ach, 1), "peak": 2500.0, "unit": "TFLOP/s", "frac": round(ach / 2500.0, 4),
-                "traffic": None, "algorithmic_flops": round(flops), "avg_us": round(fwd_us, 1)}
+    ach = flops / (fwd_us * 1e-6) / 1e12
+    roof = {"bound": "mfma", "kernel": "decoder forward (64 x 33 canvas rows, every layer)",
+            "achieved": round(ach, 1), "peak": 2500.0, "unit": "TFLOP/s", "frac": round(ach / 2500.0, 4),
+            "traffic": _measured_traffic("e2e_forward_bs64"), "algorithmic_flops": round(flops),
+            "avg_us": round(fwd_us, 1)}
     cpu = None if args.no_cpu else _cpu_baseline_e2e64(rt, cfg, prompts, args)
     value = acc_tokens / elapsed
+    del step, cache
     return {
         "metric": METRIC, "value": round(value, 2), "unit": "accepted tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 3), "higher_is_better": True,
@@ -573,11 +647,14 @@ def bench_e2e64(args):
                                "prompts of 512-4096 tokens, block 32 with 4 denoising passes + verify, temperature "
                                "0.7, top-p 0.95, rejection sampling of the causal-head p against the draft q, "
                                "per-sequence KV crops and GDN restores",
-                   "batch": B64, "prompt_lens": [min(lens), max(lens), round(sum(lens) / B64, 1)], "block": BLOCK,
+                   "model_geometry": GEOMETRY, "batch": B64,
+                   "prompt_lens": [min(lens), max(lens), round(sum(lens) / B64, 1)], "block": BLOCK,
                    "denoise_passes": DENOISE, "temperature": TEMP, "top_p": TOP_P,
                    "generated_tokens": acc_tokens, "tokens_per_seq_step": round(acc_tokens / args.steps / B64, 3),
                    "accept_hist": hist, "params": cfg.n_params()},
-        "verify_step_us": round(timers["verify_step"], 1) if "verify_step" in timers else None,
+        "verify_step_us": round(verify_us, 1),
+        "verify_step_how": "median of 3 HIP-graph replays of the verify half of a step (verify forward + rejection-"
+                           "sampling acceptance + hybrid rollback), HIP events",
         "prefill_s": round(prefill_s, 3),
         "kernel_avg_us": kern,
         "roofline": roof,
@@ -585,6 +662,23 @@ def bench_e2e64(args):
         "speedup_vs_cpu": round(value / cpu["value"], 1) if cpu else None,
     }
 
+
+def bench_default(args):
+    """The headline line: batch 1 (value) and batch 64 (the "bs64" object) on one random-init runtime."""
+    import torch
+
+    from trida_stack_amd.model import HybridConfig, build_runtime
+
+    rt = build_runtime(HybridConfig.four_b(), seed=0)
+    res = bench_e2e(args, rt)
+    sub = argparse.Namespace(**vars(args))
+    sub.steps, sub.warmup = args.bs64_steps, args.bs64_warmup
+    torch.cuda.empty_cache()
+    r64 = bench_e2e64(sub, rt)
+    keep = ("value", "unit", "steps", "warmup", "ms_per_step", "verify_step_us", "verify_step_how", "roofline",
+            "cpu_baseline", "speedup_vs_cpu", "config", "prefill_s", "kernel_avg_us")
+    res["bs64"] = {k: r64[k] for k in keep}
+    return res
 
 
 # ------------------------------------------------------------------------------ chunked GDR (config 2)
@@ -763,7 +857,7 @@ def bench_gemm(args):
             "cpu_baseline": None}
 
 
-WORKLOADS = {"e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "gdr": (bench_gdr, 20, 3), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
+WORKLOADS = {"default": (bench_default, 20, 5), "e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "gdr": (bench_gdr, 20, 3), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
              "sample": (bench_sample, 20, 3), "attn": (bench_attn, 100, 10)}
 
 
@@ -772,9 +866,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="e2e", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="default", choices=sorted(WORKLOADS),
+                    help="default: batch 1 (value) plus a batch-64 object; e2e / e2e64: one of them")
+    ap.add_argument("--bs64-steps", type=int, default=6, help="default workload: timed batch-64 steps")
+    ap.add_argument("--bs64-warmup", type=int, default=2)
     ap.add_argument("--splits", type=int, default=0)
-    ap.add_argument("--cpu-steps", type=int, default=1)
+    ap.add_argument("--cpu-steps", type=int, default=3, help="timed CPU-oracle steps (median; after one warm-up)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-events", action="store_true", help="skip the live per-kernel event timers")
     ap.add_argument("--no-graph", action="store_true", help="e2e: launch the step eagerly instead of from a HIP graph")

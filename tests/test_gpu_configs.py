@@ -1,0 +1,210 @@
+"""GPU: the end-to-end configurations at their stated sizes (random-init 4B-shape hybrid: hidden 2560, 24 GDN
+layers with 16 key / 16 value heads of 128 (conv 6144) and 8 attention layers with 16 q / 4 kv heads of 256,
+FFN 9728, vocab 248320).
+
+Batch 1, 2048-token prompt, block 32 with 4 denoising passes, greedy:
+  - the chunked prefill (512-row chunks on the MFMA delta rule) against the token-recurrent prefill of the
+    same prompt: last-token logits and every GDN state;
+  - three draft-then-verify steps; after each, every GDN layer's committed state and conv window equal the
+    oracle's rollback (oracle.gdn.restore, model.py:486-507) of the rows that step's verify pass computed,
+    from the state before the step, and the KV length is prompt + committed tokens;
+  - the committed cache against a fresh causal prefill over the committed tokens (test_tiny.py:84-97):
+    GDN states and the next token's logits.
+Batch 64, ragged 512-4096-token prompts, temperature 0.7, top-p 0.95, rejection sampling:
+  - per-sequence KV crops (prompt + 1 + n_acc) and GDN restores of every sequence against the oracle's
+    rollback of its own accepted length;
+  - four sequences' draws and acceptance replayed on the oracle from the step's own logits and uniforms;
+  - those sequences' committed state against the same verify + commit run as single-sequence batches.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as A
+from oracle import gdn as OG
+from trida_stack_amd.decode import BlockSpecStep, SamplingParams
+from trida_stack_amd.model import HybridConfig, build_runtime
+from trida_stack_amd.sampling import SampledBlockSpecStep, Sampler, prefill_batch
+
+pytestmark = pytest.mark.gpu
+CFG = HybridConfig.four_b()
+BLOCK, DENOISE = 32, 4
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+@pytest.fixture(scope="module")
+def rt4b(gpu):
+    rt = build_runtime(CFG, seed=0, device=gpu)
+    yield rt
+    del rt
+    torch.cuda.empty_cache()
+
+
+def check_rollback(rt, cache, snap_state, snap_window, layers, b=0, n_keep=None, T=BLOCK + 1, tol=1e-3):
+    """The committed state / window of sequence b in `layers` against oracle.gdn.restore of the block rows
+    the last verify pass left in the runtime's scratch."""
+    s = rt.scratch(cache.B, T)
+    n = int(n_keep)
+    for j in layers:
+        st, win = OG.restore(snap_state[j, b: b + 1].cpu(), snap_window[j, b: b + 1].cpu(),
+                             s.k_rec[j, b: b + 1].cpu(), s.v_rec[j, b: b + 1].cpu(), s.g_rec[j, b: b + 1].cpu(),
+                             s.b_rec[j, b: b + 1].cpu(), s.pre_rec[j, b: b + 1].cpu(), [n])
+        assert rel(cache.state[j, b], st[0]) < tol, (j, b, n)
+        assert torch.equal(cache.window[j, b].float().cpu(), win[0].to(torch.bfloat16).float()), (j, b, n)
+
+
+def nw(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).norm() / b.norm().clamp_min(1e-30))
+
+
+def test_config4_prefill_chunked_vs_recurrent(gpu, rt4b):
+    """The 2048-token prefill in one chunk under each GDN form: the last GDN layer's output and final state
+    against the oracle on the very rows the model fed that layer (relative 1e-2 for the bf16 output, 1e-3
+    for the fp32 state). Then the end-to-end logits of the chunked prefill (512-row chunks on the MFMA
+    delta rule) against the token-recurrent prefill. A random-init model amplifies bf16 rounding: the gate
+    g = -exp(A_log) softplus(a + dt_bias) has a gain of up to 16 (A_log = log 16), so a one-ulp change of
+    a bf16 input moves e^g by up to ~3%. The two forms round differently from the first GDN layer on, so
+    their logits are compared against the difference that a change of prefill chunk size alone makes
+    within one form (the noise floor of this model; measured ~3e-2 normwise, the forms ~7e-2)."""
+    rt = rt4b
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, CFG.vocab - 1024, (2048,), generator=g).tolist()
+    old = rt.gdr_form, rt.prefill_chunk
+    j = len(rt.gdn_layers) - 1
+    outs = {}
+    try:
+        for form in ("chunked", "recurrent"):
+            rt.gdr_form, rt.prefill_chunk = form, 2048
+            c = rt.make_cache(1, max_len=2304)
+            rt.prefill(c, prompt)
+            s = rt.scratch(1, 2048)  # holds the last GDN layer's rows and output of this forward
+            q, k, v = s.q.cpu(), s.k_rec[j].cpu(), s.v_rec[j].cpu()
+            gg, bb = s.g_rec[j].cpu(), s.b_rec[j].cpu()
+            o_ref, S_ref = OG.chunked(q, k, v, gg, bb, torch.zeros(1, CFG.lin_v_heads, CFG.lin_v_dim, CFG.lin_k_dim))
+            print(f"[config4] {form} 2048-row layer {j}: out rel {rel(s.y, o_ref):.2e}, state rel "
+                  f"{rel(c.state[j], S_ref):.2e}", flush=True)
+            assert rel(s.y, o_ref) < 1e-2, form
+            assert rel(c.state[j], S_ref) < 1e-3, form
+        for form, chunk in (("auto", 512), ("recurrent", 512), ("recurrent", 256)):
+            rt.gdr_form, rt.prefill_chunk = form, chunk
+            c = rt.make_cache(1, max_len=2304)
+            outs[(form, chunk)] = (rt.prefill(c, prompt), c.state.clone())
+    finally:
+        rt.gdr_form, rt.prefill_chunk = old
+    la, sa = outs[("auto", 512)]
+    lb, sb = outs[("recurrent", 512)]
+    lc, sc = outs[("recurrent", 256)]
+    floor, forms = nw(lc, lb), nw(la, lb)
+    print(f"[config4] prefill logits normwise: chunked vs recurrent {forms:.2e}, recurrent chunk 256 vs 512 "
+          f"{floor:.2e}; states {nw(sa, sb):.2e} / {nw(sc, sb):.2e}", flush=True)
+    assert forms < max(4 * floor, 2e-2) and forms < 0.15
+    assert nw(sa, sb) < max(4 * nw(sc, sb), 2e-2)
+    top2 = torch.topk(lb, 2).values
+    assert int(la.argmax()) == int(lb.argmax()) or float(top2[0] - top2[1]) < 0.1
+
+
+def test_config4_block_steps_commit_and_rollback(gpu, rt4b):
+    rt = rt4b
+    g = torch.Generator().manual_seed(5)
+    prompt = torch.randint(0, CFG.vocab - 1024, (2048,), generator=g).tolist()
+    cache = rt.make_cache(1, max_len=2048 + 4 * (BLOCK + 1) + 64)
+    logits = rt.prefill(cache, prompt)
+    step = BlockSpecStep(rt, cache, BLOCK, DENOISE)
+    t0 = int(logits.argmax())
+    step.t0.fill_(t0)
+    gdn = list(range(len(rt.gdn_layers)))
+    for it in range(3):
+        snap_state, snap_window = cache.state.clone(), cache.window.clone()
+        n0 = int(cache.length[0])
+        step.run()
+        acc = int(step.n_acc[0])
+        drafts = step.canvas[0, 1:].tolist()
+        cache.tokens[0].extend([t0] + drafts[:acc])
+        cache.ctx_hint = len(cache.tokens[0])
+        t0 = int(step.bonus[0])
+        assert int(cache.length[0]) == n0 + 1 + acc == len(cache.tokens[0])
+        check_rollback(rt, cache, snap_state, snap_window, gdn[:: 7] + [gdn[-1]], n_keep=1 + acc)
+    # the stepped cache against a fresh causal prefill of the same committed tokens
+    fresh = rt.make_cache(1, max_len=cache.Lmax)
+    rt.prefill(fresh, list(cache.tokens[0]))
+    nxt = 12345
+    la, lb = rt.ar_step(cache, nxt), rt.ar_step(fresh, nxt)
+    print(f"[config4] stepped vs fresh causal cache: states normwise {nw(cache.state, fresh.state):.2e}, next "
+          f"logits normwise {nw(la, lb):.2e}", flush=True)
+    # the two caches saw the same tokens through different row counts per forward (rounding differs; the
+    # bound is that of the prefill comparison above)
+    assert nw(cache.state, fresh.state) < 0.15 and nw(la, lb) < 0.15
+    top2 = torch.topk(lb, 2).values
+    assert int(la.argmax()) == int(lb.argmax()) or float(top2[0] - top2[1]) < 0.1
+
+
+def test_config5_batch64_sampled_step(gpu, rt4b):
+    rt = rt4b
+    B = 64
+    g = torch.Generator().manual_seed(6)
+    lens = torch.randint(512, 4096 + 1, (B,), generator=g).tolist()
+    prompts = [torch.randint(0, CFG.vocab - 1024, (n,), generator=g).tolist() for n in lens]
+    T, top_p = 0.7, 0.95
+    cache = rt.make_cache(B, max_len=max(lens) + 2 * (BLOCK + 1) + 64)
+    smp = Sampler(SamplingParams(temperature=T, top_k=0, top_p=top_p, seed=1), rt.dev, ban_id=rt.mask_id)
+    logits = prefill_batch(rt, cache, prompts)
+    step = SampledBlockSpecStep(rt, cache, BLOCK, DENOISE, smp)
+    step.t0.copy_(smp.draw(smp.prepare(logits)))
+    t0 = step.t0.clone()
+    snap_state, snap_window = cache.state.clone(), cache.window.clone()
+    step.trace = []
+    step.run()
+    smp.check()
+    n_acc = step.n_acc.cpu()
+    # ragged crops: every sequence keeps its pending token and its accepted drafts
+    assert torch.equal(cache.length.cpu(), torch.tensor(lens, dtype=torch.int32) + 1 + n_acc)
+    assert (step.token != rt.mask_id).all()
+    # ragged GDN restores: every sequence's state against the oracle's rollback of its own accepted length
+    for b in range(B):
+        check_rollback(rt, cache, snap_state, snap_window, [0, len(rt.gdn_layers) - 1], b=b,
+                       n_keep=1 + int(n_acc[b]))
+    # four sequences replayed on the oracle: the draws of each pass and the acceptance
+    order = np.argsort(lens)
+    sub = [int(order[0]), int(order[-1]), int(order[B // 3]), int(order[2 * B // 3])]
+    passes, ver = step.trace[:-1], step.trace[-1]
+    drafts = ver["drafts"][sub].cpu().numpy()
+    for pi, tr in enumerate(passes):
+        lf = tr["lf"][sub].cpu().numpy()
+        u = tr["u"].view(B, -1)[sub].cpu().numpy()
+        x = tr["x"][sub].cpu().numpy()
+        P, info = A.truncated_probs(lf, T, 0, top_p, rt.mask_id, return_info=True)
+        for i in range(len(sub)):
+            for r in range(lf.shape[1]):
+                tok, gap = A.sample_inverse_cdf(P[i, r], float(u[i, r]))
+                if gap > 1e-6 and info.boundary_gap[i, r] > 1e-6:
+                    assert x[i, r] == tok, (pi, sub[i], r)
+                assert drafts[i, tr["start"] + r] == x[i, r]
+    res = A.rejection_accept(ver["pf"][sub].cpu().numpy(), ver["q"][sub].cpu().numpy(), drafts,
+                             ver["ua"][sub].cpu().numpy(), ver["us"][sub].cpu().numpy(), temperature=T, top_k=0,
+                             top_p=top_p, mask_id=rt.mask_id)
+    ok = ~res["tie"]
+    got_acc, got_tok = n_acc[sub].numpy(), step.token[sub].cpu().numpy()
+    assert (got_acc[ok] == res["n_acc"][ok]).all() and (got_tok[ok] == res["token"][ok]).all()
+    step.trace = None
+    del passes, ver
+    # the same verify + commit as single-sequence batches, teacher-forced on the batched step's drafts
+    canvas = step.canvas.clone()  # [t0, drafts] of the step that ran
+    assert torch.equal(canvas[:, 0], t0)
+    for b in sub[:2]:
+        one = rt.make_cache(1, max_len=cache.Lmax)
+        rt.prefill(one, prompts[b])
+        rt.verify(one, canvas[b: b + 1].to(rt.dev))
+        rt.commit(one, 1 + int(n_acc[b]))
+        assert int(one.length[0]) == int(cache.length[b])
+        # a verify pass of 33 rows against one of 64 x 33 rows: the GEMMs round differently, which the gates
+        # amplify for the committed rows (see the prefill comparison); the rollback itself is exact above
+        print(f"[config5] sequence {b}: single vs batched commit, state normwise "
+              f"{nw(one.state[:, 0], cache.state[:, b]):.2e}, window {nw(one.window[:, 0], cache.window[:, b]):.2e}",
+              flush=True)
+        assert nw(one.state[:, 0], cache.state[:, b]) < 0.1, b
+        assert nw(one.window[:, 0], cache.window[:, b]) < 5e-2, b

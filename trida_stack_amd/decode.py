@@ -472,7 +472,12 @@ class BlockSpecStep:
             self.raw_p = torch.zeros(B, block + 1, self.rules.n_gate, dtype=torch.float32, device=dev)
 
     def run(self) -> None:
-        rt, cache, blk = self.rt, self.cache, self.block
+        self.draft()
+        self.verify()
+
+    def draft(self) -> None:
+        """The denoising passes: canvas = [t0, drafts]."""
+        rt, cache = self.rt, self.cache
         self.canvas.fill_(rt.mask_id)
         self.canvas[:, 0] = self.t0
         self.masked.fill_(True)
@@ -485,6 +490,10 @@ class BlockSpecStep:
                 K.row_argmax(L, out=(self.d_am, self.d_conf))
             # the per[p] most confident MASK slots (ties: the lower slot first) take their predictions
             K.unmask_top(self.d_am, self.d_conf, self.masked, self.canvas, self.per[p])
+
+    def verify(self) -> None:
+        """The verify pass over the canvas, greedy acceptance and the rollback; t0 = the bonus token."""
+        rt, cache, blk = self.rt, self.cache, self.block
         vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
         if self.rules is not None:

@@ -245,6 +245,8 @@ class SampledBlockSpecStep:
         self.lf = torch.empty(B * max(self.per) * V, dtype=torch.float32, device=dev)  # a pass's rows, fp32
         self.q = torch.zeros(B, block, V, dtype=torch.float32, device=dev)             # q row per draft slot
         self.pf = torch.empty(B, block + 1, V, dtype=torch.float32, device=dev)        # verify rows
+        self.ua = torch.zeros(B, block, dtype=torch.float32, device=dev)               # acceptance uniforms
+        self.us = torch.zeros(B, dtype=torch.float32, device=dev)                      # correction / bonus
         # raw gate probabilities of the verify rows, when the decode keeps gate notes
         self.raw_p = None
         if sampler.rules.log is not None:
@@ -260,7 +262,19 @@ class SampledBlockSpecStep:
         return self.out[1]
 
     def run(self) -> None:
-        rt, cache, blk, smp = self.rt, self.cache, self.block, self.smp
+        self.draft()
+        self.draw_uniforms()
+        self.verify()
+
+    def draw_uniforms(self) -> None:
+        """The acceptance uniforms of the verify pass (drawn before it, so the verify half has no RNG)."""
+        B = self.cache.B
+        self.ua.copy_(self.smp.uniform(B, self.block))
+        self.us.copy_(self.smp.uniform(B))
+
+    def draft(self) -> None:
+        """The denoising passes: canvas = [t0, drafts], q rows of the drafted slots."""
+        rt, cache, smp = self.rt, self.cache, self.smp
         B, V = cache.B, rt.cfg.vocab
         self.canvas.fill_(rt.mask_id)
         self.canvas[:, 0] = self.t0
@@ -280,13 +294,18 @@ class SampledBlockSpecStep:
             self.canvas[:, 1 + s0: 1 + s0 + k] = x
             with K.timed("draft_q"):  # q[slot] = P of the slot's row, written in place
                 K.truncated_probs_rows(lf, st, self.sel[p], self.slots[p], self.q, temperature=smp.T, ban_id=smp.ban)
+
+    def verify(self) -> None:
+        """The verify pass, rejection-sampling acceptance with the drawn uniforms, and the rollback; t0 = the
+        correction or bonus token."""
+        rt, cache, blk, smp = self.rt, self.cache, self.block, self.smp
         vt = K.timed("verify_step").__enter__()
         L = rt.forward(self.canvas, cache, "verify")
         self.pf.copy_(L)
         smp.prepare(self.pf, self.raw_p)
         self.ctx.copy_(cache.length)
+        ua, us = self.ua, self.us
         with K.timed("sample_accept"):
-            ua, us = smp.uniform(B, blk), smp.uniform(B)
             smp.accept(self.pf, self.q, self.canvas[:, 1:], ctx_len=self.ctx, u_accept=ua, u_sample=us, out=self.out)
         if self.trace is not None:
             self.trace.append({"pf": self.pf.clone(), "q": self.q.clone(), "drafts": self.canvas[:, 1:].clone(),
