@@ -663,6 +663,73 @@ def bench_e2e64(args, rt=None):
     }
 
 
+def bench_canvas(args, rt=None, n: int = 4):
+    """The reference's own self-spec algorithm (bd_bidir_shift, decode.py:318-384): one canvas forward of
+    2n-1 rows per step, greedy acceptance, the next canvas decided on the device and the rollback, the
+    whole step replayed from one HIP graph, batch 1 after a 2048-token prompt. The reference's published
+    step time for this algorithm on H100 is 7.5 ms at n = 4 (canvas 7) with vLLM and full CUDA graphs."""
+    import statistics
+
+    import torch
+
+    from trida_stack_amd.decode import CanvasSpecStep
+    from trida_stack_amd.model import HybridConfig, build_runtime
+
+    cfg = HybridConfig.four_b()
+    rt = rt or build_runtime(cfg, seed=0)
+    g = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, cfg.vocab - 1024, (PROMPT_LEN,), generator=g).tolist()
+    steps = args.canvas_steps
+    cache = rt.make_cache(1, max_len=PROMPT_LEN + n * (steps + 16) + 64)
+    logits = rt.prefill(cache, prompt)
+    step = CanvasSpecStep(rt, cache, n)
+    step.start(logits.argmax().reshape(1))
+    step.run()
+    step.capture()
+    emitted, hist, cold = 0, [0] * n, 0
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(steps):
+        step.replay()
+        kind, ne = step.kind[:1].tolist()[0], int(step.n_emit[0])  # the host reads the emitted tokens each step
+        emitted += ne
+        if kind:
+            hist[ne - 1] += 1
+        else:
+            cold += 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    # one canvas forward, replayed from its own graph
+    ids = step.canvas.clone()
+    fwd = lambda: rt.forward(ids, cache, "canvas", n_clean=n)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fwd()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        fwd()
+    times = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        gr.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3)
+    cache.pending = None
+    return {"value": round(emitted / elapsed, 2), "unit": "accepted tok/s", "steps": steps,
+            "ms_per_step": round(elapsed * 1e3 / steps, 3), "canvas_forward_us": round(statistics.median(times), 1),
+            "tokens_per_step": round(emitted / steps, 3), "accept_hist": hist, "cold_steps": cold,
+            "config": {"workload": f"self-spec canvas algorithm (bd_bidir_shift, N = {n}, canvas {2 * n - 1}), "
+                                   "batch 1, 2048-token prompt, greedy, one HIP graph per step",
+                       "n": n, "canvas": 2 * n - 1},
+            "reference_published": "7.5 ms/step on H100 at N = 4 (vLLM, full CUDA graphs, real checkpoint; "
+                                   "inference/zoro-1/vllm/docs/SELFSPEC_VLLM_PLAN.md:83)"}
+
+
 def bench_default(args):
     """The headline line: batch 1 (value) and batch 64 (the "bs64" object) on one random-init runtime."""
     import torch
@@ -678,6 +745,9 @@ def bench_default(args):
     keep = ("value", "unit", "steps", "warmup", "ms_per_step", "verify_step_us", "verify_step_how", "roofline",
             "cpu_baseline", "speedup_vs_cpu", "config", "prefill_s", "kernel_avg_us")
     res["bs64"] = {k: r64[k] for k in keep}
+    if args.canvas_steps > 0:
+        for n in (4, 8):
+            res[f"canvas_n{n}"] = bench_canvas(args, rt, n)
     return res
 
 
@@ -857,7 +927,7 @@ def bench_gemm(args):
             "cpu_baseline": None}
 
 
-WORKLOADS = {"default": (bench_default, 20, 5), "e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "gdr": (bench_gdr, 20, 3), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
+WORKLOADS = {"default": (bench_default, 20, 5), "canvas": (lambda a: bench_canvas(argparse.Namespace(**dict(vars(a), canvas_steps=a.steps))), 64, 0), "e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "gdr": (bench_gdr, 20, 3), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
              "sample": (bench_sample, 20, 3), "attn": (bench_attn, 100, 10)}
 
 
@@ -870,6 +940,7 @@ def main():
                     help="default: batch 1 (value) plus a batch-64 object; e2e / e2e64: one of them")
     ap.add_argument("--bs64-steps", type=int, default=6, help="default workload: timed batch-64 steps")
     ap.add_argument("--bs64-warmup", type=int, default=2)
+    ap.add_argument("--canvas-steps", type=int, default=32, help="default workload: timed canvas-algorithm steps")
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=3, help="timed CPU-oracle steps (median; after one warm-up)")
     ap.add_argument("--no-cpu", action="store_true")

@@ -95,6 +95,25 @@ int trida_unmask_top(const int64_t* argmax, const float* conf, int64_t row_strid
 int trida_row_argmax(const void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, int64_t* argmax,
                      float* conf, void* scratch, int64_t scratch_bytes, int64_t splits, void* stream);
 
+/* One step of the bd_bidir_shift self-spec canvas decided on the device (the host logic of
+ * selfspec_generate, inference/zoro-1/mlx/trida_mlx/decode.py:318-384; the vLLM plugin's next-canvas
+ * build, qwen3_5_diffusion.py:924-951), so that canvas forward, acceptance, this and the rollback replay
+ * from one graph. Per sequence b (canvas [B, 2N-1] int64 with row stride canvas_stride; argmax [B, >= 2N-1]
+ * of the canvas logits, row j predicting slot j + 1; n_acc [B] = leading specs accepted, as
+ * trida_greedy_accept returns with n_live = N - 1 for a verify canvas and 0 for a cold one):
+ *   verify[b] == 0 (cold canvas [t0, MASK x (2N-2)]): emit argmax[0]; next canvas [argmax[0],
+ *     argmax[1..N-1], MASK x (N-1)], verify; keep 1 row.
+ *   verify[b] != 0 ([pending, spec_1..spec_{N-1}, MASK x (N-1)]), a = n_acc[b]: a < N-1: emit
+ *     spec_1..spec_a, argmax[a]; next canvas [argmax[a], MASK x (2N-2)], cold; keep 1 + a rows. a = N-1:
+ *     emit the specs and argmax[N-1]; next canvas [argmax[N-1], argmax[N..2N-2], MASK x (N-1)], verify;
+ *     keep N rows.
+ * Outputs: canvas and verify updated in place, n_keep [B] int32 (rows to commit), emit [B, N] int64 and
+ * n_emit [B] int32 (tokens emitted this step), committed [B, N] int64 (the first n_keep canvas tokens this
+ * step commits), kind [B] int32 (1 if the step was a verify round). 2 <= N <= 512. */
+int trida_canvas_advance(const int64_t* argmax, int64_t argmax_stride, const int32_t* n_acc, int64_t* canvas,
+                         int64_t canvas_stride, uint8_t* verify, int32_t* n_keep, int64_t* emit, int32_t* n_emit,
+                         int64_t* committed, int32_t* kind, int64_t B, int64_t N, int64_t mask_id, void* stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Banned and gated tokens, in place on logit rows before an argmax or a sampling entry point reads
  * them. Replaces apply_ban (inference/zoro-1/mlx/trida_mlx/decode.py:76-99), which the reference applies

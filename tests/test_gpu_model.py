@@ -351,3 +351,61 @@ def test_diffusion_mode_follows_oracle(gpu, threshold, canvas):
         ref = OM.diffusion_generate(m, p, 40, canvas=canvas, threshold=threshold)
         assert len(got) == 40 and st.mode == "diffusion" and st.steps == -(-40 // canvas)
         assert got == ref or same_or_near_tie(rt, p, ref, got), (seed, got, ref)
+
+
+def _canvas_advance_ref(am, n_acc, canvas, verify, N, mask):
+    """The host decision of selfspec_generate (inference/zoro-1/mlx/trida_mlx/decode.py:318-384) per
+    sequence: (next canvas, next verify, emitted, committed)."""
+    blk = 2 * N - 1
+    if not verify:  # cold start: clean = row 0, specs = rows 1..N-1, commit the t0 row
+        return [am[0]] + am[1:N] + [mask] * (N - 1), True, [am[0]], canvas[:1]
+    specs, acc = canvas[1:N], n_acc
+    if acc < N - 1:
+        return [am[acc]] + [mask] * (blk - 1), False, specs[:acc] + [am[acc]], canvas[: 1 + acc]
+    return [am[N - 1]] + am[N:blk] + [mask] * (N - 1), True, specs + [am[N - 1]], canvas[:N]
+
+
+@pytest.mark.parametrize("N", [2, 4, 8])
+def test_canvas_advance_matches_host_logic(gpu, N):
+    B, blk, mask = 9, 2 * N - 1, 999
+    g = torch.Generator().manual_seed(N)
+    am = torch.randint(0, 50, (B, blk + 1), generator=g)
+    canvas = torch.randint(0, 50, (B, blk), generator=g)
+    verify = torch.tensor([b % 3 != 0 for b in range(B)], dtype=torch.uint8)
+    n_acc = torch.tensor([b % N for b in range(B)], dtype=torch.int32)
+    dev = DEV
+    cv, vf = canvas.to(dev), verify.to(dev)
+    outs = (torch.zeros(B, dtype=torch.int32, device=dev), torch.zeros(B, N, dtype=torch.int64, device=dev),
+            torch.zeros(B, dtype=torch.int32, device=dev), torch.zeros(B, N, dtype=torch.int64, device=dev),
+            torch.zeros(B, dtype=torch.int32, device=dev))
+    K.canvas_advance(am.to(dev), n_acc.to(dev), cv, vf, outs, mask)
+    n_keep, emit, n_emit, committed, kind = [o.cpu() for o in outs]
+    for b in range(B):
+        nxt, ver, em, cm = _canvas_advance_ref(am[b].tolist(), int(n_acc[b]), canvas[b].tolist(), bool(verify[b]), N,
+                                               mask)
+        assert cv[b].tolist() == nxt and bool(vf[b]) == ver and int(kind[b]) == int(verify[b])
+        assert emit[b, : n_emit[b]].tolist() == em and committed[b, : n_keep[b]].tolist() == cm
+
+
+def test_canvas_step_graph_replay_matches_eager(gpu, pair):
+    """The canvas step replayed from its HIP graph gives the eager step's emitted tokens, canvases and cache
+    lengths, step after step (eager work between replays)."""
+    from trida_stack_amd.decode import CanvasSpecStep
+
+    rt, _ = pair
+    p = prompt(23, seed=31)
+    runs = []
+    for graph in (False, True):
+        c = rt.make_cache(max_len=256)
+        lg = rt.prefill(c, p)
+        step = CanvasSpecStep(rt, c, 4)
+        step.start(lg.argmax().reshape(1))
+        seq = []
+        for i in range(6):
+            if graph and step.graph is None and i == 1:
+                step.capture()
+            step.replay() if step.graph is not None else step.run()
+            seq.append((step.emit[0, : int(step.n_emit[0])].tolist(), step.canvas[0].tolist(), int(c.length[0])))
+            torch.zeros(3, device=DEV).sum()  # unrelated eager work between replays
+        runs.append(seq)
+    assert runs[0] == runs[1]

@@ -34,6 +34,7 @@ SIGNATURES = {
     "trida_row_argmax_scratch_bytes": (I64, [I64, I64, C.c_int, I64]),
     "trida_row_argmax": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, P, I64, I64, P]),
     "trida_unmask_top": (C.c_int, [P, P, I64, P, P, I64, I64, I64, I64, P]),
+    "trida_canvas_advance": (C.c_int, [P, I64, P, P, I64, P, P, P, P, P, P, I64, I64, I64, P]),
     "trida_ban_tokens": (C.c_int, [P, C.c_int, I64, I64, I64, P, I64, P]),
     "trida_gate_tokens": (C.c_int, [P, C.c_int, I64, I64, I64, P, P, I64, P, P]),
     "trida_sample_accept_scratch_bytes": (I64, [I64, I64, I64, I64]),

@@ -419,6 +419,56 @@ __global__ __launch_bounds__(256) void unmask_top_kernel(const int64_t* am, cons
   }
 }
 
+// One sequence per thread: the host decision of a bd_bidir_shift self-spec step, taken on the device so
+// that a whole step (canvas forward, acceptance, this, the rollback) replays from one graph.
+__global__ __launch_bounds__(64) void canvas_advance_kernel(const int64_t* am, int64_t am_st, const int32_t* n_acc,
+                                                            int64_t* canvas, int64_t cv_st, uint8_t* verify,
+                                                            int32_t* n_keep, int64_t* emit, int32_t* n_emit,
+                                                            int64_t* committed, int32_t* kind, int B, int N,
+                                                            int64_t mask_id) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= B) return;
+  const int64_t* a = am + (int64_t)b * am_st;
+  int64_t* cv = canvas + (int64_t)b * cv_st;
+  int64_t* em = emit + (int64_t)b * N;
+  int64_t* cm = committed + (int64_t)b * N;
+  const int blk = 2 * N - 1;
+  const bool ver = verify[b] != 0;
+  kind[b] = ver ? 1 : 0;
+  if (!ver) {  // cold start [t0, MASK...]: emit the clean token, its row's successors become the specs
+    em[0] = a[0];
+    n_emit[b] = 1;
+    cm[0] = cv[0];
+    n_keep[b] = 1;
+    cv[0] = a[0];
+    for (int j = 1; j < N; ++j) cv[j] = a[j];
+    for (int j = N; j < blk; ++j) cv[j] = mask_id;
+    verify[b] = 1;
+    return;
+  }
+  const int acc = min(max(n_acc[b], 0), N - 1);
+  cm[0] = cv[0];
+  for (int j = 0; j < acc; ++j) {
+    em[j] = cv[1 + j];
+    cm[1 + j] = cv[1 + j];
+  }
+  n_keep[b] = 1 + acc;
+  if (acc < N - 1) {  // rejected at spec acc: the correction, then a cold start from it
+    em[acc] = a[acc];
+    n_emit[b] = acc + 1;
+    cv[0] = a[acc];
+    for (int j = 1; j < blk; ++j) cv[j] = mask_id;
+    verify[b] = 0;
+  } else {  // every spec accepted: the clean token, and the MASK rows' predictions as the next specs
+    em[N - 1] = a[N - 1];
+    n_emit[b] = N;
+    cv[0] = a[N - 1];
+    for (int j = 1; j < N; ++j) cv[j] = a[N - 1 + j];
+    for (int j = N; j < blk; ++j) cv[j] = mask_id;
+    verify[b] = 1;
+  }
+}
+
 // Split a row into chunks of one tile each (kThreads * U float4), U in {4, 8, 16}: the largest U
 // that still gives at least ~512 blocks; callers may force the split count.
 void plan(int64_t B, int64_t R, int64_t V, int64_t splits_req, int elems, int64_t* S, int64_t* chunk) {
@@ -617,4 +667,19 @@ extern "C" int trida_unmask_top(const int64_t* argmax, const float* conf, int64_
   hipLaunchKernelGGL(unmask_top_kernel, dim3((unsigned)B), dim3(256), 0, static_cast<hipStream_t>(stream), argmax, conf,
                      row_stride, masked, canvas, canvas_stride, (int)block, (int)count);
   return launch_status("unmask_top");
+}
+
+extern "C" int trida_canvas_advance(const int64_t* argmax, int64_t argmax_stride, const int32_t* n_acc, int64_t* canvas,
+                                    int64_t canvas_stride, uint8_t* verify, int32_t* n_keep, int64_t* emit,
+                                    int32_t* n_emit, int64_t* committed, int32_t* kind, int64_t B, int64_t N,
+                                    int64_t mask_id, void* stream) {
+  TRIDA_CHECK(argmax && n_acc && canvas && verify && n_keep && emit && n_emit && committed && kind, TRIDA_ERR_NULL,
+              "canvas_advance: every pointer is required");
+  TRIDA_CHECK(B > 0 && B < INT32_MAX && N >= 2 && N <= 512, TRIDA_ERR_ARG, "canvas_advance: bad sizes B=%lld N=%lld",
+              (long long)B, (long long)N);
+  TRIDA_CHECK(argmax_stride >= 2 * N - 1 && canvas_stride >= 2 * N - 1, TRIDA_ERR_ARG, "canvas_advance: strides");
+  hipLaunchKernelGGL(canvas_advance_kernel, dim3((unsigned)cdiv(B, 64)), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     argmax, argmax_stride, n_acc, canvas, canvas_stride, verify, n_keep, emit, n_emit, committed, kind,
+                     (int)B, (int)N, mask_id);
+  return launch_status("canvas_advance");
 }

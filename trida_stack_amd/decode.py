@@ -6,7 +6,8 @@ selfspec_generate; decode.py:35-387) over the GPU runtime of trida_stack_amd.mod
   selfspec_generate(..., n, denoise_steps=0)   the reference canvas algorithm (bd_bidir_shift):
       cold start [t0, MASK x (2n-2)]; verify round [pending, spec_1..spec_{n-1}, MASK x (n-1)] with
       n_clean = n; spec_i verified against row i; all accepted -> clean = row n-1, new specs = rows
-      n..2n-2; reject at i -> emit the accepted specs + correction, next step cold.
+      n..2n-2; reject at i -> emit the accepted specs + correction, next step cold. Greedy steps run
+      as CanvasSpecStep (the next-canvas decision on the device), replayed from one HIP graph.
   selfspec_generate(..., n, denoise_steps=D)   draft-then-verify over a block of n: D block-diffusion
       passes over [t0, MASK x n] (each unmasks the most confident MASK slots, shift readout), then a
       token-causal verify pass over [t0, d_1..d_n], greedy acceptance and rollback of the hybrid state
@@ -384,57 +385,145 @@ def selfspec_generate(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_ne
         yield from _blockspec(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids, mask_id=mask_id,
                               block=n, denoise=denoise_steps, stats=stats, sp=sp)
         return
+    yield from _canvas_spec(rt, cache, prompt, max_new_tokens=max_new_tokens, eos_ids=eos_ids, sp=sp, mask_id=mask_id,
+                            n=n, stats=stats)
+
+
+def _capture_step(step, cache, state: list) -> "torch.cuda.CUDAGraph":
+    """Records step.run() into a HIP graph. Two warm-up runs on a side stream first create workspaces,
+    allocator pools and library handles; they are undone (cache state, lengths and the `state` tensors
+    restored), so the cache is left as it was. Attention key splits are planned for the cache capacity
+    (splits past a sequence's keys exit at once), so one graph serves every step."""
+    rt = step.rt
+    cache.ctx_hint = max(cache.ctx_hint, cache.Lmax)
+    snap = cache.snapshot()
+    saved = [t.clone() for t in state]
+
+    def undo():
+        cache.restore(snap)
+        for t, v in zip(state, saved):
+            t.copy_(v)
+
+    side = torch.cuda.Stream(rt.dev)
+    side.wait_stream(torch.cuda.current_stream(rt.dev))
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step.run()
+            undo()
+    torch.cuda.current_stream(rt.dev).wait_stream(side)
+    torch.cuda.synchronize(rt.dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step.run()
+    torch.cuda.synchronize(rt.dev)
+    undo()
+    return g
+
+
+class CanvasSpecStep:
+    """One batched bd_bidir_shift canvas step (decode.py:318-384) on device buffers of fixed shape, so that a
+    whole step replays from one HIP graph: the canvas forward (rows < n token-causal; MASK rows see the
+    block and read the block-end GDN state), greedy acceptance of the specs against rows 0..n-2, the
+    device-side decision of what is emitted and what the next canvas is (trida_canvas_advance), and the
+    rollback to the committed rows (KV crop + GDN restore).
+
+    State: canvas [B, 2n-1] ([t0, MASK...] cold, or [pending, specs, MASK...]) and verify [B] (uint8).
+    Outputs after run(): emit [B, n] / n_emit [B] (tokens emitted), committed [B, n] / n_keep [B] (rows
+    committed), kind [B] (1 for a verify round). rules: the decode's ban / gate rules (every row), or None;
+    with gate notes wanted, raw_p [B, 2n-1, n_gate] holds the rows' raw gate probabilities."""
+
+    def __init__(self, rt: TridaRuntime, cache: SeqCache, n: int, rules: Optional[LogitRules] = None):
+        if n < 2:
+            raise ValueError("the canvas needs n >= 2 (one pending token and at least one spec)")
+        self.rt, self.cache, self.n = rt, cache, n
+        self.rules = rules if rules is not None and rules.active else None
+        B, blk = cache.B, 2 * n - 1
+        dev = rt.dev
+        i32, i64 = dict(dtype=torch.int32, device=dev), dict(dtype=torch.int64, device=dev)
+        self.canvas = torch.full((B, blk), rt.mask_id, **i64)
+        self.verify = torch.zeros(B, dtype=torch.uint8, device=dev)
+        self.live = torch.zeros(B, **i32)
+        self.am = torch.empty(B, blk, **i64)
+        self.acc = (torch.empty(B, **i32), torch.empty(B, **i64), torch.empty(B, **i64))
+        self.n_keep, self.n_emit, self.kind = torch.zeros(B, **i32), torch.zeros(B, **i32), torch.zeros(B, **i32)
+        self.emit, self.committed = torch.zeros(B, n, **i64), torch.zeros(B, n, **i64)
+        self.raw_p = None
+        if self.rules is not None and self.rules.log is not None:
+            self.raw_p = torch.zeros(B, blk, self.rules.n_gate, dtype=torch.float32, device=dev)
+        self.graph = None
+
+    def start(self, t0: torch.Tensor) -> None:
+        """Cold canvases [t0, MASK...] for every sequence (t0 [B] int64, already emitted)."""
+        self.canvas.fill_(self.rt.mask_id)
+        self.canvas[:, 0] = t0
+        self.verify.zero_()
+
+    def run(self) -> None:
+        rt, cache, n = self.rt, self.cache, self.n
+        self.live.copy_(self.verify)
+        self.live.mul_(n - 1)  # specs that count: n - 1 on a verify canvas, none on a cold one
+        L = rt.forward(self.canvas, cache, "canvas", n_clean=n)
+        if self.rules is not None:
+            self.rules.apply(L, self.raw_p)
+        n_acc, bonus, crop = self.acc
+        with K.timed("greedy_accept"):
+            K.greedy_accept(L, self.canvas[:, 1:n], n_live=self.live, out=(self.am, n_acc, bonus, crop))
+        K.canvas_advance(self.am, n_acc, self.canvas, self.verify,
+                         (self.n_keep, self.emit, self.n_emit, self.committed, self.kind), rt.mask_id)
+        cache.pending = {"T": 2 * n - 1}
+        rt.commit(cache, self.n_keep)
+
+    def capture(self) -> None:
+        self.graph = _capture_step(self, self.cache, [self.canvas, self.verify])
+
+    def replay(self) -> None:
+        self.graph.replay()
+
+
+def _canvas_spec(rt: TridaRuntime, cache: SeqCache, prompt: list, *, max_new_tokens: int, eos_ids: set,
+                 sp: SamplingParams, mask_id: int, n: int, stats: Optional[DecodeStats],
+                 graph: bool = True) -> Iterator[list]:
+    """Greedy self-spec with the bd_bidir_shift canvas (decode.py:297-387), each step a CanvasSpecStep
+    replayed from one HIP graph; the host reads the step's emitted and committed tokens once."""
     stats = stats or DecodeStats()
     stats.mode = f"self-spec(N={n})"
     stats.accept_hist = [0] * n
     rules = LogitRules(sp, rt.dev)
-    blk, Kd = 2 * n - 1, n - 1
+    if mask_id != rt.mask_id:
+        raise ValueError(f"mask_id {mask_id} is not the runtime's ({rt.mask_id})")
     logits = _prefill(rt, cache, prompt, stats)
     emit = _Emitter(stats, max_new_tokens, eos_ids)
     t_start = time.perf_counter()
     t0 = _greedy_row(rules, logits)
-    t0_emitted = False
-    pending = specs = None
-    dev = rt.dev
-    raw = rules.raw_buffer(blk, dev)
+    out = emit([t0])
+    if out:
+        yield out
+    step = CanvasSpecStep(rt, cache, n, rules)
+    step.start(torch.full((1,), t0, dtype=torch.int64, device=rt.dev))
+    use_graph = graph and rt.dev.type == "cuda"
     while not emit.done:
-        _room(cache, blk)
-        if specs is not None:  # ---- verify round
-            L = rt.canvas(cache, [pending] + specs + [mask_id] * (n - 1), n, as_float=False)
-            stats.forwards += 1
-            if rules.active:
-                rules.apply(L, raw)
-            drafts = torch.as_tensor([specs], dtype=torch.int64, device=dev)
-            am, n_acc, _, _ = K.greedy_accept(L[None], drafts)
-            vals = am[0].tolist()
-            acc = int(n_acc[0])
-            if raw is not None:  # rows that saw real context (decode.py:358)
-                rules.note(raw[: acc + 1 if acc < Kd else n].tolist())
-            if acc < Kd:  # rejected at spec `acc`: emit accepted specs + correction, next step cold
-                rt.commit(cache, 1 + acc)
-                stats.accept_hist[acc] += 1
-                out = emit(specs[:acc] + [vals[acc]])
-                t0, t0_emitted = vals[acc], True
-                pending = specs = None
-            else:  # all accepted: n tokens this forward
-                rt.commit(cache, n)
-                stats.accept_hist[Kd] += 1
-                out = emit(specs + [vals[n - 1]])
-                pending, specs = vals[n - 1], vals[n:blk]
-        else:  # ---- cold start
-            L = rt.canvas(cache, [t0] + [mask_id] * (blk - 1), n, rows=n if rt.skip_rows else None, as_float=False)
-            stats.forwards += 1
+        _room(cache, 2 * n - 1)
+        if use_graph and step.graph is None and stats.forwards >= 1:
+            step.capture()
+        if step.graph is not None:
+            step.replay()
+        else:
+            step.run()
+        stats.forwards += 1
+        stats.steps += 1
+        packed = torch.cat([step.kind[:1].to(torch.int64), step.n_emit[:1].to(torch.int64),
+                            step.n_keep[:1].to(torch.int64), step.emit[0], step.committed[0]]).tolist()
+        kind, ne, nk = packed[0], packed[1], packed[2]
+        toks, committed = packed[3: 3 + ne], packed[3 + n: 3 + n + nk]
+        cache.tokens[0].extend(committed)
+        cache.ctx_hint = len(cache.tokens[0])
+        if kind:
+            stats.accept_hist[ne - 1] += 1
+        else:
             stats.cold_forwards += 1
-            if rules.active:
-                rules.apply(L[:n], None if raw is None else raw[:n])
-                if raw is not None:
-                    rules.note(raw[:1].tolist())
-            am, _ = K.row_argmax(L[:n], want_conf=False)
-            vals = am.tolist()
-            rt.commit(cache, 1)
-            out = emit(([] if t0_emitted else [t0]) + [vals[0]])
-            t0_emitted = True
-            pending, specs = vals[0], vals[1:n]
+        if step.raw_p is not None:  # rows that saw real context (decode.py:358)
+            rules.note(step.raw_p[0, :ne].tolist())
+        out = emit(toks)
         if out:
             yield out
     stats.decode_s = time.perf_counter() - t_start
@@ -512,27 +601,8 @@ class BlockSpecStep:
 
     def capture(self) -> None:
         """Records one whole step (every kernel of the denoise and verify forwards, the acceptance and the
-        rollback) into a HIP graph; replay() then launches it with one call. The step reads lengths and
-        positions on the device, so one graph serves every step; the attention key splits are planned for
-        the cache capacity (splits past a sequence's keys exit at once). The warm-up runs that precede the
-        capture are undone (cache state, lengths and t0 restored), so the cache is left as it was."""
-        rt, cache = self.rt, self.cache
-        cache.ctx_hint = max(cache.ctx_hint, cache.Lmax)
-        snap, t0 = cache.snapshot(), self.t0.clone()
-        side = torch.cuda.Stream(rt.dev)
-        side.wait_stream(torch.cuda.current_stream(rt.dev))
-        with torch.cuda.stream(side):
-            for _ in range(2):  # workspaces, allocator pools and library handles exist before capture
-                self.run()
-                cache.restore(snap)
-                self.t0.copy_(t0)
-        torch.cuda.current_stream(rt.dev).wait_stream(side)
-        torch.cuda.synchronize(rt.dev)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            self.run()
-        torch.cuda.synchronize(rt.dev)
-        self.graph = g
+        rollback) into a HIP graph; replay() then launches it with one call (_capture_step)."""
+        self.graph = _capture_step(self, self.cache, [self.t0])
 
     def replay(self) -> None:
         """One step from the captured graph (capture() first)."""

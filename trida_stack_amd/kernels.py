@@ -185,6 +185,32 @@ def unmask_top(argmax: torch.Tensor, conf: torch.Tensor, masked: torch.Tensor, c
     _lib.check(rc, "trida_unmask_top")
 
 
+def canvas_advance(argmax: torch.Tensor, n_acc: torch.Tensor, canvas: torch.Tensor, verify: torch.Tensor,
+                   out, mask_id: int) -> None:
+    """The device-side decision of a bd_bidir_shift canvas step (selfspec_generate, decode.py:318-384):
+    canvas [B, 2N-1] int64 and verify [B] uint8 are updated in place; out = (n_keep [B] int32, emit [B, N]
+    int64, n_emit [B] int32, committed [B, N] int64, kind [B] int32)."""
+    dev = _need_gpu(argmax, n_acc, canvas, verify)
+    B, blk = canvas.shape
+    N = (blk + 1) // 2
+    n_keep, emit, n_emit, committed, kind = out
+    if blk != 2 * N - 1 or canvas.dtype != torch.int64 or canvas.stride(1) != 1:
+        raise ValueError("canvas must be int64 [B, 2N-1] with contiguous rows")
+    if argmax.dtype != torch.int64 or argmax.shape[0] != B or argmax.shape[1] < blk or argmax.stride(1) != 1:
+        raise ValueError("argmax must be int64 [B, >= 2N-1]")
+    if verify.dtype != torch.uint8 or verify.shape != (B,) or n_acc.dtype != torch.int32 or n_acc.shape != (B,):
+        raise ValueError("verify must be uint8 [B] and n_acc int32 [B]")
+    for t, dt, shape in ((n_keep, torch.int32, (B,)), (emit, torch.int64, (B, N)), (n_emit, torch.int32, (B,)),
+                         (committed, torch.int64, (B, N)), (kind, torch.int32, (B,))):
+        if t.dtype != dt or t.shape != shape or not t.is_contiguous():
+            raise ValueError("canvas_advance outputs have the wrong dtype or shape")
+    rc = _lib.load().trida_canvas_advance(argmax.data_ptr(), argmax.stride(0), n_acc.data_ptr(), canvas.data_ptr(),
+                                          canvas.stride(0), verify.data_ptr(), n_keep.data_ptr(), emit.data_ptr(),
+                                          n_emit.data_ptr(), committed.data_ptr(), kind.data_ptr(), B, N, int(mask_id),
+                                          _stream(dev))
+    _lib.check(rc, "trida_canvas_advance")
+
+
 def _rows2d(logits: torch.Tensor):
     """(rows, V, row stride) of logits [..., V] whose rows are evenly strided (a row-major view)."""
     V = logits.shape[-1]
