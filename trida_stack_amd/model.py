@@ -178,25 +178,43 @@ class SeqCache:
         self.tokens = [list(t) for t in tokens]
 
 
+# hipBLASLt's heuristic picks a kernel about twice as slow for M <= 16 rows as for M = 17 at the decode
+# projection shapes (gate/up 19456 x 2560: 46.8 us at M = 1..16, 23.5 us at M = 17; gdn in, attention
+# qkv / o likewise slower), so the projections of forwards of at most 16 rows (AR steps, canvases of
+# 2n - 1 <= 15 rows) run on GEMM_MIN_ROWS rows, the extra rows zero and their outputs unused.
+GEMM_MIN_ROWS = 17
+
+
 class _Scratch:
-    """Per-(B, T) activation buffers, reused across forwards (fixed addresses for graph capture)."""
+    """Per-(B, T) activation buffers, reused across forwards (fixed addresses for graph capture). The GEMM
+    operands are allocated with Np >= B * T rows (zeros past B * T; see GEMM_MIN_ROWS); the attributes
+    without `_p` are the B * T-row views the row-wise kernels use."""
 
     def __init__(self, cfg: HybridConfig, B: int, T: int, n_gdn: int, dev):
         bf = dict(dtype=torch.bfloat16, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
         N = B * T
+        Np = GEMM_MIN_ROWS if N < GEMM_MIN_ROWS else N
+        self.N, self.Np = N, Np
         h = cfg.hidden
+        W_in = cfg.conv_dim + cfg.value_dim + 2 * cfg.lin_v_heads
+        W_qkv = (2 * cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim
         self.h = torch.empty(N, h, **bf)
-        self.x = torch.empty(N, h, **bf)
-        self.r = torch.empty(N, h, **bf)
-        self.gu = torch.empty(N, 2 * cfg.intermediate, **bf)
-        self.act = torch.empty(N, cfg.intermediate, **bf)
-        self.proj = torch.empty(B, T, cfg.conv_dim + cfg.value_dim + 2 * cfg.lin_v_heads, **bf)
-        self.qkv = torch.empty(B, T, (2 * cfg.n_heads + 2 * cfg.n_kv_heads) * cfg.head_dim, **bf)
+        self.x_p = torch.zeros(Np, h, **bf)
+        self.r_p = torch.zeros(Np, h, **bf)
+        self.gu_p = torch.zeros(Np, 2 * cfg.intermediate, **bf)
+        self.act_p = torch.zeros(Np, cfg.intermediate, **bf)
+        self.proj_p = torch.zeros(Np, W_in, **bf)
+        self.qkv_p = torch.zeros(Np, W_qkv, **bf)
+        self.o_att_p = torch.zeros(Np, cfg.n_heads * cfg.head_dim, **bf)
+        self.yn_p = torch.zeros(Np, cfg.lin_v_heads * cfg.lin_v_dim, **bf)
+        self.x, self.r, self.gu, self.act = self.x_p[:N], self.r_p[:N], self.gu_p[:N], self.act_p[:N]
+        self.proj = self.proj_p[:N].view(B, T, W_in)
+        self.qkv = self.qkv_p[:N].view(B, T, W_qkv)
+        self.o_att = self.o_att_p[:N].view(B, T, cfg.n_heads, cfg.head_dim)
+        self.yn = self.yn_p[:N].view(N, cfg.lin_v_heads, cfg.lin_v_dim)
         self.q_att = torch.empty(B, T, cfg.n_heads, cfg.head_dim, **bf)
-        self.o_att = torch.empty(B, T, cfg.n_heads, cfg.head_dim, **bf)
         self.y = torch.empty(B, T, cfg.lin_v_heads, cfg.lin_v_dim, **bf)
-        self.yn = torch.empty(N, cfg.lin_v_heads, cfg.lin_v_dim, **bf)
         self.q = torch.empty(B, T, cfg.lin_k_heads, cfg.lin_k_dim, **bf)
         self.win_tmp = torch.empty(B, cfg.conv_kernel - 1, cfg.conv_dim, **bf)
         # per-GDN-layer block rows kept for commit (stacked so one restore launch covers every layer)
@@ -328,7 +346,7 @@ class TridaRuntime:
             first = False
             j = self._slot[i]
             if c.is_attention(i):
-                self._mm(s.x, w[p + "w_qkv"], s.qkv.view(N, -1))
+                self._mm(s.x_p, w[p + "w_qkv"], s.qkv_p)
                 with K.timed("attn_prep"):
                     K.attn_prep(s.qkv, w[p + "q_norm"], w[p + "k_norm"], pos, length, s.q_att, kv_k[j], kv_v[j],
                                 Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, rot_dim=c.rot_dim,
@@ -340,9 +358,9 @@ class TridaRuntime:
                 with K.timed("attn_canvas"):
                     K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
                                   out=s.o_att, max_keys=max_keys)
-                self._mm(s.o_att.view(N, -1), w[p + "w_o"], s.r)
+                self._mm(s.o_att_p, w[p + "w_o"], s.r_p)
             else:
-                self._mm(s.x, w[p + "w_in"], s.proj.view(N, -1))
+                self._mm(s.x_p, w[p + "w_in"], s.proj_p)
                 xv = s.proj[..., : c.conv_dim]
                 off = c.conv_dim + c.value_dim
                 b_in = s.proj[..., off: off + c.lin_v_heads]
@@ -379,11 +397,11 @@ class TridaRuntime:
                     window[j].copy_(s.win_tmp)
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
                 K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
-                self._mm(s.yn.view(N, -1), w[p + "w_out"], s.r)
+                self._mm(s.yn_p, w[p + "w_out"], s.r_p)
             K.add_rmsnorm(s.h, s.r, w[p + "post_norm"], s.x, eps=c.rms_eps)
-            self._mm(s.x, w[p + "w_gu"], s.gu)
+            self._mm(s.x_p, w[p + "w_gu"], s.gu_p)
             K.silu_mul(s.gu, s.act)
-            self._mm(s.act, w[p + "w_down"], s.r)
+            self._mm(s.act_p, w[p + "w_down"], s.r_p)
         K.add_rmsnorm(s.h, s.r, w["final_norm"], s.x, eps=c.rms_eps)
         x = s.x.view(B, T, -1)
         if rows is not None or row0:
