@@ -730,6 +730,40 @@ def bench_canvas(args, rt=None, n: int = 4):
                                    "inference/zoro-1/vllm/docs/SELFSPEC_VLLM_PLAN.md:83)"}
 
 
+def bench_fwd(args):
+    """Decoder forwards only, for counter runs: `steps` eager verify forwards of 33 rows at batch 1 (or
+    64 x 33 rows with --fwd-batch 64) over a cache whose committed length is set to 2048 tokens (the
+    KV entries and states are zeros; the kernels read them in full all the same), so that every dispatch
+    after the weights are drawn belongs to a forward. Prints the per-forward time."""
+    import torch
+
+    from trida_stack_amd.model import HybridConfig, build_runtime
+
+    cfg = HybridConfig.four_b()
+    rt = build_runtime(cfg, seed=0)
+    B = args.fwd_batch
+    cache = rt.make_cache(B, max_len=PROMPT_LEN + BLOCK + 1 + 64)
+    cache.length.fill_(PROMPT_LEN)
+    cache.pos.fill_(PROMPT_LEN)
+    cache.tokens = [[0] * PROMPT_LEN for _ in range(B)]
+    cache.ctx_hint = PROMPT_LEN
+    ids = torch.randint(0, cfg.vocab - 1024, (B, BLOCK + 1), device=rt.dev)
+    # a calibration copy of known size (256 MiB read + 256 MiB written), for scaling the counters
+    src = torch.ones(64 << 20, dtype=torch.float32, device=rt.dev)
+    torch.empty_like(src).copy_(src)
+    del src
+    for _ in range(max(1, args.warmup)):
+        rt.forward(ids, cache, "verify")
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(args.steps):
+        rt.forward(ids, cache, "verify")
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t) / args.steps
+    return {"workload": f"{args.steps} eager verify forwards, batch {B} x 33 rows, 2048-token context",
+            "forwards": args.steps + max(1, args.warmup), "ms_per_forward_eager": round(dt * 1e3, 3)}
+
+
 def bench_default(args):
     """The headline line: batch 1 (value) and batch 64 (the "bs64" object) on one random-init runtime."""
     import torch
@@ -927,7 +961,7 @@ def bench_gemm(args):
             "cpu_baseline": None}
 
 
-WORKLOADS = {"default": (bench_default, 20, 5), "canvas": (lambda a: bench_canvas(argparse.Namespace(**dict(vars(a), canvas_steps=a.steps))), 64, 0), "e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "gdr": (bench_gdr, 20, 3), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
+WORKLOADS = {"default": (bench_default, 20, 5), "fwd": (bench_fwd, 8, 1), "canvas": (lambda a: bench_canvas(argparse.Namespace(**dict(vars(a), canvas_steps=a.steps))), 64, 0), "e2e": (bench_e2e, 256, 8), "e2e64": (bench_e2e64, 12, 2), "gdr": (bench_gdr, 20, 3), "accept": (bench_accept, 100, 10), "gemm": (bench_gemm, 50, 1),
              "sample": (bench_sample, 20, 3), "attn": (bench_attn, 100, 10)}
 
 
@@ -941,6 +975,7 @@ def main():
     ap.add_argument("--bs64-steps", type=int, default=6, help="default workload: timed batch-64 steps")
     ap.add_argument("--bs64-warmup", type=int, default=2)
     ap.add_argument("--canvas-steps", type=int, default=32, help="default workload: timed canvas-algorithm steps")
+    ap.add_argument("--fwd-batch", type=int, default=1, help="fwd workload: sequences per forward")
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=3, help="timed CPU-oracle steps (median; after one warm-up)")
     ap.add_argument("--no-cpu", action="store_true")
