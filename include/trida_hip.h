@@ -375,19 +375,33 @@ int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t
  *   [B, T, Hq, D], k and v to the caches [B, Hkv, Lmax, D] at slot slot0[b] + t (rows whose slot is
  *   outside [0, Lmax) write no K / V).
  */
-/* Skinny bf16 GEMM for canvas-sized activations: Y[M, N] = X[M, K] W[N, K]^T (torch Linear weight
- * layout), fp32 accumulation, bf16 output, 1 <= M <= 64, N % 16 == 0, K % 32 == 0. It replaces the
- * projection / MLP / LM-head matmuls of the decoder forward at decode-step sizes
- * (TridaRuntime._forward, inference/zoro-1/mlx/trida_mlx/model.py:337-364), which are bound by the
- * weight stream. Row strides in elements. splits = 0 picks the K split; scratch:
- * trida_skinny_gemm_scratch_bytes(M, N, K, splits) bytes (0 when no split is used). */
-int64_t trida_skinny_gemm_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t splits);
-int trida_skinny_gemm(const uint16_t* X, int64_t x_row_stride, const uint16_t* W, int64_t w_row_stride, uint16_t* Y,
-                      int64_t y_row_stride, int64_t M, int64_t N, int64_t K, void* scratch, int64_t scratch_bytes,
-                      int64_t splits, void* stream);
+/* Weight-streaming bf16 GEMM for canvas-sized activations: out = X[M, K] W[N, K]^T (torch Linear weight
+ * layout), fp32 accumulation, 1 <= M <= 48, N % 16 == 0, K % 32 == 0. It replaces the projection and MLP
+ * matmuls of the decoder forward at decode-step sizes (TridaRuntime._forward,
+ * inference/zoro-1/mlx/trida_mlx/model.py:337-364), which are bound by the weight stream.
+ * trida_wsgemm_shuffle writes the weights once into the kernel's layout Wp (N * K bf16, 16-byte aligned):
+ *   tile t (16 rows) x k-step s (32 columns) x lane l = 16 g + r -> 8 bf16 of W[row][32 s + 8 g ..];
+ *   row = 16 t + r, or with pair_halves = 1 (W = [gate; up], N / 2 rows each) row = 8 t + r for r < 8
+ *   and N / 2 + 8 t + r - 8 otherwise, which the SwiGLU epilogue needs.
+ * trida_wsgemm epilogues: 0 = bf16 out [M, N] (row stride out_row_stride); 1 = fp32 partial planes
+ *   out[kg][M][N] (dense; kg from trida_wsgemm_plan), summed by trida_add_rmsnorm_parts;
+ *   2 = SwiGLU: bf16 out[M, N / 2] = silu(gate) * up over pair_halves weights (gate and up rounded to
+ *   bf16 first, as a bf16 GEMM output would be).
+ * The plan depends on (N, K, epilogue) only, so a row of the result is bitwise independent of M.
+ * trida_wsgemm_plan returns in *kgroups the number of partial planes epilogue 1 writes (1 otherwise). */
+int trida_wsgemm_shuffle(const uint16_t* W, int64_t N, int64_t K, int64_t w_row_stride, int pair_halves, uint16_t* Wp,
+                         void* stream);
+int trida_wsgemm_plan(int64_t N, int64_t K, int epilogue, int32_t* kgroups);
+int trida_wsgemm(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M, int64_t N, int64_t K,
+                 int epilogue, void* out, int64_t out_row_stride, void* stream);
 
 int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim,
                       int64_t x_st, int64_t r_st, int64_t o_st, float eps, int zero_centred, void* stream);
+/* add_rmsnorm whose residual is the sum of n_parts fp32 planes (plane_stride elements apart, rows of dim
+ * floats): the partial planes of trida_wsgemm epilogue 1, summed in plane order and rounded to bf16. */
+int trida_add_rmsnorm_parts(uint16_t* x, const float* parts, int64_t n_parts, int64_t plane_stride, const uint16_t* w,
+                            uint16_t* out, int64_t rows, int64_t dim, int64_t x_st, int64_t o_st, float eps,
+                            int zero_centred, void* stream);
 int trida_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter, int64_t g_st, int64_t o_st,
                    void* stream);
 int trida_gated_rmsnorm(const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out, int64_t rows,

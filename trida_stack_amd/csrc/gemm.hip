@@ -1,17 +1,21 @@
-// Skinny bf16 GEMM for the decode-step projections: Y[M, N] = X[M, K] W[N, K]^T with M <= 64
-// (a canvas of <= 64 rows), fp32 accumulation, bf16 output. At these M the GEMM is bound by the weight
-// stream, so the kernel is built to read every weight byte exactly once, with enough of them in flight
-// to cover the HBM latency:
-//   - v_mfma_f32_16x16x32_bf16 accumulates C^T[n, m]: the weight rows are the A operand (16-byte
-//     loads straight into registers; plain loads: the nontemporal hint measured 15-30% slower on a
-//     pure weight stream), the activation rows the B operand (L2-resident);
-//   - a wave owns NR tiles of 16 weight rows, so each activation fragment it loads feeds NR MFMAs,
-//     and issues KU k-steps of loads (NR * KU weight fragments) before the MFMAs that consume them;
-//   - the NW waves of a workgroup split K and reduce through LDS; NR and NW are chosen per shape so
-//     that the grid holds ~1000 or more waves without splitting K across workgroups (which would cost
-//     fp32 partials and a reduce launch; kept for shapes too narrow for that).
-// Each output's K sum runs in an order that depends on N and K only, so a row of Y is the same whether
-// X holds 1 row or 64.
+// Weight-streaming bf16 GEMM for the decode-step projections: Y[M, N] = X[M, K] W[N, K]^T with M <= 48
+// (a canvas of <= 48 rows), fp32 accumulation. At these M every projection is bound by the weight stream
+// (N * K * 2 bytes read once), so the kernel is built around that stream:
+//   - the weights are stored once more in a pre-shuffled layout (trida_wsgemm_shuffle): tile t of 16
+//     rows, k-step s of 32 columns, lane l = 16 g + r holds W[16 t + r][32 s + 8 g .. + 8] as 16 bytes, the
+//     A operand of v_mfma_f32_16x16x32_bf16 as it lands in a register. A wave's walk over one tile is
+//     then one contiguous run of memory;
+//   - X is stationary: wave w of a workgroup owns KWS consecutive k-steps and loads its slice of X (the
+//     B operand, tokens as columns) into registers once; it then streams the weights of the workgroup's
+//     T tiles over that K slice with D k-steps of loads in flight (a register ring whose loads are pinned
+//     in issue order by sched_barrier, so the compiler neither sinks them nor drains the ring);
+//   - per tile the NW waves' partial 16 x 16*MT tiles meet in LDS (double-buffered slot, one s_barrier
+//     per tile, no wait on the weight loads still in flight) and 64*MT threads finish them;
+//   - K beyond NW * KWS steps is split over kg workgroup groups that write fp32 partial planes
+//     [kg][M][N]; trida_add_rmsnorm_parts (norms.hip) sums them in plane order.
+// Epilogues: bf16 store, fp32 partials, or SwiGLU (silu(gate) * up) over weights whose tiles interleave 8
+// gate rows with the matching 8 up rows. The plan (NW, KWS, T, kg) depends on N, K and the epilogue only:
+// a row of Y is bitwise the same whether X holds 1 row or 48.
 #include <algorithm>
 
 #include "common.h"
@@ -19,155 +23,219 @@
 namespace trida {
 namespace {
 
+constexpr int kCUs = 256;  // MI355X (gfx950): workgroups of a plan <= one per CU, see plan_for()
+constexpr int kMaxM = 48;
+
+enum Epilogue { kStore = 0, kParts = 1, kSilu = 2 };
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ bf16x8 as_bf(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
+__device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
 
-struct GemmArgs {
+struct WsArgs {
   const uint16_t* X;
-  const uint16_t* W;
-  uint16_t* Y;
-  float* partial;  // [SK, M, N] when SK > 1
-  int64_t x_st, w_st, y_st;
-  int M, N, K, SK;
+  const u32x4* Wp;
+  void* out;
+  int64_t x_st, o_st;
+  int M, N, K, T;
 };
 
-template <int MT, int NR, int NW, int KU>
-__global__ __launch_bounds__(NW* kWave) void skinny_gemm_kernel(GemmArgs a) {
-  const int ng = blockIdx.x, sk = blockIdx.y;
+template <int NW, int KWS, int D, int MT, int EPI>
+__global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
+  static_assert(KWS % D == 0 || D % KWS == 0, "the ring and the K slice must tile the unrolled loop");
+  static_assert(MT <= NW, "the epilogue uses 64 * MT threads");
+  __shared__ f32x4 red[2][NW][MT][kWave];
   const int wave = threadIdx.x / kWave, l = threadIdx.x % kWave;
-  const int ksteps = a.K / 32;
-  const int part = sk * NW + wave, nparts = a.SK * NW;
-  const int s0 = (int)((int64_t)ksteps * part / nparts);
-  const int s1 = (int)((int64_t)ksteps * (part + 1) / nparts);
-  const int n0 = ng * NR * 16;
-  const u32x4* wrow[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r)
-    wrow[r] = reinterpret_cast<const u32x4*>(a.W + (int64_t)(n0 + r * 16 + (l % 16)) * a.w_st + (l / 16) * 8);
-  const u32x4* xrow[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = min(mt * 16 + (l % 16), a.M - 1);  // rows past M repeat the last row; never stored
-    xrow[mt] = reinterpret_cast<const u32x4*>(a.X + (int64_t)m * a.x_st + (l / 16) * 8);
-  }
-  f32x4 acc[NR][MT];
-#pragma unroll
-  for (int r = 0; r < NR; ++r)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[r][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int tiles = a.N / 16, nsteps = a.K / 32;
+  const int t0 = blockIdx.x * a.T, nt = min(tiles, t0 + a.T) - t0;
+  const int s_base = (blockIdx.y * NW + wave) * KWS;
+  const int my_steps = max(0, min(KWS, nsteps - s_base));  // k-steps of this wave inside K
 
-  int s = s0;
-  for (; s + KU <= s1; s += KU) {
-    u32x4 wv[KU][NR];
+  // weight stream: unit u = (tile t0 + u / KWS, k-step s_base + u % KWS); loads past the last unit
+  // re-read it and steps past K read the last step (in bounds; their X is zero)
+  const int nu = nt * KWS;
+  auto wptr = [&](int u) {
+    u = min(u, nu - 1);
+    const int t = t0 + u / KWS, s = min(s_base + u % KWS, nsteps - 1);
+    return a.Wp + ((int64_t)t * nsteps + s) * kWave + l;
+  };
+  u32x4 wv[D];
 #pragma unroll
-    for (int u = 0; u < KU; ++u)
-#pragma unroll
-      for (int r = 0; r < NR; ++r) wv[u][r] = wrow[r][(int64_t)(s + u) * 4];
-    u32x4 xv[KU][MT];
-#pragma unroll
-    for (int u = 0; u < KU; ++u)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xv[u][mt] = xrow[mt][(int64_t)(s + u) * 4];
-    // every load of the batch is issued before the first MFMA waits on one (the scheduler would
-    // otherwise interleave them and keep only a few in flight)
+  for (int j = 0; j < D; ++j) {
+    wv[j] = *wptr(j);
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < KU; ++u)
-#pragma unroll
-      for (int r = 0; r < NR; ++r)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-          acc[r][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(wv[u][r]), as_bf(xv[u][mt]), acc[r][mt], 0, 0, 0);
   }
-  for (; s < s1; ++s) {
-    u32x4 wv[NR], xv[MT];
+  // X slice (issued after the first weight loads, so their latency overlaps): tokens past M repeat row
+  // M - 1 (never stored), steps past K are zeroed
+  u32x4 xs[KWS][MT];
 #pragma unroll
-    for (int r = 0; r < NR; ++r) wv[r] = wrow[r][(int64_t)s * 4];
+  for (int j = 0; j < KWS; ++j) {
+    const int s = min(s_base + j, nsteps - 1);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xv[mt] = xrow[mt][(int64_t)s * 4];
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = min(mt * 16 + (l % 16), a.M - 1);
+      xs[j][mt] = *reinterpret_cast<const u32x4*>(a.X + (int64_t)m * a.x_st + s * 32 + (l / 16) * 8);
+    }
+  }
 #pragma unroll
-    for (int r = 0; r < NR; ++r)
+  for (int j = 0; j < KWS; ++j)
+    if (j >= my_steps) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) xs[j][mt] = u32x4{0u, 0u, 0u, 0u};
+    }
+
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  constexpr int U = KWS > D ? KWS : D;  // units per unrolled pass: ring slot and X step are static
+  for (int u0 = 0; u0 < nu; u0 += U) {
+#pragma unroll
+    for (int jj = 0; jj < U; ++jj) {
+      const int u = u0 + jj;
+      const int j = jj % KWS, r = jj % D;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        acc[r][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(wv[r]), as_bf(xv[mt]), acc[r][mt], 0, 0, 0);
-  }
-
-  // reduce the NW waves' K parts; lane l holds C^T[n = (l/16)*4 + i][m = mt*16 + l%16] of each tile.
-  // Waves 1.. park their partials, then wave w sums the tiles t = w, w + NW, ... and writes them.
-  constexpr int NTILE = NR * MT;
-  __shared__ f32x4 red[NW][NTILE][kWave];
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf(wv[r]), as_bf(xs[j][mt]), acc[mt], 0, 0, 0);
+      wv[r] = *wptr(u + D);
+      __builtin_amdgcn_sched_barrier(0);
+      const int tl = u / KWS;
+      if (j == KWS - 1 && tl < nt) {  // tile tl complete in every wave (the condition is uniform)
+        const int slot = tl & 1;
 #pragma unroll
-  for (int r = 0; r < NR; ++r)
+        for (int mt = 0; mt < MT; ++mt) {
+          red[slot][wave][mt][l] = acc[mt];
+          acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        // LDS writes done, then the barrier; no fence, so the weight loads in flight stay in flight.
+        // Slot reuse is safe: a slot is rewritten two tiles later, after every thread has passed the
+        // next barrier, i.e. finished reading it.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const int i = threadIdx.x;
+        const int tile = t0 + tl;
+        if (EPI == kSilu) {
+          // lanes 0..31 of a C tile hold rows 0..7 (gate), lanes 32..63 rows 8..15 (the matching up)
+          if (i < MT * 32) {
+            const int mt = i / 32, ln = i % 32;
+            f32x4 g = red[slot][0][mt][ln], up = red[slot][0][mt][ln + 32];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) red[wave][r * MT + mt][l] = acc[r][mt];
-  __syncthreads();
-  for (int t = wave; t < NTILE; t += NW) {
-    f32x4 sum = red[0][t][l];
+            for (int w = 1; w < NW; ++w) {
+              g += red[slot][w][mt][ln];
+              up += red[slot][w][mt][ln + 32];
+            }
+            const int m = mt * 16 + (ln % 16);
+            if (m < a.M) {
+              const int f = tile * 8 + (ln / 16) * 4;
+              const float y0 = silu(bf2f(f2bf(g.x))) * bf2f(f2bf(up.x));
+              const float y1 = silu(bf2f(f2bf(g.y))) * bf2f(f2bf(up.y));
+              const float y2 = silu(bf2f(f2bf(g.z))) * bf2f(f2bf(up.z));
+              const float y3 = silu(bf2f(f2bf(g.w))) * bf2f(f2bf(up.w));
+              u32x2 packed;
+              packed.x = f2bf2(y0, y1);
+              packed.y = f2bf2(y2, y3);
+              *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + f) = packed;
+            }
+          }
+        } else if (i < MT * kWave) {
+          const int mt = i / kWave, ln = i % kWave;
+          f32x4 s = red[slot][0][mt][ln];
 #pragma unroll
-    for (int w = 1; w < NW; ++w) sum += red[w][t][l];
-    const int r = t / MT, mt = t % MT;
-    const int m = mt * 16 + (l % 16);
-    if (m >= a.M) continue;
-    const int n = n0 + r * 16 + (l / 16) * 4;
-    if (a.SK == 1) {
-      u32x2 packed;
-      packed.x = f2bf2(sum.x, sum.y);
-      packed.y = f2bf2(sum.z, sum.w);
-      *reinterpret_cast<u32x2*>(a.Y + (int64_t)m * a.y_st + n) = packed;
-    } else {
-      *reinterpret_cast<f32x4*>(a.partial + ((int64_t)sk * a.M + m) * a.N + n) = sum;
+          for (int w = 1; w < NW; ++w) s += red[slot][w][mt][ln];
+          const int m = mt * 16 + (ln % 16);
+          const int n = tile * 16 + (ln / 16) * 4;
+          if (m < a.M) {
+            if (EPI == kStore) {
+              u32x2 packed;
+              packed.x = f2bf2(s.x, s.y);
+              packed.y = f2bf2(s.z, s.w);
+              *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + n) = packed;
+            } else {
+              *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = s;
+            }
+          }
+        }
+      }
     }
   }
 }
 
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* partial, uint16_t* Y, int64_t y_st, int M, int N,
-                                                            int SK) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one thread per 4 outputs
-  if (i >= (int64_t)M * N / 4) return;
-  const int m = (int)(i / (N / 4)), n = (int)(i % (N / 4)) * 4;
-  f32x4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int k = 0; k < SK; ++k) s += *reinterpret_cast<const f32x4*>(partial + ((int64_t)k * M + m) * N + n);
-  u32x2 packed;
-  packed.x = f2bf2(s.x, s.y);
-  packed.y = f2bf2(s.z, s.w);
-  *reinterpret_cast<u32x2*>(Y + (int64_t)m * y_st + n) = packed;
+// pre-shuffle: one thread per 16-byte piece of Wp, in Wp order
+__global__ __launch_bounds__(256) void shuffle_kernel(const uint16_t* W, int64_t ld, int N, int K, int pair,
+                                                      u32x4* Wp) {
+  const int64_t nsteps = K / 32, total = (int64_t)(N / 16) * nsteps * kWave;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int lane = (int)(i % kWave);
+  const int64_t rest = i / kWave;
+  const int s = (int)(rest % nsteps), t = (int)(rest / nsteps);
+  const int r = lane % 16, g = lane / 16;
+  const int row = pair ? (r < 8 ? 8 * t + r : N / 2 + 8 * t + (r - 8)) : 16 * t + r;
+  Wp[i] = *reinterpret_cast<const u32x4*>(W + (int64_t)row * ld + (int64_t)s * 32 + g * 8);
 }
 
-// Launch plan from N and K only: rows per wave (NR tiles of 16), waves per workgroup splitting K (NW),
-// k-steps in flight (KU) and K splits across workgroups (SK).
-struct Plan {
-  int nr, nw, ku, sk;
+// ---------------------------------------------------------------- plans
+struct Cfg {
+  int nw, kws;
 };
-Plan plan(int64_t N, int64_t K, int64_t splits) {
-  const int64_t tiles = N / 16, ksteps = K / 32;
-  Plan p;
-  if (tiles >= 1024 && N % 64 == 0) {
-    p = {4, 4, 4, 1};
-  } else if (tiles >= 512 && N % 32 == 0) {
-    p = {2, 4, 8, 1};
-  } else {
-    p = {1, 8, 8, 1};
+constexpr Cfg kCfgs[] = {{8, 10}, {8, 5}, {8, 4}};  // 16-wave workgroups measured 10-15% slower
+constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+
+struct Plan {
+  int cfg, T, kg;
+};
+
+// Deterministic plan from (N, K, epilogue): for each kernel shape, the fewest tiles per workgroup that keep
+// the grid within one workgroup per CU (a CU that had to run two would finish last), then the lowest cost
+// in units of one weight k-step of a workgroup (~0.05 us measured at 33 rows): the k-steps per workgroup,
+// + 4 per k-step of X slice (its load precedes the stream, ~0.2 us each), + 6 per extra partial plane
+// (read again by its consumer: ~0.3 us per plane at 33 rows). Bf16 and SwiGLU epilogues need the whole K
+// in one workgroup (kg == 1); ties go to the thinner X slice.
+Plan plan_for(int64_t N, int64_t K, int epi) {
+  const int64_t tiles = N / 16, nsteps = K / 32;
+  Plan best{-1, 0, 0};
+  int64_t best_cost = INT64_MAX;
+  for (int c = 0; c < kNumCfgs; ++c) {
+    const int64_t per = (int64_t)kCfgs[c].nw * kCfgs[c].kws;
+    const int64_t kg = cdiv(nsteps, per);
+    if (epi != kParts && kg != 1) continue;
+    if (kg > 64) continue;
+    const int64_t T = std::max<int64_t>(1, cdiv(tiles * kg, kCUs));
+    const int64_t work = T * std::min(per, nsteps);
+    const int64_t cost = work + 4 * kCfgs[c].kws + 6 * (kg - 1);
+    if (cost < best_cost || (cost == best_cost && kCfgs[c].kws < kCfgs[best.cfg].kws)) {
+      best_cost = cost;
+      best = {c, (int)T, (int)kg};
+    }
   }
-  int64_t sk = splits > 0 ? splits : 1;
-  if (splits <= 0) {
-    const int64_t waves = tiles / p.nr * p.nw;
-    if (waves < 512) sk = cdiv(512, waves);
-  }
-  const int64_t cap = std::max<int64_t>(1, ksteps / (p.nw * 2));  // at least ~2 k-steps per wave
-  p.sk = (int)std::min<int64_t>(sk, cap);
-  return p;
+  return best;
 }
 
-template <int MT, int NR, int NW, int KU>
-void launch(const GemmArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)(a.N / (16 * NR)), (unsigned)a.SK);
-  hipLaunchKernelGGL((skinny_gemm_kernel<MT, NR, NW, KU>), grid, dim3(NW * kWave), 0, st, a);
+template <int NW, int KWS, int D, int MT, int EPI>
+void launch(const WsArgs& a, int kg, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(a.N / 16, a.T), (unsigned)kg);
+  hipLaunchKernelGGL((wsgemm_kernel<NW, KWS, D, MT, EPI>), grid, dim3(NW * kWave), 0, st, a);
 }
-template <int MT>
-void launch_mt(const GemmArgs& a, const Plan& p, hipStream_t st) {
-  if (p.nr == 4) launch<MT, 4, 4, 4>(a, st);
-  else if (p.nr == 2) launch<MT, 2, 4, 8>(a, st);
-  else launch<MT, 1, 8, 8>(a, st);
+template <int NW, int KWS, int D, int EPI>
+void launch_mt(const WsArgs& a, int kg, hipStream_t st) {
+  switch ((a.M + 15) / 16) {
+    case 1: launch<NW, KWS, D, 1, EPI>(a, kg, st); break;
+    case 2: launch<NW, KWS, D, 2, EPI>(a, kg, st); break;
+    default: launch<NW, KWS, D, 3, EPI>(a, kg, st); break;
+  }
+}
+template <int EPI>
+void launch_cfg(const WsArgs& a, const Plan& p, hipStream_t st) {
+  switch (p.cfg) {
+    case 0: launch_mt<8, 10, 10, EPI>(a, p.kg, st); break;
+    case 1: launch_mt<8, 5, 10, EPI>(a, p.kg, st); break;
+    default: launch_mt<8, 4, 8, EPI>(a, p.kg, st); break;
+  }
+}
+
+bool shape_ok(int64_t N, int64_t K, int epi) {
+  return N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0 && N / 16 < INT32_MAX && K < INT32_MAX &&
+         (epi != kSilu || N % 16 == 0);
 }
 
 }  // namespace
@@ -175,40 +243,49 @@ void launch_mt(const GemmArgs& a, const Plan& p, hipStream_t st) {
 
 using namespace trida;
 
-extern "C" int64_t trida_skinny_gemm_scratch_bytes(int64_t M, int64_t N, int64_t K, int64_t splits) {
-  if (M <= 0 || N <= 0 || K <= 0) return 0;
-  const Plan p = plan(N, K, splits);
-  return p.sk > 1 ? align_up((int64_t)p.sk * M * N * 4, 256) : 0;
+extern "C" int trida_wsgemm_shuffle(const uint16_t* W, int64_t N, int64_t K, int64_t w_row_stride, int pair_halves,
+                                    uint16_t* Wp, void* stream) {
+  TRIDA_CHECK(W && Wp, TRIDA_ERR_NULL, "wsgemm_shuffle: W and Wp are required");
+  TRIDA_CHECK(N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0 && w_row_stride >= K && w_row_stride % 8 == 0,
+              TRIDA_ERR_ARG, "wsgemm_shuffle: need N %% 16 == 0, K %% 32 == 0 (N=%lld K=%lld)", (long long)N,
+              (long long)K);
+  TRIDA_CHECK(((((uintptr_t)W) | (uintptr_t)Wp) & 15) == 0, TRIDA_ERR_ALIGN, "wsgemm_shuffle: 16-byte alignment");
+  const int64_t total = N / 16 * (K / 32) * kWave;
+  hipLaunchKernelGGL(shuffle_kernel, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     W, w_row_stride, (int)N, (int)K, pair_halves ? 1 : 0, reinterpret_cast<u32x4*>(Wp));
+  return launch_status("wsgemm_shuffle");
 }
 
-extern "C" int trida_skinny_gemm(const uint16_t* X, int64_t x_row_stride, const uint16_t* W, int64_t w_row_stride,
-                                 uint16_t* Y, int64_t y_row_stride, int64_t M, int64_t N, int64_t K, void* scratch,
-                                 int64_t scratch_bytes, int64_t splits, void* stream) {
-  TRIDA_CHECK(X && W && Y, TRIDA_ERR_NULL, "skinny_gemm: X, W and Y are required");
-  TRIDA_CHECK(M >= 1 && M <= 64 && N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0, TRIDA_ERR_ARG,
-              "skinny_gemm: need 1 <= M <= 64, N % 16 == 0, K % 32 == 0 (M=%lld N=%lld K=%lld)", (long long)M,
+extern "C" int trida_wsgemm_plan(int64_t N, int64_t K, int epilogue, int32_t* kgroups) {
+  TRIDA_CHECK(kgroups, TRIDA_ERR_NULL, "wsgemm_plan: kgroups is required");
+  TRIDA_CHECK(epilogue >= kStore && epilogue <= kSilu, TRIDA_ERR_ARG, "wsgemm_plan: unknown epilogue %d", epilogue);
+  TRIDA_CHECK(shape_ok(N, K, epilogue), TRIDA_ERR_ARG, "wsgemm_plan: need N %% 16 == 0, K %% 32 == 0");
+  const Plan p = plan_for(N, K, epilogue);
+  TRIDA_CHECK(p.cfg >= 0, TRIDA_ERR_ARG, "wsgemm_plan: K too long for one workgroup (epilogue %d needs kg == 1)",
+              epilogue);
+  *kgroups = p.kg;
+  return TRIDA_OK;
+}
+
+extern "C" int trida_wsgemm(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M, int64_t N,
+                            int64_t K, int epilogue, void* out, int64_t out_row_stride, void* stream) {
+  TRIDA_CHECK(X && Wp && out, TRIDA_ERR_NULL, "wsgemm: X, Wp and out are required");
+  TRIDA_CHECK(epilogue >= kStore && epilogue <= kSilu, TRIDA_ERR_ARG, "wsgemm: unknown epilogue %d", epilogue);
+  TRIDA_CHECK(M >= 1 && M <= kMaxM && shape_ok(N, K, epilogue), TRIDA_ERR_ARG,
+              "wsgemm: need 1 <= M <= %d, N %% 16 == 0, K %% 32 == 0 (M=%lld N=%lld K=%lld)", kMaxM, (long long)M,
               (long long)N, (long long)K);
-  TRIDA_CHECK(x_row_stride >= K && w_row_stride >= K && y_row_stride >= N && x_row_stride % 8 == 0 &&
-                  w_row_stride % 8 == 0 && y_row_stride % 4 == 0,
-              TRIDA_ERR_ARG, "skinny_gemm: bad strides");
-  TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)W) & 15) == 0 && ((uintptr_t)Y & 7) == 0, TRIDA_ERR_ALIGN,
-              "skinny_gemm: X and W 16-byte aligned, Y 8-byte aligned");
-  const Plan p = plan(N, K, splits);
-  TRIDA_CHECK(p.sk >= 1 && p.sk <= 65535 && N / 16 < INT32_MAX, TRIDA_ERR_ARG, "skinny_gemm: bad split count");
-  TRIDA_CHECK(p.sk == 1 || (scratch && scratch_bytes >= trida_skinny_gemm_scratch_bytes(M, N, K, splits)),
-              TRIDA_ERR_WORKSPACE, "skinny_gemm: scratch too small for %d K splits", p.sk);
-  GemmArgs a{X, W, Y, static_cast<float*>(scratch), x_row_stride, w_row_stride, y_row_stride, (int)M, (int)N,
-             (int)K, p.sk};
+  TRIDA_CHECK(x_row_stride >= K && x_row_stride % 8 == 0, TRIDA_ERR_ARG, "wsgemm: bad X row stride");
+  TRIDA_CHECK(epilogue == kParts || (out_row_stride >= (epilogue == kSilu ? N / 2 : N) && out_row_stride % 4 == 0),
+              TRIDA_ERR_ARG, "wsgemm: bad output row stride");
+  TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Wp | (uintptr_t)out) & 15) == 0, TRIDA_ERR_ALIGN,
+              "wsgemm: X, Wp and out must be 16-byte aligned");
+  const Plan p = plan_for(N, K, epilogue);
+  TRIDA_CHECK(p.cfg >= 0, TRIDA_ERR_ARG, "wsgemm: K too long for one workgroup (epilogue %d needs kg == 1)",
+              epilogue);
+  WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  switch ((int)cdiv(M, 16)) {
-    case 1: launch_mt<1>(a, p, st); break;
-    case 2: launch_mt<2>(a, p, st); break;
-    case 3: launch_mt<3>(a, p, st); break;
-    default: launch_mt<4>(a, p, st); break;
-  }
-  int rc = launch_status("skinny_gemm");
-  if (rc || p.sk == 1) return rc;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)cdiv(M * N / 4, 256)), dim3(256), 0, st,
-                     static_cast<const float*>(scratch), Y, y_row_stride, (int)M, (int)N, p.sk);
-  return launch_status("skinny_gemm/reduce");
+  if (epilogue == kStore) launch_cfg<kStore>(a, p, st);
+  else if (epilogue == kParts) launch_cfg<kParts>(a, p, st);
+  else launch_cfg<kSilu>(a, p, st);
+  return launch_status("wsgemm");
 }

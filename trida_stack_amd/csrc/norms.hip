@@ -48,7 +48,11 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // ------------------------------------------------------------------ add + rmsnorm (one block per row)
 constexpr int kMaxPieces = 4;  // 8 elements each per thread: dim <= 256 * 8 * 4 = 8192
 
-__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, const uint16_t* r, const uint16_t* w,
+// The residual r is either bf16 rows (r, r_st) or, with `parts`, the sum of n_parts fp32 planes of
+// plane_st elements each (rows of dim floats): the split-K partial results of the weight-streaming GEMM,
+// summed in plane order and rounded to bf16 as the GEMM's own output would be.
+__global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, const uint16_t* r, const float* parts,
+                                                               int n_parts, int64_t plane_st, const uint16_t* w,
                                                                uint16_t* out, int dim, int64_t x_st, int64_t r_st,
                                                                int64_t o_st, float eps, int zero_centred) {
   __shared__ float red[kThreads / kWave];
@@ -65,6 +69,29 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, cons
       wr[u] = *reinterpret_cast<const u32x4*>(w + p * 8);
     }
   }
+  if (parts) {
+    float acc[kMaxPieces][8];
+#pragma unroll
+    for (int u = 0; u < kMaxPieces; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[u][j] = 0.f;
+    for (int s = 0; s < n_parts; ++s) {
+      const float* pl = parts + s * plane_st + row * dim;
+#pragma unroll
+      for (int u = 0; u < kMaxPieces; ++u) {
+        const int p = threadIdx.x + u * kThreads;
+        if (p < pieces) {
+          const f32x4 a = *reinterpret_cast<const f32x4*>(pl + p * 8);
+          const f32x4 b = *reinterpret_cast<const f32x4*>(pl + p * 8 + 4);
+          acc[u][0] += a.x; acc[u][1] += a.y; acc[u][2] += a.z; acc[u][3] += a.w;
+          acc[u][4] += b.x; acc[u][5] += b.y; acc[u][6] += b.z; acc[u][7] += b.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kMaxPieces; ++u) rr[u] = pack8(acc[u]);
+  }
+  const bool has_r = r || parts;  // its bf16 values are in rr
   float v[kMaxPieces][8];
   float ss = 0.f;
 #pragma unroll
@@ -72,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, cons
     const int p = threadIdx.x + u * kThreads;
     if (p < pieces) {
       unpack8(xr[u], v[u]);
-      if (r) {
+      if (has_r) {
         float rv[8];
         unpack8(rr[u], rv);
 #pragma unroll
@@ -250,8 +277,26 @@ extern "C" int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t*
                   ((((uintptr_t)x) | (uintptr_t)r | (uintptr_t)w | (uintptr_t)out) & 15) == 0,
               TRIDA_ERR_ALIGN, "add_rmsnorm: 16-byte aligned rows required");
   hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     x, r, w, out, (int)dim, x_st, r_st, o_st, eps, zero_centred);
+                     x, r, static_cast<const float*>(nullptr), 0, (int64_t)0, w, out, (int)dim, x_st, r_st, o_st, eps,
+                     zero_centred);
   return launch_status("add_rmsnorm");
+}
+
+extern "C" int trida_add_rmsnorm_parts(uint16_t* x, const float* parts, int64_t n_parts, int64_t plane_stride,
+                                       const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim, int64_t x_st,
+                                       int64_t o_st, float eps, int zero_centred, void* stream) {
+  TRIDA_CHECK(x && parts && w && out, TRIDA_ERR_NULL, "add_rmsnorm_parts: x, parts, w and out are required");
+  TRIDA_CHECK(rows > 0 && rows < 65536 && dim > 0 && dim % 8 == 0 && dim <= kThreads * 8 * kMaxPieces &&
+                  n_parts >= 1 && n_parts <= 64 && plane_stride >= rows * dim,
+              TRIDA_ERR_ARG, "add_rmsnorm_parts: bad sizes (dim a multiple of 8 <= %d, 1 <= n_parts <= 64)",
+              kThreads * 8 * kMaxPieces);
+  TRIDA_CHECK(x_st % 8 == 0 && o_st % 8 == 0 && plane_stride % 4 == 0 &&
+                  ((((uintptr_t)x) | (uintptr_t)parts | (uintptr_t)w | (uintptr_t)out) & 15) == 0,
+              TRIDA_ERR_ALIGN, "add_rmsnorm_parts: 16-byte aligned rows required");
+  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                     x, static_cast<const uint16_t*>(nullptr), parts, (int)n_parts, plane_stride, w, out, (int)dim, x_st,
+                     (int64_t)0, o_st, eps, zero_centred);
+  return launch_status("add_rmsnorm_parts");
 }
 
 extern "C" int trida_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inter, int64_t g_st,

@@ -6,6 +6,7 @@ or a CPU tensor is an error.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -819,28 +820,58 @@ def attn_canvas(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, p
 
 
 # --------------------------------------------------------------------------------------------------
-# skinny GEMM
-SKINNY_MAX_M = 64
+# weight-streaming GEMM (decode-step projections)
+WS_MAX_M = 48
+WS_STORE, WS_PARTS, WS_SILU = 0, 1, 2
 
 
-def linear(x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None, *, splits: int = 0) -> torch.Tensor:
-    """y = x @ w.T for bf16 x [M, K] (M <= 64, contiguous rows) and w [N, K] (torch Linear layout);
-    fp32 accumulation, bf16 out [M, N]."""
-    dev = _need_gpu(x, w, out)
-    _bf16(x, "x")
+def ws_shuffle(w: torch.Tensor, *, pair_halves: bool = False) -> torch.Tensor:
+    """The weight-streaming layout of a torch Linear weight w [N, K] bf16 (N % 16 == 0, K % 32 == 0): a new
+    bf16 tensor of N * K elements (flat). pair_halves: w = [gate; up] (N / 2 rows each), interleaved so
+    the SwiGLU epilogue finds each gate row beside its up row."""
+    dev = _need_gpu(w)
     _bf16(w, "w")
+    N, Kd = w.shape
+    if w.stride(1) != 1:
+        raise ValueError("ws_shuffle: w needs contiguous rows")
+    wp = torch.empty(N * Kd, dtype=torch.bfloat16, device=dev)
+    rc = _lib.load().trida_wsgemm_shuffle(w.data_ptr(), N, Kd, w.stride(0), int(pair_halves), wp.data_ptr(),
+                                          _stream(dev))
+    _lib.check(rc, "trida_wsgemm_shuffle")
+    return wp
+
+
+def ws_plan(N: int, Kd: int, epilogue: int) -> int:
+    """Partial planes the weight-streaming GEMM writes for (N, K) with `epilogue` (1 unless WS_PARTS)."""
+    kg = ctypes.c_int32(0)
+    rc = _lib.load().trida_wsgemm_plan(N, Kd, epilogue, ctypes.byref(kg))
+    _lib.check(rc, "trida_wsgemm_plan")
+    return kg.value
+
+
+def ws_gemm(x: torch.Tensor, wp: torch.Tensor, N: int, out: torch.Tensor, *, epilogue: int = WS_STORE) -> torch.Tensor:
+    """x [M, K] bf16 (M <= 48, contiguous rows) times the weight in ws_shuffle layout (N rows):
+    WS_STORE: out [M, N] bf16 = x @ w.T; WS_PARTS: out fp32 [kg, M, N] partial planes (kg = ws_plan);
+    WS_SILU: out [M, N / 2] bf16 = silu(x @ gate.T) * (x @ up.T) over a pair_halves weight."""
+    dev = _need_gpu(x, wp, out)
+    _bf16(x, "x")
     M, Kd = x.shape
-    N = w.shape[0]
-    if w.shape[1] != Kd or x.stride(1) != 1 or w.stride(1) != 1:
-        raise ValueError("linear: shapes / strides")
-    if out is None:
-        out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
-    lib = _lib.load()
-    nbytes = lib.trida_skinny_gemm_scratch_bytes(M, N, Kd, splits)
-    scr = workspaces.get(dev, "skinny_gemm", nbytes) if nbytes else None
-    rc = lib.trida_skinny_gemm(x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out.data_ptr(), out.stride(0),
-                               M, N, Kd, _ptr(scr), scr.numel() if scr is not None else 0, splits, _stream(dev))
-    _lib.check(rc, "trida_skinny_gemm")
+    if x.stride(1) != 1 or wp.numel() != N * Kd:
+        raise ValueError("ws_gemm: x needs contiguous rows and wp N * K elements")
+    if epilogue == WS_PARTS:
+        kg = ws_plan(N, Kd, epilogue)
+        if out.dtype != torch.float32 or not out.is_contiguous() or out.numel() < kg * M * N:
+            raise ValueError(f"ws_gemm: partial planes need a contiguous fp32 out of >= {kg} x {M} x {N}")
+        o_st = N
+    else:
+        width = N // 2 if epilogue == WS_SILU else N
+        _bf16(out, "out")
+        if out.dim() != 2 or out.shape[0] < M or out.shape[1] < width or out.stride(1) != 1:
+            raise ValueError(f"ws_gemm: out must be [>= {M}, >= {width}] bf16 with contiguous rows")
+        o_st = out.stride(0)
+    rc = _lib.load().trida_wsgemm(x.data_ptr(), x.stride(0), wp.data_ptr(), M, N, Kd, epilogue, out.data_ptr(), o_st,
+                                  _stream(dev))
+    _lib.check(rc, "trida_wsgemm")
     return out
 
 
@@ -856,6 +887,21 @@ def add_rmsnorm(x: torch.Tensor, r: Optional[torch.Tensor], w: torch.Tensor, out
                                        r.stride(0) if r is not None else 0, out.stride(0), eps, int(zero_centred),
                                        _stream(dev))
     _lib.check(rc, "trida_add_rmsnorm")
+    return out
+
+
+def add_rmsnorm_parts(x: torch.Tensor, parts: torch.Tensor, n_parts: int, w: torch.Tensor, out: torch.Tensor, *,
+                      eps: float = 1e-6, zero_centred: bool = True) -> torch.Tensor:
+    """add_rmsnorm whose residual is the sum of the first n_parts planes of parts (fp32 [>= n_parts, rows, dim],
+    contiguous: the WS_PARTS output of ws_gemm), summed in plane order and rounded to bf16."""
+    dev = _need_gpu(x, parts, w, out)
+    rows, dim = x.shape
+    if parts.dtype != torch.float32 or not parts.is_contiguous() or parts.numel() < n_parts * rows * dim:
+        raise ValueError("add_rmsnorm_parts: parts must be contiguous fp32 holding n_parts x rows x dim")
+    rc = _lib.load().trida_add_rmsnorm_parts(x.data_ptr(), parts.data_ptr(), n_parts, rows * dim, w.data_ptr(),
+                                             out.data_ptr(), rows, dim, x.stride(0), out.stride(0), eps,
+                                             int(zero_centred), _stream(dev))
+    _lib.check(rc, "trida_add_rmsnorm_parts")
     return out
 
 

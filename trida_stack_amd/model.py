@@ -190,7 +190,7 @@ class _Scratch:
     operands are allocated with Np >= B * T rows (zeros past B * T; see GEMM_MIN_ROWS); the attributes
     without `_p` are the B * T-row views the row-wise kernels use."""
 
-    def __init__(self, cfg: HybridConfig, B: int, T: int, n_gdn: int, dev):
+    def __init__(self, cfg: HybridConfig, B: int, T: int, n_gdn: int, dev, ws_parts: int = 0):
         bf = dict(dtype=torch.bfloat16, device=dev)
         f32 = dict(dtype=torch.float32, device=dev)
         N = B * T
@@ -223,6 +223,8 @@ class _Scratch:
         self.g_rec = torch.empty(n_gdn, B, T, cfg.lin_v_heads, **f32)
         self.b_rec = torch.empty(n_gdn, B, T, cfg.lin_v_heads, **f32)
         self.pre_rec = torch.empty(n_gdn, B, T, cfg.conv_dim, **bf)
+        # split-K partial planes of the weight-streaming GEMM ([kg, N, hidden] fp32), when it runs here
+        self.parts = torch.empty(max(1, ws_parts) * N * h, **f32) if ws_parts else None
 
 
 class TridaRuntime:
@@ -242,6 +244,10 @@ class TridaRuntime:
         for j, i in enumerate(self.gdn_layers):
             self._slot[i] = j
         self._scratch: Dict[tuple, _Scratch] = {}
+        self.ws: Dict[str, tuple] = {}
+        self.ws_parts = 0
+        if self.use_wsgemm:
+            self._shuffle_weights()
         self.skip_rows = False
         self.mask_id = cfg.mask_id
         self.progress_cb = None  # optional fn(tokens done this call) after each prefill chunk (model.py:241)
@@ -277,11 +283,40 @@ class TridaRuntime:
         key = (B, T)
         s = self._scratch.get(key)
         if s is None:
-            s = self._scratch[key] = _Scratch(self.cfg, B, T, len(self.gdn_layers), self.dev)
+            parts = self.ws_parts if B * T <= K.WS_MAX_M else 0
+            s = self._scratch[key] = _Scratch(self.cfg, B, T, len(self.gdn_layers), self.dev, ws_parts=parts)
         return s
 
+    # projection -> epilogue of the weight-streaming GEMM: bf16 outputs feed the GDN / attention kernels,
+    # the out-projections and the MLP down projection leave fp32 partial planes for add_rmsnorm_parts,
+    # gate/up runs with the SwiGLU epilogue
+    _WS_ROLE = {"w_in": K.WS_STORE, "w_qkv": K.WS_STORE, "w_out": K.WS_PARTS, "w_o": K.WS_PARTS,
+                "w_gu": K.WS_SILU, "w_down": K.WS_PARTS}
+
+    def _shuffle_weights(self) -> None:
+        """A second copy of every decoder projection in the weight-streaming layout (bf16, the same
+        bytes again: 7.4 GB at the 4B shape), for forwards of <= K.WS_MAX_M rows. A projection whose
+        shape the kernel does not take (N % 16, K % 32, or K too long for a whole-K epilogue) keeps the
+        hipBLASLt path."""
+        for key, wt in self.w.items():
+            role = self._WS_ROLE.get(key.split(".", 1)[-1])
+            if role is None:
+                continue
+            N, Kd = wt.shape
+            if N % 16 or Kd % 32 or (role == K.WS_SILU and (N // 2) % 8):
+                continue
+            try:
+                kg = K.ws_plan(N, Kd, role)
+            except ValueError:
+                continue
+            self.ws[key] = (K.ws_shuffle(wt.contiguous(), pair_halves=role == K.WS_SILU), N, role, kg)
+            if role == K.WS_PARTS:
+                self.ws_parts = max(self.ws_parts, kg)
+
     # ---------------------------------------------------------------- forward
-    use_skinny_gemm = False  # the skinny kernel is slower than hipBLASLt at these shapes so far
+    # decoder projections of forwards with <= K.WS_MAX_M rows run on the weight-streaming GEMM over
+    # pre-shuffled weights (class default; set before building the runtime)
+    use_wsgemm = True
     # GDN recurrence form: "chunked" (WY / UT chunks on MFMA, trida_gdr_chunk), "recurrent" (token by
     # token, trida_gdr_recurrent) or "auto" (chunked over more than one chunk of rows, i.e. prefill;
     # recurrent for canvas blocks and the rollback, where it measures faster). Both kernels follow the
@@ -303,15 +338,40 @@ class TridaRuntime:
         return gdn_mode == 1 or T <= 64
 
     def _mm(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """x @ w.T: the skinny weight-streaming kernel for canvas-sized x (<= 64 rows), hipBLASLt
-        (torch.matmul) for prefill chunks."""
-        if self.use_skinny_gemm and x.shape[0] <= K.SKINNY_MAX_M and w.shape[0] % 16 == 0 and w.shape[1] % 32 == 0:
-            with K.timed("skinny_gemm"):
-                return K.linear(x, w, out=out)
+        """x @ w.T on hipBLASLt (torch.matmul): prefill chunks, batched steps and the LM head."""
         with K.timed("gemm"):
             if out is None:
                 return torch.matmul(x, w.t())
             return torch.matmul(x, w.t(), out=out)
+
+    def _proj(self, s: "_Scratch", key: str, x: torch.Tensor, x_p: torch.Tensor, out_p: torch.Tensor):
+        """One decoder projection of the N = B * T rows in x (x_p: the padded rows hipBLASLt reads).
+        Returns the pending residual for add_norm when the projection feeds one (("parts", planes) from
+        the weight-streaming GEMM, ("bf16", rows) from hipBLASLt), else None (output in out_p's rows)."""
+        ws = self.ws.get(key) if s.N <= K.WS_MAX_M else None
+        if ws is None:
+            self._mm(x_p, self.w[key], out_p)
+            return ("bf16", out_p[: s.N])
+        wp, N, role, kg = ws
+        with K.timed("ws_gemm"):
+            if role == K.WS_PARTS:
+                K.ws_gemm(x, wp, N, s.parts, epilogue=role)
+                return ("parts", kg)
+            K.ws_gemm(x, wp, N, out_p, epilogue=role)
+        return None
+
+    def _ws_silu(self, s: "_Scratch", p: str) -> bool:
+        """True when the gate/up projection of layer prefix p runs with the SwiGLU epilogue here."""
+        return s.N <= K.WS_MAX_M and p + "w_gu" in self.ws
+
+    def _add_norm(self, s: "_Scratch", pending, w: torch.Tensor) -> None:
+        """h += the pending residual (none before the first layer), x = rmsnorm(h) * (1 + w)."""
+        eps = self.cfg.rms_eps
+        with K.timed("add_rmsnorm"):
+            if pending is not None and pending[0] == "parts":
+                K.add_rmsnorm_parts(s.h, s.parts, pending[1], w, s.x, eps=eps)
+            else:
+                K.add_rmsnorm(s.h, None if pending is None else pending[1], w, s.x, eps=eps)
 
     def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
                 rows: Optional[int] = None, seq: Optional[slice] = None, row0: int = 0) -> torch.Tensor:
@@ -339,14 +399,13 @@ class TridaRuntime:
         max_keys = min(cache.Lmax, cache.ctx_hint + T)
         fwd_timer = K.timed("forward").__enter__()
         torch.index_select(w["embed"], 0, ids.reshape(-1), out=s.h)
-        first = True
+        pending = None  # the residual branch not yet added to h
         for i in range(c.n_layers):
             p = f"l{i}."
-            K.add_rmsnorm(s.h, None if first else s.r, w[p + "in_norm"], s.x, eps=c.rms_eps)
-            first = False
+            self._add_norm(s, pending, w[p + "in_norm"])
             j = self._slot[i]
             if c.is_attention(i):
-                self._mm(s.x_p, w[p + "w_qkv"], s.qkv_p)
+                self._proj(s, p + "w_qkv", s.x, s.x_p, s.qkv_p)
                 with K.timed("attn_prep"):
                     K.attn_prep(s.qkv, w[p + "q_norm"], w[p + "k_norm"], pos, length, s.q_att, kv_k[j], kv_v[j],
                                 Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, rot_dim=c.rot_dim,
@@ -358,9 +417,9 @@ class TridaRuntime:
                 with K.timed("attn_canvas"):
                     K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
                                   out=s.o_att, max_keys=max_keys)
-                self._mm(s.o_att_p, w[p + "w_o"], s.r_p)
+                pending = self._proj(s, p + "w_o", s.o_att_p[:N], s.o_att_p, s.r_p)
             else:
-                self._mm(s.x_p, w[p + "w_in"], s.proj_p)
+                self._proj(s, p + "w_in", s.x, s.x_p, s.proj_p)
                 xv = s.proj[..., : c.conv_dim]
                 off = c.conv_dim + c.value_dim
                 b_in = s.proj[..., off: off + c.lin_v_heads]
@@ -397,12 +456,12 @@ class TridaRuntime:
                     window[j].copy_(s.win_tmp)
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
                 K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
-                self._mm(s.yn_p, w[p + "w_out"], s.r_p)
-            K.add_rmsnorm(s.h, s.r, w[p + "post_norm"], s.x, eps=c.rms_eps)
-            self._mm(s.x_p, w[p + "w_gu"], s.gu_p)
-            K.silu_mul(s.gu, s.act)
-            self._mm(s.act_p, w[p + "w_down"], s.r_p)
-        K.add_rmsnorm(s.h, s.r, w["final_norm"], s.x, eps=c.rms_eps)
+                pending = self._proj(s, p + "w_out", s.yn_p[:N], s.yn_p, s.r_p)
+            self._add_norm(s, pending, w[p + "post_norm"])
+            if self._proj(s, p + "w_gu", s.x, s.x_p, s.act_p if self._ws_silu(s, p) else s.gu_p) is not None:
+                K.silu_mul(s.gu, s.act)
+            pending = self._proj(s, p + "w_down", s.act, s.act_p, s.r_p)
+        self._add_norm(s, pending, w["final_norm"])
         x = s.x.view(B, T, -1)
         if rows is not None or row0:
             x = x[:, row0: row0 + (rows if rows is not None else T - row0)]
