@@ -9,8 +9,11 @@
 //     B operand, tokens as columns) into registers once; it then streams the weights of the workgroup's
 //     T tiles over that K slice with D k-steps of loads in flight (a register ring whose loads are pinned
 //     in issue order by sched_barrier, so the compiler neither sinks them nor drains the ring);
-//   - per tile the NW waves' partial 16 x 16*MT tiles meet in LDS (double-buffered slot, one s_barrier
-//     per tile, no wait on the weight loads still in flight) and 64*MT threads finish them;
+//   - each wave parks its partial 16 x 16*MT tile of every finished tile in an LDS slot and streams on;
+//     when the slots are full or the tiles done, the workgroup meets once and all its threads sum the
+//     parked tiles in wave order and run the epilogue. A plan's T tiles fit in the slots, so the weight
+//     stream never waits on another wave (longer plans flush every NSLOT tiles);
+//   - X rows past M are not loaded (lanes masked), so a 33-row canvas moves 2 KB + 64 B of X per k-step;
 //   - K beyond NW * KWS steps is split over kg workgroup groups that write fp32 partial planes
 //     [kg][M][N]; trida_add_rmsnorm_parts (norms.hip) sums them in plane order.
 // Epilogues: bf16 store, fp32 partials, or SwiGLU (silu(gate) * up) over weights whose tiles interleave 8
@@ -40,11 +43,18 @@ struct WsArgs {
   int M, N, K, T;
 };
 
+// LDS slots of partial tiles: as many as fit in 144 KiB, at most 8
+template <int NW, int MT>
+constexpr int nslot() {
+  return (147456 / (NW * MT * 1024)) < 8 ? (147456 / (NW * MT * 1024)) : 8;
+}
+
 template <int NW, int KWS, int D, int MT, int EPI>
 __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
   static_assert(KWS % D == 0 || D % KWS == 0, "the ring and the K slice must tile the unrolled loop");
-  static_assert(MT <= NW, "the epilogue uses 64 * MT threads");
-  __shared__ f32x4 red[2][NW][MT][kWave];
+  constexpr int NSLOT = nslot<NW, MT>();
+  static_assert(NSLOT >= 2, "LDS slots");
+  __shared__ f32x4 red[NSLOT][NW][MT][kWave];
   const int wave = threadIdx.x / kWave, l = threadIdx.x % kWave;
   const int tiles = a.N / 16, nsteps = a.K / 32;
   const int t0 = blockIdx.x * a.T, nt = min(tiles, t0 + a.T) - t0;
@@ -65,24 +75,83 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
     wv[j] = *wptr(j);
     __builtin_amdgcn_sched_barrier(0);
   }
-  // X slice (issued after the first weight loads, so their latency overlaps): tokens past M repeat row
-  // M - 1 (never stored), steps past K are zeroed
+  // X slice (issued after the first weight loads, so their latency overlaps): lanes of tokens past M
+  // load nothing (their columns are never stored); steps past K are zero
   u32x4 xs[KWS][MT];
 #pragma unroll
   for (int j = 0; j < KWS; ++j) {
     const int s = min(s_base + j, nsteps - 1);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const int m = min(mt * 16 + (l % 16), a.M - 1);
-      xs[j][mt] = *reinterpret_cast<const u32x4*>(a.X + (int64_t)m * a.x_st + s * 32 + (l / 16) * 8);
+      const int m = mt * 16 + (l % 16);
+      xs[j][mt] = u32x4{0u, 0u, 0u, 0u};
+      if (m < a.M && j < my_steps)
+        xs[j][mt] = *reinterpret_cast<const u32x4*>(a.X + (int64_t)m * a.x_st + s * 32 + (l / 16) * 8);
     }
   }
+  // Wait for the prologue's loads here: the first MFMA needs the last of them anyway (X was issued after
+  // the ring), and a known-empty queue lets the compiler count the ring's loads exactly in the loop (the
+  // masked X loads would otherwise make it drain the ring at every pass). vmcnt(0) only (gfx9 encoding:
+  // expcnt and lgkmcnt at their maximum).
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+
+  // tiles [first, last] are parked in their slots: meet, sum the NW partials of each in wave order, run the
+  // epilogue (64 * NW threads over the parked tiles' outputs)
+  auto flush = [&](int first, int last) {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // LDS only: the weight loads stay in flight
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    constexpr int per_tile = EPI == kSilu ? MT * 32 : MT * kWave;
+    const int items = (last - first + 1) * per_tile;
+    for (int it = threadIdx.x; it < items; it += NW * kWave) {
+      const int tl = first + it / per_tile, q = it % per_tile;
+      const int slot = tl % NSLOT, tile = t0 + tl;
+      if (EPI == kSilu) {
+        // lanes 0..31 of a C tile hold rows 0..7 (gate), lanes 32..63 rows 8..15 (the matching up)
+        const int mt = q / 32, ln = q % 32;
+        f32x4 g = red[slot][0][mt][ln], up = red[slot][0][mt][ln + 32];
 #pragma unroll
-  for (int j = 0; j < KWS; ++j)
-    if (j >= my_steps) {
+        for (int w = 1; w < NW; ++w) {
+          g += red[slot][w][mt][ln];
+          up += red[slot][w][mt][ln + 32];
+        }
+        const int m = mt * 16 + (ln % 16);
+        if (m < a.M) {
+          const int f = tile * 8 + (ln / 16) * 4;
+          const float y0 = silu(bf2f(f2bf(g.x))) * bf2f(f2bf(up.x));
+          const float y1 = silu(bf2f(f2bf(g.y))) * bf2f(f2bf(up.y));
+          const float y2 = silu(bf2f(f2bf(g.z))) * bf2f(f2bf(up.z));
+          const float y3 = silu(bf2f(f2bf(g.w))) * bf2f(f2bf(up.w));
+          u32x2 packed;
+          packed.x = f2bf2(y0, y1);
+          packed.y = f2bf2(y2, y3);
+          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + f) = packed;
+        }
+      } else {
+        const int mt = q / kWave, ln = q % kWave;
+        f32x4 sum = red[slot][0][mt][ln];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xs[j][mt] = u32x4{0u, 0u, 0u, 0u};
+        for (int w = 1; w < NW; ++w) sum += red[slot][w][mt][ln];
+        const int m = mt * 16 + (ln % 16);
+        const int n = tile * 16 + (ln / 16) * 4;
+        if (m < a.M) {
+          if (EPI == kStore) {
+            u32x2 packed;
+            packed.x = f2bf2(sum.x, sum.y);
+            packed.y = f2bf2(sum.z, sum.w);
+            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + n) = packed;
+          } else {
+            *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = sum;
+          }
+        }
+      }
     }
+    if (last + 1 < nt) {  // the slots are rewritten: every thread has finished reading them
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+  };
 
   f32x4 acc[MT];
 #pragma unroll
@@ -99,62 +168,14 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
       wv[r] = *wptr(u + D);
       __builtin_amdgcn_sched_barrier(0);
       const int tl = u / KWS;
-      if (j == KWS - 1 && tl < nt) {  // tile tl complete in every wave (the condition is uniform)
-        const int slot = tl & 1;
+      if (j == KWS - 1 && tl < nt) {  // this wave's part of tile tl is complete (uniform condition)
+        const int slot = tl % NSLOT;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           red[slot][wave][mt][l] = acc[mt];
           acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
-        // LDS writes done, then the barrier; no fence, so the weight loads in flight stay in flight.
-        // Slot reuse is safe: a slot is rewritten two tiles later, after every thread has passed the
-        // next barrier, i.e. finished reading it.
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        const int i = threadIdx.x;
-        const int tile = t0 + tl;
-        if (EPI == kSilu) {
-          // lanes 0..31 of a C tile hold rows 0..7 (gate), lanes 32..63 rows 8..15 (the matching up)
-          if (i < MT * 32) {
-            const int mt = i / 32, ln = i % 32;
-            f32x4 g = red[slot][0][mt][ln], up = red[slot][0][mt][ln + 32];
-#pragma unroll
-            for (int w = 1; w < NW; ++w) {
-              g += red[slot][w][mt][ln];
-              up += red[slot][w][mt][ln + 32];
-            }
-            const int m = mt * 16 + (ln % 16);
-            if (m < a.M) {
-              const int f = tile * 8 + (ln / 16) * 4;
-              const float y0 = silu(bf2f(f2bf(g.x))) * bf2f(f2bf(up.x));
-              const float y1 = silu(bf2f(f2bf(g.y))) * bf2f(f2bf(up.y));
-              const float y2 = silu(bf2f(f2bf(g.z))) * bf2f(f2bf(up.z));
-              const float y3 = silu(bf2f(f2bf(g.w))) * bf2f(f2bf(up.w));
-              u32x2 packed;
-              packed.x = f2bf2(y0, y1);
-              packed.y = f2bf2(y2, y3);
-              *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + f) = packed;
-            }
-          }
-        } else if (i < MT * kWave) {
-          const int mt = i / kWave, ln = i % kWave;
-          f32x4 s = red[slot][0][mt][ln];
-#pragma unroll
-          for (int w = 1; w < NW; ++w) s += red[slot][w][mt][ln];
-          const int m = mt * 16 + (ln % 16);
-          const int n = tile * 16 + (ln / 16) * 4;
-          if (m < a.M) {
-            if (EPI == kStore) {
-              u32x2 packed;
-              packed.x = f2bf2(s.x, s.y);
-              packed.y = f2bf2(s.z, s.w);
-              *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + n) = packed;
-            } else {
-              *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = s;
-            }
-          }
-        }
+        if (slot == NSLOT - 1 || tl == nt - 1) flush(tl - slot, tl);
       }
     }
   }
