@@ -382,18 +382,36 @@ int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t
  * trida_wsgemm_shuffle writes the weights once into the kernel's layout Wp (N * K bf16, 16-byte aligned):
  *   tile t (16 rows) x k-step s (32 columns) x lane l = 16 g + r -> 8 bf16 of W[row][32 s + 8 g ..];
  *   row = 16 t + r, or with pair_halves = 1 (W = [gate; up], N / 2 rows each) row = 8 t + r for r < 8
- *   and N / 2 + 8 t + r - 8 otherwise, which the SwiGLU epilogue needs.
+ *   and N / 2 + 8 t + r - 8 otherwise, which the SwiGLU epilogue needs. With col_scale (K bf16, may be
+ *   NULL) every column k is scaled first: bf16(W[row][k] * (1 + col_scale[k])) (zero_centred = 1) or
+ *   bf16(W[row][k] * col_scale[k]): an RMSNorm weight folded in for trida_wsgemm_norm.
  * trida_wsgemm epilogues: 0 = bf16 out [M, N] (row stride out_row_stride); 1 = fp32 partial planes
- *   out[kg][M][N] (dense; kg from trida_wsgemm_plan), summed by trida_add_rmsnorm_parts;
- *   2 = SwiGLU: bf16 out[M, N / 2] = silu(gate) * up over pair_halves weights (gate and up rounded to
- *   bf16 first, as a bf16 GEMM output would be).
- * The plan depends on (N, K, epilogue) only, so a row of the result is bitwise independent of M.
+ *   out[kg][M][N] (dense; kg from trida_wsgemm_plan), summed by trida_add_rmsnorm_parts or
+ *   trida_residual_parts; 2 = SwiGLU: bf16 out[M, N / 2] = silu(gate) * up over pair_halves weights
+ *   (gate and up rounded to bf16 first, as a bf16 GEMM output would be).
+ * Epilogues 0 and 2 need K <= 2560 (one workgroup holds the whole K). The plan depends on (N, K, epilogue)
+ * only, so a row of the result is bitwise independent of M.
  * trida_wsgemm_plan returns in *kgroups the number of partial planes epilogue 1 writes (1 otherwise). */
-int trida_wsgemm_shuffle(const uint16_t* W, int64_t N, int64_t K, int64_t w_row_stride, int pair_halves, uint16_t* Wp,
-                         void* stream);
+int trida_wsgemm_shuffle(const uint16_t* W, int64_t N, int64_t K, int64_t w_row_stride, int pair_halves,
+                         const uint16_t* col_scale, int zero_centred, uint16_t* Wp, void* stream);
 int trida_wsgemm_plan(int64_t N, int64_t K, int epilogue, int32_t* kgroups);
 int trida_wsgemm(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M, int64_t N, int64_t K,
                  int epilogue, void* out, int64_t out_row_stride, void* stream);
+/* trida_wsgemm with the decoder layer's RMSNorm fused in (epilogue 0 or 2): X is the raw residual stream h
+ * [M, K] and Wp was shuffled with the norm weight as col_scale; row m of the result (before the SwiGLU) is
+ * inv_m * (h W'^T)[m], inv_m = rsqrt(sum_c ss[m][c] / K + eps) over the trida_residual_ss_chunks(K)
+ * per-chunk sums of squares trida_residual_parts wrote for row m. It stands for the reference's
+ * RMSNorm + projection (inference/zoro-1/mlx/trida_mlx/model.py:337-364) with the norm weight applied to
+ * the weights instead of the activations (a different bf16 rounding point, same operator). */
+int trida_wsgemm_norm(const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp, int64_t M,
+                      int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride, void* stream);
+/* The residual add of a projection's partial planes, spread over rows x trida_residual_ss_chunks(dim)
+ * one-wave workgroups: h = bf16(h + bf16(sum of the n_parts fp32 planes [rows, dim], plane_stride elements
+ * apart, summed in plane order)) in place (n_parts = 0: h unchanged), and ss[row][c] = sum of h^2 over
+ * elements [256 c, 256 c + 256) of the row (fp32 [rows, trida_residual_ss_chunks(dim)]). */
+int64_t trida_residual_ss_chunks(int64_t dim);
+int trida_residual_parts(uint16_t* h, int64_t h_row_stride, const float* parts, int64_t n_parts, int64_t plane_stride,
+                         int64_t rows, int64_t dim, float* ss, void* stream);
 
 int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim,
                       int64_t x_st, int64_t r_st, int64_t o_st, float eps, int zero_centred, void* stream);

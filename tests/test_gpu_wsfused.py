@@ -1,0 +1,151 @@
+"""GPU parity of the fused decode-step path: the residual add over partial planes (residual_parts), the
+weight-streaming GEMM with the RMSNorm prologue (ws_gemm_norm), and a small model whose every projection
+runs on them, against torch references and the CPU oracle."""
+import random
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model as OM
+from trida_stack_amd import kernels as TK
+from trida_stack_amd.decode import SamplingParams, ar_generate, selfspec_generate
+from trida_stack_amd.model import HybridConfig, TridaRuntime, init_weights
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+# every projection shape divisible for the weight-streaming GEMM (N % 16, K % 32), hidden <= 2560
+CFG = HybridConfig(hidden=256, n_layers=4, intermediate=512, vocab=300, lin_k_heads=2, lin_v_heads=8, lin_k_dim=32,
+                   lin_v_dim=64, n_heads=4, n_kv_heads=2, head_dim=64, rope_theta=10000.0, mask_id=299)
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).abs().max() / b.abs().max().clamp_min(1e-30))
+
+
+def bf(x):
+    return x.to(torch.bfloat16).float()
+
+
+@pytest.mark.parametrize("dim,n_parts", [(2560, 0), (2560, 1), (2560, 8), (128, 3), (260, 2)])
+def test_residual_parts(gpu, dim, n_parts):
+    g = torch.Generator().manual_seed(dim + n_parts)
+    rows = 33
+    h = torch.randn(rows, dim, generator=g).to(torch.bfloat16)
+    parts = torch.randn(max(n_parts, 1), rows, dim, generator=g) * 0.3
+    acc = torch.zeros(rows, dim)
+    for s in range(n_parts):
+        acc += parts[s]
+    h_ref = bf(h.float() + bf(acc)) if n_parts else h.float()
+    C = TK.ss_chunks(dim)
+    assert C == -(-dim // 256)
+    ss_ref = torch.stack([(h_ref[:, c * 256:(c + 1) * 256] ** 2).sum(1) for c in range(C)], 1)
+    hd, ss = h.to(DEV), torch.full((rows, C), float("nan"), device=DEV)
+    TK.residual_parts(hd, parts.to(DEV) if n_parts else None, n_parts, ss)
+    assert torch.equal(hd.float().cpu(), h_ref)  # the bf16 residual stream, bit for bit
+    assert rel(ss, ss_ref) < 1e-5
+
+
+@pytest.mark.parametrize("M,N,K,epi", [(33, 8224, 2560, 0), (1, 10240, 2560, 0), (33, 19456, 2560, 2),
+                                       (17, 64, 256, 0), (5, 128, 96, 2)])
+def test_ws_gemm_norm(gpu, M, N, K, epi):
+    """rmsnorm(h) * (1 + w) @ W^T with the norm weight folded into the shuffled weights' columns and the
+    row scale rsqrt(mean(h^2) + eps) applied in the epilogue."""
+    g = torch.Generator().manual_seed(M + N + K)
+    h = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    nw = (torch.randn(K, generator=g) * 0.1).to(torch.bfloat16)
+    hd = h.to(DEV)
+    ss = torch.empty(M, TK.ss_chunks(K), device=DEV)
+    TK.residual_parts(hd, None, 0, ss)
+    inv = torch.rsqrt(h.float().pow(2).mean(1) + 1e-6)
+    y = (h.float() * inv[:, None] * (1.0 + nw.float())) @ w.float().t()  # the operator, in fp32
+    if epi == TK.WS_SILU:
+        y = bf(y)
+        y = F.silu(y[:, : N // 2]) * y[:, N // 2:]
+    wp = TK.ws_shuffle(w.to(DEV), pair_halves=epi == TK.WS_SILU, col_scale=nw.to(DEV))
+    # the folded copy: bf16(w * (1 + nw)) column by column
+    plain = TK.ws_shuffle(bf(w.float() * (1.0 + nw.float())).to(torch.bfloat16).to(DEV), pair_halves=epi == TK.WS_SILU)
+    assert torch.equal(wp, plain)
+    out = torch.empty(M, N // 2 if epi == TK.WS_SILU else N, dtype=torch.bfloat16, device=DEV)
+    TK.ws_gemm_norm(hd, ss, wp, N, out, epilogue=epi)
+    assert rel(out, y) < 2e-2
+    # the same rows for any M (row 0 alone)
+    out1 = torch.empty(1, out.shape[1], dtype=torch.bfloat16, device=DEV)
+    TK.ws_gemm_norm(hd[:1], ss[:1], wp, N, out1, epilogue=epi)
+    assert torch.equal(out1, out[:1])
+
+
+@pytest.fixture(scope="module")
+def fused_pair():
+    w = init_weights(CFG, seed=0, embed_scale=4.0)
+    rt = TridaRuntime(CFG, w, device=DEV)
+    assert rt.ws_fused, "the test config must run every projection on the weight-streaming GEMM"
+    return rt, OM.CpuHybrid(CFG, w)
+
+
+def prompt(n, seed=1):
+    rng = random.Random(seed)
+    return [rng.randrange(0, CFG.vocab - 10) for _ in range(n)]
+
+
+def test_fused_forward_matches_oracle(gpu, fused_pair):
+    rt, m = fused_pair
+    p = prompt(29)
+    c, co = rt.make_cache(max_len=160), m.make_cache()
+    assert rel(rt.prefill(c, p), m.prefill(co, p)) < 2e-2
+    n = 16  # a canvas of 31 rows: the fused path (<= 48 rows)
+    canvas = prompt(n, seed=5) + [CFG.mask_id] * (n - 1)
+    for mode in ("canvas", "draft", "verify"):
+        g = rt.forward(torch.tensor([canvas], device=DEV), c, mode, n_clean=n)[0]
+        o = m.forward(canvas, co, mode, n_clean=n)
+        co.pending = None
+        assert rel(g, o) < 2e-2, mode
+
+
+def test_fused_forward_matches_unfused(gpu, fused_pair):
+    """The same weights through add_rmsnorm + hipBLASLt projections (use_wsgemm off)."""
+    rt, _ = fused_pair
+    old = TridaRuntime.use_wsgemm
+    try:
+        TridaRuntime.use_wsgemm = False
+        ref = TridaRuntime(CFG, {k: v.cpu() for k, v in rt.w.items()}, device=DEV)
+    finally:
+        TridaRuntime.use_wsgemm = old
+    assert not ref.ws and not ref.ws_fused
+    p = prompt(40, seed=3)
+    ca, cb = rt.make_cache(max_len=128), ref.make_cache(max_len=128)
+    rt.prefill(ca, p)
+    ref.prefill(cb, p)
+    ids = torch.tensor([prompt(33, seed=9)], device=DEV)
+    assert rel(rt.forward(ids, ca, "verify"), ref.forward(ids, cb, "verify")) < 2e-2
+
+
+def collect(gen):
+    out = []
+    for ch in gen:
+        out.extend(ch)
+    return out
+
+
+def test_fused_greedy_selfspec_equals_ar(gpu, fused_pair):
+    """Lossless greedy self-spec on the fused path: the same tokens as greedy AR under the token-recurrent
+    GDN form (AR rows run the projections with M = 1, canvas rows with M = 7 or 16; the projections are
+    bitwise independent of M)."""
+    rt, _ = fused_pair
+    old = rt.gdr_form
+    rt.gdr_form = "recurrent"
+    try:
+        sp = SamplingParams(temperature=0.0)
+        for seed in range(2):
+            p = prompt(25, seed=seed + 10)
+            ar = collect(ar_generate(rt, rt.make_cache(max_len=256), p, max_new_tokens=48, eos_ids=set(), sp=sp))
+            ss = collect(selfspec_generate(rt, rt.make_cache(max_len=256), p, max_new_tokens=48, eos_ids=set(),
+                                           sp=sp, mask_id=CFG.mask_id, n=4))
+            bs = collect(selfspec_generate(rt, rt.make_cache(max_len=256), p, max_new_tokens=48, eos_ids=set(),
+                                           sp=sp, mask_id=CFG.mask_id, n=8, denoise_steps=2))
+            assert ss == ar, f"seed {seed}"
+            assert bs == ar, f"seed {seed} block"
+    finally:
+        rt.gdr_form = old

@@ -47,9 +47,12 @@ SIGNATURES = {
     "trida_truncated_probs_rows": (C.c_int, [P, I64, I64, I64, I64, I64, F32, I64, P, P, P, P, P, I64, P, I64, I64,
                                              I64, P]),
     "trida_gather_rows": (C.c_int, [P, C.c_int, I64, I64, I64, I64, I64, P, I64, P, I64, I64, P]),
-    "trida_wsgemm_shuffle": (C.c_int, [P, I64, I64, I64, C.c_int, P, P]),
+    "trida_wsgemm_shuffle": (C.c_int, [P, I64, I64, I64, C.c_int, P, C.c_int, P, P]),
     "trida_wsgemm_plan": (C.c_int, [I64, I64, C.c_int, P]),
     "trida_wsgemm": (C.c_int, [P, I64, P, I64, I64, I64, C.c_int, P, I64, P]),
+    "trida_wsgemm_norm": (C.c_int, [P, I64, P, F32, P, I64, I64, I64, C.c_int, P, I64, P]),
+    "trida_residual_ss_chunks": (I64, [I64]),
+    "trida_residual_parts": (C.c_int, [P, I64, P, I64, I64, I64, I64, P, P]),
     "trida_add_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, I64, F32, C.c_int, P]),
     "trida_add_rmsnorm_parts": (C.c_int, [P, P, I64, I64, P, P, I64, I64, I64, I64, F32, C.c_int, P]),
     "trida_silu_mul": (C.c_int, [P, P, I64, I64, I64, I64, P]),

@@ -41,7 +41,16 @@ struct WsArgs {
   void* out;
   int64_t x_st, o_st;
   int M, N, K, T;
+  // RMSNorm (NORM kernels): X is the raw residual stream and the weights were shuffled with the norm weight
+  // folded into their columns, so row m of the result is inv_m * (X W'^T)[m], inv_m = rsqrt(sum_c ss[m][c] /
+  // K + eps) over the ss_chunks(K) per-chunk sums of squares, applied in the epilogue
+  const float* ss;
+  float eps;
 };
+
+// chunks of the per-row sums of squares that trida_residual_parts writes: 256 elements each
+__host__ __device__ constexpr int ss_chunks(int dim) { return (dim + 255) / 256; }
+constexpr int kMaxSsChunks = 10;  // K <= 2560: every whole-K plan (<= 80 k-steps)
 
 // LDS slots of partial tiles: as many as fit in 144 KiB, at most 8
 template <int NW, int MT>
@@ -49,7 +58,7 @@ constexpr int nslot() {
   return (147456 / (NW * MT * 1024)) < 8 ? (147456 / (NW * MT * 1024)) : 8;
 }
 
-template <int NW, int KWS, int D, int MT, int EPI>
+template <int NW, int KWS, int D, int MT, int EPI, bool NORM>
 __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
   static_assert(KWS % D == 0 || D % KWS == 0, "the ring and the K slice must tile the unrolled loop");
   constexpr int NSLOT = nslot<NW, MT>();
@@ -94,6 +103,21 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
   // masked X loads would otherwise make it drain the ring at every pass). vmcnt(0) only (gfx9 encoding:
   // expcnt and lgkmcnt at their maximum).
   __builtin_amdgcn_s_waitcnt(0x0F70);
+  // RMSNorm scale of each token, for the epilogue: wave 0 sums the token's chunk sums of squares in chunk
+  // order (whole-K plans have K <= 2560, i.e. <= 10 chunks: unrolled, unconditional loads); the first flush's
+  // barrier publishes them
+  __shared__ float inv_s[MT * 16];
+  if (NORM && threadIdx.x < MT * 16) {
+    const int C = ss_chunks(a.K);
+    const int m = min((int)threadIdx.x, a.M - 1);
+    float v[kMaxSsChunks];
+#pragma unroll
+    for (int c = 0; c < kMaxSsChunks; ++c) v[c] = a.ss[(int64_t)m * C + min(c, C - 1)];
+    float sum = 0.f;
+#pragma unroll
+    for (int c = 0; c < kMaxSsChunks; ++c) sum += c < C ? v[c] : 0.f;
+    inv_s[threadIdx.x] = rsqrtf(sum / (float)a.K + a.eps);
+  }
 
   // tiles [first, last] are parked in their slots: meet, sum the NW partials of each in wave order, run the
   // epilogue (64 * NW threads over the parked tiles' outputs)
@@ -116,6 +140,11 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
           up += red[slot][w][mt][ln + 32];
         }
         const int m = mt * 16 + (ln % 16);
+        if (NORM) {
+          const float inv = inv_s[m];
+          g *= inv;
+          up *= inv;
+        }
         if (m < a.M) {
           const int f = tile * 8 + (ln / 16) * 4;
           const float y0 = silu(bf2f(f2bf(g.x))) * bf2f(f2bf(up.x));
@@ -134,6 +163,7 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
         for (int w = 1; w < NW; ++w) sum += red[slot][w][mt][ln];
         const int m = mt * 16 + (ln % 16);
         const int n = tile * 16 + (ln / 16) * 4;
+        if (NORM) sum *= inv_s[m];
         if (m < a.M) {
           if (EPI == kStore) {
             u32x2 packed;
@@ -183,7 +213,7 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
 
 // pre-shuffle: one thread per 16-byte piece of Wp, in Wp order
 __global__ __launch_bounds__(256) void shuffle_kernel(const uint16_t* W, int64_t ld, int N, int K, int pair,
-                                                      u32x4* Wp) {
+                                                      const uint16_t* col_scale, int zero_centred, u32x4* Wp) {
   const int64_t nsteps = K / 32, total = (int64_t)(N / 16) * nsteps * kWave;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= total) return;
@@ -192,7 +222,21 @@ __global__ __launch_bounds__(256) void shuffle_kernel(const uint16_t* W, int64_t
   const int s = (int)(rest % nsteps), t = (int)(rest / nsteps);
   const int r = lane % 16, g = lane / 16;
   const int row = pair ? (r < 8 ? 8 * t + r : N / 2 + 8 * t + (r - 8)) : 16 * t + r;
-  Wp[i] = *reinterpret_cast<const u32x4*>(W + (int64_t)row * ld + (int64_t)s * 32 + g * 8);
+  const int k0 = s * 32 + g * 8;
+  u32x4 v = *reinterpret_cast<const u32x4*>(W + (int64_t)row * ld + k0);
+  if (col_scale) {  // W'[row][k] = bf16(W[row][k] * (1 + c[k])) (zero_centred) or bf16(W[row][k] * c[k])
+    const u32x4 cv = *reinterpret_cast<const u32x4*>(col_scale + k0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float c0 = bf2f((uint16_t)(cv[q] & 0xffff)), c1 = bf2f((uint16_t)(cv[q] >> 16));
+      if (zero_centred) {
+        c0 = 1.f + c0;
+        c1 = 1.f + c1;
+      }
+      v[q] = f2bf2(bf2f((uint16_t)(v[q] & 0xffff)) * c0, bf2f((uint16_t)(v[q] >> 16)) * c1);
+    }
+  }
+  Wp[i] = v;
 }
 
 // ---------------------------------------------------------------- plans
@@ -232,26 +276,59 @@ Plan plan_for(int64_t N, int64_t K, int epi) {
   return best;
 }
 
-template <int NW, int KWS, int D, int MT, int EPI>
+template <int NW, int KWS, int D, int MT, int EPI, bool NORM>
 void launch(const WsArgs& a, int kg, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(a.N / 16, a.T), (unsigned)kg);
-  hipLaunchKernelGGL((wsgemm_kernel<NW, KWS, D, MT, EPI>), grid, dim3(NW * kWave), 0, st, a);
+  hipLaunchKernelGGL((wsgemm_kernel<NW, KWS, D, MT, EPI, NORM>), grid, dim3(NW * kWave), 0, st, a);
 }
-template <int NW, int KWS, int D, int EPI>
+template <int NW, int KWS, int D, int EPI, bool NORM>
 void launch_mt(const WsArgs& a, int kg, hipStream_t st) {
   switch ((a.M + 15) / 16) {
-    case 1: launch<NW, KWS, D, 1, EPI>(a, kg, st); break;
-    case 2: launch<NW, KWS, D, 2, EPI>(a, kg, st); break;
-    default: launch<NW, KWS, D, 3, EPI>(a, kg, st); break;
+    case 1: launch<NW, KWS, D, 1, EPI, NORM>(a, kg, st); break;
+    case 2: launch<NW, KWS, D, 2, EPI, NORM>(a, kg, st); break;
+    default: launch<NW, KWS, D, 3, EPI, NORM>(a, kg, st); break;
   }
 }
-template <int EPI>
+template <int EPI, bool NORM>
 void launch_cfg(const WsArgs& a, const Plan& p, hipStream_t st) {
   switch (p.cfg) {
-    case 0: launch_mt<8, 10, 10, EPI>(a, p.kg, st); break;
-    case 1: launch_mt<8, 5, 10, EPI>(a, p.kg, st); break;
-    default: launch_mt<8, 4, 8, EPI>(a, p.kg, st); break;
+    case 0: launch_mt<8, 10, 10, EPI, NORM>(a, p.kg, st); break;
+    case 1: launch_mt<8, 5, 10, EPI, NORM>(a, p.kg, st); break;
+    default: launch_mt<8, 4, 8, EPI, NORM>(a, p.kg, st); break;
   }
+}
+
+// residual add of split-K partial planes (grid rows x ss_chunks(dim), one wave per 256-element chunk):
+// h = bf16(h + bf16(sum_s parts[s][row])) (planes summed in order; n_parts = 0 leaves h as it is), and
+// ss[row][chunk] = the chunk's sum of h^2, which the RMSNorm prologue of the next GEMM reads
+__global__ __launch_bounds__(kWave) void residual_kernel(uint16_t* h, int64_t h_st, const float* parts, int n_parts,
+                                                         int64_t plane_st, int dim, float* ss) {
+  const int64_t row = blockIdx.x;
+  const int c = blockIdx.y, l = threadIdx.x;
+  const int e = c * 256 + l * 4;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (e < dim) {
+    uint16_t* hp = h + row * h_st + e;
+    const u32x2 hv = *reinterpret_cast<const u32x2*>(hp);
+    v[0] = bf2f((uint16_t)(hv.x & 0xffff));
+    v[1] = bf2f((uint16_t)(hv.x >> 16));
+    v[2] = bf2f((uint16_t)(hv.y & 0xffff));
+    v[3] = bf2f((uint16_t)(hv.y >> 16));
+    if (n_parts > 0) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < n_parts; ++s) acc += *reinterpret_cast<const f32x4*>(parts + s * plane_st + row * dim + e);
+      v[0] = bf2f(f2bf(v[0] + bf2f(f2bf(acc.x))));  // the residual stream is bf16
+      v[1] = bf2f(f2bf(v[1] + bf2f(f2bf(acc.y))));
+      v[2] = bf2f(f2bf(v[2] + bf2f(f2bf(acc.z))));
+      v[3] = bf2f(f2bf(v[3] + bf2f(f2bf(acc.w))));
+      *reinterpret_cast<u32x2*>(hp) = u32x2{f2bf2(v[0], v[1]), f2bf2(v[2], v[3])};
+    }
+  }
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) q = fmaf(v[i], v[i], q);
+  q = wave_sum(q);
+  if (l == 0) ss[row * ss_chunks(dim) + c] = q;
 }
 
 bool shape_ok(int64_t N, int64_t K, int epi) {
@@ -265,15 +342,17 @@ bool shape_ok(int64_t N, int64_t K, int epi) {
 using namespace trida;
 
 extern "C" int trida_wsgemm_shuffle(const uint16_t* W, int64_t N, int64_t K, int64_t w_row_stride, int pair_halves,
-                                    uint16_t* Wp, void* stream) {
+                                    const uint16_t* col_scale, int zero_centred, uint16_t* Wp, void* stream) {
   TRIDA_CHECK(W && Wp, TRIDA_ERR_NULL, "wsgemm_shuffle: W and Wp are required");
   TRIDA_CHECK(N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0 && w_row_stride >= K && w_row_stride % 8 == 0,
               TRIDA_ERR_ARG, "wsgemm_shuffle: need N %% 16 == 0, K %% 32 == 0 (N=%lld K=%lld)", (long long)N,
               (long long)K);
-  TRIDA_CHECK(((((uintptr_t)W) | (uintptr_t)Wp) & 15) == 0, TRIDA_ERR_ALIGN, "wsgemm_shuffle: 16-byte alignment");
+  TRIDA_CHECK(((((uintptr_t)W) | (uintptr_t)Wp | (uintptr_t)col_scale) & 15) == 0, TRIDA_ERR_ALIGN,
+              "wsgemm_shuffle: 16-byte alignment");
   const int64_t total = N / 16 * (K / 32) * kWave;
   hipLaunchKernelGGL(shuffle_kernel, dim3((unsigned)cdiv(total, 256)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     W, w_row_stride, (int)N, (int)K, pair_halves ? 1 : 0, reinterpret_cast<u32x4*>(Wp));
+                     W, w_row_stride, (int)N, (int)K, pair_halves ? 1 : 0, col_scale, zero_centred ? 1 : 0,
+                     reinterpret_cast<u32x4*>(Wp));
   return launch_status("wsgemm_shuffle");
 }
 
@@ -303,10 +382,50 @@ extern "C" int trida_wsgemm(const uint16_t* X, int64_t x_row_stride, const uint1
   const Plan p = plan_for(N, K, epilogue);
   TRIDA_CHECK(p.cfg >= 0, TRIDA_ERR_ARG, "wsgemm: K too long for one workgroup (epilogue %d needs kg == 1)",
               epilogue);
-  WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T};
+  WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T,
+           nullptr, 0.f};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (epilogue == kStore) launch_cfg<kStore>(a, p, st);
-  else if (epilogue == kParts) launch_cfg<kParts>(a, p, st);
-  else launch_cfg<kSilu>(a, p, st);
+  if (epilogue == kStore) launch_cfg<kStore, false>(a, p, st);
+  else if (epilogue == kParts) launch_cfg<kParts, false>(a, p, st);
+  else launch_cfg<kSilu, false>(a, p, st);
   return launch_status("wsgemm");
+}
+
+extern "C" int trida_wsgemm_norm(const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp,
+                                 int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride,
+                                 void* stream) {
+  TRIDA_CHECK(X && ss && Wp && out, TRIDA_ERR_NULL, "wsgemm_norm: X, ss, Wp and out are required");
+  TRIDA_CHECK(epilogue == kStore || epilogue == kSilu, TRIDA_ERR_ARG,
+              "wsgemm_norm: the RMSNorm prologue takes the bf16 (0) or SwiGLU (2) epilogue");
+  TRIDA_CHECK(M >= 1 && M <= kMaxM && shape_ok(N, K, epilogue), TRIDA_ERR_ARG,
+              "wsgemm_norm: need 1 <= M <= %d, N %% 16 == 0, K %% 32 == 0 (M=%lld N=%lld K=%lld)", kMaxM, (long long)M,
+              (long long)N, (long long)K);
+  TRIDA_CHECK(x_row_stride >= K && x_row_stride % 8 == 0, TRIDA_ERR_ARG, "wsgemm_norm: bad X row stride");
+  TRIDA_CHECK(out_row_stride >= (epilogue == kSilu ? N / 2 : N) && out_row_stride % 4 == 0, TRIDA_ERR_ARG,
+              "wsgemm_norm: bad output row stride");
+  TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Wp | (uintptr_t)out) & 15) == 0 && ((uintptr_t)ss & 3) == 0,
+              TRIDA_ERR_ALIGN, "wsgemm_norm: X, Wp and out must be 16-byte aligned");
+  const Plan p = plan_for(N, K, epilogue);
+  TRIDA_CHECK(p.cfg >= 0 && ss_chunks((int)K) <= kMaxSsChunks, TRIDA_ERR_ARG, "wsgemm_norm: K too long for one workgroup");
+  WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T, ss,
+           eps};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (epilogue == kStore) launch_cfg<kStore, true>(a, p, st);
+  else launch_cfg<kSilu, true>(a, p, st);
+  return launch_status("wsgemm_norm");
+}
+
+extern "C" int64_t trida_residual_ss_chunks(int64_t dim) { return dim > 0 ? ss_chunks((int)dim) : 0; }
+
+extern "C" int trida_residual_parts(uint16_t* h, int64_t h_row_stride, const float* parts, int64_t n_parts,
+                                    int64_t plane_stride, int64_t rows, int64_t dim, float* ss, void* stream) {
+  TRIDA_CHECK(h && ss && (parts || n_parts == 0), TRIDA_ERR_NULL, "residual_parts: h and ss (and parts) are required");
+  TRIDA_CHECK(rows > 0 && rows < INT32_MAX && dim > 0 && dim % 4 == 0 && dim < INT32_MAX && n_parts >= 0 &&
+                  n_parts <= 64 && (n_parts == 0 || plane_stride >= rows * dim) && h_row_stride >= dim,
+              TRIDA_ERR_ARG, "residual_parts: bad sizes (dim %% 4 == 0, 0 <= n_parts <= 64)");
+  TRIDA_CHECK(((uintptr_t)h & 7) == 0 && h_row_stride % 4 == 0 && ((uintptr_t)parts & 15) == 0 && plane_stride % 4 == 0,
+              TRIDA_ERR_ALIGN, "residual_parts: h rows 8-byte and parts 16-byte aligned");
+  hipLaunchKernelGGL(residual_kernel, dim3((unsigned)rows, (unsigned)ss_chunks((int)dim)), dim3(kWave), 0,
+                     static_cast<hipStream_t>(stream), h, h_row_stride, parts, (int)n_parts, plane_stride, (int)dim, ss);
+  return launch_status("residual_parts");
 }

@@ -825,18 +825,24 @@ WS_MAX_M = 48
 WS_STORE, WS_PARTS, WS_SILU = 0, 1, 2
 
 
-def ws_shuffle(w: torch.Tensor, *, pair_halves: bool = False) -> torch.Tensor:
+def ws_shuffle(w: torch.Tensor, *, pair_halves: bool = False, col_scale: Optional[torch.Tensor] = None,
+               zero_centred: bool = True) -> torch.Tensor:
     """The weight-streaming layout of a torch Linear weight w [N, K] bf16 (N % 16 == 0, K % 32 == 0): a new
     bf16 tensor of N * K elements (flat). pair_halves: w = [gate; up] (N / 2 rows each), interleaved so
-    the SwiGLU epilogue finds each gate row beside its up row."""
-    dev = _need_gpu(w)
+    the SwiGLU epilogue finds each gate row beside its up row. col_scale [K] bf16: an RMSNorm weight folded
+    into the columns (bf16(w * (1 + c)) when zero_centred, else bf16(w * c)) for ws_gemm_norm."""
+    dev = _need_gpu(w, col_scale)
     _bf16(w, "w")
     N, Kd = w.shape
     if w.stride(1) != 1:
         raise ValueError("ws_shuffle: w needs contiguous rows")
+    if col_scale is not None:
+        _bf16(col_scale, "col_scale")
+        if col_scale.numel() != Kd or not col_scale.is_contiguous():
+            raise ValueError("ws_shuffle: col_scale must be K contiguous elements")
     wp = torch.empty(N * Kd, dtype=torch.bfloat16, device=dev)
-    rc = _lib.load().trida_wsgemm_shuffle(w.data_ptr(), N, Kd, w.stride(0), int(pair_halves), wp.data_ptr(),
-                                          _stream(dev))
+    rc = _lib.load().trida_wsgemm_shuffle(w.data_ptr(), N, Kd, w.stride(0), int(pair_halves), _ptr(col_scale),
+                                          int(zero_centred), wp.data_ptr(), _stream(dev))
     _lib.check(rc, "trida_wsgemm_shuffle")
     return wp
 
@@ -872,6 +878,50 @@ def ws_gemm(x: torch.Tensor, wp: torch.Tensor, N: int, out: torch.Tensor, *, epi
     rc = _lib.load().trida_wsgemm(x.data_ptr(), x.stride(0), wp.data_ptr(), M, N, Kd, epilogue, out.data_ptr(), o_st,
                                   _stream(dev))
     _lib.check(rc, "trida_wsgemm")
+    return out
+
+
+def ss_chunks(dim: int) -> int:
+    """Columns of the per-row sums of squares residual_parts writes (256-element chunks)."""
+    return int(_lib.load().trida_residual_ss_chunks(dim))
+
+
+def residual_parts(h: torch.Tensor, parts: Optional[torch.Tensor], n_parts: int, ss: torch.Tensor) -> torch.Tensor:
+    """h += bf16(sum of the first n_parts planes of parts) in place (bf16 residual stream [rows, dim], planes
+    fp32 [>= n_parts, rows, dim] contiguous; n_parts = 0: h unchanged) and ss [rows, ss_chunks(dim)] fp32 = the
+    per-chunk sums of h^2 that ws_gemm_norm reads."""
+    dev = _need_gpu(h, parts, ss)
+    rows, dim = h.shape
+    if ss.dtype != torch.float32 or not ss.is_contiguous() or ss.numel() < rows * ss_chunks(dim):
+        raise ValueError("residual_parts: ss must be contiguous fp32 [rows, ss_chunks(dim)]")
+    if n_parts and (parts is None or parts.dtype != torch.float32 or not parts.is_contiguous()
+                    or parts.numel() < n_parts * rows * dim):
+        raise ValueError("residual_parts: parts must be contiguous fp32 holding n_parts x rows x dim")
+    rc = _lib.load().trida_residual_parts(h.data_ptr(), h.stride(0), _ptr(parts), n_parts, rows * dim, rows, dim,
+                                          ss.data_ptr(), _stream(dev))
+    _lib.check(rc, "trida_residual_parts")
+    return h
+
+
+def ws_gemm_norm(h: torch.Tensor, ss: torch.Tensor, wp: torch.Tensor, N: int, out: torch.Tensor, *,
+                 eps: float = 1e-6, epilogue: int = WS_STORE) -> torch.Tensor:
+    """ws_gemm of rmsnorm(h) against a weight shuffled with the norm weight as col_scale: h the raw bf16
+    residual stream [M, K] (M <= 48), ss its per-chunk sums of squares from residual_parts; row m is scaled
+    by rsqrt(mean(h_m^2) + eps) in the epilogue. Epilogue WS_STORE or WS_SILU."""
+    dev = _need_gpu(h, ss, wp, out)
+    _bf16(h, "h")
+    M, Kd = h.shape
+    if h.stride(1) != 1 or wp.numel() != N * Kd:
+        raise ValueError("ws_gemm_norm: h needs contiguous rows and wp N * K elements")
+    if ss.dtype != torch.float32 or not ss.is_contiguous() or ss.numel() < M * ss_chunks(Kd):
+        raise ValueError("ws_gemm_norm: ss must be contiguous fp32 [M, ss_chunks(K)]")
+    width = N // 2 if epilogue == WS_SILU else N
+    _bf16(out, "out")
+    if out.dim() != 2 or out.shape[0] < M or out.shape[1] < width or out.stride(1) != 1:
+        raise ValueError(f"ws_gemm_norm: out must be [>= {M}, >= {width}] bf16 with contiguous rows")
+    rc = _lib.load().trida_wsgemm_norm(h.data_ptr(), h.stride(0), ss.data_ptr(), eps, wp.data_ptr(), M, N, Kd,
+                                       epilogue, out.data_ptr(), out.stride(0), _stream(dev))
+    _lib.check(rc, "trida_wsgemm_norm")
     return out
 
 

@@ -225,6 +225,7 @@ class _Scratch:
         self.pre_rec = torch.empty(n_gdn, B, T, cfg.conv_dim, **bf)
         # split-K partial planes of the weight-streaming GEMM ([kg, N, hidden] fp32), when it runs here
         self.parts = torch.empty(max(1, ws_parts) * N * h, **f32) if ws_parts else None
+        self.ss = torch.empty(N, (h + 255) // 256, **f32) if ws_parts else None  # per-chunk sums of h^2
 
 
 class TridaRuntime:
@@ -246,6 +247,7 @@ class TridaRuntime:
         self._scratch: Dict[tuple, _Scratch] = {}
         self.ws: Dict[str, tuple] = {}
         self.ws_parts = 0
+        self.ws_fused = False
         if self.use_wsgemm:
             self._shuffle_weights()
         self.skip_rows = False
@@ -297,7 +299,11 @@ class TridaRuntime:
         """A second copy of every decoder projection in the weight-streaming layout (bf16, the same
         bytes again: 7.4 GB at the 4B shape), for forwards of <= K.WS_MAX_M rows. A projection whose
         shape the kernel does not take (N % 16, K % 32, or K too long for a whole-K epilogue) keeps the
-        hipBLASLt path."""
+        hipBLASLt path. When every projection qualifies (and hidden <= 2560), the forward runs fused: the
+        RMSNorm in front of a projection moves into its GEMM, with the norm weight folded into the copy's
+        columns (bf16(w * (1 + norm)), the Qwen3.5 zero-centred norm)."""
+        c = self.cfg
+        plans = {}
         for key, wt in self.w.items():
             role = self._WS_ROLE.get(key.split(".", 1)[-1])
             if role is None:
@@ -306,10 +312,22 @@ class TridaRuntime:
             if N % 16 or Kd % 32 or (role == K.WS_SILU and (N // 2) % 8):
                 continue
             try:
-                kg = K.ws_plan(N, Kd, role)
+                plans[key] = (role, K.ws_plan(N, Kd, role))
             except ValueError:
                 continue
-            self.ws[key] = (K.ws_shuffle(wt.contiguous(), pair_halves=role == K.WS_SILU), N, role, kg)
+        proj = [f"l{i}.{k}" for i in range(c.n_layers)
+                for k in (("w_qkv", "w_o") if c.is_attention(i) else ("w_in", "w_out")) + ("w_gu", "w_down")]
+        self.ws_fused = all(k in plans for k in proj) and K.ss_chunks(c.hidden) <= 10
+        for key, (role, kg) in plans.items():
+            layer, name = key.split(".", 1)
+            norm = None
+            if self.ws_fused and name in ("w_in", "w_qkv"):
+                norm = self.w[layer + ".in_norm"]
+            elif self.ws_fused and name == "w_gu":
+                norm = self.w[layer + ".post_norm"]
+            wt = self.w[key]
+            wp = K.ws_shuffle(wt.contiguous(), pair_halves=role == K.WS_SILU, col_scale=norm)
+            self.ws[key] = (wp, wt.shape[0], role, kg)
             if role == K.WS_PARTS:
                 self.ws_parts = max(self.ws_parts, kg)
 
@@ -360,6 +378,22 @@ class TridaRuntime:
             K.ws_gemm(x, wp, N, out_p, epilogue=role)
         return None
 
+    def _proj_normed(self, s: "_Scratch", key: str, out_p: torch.Tensor, fused: bool) -> None:
+        """A projection of the normed hidden rows: with `fused`, rmsnorm(h) inside the weight-streaming GEMM
+        (the norm weight is in the weight copy's columns; bf16 or SwiGLU epilogue into out_p's rows);
+        otherwise of x, which add_norm already normed."""
+        if not fused:
+            self._proj(s, key, s.x, s.x_p, out_p)
+            return
+        wp, N, role, _ = self.ws[key]
+        with K.timed("ws_gemm"):
+            K.ws_gemm_norm(s.h, s.ss, wp, N, out_p, eps=self.cfg.rms_eps, epilogue=role)
+
+    def _residual(self, s: "_Scratch", pending) -> None:
+        """h += the partial planes of the projection just run, and the sums of squares for the next norm."""
+        with K.timed("residual"):
+            K.residual_parts(s.h, s.parts, pending[1], s.ss)
+
     def _ws_silu(self, s: "_Scratch", p: str) -> bool:
         """True when the gate/up projection of layer prefix p runs with the SwiGLU epilogue here."""
         return s.N <= K.WS_MAX_M and p + "w_gu" in self.ws
@@ -399,13 +433,20 @@ class TridaRuntime:
         max_keys = min(cache.Lmax, cache.ctx_hint + T)
         fwd_timer = K.timed("forward").__enter__()
         torch.index_select(w["embed"], 0, ids.reshape(-1), out=s.h)
+        # fused: every projection on the weight-streaming GEMM, each RMSNorm inside the GEMM that reads it
+        # (residual_parts adds a projection's partial planes to h and leaves the sums of squares)
+        fused = self.ws_fused and N <= K.WS_MAX_M
+        if fused:
+            with K.timed("residual"):
+                K.residual_parts(s.h, None, 0, s.ss)
         pending = None  # the residual branch not yet added to h
         for i in range(c.n_layers):
             p = f"l{i}."
-            self._add_norm(s, pending, w[p + "in_norm"])
+            if not fused:
+                self._add_norm(s, pending, w[p + "in_norm"])
             j = self._slot[i]
             if c.is_attention(i):
-                self._proj(s, p + "w_qkv", s.x, s.x_p, s.qkv_p)
+                self._proj_normed(s, p + "w_qkv", s.qkv_p, fused)
                 with K.timed("attn_prep"):
                     K.attn_prep(s.qkv, w[p + "q_norm"], w[p + "k_norm"], pos, length, s.q_att, kv_k[j], kv_v[j],
                                 Hq=c.n_heads, Hkv=c.n_kv_heads, D=c.head_dim, rot_dim=c.rot_dim,
@@ -419,7 +460,7 @@ class TridaRuntime:
                                   out=s.o_att, max_keys=max_keys)
                 pending = self._proj(s, p + "w_o", s.o_att_p[:N], s.o_att_p, s.r_p)
             else:
-                self._proj(s, p + "w_in", s.x, s.x_p, s.proj_p)
+                self._proj_normed(s, p + "w_in", s.proj_p, fused)
                 xv = s.proj[..., : c.conv_dim]
                 off = c.conv_dim + c.value_dim
                 b_in = s.proj[..., off: off + c.lin_v_heads]
@@ -457,10 +498,17 @@ class TridaRuntime:
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
                 K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
                 pending = self._proj(s, p + "w_out", s.yn_p[:N], s.yn_p, s.r_p)
-            self._add_norm(s, pending, w[p + "post_norm"])
-            if self._proj(s, p + "w_gu", s.x, s.x_p, s.act_p if self._ws_silu(s, p) else s.gu_p) is not None:
-                K.silu_mul(s.gu, s.act)
+            if fused:
+                self._residual(s, pending)
+                self._proj_normed(s, p + "w_gu", s.act_p, fused)
+            else:
+                self._add_norm(s, pending, w[p + "post_norm"])
+                if self._proj(s, p + "w_gu", s.x, s.x_p, s.act_p if self._ws_silu(s, p) else s.gu_p) is not None:
+                    K.silu_mul(s.gu, s.act)
             pending = self._proj(s, p + "w_down", s.act, s.act_p, s.r_p)
+            if fused:
+                self._residual(s, pending)
+                pending = None
         self._add_norm(s, pending, w["final_norm"])
         x = s.x.view(B, T, -1)
         if rows is not None or row0:
