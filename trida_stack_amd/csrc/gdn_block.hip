@@ -1,0 +1,334 @@
+// Gated delta rule over one canvas block (T <= 64 rows, Dk = 128), the readout of a draft / verify / canvas
+// pass, in the single-chunk WY / UT form on MFMA. It serves trida_gdr_chunk's readout-only blocks (out given,
+// no state_out), the form the decode step runs 4-5 times per step and layer.
+//
+// Per (sequence, value head), with G_t = sum_{s<=t} g_s, St = S^T [Dk, Dv] the state before the block
+// (S as stored [Dv, Dk]; never written) and TP = T rounded up to 16 (rows past T are zero):
+//   A[t][s] = beta_t (k_t . k_s) e^{G_t - G_s} (s < t)          T = (I + A)^{-1}  (unit lower triangular)
+//   R       = diag(beta) (V - diag(e^G) K St)                  v_new = T R
+//   causal row t:    o_t = scale (e^{G_t} q_t St + sum_{s<=t} (q_t . k_s) e^{G_t - G_s} v_new_s)
+//   block-end row t: o_t = scale (e^{G_L} q_t St + sum_{s<T} (q_t . k_s) e^{G_L - G_s} v_new_s)   (L = T - 1)
+// (causal_mode 1: every row causal; 2: rows >= num_clean read the block-end state), the chunk form of
+// S = e^g S; S += beta (v - S k) k^T; o = S q. Every exponent taken is <= 0.
+//
+// Workgroup = (sequence, value head, NWV x 32 value columns), one wave per 32 columns:
+//   1. K, Q (the head's rows) and the group's V columns into LDS; G by a wave prefix sum;
+//   2. K K^T and Q K^T (16 x 16 tiles over Dk on v_mfma_f32_16x16x32_bf16, shared out among the waves),
+//      decayed and masked into A and M (the readout matrix of every row, causal or block-end);
+//   3. every wave forms K St and Q St for its columns (St from HBM as split bf16 hi + lo, K and Q exact)
+//      while wave 0 solves T = (I + A)^{-1} by forward substitution, one column per lane in registers;
+//   4. v_new = T R and o = diag(e^G or e^{G_L}) Q St + M v_new on v_mfma_f32_16x16x16_bf16: the
+//      accumulator layout of R and v_new (rows 4 (l / 16) + i of column l % 16) is the B operand of the
+//      16x16x16 MFMA, so they never leave registers. fp32 operands enter as hi + lo bf16 with
+//      hi*hi + hi*lo + lo*hi (about 16 mantissa bits); fp32 accumulation.
+#include <math.h>
+
+#include "common.h"
+#include "gdn_block.h"
+
+namespace trida {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int DK = 128;
+constexpr int CW = 32;  // value columns per wave
+
+__device__ __forceinline__ f32x4 mma32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+// fp32 x 4 -> bf16 hi and lo (x ~ hi + lo)
+__device__ __forceinline__ void split4(f32x4 x, s16x4& hi, s16x4& lo) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const uint16_t h = f2bf(x[r]);
+    hi[r] = (short)h;
+    lo[r] = (short)f2bf(x[r] - bf2f(h));
+  }
+}
+// 8 fp32 -> 8 bf16 hi and lo, packed as 16x16x32 fragments
+__device__ __forceinline__ void split8(f32x4 a, f32x4 b, u32x4& hi, u32x4& lo) {
+  float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t h0 = f2bf(x[2 * i]), h1 = f2bf(x[2 * i + 1]);
+    h[i] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    l[i] = (uint32_t)f2bf(x[2 * i] - bf2f(h0)) | ((uint32_t)f2bf(x[2 * i + 1] - bf2f(h1)) << 16);
+  }
+  hi = u32x4{h[0], h[1], h[2], h[3]};
+  lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+// hi*hi + hi*lo + lo*hi of an fp32 A fragment and an fp32 B fragment (16x16x16 layouts)
+__device__ __forceinline__ f32x4 mm3(f32x4 a, f32x4 b, f32x4 c) {
+  s16x4 ah, al, bh, bl;
+  split4(a, ah, al);
+  split4(b, bh, bl);
+  c = mma16(ah, bh, c);
+  c = mma16(ah, bl, c);
+  return mma16(al, bh, c);
+}
+
+// K / Q rows [TP][128] bf16 in LDS, 16-byte groups XOR-swizzled by the row (fragment reads of 16 rows
+// touch distinct bank groups)
+__device__ __forceinline__ int kq_off(int r, int grp) { return r * DK + ((grp ^ (r & 15)) << 3); }
+
+template <int TP>
+struct BlockLds {
+  static constexpr int PS = TP + 4;  // fp32 row stride of the TP x TP matrices
+  uint16_t K[TP * DK];
+  uint16_t Q[TP * DK];
+  float A[TP * PS];  // A, then T after the solve
+  float M[TP * PS];
+  float G[TP];
+  float beta[TP];
+  float rs[TP];  // the row scale of the Q St term: e^{G_t} (causal) or e^{G_L} (block-end)
+};
+
+template <int TP, int NWV>
+__global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
+  static_assert(TP % 16 == 0 && TP <= 64, "one chunk of <= 64 rows");
+  constexpr int NT = NWV * kWave, RT = TP / 16;  // threads, row tiles
+  constexpr int PS = BlockLds<TP>::PS;
+  __shared__ BlockLds<TP> sh;
+  __shared__ __align__(16) uint16_t sV[TP * NWV * CW];  // the group's value columns [TP][NWV * 32]
+
+  const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
+  const int groups = a.Dv / (NWV * CW);
+  const int grp = blockIdx.x % groups;
+  const int bh = blockIdx.x / groups;
+  const int b = bh / a.Hv, h = bh % a.Hv, hk = h / (a.Hv / a.Hk);
+  const int T = a.T;
+  const int c0 = grp * NWV * CW + w * CW;  // this wave's first value column
+
+  // ---- 1. rows into LDS (zero past T), g and beta
+  for (int i = tid; i < TP * (DK / 8); i += NT) {
+    const int t = i / (DK / 8), gi = i % (DK / 8);
+    u32x4 kv = {0u, 0u, 0u, 0u}, qv = {0u, 0u, 0u, 0u};
+    if (t < T) {
+      const int64_t row = ((int64_t)b * T + t) * a.Hk + hk;
+      kv = *reinterpret_cast<const u32x4*>(a.k + row * DK + gi * 8);
+      qv = *reinterpret_cast<const u32x4*>(a.q + row * DK + gi * 8);
+    }
+    *reinterpret_cast<u32x4*>(&sh.K[kq_off(t, gi)]) = kv;
+    *reinterpret_cast<u32x4*>(&sh.Q[kq_off(t, gi)]) = qv;
+  }
+  for (int i = tid; i < TP * (NWV * CW / 8); i += NT) {
+    const int t = i / (NWV * CW / 8), gi = i % (NWV * CW / 8);
+    u32x4 vv = {0u, 0u, 0u, 0u};
+    if (t < T)
+      vv = *reinterpret_cast<const u32x4*>(a.v + (((int64_t)b * T + t) * a.Hv + h) * a.Dv + grp * NWV * CW + gi * 8);
+    *reinterpret_cast<u32x4*>(&sV[t * NWV * CW + gi * 8]) = vv;
+  }
+  // this wave's slice of St as 16x16x32 B fragments: column n of tile nt is state row v = c0 + 16 nt + l % 16,
+  // k = 32 kb + 8 (l / 16) .. + 8 contiguous in S[v][:], split into hi and lo
+  u32x4 sth[4][2], stl[4][2];
+  {
+    const float* sb = a.state + ((int64_t)b * a.Hv + h) * a.Dv * DK;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const float* sr = sb + (int64_t)(c0 + nt * 16 + l % 16) * DK + (l / 16) * 8;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(sr + kb * 32);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(sr + kb * 32 + 4);
+        split8(x0, x1, sth[kb][nt], stl[kb][nt]);
+      }
+    }
+  }
+  if (w == 0) {
+    // G = inclusive prefix sum of g over the block (lanes past T add 0), and beta
+    const int t = l;
+    float gv = 0.f, bv = 0.f;
+    if (t < T) {
+      const int64_t gi = ((int64_t)b * T + t) * a.Hv + h;
+      gv = a.g[gi];
+      bv = a.beta[gi];
+    }
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const float o = __shfl_up(gv, off, kWave);
+      if (l >= off) gv += o;
+    }
+    if (t < TP) {
+      sh.G[t] = gv;
+      sh.beta[t] = bv;
+    }
+  }
+  __syncthreads();
+
+  // ---- 2. K K^T (lower tiles) and Q K^T (all tiles) -> A and M
+  const float GL = sh.G[T - 1];
+  constexpr int NKK = RT * (RT + 1) / 2, NQK = RT * RT;
+  for (int job = w; job < NKK + NQK; job += NWV) {
+    const bool is_a = job < NKK;
+    int ti, tj;
+    if (is_a) {  // lower-triangular tile index -> (ti, tj), tj <= ti
+      ti = 0;
+      int r = job;
+      while (r > ti) {
+        r -= ti + 1;
+        ++ti;
+      }
+      tj = r;
+    } else {
+      ti = (job - NKK) / RT;
+      tj = (job - NKK) % RT;
+    }
+    const uint16_t* X = is_a ? sh.K : sh.Q;
+    f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < DK / 32; ++kb) {
+      const u32x4 xa = *reinterpret_cast<const u32x4*>(&X[kq_off(ti * 16 + l % 16, kb * 4 + l / 16)]);
+      const u32x4 kbv = *reinterpret_cast<const u32x4*>(&sh.K[kq_off(tj * 16 + l % 16, kb * 4 + l / 16)]);
+      c = mma32(xa, kbv, c);
+    }
+    // c holds rows t = 16 ti + 4 (l / 16) + i, column s = 16 tj + l % 16
+    const int s = tj * 16 + l % 16;
+    const float Gs = sh.G[s];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = ti * 16 + (l / 16) * 4 + i;
+      const float Gt = sh.G[t];
+      if (is_a) {
+        sh.A[t * PS + s] = s < t ? sh.beta[t] * c[i] * __expf(Gt - Gs) : 0.f;
+      } else {
+        const bool causal = a.causal_mode == 1 || t < a.num_clean;
+        float m = 0.f;
+        if (causal) m = s <= t ? c[i] * __expf(Gt - Gs) : 0.f;
+        else m = s < T ? c[i] * __expf(GL - Gs) : 0.f;
+        sh.M[t * PS + s] = m;
+      }
+    }
+  }
+  if (tid < TP) {
+    const int t = tid;
+    const bool causal = a.causal_mode == 1 || t < a.num_clean;
+    sh.rs[t] = __expf(causal ? sh.G[t] : GL);
+  }
+  __syncthreads();
+
+  // ---- 3. every wave: K St and Q St for its 32 columns (St hi + lo; K and Q exact), issued before
+  //         the solve so that the MFMAs run while wave 0's substitution occupies its VALU
+  f32x4 ks[RT][2], qs[RT][2];
+#pragma unroll
+  for (int it = 0; it < RT; ++it)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      ks[it][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      qs[it][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+  for (int it = 0; it < RT; ++it)
+#pragma unroll
+    for (int kb = 0; kb < DK / 32; ++kb) {
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(&sh.K[kq_off(it * 16 + l % 16, kb * 4 + l / 16)]);
+      const u32x4 qf = *reinterpret_cast<const u32x4*>(&sh.Q[kq_off(it * 16 + l % 16, kb * 4 + l / 16)]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        ks[it][nt] = mma32(kf, sth[kb][nt], ks[it][nt]);
+        ks[it][nt] = mma32(kf, stl[kb][nt], ks[it][nt]);
+        qs[it][nt] = mma32(qf, sth[kb][nt], qs[it][nt]);
+        qs[it][nt] = mma32(qf, stl[kb][nt], qs[it][nt]);
+      }
+    }
+  // wave 0: T = (I + A)^{-1} by forward substitution, lane j holds column j in registers:
+  //         T[t][j] = [t == j] - sum_{s<t} A[t][s] T[s][j]  (A rows read as LDS broadcasts), then T -> LDS (over A)
+  if (w == 0) {
+    float tc[TP];
+#pragma unroll
+    for (int t = 0; t < TP; ++t) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};  // four independent chains (s mod 4), summed at the end
+#pragma unroll
+      for (int s4 = 0; s4 < t; s4 += 4) {
+        const f32x4 ar = *reinterpret_cast<const f32x4*>(&sh.A[t * PS + s4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (s4 + e < t) acc[e] = fmaf(ar[e], tc[s4 + e], acc[e]);
+      }
+      tc[t] = (t == l ? 1.f : 0.f) - ((acc[0] + acc[1]) + (acc[2] + acc[3]));
+    }
+    // every lane has read its last A row above (one wave: in order), so T may overwrite A
+    if (l < TP) {
+#pragma unroll
+      for (int t = 0; t < TP; ++t) sh.A[t * PS + l] = tc[t];
+    }
+  }
+  // R = diag(beta) (V - diag(e^G) K St), in the accumulator layout (the B operand of the 16x16x16 MFMA)
+#pragma unroll
+  for (int it = 0; it < RT; ++it)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = it * 16 + (l / 16) * 4 + i;
+        const float vv = bf2f(sV[t * NWV * CW + w * CW + nt * 16 + l % 16]);
+        ks[it][nt][i] = sh.beta[t] * (vv - __expf(sh.G[t]) * ks[it][nt][i]);
+      }
+  __syncthreads();  // T is in LDS
+
+  // ---- 4. v_new = T R (T lower triangular: k-tiles kt <= it), then o = diag(rs) Q St + M v_new
+  f32x4 vn[RT][2];
+#pragma unroll
+  for (int it = 0; it < RT; ++it)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt <= it; ++kt) {
+        const f32x4 tf = *reinterpret_cast<const f32x4*>(&sh.A[(it * 16 + l % 16) * PS + kt * 16 + (l / 16) * 4]);
+        c = mm3(tf, ks[kt][nt], c);
+      }
+      vn[it][nt] = c;
+    }
+#pragma unroll
+  for (int it = 0; it < RT; ++it)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kt = 0; kt < RT; ++kt) {
+        const f32x4 mf = *reinterpret_cast<const f32x4*>(&sh.M[(it * 16 + l % 16) * PS + kt * 16 + (l / 16) * 4]);
+        c = mm3(mf, vn[kt][nt], c);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = it * 16 + (l / 16) * 4 + i;
+        if (t < T) {
+          const float o = a.scale * (sh.rs[t] * qs[it][nt][i] + c[i]);
+          a.out[(((int64_t)b * T + t) * a.Hv + h) * a.Dv + c0 + nt * 16 + l % 16] = f2bf(o);
+        }
+      }
+    }
+}
+
+template <int NWV>
+void launch_tp(const BlockArgs& a, int B, hipStream_t st) {
+  const dim3 grid((unsigned)(B * a.Hv * (a.Dv / (NWV * CW))));
+  const dim3 block(NWV * kWave);
+  switch ((a.T + 15) / 16) {
+    case 1: hipLaunchKernelGGL((gdr_block_kernel<16, NWV>), grid, block, 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gdr_block_kernel<32, NWV>), grid, block, 0, st, a); break;
+    case 3: hipLaunchKernelGGL((gdr_block_kernel<48, NWV>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((gdr_block_kernel<64, NWV>), grid, block, 0, st, a); break;
+  }
+}
+
+}  // namespace
+
+bool gdr_block_supported(int64_t T, int64_t Dk, int64_t Dv) { return T >= 1 && T <= 64 && Dk == DK && Dv % 128 == 0; }
+
+int gdr_block_launch(const BlockArgs& a, int64_t B, hipStream_t stream) {
+  // small grids: one wave per 32 columns spreads a head over 4 workgroups; large grids: one workgroup per
+  // head shares the K K^T / Q K^T / inverse work among its 4 waves
+  if (B * a.Hv >= 128) launch_tp<4>(a, (int)B, stream);
+  else launch_tp<1>(a, (int)B, stream);
+  return launch_status("gdr_chunk/block");
+}
+
+}  // namespace trida

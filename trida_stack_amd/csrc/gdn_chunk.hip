@@ -34,6 +34,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "gdn_block.h"
 
 namespace trida {
 namespace {
@@ -841,6 +842,12 @@ extern "C" int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint1
   const int64_t need = trida_gdr_chunk_workspace_bytes(B, T, Hv);
   TRIDA_CHECK(need == 0 || (workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0),
               TRIDA_ERR_WORKSPACE, "gdr_chunk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
+  if (out && !state_out && !n_keep && gdr_block_supported(T, Dk, Dv)) {
+    // a canvas block's readout (draft / verify / canvas passes): the single-block MFMA kernel
+    BlockArgs ba{q, k, v, g, beta, state_in, out, (int)T, (int)Hk, (int)Hv, (int)Dv, causal_mode,
+                 causal_mode == 2 ? (int)(num_clean < T ? num_clean : T) : (int)T, scale};
+    return gdr_block_launch(ba, B, static_cast<hipStream_t>(stream));
+  }
   ChunkArgs a{q,        k,   v,       g,         beta,       state_in,      out,
               state_out, n_keep, static_cast<uint16_t*>(workspace), (int)T, (int)Hk, (int)Hv, (int)Dv,
               causal_mode == 2 ? (int)(num_clean < T ? num_clean : T) : (int)T, n_keep ? (int)seq_mod : 1, (int)nchunks,

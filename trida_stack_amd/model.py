@@ -336,10 +336,10 @@ class TridaRuntime:
     # pre-shuffled weights (class default; set before building the runtime)
     use_wsgemm = True
     # GDN recurrence form: "chunked" (WY / UT chunks on MFMA, trida_gdr_chunk), "recurrent" (token by
-    # token, trida_gdr_recurrent) or "auto" (chunked over more than one chunk of rows, i.e. prefill;
-    # recurrent for canvas blocks and the rollback, where it measures faster). Both kernels follow the
-    # same recurrence; only "recurrent" makes the rows of a verify block bitwise equal to the same rows
-    # decoded one AR step at a time.
+    # token, trida_gdr_recurrent) or "auto" (chunked over more than one chunk of rows, i.e. prefill, and
+    # for canvas blocks of large batches, where the single-block MFMA readout wins; recurrent for small
+    # batches' blocks and the rollback). Both kernels follow the same recurrence; only "recurrent" makes
+    # the rows of a verify block bitwise equal to the same rows decoded one AR step at a time.
     gdr_form = "auto"
     # recurrent blocks of <= 64 rows may run conv + prep + recurrence as one launch
     # (trida_gdn_fused_layer, bit-identical to trida_gdn_prep then trida_gdr_recurrent). Off: each
@@ -347,12 +347,19 @@ class TridaRuntime:
     # than the separate prep launch (27 vs 23 us per layer at batch 1, 407 vs 236 us at batch 64).
     fused_gdn = False
 
-    def _chunked_gdr(self, T: int, gdn_mode: int) -> bool:
+    # canvas blocks of at least this many (sequence, value head) pairs take the single-block MFMA readout
+    # under "auto" (batch 64 x 16 heads: 49 vs 132-155 us per layer); smaller grids keep the token-recurrent
+    # kernel (batch 1: 12-16 vs 23 us), whose verify rows are bitwise the AR rows
+    GDR_BLOCK_MIN_HEADS = 128
+
+    def _chunked_gdr(self, T: int, gdn_mode: int, B: int = 1, persist: bool = True) -> bool:
         c = self.cfg
         if self.gdr_form == "recurrent" or c.lin_k_dim not in (32, 64, 128) or c.lin_v_dim % 16:
             return False
         if self.gdr_form == "auto":
-            return gdn_mode == 1 and T > 64
+            block = (not persist and T <= 64 and c.lin_k_dim == 128 and c.lin_v_dim % 128 == 0
+                     and B * c.lin_v_heads >= self.GDR_BLOCK_MIN_HEADS)
+            return (gdn_mode == 1 and T > 64) or block
         return gdn_mode == 1 or T <= 64
 
     def _mm(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -466,7 +473,7 @@ class TridaRuntime:
                 b_in = s.proj[..., off: off + c.lin_v_heads]
                 a_in = s.proj[..., off + c.lin_v_heads: off + 2 * c.lin_v_heads]
                 rec = (s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j])
-                chunked = self._chunked_gdr(T, gdn_mode)
+                chunked = self._chunked_gdr(T, gdn_mode, B, persist)
                 keep = mode != "draft"  # a draft pass is never committed
                 if not chunked and self.fused_gdn and T <= 64 and c.lin_k_dim in (32, 64, 128):
                     with K.timed("gdn_fused"):
