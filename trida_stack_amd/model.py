@@ -415,11 +415,14 @@ class TridaRuntime:
                 K.add_rmsnorm(s.h, None if pending is None else pending[1], w, s.x, eps=eps)
 
     def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
-                rows: Optional[int] = None, seq: Optional[slice] = None, row0: int = 0) -> torch.Tensor:
+                rows: Optional[int] = None, seq: Optional[slice] = None, row0: int = 0,
+                logits_out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """One forward of a [B, T] block of token ids (device int64) on top of the cache.
         Returns bf16 logits [B, rows, V] of block rows row0 .. row0 + rows - 1 (default: every row; the
         LM head runs on those rows only). seq restricts the forward to a contiguous range of the
-        cache's sequences (used by per-sequence prefill of ragged prompts)."""
+        cache's sequences (used by per-sequence prefill of ragged prompts). logits_out: a contiguous fp32
+        [B, rows, V] buffer the LM head writes instead (its fp32 accumulators, no bf16 rounding); it is
+        returned."""
         c, w = self.cfg, self.w
         B, T = ids.shape
         sq = seq if seq is not None else slice(0, cache.B)
@@ -521,7 +524,17 @@ class TridaRuntime:
         if rows is not None or row0:
             x = x[:, row0: row0 + (rows if rows is not None else T - row0)]
         with K.timed("lm_head"):
-            logits = self._mm(x.reshape(-1, x.shape[-1]), w.get("lm_head", w["embed"])).view(B, x.shape[1], -1)
+            x2 = x.reshape(-1, x.shape[-1])
+            wl = w.get("lm_head", w["embed"])
+            if logits_out is not None:
+                # fp32 logits straight from the GEMM's fp32 accumulators (no bf16 output widened again)
+                if logits_out.dtype != torch.float32 or not logits_out.is_contiguous() \
+                        or logits_out.numel() != x2.shape[0] * wl.shape[0]:
+                    raise ValueError("forward: logits_out must be contiguous fp32 [B, rows, V]")
+                torch.ops.aten.mm.dtype_out(x2, wl.t(), torch.float32, out=logits_out.view(x2.shape[0], -1))
+                logits = logits_out.view(B, x.shape[1], -1)
+            else:
+                logits = self._mm(x2, wl).view(B, x.shape[1], -1)
         fwd_timer.__exit__(None, None, None)
         if persist:
             length += T

@@ -300,8 +300,7 @@ class SampledBlockSpecStep:
         correction or bonus token."""
         rt, cache, blk, smp = self.rt, self.cache, self.block, self.smp
         vt = K.timed("verify_step").__enter__()
-        L = rt.forward(self.canvas, cache, "verify")
-        self.pf.copy_(L)
+        rt.forward(self.canvas, cache, "verify", logits_out=self.pf)  # fp32 logits from the LM head
         smp.prepare(self.pf, self.raw_p)
         self.ctx.copy_(cache.length)
         ua, us = self.ua, self.us
