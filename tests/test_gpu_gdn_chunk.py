@@ -23,6 +23,8 @@ SHAPES = [  # (B, T, Hk, Hv, Dk, Dv)
     (1, 65, 2, 2, 128, 32),      # two chunks, the second of one row
     (2, 200, 2, 4, 64, 64),      # several chunks, a ragged last chunk
     (1, 300, 4, 4, 128, 128),
+    (2, 200, 2, 4, 128, 64),     # the one-launch prefix kernel (Dk 128, T > 64): GQA, batch 2, ragged
+    (1, 130, 2, 2, 128, 256),    # 16 value-column slices per head
 ]
 
 
@@ -48,6 +50,23 @@ def test_gdr_chunk_state_in_place_and_strong_decay(gpu):
     o_ref, s_ref, _ = G.recurrent(q, k, v, g, beta, s0)
     qd, kd, vd, gd, bd, sd = to_dev(q, k, v, g, beta, s0)
     o = kernels.gdr_chunk(qd, kd, vd, gd, bd, sd, state_out=sd)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(sd).all()
+    assert rel(o, o_ref) < TOL_BF16 and rel(sd, s_ref) < TOL_F32
+
+
+@pytest.mark.parametrize("T", [129, 257])
+def test_gdr_prefix_state_only_and_strong_decay(gpu, T):
+    """The prefix kernel (Dk 128, T > 64) without a readout (state only), and with log decays down to
+    -30 per row: every exponent it takes is <= 0."""
+    B, Hk, Hv, Dk, Dv = 2, 2, 2, 128, 32
+    q, k, v, g, beta, s0 = gdr_inputs(T, B, T, Hk, Hv, Dk, Dv)
+    g = -torch.rand(B, T, Hv, generator=torch.Generator().manual_seed(T)) * 30
+    o_ref, s_ref, _ = G.recurrent(q, k, v, g, beta, s0)
+    qd, kd, vd, gd, bd, sd = to_dev(q, k, v, g, beta, s0)
+    s_out = torch.full_like(sd, float("nan"))
+    assert kernels.gdr_chunk(None, kd, vd, gd, bd, sd, state_out=s_out, want_out=False) is None
+    assert rel(s_out, s_ref) < TOL_F32
+    o = kernels.gdr_chunk(qd, kd, vd, gd, bd, sd, state_out=sd)  # in place
     assert torch.isfinite(o.float()).all() and torch.isfinite(sd).all()
     assert rel(o, o_ref) < TOL_BF16 and rel(sd, s_ref) < TOL_F32
 

@@ -35,6 +35,7 @@
 
 #include "common.h"
 #include "gdn_block.h"
+#include "gdn_prefix.h"
 
 namespace trida {
 namespace {
@@ -847,6 +848,12 @@ extern "C" int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint1
     BlockArgs ba{q, k, v, g, beta, state_in, out, (int)T, (int)Hk, (int)Hv, (int)Dv, causal_mode,
                  causal_mode == 2 ? (int)(num_clean < T ? num_clean : T) : (int)T, scale};
     return gdr_block_launch(ba, B, static_cast<hipStream_t>(stream));
+  }
+  if (!n_keep && gdr_prefix_supported(B, T, Hv, Dk, Dv)) {
+    // a prompt prefix (every row causal, the state after the last row): the pipelined one-launch kernel
+    PrefixArgs pa{q, k, v, g, beta, state_in, out, state_out, (int)T, (int)Hk, (int)Hv, (int)Dv, (int)nchunks,
+                  scale};
+    return gdr_prefix_launch(pa, B, static_cast<hipStream_t>(stream));
   }
   ChunkArgs a{q,        k,   v,       g,         beta,       state_in,      out,
               state_out, n_keep, static_cast<uint16_t*>(workspace), (int)T, (int)Hk, (int)Hv, (int)Dv,
