@@ -119,21 +119,28 @@ __device__ __forceinline__ void load_raw(Raw& r, const PrefixArgs& a, int b, int
     const int t = t0 + 16 * pw + 4 * (l / 16) + u;
     const bool ok = t < a.T;
     const int64_t off = ((int64_t)(b * a.T + (ok ? t : 0)) * a.Hk + hk) * DK + 8 * (l % 16);
-    r.k[u] = ok ? *reinterpret_cast<const u32x4*>(a.k + off) : u32x4{0u, 0u, 0u, 0u};
-    if (OUT) r.q[u] = ok ? *reinterpret_cast<const u32x4*>(a.q + off) : u32x4{0u, 0u, 0u, 0u};
+    // rows past T read row 0 (in bounds) and are zeroed after the load: no branch around the loads
+    const u32x4 kv = *reinterpret_cast<const u32x4*>(a.k + off);
+    r.k[u] = ok ? kv : u32x4{0u, 0u, 0u, 0u};
+    if (OUT) {
+      const u32x4 qv = *reinterpret_cast<const u32x4*>(a.q + off);
+      r.q[u] = ok ? qv : u32x4{0u, 0u, 0u, 0u};
+    }
   }
   {
     const int t = t0 + 16 * pw + l / 4;
     const bool ok = t < a.T;
     const int64_t off = ((int64_t)(b * a.T + (ok ? t : 0)) * a.Hv + h) * a.Dv + dv0 + 4 * (l % 4);
-    r.v = ok ? *reinterpret_cast<const u32x2*>(a.v + off) : u32x2{0u, 0u};
+    const u32x2 vv = *reinterpret_cast<const u32x2*>(a.v + off);
+    r.v = ok ? vv : u32x2{0u, 0u};
   }
   {
     const int t = t0 + l;
     const bool ok = t < a.T;
     const int64_t gi = (int64_t)(b * a.T + (ok ? t : 0)) * a.Hv + h;
-    r.g = ok ? a.g[gi] : 0.f;
-    r.be = ok ? a.beta[gi] : 0.f;
+    const float gv = a.g[gi], bv = a.beta[gi];
+    r.g = ok ? gv : 0.f;
+    r.be = ok ? bv : 0.f;
   }
 }
 
@@ -263,11 +270,13 @@ struct Prefix {
       }
       const int64_t vrow = (int64_t)a.Hv * a.Dv;
       uint16_t* ob = a.out + (int64_t)b * a.T * vrow + (int64_t)h * a.Dv + dv0 + l % 16;
+      uint16_t ov[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = f2bf(a.scale * (sh.vec[kb][2][16 * w + 4 * (l / 16) + e] * qs[e] + acc[e]));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int t = 16 * w + 4 * (l / 16) + e;
-        const int tg = i * CH + t;
-        if (tg < a.T) ob[(int64_t)tg * vrow] = f2bf(a.scale * (sh.vec[kb][2][t] * qs[e] + acc[e]));
+        const int tg = i * CH + 16 * w + 4 * (l / 16) + e;
+        if (tg < a.T) ob[(int64_t)tg * vrow] = ov[e];
       }
     }
     // state: St' = e^{G_L} St + K^T diag(e^{G_L - G}) v_new on this wave's Dk tiles 2w, 2w+1
@@ -312,9 +321,10 @@ struct Prefix {
         const int s = 16 * tj + l % 16;
         const float Gs = sh.vec[kb][0][s];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
+        for (int e = 0; e < 4; ++e) {  // branch-free: the decay is clamped to <= 0 where it is masked out
           const int t = 16 * ti + 4 * (l / 16) + e;
-          sh.Mh[t * TS + s] = f2bf(s <= t ? cq[e] * ex2(sh.vec[kb][0][t] - Gs) : 0.f);
+          const float x = cq[e] * ex2(fminf(sh.vec[kb][0][t] - Gs, 0.f));
+          sh.Mh[t * TS + s] = f2bf(s <= t ? x : 0.f);
         }
       }
     }
@@ -375,10 +385,13 @@ struct Prefix {
       const float Gr = G2[p0 + r], br = be[p0 + r];
       f32x4 nc, na;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 4; ++e) {  // branch-free: decays clamped to <= 0 where masked out
         const int t = q4 + e;
-        nc[e] = r < t ? -be[p0 + t] * cd[e] * ex2(G2[p0 + t] - Gr) : 0.f;  // N[t][r]
-        na[e] = t < r ? -br * cd[e] * ex2(Gr - G2[p0 + t]) : 0.f;           // N[r][t]
+        const float gt = G2[p0 + t], bt = be[p0 + t];
+        const float xc = -bt * cd[e] * ex2(fminf(gt - Gr, 0.f));
+        const float xa = -br * cd[e] * ex2(fminf(Gr - gt, 0.f));
+        nc[e] = r < t ? xc : 0.f;  // N[t][r]
+        na[e] = t < r ? xa : 0.f;  // N[r][t]
       }
       s16x4 nah, nal, nch, ncl;
       split4(na, nah, nal);
