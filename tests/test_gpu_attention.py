@@ -32,7 +32,7 @@ CASES = [  # B, T, Hq, Hkv, D, L, prefixes
     # ragged batches whose (sequence, KV head) pairs fill whole XCD rounds: scheduled longest-first
     (4, 7, 8, 2, 64, 400, [5, 390, 120, 390]),
     (8, 33, 16, 4, 256, 700, [600, 10, 333, 600, 0, 59, 512, 256]),
-    # past one workgroup per CU with 32-row query tiles: the 128-row tiles, one split each
+    # 20 sequences x 4 KV heads x 2 query tiles: one key split per tile
     (20, 33, 16, 4, 256, 300, [(37 * i) % 260 for i in range(20)]),
 ]
 
