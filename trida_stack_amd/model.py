@@ -296,8 +296,8 @@ class TridaRuntime:
                 "w_gu": K.WS_SILU, "w_down": K.WS_PARTS}
 
     def _shuffle_weights(self) -> None:
-        """A second copy of every decoder projection in the weight-streaming layout (bf16, the same
-        bytes again: 7.4 GB at the 4B shape), for forwards of <= K.WS_MAX_M rows. A projection whose
+        """A second copy of every decoder projection and of the LM head in the weight-streaming layout
+        (bf16, the same bytes again: 7.4 + 1.27 GB at the 4B shape), for forwards of <= K.WS_MAX_M rows. A projection whose
         shape the kernel does not take (N % 16, K % 32, or K too long for a whole-K epilogue) keeps the
         hipBLASLt path. When every projection qualifies (and hidden <= 2560), the forward runs fused: the
         RMSNorm in front of a projection moves into its GEMM, with the norm weight folded into the copy's
@@ -330,6 +330,14 @@ class TridaRuntime:
             self.ws[key] = (wp, wt.shape[0], role, kg)
             if role == K.WS_PARTS:
                 self.ws_parts = max(self.ws_parts, kg)
+        # the LM head (bf16 logits of <= K.WS_MAX_M rows; the fp32 logits_out path keeps hipBLASLt)
+        wl = self.w.get("lm_head", self.w["embed"])
+        if wl.shape[0] % 16 == 0 and wl.shape[1] % 32 == 0:
+            try:
+                kg = K.ws_plan(wl.shape[0], wl.shape[1], K.WS_STORE)
+                self.ws["lm_head"] = (K.ws_shuffle(wl.contiguous()), wl.shape[0], K.WS_STORE, kg)
+            except ValueError:
+                pass
 
     # ---------------------------------------------------------------- forward
     # decoder projections of forwards with <= K.WS_MAX_M rows run on the weight-streaming GEMM over
@@ -533,6 +541,11 @@ class TridaRuntime:
                     raise ValueError("forward: logits_out must be contiguous fp32 [B, rows, V]")
                 torch.ops.aten.mm.dtype_out(x2, wl.t(), torch.float32, out=logits_out.view(x2.shape[0], -1))
                 logits = logits_out.view(B, x.shape[1], -1)
+            elif x2.shape[0] <= K.WS_MAX_M and "lm_head" in self.ws:
+                wp, V, _, _ = self.ws["lm_head"]
+                logits = torch.empty(x2.shape[0], V, dtype=torch.bfloat16, device=self.dev)
+                K.ws_gemm(x2, wp, V, logits, epilogue=K.WS_STORE)
+                logits = logits.view(B, x.shape[1], -1)
             else:
                 logits = self._mm(x2, wl).view(B, x.shape[1], -1)
         fwd_timer.__exit__(None, None, None)
