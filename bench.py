@@ -872,9 +872,9 @@ def bench_gdr(args):
                    "kernel_us": {kk: round(vv, 2) for kk, vv in us.items()},
                    "prefix_gflop": round(flops / 1e9, 3), "prefix_hbm_GBps": round(prefix_bytes / us["prefix"] / 1e3, 1),
                    "snapshot_GBps": round(snap_bytes / us["snapshot"] / 1e3, 1)},
-        "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (prep + scan)", "achieved": round(tflops, 1),
+        "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (gdr_prefix, one launch)", "achieved": round(tflops, 1),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
-                     "traffic": _measured_traffic("gdr_chunk_prep", "gdr_chunk_scan")},
+                     "traffic": _measured_traffic("gdr_prefix")},
         "at_scale": _snapshot_restore_at_scale(dev, H, D, CH),
         "cpu_baseline": cpu,
     }
@@ -919,6 +919,18 @@ def _snapshot_restore_at_scale(dev, H, D, CH, L=24, B=64, T=33):
         us = _events_time_ms(fn, 10) * 1e3
         gbs = nb / (us * 1e-6) / 1e9
         res[name] = {"us": round(us, 1), "bytes": nb, "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    # the device's copy ceiling for the same state bytes (torch's copy kernel), and the rollback's state
+    # advance in the chunked MFMA form (trida_gdr_chunk with n_keep) against the token-recurrent restore
+    us = _events_time_ms(lambda: sn.copy_(st), 10) * 1e3
+    res["copy_ceiling"] = {"us": round(us, 1), "bytes": 2 * state_b, "GBps": round(2 * state_b / (us * 1e-6) / 1e9, 1),
+                           "kernel": "torch copy_ of the fp32 states"}
+    alt = torch.empty_like(st)
+    res["restore_state_us"] = {
+        "token_recurrent": round(_events_time_ms(lambda: K.gdn_restore(n_keep, snap_state=sn, state=st, k=kb, v=vb, g=gb,
+                                                                      beta=bb), 5) * 1e3, 1),
+        "chunked_mfma": round(_events_time_ms(lambda: K.gdr_chunk(None, kb, vb, gb, bb, sn, state_out=alt, n_keep=n_keep,
+                                                                  want_out=False), 5) * 1e3, 1)}
+    del alt
     del st, sn, win, snw, kb, vb, gb, bb, pre
     return res
 
