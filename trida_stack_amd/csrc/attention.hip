@@ -11,7 +11,7 @@
 //   rows each. Per 64-key step, K and V^T are staged in LDS (XOR-swizzled) while the next step is
 //   loaded into registers; every wave computes S = Q K^T for its rows with v_mfma_f32_16x16x32_bf16 (Q
 //   fragments in registers), runs the online softmax within the wave, and accumulates O += P V.
-//   Writes the unnormalised O, row max and row sum of its split.
+//   Writes the unnormalised O (bf16), row max and row sum (fp32) of its split.
 // attn_combine: merges the splits per row (log-sum-exp weights), applies the optional output gate
 //   sigmoid(gate) and writes bf16.
 #include <math.h>
@@ -57,7 +57,7 @@ struct AttnArgs {
   const uint16_t* k_cache;  // [B, Hkv, Lmax, D]
   const uint16_t* v_cache;
   const int32_t* prefix;    // [B]
-  float* opart;             // [B, Hkv, QT, S, kMT, D]
+  uint16_t* opart;          // [B, Hkv, QT, S, kMT, D] bf16
   float* mpart;             // [B, Hkv, QT, S, kMT]
   float* lpart;
   int T, Hq, Hkv, G, Lmax, S, QT, mask_mode, n_clean;
@@ -319,14 +319,14 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
       }
     }
   }
-  // ---- write this split's unnormalised O and row stats
-  float* op = a.opart + pbase * kMT * D;
+  // ---- write this split's unnormalised O (bf16: half the partial traffic) and row stats (fp32)
+  uint16_t* op = a.opart + pbase * kMT * D;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = w * kWR + (l / 16) * 4 + i;
     if (r < rows) {
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) op[(int64_t)r * D + ct * 16 + (l % 16)] = o[ct][i];
+      for (int ct = 0; ct < CT; ++ct) op[(int64_t)r * D + ct * 16 + (l % 16)] = f2bf(o[ct][i]);
       if ((l % 16) == 0) {
         a.mpart[pbase * kMT + r] = m_run[i];
         a.lpart[pbase * kMT + r] = l_run[i];
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
 }
 
 struct CombineArgs {
-  const float* opart;
+  const uint16_t* opart;  // bf16
   const float* mpart;
   const float* lpart;
   const uint16_t* gate;  // row t, head h, dim d at gate + t * gate_st + h * gate_hs + d; or null
@@ -408,18 +408,23 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
   const int c = (tid % per_row) * 4;
   const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
   const int r = m % kMT;
-  const float* obase = a.opart + (int64_t)r * a.D + c;
-  const int64_t sstride = (int64_t)kMT * a.D;  // floats between consecutive splits
+  const uint16_t* obase = a.opart + (int64_t)r * a.D + c;
+  const int64_t sstride = (int64_t)kMT * a.D;  // elements between consecutive splits
+  auto ld4 = [](const uint16_t* p) {  // 4 bf16 -> fp32
+    const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+    return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
+                 __uint_as_float(w.y & 0xffff0000u)};
+  };
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   int j = 0;
   for (; j + 4 <= ns; j += 4) {
     f32x4 x[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const f32x4*>(obase + (bs + s_list[j + u]) * sstride);
+    for (int u = 0; u < 4; ++u) x[u] = ld4(obase + (bs + s_list[j + u]) * sstride);
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc += s_w[i][j + u] * x[u];
   }
-  for (; j < ns; ++j) acc += s_w[i][j] * *reinterpret_cast<const f32x4*>(obase + (bs + s_list[j]) * sstride);
+  for (; j < ns; ++j) acc += s_w[i][j] * ld4(obase + (bs + s_list[j]) * sstride);
   const float inv = s_inv[i];
   const int t = m / a.G, g = m % a.G, hq = hk * a.G + g;
   float y[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
@@ -459,7 +464,7 @@ extern "C" int64_t trida_attn_canvas_scratch_bytes(int64_t B, int64_t T, int64_t
   const int64_t QT = cdiv(T * (Hq / Hkv), kMT);
   const int64_t S = plan_splits(B, Hkv, QT, max_keys, splits);
   const int64_t slots = B * Hkv * QT * S;
-  return align_up(slots * kMT * D * 4, 256) + 2 * align_up(slots * kMT * 4, 256);
+  return align_up(slots * kMT * D * 2, 256) + 2 * align_up(slots * kMT * 4, 256);
 }
 
 extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
@@ -488,9 +493,9 @@ extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, con
   const int64_t slots = B * Hkv * QT * S;
   TRIDA_CHECK(slots < INT32_MAX && B * Hkv < 65535, TRIDA_ERR_ARG, "attn_canvas: grid too large");
   char* ws = static_cast<char*>(scratch);
-  float* opart = reinterpret_cast<float*>(ws);
-  float* mpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 4, 256));
-  float* lpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 4, 256) + align_up(slots * kMT * 4, 256));
+  uint16_t* opart = reinterpret_cast<uint16_t*>(ws);
+  float* mpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 2, 256));
+  float* lpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 2, 256) + align_up(slots * kMT * 4, 256));
   hipStream_t st = static_cast<hipStream_t>(stream);
   AttnArgs a{q, k_cache, v_cache, prefix_len, opart, mpart, lpart, (int)T, (int)Hq, (int)Hkv, (int)G,
              (int)Lmax, (int)S, (int)QT, mask_mode, (int)n_clean, scale * kLog2e};
