@@ -309,19 +309,31 @@ __global__ __launch_bounds__(kWave) void residual_kernel(uint16_t* h, int64_t h_
   float v[4] = {0.f, 0.f, 0.f, 0.f};
   if (e < dim) {
     uint16_t* hp = h + row * h_st + e;
-    const u32x2 hv = *reinterpret_cast<const u32x2*>(hp);
-    v[0] = bf2f((uint16_t)(hv.x & 0xffff));
-    v[1] = bf2f((uint16_t)(hv.x >> 16));
-    v[2] = bf2f((uint16_t)(hv.y & 0xffff));
-    v[3] = bf2f((uint16_t)(hv.y >> 16));
     if (n_parts > 0) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < n_parts; ++s) acc += *reinterpret_cast<const f32x4*>(parts + s * plane_st + row * dim + e);
-      v[0] = bf2f(f2bf(v[0] + bf2f(f2bf(acc.x))));  // the residual stream is bf16
-      v[1] = bf2f(f2bf(v[1] + bf2f(f2bf(acc.y))));
-      v[2] = bf2f(f2bf(v[2] + bf2f(f2bf(acc.z))));
-      v[3] = bf2f(f2bf(v[3] + bf2f(f2bf(acc.w))));
+      // every plane's load issued first (8 loads; planes past n_parts re-read the last one, in bounds, and
+      // are dropped), then h; branch-free; the sum stays in plane order
+      const float* pp = parts + row * dim + e;
+      f32x4 pv[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) pv[s] = *reinterpret_cast<const f32x4*>(pp + min(s, n_parts - 1) * plane_st);
+      const u32x2 hv = *reinterpret_cast<const u32x2*>(hp);
+      f32x4 acc = pv[0];
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 1; s < 8; ++s) acc += s < n_parts ? pv[s] : zero;
+      for (int s = 8; s < n_parts; ++s) acc += *reinterpret_cast<const f32x4*>(pp + s * plane_st);
+      // the residual stream is bf16
+      v[0] = bf2f(f2bf(bf2f((uint16_t)(hv.x & 0xffff)) + bf2f(f2bf(acc.x))));
+      v[1] = bf2f(f2bf(bf2f((uint16_t)(hv.x >> 16)) + bf2f(f2bf(acc.y))));
+      v[2] = bf2f(f2bf(bf2f((uint16_t)(hv.y & 0xffff)) + bf2f(f2bf(acc.z))));
+      v[3] = bf2f(f2bf(bf2f((uint16_t)(hv.y >> 16)) + bf2f(f2bf(acc.w))));
       *reinterpret_cast<u32x2*>(hp) = u32x2{f2bf2(v[0], v[1]), f2bf2(v[2], v[3])};
+    } else {
+      const u32x2 hv = *reinterpret_cast<const u32x2*>(hp);
+      v[0] = bf2f((uint16_t)(hv.x & 0xffff));
+      v[1] = bf2f((uint16_t)(hv.x >> 16));
+      v[2] = bf2f((uint16_t)(hv.y & 0xffff));
+      v[3] = bf2f((uint16_t)(hv.y >> 16));
     }
   }
   float q = 0.f;
