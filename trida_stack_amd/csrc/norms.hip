@@ -51,6 +51,10 @@ constexpr int kMaxPieces = 4;  // 8 elements each per thread: dim <= 256 * 8 * 4
 // The residual r is either bf16 rows (r, r_st) or, with `parts`, the sum of n_parts fp32 planes of
 // plane_st elements each (rows of dim floats): the split-K partial results of the weight-streaming GEMM,
 // summed in plane order and rounded to bf16 as the GEMM's own output would be.
+// NU = pieces of 8 elements per thread (dim <= 2048 NU); MODE 0: no residual, 1: bf16 rows r, 2: fp32 planes.
+// Every load is unconditional (the index clamped into the row; loads past it are dropped), so all of them
+// are in flight together: one memory round trip per row.
+template <int NU, int MODE>
 __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, const uint16_t* r, const float* parts,
                                                                int n_parts, int64_t plane_st, const uint16_t* w,
                                                                uint16_t* out, int dim, int64_t x_st, int64_t r_st,
@@ -58,62 +62,66 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, cons
   __shared__ float red[kThreads / kWave];
   const int64_t row = blockIdx.x;
   const int pieces = dim / 8;
-  // every load (x, residual, weight) is issued before the reduction: one memory round trip per row
-  u32x4 xr[kMaxPieces], rr[kMaxPieces], wr[kMaxPieces];
+  u32x4 xr[NU], rr[NU], wr[NU];
+  f32x4 pv[MODE == 2 ? 8 : 1][NU][2];
 #pragma unroll
-  for (int u = 0; u < kMaxPieces; ++u) {
-    const int p = threadIdx.x + u * kThreads;
-    if (p < pieces) {
-      xr[u] = *reinterpret_cast<const u32x4*>(x + row * x_st + p * 8);
-      if (r) rr[u] = *reinterpret_cast<const u32x4*>(r + row * r_st + p * 8);
-      wr[u] = *reinterpret_cast<const u32x4*>(w + p * 8);
-    }
-  }
-  if (parts) {
-    float acc[kMaxPieces][8];
+  for (int u = 0; u < NU; ++u) {
+    const int p = min((int)threadIdx.x + u * kThreads, pieces - 1);
+    if (MODE == 2) {
+      const float* pl = parts + row * dim + p * 8;
 #pragma unroll
-    for (int u = 0; u < kMaxPieces; ++u)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[u][j] = 0.f;
-    for (int s = 0; s < n_parts; ++s) {
-      const float* pl = parts + s * plane_st + row * dim;
-#pragma unroll
-      for (int u = 0; u < kMaxPieces; ++u) {
-        const int p = threadIdx.x + u * kThreads;
-        if (p < pieces) {
-          const f32x4 a = *reinterpret_cast<const f32x4*>(pl + p * 8);
-          const f32x4 b = *reinterpret_cast<const f32x4*>(pl + p * 8 + 4);
-          acc[u][0] += a.x; acc[u][1] += a.y; acc[u][2] += a.z; acc[u][3] += a.w;
-          acc[u][4] += b.x; acc[u][5] += b.y; acc[u][6] += b.z; acc[u][7] += b.w;
-        }
+      for (int s = 0; s < 8; ++s) {  // planes past n_parts re-read the last one and are dropped
+        const float* q = pl + min(s, n_parts - 1) * plane_st;
+        pv[s][u][0] = *reinterpret_cast<const f32x4*>(q);
+        pv[s][u][1] = *reinterpret_cast<const f32x4*>(q + 4);
       }
     }
-#pragma unroll
-    for (int u = 0; u < kMaxPieces; ++u) rr[u] = pack8(acc[u]);
+    xr[u] = *reinterpret_cast<const u32x4*>(x + row * x_st + p * 8);
+    if (MODE == 1) rr[u] = *reinterpret_cast<const u32x4*>(r + row * r_st + p * 8);
+    wr[u] = *reinterpret_cast<const u32x4*>(w + p * 8);
   }
-  const bool has_r = r || parts;  // its bf16 values are in rr
-  float v[kMaxPieces][8];
+  if (MODE == 2) {  // the planes summed in order and rounded to bf16, as the GEMM's own output would be
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int p = min((int)threadIdx.x + u * kThreads, pieces - 1);
+      f32x4 a0 = pv[0][u][0], a1 = pv[0][u][1];
+      const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 1; s < 8; ++s) {
+        a0 += s < n_parts ? pv[s][u][0] : zero;
+        a1 += s < n_parts ? pv[s][u][1] : zero;
+      }
+      for (int s = 8; s < n_parts; ++s) {
+        const float* q = parts + s * plane_st + row * dim + p * 8;
+        a0 += *reinterpret_cast<const f32x4*>(q);
+        a1 += *reinterpret_cast<const f32x4*>(q + 4);
+      }
+      const float acc[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      rr[u] = pack8(acc);
+    }
+  }
+  float v[NU][8];
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < kMaxPieces; ++u) {
-    const int p = threadIdx.x + u * kThreads;
-    if (p < pieces) {
-      unpack8(xr[u], v[u]);
-      if (has_r) {
-        float rv[8];
-        unpack8(rr[u], rv);
+  for (int u = 0; u < NU; ++u) {
+    const int p = (int)threadIdx.x + u * kThreads;
+    unpack8(xr[u], v[u]);
+    if (MODE != 0) {
+      float rv[8];
+      unpack8(rr[u], rv);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[u][j] = bf2f(f2bf(v[u][j] + rv[j]));  // the residual stream is bf16
-        *reinterpret_cast<u32x4*>(x + row * x_st + p * 8) = pack8(v[u]);
-      }
+      for (int j = 0; j < 8; ++j) v[u][j] = bf2f(f2bf(v[u][j] + rv[j]));  // the residual stream is bf16
+      if (p < pieces) *reinterpret_cast<u32x4*>(x + row * x_st + p * 8) = pack8(v[u]);
+    }
+    if (p < pieces) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss = fmaf(v[u][j], v[u][j], ss);
     }
   }
   const float inv = rsqrtf(block_sum(ss, red) / dim + eps);
 #pragma unroll
-  for (int u = 0; u < kMaxPieces; ++u) {
-    const int p = threadIdx.x + u * kThreads;
+  for (int u = 0; u < NU; ++u) {
+    const int p = (int)threadIdx.x + u * kThreads;
     if (p < pieces) {
       float wv[8], y[8];
       unpack8(wr[u], wv);
@@ -122,6 +130,23 @@ __global__ __launch_bounds__(kThreads) void add_rmsnorm_kernel(uint16_t* x, cons
       *reinterpret_cast<u32x4*>(out + row * o_st + p * 8) = pack8(y);
     }
   }
+}
+
+template <int MODE>
+void launch_add_rmsnorm(int64_t rows, int64_t dim, hipStream_t st, uint16_t* x, const uint16_t* r, const float* parts,
+                        int n_parts, int64_t plane_st, const uint16_t* w, uint16_t* out, int64_t x_st, int64_t r_st,
+                        int64_t o_st, float eps, int zero_centred) {
+  const int nu = (int)cdiv(dim / 8, kThreads);
+#define TRIDA_ARN(NU)                                                                                                 \
+  hipLaunchKernelGGL((add_rmsnorm_kernel<NU, MODE>), dim3((unsigned)rows), dim3(kThreads), 0, st, x, r, parts, n_parts, \
+                     plane_st, w, out, (int)dim, x_st, r_st, o_st, eps, zero_centred)
+  switch (nu) {
+    case 1: TRIDA_ARN(1); break;
+    case 2: TRIDA_ARN(2); break;
+    case 3: TRIDA_ARN(3); break;
+    default: TRIDA_ARN(4); break;
+  }
+#undef TRIDA_ARN
 }
 
 // ------------------------------------------------------------------ silu(g) * u
@@ -141,40 +166,50 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, 
 }
 
 // ------------------------------------------------------------------ gated rmsnorm (one wave per (row, head))
+// PER = Dv / 64 elements per lane, read as one vector per operand (o, gate, weight) before the reduction
+template <int PER>
 __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t* o, const uint16_t* z,
                                                                  const uint16_t* w, uint16_t* out, int64_t rows,
-                                                                 int H, int Dv, int64_t z_st, float eps) {
+                                                                 int H, int64_t z_st, float eps) {
+  constexpr int Dv = PER * kWave;
   const int64_t gw = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
   if (gw >= rows * H) return;
   const int l = threadIdx.x % kWave;
   const int64_t row = gw / H;
   const int h = (int)(gw % H);
-  const int per = Dv / kWave;  // elements per lane (Dv in {64, 128, 256})
-  const uint16_t* op = o + (row * H + h) * Dv + l * per;
-  const uint16_t* zp = z + row * z_st + (int64_t)h * Dv + l * per;
-  // o, gate and weight are all loaded before the reduction: one memory round trip
-  float v[4], zv[4], wv[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (j < per) {
-      v[j] = bf2f(op[j]);
-      zv[j] = bf2f(zp[j]);
-      wv[j] = bf2f(w[l * per + j]);
-    }
+  const uint16_t* op = o + (row * H + h) * Dv + l * PER;
+  const uint16_t* zp = z + row * z_st + (int64_t)h * Dv + l * PER;
+  uint16_t ov[PER], zv[PER], wv[PER];
+  if (PER == 4) {
+    *reinterpret_cast<u32x2*>(ov) = *reinterpret_cast<const u32x2*>(op);
+    *reinterpret_cast<u32x2*>(zv) = *reinterpret_cast<const u32x2*>(zp);
+    *reinterpret_cast<u32x2*>(wv) = *reinterpret_cast<const u32x2*>(w + l * PER);
+  } else if (PER == 2) {
+    *reinterpret_cast<uint32_t*>(ov) = *reinterpret_cast<const uint32_t*>(op);
+    *reinterpret_cast<uint32_t*>(zv) = *reinterpret_cast<const uint32_t*>(zp);
+    *reinterpret_cast<uint32_t*>(wv) = *reinterpret_cast<const uint32_t*>(w + l * PER);
+  } else {
+    ov[0] = op[0];
+    zv[0] = zp[0];
+    wv[0] = w[l];
   }
-  float ss = 0.f;
+  float v[PER], ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (j < per) ss = fmaf(v[j], v[j], ss);
+  for (int j = 0; j < PER; ++j) {
+    v[j] = bf2f(ov[j]);
+    ss = fmaf(v[j], v[j], ss);
+  }
   const float inv = rsqrtf(wave_sum(ss) / Dv + eps);
-  uint16_t* dst = out + (row * H + h) * Dv + l * per;
+  uint16_t y[PER];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if (j < per) {
-      const float nrm = bf2f(f2bf(v[j] * inv));  // normalised value in the input dtype, then weight and gate
-      dst[j] = f2bf(nrm * wv[j] * silu(zv[j]));
-    }
+  for (int j = 0; j < PER; ++j) {
+    const float nrm = bf2f(f2bf(v[j] * inv));  // normalised value in the input dtype, then weight and gate
+    y[j] = f2bf(nrm * bf2f(wv[j]) * silu(bf2f(zv[j])));
   }
+  uint16_t* dst = out + (row * H + h) * Dv + l * PER;
+  if (PER == 4) *reinterpret_cast<u32x2*>(dst) = *reinterpret_cast<const u32x2*>(y);
+  else if (PER == 2) *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(y);
+  else dst[0] = y[0];
 }
 
 // ------------------------------------------------------------------ attention prep (one wave per (row, head))
@@ -276,9 +311,11 @@ extern "C" int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t*
   TRIDA_CHECK(x_st % 8 == 0 && r_st % 8 == 0 && o_st % 8 == 0 &&
                   ((((uintptr_t)x) | (uintptr_t)r | (uintptr_t)w | (uintptr_t)out) & 15) == 0,
               TRIDA_ERR_ALIGN, "add_rmsnorm: 16-byte aligned rows required");
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     x, r, static_cast<const float*>(nullptr), 0, (int64_t)0, w, out, (int)dim, x_st, r_st, o_st, eps,
-                     zero_centred);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (r)
+    launch_add_rmsnorm<1>(rows, dim, st, x, r, nullptr, 0, 0, w, out, x_st, r_st, o_st, eps, zero_centred);
+  else
+    launch_add_rmsnorm<0>(rows, dim, st, x, r, nullptr, 0, 0, w, out, x_st, r_st, o_st, eps, zero_centred);
   return launch_status("add_rmsnorm");
 }
 
@@ -293,9 +330,8 @@ extern "C" int trida_add_rmsnorm_parts(uint16_t* x, const float* parts, int64_t 
   TRIDA_CHECK(x_st % 8 == 0 && o_st % 8 == 0 && plane_stride % 4 == 0 &&
                   ((((uintptr_t)x) | (uintptr_t)parts | (uintptr_t)w | (uintptr_t)out) & 15) == 0,
               TRIDA_ERR_ALIGN, "add_rmsnorm_parts: 16-byte aligned rows required");
-  hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(kThreads), 0, static_cast<hipStream_t>(stream),
-                     x, static_cast<const uint16_t*>(nullptr), parts, (int)n_parts, plane_stride, w, out, (int)dim, x_st,
-                     (int64_t)0, o_st, eps, zero_centred);
+  launch_add_rmsnorm<2>(rows, dim, static_cast<hipStream_t>(stream), x, nullptr, parts, (int)n_parts, plane_stride, w,
+                        out, x_st, 0, o_st, eps, zero_centred);
   return launch_status("add_rmsnorm_parts");
 }
 
@@ -317,8 +353,17 @@ extern "C" int trida_gated_rmsnorm(const uint16_t* o, const uint16_t* z, const u
   TRIDA_CHECK(rows > 0 && H > 0 && (Dv == 64 || Dv == 128 || Dv == 256) && z_st >= H * Dv, TRIDA_ERR_ARG,
               "gated_rmsnorm: Dv must be 64, 128 or 256");
   const int64_t waves = rows * H;
-  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((unsigned)cdiv(waves, kThreads / kWave)), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), o, z, w, out, rows, (int)H, (int)Dv, z_st, eps);
+  const dim3 grid((unsigned)cdiv(waves, kThreads / kWave));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t per = Dv / kWave;  // elements per lane, read as one vector of 2 * per bytes
+  TRIDA_CHECK(((((uintptr_t)o) | (uintptr_t)z | (uintptr_t)w | (uintptr_t)out) & (2 * per - 1)) == 0 && z_st % per == 0,
+              TRIDA_ERR_ALIGN, "gated_rmsnorm: rows aligned to 2 * Dv / 64 bytes required");
+  if (Dv == 256)
+    hipLaunchKernelGGL(gated_rmsnorm_kernel<4>, grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H, z_st, eps);
+  else if (Dv == 128)
+    hipLaunchKernelGGL(gated_rmsnorm_kernel<2>, grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H, z_st, eps);
+  else
+    hipLaunchKernelGGL(gated_rmsnorm_kernel<1>, grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H, z_st, eps);
   return launch_status("gated_rmsnorm");
 }
 
