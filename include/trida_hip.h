@@ -412,6 +412,28 @@ int trida_wsgemm_norm(const uint16_t* X, int64_t x_row_stride, const float* ss, 
 int64_t trida_residual_ss_chunks(int64_t dim);
 int trida_residual_parts(uint16_t* h, int64_t h_row_stride, const float* parts, int64_t n_parts, int64_t plane_stride,
                          int64_t rows, int64_t dim, float* ss, void* stream);
+/* Fragment order of a weight-streaming GEMM's activations X [M, K] (M <= 48, K % 32 == 0): the operand
+ * layout of the kernel's matrix-core step, so that each of its X loads reads 1 KB of consecutive bytes
+ * (row-major X gives each load 16 rows x 64 bytes, half a cache line per row, and the workgroup's X slice
+ * takes twice as long to arrive). Xf holds trida_ws_frag_elems(K) bf16 (16-byte aligned); X[m][k] sits at
+ * element ((k / 32 * 3 + m / 16) * 64 + (k % 32) / 8 * 16 + m % 16) * 8 + k % 8, whatever M is; entries
+ * of rows >= M are neither written nor read. No counterpart in the reference (an internal layout between
+ * the kernels of one decoder forward, inference/zoro-1/mlx/trida_mlx/model.py:337-364).
+ * trida_ws_frag converts row-major X; trida_residual_parts_frag is trida_residual_parts that also writes
+ * the updated h in fragment order to h_frag (rows <= 48, dim % 32 == 0); trida_gated_rmsnorm_frag writes
+ * trida_gated_rmsnorm's output in fragment order (K = H * Dv). trida_wsgemm_ex is trida_wsgemm (ss NULL)
+ * or trida_wsgemm_norm (ss given) with flags: TRIDA_WS_X_FRAG = X in fragment order (x_row_stride
+ * unused), TRIDA_WS_OUT_FRAG = the bf16 output of epilogue 0 or 2 in fragment order for the next GEMM
+ * (out_row_stride unused). The results are bitwise those of the row-major forms. */
+#define TRIDA_WS_X_FRAG 1
+#define TRIDA_WS_OUT_FRAG 2
+int64_t trida_ws_frag_elems(int64_t K);
+int trida_ws_frag(const uint16_t* X, int64_t x_row_stride, int64_t M, int64_t K, uint16_t* Xf, void* stream);
+int trida_wsgemm_ex(const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp, int64_t M,
+                    int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride, int flags, void* stream);
+int trida_residual_parts_frag(uint16_t* h, int64_t h_row_stride, const float* parts, int64_t n_parts,
+                              int64_t plane_stride, int64_t rows, int64_t dim, float* ss, uint16_t* h_frag,
+                              void* stream);
 
 int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim,
                       int64_t x_st, int64_t r_st, int64_t o_st, float eps, int zero_centred, void* stream);
@@ -424,6 +446,8 @@ int trida_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, int64_t inte
                    void* stream);
 int trida_gated_rmsnorm(const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out, int64_t rows,
                         int64_t H, int64_t Dv, int64_t z_st, float eps, void* stream);
+int trida_gated_rmsnorm_frag(const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out_frag, int64_t rows,
+                             int64_t H, int64_t Dv, int64_t z_st, float eps, void* stream);
 int trida_attn_prep(const uint16_t* qkv, int64_t qkv_row_stride, const uint16_t* q_norm_w, const uint16_t* k_norm_w,
                     const int32_t* pos0, const int32_t* slot0, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
                     int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax, int64_t rot_dim,

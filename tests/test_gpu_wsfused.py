@@ -77,6 +77,72 @@ def test_ws_gemm_norm(gpu, M, N, K, epi):
     assert torch.equal(out1, out[:1])
 
 
+@pytest.mark.parametrize("M,N,K,epi,norm", [(33, 8224, 2560, 0, True), (33, 19456, 2560, 2, True),
+                                            (33, 2560, 9728, 1, False), (1, 2560, 2048, 1, False),
+                                            (48, 256, 96, 2, False), (17, 128, 256, 0, False), (5, 64, 320, 2, True)])
+def test_ws_gemm_fragment_order(gpu, M, N, K, epi, norm):
+    """X in fragment order (converted, or written by the producers the fused forward uses) gives bitwise
+    the row-major GEMM's result, and a fragment-order output is bitwise the row-major output converted."""
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    wp = TK.ws_shuffle(w, pair_halves=epi == TK.WS_SILU)
+    xf = TK.ws_frag(x)
+    ss = None
+    if norm:
+        ss = torch.empty(M, TK.ss_chunks(K), device=DEV)
+        hf = torch.full((TK.ws_frag_numel(K),), float("nan"), dtype=torch.bfloat16, device=DEV)
+        TK.residual_parts(x, None, 0, ss, h_frag=hf)  # the residual kernel's own copy of h
+        mask = _frag_mask(M, K)
+        assert torch.equal(hf.view(torch.int16).cpu()[mask], xf.view(torch.int16).cpu()[mask])
+    width = N // 2 if epi == TK.WS_SILU else N
+    if epi == TK.WS_PARTS:
+        kg = TK.ws_plan(N, K, epi)
+        ref = torch.empty(kg * M * N, device=DEV)
+        got = torch.full_like(ref, float("nan"))
+        TK.ws_gemm(x, wp, N, ref, epilogue=epi)
+        TK.ws_gemm_frag(xf, M, wp, N, got, epilogue=epi)
+        assert torch.equal(got, ref)
+        return
+    ref = torch.empty(M, width, dtype=torch.bfloat16, device=DEV)
+    if norm:
+        TK.ws_gemm_norm(x, ss, wp, N, ref, epilogue=epi)
+    else:
+        TK.ws_gemm(x, wp, N, ref, epilogue=epi)
+    got = torch.empty_like(ref)
+    TK.ws_gemm_frag(xf, M, wp, N, got, ss=ss, epilogue=epi)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    if width % 32 == 0:
+        of = torch.zeros(TK.ws_frag_numel(width), dtype=torch.bfloat16, device=DEV)
+        TK.ws_gemm_frag(xf, M, wp, N, of, ss=ss, epilogue=epi, out_frag=True)
+        mask = _frag_mask(M, width)
+        assert torch.equal(of.view(torch.int16).cpu()[mask], TK.ws_frag(ref).view(torch.int16).cpu()[mask])
+
+
+def _frag_mask(M, K):
+    """The fragment-order entries of rows < M (the rest is never written nor read)."""
+    import numpy as np
+    m, k = np.meshgrid(np.arange(M), np.arange(K), indexing="ij")
+    off = (((k // 32) * 3 + m // 16) * 64 + ((k % 32) // 8) * 16 + m % 16) * 8 + k % 8
+    mask = torch.zeros(K // 32 * 3 * 64 * 8, dtype=torch.bool)
+    mask[torch.from_numpy(off.ravel())] = True
+    return mask
+
+
+@pytest.mark.parametrize("rows,H,Dv", [(33, 16, 128), (7, 4, 256), (48, 2, 64)])
+def test_gated_rmsnorm_fragment_order(gpu, rows, H, Dv):
+    g = torch.Generator().manual_seed(rows + H + Dv)
+    o = torch.randn(rows, H, Dv, generator=g).to(torch.bfloat16).to(DEV)
+    z = torch.randn(rows, H * Dv + 64, generator=g).to(torch.bfloat16).to(DEV)[:, 32: 32 + H * Dv]
+    w = (torch.randn(Dv, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    ref = torch.empty(rows, H, Dv, dtype=torch.bfloat16, device=DEV)
+    TK.gated_rmsnorm(o, z, w, ref)
+    of = torch.zeros(TK.ws_frag_numel(H * Dv), dtype=torch.bfloat16, device=DEV)
+    TK.gated_rmsnorm(o, z, w, of, out_frag=True)
+    mask = _frag_mask(rows, H * Dv)
+    assert torch.equal(of.view(torch.int16).cpu()[mask], TK.ws_frag(ref.view(rows, -1)).view(torch.int16).cpu()[mask])
+
+
 @pytest.fixture(scope="module")
 def fused_pair():
     w = init_weights(CFG, seed=0, embed_scale=4.0)

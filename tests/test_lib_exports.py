@@ -117,3 +117,34 @@ def test_gdr_chunk_argument_checks():
     assert call(mode=2) == _lib.TRIDA_ERR_ARG and b"causal_mode 2" in lib.trida_last_error()
     assert call(T=64, mode=2, n_keep=P) == _lib.TRIDA_ERR_ARG
     assert call(T=100) == _lib.TRIDA_ERR_WORKSPACE
+
+
+def test_ws_fragment_order_host_checks():
+    """The fragment order of the weight-streaming GEMM's X: its size and the argument checks of the entry
+    points that read or write it (dummy pointers; nothing is launched)."""
+    lib = _lib.load()
+    assert lib.trida_ws_frag_elems(2560) == 2560 // 32 * 3 * 64 * 8
+    assert lib.trida_ws_frag_elems(100) == 0
+    P = 256
+    # partial planes have no fragment order; unknown flag bits; M above 48
+    assert lib.trida_wsgemm_ex(P, 0, None, 1e-6, P, 4, 64, 256, 1, P, 0, 2, None) == _lib.TRIDA_ERR_ARG
+    assert lib.trida_wsgemm_ex(P, 0, None, 1e-6, P, 4, 64, 256, 0, P, 0, 4, None) == _lib.TRIDA_ERR_ARG
+    assert lib.trida_wsgemm_ex(P, 0, None, 1e-6, P, 49, 64, 256, 0, P, 0, 1, None) == _lib.TRIDA_ERR_ARG
+    # the RMSNorm prologue takes no partial planes
+    assert lib.trida_wsgemm_ex(P, 256, P, 1e-6, P, 4, 64, 256, 1, P, 0, 0, None) == _lib.TRIDA_ERR_ARG
+    assert lib.trida_ws_frag(P, 256, 49, 256, P, None) == _lib.TRIDA_ERR_ARG
+    assert lib.trida_residual_parts_frag(P, 256, None, 0, 0, 49, 256, P, P, None) == _lib.TRIDA_ERR_ARG
+    assert lib.trida_gated_rmsnorm_frag(P, P, P, P, 49, 2, 128, 256, 1e-6, None) == _lib.TRIDA_ERR_ARG
+
+
+def test_ws_fragment_offsets_are_a_bijection():
+    """The fragment order's element offset (restated from the header's formula) maps the rows < 48 x K
+    elements one to one onto [0, trida_ws_frag_elems(K)), and keeps each lane's 8 elements of a k-step
+    consecutive (what makes one 16-byte load per lane)."""
+    import numpy as np
+
+    K = 96
+    m, k = np.meshgrid(np.arange(48), np.arange(K), indexing="ij")
+    off = (((k // 32) * 3 + m // 16) * 64 + ((k % 32) // 8) * 16 + m % 16) * 8 + k % 8
+    assert np.array_equal(np.sort(off.ravel()), np.arange(_lib.load().trida_ws_frag_elems(K)))
+    assert np.all(np.diff(off.reshape(48, K // 8, 8), axis=2) == 1)

@@ -53,10 +53,15 @@ SIGNATURES = {
     "trida_wsgemm_norm": (C.c_int, [P, I64, P, F32, P, I64, I64, I64, C.c_int, P, I64, P]),
     "trida_residual_ss_chunks": (I64, [I64]),
     "trida_residual_parts": (C.c_int, [P, I64, P, I64, I64, I64, I64, P, P]),
+    "trida_ws_frag_elems": (I64, [I64]),
+    "trida_ws_frag": (C.c_int, [P, I64, I64, I64, P, P]),
+    "trida_wsgemm_ex": (C.c_int, [P, I64, P, F32, P, I64, I64, I64, C.c_int, P, I64, C.c_int, P]),
+    "trida_residual_parts_frag": (C.c_int, [P, I64, P, I64, I64, I64, I64, P, P, P]),
     "trida_add_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, I64, F32, C.c_int, P]),
     "trida_add_rmsnorm_parts": (C.c_int, [P, P, I64, I64, P, P, I64, I64, I64, I64, F32, C.c_int, P]),
     "trida_silu_mul": (C.c_int, [P, P, I64, I64, I64, I64, P]),
     "trida_gated_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, F32, P]),
+    "trida_gated_rmsnorm_frag": (C.c_int, [P, P, P, P, I64, I64, I64, I64, F32, P]),
     "trida_attn_prep": (C.c_int, [P, I64, P, P, P, P, P, P, P] + [I64] * 7 + [F32, F32, P]),
     "trida_gdn_prep": (C.c_int, [P] * 14 + [I64] * 11 + [P]),
     "trida_gdr_recurrent": (C.c_int, [P] * 9 + [I64] * 6 + [C.c_int, I64, F32, P]),

@@ -68,6 +68,14 @@ __device__ __forceinline__ int xcd_major(int i, int n) {
   return (n % kXcds) ? i : (i % kXcds) * (n / kXcds) + i / kXcds;
 }
 
+// Fragment order of the weight-streaming GEMM's activations X [M <= 48, K]: per k-step s of 32 columns and
+// m-tile mt of 16 rows, 64 lanes x 16 bytes, lane 16 g + r holding X[16 mt + r][32 s + 8 g .. + 8] (the
+// B operand of v_mfma_f32_16x16x32_bf16 as it lands in a register). Element offset of X[m][k]:
+constexpr int kWsFragMT = 3;  // m-tiles per k-step, whatever M is
+__host__ __device__ inline int64_t ws_frag_off(int m, int64_t k) {
+  return (((k / 32) * kWsFragMT + m / 16) * 64 + ((k % 32) / 8) * 16 + m % 16) * 8 + k % 8;
+}
+
 // ---------------------------------------------------------------- host error plumbing
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);

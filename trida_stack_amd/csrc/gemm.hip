@@ -14,6 +14,11 @@
 //     parked tiles in wave order and run the epilogue. A plan's T tiles fit in the slots, so the weight
 //     stream never waits on another wave (longer plans flush every NSLOT tiles);
 //   - X rows past M are not loaded (lanes masked), so a 33-row canvas moves 2 KB + 64 B of X per k-step;
+//   - X may come in fragment order (Xf[s][mt][lane], lane 16 g + r holding X[16 mt + r][32 s + 8 g .. + 8],
+//     mt stride kWsFragMT whatever M is): every X load of a wave is then 1 KB of consecutive bytes, whole
+//     cache lines, where row-major X gives each load 16 rows x 64 B, half a line per row (the whole slice of
+//     a 33-row canvas: 2.4 instead of 4.6 us per workgroup). The producers of the decode-step activations
+//     (trida_residual_parts_frag, trida_gated_rmsnorm_frag, this kernel's own epilogues) write that order;
 //   - K beyond NW * KWS steps is split over kg workgroup groups that write fp32 partial planes
 //     [kg][M][N]; trida_add_rmsnorm_parts (norms.hip) sums them in plane order.
 // Epilogues: bf16 store, fp32 partials, or SwiGLU (silu(gate) * up) over weights whose tiles interleave 8
@@ -46,7 +51,10 @@ struct WsArgs {
   // K + eps) over the ss_chunks(K) per-chunk sums of squares, applied in the epilogue
   const float* ss;
   float eps;
+  int xf;  // X in fragment order (x_st unused)
+  int of;  // bf16 output (store / SwiGLU epilogues) in fragment order for the next GEMM (o_st unused)
 };
+
 
 // chunks of the per-row sums of squares that trida_residual_parts writes: 256 elements each
 __host__ __device__ constexpr int ss_chunks(int dim) { return (dim + 255) / 256; }
@@ -87,15 +95,28 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
   // X slice (issued after the first weight loads, so their latency overlaps): lanes of tokens past M
   // load nothing (their columns are never stored); steps past K are zero
   u32x4 xs[KWS][MT];
+  if (a.xf) {
+    const u32x4* xb = reinterpret_cast<const u32x4*>(a.X) + l;
 #pragma unroll
-  for (int j = 0; j < KWS; ++j) {
-    const int s = min(s_base + j, nsteps - 1);
+    for (int j = 0; j < KWS; ++j) {
+      const int s = min(s_base + j, nsteps - 1);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = mt * 16 + (l % 16);
-      xs[j][mt] = u32x4{0u, 0u, 0u, 0u};
-      if (m < a.M && j < my_steps)
-        xs[j][mt] = *reinterpret_cast<const u32x4*>(a.X + (int64_t)m * a.x_st + s * 32 + (l / 16) * 8);
+      for (int mt = 0; mt < MT; ++mt) {
+        xs[j][mt] = u32x4{0u, 0u, 0u, 0u};
+        if (mt * 16 + (l % 16) < a.M && j < my_steps) xs[j][mt] = xb[((int64_t)s * kWsFragMT + mt) * kWave];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < KWS; ++j) {
+      const int s = min(s_base + j, nsteps - 1);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + (l % 16);
+        xs[j][mt] = u32x4{0u, 0u, 0u, 0u};
+        if (m < a.M && j < my_steps)
+          xs[j][mt] = *reinterpret_cast<const u32x4*>(a.X + (int64_t)m * a.x_st + s * 32 + (l / 16) * 8);
+      }
     }
   }
   // Wait for the prologue's loads here: the first MFMA needs the last of them anyway (X was issued after
@@ -119,6 +140,11 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
     inv_s[threadIdx.x] = rsqrtf(sum / (float)a.K + a.eps);
   }
 
+  // 4 consecutive bf16 outputs (n % 4 == 0) of row m: row-major, or in fragment order for the next GEMM
+  auto out_at = [&](int m, int n) -> u32x2* {
+    uint16_t* o = static_cast<uint16_t*>(a.out);
+    return reinterpret_cast<u32x2*>(a.of ? o + ws_frag_off(m, n) : o + (int64_t)m * a.o_st + n);
+  };
   // tiles [first, last] are parked in their slots: meet, sum the NW partials of each in wave order, run the
   // epilogue (64 * NW threads over the parked tiles' outputs)
   auto flush = [&](int first, int last) {
@@ -154,7 +180,7 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
           u32x2 packed;
           packed.x = f2bf2(y0, y1);
           packed.y = f2bf2(y2, y3);
-          *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + f) = packed;
+          *out_at(m, f) = packed;
         }
       } else {
         const int mt = q / kWave, ln = q % kWave;
@@ -169,7 +195,7 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
             u32x2 packed;
             packed.x = f2bf2(sum.x, sum.y);
             packed.y = f2bf2(sum.z, sum.w);
-            *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + (int64_t)m * a.o_st + n) = packed;
+            *out_at(m, n) = packed;
           } else {
             *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = sum;
           }
@@ -300,9 +326,10 @@ void launch_cfg(const WsArgs& a, const Plan& p, hipStream_t st) {
 
 // residual add of split-K partial planes (grid rows x ss_chunks(dim), one wave per 256-element chunk):
 // h = bf16(h + bf16(sum_s parts[s][row])) (planes summed in order; n_parts = 0 leaves h as it is), and
-// ss[row][chunk] = the chunk's sum of h^2, which the RMSNorm prologue of the next GEMM reads
+// ss[row][chunk] = the chunk's sum of h^2, which the RMSNorm prologue of the next GEMM reads; hf (rows <= 48,
+// or null): h once more in fragment order, the next GEMM's X
 __global__ __launch_bounds__(kWave) void residual_kernel(uint16_t* h, int64_t h_st, const float* parts, int n_parts,
-                                                         int64_t plane_st, int dim, float* ss) {
+                                                         int64_t plane_st, int dim, float* ss, uint16_t* hf) {
   const int64_t row = blockIdx.x;
   const int c = blockIdx.y, l = threadIdx.x;
   const int e = c * 256 + l * 4;
@@ -335,12 +362,21 @@ __global__ __launch_bounds__(kWave) void residual_kernel(uint16_t* h, int64_t h_
       v[2] = bf2f((uint16_t)(hv.y & 0xffff));
       v[3] = bf2f((uint16_t)(hv.y >> 16));
     }
+    if (hf) *reinterpret_cast<u32x2*>(hf + ws_frag_off((int)row, e)) = u32x2{f2bf2(v[0], v[1]), f2bf2(v[2], v[3])};
   }
   float q = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) q = fmaf(v[i], v[i], q);
   q = wave_sum(q);
   if (l == 0) ss[row * ss_chunks(dim) + c] = q;
+}
+
+// row-major X [M, K] to fragment order: one thread per 16-byte piece
+__global__ __launch_bounds__(256) void frag_kernel(const uint16_t* X, int64_t x_st, int M, int K, uint16_t* Xf) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * (K / 8)) return;
+  const int m = (int)(i / (K / 8)), k = (int)(i % (K / 8)) * 8;
+  *reinterpret_cast<u32x4*>(Xf + ws_frag_off(m, k)) = *reinterpret_cast<const u32x4*>(X + (int64_t)m * x_st + k);
 }
 
 bool shape_ok(int64_t N, int64_t K, int epi) {
@@ -379,65 +415,100 @@ extern "C" int trida_wsgemm_plan(int64_t N, int64_t K, int epilogue, int32_t* kg
   return TRIDA_OK;
 }
 
+namespace {
+// the weight-streaming GEMM behind every entry point: ss null = no RMSNorm prologue; flags TRIDA_WS_X_FRAG /
+// TRIDA_WS_OUT_FRAG select the fragment order of X / of the bf16 output
+int ws_run(const char* name, const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp,
+           int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride, int flags, void* stream) {
+  TRIDA_CHECK(X && Wp && out, TRIDA_ERR_NULL, "%s: X, Wp and out are required", name);
+  TRIDA_CHECK(epilogue >= kStore && epilogue <= kSilu, TRIDA_ERR_ARG, "%s: unknown epilogue %d", name, epilogue);
+  TRIDA_CHECK(!ss || epilogue != kParts, TRIDA_ERR_ARG,
+              "%s: the RMSNorm prologue takes the bf16 (0) or SwiGLU (2) epilogue", name);
+  TRIDA_CHECK((flags & ~(TRIDA_WS_X_FRAG | TRIDA_WS_OUT_FRAG)) == 0 &&
+                  (!(flags & TRIDA_WS_OUT_FRAG) || epilogue != kParts),
+              TRIDA_ERR_ARG, "%s: bad flags %d (a fragment-order output needs the bf16 or SwiGLU epilogue)", name,
+              flags);
+  TRIDA_CHECK(M >= 1 && M <= kMaxM && shape_ok(N, K, epilogue), TRIDA_ERR_ARG,
+              "%s: need 1 <= M <= %d, N %% 16 == 0, K %% 32 == 0 (M=%lld N=%lld K=%lld)", name, kMaxM, (long long)M,
+              (long long)N, (long long)K);
+  const bool xf = flags & TRIDA_WS_X_FRAG, of = flags & TRIDA_WS_OUT_FRAG;
+  TRIDA_CHECK(!of || (epilogue == kSilu ? N / 2 : N) % 32 == 0, TRIDA_ERR_ARG,
+              "%s: a fragment-order output needs a width that is a multiple of 32", name);
+  TRIDA_CHECK(xf || (x_row_stride >= K && x_row_stride % 8 == 0), TRIDA_ERR_ARG, "%s: bad X row stride", name);
+  TRIDA_CHECK(epilogue == kParts || of ||
+                  (out_row_stride >= (epilogue == kSilu ? N / 2 : N) && out_row_stride % 4 == 0),
+              TRIDA_ERR_ARG, "%s: bad output row stride", name);
+  TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Wp | (uintptr_t)out) & 15) == 0 && ((uintptr_t)ss & 3) == 0,
+              TRIDA_ERR_ALIGN, "%s: X, Wp and out must be 16-byte aligned", name);
+  const Plan p = plan_for(N, K, epilogue);
+  TRIDA_CHECK(p.cfg >= 0 && (!ss || ss_chunks((int)K) <= kMaxSsChunks), TRIDA_ERR_ARG,
+              "%s: K too long for one workgroup (epilogue %d needs kg == 1)", name, epilogue);
+  WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T, ss,
+           eps, xf ? 1 : 0, of ? 1 : 0};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (ss) {
+    if (epilogue == kStore) launch_cfg<kStore, true>(a, p, st);
+    else launch_cfg<kSilu, true>(a, p, st);
+  } else {
+    if (epilogue == kStore) launch_cfg<kStore, false>(a, p, st);
+    else if (epilogue == kParts) launch_cfg<kParts, false>(a, p, st);
+    else launch_cfg<kSilu, false>(a, p, st);
+  }
+  return launch_status(name);
+}
+}  // namespace
+
 extern "C" int trida_wsgemm(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M, int64_t N,
                             int64_t K, int epilogue, void* out, int64_t out_row_stride, void* stream) {
-  TRIDA_CHECK(X && Wp && out, TRIDA_ERR_NULL, "wsgemm: X, Wp and out are required");
-  TRIDA_CHECK(epilogue >= kStore && epilogue <= kSilu, TRIDA_ERR_ARG, "wsgemm: unknown epilogue %d", epilogue);
-  TRIDA_CHECK(M >= 1 && M <= kMaxM && shape_ok(N, K, epilogue), TRIDA_ERR_ARG,
-              "wsgemm: need 1 <= M <= %d, N %% 16 == 0, K %% 32 == 0 (M=%lld N=%lld K=%lld)", kMaxM, (long long)M,
-              (long long)N, (long long)K);
-  TRIDA_CHECK(x_row_stride >= K && x_row_stride % 8 == 0, TRIDA_ERR_ARG, "wsgemm: bad X row stride");
-  TRIDA_CHECK(epilogue == kParts || (out_row_stride >= (epilogue == kSilu ? N / 2 : N) && out_row_stride % 4 == 0),
-              TRIDA_ERR_ARG, "wsgemm: bad output row stride");
-  TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Wp | (uintptr_t)out) & 15) == 0, TRIDA_ERR_ALIGN,
-              "wsgemm: X, Wp and out must be 16-byte aligned");
-  const Plan p = plan_for(N, K, epilogue);
-  TRIDA_CHECK(p.cfg >= 0, TRIDA_ERR_ARG, "wsgemm: K too long for one workgroup (epilogue %d needs kg == 1)",
-              epilogue);
-  WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T,
-           nullptr, 0.f};
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (epilogue == kStore) launch_cfg<kStore, false>(a, p, st);
-  else if (epilogue == kParts) launch_cfg<kParts, false>(a, p, st);
-  else launch_cfg<kSilu, false>(a, p, st);
-  return launch_status("wsgemm");
+  return ws_run("wsgemm", X, x_row_stride, nullptr, 0.f, Wp, M, N, K, epilogue, out, out_row_stride, 0, stream);
 }
 
 extern "C" int trida_wsgemm_norm(const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp,
                                  int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride,
                                  void* stream) {
-  TRIDA_CHECK(X && ss && Wp && out, TRIDA_ERR_NULL, "wsgemm_norm: X, ss, Wp and out are required");
-  TRIDA_CHECK(epilogue == kStore || epilogue == kSilu, TRIDA_ERR_ARG,
-              "wsgemm_norm: the RMSNorm prologue takes the bf16 (0) or SwiGLU (2) epilogue");
-  TRIDA_CHECK(M >= 1 && M <= kMaxM && shape_ok(N, K, epilogue), TRIDA_ERR_ARG,
-              "wsgemm_norm: need 1 <= M <= %d, N %% 16 == 0, K %% 32 == 0 (M=%lld N=%lld K=%lld)", kMaxM, (long long)M,
-              (long long)N, (long long)K);
-  TRIDA_CHECK(x_row_stride >= K && x_row_stride % 8 == 0, TRIDA_ERR_ARG, "wsgemm_norm: bad X row stride");
-  TRIDA_CHECK(out_row_stride >= (epilogue == kSilu ? N / 2 : N) && out_row_stride % 4 == 0, TRIDA_ERR_ARG,
-              "wsgemm_norm: bad output row stride");
-  TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Wp | (uintptr_t)out) & 15) == 0 && ((uintptr_t)ss & 3) == 0,
-              TRIDA_ERR_ALIGN, "wsgemm_norm: X, Wp and out must be 16-byte aligned");
-  const Plan p = plan_for(N, K, epilogue);
-  TRIDA_CHECK(p.cfg >= 0 && ss_chunks((int)K) <= kMaxSsChunks, TRIDA_ERR_ARG, "wsgemm_norm: K too long for one workgroup");
-  WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T, ss,
-           eps};
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  if (epilogue == kStore) launch_cfg<kStore, true>(a, p, st);
-  else launch_cfg<kSilu, true>(a, p, st);
-  return launch_status("wsgemm_norm");
+  TRIDA_CHECK(ss, TRIDA_ERR_NULL, "wsgemm_norm: ss is required");
+  return ws_run("wsgemm_norm", X, x_row_stride, ss, eps, Wp, M, N, K, epilogue, out, out_row_stride, 0, stream);
+}
+
+extern "C" int trida_wsgemm_ex(const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp,
+                               int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride,
+                               int flags, void* stream) {
+  return ws_run("wsgemm_ex", X, x_row_stride, ss, eps, Wp, M, N, K, epilogue, out, out_row_stride, flags, stream);
+}
+
+extern "C" int64_t trida_ws_frag_elems(int64_t K) { return K > 0 && K % 32 == 0 ? K / 32 * kWsFragMT * 64 * 8 : 0; }
+
+extern "C" int trida_ws_frag(const uint16_t* X, int64_t x_row_stride, int64_t M, int64_t K, uint16_t* Xf, void* stream) {
+  TRIDA_CHECK(X && Xf, TRIDA_ERR_NULL, "ws_frag: X and Xf are required");
+  TRIDA_CHECK(M >= 1 && M <= kMaxM && K > 0 && K % 32 == 0 && K < INT32_MAX && x_row_stride >= K &&
+                  x_row_stride % 8 == 0,
+              TRIDA_ERR_ARG, "ws_frag: need 1 <= M <= %d, K %% 32 == 0", kMaxM);
+  TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Xf) & 15) == 0, TRIDA_ERR_ALIGN, "ws_frag: 16-byte aligned X and Xf");
+  hipLaunchKernelGGL(frag_kernel, dim3((unsigned)cdiv(M * (K / 8), 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), X, x_row_stride, (int)M, (int)K, Xf);
+  return launch_status("ws_frag");
 }
 
 extern "C" int64_t trida_residual_ss_chunks(int64_t dim) { return dim > 0 ? ss_chunks((int)dim) : 0; }
 
 extern "C" int trida_residual_parts(uint16_t* h, int64_t h_row_stride, const float* parts, int64_t n_parts,
                                     int64_t plane_stride, int64_t rows, int64_t dim, float* ss, void* stream) {
+  return trida_residual_parts_frag(h, h_row_stride, parts, n_parts, plane_stride, rows, dim, ss, nullptr, stream);
+}
+
+extern "C" int trida_residual_parts_frag(uint16_t* h, int64_t h_row_stride, const float* parts, int64_t n_parts,
+                                         int64_t plane_stride, int64_t rows, int64_t dim, float* ss, uint16_t* h_frag,
+                                         void* stream) {
   TRIDA_CHECK(h && ss && (parts || n_parts == 0), TRIDA_ERR_NULL, "residual_parts: h and ss (and parts) are required");
+  TRIDA_CHECK(!h_frag || (rows <= kMaxM && dim % 32 == 0 && ((uintptr_t)h_frag & 15) == 0), TRIDA_ERR_ARG,
+              "residual_parts: a fragment-order copy needs rows <= %d, dim %% 32 == 0 and 16-byte alignment", kMaxM);
   TRIDA_CHECK(rows > 0 && rows < INT32_MAX && dim > 0 && dim % 4 == 0 && dim < INT32_MAX && n_parts >= 0 &&
                   n_parts <= 64 && (n_parts == 0 || plane_stride >= rows * dim) && h_row_stride >= dim,
               TRIDA_ERR_ARG, "residual_parts: bad sizes (dim %% 4 == 0, 0 <= n_parts <= 64)");
   TRIDA_CHECK(((uintptr_t)h & 7) == 0 && h_row_stride % 4 == 0 && ((uintptr_t)parts & 15) == 0 && plane_stride % 4 == 0,
               TRIDA_ERR_ALIGN, "residual_parts: h rows 8-byte and parts 16-byte aligned");
   hipLaunchKernelGGL(residual_kernel, dim3((unsigned)rows, (unsigned)ss_chunks((int)dim)), dim3(kWave), 0,
-                     static_cast<hipStream_t>(stream), h, h_row_stride, parts, (int)n_parts, plane_stride, (int)dim, ss);
+                     static_cast<hipStream_t>(stream), h, h_row_stride, parts, (int)n_parts, plane_stride, (int)dim, ss,
+                     h_frag);
   return launch_status("residual_parts");
 }

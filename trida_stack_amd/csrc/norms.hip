@@ -167,7 +167,8 @@ __global__ __launch_bounds__(kThreads) void silu_mul_kernel(const uint16_t* gu, 
 
 // ------------------------------------------------------------------ gated rmsnorm (one wave per (row, head))
 // PER = Dv / 64 elements per lane, read as one vector per operand (o, gate, weight) before the reduction
-template <int PER>
+// FRAG: out in the weight-streaming GEMM's fragment order (rows <= 48, K = H * Dv)
+template <int PER, bool FRAG>
 __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t* o, const uint16_t* z,
                                                                  const uint16_t* w, uint16_t* out, int64_t rows,
                                                                  int H, int64_t z_st, float eps) {
@@ -206,7 +207,7 @@ __global__ __launch_bounds__(kThreads) void gated_rmsnorm_kernel(const uint16_t*
     const float nrm = bf2f(f2bf(v[j] * inv));  // normalised value in the input dtype, then weight and gate
     y[j] = f2bf(nrm * bf2f(wv[j]) * silu(bf2f(zv[j])));
   }
-  uint16_t* dst = out + (row * H + h) * Dv + l * PER;
+  uint16_t* dst = FRAG ? out + ws_frag_off((int)row, (int64_t)h * Dv + l * PER) : out + (row * H + h) * Dv + l * PER;
   if (PER == 4) *reinterpret_cast<u32x2*>(dst) = *reinterpret_cast<const u32x2*>(y);
   else if (PER == 2) *reinterpret_cast<uint32_t*>(dst) = *reinterpret_cast<const uint32_t*>(y);
   else dst[0] = y[0];
@@ -347,24 +348,47 @@ extern "C" int trida_silu_mul(const uint16_t* gu, uint16_t* out, int64_t rows, i
   return launch_status("silu_mul");
 }
 
-extern "C" int trida_gated_rmsnorm(const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out,
-                                   int64_t rows, int64_t H, int64_t Dv, int64_t z_st, float eps, void* stream) {
-  TRIDA_CHECK(o && z && w && out, TRIDA_ERR_NULL, "gated_rmsnorm: o, z, w and out are required");
+namespace {
+int gated_rmsnorm_run(const char* name, const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out,
+                      bool frag, int64_t rows, int64_t H, int64_t Dv, int64_t z_st, float eps, void* stream) {
+  TRIDA_CHECK(o && z && w && out, TRIDA_ERR_NULL, "%s: o, z, w and out are required", name);
   TRIDA_CHECK(rows > 0 && H > 0 && (Dv == 64 || Dv == 128 || Dv == 256) && z_st >= H * Dv, TRIDA_ERR_ARG,
-              "gated_rmsnorm: Dv must be 64, 128 or 256");
+              "%s: Dv must be 64, 128 or 256", name);
+  TRIDA_CHECK(!frag || (rows <= 48 && ((uintptr_t)out & 15) == 0), TRIDA_ERR_ARG,
+              "%s: the fragment order holds at most 48 rows (16-byte aligned)", name);
   const int64_t waves = rows * H;
   const dim3 grid((unsigned)cdiv(waves, kThreads / kWave));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t per = Dv / kWave;  // elements per lane, read as one vector of 2 * per bytes
   TRIDA_CHECK(((((uintptr_t)o) | (uintptr_t)z | (uintptr_t)w | (uintptr_t)out) & (2 * per - 1)) == 0 && z_st % per == 0,
-              TRIDA_ERR_ALIGN, "gated_rmsnorm: rows aligned to 2 * Dv / 64 bytes required");
-  if (Dv == 256)
-    hipLaunchKernelGGL(gated_rmsnorm_kernel<4>, grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H, z_st, eps);
-  else if (Dv == 128)
-    hipLaunchKernelGGL(gated_rmsnorm_kernel<2>, grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H, z_st, eps);
-  else
-    hipLaunchKernelGGL(gated_rmsnorm_kernel<1>, grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H, z_st, eps);
-  return launch_status("gated_rmsnorm");
+              TRIDA_ERR_ALIGN, "%s: rows aligned to 2 * Dv / 64 bytes required", name);
+#define TRIDA_GRN(PER)                                                                                              \
+  if (frag)                                                                                                         \
+    hipLaunchKernelGGL((gated_rmsnorm_kernel<PER, true>), grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H,  \
+                       z_st, eps);                                                                                  \
+  else                                                                                                              \
+    hipLaunchKernelGGL((gated_rmsnorm_kernel<PER, false>), grid, dim3(kThreads), 0, st, o, z, w, out, rows, (int)H, \
+                       z_st, eps);
+  if (Dv == 256) {
+    TRIDA_GRN(4)
+  } else if (Dv == 128) {
+    TRIDA_GRN(2)
+  } else {
+    TRIDA_GRN(1)
+  }
+#undef TRIDA_GRN
+  return launch_status(name);
+}
+}  // namespace
+
+extern "C" int trida_gated_rmsnorm(const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out,
+                                   int64_t rows, int64_t H, int64_t Dv, int64_t z_st, float eps, void* stream) {
+  return gated_rmsnorm_run("gated_rmsnorm", o, z, w, out, false, rows, H, Dv, z_st, eps, stream);
+}
+
+extern "C" int trida_gated_rmsnorm_frag(const uint16_t* o, const uint16_t* z, const uint16_t* w, uint16_t* out_frag,
+                                        int64_t rows, int64_t H, int64_t Dv, int64_t z_st, float eps, void* stream) {
+  return gated_rmsnorm_run("gated_rmsnorm_frag", o, z, w, out_frag, true, rows, H, Dv, z_st, eps, stream);
 }
 
 extern "C" int trida_attn_prep(const uint16_t* qkv, int64_t qkv_row_stride, const uint16_t* q_norm_w,

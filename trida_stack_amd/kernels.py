@@ -886,21 +886,94 @@ def ss_chunks(dim: int) -> int:
     return int(_lib.load().trida_residual_ss_chunks(dim))
 
 
-def residual_parts(h: torch.Tensor, parts: Optional[torch.Tensor], n_parts: int, ss: torch.Tensor) -> torch.Tensor:
+def residual_parts(h: torch.Tensor, parts: Optional[torch.Tensor], n_parts: int, ss: torch.Tensor,
+                   h_frag: Optional[torch.Tensor] = None) -> torch.Tensor:
     """h += bf16(sum of the first n_parts planes of parts) in place (bf16 residual stream [rows, dim], planes
     fp32 [>= n_parts, rows, dim] contiguous; n_parts = 0: h unchanged) and ss [rows, ss_chunks(dim)] fp32 = the
-    per-chunk sums of h^2 that ws_gemm_norm reads."""
-    dev = _need_gpu(h, parts, ss)
+    per-chunk sums of h^2 that ws_gemm_norm reads. h_frag: the updated h once more, in the fragment order
+    ws_gemm_frag reads (rows <= 48)."""
+    dev = _need_gpu(h, parts, ss, h_frag)
     rows, dim = h.shape
     if ss.dtype != torch.float32 or not ss.is_contiguous() or ss.numel() < rows * ss_chunks(dim):
         raise ValueError("residual_parts: ss must be contiguous fp32 [rows, ss_chunks(dim)]")
     if n_parts and (parts is None or parts.dtype != torch.float32 or not parts.is_contiguous()
                     or parts.numel() < n_parts * rows * dim):
         raise ValueError("residual_parts: parts must be contiguous fp32 holding n_parts x rows x dim")
-    rc = _lib.load().trida_residual_parts(h.data_ptr(), h.stride(0), _ptr(parts), n_parts, rows * dim, rows, dim,
-                                          ss.data_ptr(), _stream(dev))
+    if h_frag is not None:
+        _frag_buf(h_frag, dim, "h_frag")
+    rc = _lib.load().trida_residual_parts_frag(h.data_ptr(), h.stride(0), _ptr(parts), n_parts, rows * dim, rows,
+                                               dim, ss.data_ptr(), _ptr(h_frag), _stream(dev))
     _lib.check(rc, "trida_residual_parts")
     return h
+
+
+WS_X_FRAG, WS_OUT_FRAG = 1, 2
+
+
+def ws_frag_numel(Kd: int) -> int:
+    """bf16 elements of the fragment order of a weight-streaming GEMM's X with K = Kd columns (any M <= 48)."""
+    n = int(_lib.load().trida_ws_frag_elems(Kd))
+    if n <= 0:
+        raise ValueError("ws_frag_numel: K must be a positive multiple of 32")
+    return n
+
+
+def ws_frag(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """x [M, K] bf16 (M <= 48, contiguous rows) in the fragment order the weight-streaming GEMM reads with
+    x_frag (flat bf16, ws_frag_numel(K) elements; rows >= M left unwritten)."""
+    dev = _need_gpu(x, out)
+    _bf16(x, "x")
+    M, Kd = x.shape
+    if x.stride(1) != 1:
+        raise ValueError("ws_frag: x needs contiguous rows")
+    if out is None:
+        out = torch.empty(ws_frag_numel(Kd), dtype=torch.bfloat16, device=dev)
+    _frag_buf(out, Kd, "out")
+    rc = _lib.load().trida_ws_frag(x.data_ptr(), x.stride(0), M, Kd, out.data_ptr(), _stream(dev))
+    _lib.check(rc, "trida_ws_frag")
+    return out
+
+
+def _frag_buf(t: torch.Tensor, Kd: int, name: str) -> None:
+    _bf16(t, name)
+    if not t.is_contiguous() or t.numel() < ws_frag_numel(Kd):
+        raise ValueError(f"{name}: a fragment-order buffer needs {ws_frag_numel(Kd)} contiguous bf16 elements")
+
+
+def ws_gemm_frag(xf: torch.Tensor, M: int, wp: torch.Tensor, N: int, out: torch.Tensor, *,
+                 ss: Optional[torch.Tensor] = None, eps: float = 1e-6, epilogue: int = WS_STORE,
+                 out_frag: bool = False) -> torch.Tensor:
+    """ws_gemm (ss None) or ws_gemm_norm (ss given) of the M rows of X held in fragment order in xf
+    (ws_frag, or a producer's fragment-order output; K = wp.numel() // N). out_frag: the bf16 output of
+    WS_STORE / WS_SILU goes to out in fragment order (ws_frag_numel of the output width), the next GEMM's X.
+    Bitwise the row-major results."""
+    dev = _need_gpu(xf, wp, out, ss)
+    Kd = wp.numel() // N
+    _frag_buf(xf, Kd, "xf")
+    if not 1 <= M <= WS_MAX_M:
+        raise ValueError(f"ws_gemm_frag: need 1 <= M <= {WS_MAX_M}")
+    if ss is not None and (ss.dtype != torch.float32 or not ss.is_contiguous() or ss.numel() < M * ss_chunks(Kd)):
+        raise ValueError("ws_gemm_frag: ss must be contiguous fp32 [M, ss_chunks(K)]")
+    width = N // 2 if epilogue == WS_SILU else N
+    o_st = 0
+    if epilogue == WS_PARTS:
+        if out_frag:
+            raise ValueError("ws_gemm_frag: partial planes have no fragment order")
+        kg = ws_plan(N, Kd, epilogue)
+        if out.dtype != torch.float32 or not out.is_contiguous() or out.numel() < kg * M * N:
+            raise ValueError(f"ws_gemm_frag: partial planes need a contiguous fp32 out of >= {kg} x {M} x {N}")
+    elif out_frag:
+        _frag_buf(out, width, "out")
+    else:
+        _bf16(out, "out")
+        if out.dim() != 2 or out.shape[0] < M or out.shape[1] < width or out.stride(1) != 1:
+            raise ValueError(f"ws_gemm_frag: out must be [>= {M}, >= {width}] bf16 with contiguous rows")
+        o_st = out.stride(0)
+    flags = WS_X_FRAG | (WS_OUT_FRAG if out_frag else 0)
+    rc = _lib.load().trida_wsgemm_ex(xf.data_ptr(), 0, _ptr(ss), eps, wp.data_ptr(), M, N, Kd, epilogue,
+                                     out.data_ptr(), o_st, flags, _stream(dev))
+    _lib.check(rc, "trida_wsgemm_ex")
+    return out
 
 
 def ws_gemm_norm(h: torch.Tensor, ss: torch.Tensor, wp: torch.Tensor, N: int, out: torch.Tensor, *,
@@ -965,13 +1038,19 @@ def silu_mul(gu: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def gated_rmsnorm(o: torch.Tensor, z: torch.Tensor, w: torch.Tensor, out: torch.Tensor, *, eps: float = 1e-6):
+def gated_rmsnorm(o: torch.Tensor, z: torch.Tensor, w: torch.Tensor, out: torch.Tensor, *, eps: float = 1e-6,
+                  out_frag: bool = False):
     """Per value head: out = bf16(rmsnorm(o)) * w * silu(z). o, out [rows, H, Dv] contiguous bf16;
-    z [rows, >= H*Dv] bf16 with contiguous rows; w [Dv] bf16."""
+    z [rows, >= H*Dv] bf16 with contiguous rows; w [Dv] bf16. out_frag: out is instead a buffer for the
+    rows [rows, H * Dv] in the fragment order ws_gemm_frag reads (rows <= 48)."""
     dev = _need_gpu(o, z, w, out)
     rows, H, Dv = o.shape
-    rc = _lib.load().trida_gated_rmsnorm(o.data_ptr(), z.data_ptr(), w.data_ptr(), out.data_ptr(), rows, H, Dv,
-                                         z.stride(0), eps, _stream(dev))
+    if out_frag:
+        _frag_buf(out, H * Dv, "out")
+        fn = _lib.load().trida_gated_rmsnorm_frag
+    else:
+        fn = _lib.load().trida_gated_rmsnorm
+    rc = fn(o.data_ptr(), z.data_ptr(), w.data_ptr(), out.data_ptr(), rows, H, Dv, z.stride(0), eps, _stream(dev))
     _lib.check(rc, "trida_gated_rmsnorm")
     return out
 

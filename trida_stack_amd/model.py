@@ -226,6 +226,12 @@ class _Scratch:
         # split-K partial planes of the weight-streaming GEMM ([kg, N, hidden] fp32), when it runs here
         self.parts = torch.empty(max(1, ws_parts) * N * h, **f32) if ws_parts else None
         self.ss = torch.empty(N, (h + 255) // 256, **f32) if ws_parts else None  # per-chunk sums of h^2
+        # the fused forward's GEMM inputs in the weight-streaming GEMM's fragment order (h, the SwiGLU
+        # output, the gated-norm output), written by their producers
+        frag = ws_parts and N <= K.WS_MAX_M
+        self.hf = torch.empty(K.ws_frag_numel(h), **bf) if frag else None
+        self.actf = torch.empty(K.ws_frag_numel(cfg.intermediate), **bf) if frag else None
+        self.ynf = torch.empty(K.ws_frag_numel(cfg.lin_v_heads * cfg.lin_v_dim), **bf) if frag else None
 
 
 class TridaRuntime:
@@ -377,8 +383,10 @@ class TridaRuntime:
                 return torch.matmul(x, w.t())
             return torch.matmul(x, w.t(), out=out)
 
-    def _proj(self, s: "_Scratch", key: str, x: torch.Tensor, x_p: torch.Tensor, out_p: torch.Tensor):
-        """One decoder projection of the N = B * T rows in x (x_p: the padded rows hipBLASLt reads).
+    def _proj(self, s: "_Scratch", key: str, x: torch.Tensor, x_p: torch.Tensor, out_p: torch.Tensor,
+              xf: Optional[torch.Tensor] = None):
+        """One decoder projection of the N = B * T rows in x (x_p: the padded rows hipBLASLt reads; xf: the
+        same rows in the weight-streaming GEMM's fragment order, when their producer wrote it).
         Returns the pending residual for add_norm when the projection feeds one (("parts", planes) from
         the weight-streaming GEMM, ("bf16", rows) from hipBLASLt), else None (output in out_p's rows)."""
         ws = self.ws.get(key) if s.N <= K.WS_MAX_M else None
@@ -388,26 +396,33 @@ class TridaRuntime:
         wp, N, role, kg = ws
         with K.timed("ws_gemm"):
             if role == K.WS_PARTS:
-                K.ws_gemm(x, wp, N, s.parts, epilogue=role)
+                if xf is not None:
+                    K.ws_gemm_frag(xf, s.N, wp, N, s.parts, epilogue=role)
+                else:
+                    K.ws_gemm(x, wp, N, s.parts, epilogue=role)
                 return ("parts", kg)
             K.ws_gemm(x, wp, N, out_p, epilogue=role)
         return None
 
     def _proj_normed(self, s: "_Scratch", key: str, out_p: torch.Tensor, fused: bool) -> None:
         """A projection of the normed hidden rows: with `fused`, rmsnorm(h) inside the weight-streaming GEMM
-        (the norm weight is in the weight copy's columns; bf16 or SwiGLU epilogue into out_p's rows);
-        otherwise of x, which add_norm already normed."""
+        over h in fragment order (the norm weight is in the weight copy's columns; bf16 epilogue into out_p's
+        rows, or the SwiGLU epilogue into s.actf in fragment order for the down projection); otherwise of x,
+        which add_norm already normed."""
         if not fused:
             self._proj(s, key, s.x, s.x_p, out_p)
             return
         wp, N, role, _ = self.ws[key]
         with K.timed("ws_gemm"):
-            K.ws_gemm_norm(s.h, s.ss, wp, N, out_p, eps=self.cfg.rms_eps, epilogue=role)
+            if role == K.WS_SILU:
+                K.ws_gemm_frag(s.hf, s.N, wp, N, s.actf, ss=s.ss, eps=self.cfg.rms_eps, epilogue=role, out_frag=True)
+            else:
+                K.ws_gemm_frag(s.hf, s.N, wp, N, out_p, ss=s.ss, eps=self.cfg.rms_eps, epilogue=role)
 
     def _residual(self, s: "_Scratch", pending) -> None:
         """h += the partial planes of the projection just run, and the sums of squares for the next norm."""
         with K.timed("residual"):
-            K.residual_parts(s.h, s.parts, pending[1], s.ss)
+            K.residual_parts(s.h, s.parts, pending[1], s.ss, h_frag=s.hf)
 
     def _ws_silu(self, s: "_Scratch", p: str) -> bool:
         """True when the gate/up projection of layer prefix p runs with the SwiGLU epilogue here."""
@@ -456,7 +471,7 @@ class TridaRuntime:
         fused = self.ws_fused and N <= K.WS_MAX_M
         if fused:
             with K.timed("residual"):
-                K.residual_parts(s.h, None, 0, s.ss)
+                K.residual_parts(s.h, None, 0, s.ss, h_frag=s.hf)
         pending = None  # the residual branch not yet added to h
         for i in range(c.n_layers):
             p = f"l{i}."
@@ -514,8 +529,13 @@ class TridaRuntime:
                 if persist:
                     window[j].copy_(s.win_tmp)
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
-                K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
-                pending = self._proj(s, p + "w_out", s.yn_p[:N], s.yn_p, s.r_p)
+                if fused:  # straight into the out projection's fragment-order X
+                    K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.ynf,
+                                    eps=c.rms_eps, out_frag=True)
+                    pending = self._proj(s, p + "w_out", s.yn_p[:N], s.yn_p, s.r_p, xf=s.ynf)
+                else:
+                    K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.yn, eps=c.rms_eps)
+                    pending = self._proj(s, p + "w_out", s.yn_p[:N], s.yn_p, s.r_p)
             if fused:
                 self._residual(s, pending)
                 self._proj_normed(s, p + "w_gu", s.act_p, fused)
@@ -523,7 +543,7 @@ class TridaRuntime:
                 self._add_norm(s, pending, w[p + "post_norm"])
                 if self._proj(s, p + "w_gu", s.x, s.x_p, s.act_p if self._ws_silu(s, p) else s.gu_p) is not None:
                     K.silu_mul(s.gu, s.act)
-            pending = self._proj(s, p + "w_down", s.act, s.act_p, s.r_p)
+            pending = self._proj(s, p + "w_down", s.act, s.act_p, s.r_p, xf=s.actf if fused else None)
             if fused:
                 self._residual(s, pending)
                 pending = None
