@@ -382,7 +382,72 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   };
   for (int t0 = 0; t0 < a.T; t0 += tcn) {
     const int tn = min(tcn, a.T - t0);
-    if constexpr (!PREP) {
+    if constexpr (F32) {
+      __syncthreads();  // previous chunk fully consumed (its readout rows stored)
+      // stage the chunk through registers in one round trip (clamped, unconditional loads): q * scale and
+      // k converted to fp32 once, the v tile, g and beta; with KPL = 8 the thread holding piece j of a row
+      // also forms lane j's share of k . (q * scale) -- the slice and fma order of the separate pass below
+      // -- and its 16-lane group (the row's 16 pieces) reduces it with the same row16_sum
+      constexpr int NT = NW * kWave;
+      constexpr int PPR = Dk / 8;  // 16-byte pieces per q / k row
+      constexpr int QIT = (TC * PPR + NT - 1) / NT;
+      constexpr int VW = VPB / 2;  // 4-byte pieces per v tile row
+      constexpr int VIT = (TC * VW + NT - 1) / NT;
+      const int nq = tn * PPR, nv = tn * VW;
+      const uint16_t* qc = qb + (int64_t)t0 * qk_row;
+      const uint16_t* kc = kb + (int64_t)t0 * qk_row;
+      const uint16_t* vc = vb + (int64_t)t0 * v_row;
+      u32x4 qr[QIT], kr[QIT];
+      uint32_t vr[VIT];
+#pragma unroll
+      for (int it = 0; it < QIT; ++it) {
+        const int i = min(tid + it * NT, nq - 1);
+        const int off = (i / PPR) * (int)qk_row + (i % PPR) * 8;
+        qr[it] = *reinterpret_cast<const u32x4*>(qc + off);
+        kr[it] = *reinterpret_cast<const u32x4*>(kc + off);
+      }
+#pragma unroll
+      for (int it = 0; it < VIT; ++it) {
+        const int i = min(tid + it * NT, nv - 1);
+        vr[it] = *reinterpret_cast<const uint32_t*>(vc + (i / VW) * (int)v_row + (i % VW) * 2);
+      }
+      const int tr = min(tid, tn - 1);
+      const float gv = gb[(int64_t)(t0 + tr) * a.Hv], bv = bb[(int64_t)(t0 + tr) * a.Hv];
+      if (tid < tn) {
+        s_g[tid] = __expf(gv);
+        s_b[tid] = bv;
+      }
+#pragma unroll
+      for (int it = 0; it < VIT; ++it) {
+        const int i = tid + it * NT;
+        if (i < nv) *reinterpret_cast<uint32_t*>(&s_v[i / VW][(i % VW) * 2]) = vr[it];
+      }
+#pragma unroll
+      for (int it = 0; it < QIT; ++it) {
+        const int i = tid + it * NT;
+        if (i < nq) {  // whole rows: uniform over each 16-lane group
+          const int row = i / PPR, pc = i % PPR;
+          float qf[8], kf[8];
+          unpack8(qr[it], qf);
+          unpack8(kr[it], kf);
+          float kq = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            qf[j] *= a.scale;
+            kq = fmaf(kf[j], qf[j], kq);
+          }
+          *reinterpret_cast<f32x4*>(&s_qf32[row][pc * 8]) = f32x4{qf[0], qf[1], qf[2], qf[3]};
+          *reinterpret_cast<f32x4*>(&s_qf32[row][pc * 8 + 4]) = f32x4{qf[4], qf[5], qf[6], qf[7]};
+          *reinterpret_cast<f32x4*>(&s_kf32[row][pc * 8]) = f32x4{kf[0], kf[1], kf[2], kf[3]};
+          *reinterpret_cast<f32x4*>(&s_kf32[row][pc * 8 + 4]) = f32x4{kf[4], kf[5], kf[6], kf[7]};
+          if constexpr (KPL == 8) {
+            kq = row16_sum(kq);
+            if (pc == 0) s_kq[row] = kq;
+          }
+        }
+      }
+      __syncthreads();
+    } else if constexpr (!PREP) {
     __syncthreads();  // previous chunk fully consumed
     // stage q, k rows (16-byte pieces) and the v tile straight to LDS, g and beta through registers
     // (tn <= kTC <= block size: one row per thread), all in one round trip
@@ -407,27 +472,22 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       s_b[tid] = bv;
     }
     __syncthreads();
-    if constexpr (F32) {
-      for (int e = tid; e < tn * Dk; e += NW * kWave) {
-        s_qf32[e / Dk][e % Dk] = bf2f(s_q[e / Dk][e % Dk]) * a.scale;
-        s_kf32[e / Dk][e % Dk] = bf2f(s_k[e / Dk][e % Dk]);
+    }
+    if constexpr (!F32 || KPL != 8) {
+      // k . (q * scale) of every staged row, once per block instead of once per value column: each
+      // 16-lane group takes a row, lane j the same KPL-element slice and fma order as the column lanes'
+      // row step, then the same row16_sum, so the value is the one a row step would compute itself
+      for (int rr = tid / kLanesPerV; rr < tn; rr += NW * kVPerWave) {  // uniform within a 16-lane group
+        const int j = tid % kLanesPerV;
+        float kq = 0.f;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i)
+          kq = fmaf(kval(rr, j * KPL + i), qval(rr, j * KPL + i), kq);
+        kq = row16_sum(kq);
+        if (j == 0) s_kq[rr] = kq;
       }
       __syncthreads();
     }
-    }
-    // k . (q * scale) of every staged row, once per block instead of once per value column: each
-    // 16-lane group takes a row, lane j the same KPL-element slice and fma order as the column lanes'
-    // row step, then the same row16_sum, so the value is the one a row step would compute itself
-    for (int rr = tid / kLanesPerV; rr < tn; rr += NW * kVPerWave) {  // uniform within a 16-lane group
-      const int j = tid % kLanesPerV;
-      float kq = 0.f;
-#pragma unroll
-      for (int i = 0; i < KPL; ++i)
-        kq = fmaf(kval(rr, j * KPL + i), qval(rr, j * KPL + i), kq);
-      kq = row16_sum(kq);
-      if (j == 0) s_kq[rr] = kq;
-    }
-    __syncthreads();
     if (a.bidir > 0) {
       // each block: a backward sub-scan from the block-entry state (a register copy), then the causal
       // forward sub-scan; a row reads out the mean of the two
@@ -447,26 +507,43 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       }
       continue;
     }
-    // the next row's operands are read from LDS while the current row computes (two register sets,
-    // unconditional reads of a clamped row, so the waits are the same on every path)
-    auto emit = [&](int r, float o) {
-      const int t = t0 + r;
-      if (t < nc && kl == 0) ob[(int64_t)t * v_row] = f2bf(o);
-      if (t == nc - 1 && a.state_clean) {
-#pragma unroll
-        for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = s[i];
+    // rows [r0, r1) of the chunk; the next row's operands are read from LDS while the current row computes
+    // (two register sets, unconditional reads of a clamped row, so the waits are the same on every path).
+    // A row's readout: F32 keeps it in LDS (every lane of a column holds the same reduced value) and the
+    // block stores the chunk's rows together; otherwise lane 0 of the column stores it
+    auto run = [&](int r0, int r1, bool keep) {
+      if (r0 >= r1) return;
+      auto put = [&](int r, float o) {
+        if constexpr (F32) {
+          if (keep) s_ob[r][vl] = o;
+        } else {
+          if (keep && kl == 0) ob[(int64_t)(t0 + r) * v_row] = f2bf(o);
+        }
+      };
+      Row ra, rb;
+      fetch(ra, r0);
+      int r = r0;
+      for (; r + 1 < r1; r += 2) {
+        fetch(rb, r + 1);
+        put(r, apply(s, ra));
+        fetch(ra, min(r + 2, r1 - 1));
+        put(r + 1, apply(s, rb));
       }
+      if (r < r1) put(r, apply(s, ra));
     };
-    Row ra, rb;
-    fetch(ra, 0);
-    int r = 0;
-    for (; r + 1 < tn; r += 2) {
-      fetch(rb, r + 1);
-      emit(r, apply(s, ra));
-      fetch(ra, min(r + 2, tn - 1));
-      emit(r + 1, apply(s, rb));
+    const int rc = min(max(nc - t0, 0), tn);  // the chunk's rows t < nc, whose readout is kept
+    run(0, rc, true);
+    if (a.state_clean && rc > 0 && t0 + rc == nc) {  // the state after the last clean row
+#pragma unroll
+      for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = s[i];
     }
-    if (r < tn) emit(r, apply(s, ra));
+    run(rc, tn, false);
+    if constexpr (F32) {
+      __syncthreads();
+      uint16_t* otile = a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + vt * VPB;
+      for (int e = tid; e < rc * VPB; e += NW * kWave)
+        otile[(int64_t)(t0 + e / VPB) * v_row + e % VPB] = f2bf(s_ob[e / VPB][e % VPB]);
+    }
   }
   if (nc == 0 && a.state_clean) {
 #pragma unroll
