@@ -2,7 +2,9 @@
 // into q / k / v, l2norm of q and k per head, and the gates g = -exp(A_log) softplus(a + dt_bias),
 // beta = sigmoid(b).
 //
-// Launch: one 256-thread block per (sequence, row). A thread owns 8 consecutive channels (one 16-byte
+// Launch: a grid of (sequence, row) x 128-piece channel slices (the C = conv_dim channels of a row spread
+// over several CUs: at batch 1 a row per block would leave most of the GPU idle while each block pulls
+// its 4 source rows and the whole conv weight). A thread owns 8 consecutive channels (one 16-byte
 // piece); the Dk/8 threads of a q or k head reduce its sum of squares with a row-local reduction.
 // Rounding follows the CPU oracle: conv and SiLU in fp32, rounded to bf16, then l2norm in fp32 of the
 // rounded values, rounded to bf16 again.
@@ -11,7 +13,7 @@
 namespace trida {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 128;  // channel pieces (8 channels each) per block
 constexpr int kMaxKc = 4;
 
 template <int CTRL>
@@ -75,8 +77,6 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); 
 // torch.nn.functional.softplus with beta 1 and threshold 20
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-constexpr int kMaxPasses = 4;  // channel pieces of 8 per thread: C <= 8 * 256 * 4 = 8192
-
 template <int GW, int KC>  // lanes per q/k head = Dk / 8; conv width
 __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
   const int t = blockIdx.x % a.T;
@@ -84,107 +84,94 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
   const int tid = threadIdx.x;
   const int key_dim = a.Hk * a.Dk;
   const int pieces = a.C / 8;
+  const int p0 = blockIdx.y * kThreads;  // the block's first piece: a multiple of GW
+  const int p = p0 + tid;
+  const bool live = p < pieces;
+  const int c = min(p, pieces - 1) * 8;  // lanes past the last piece compute on it and store nothing
   const uint16_t* xb = a.x + (int64_t)b * a.x_sb;
   const uint16_t* wb = a.window + (int64_t)b * (a.Kc - 1) * a.C;
 
-  // every load of the block first (one memory round trip): per pass, the KC source rows of the thread's
-  // 8 channels and their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces), and the
-  // gate inputs
-  u32x4 xs[kMaxPasses][KC], wsv[kMaxPasses][KC];
+  // every load of the block first (one memory round trip, unconditional): the KC source rows of the
+  // thread's 8 channels, their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces), and
+  // the gate inputs
+  u32x4 xs[KC], wsv[KC];
 #pragma unroll
-  for (int ps = 0; ps < kMaxPasses; ++ps) {
-    const int p = ps * kThreads + tid;
-    if (p < pieces) {
-      const int c = p * 8;
-#pragma unroll
-      for (int j = 0; j < KC; ++j) {
-        const int tau = t - (KC - 1) + j;  // source row; negative rows come from the window
-        const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(KC - 1 + tau) * a.C + c;
-        xs[ps][j] = *reinterpret_cast<const u32x4*>(src);
-        wsv[ps][j] = reinterpret_cast<const u32x4*>(a.conv_w + (int64_t)c * KC)[j];
-      }
-    }
+  for (int j = 0; j < KC; ++j) {
+    const int tau = t - (KC - 1) + j;  // source row; negative rows come from the window
+    const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(KC - 1 + tau) * a.C + c;
+    xs[j] = *reinterpret_cast<const u32x4*>(src);
+    wsv[j] = reinterpret_cast<const u32x4*>(a.conv_w + (int64_t)c * KC)[j];
+  }
+  const bool gates = blockIdx.y == 0;  // block-uniform
+  const int hg = min(tid, a.Hv - 1);
+  float av = 0.f, bv = 0.f;
+  if (gates) {
+    av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hg]);
+    bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hg]);
   }
   // the pre-conv rows a rollback rebuilds the window from: the block's own row is its last source row
-  if (a.pre_out) {
-#pragma unroll
-    for (int ps = 0; ps < kMaxPasses; ++ps) {
-      const int p = ps * kThreads + tid;
-      if (p < pieces)
-        *reinterpret_cast<u32x4*>(a.pre_out + ((int64_t)b * a.T + t) * a.C + p * 8) = xs[ps][KC - 1];
-    }
-  }
-  float av = 0.f, bv = 0.f;
-  if (tid < a.Hv) {
-    av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
-    bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + tid]);
-  }
+  if (a.pre_out && live) *reinterpret_cast<u32x4*>(a.pre_out + ((int64_t)b * a.T + t) * a.C + c) = xs[KC - 1];
 
-  // the q/k pieces come first (2 * key_dim / 8 of them, a multiple of GW), so every group of GW
-  // lanes of one pass belongs to one head and the whole group is active together
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  {
+    float w[8][KC];
 #pragma unroll
-  for (int ps = 0; ps < kMaxPasses; ++ps) {
-    const int p0 = ps * kThreads;
-    if (p0 >= pieces) break;  // uniform
-    const int p = p0 + tid;
-    const bool live = p < pieces;
-    const int c = (live ? p : 0) * 8;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (live) {
-      float w[8][KC];
-#pragma unroll
-      for (int ch = 0; ch < 8; ++ch)
-#pragma unroll
-        for (int j = 0; j < KC; ++j) {
-          const int e = ch * KC + j;  // element of the 8 x KC weight block
-          const uint32_t word = wsv[ps][e / 8][(e % 8) / 2];
-          w[ch][j] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
-        }
+    for (int ch = 0; ch < 8; ++ch)
 #pragma unroll
       for (int j = 0; j < KC; ++j) {
-        float f[8];
-        unpack8(xs[ps][j], f);
-#pragma unroll
-        for (int ch = 0; ch < 8; ++ch) acc[ch] = fmaf(w[ch][j], f[ch], acc[ch]);
+        const int e = ch * KC + j;  // element of the 8 x KC weight block
+        const uint32_t word = wsv[e / 8][(e % 8) / 2];
+        w[ch][j] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
       }
 #pragma unroll
-      for (int ch = 0; ch < 8; ++ch) acc[ch] = bf2f(f2bf(silu(acc[ch])));
+    for (int j = 0; j < KC; ++j) {
+      float f[8];
+      unpack8(xs[j], f);
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) acc[ch] = fmaf(w[ch][j], f[ch], acc[ch]);
     }
+#pragma unroll
+    for (int ch = 0; ch < 8; ++ch) acc[ch] = bf2f(f2bf(silu(acc[ch])));
+  }
+  // the q/k pieces come first (2 * key_dim / 8 of them, a multiple of GW) and are all live, so every
+  // group of GW lanes belongs to one head
+  if (p0 < 2 * key_dim / 8) {  // block-uniform: per-head l2norm (all lanes take part in the reduction)
     const bool is_qk = c < 2 * key_dim;  // uniform across a GW-lane group
-    if (p0 < 2 * key_dim / 8) {
-      // this pass may hold q/k pieces: per-head l2norm (all lanes take part in the reduction)
-      float ss = 0.f;
+    float ss = 0.f;
 #pragma unroll
-      for (int ch = 0; ch < 8; ++ch) ss = fmaf(acc[ch], acc[ch], ss);
-      ss = lane_group_sum<GW>(ss);
-      if (live && is_qk) {
-        const float inv = rsqrtf(ss + 1e-6f);
+    for (int ch = 0; ch < 8; ++ch) ss = fmaf(acc[ch], acc[ch], ss);
+    ss = lane_group_sum<GW>(ss);
+    if (is_qk) {
+      const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
-        for (int ch = 0; ch < 8; ++ch) acc[ch] *= inv;
+      for (int ch = 0; ch < 8; ++ch) acc[ch] *= inv;
+    }
+  }
+  if (live) {
+    const u32x4 w = pack8(acc);
+    const int64_t row = (int64_t)b * a.T + t;
+    if (c < key_dim)
+      *reinterpret_cast<u32x4*>(a.q + row * key_dim + c) = w;
+    else if (c < 2 * key_dim)
+      *reinterpret_cast<u32x4*>(a.k + row * key_dim + (c - key_dim)) = w;
+    else
+      *reinterpret_cast<u32x4*>(a.v + row * (int64_t)a.Hv * a.Dv + (c - 2 * key_dim)) = w;
+  }
+  if (gates) {
+    for (int hh = tid; hh < a.Hv; hh += kThreads) {
+      if (hh != tid) {  // more heads than threads: the later ones load their own inputs
+        av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hh]);
+        bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hh]);
       }
-    }
-    if (live) {
-      const u32x4 w = pack8(acc);
-      const int64_t row = (int64_t)b * a.T + t;
-      if (c < key_dim)
-        *reinterpret_cast<u32x4*>(a.q + row * key_dim + c) = w;
-      else if (c < 2 * key_dim)
-        *reinterpret_cast<u32x4*>(a.k + row * key_dim + (c - key_dim)) = w;
-      else
-        *reinterpret_cast<u32x4*>(a.v + row * (int64_t)a.Hv * a.Dv + (c - 2 * key_dim)) = w;
+      const int64_t o = ((int64_t)b * a.T + t) * a.Hv + hh;
+      a.g[o] = -__expf(a.A_log[hh]) * softplus(av + a.dt_bias[hh]);
+      a.beta[o] = 1.f / (1.f + __expf(-bv));
     }
   }
 
-  if (tid < a.Hv) {
-    const int64_t o = ((int64_t)b * a.T + t) * a.Hv + tid;
-    a.g[o] = -__expf(a.A_log[tid]) * softplus(av + a.dt_bias[tid]);
-    a.beta[o] = 1.f / (1.f + __expf(-bv));
-  }
-
-  // the new conv window (last Kc-1 rows of [window ++ x]) is written by the last row's block
-  if (a.window_out && t == a.T - 1) {
-    for (int p = tid; p < (a.Kc - 1) * pieces; p += kThreads) {
-      const int wr = p / pieces, c = (p % pieces) * 8;
+  // the new conv window (last Kc-1 rows of [window ++ x]): the last row's blocks, each its own pieces
+  if (a.window_out && t == a.T - 1 && live) {
+    for (int wr = 0; wr < a.Kc - 1; ++wr) {
       const int tau = a.T - (a.Kc - 1) + wr;
       const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(a.Kc - 1 + tau) * a.C + c;
       *reinterpret_cast<u32x4*>(a.window_out + ((int64_t)b * (a.Kc - 1) + wr) * a.C + c) =
@@ -210,13 +197,11 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
               "gdn_prep: bad sizes B=%lld T=%lld Hk=%lld Hv=%lld Kc=%lld", (long long)B, (long long)T,
               (long long)Hk, (long long)Hv, (long long)Kc);
   TRIDA_CHECK(Dk == 32 || Dk == 64 || Dk == 128, TRIDA_ERR_ARG, "gdn_prep: Dk must be 32, 64 or 128");
-  TRIDA_CHECK(Dv % 8 == 0 && Hv <= kThreads, TRIDA_ERR_ARG, "gdn_prep: Dv % 8 == 0 and Hv <= 256 required");
+  TRIDA_CHECK(Dv % 8 == 0, TRIDA_ERR_ARG, "gdn_prep: Dv %% 8 == 0 required");
   const int64_t C = 2 * Hk * Dk + Hv * Dv;
   TRIDA_CHECK(x_st % 8 == 0 && x_sb % 8 == 0 && ((uintptr_t)x & 15) == 0 && ((uintptr_t)window & 15) == 0,
               TRIDA_ERR_ALIGN, "gdn_prep: x / window must be 16-byte aligned with strides in multiples of 8");
   TRIDA_CHECK(x_st >= C, TRIDA_ERR_ARG, "gdn_prep: row stride of x smaller than conv_dim");
-  TRIDA_CHECK(C <= 8 * kThreads * kMaxPasses, TRIDA_ERR_ARG, "gdn_prep: conv_dim %lld above %d", (long long)C,
-              8 * kThreads * kMaxPasses);
   TRIDA_CHECK(((uintptr_t)conv_w & 15) == 0, TRIDA_ERR_ALIGN, "gdn_prep: conv_w must be 16-byte aligned");
   TRIDA_CHECK(window_out == nullptr || window_out != window, TRIDA_ERR_ARG,
               "gdn_prep: window_out must not alias window");
@@ -226,7 +211,7 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
   PrepArgs a{x, window, conv_w, a_in, b_in, A_log, dt_bias, q, k, v, g, beta, window_out, pre_out,
              (int)T, (int)C, (int)Kc, (int)Hk, (int)Hv, (int)Dk, (int)Dv, x_sb, x_st, ab_sb, ab_st};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)(B * T));
+  const dim3 grid((unsigned)(B * T), (unsigned)cdiv(C / 8, kThreads));
 #define TRIDA_PREP_LAUNCH(GW)                                                                   \
   switch (Kc) {                                                                                 \
     case 2: hipLaunchKernelGGL((gdn_prep_kernel<GW, 2>), grid, dim3(kThreads), 0, st, a); break; \
