@@ -35,20 +35,32 @@ __device__ __forceinline__ float dpp(float x) {
   // update_dpp with a defined old value and bound_ctrl: folds into the consuming add / max
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
-__device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp<0x128>(v));
-  v = fmaxf(v, dpp<0x124>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0xB1>(v));
-  return v;
+
+// four independent 16-lane row reductions (max or sum over each DPP row; every lane of a row receives
+// its total), interleaved so the DPP latencies overlap
+__device__ __forceinline__ void row16_max4(float (&v)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0x128>(v[i]));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0x124>(v[i]));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0x4E>(v[i]));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0xB1>(v[i]));
 }
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp<0x128>(v);
-  v += dpp<0x124>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0xB1>(v);
-  return v;
+__device__ __forceinline__ void row16_sum4(float (&v)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] += dpp<0x128>(v[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] += dpp<0x124>(v[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] += dpp<0x4E>(v[i]);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] += dpp<0xB1>(v[i]);
 }
+// 2^x with the hardware instruction: exact for the softmax's arguments x <= 0 down to -126, 0 below
+// (where the library exp2f would return a denormal)
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
 
@@ -160,26 +172,6 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   const uint16_t* kh = a.k_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
   const uint16_t* vh = a.v_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
 
-  // ---- the tile's Q rows into LDS (padding rows zero); read back as A fragments every step. Every
-  // load of the tile is issued before the first store, so the staging costs one memory latency.
-  {
-    constexpr int QPT = kMT * GPR / NT;  // 16-byte pieces per thread
-    u32x4 qv[QPT];
-#pragma unroll
-    for (int j = 0; j < QPT; ++j) {
-      const int gi = tid + j * NT;
-      const int r = gi / GPR, grp = gi % GPR;
-      const int m = m0 + min(r, rows - 1), t = m / a.G, g = m % a.G;
-      qv[j] = *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + grp * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < QPT; ++j) {
-      const int gi = tid + j * NT;
-      const int r = gi / GPR, grp = gi % GPR;
-      *reinterpret_cast<u32x4*>(&sQ[k_off<D>(r, grp)]) = r < rows ? qv[j] : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-
   // ---- prefetch registers: K groups (coalesced rows) and one V piece (8 keys x 4 columns)
   u32x4 kreg[NKG];
   u32x2 vreg[8];
@@ -200,6 +192,29 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
       }
     }
   };
+  // the first step's K / V loads go out with the Q loads: one memory latency for both
+  load_step(kb0);
+
+  // ---- the tile's Q rows into LDS (padding rows zero); read back as A fragments every step. Every
+  // load of the tile is issued before the first store, so the staging costs one memory latency.
+  {
+    constexpr int QPT = kMT * GPR / NT;  // 16-byte pieces per thread
+    u32x4 qv[QPT];
+#pragma unroll
+    for (int j = 0; j < QPT; ++j) {
+      const int gi = tid + j * NT;
+      const int r = gi / GPR, grp = gi % GPR;
+      const int m = m0 + min(r, rows - 1), t = m / a.G, g = m % a.G;
+      qv[j] = *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + grp * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < QPT; ++j) {
+      const int gi = tid + j * NT;
+      const int r = gi / GPR, grp = gi % GPR;
+      *reinterpret_cast<u32x4*>(&sQ[k_off<D>(r, grp)]) = r < rows ? qv[j] : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
   auto stage_step = [&]() {
 #pragma unroll
     for (int j = 0; j < NKG; ++j) {
@@ -242,7 +257,6 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     klim[i] = all ? nk : min(nk, prefix + t + 1);
   }
 
-  load_step(kb0);
   for (int kb = kb0; kb < kb1; ++kb) {
     const int key0 = kb * kKB;
     __syncthreads();  // the previous step's tiles are consumed
@@ -266,41 +280,52 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
         sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf, kf, sacc[kt], 0, 0, 0);
       }
     }
-    // ---- mask, scale, online softmax (rows (l/16)*4+i; a row's keys across 16 lanes x 4 tiles)
-    const bool edge = key0 + kKB > prefix || key0 + kKB > nk;  // block keys or the cache end
-    float alpha[4];
-    bool moved = false;
+    // ---- mask, scale, online softmax (rows (l/16)*4+i; a row's keys across 16 lanes x 4 tiles). The
+    // mask applies only on steps that reach the block keys or the cache end (uniform)
+    const bool edge = key0 + kKB > prefix || key0 + kKB > nk;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = (l / 16) * 4 + i;  // row within the wave
-      float mx = -INFINITY;
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sacc[kt][i] *= a.scale_log2;
+    if (edge) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         const int key = key0 + kt * 16 + (l % 16);
-        float v = sacc[kt][i] * a.scale_log2;
-        if (edge) v = key < klim[i] ? v : -INFINITY;
-        sacc[kt][i] = v;
-        mx = fmaxf(mx, v);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sacc[kt][i] = key < klim[i] ? sacc[kt][i] : -INFINITY;
       }
-      mx = row16_max(mx);
-      const float m_new = fmaxf(m_run[i], mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      alpha[i] = exp2f(m_run[i] - m_use);
+    }
+    float mx[4], alpha[4], m_use[4], ps[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx[i] = fmaxf(fmaxf(sacc[0][i], sacc[1][i]), fmaxf(sacc[2][i], sacc[3][i]));
+    row16_max4(mx);
+    bool moved = false;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float m_new = fmaxf(m_run[i], mx[i]);
+      m_use[i] = m_new == -INFINITY ? 0.f : m_new;
+      alpha[i] = exp2_hw(m_run[i] - m_use[i]);
       moved |= alpha[i] != 1.f;
-      float ps = 0.f;
+      m_run[i] = m_new;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = (l / 16) * 4 + i;  // row within the wave
+      ps[i] = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 4; kt += 2) {  // two key tiles per packed conversion
-        const float p0 = exp2f(sacc[kt][i] - m_use), p1 = exp2f(sacc[kt + 1][i] - m_use);
-        ps += p0;
-        ps += p1;
+        const float p0 = exp2_hw(sacc[kt][i] - m_use[i]), p1 = exp2_hw(sacc[kt + 1][i] - m_use[i]);
+        ps[i] += p0;
+        ps[i] += p1;
         const uint32_t w2 = f2bf2(p0, p1);
         const int k0 = kt * 16 + (l % 16), k1 = k0 + 16;
         pw[p_off(rr, k0 >> 3) + (k0 & 7)] = (uint16_t)w2;
         pw[p_off(rr, k1 >> 3) + (k1 & 7)] = (uint16_t)(w2 >> 16);
       }
-      l_run[i] = l_run[i] * alpha[i] + row16_sum(ps);
-      m_run[i] = m_new;
     }
+    row16_sum4(ps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) l_run[i] = l_run[i] * alpha[i] + ps[i];
     // rescale O only when some row's running max moved (rare once the max settles)
     if (__ballot(moved)) {
 #pragma unroll
