@@ -359,6 +359,15 @@ int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t
                       int64_t gate_head_stride, uint16_t* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
                       int64_t D, int64_t Lmax, int mask_mode, int64_t n_clean, float scale, int64_t max_keys,
                       int64_t splits, void* scratch, int64_t scratch_bytes, void* stream);
+/* trida_attn_canvas with the output rows [B * T, Hq * D] (B * T <= 48) written in the fragment order of a
+ * weight-streaming GEMM's X (trida_ws_frag below) to out_frag (trida_ws_frag_elems(Hq * D) bf16,
+ * 16-byte aligned), the output projection's input. No counterpart in the reference (an internal layout
+ * between two kernels of the decoder forward). */
+int trida_attn_canvas_frag(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                           const int32_t* prefix_len, const uint16_t* gate, int64_t gate_row_stride,
+                           int64_t gate_head_stride, uint16_t* out_frag, int64_t B, int64_t T, int64_t Hq,
+                           int64_t Hkv, int64_t D, int64_t Lmax, int mask_mode, int64_t n_clean, float scale,
+                           int64_t max_keys, int64_t splits, void* scratch, int64_t scratch_bytes, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Row-wise decoder kernels around the GEMMs (bf16 storage, fp32 arithmetic). They replace the torch

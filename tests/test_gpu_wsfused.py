@@ -143,6 +143,23 @@ def test_gated_rmsnorm_fragment_order(gpu, rows, H, Dv):
     assert torch.equal(of.view(torch.int16).cpu()[mask], TK.ws_frag(ref.view(rows, -1)).view(torch.int16).cpu()[mask])
 
 
+def test_attn_canvas_fragment_order(gpu):
+    """The attention output written in fragment order is bitwise the row-major output converted."""
+    g = torch.Generator().manual_seed(3)
+    B, T, Hq, Hkv, D, L = 1, 33, 16, 4, 256, 200
+    q = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
+    kc = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16).to(DEV)
+    gate = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
+    pl = torch.tensor([120], dtype=torch.int32, device=DEV)
+    ref = TK.attn_canvas(q, kc, vc, pl, mask_mode=TK.MASK_VERIFY, gate=gate)
+    of = torch.zeros(TK.ws_frag_numel(Hq * D), dtype=torch.bfloat16, device=DEV)
+    TK.attn_canvas(q, kc, vc, pl, mask_mode=TK.MASK_VERIFY, gate=gate, out=of, out_frag=True)
+    mask = _frag_mask(B * T, Hq * D)
+    assert torch.equal(of.view(torch.int16).cpu()[mask],
+                       TK.ws_frag(ref.view(B * T, -1)).view(torch.int16).cpu()[mask])
+
+
 @pytest.fixture(scope="module")
 def fused_pair():
     w = init_weights(CFG, seed=0, embed_scale=4.0)

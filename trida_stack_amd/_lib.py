@@ -73,6 +73,8 @@ SIGNATURES = {
     "trida_gdn_restore": (C.c_int, [P] * 10 + [I64] * 11 + [C.c_int, P]),
     "trida_attn_canvas_scratch_bytes": (I64, [I64] * 7),
     "trida_attn_canvas": (C.c_int, [P, P, P, P, P, I64, I64, P] + [I64] * 6 + [C.c_int, I64, F32, I64, I64, P, I64, P]),
+    "trida_attn_canvas_frag": (C.c_int, [P, P, P, P, P, I64, I64, P] + [I64] * 6 + [C.c_int, I64, F32, I64, I64, P, I64,
+                                                                                   P]),
 }
 
 _lock = threading.Lock()

@@ -365,9 +365,11 @@ struct CombineArgs {
   const float* mpart;
   const float* lpart;
   const uint16_t* gate;  // row t, head h, dim d at gate + t * gate_st + h * gate_hs + d; or null
-  uint16_t* out;         // [B, T, Hq, D]
+  uint16_t* out;         // [B, T, Hq, D], or the rows [B * T, Hq * D] in the weight-streaming GEMM's
+                         // fragment order (frag)
   int T, Hq, Hkv, G, D, S, QT;
   int64_t gate_st, gate_hs;
+  int frag;
 };
 
 // Block = a group of RB = 1024 / D rows of one (sequence, KV head); thread = (row, 4 output columns).
@@ -459,7 +461,9 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
     for (int u = 0; u < 4; ++u)  // the attention output is rounded to bf16 before the gate, as torch does
       y[u] = bf2f(f2bf(y[u])) * (1.f / (1.f + __expf(-bf2f(gp[u]))));
   }
-  *reinterpret_cast<u32x2*>(a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * a.D + c) =
+  uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * a.D + c)
+                         : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * a.D + c;
+  *reinterpret_cast<u32x2*>(dst) =
       u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
 }
 
@@ -492,11 +496,12 @@ extern "C" int64_t trida_attn_canvas_scratch_bytes(int64_t B, int64_t T, int64_t
   return align_up(slots * kMT * D * 2, 256) + 2 * align_up(slots * kMT * 4, 256);
 }
 
-extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                                 const int32_t* prefix_len, const uint16_t* gate, int64_t gate_row_stride,
-                                 int64_t gate_head_stride, uint16_t* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
-                                 int64_t Lmax, int mask_mode, int64_t n_clean, float scale, int64_t max_keys,
-                                 int64_t splits, void* scratch, int64_t scratch_bytes, void* stream) {
+namespace {
+int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* prefix_len,
+                    const uint16_t* gate, int64_t gate_row_stride, int64_t gate_head_stride, uint16_t* out, bool frag,
+                    int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t Lmax, int mask_mode,
+                    int64_t n_clean, float scale, int64_t max_keys, int64_t splits, void* scratch,
+                    int64_t scratch_bytes, void* stream) {
   TRIDA_CHECK(q && k_cache && v_cache && prefix_len && out && scratch, TRIDA_ERR_NULL,
               "attn_canvas: q, k_cache, v_cache, prefix_len, out and scratch are required");
   TRIDA_CHECK(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Lmax >= T, TRIDA_ERR_ARG,
@@ -532,10 +537,32 @@ extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, con
   }
   int rc = launch_status("attn_canvas/partial");
   if (rc) return rc;
+  TRIDA_CHECK(!frag || B * T <= 48, TRIDA_ERR_ARG, "attn_canvas_frag: the fragment order holds at most 48 rows");
   CombineArgs c{opart, mpart, lpart, gate, out, (int)T, (int)Hq, (int)Hkv, (int)G, (int)D, (int)S, (int)QT,
-                gate_row_stride, gate_head_stride};
+                gate_row_stride, gate_head_stride, frag ? 1 : 0};
   const int64_t rows_per_block = 256 / (D / 4);
   hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv)), dim3(256),
                      0, st, c);
   return launch_status("attn_canvas/combine");
+}
+}  // namespace
+
+extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                 const int32_t* prefix_len, const uint16_t* gate, int64_t gate_row_stride,
+                                 int64_t gate_head_stride, uint16_t* out, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                 int64_t Lmax, int mask_mode, int64_t n_clean, float scale, int64_t max_keys,
+                                 int64_t splits, void* scratch, int64_t scratch_bytes, void* stream) {
+  return attn_canvas_run(q, k_cache, v_cache, prefix_len, gate, gate_row_stride, gate_head_stride, out, false, B, T, Hq,
+                         Hkv, D, Lmax, mask_mode, n_clean, scale, max_keys, splits, scratch, scratch_bytes, stream);
+}
+
+extern "C" int trida_attn_canvas_frag(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                      const int32_t* prefix_len, const uint16_t* gate, int64_t gate_row_stride,
+                                      int64_t gate_head_stride, uint16_t* out_frag, int64_t B, int64_t T, int64_t Hq,
+                                      int64_t Hkv, int64_t D, int64_t Lmax, int mask_mode, int64_t n_clean, float scale,
+                                      int64_t max_keys, int64_t splits, void* scratch, int64_t scratch_bytes,
+                                      void* stream) {
+  return attn_canvas_run(q, k_cache, v_cache, prefix_len, gate, gate_row_stride, gate_head_stride, out_frag, true, B,
+                         T, Hq, Hkv, D, Lmax, mask_mode, n_clean, scale, max_keys, splits, scratch, scratch_bytes,
+                         stream);
 }

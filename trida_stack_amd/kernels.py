@@ -779,14 +779,15 @@ MASK_VERIFY, MASK_DRAFT, MASK_CANVAS = 0, 1, 2
 def attn_canvas(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, prefix_len: torch.Tensor, *,
                 mask_mode: int, n_clean: int = 0, scale: Optional[float] = None,
                 gate: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
-                max_keys: int = 0, splits: int = 0) -> torch.Tensor:
+                max_keys: int = 0, splits: int = 0, out_frag: bool = False) -> torch.Tensor:
     """Canvas attention of a block of T rows against a bf16 KV cache (split-K, MFMA).
 
     q [B, T, Hq, D] bf16 contiguous; k_cache, v_cache [B, Hkv, Lmax, D] bf16 contiguous with the
     block's keys already at [prefix_len, prefix_len + T); prefix_len [B] int32 on the device.
     mask_mode: MASK_VERIFY (causal), MASK_DRAFT (bidirectional block) or MASK_CANVAS (rows < n_clean
     causal). gate (optional) is [B, T, Hq, D]-indexable with a contiguous last dim: the output is
-    multiplied by sigmoid(gate). Returns out [B, T, Hq, D] bf16."""
+    multiplied by sigmoid(gate). Returns out [B, T, Hq, D] bf16. out_frag: out is instead a buffer for the rows
+    [B * T, Hq * D] (B * T <= 48) in the fragment order ws_gemm_frag reads."""
     dev = _need_gpu(q, k_cache, v_cache, prefix_len, gate, out)
     for t, n in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
         _bf16(t, n)
@@ -804,7 +805,11 @@ def attn_canvas(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, p
         if gate.shape != (B, T, Hq, D) or gate.stride(3) != 1 or gate.stride(0) != T * gate.stride(1):
             raise ValueError("gate must be [B, T, Hq, D] with a contiguous last dim and packed batch rows")
         g_row, g_head = gate.stride(1), gate.stride(2)
-    if out is None:
+    if out_frag:
+        if out is None:
+            raise ValueError("attn_canvas: out_frag needs an out buffer")
+        _frag_buf(out, Hq * D, "out")
+    elif out is None:
         out = torch.empty_like(q)
     elif out.shape != q.shape or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("out must be a contiguous bf16 tensor shaped like q")
@@ -812,9 +817,10 @@ def attn_canvas(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, p
     mk = max_keys if max_keys > 0 else Lmax
     scr = workspaces.get(dev, "attn_canvas", lib.trida_attn_canvas_scratch_bytes(B, T, Hq, Hkv, D, mk, splits))
     sc = D ** -0.5 if scale is None else float(scale)
-    rc = lib.trida_attn_canvas(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), prefix_len.data_ptr(),
-                               _ptr(gate), g_row, g_head, out.data_ptr(), B, T, Hq, Hkv, D, Lmax, mask_mode,
-                               n_clean, sc, mk, splits, scr.data_ptr(), scr.numel(), _stream(dev))
+    fn = lib.trida_attn_canvas_frag if out_frag else lib.trida_attn_canvas
+    rc = fn(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), prefix_len.data_ptr(), _ptr(gate), g_row, g_head,
+            out.data_ptr(), B, T, Hq, Hkv, D, Lmax, mask_mode, n_clean, sc, mk, splits, scr.data_ptr(), scr.numel(),
+            _stream(dev))
     _lib.check(rc, "trida_attn_canvas")
     return out
 

@@ -232,6 +232,7 @@ class _Scratch:
         self.hf = torch.empty(K.ws_frag_numel(h), **bf) if frag else None
         self.actf = torch.empty(K.ws_frag_numel(cfg.intermediate), **bf) if frag else None
         self.ynf = torch.empty(K.ws_frag_numel(cfg.lin_v_heads * cfg.lin_v_dim), **bf) if frag else None
+        self.oattf = torch.empty(K.ws_frag_numel(cfg.n_heads * cfg.head_dim), **bf) if frag else None
 
 
 class TridaRuntime:
@@ -489,9 +490,13 @@ class TridaRuntime:
                 gate = s.qkv.as_strided((B, T, c.n_heads, c.head_dim), (T * Wq, Wq, 2 * c.head_dim, 1),
                                         s.qkv.storage_offset() + c.head_dim)
                 with K.timed("attn_canvas"):
-                    K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
-                                  out=s.o_att, max_keys=max_keys)
-                pending = self._proj(s, p + "w_o", s.o_att_p[:N], s.o_att_p, s.r_p)
+                    if fused:  # straight into the output projection's fragment-order X
+                        K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
+                                      out=s.oattf, max_keys=max_keys, out_frag=True)
+                    else:
+                        K.attn_canvas(s.q_att, kv_k[j], kv_v[j], length, mask_mode=att_mask, n_clean=nc, gate=gate,
+                                      out=s.o_att, max_keys=max_keys)
+                pending = self._proj(s, p + "w_o", s.o_att_p[:N], s.o_att_p, s.r_p, xf=s.oattf if fused else None)
             else:
                 self._proj_normed(s, p + "w_in", s.proj_p, fused)
                 xv = s.proj[..., : c.conv_dim]
