@@ -2,10 +2,12 @@
 // into q / k / v, l2norm of q and k per head, and the gates g = -exp(A_log) softplus(a + dt_bias),
 // beta = sigmoid(b).
 //
-// Launch: a grid of (sequence, row) x 128-piece channel slices (the C = conv_dim channels of a row spread
-// over several CUs: at batch 1 a row per block would leave most of the GPU idle while each block pulls
-// its 4 source rows and the whole conv weight). A thread owns 8 consecutive channels (one 16-byte
-// piece); the Dk/8 threads of a q or k head reduce its sum of squares with a row-local reduction.
+// Launch: small grids take a grid of (sequence, row) x channel slices of 128 pieces (the C = conv_dim
+// channels of a row spread over several CUs; at batch 1 a row per block would leave most of the GPU idle
+// while each block pulls its 4 source rows and the whole conv weight); grids of >= 512 rows, which fill
+// the GPU anyway, one 256-thread block per row with up to 4 passes over its pieces. A thread owns 8
+// consecutive channels (one 16-byte piece) per pass; the Dk/8 threads of a q or k head reduce its sum of
+// squares with a row-local reduction.
 // Rounding follows the CPU oracle: conv and SiLU in fp32, rounded to bf16, then l2norm in fp32 of the
 // rounded values, rounded to bf16 again.
 #include "common.h"
@@ -13,7 +15,6 @@
 namespace trida {
 namespace {
 
-constexpr int kThreads = 128;  // channel pieces (8 channels each) per block
 constexpr int kMaxKc = 4;
 
 template <int CTRL>
@@ -77,30 +78,33 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); 
 // torch.nn.functional.softplus with beta 1 and threshold 20
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-template <int GW, int KC>  // lanes per q/k head = Dk / 8; conv width
-__global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
+template <int GW, int KC, int NT, int PASSES>  // lanes per q/k head = Dk / 8; conv width; threads; passes
+__global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
   const int t = blockIdx.x % a.T;
   const int b = blockIdx.x / a.T;
   const int tid = threadIdx.x;
   const int key_dim = a.Hk * a.Dk;
   const int pieces = a.C / 8;
-  const int p0 = blockIdx.y * kThreads;  // the block's first piece: a multiple of GW
-  const int p = p0 + tid;
-  const bool live = p < pieces;
-  const int c = min(p, pieces - 1) * 8;  // lanes past the last piece compute on it and store nothing
+  const int pbase = blockIdx.y * NT * PASSES;  // the block's first piece: a multiple of GW
   const uint16_t* xb = a.x + (int64_t)b * a.x_sb;
   const uint16_t* wb = a.window + (int64_t)b * (a.Kc - 1) * a.C;
 
-  // every load of the block first (one memory round trip, unconditional): the KC source rows of the
-  // thread's 8 channels, their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces), and
-  // the gate inputs
-  u32x4 xs[KC], wsv[KC];
+  // every load of the block first (one memory round trip): per pass, the KC source rows of the thread's
+  // 8 channels and their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces), and the
+  // gate inputs. Lanes past the last piece load it (clamped) and store nothing; passes past it are
+  // skipped (block-uniform)
+  u32x4 xs[PASSES][KC], wsv[PASSES][KC];
 #pragma unroll
-  for (int j = 0; j < KC; ++j) {
-    const int tau = t - (KC - 1) + j;  // source row; negative rows come from the window
-    const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(KC - 1 + tau) * a.C + c;
-    xs[j] = *reinterpret_cast<const u32x4*>(src);
-    wsv[j] = reinterpret_cast<const u32x4*>(a.conv_w + (int64_t)c * KC)[j];
+  for (int ps = 0; ps < PASSES; ++ps) {
+    if (pbase + ps * NT >= pieces) break;
+    const int c = min(pbase + ps * NT + tid, pieces - 1) * 8;
+#pragma unroll
+    for (int j = 0; j < KC; ++j) {
+      const int tau = t - (KC - 1) + j;  // source row; negative rows come from the window
+      const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(KC - 1 + tau) * a.C + c;
+      xs[ps][j] = *reinterpret_cast<const u32x4*>(src);
+      wsv[ps][j] = reinterpret_cast<const u32x4*>(a.conv_w + (int64_t)c * KC)[j];
+    }
   }
   const bool gates = blockIdx.y == 0;  // block-uniform
   const int hg = min(tid, a.Hv - 1);
@@ -109,56 +113,75 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
     av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hg]);
     bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hg]);
   }
-  // the pre-conv rows a rollback rebuilds the window from: the block's own row is its last source row
-  if (a.pre_out && live) *reinterpret_cast<u32x4*>(a.pre_out + ((int64_t)b * a.T + t) * a.C + c) = xs[KC - 1];
 
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  {
-    float w[8][KC];
 #pragma unroll
-    for (int ch = 0; ch < 8; ++ch)
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int p0 = pbase + ps * NT;
+    if (p0 >= pieces) break;  // uniform
+    const int p = p0 + tid;
+    const bool live = p < pieces;
+    const int c = min(p, pieces - 1) * 8;
+    // the pre-conv rows a rollback rebuilds the window from: the block's own row is its last source row
+    if (a.pre_out && live) *reinterpret_cast<u32x4*>(a.pre_out + ((int64_t)b * a.T + t) * a.C + c) = xs[ps][KC - 1];
+    float acc[8];
+    {
+      float w[8][KC];
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch)
+#pragma unroll
+        for (int j = 0; j < KC; ++j) {
+          const int e = ch * KC + j;  // element of the 8 x KC weight block
+          const uint32_t word = wsv[ps][e / 8][(e % 8) / 2];
+          w[ch][j] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+        }
+#pragma unroll
+      for (int ch = 0; ch < 8; ++ch) acc[ch] = 0.f;
 #pragma unroll
       for (int j = 0; j < KC; ++j) {
-        const int e = ch * KC + j;  // element of the 8 x KC weight block
-        const uint32_t word = wsv[e / 8][(e % 8) / 2];
-        w[ch][j] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+        float f[8];
+        unpack8(xs[ps][j], f);
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) acc[ch] = fmaf(w[ch][j], f[ch], acc[ch]);
       }
 #pragma unroll
-    for (int j = 0; j < KC; ++j) {
-      float f[8];
-      unpack8(xs[j], f);
-#pragma unroll
-      for (int ch = 0; ch < 8; ++ch) acc[ch] = fmaf(w[ch][j], f[ch], acc[ch]);
+      for (int ch = 0; ch < 8; ++ch) acc[ch] = bf2f(f2bf(silu(acc[ch])));
     }
+    // the q/k pieces come first (2 * key_dim / 8 of them, a multiple of GW) and are all live, so every
+    // group of GW lanes belongs to one head
+    if (p0 < 2 * key_dim / 8) {  // block-uniform: per-head l2norm (all lanes take part in the reduction)
+      const bool is_qk = c < 2 * key_dim;  // uniform across a GW-lane group
+      float ss = 0.f;
 #pragma unroll
-    for (int ch = 0; ch < 8; ++ch) acc[ch] = bf2f(f2bf(silu(acc[ch])));
-  }
-  // the q/k pieces come first (2 * key_dim / 8 of them, a multiple of GW) and are all live, so every
-  // group of GW lanes belongs to one head
-  if (p0 < 2 * key_dim / 8) {  // block-uniform: per-head l2norm (all lanes take part in the reduction)
-    const bool is_qk = c < 2 * key_dim;  // uniform across a GW-lane group
-    float ss = 0.f;
+      for (int ch = 0; ch < 8; ++ch) ss = fmaf(acc[ch], acc[ch], ss);
+      ss = lane_group_sum<GW>(ss);
+      if (is_qk) {
+        const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
-    for (int ch = 0; ch < 8; ++ch) ss = fmaf(acc[ch], acc[ch], ss);
-    ss = lane_group_sum<GW>(ss);
-    if (is_qk) {
-      const float inv = rsqrtf(ss + 1e-6f);
-#pragma unroll
-      for (int ch = 0; ch < 8; ++ch) acc[ch] *= inv;
+        for (int ch = 0; ch < 8; ++ch) acc[ch] *= inv;
+      }
     }
-  }
-  if (live) {
-    const u32x4 w = pack8(acc);
-    const int64_t row = (int64_t)b * a.T + t;
-    if (c < key_dim)
-      *reinterpret_cast<u32x4*>(a.q + row * key_dim + c) = w;
-    else if (c < 2 * key_dim)
-      *reinterpret_cast<u32x4*>(a.k + row * key_dim + (c - key_dim)) = w;
-    else
-      *reinterpret_cast<u32x4*>(a.v + row * (int64_t)a.Hv * a.Dv + (c - 2 * key_dim)) = w;
+    if (live) {
+      const u32x4 w = pack8(acc);
+      const int64_t row = (int64_t)b * a.T + t;
+      if (c < key_dim)
+        *reinterpret_cast<u32x4*>(a.q + row * key_dim + c) = w;
+      else if (c < 2 * key_dim)
+        *reinterpret_cast<u32x4*>(a.k + row * key_dim + (c - key_dim)) = w;
+      else
+        *reinterpret_cast<u32x4*>(a.v + row * (int64_t)a.Hv * a.Dv + (c - 2 * key_dim)) = w;
+    }
+    // the new conv window (last Kc-1 rows of [window ++ x]): the last row's blocks, each its own pieces
+    if (a.window_out && t == a.T - 1 && live) {
+      for (int wr = 0; wr < a.Kc - 1; ++wr) {
+        const int tau = a.T - (a.Kc - 1) + wr;
+        const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(a.Kc - 1 + tau) * a.C + c;
+        *reinterpret_cast<u32x4*>(a.window_out + ((int64_t)b * (a.Kc - 1) + wr) * a.C + c) =
+            *reinterpret_cast<const u32x4*>(src);
+      }
+    }
   }
   if (gates) {
-    for (int hh = tid; hh < a.Hv; hh += kThreads) {
+    for (int hh = tid; hh < a.Hv; hh += NT) {
       if (hh != tid) {  // more heads than threads: the later ones load their own inputs
         av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hh]);
         bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hh]);
@@ -166,16 +189,6 @@ __global__ __launch_bounds__(kThreads) void gdn_prep_kernel(PrepArgs a) {
       const int64_t o = ((int64_t)b * a.T + t) * a.Hv + hh;
       a.g[o] = -__expf(a.A_log[hh]) * softplus(av + a.dt_bias[hh]);
       a.beta[o] = 1.f / (1.f + __expf(-bv));
-    }
-  }
-
-  // the new conv window (last Kc-1 rows of [window ++ x]): the last row's blocks, each its own pieces
-  if (a.window_out && t == a.T - 1 && live) {
-    for (int wr = 0; wr < a.Kc - 1; ++wr) {
-      const int tau = a.T - (a.Kc - 1) + wr;
-      const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(a.Kc - 1 + tau) * a.C + c;
-      *reinterpret_cast<u32x4*>(a.window_out + ((int64_t)b * (a.Kc - 1) + wr) * a.C + c) =
-          *reinterpret_cast<const u32x4*>(src);
     }
   }
 }
@@ -211,12 +224,22 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
   PrepArgs a{x, window, conv_w, a_in, b_in, A_log, dt_bias, q, k, v, g, beta, window_out, pre_out,
              (int)T, (int)C, (int)Kc, (int)Hk, (int)Hv, (int)Dk, (int)Dv, x_sb, x_st, ab_sb, ab_st};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)(B * T), (unsigned)cdiv(C / 8, kThreads));
-#define TRIDA_PREP_LAUNCH(GW)                                                                   \
-  switch (Kc) {                                                                                 \
-    case 2: hipLaunchKernelGGL((gdn_prep_kernel<GW, 2>), grid, dim3(kThreads), 0, st, a); break; \
-    case 3: hipLaunchKernelGGL((gdn_prep_kernel<GW, 3>), grid, dim3(kThreads), 0, st, a); break; \
-    default: hipLaunchKernelGGL((gdn_prep_kernel<GW, 4>), grid, dim3(kThreads), 0, st, a); break; \
+  // small grids: 128-piece slices, one per block; grids of >= 512 rows (which fill the GPU anyway): one
+  // block of 256 threads per row, up to 4 passes over its pieces, every pass's loads in flight together
+  const bool wide = B * T >= 512;
+  TRIDA_CHECK(!wide || C <= 8 * 256 * 4, TRIDA_ERR_ARG, "gdn_prep: conv_dim %lld above %d", (long long)C, 8 * 256 * 4);
+  const dim3 grid((unsigned)(B * T), wide ? 1u : (unsigned)cdiv(C / 8, 128));
+#define TRIDA_PREP_KC(GW, NT, PS)                                                                          \
+  switch (Kc) {                                                                                            \
+    case 2: hipLaunchKernelGGL((gdn_prep_kernel<GW, 2, NT, PS>), grid, dim3(NT), 0, st, a); break;         \
+    case 3: hipLaunchKernelGGL((gdn_prep_kernel<GW, 3, NT, PS>), grid, dim3(NT), 0, st, a); break;         \
+    default: hipLaunchKernelGGL((gdn_prep_kernel<GW, 4, NT, PS>), grid, dim3(NT), 0, st, a); break;        \
+  }
+#define TRIDA_PREP_LAUNCH(GW)      \
+  if (wide) {                      \
+    TRIDA_PREP_KC(GW, 256, 4)      \
+  } else {                         \
+    TRIDA_PREP_KC(GW, 128, 1)      \
   }
   switch (Dk) {
     case 32: TRIDA_PREP_LAUNCH(4) break;
@@ -224,5 +247,6 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
     default: TRIDA_PREP_LAUNCH(16) break;
   }
 #undef TRIDA_PREP_LAUNCH
+#undef TRIDA_PREP_KC
   return launch_status("gdn_prep");
 }
