@@ -373,31 +373,50 @@ struct CombineArgs {
 };
 
 // Block = a group of RB = 1024 / D rows of one (sequence, KV head); thread = (row, 4 output columns).
-// The split weights exp2(m_s - max) / sum of the group's rows are computed once into LDS; each
-// thread then sums the O rows of the non-empty splits, four splits' loads in flight at a time.
+// The split weights exp2(m_s - max) / sum of the group's rows are computed once into LDS; each thread
+// then sums the O rows of the non-empty splits in split order. Every phase issues its loads together
+// (clamped, unconditional): the listing's row statistics, a row's max and sum (one pass over m and l),
+// 16 splits' O rows at a time, and the gate first of all, so the combine costs a few memory round trips
+// instead of one per four splits.
 constexpr int kMaxSplits = 256;
-constexpr int kCRB = 16;  // the most rows a combine block holds (D = 64)
+constexpr int kOB = 16;  // O rows in flight per thread
 
+template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
-  __shared__ float s_w[kCRB][kMaxSplits];  // rows of the group x listed splits
-  __shared__ float s_inv[kCRB];
+  constexpr int PER_ROW = D / 4;
+  constexpr int RB = 256 / PER_ROW;  // rows per block: 4 (D=256), 8 (D=128), 16 (D=64)
+  __shared__ float s_w[RB][kMaxSplits];  // rows of the group x listed splits
+  __shared__ float s_inv[RB];
   __shared__ int s_list[kMaxSplits];
   __shared__ int s_cnt[4];
   const int M = a.T * a.G;
-  const int per_row = a.D / 4;
-  const int rb = 256 / per_row;  // rows per block: 4 (D=256), 8 (D=128), 16 (D=64)
   const int b = blockIdx.y / a.Hkv, hk = blockIdx.y % a.Hkv;
-  const int m0 = blockIdx.x * rb;
+  const int m0 = blockIdx.x * RB;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int64_t pair = (int64_t)b * a.Hkv + hk;
+  // this thread's output element group (rows past M compute on row M - 1 and store nothing)
+  const int i = tid / PER_ROW;
+  const int m = m0 + i;
+  const int mc = min(m, M - 1);
+  const int c = (tid % PER_ROW) * 4;
+  const int t = mc / a.G, g = mc % a.G, hq = hk * a.G + g;
+  u32x2 gw = {0u, 0u};
+  if (a.gate)
+    gw = *reinterpret_cast<const u32x2*>(a.gate + ((int64_t)b * a.T + t) * a.gate_st + (int64_t)hq * a.gate_hs + c);
   // list, in split order, the splits with a visible key for some row of the group (one split per
   // thread, S <= 256; wave ballots give each listed split its position)
   bool any = false;
-  if (tid < a.S) {
-    for (int i = 0; i < rb && m0 + i < M; ++i) {
-      const int m = m0 + i;
-      const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
-      any |= a.mpart[(bs + tid) * kMT + m % kMT] != -INFINITY;
+  {
+    const int sp = min(tid, a.S - 1);
+    float mv[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int mr = min(m0 + r, M - 1);
+      mv[r] = a.mpart[((pair * a.QT + mr / kMT) * a.S + sp) * kMT + mr % kMT];
     }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) any |= m0 + r < M && mv[r] != -INFINITY;
+    any &= tid < a.S;
   }
   const unsigned long long mask = __ballot(any);
   if (lane == 0) s_cnt[wave] = __popcll(mask);
@@ -407,64 +426,75 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
   if (any) s_list[off + __popcll(mask & ((1ull << lane) - 1ull))] = tid;
   const int ns = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
   __syncthreads();
-  // per row: max, weights and 1 / sum (one wave per row, lanes over the listed splits)
-  for (int i = wave; i < rb; i += 4) {
-    const int m = m0 + i;
-    if (m >= M) break;
-    const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
-    const int r = m % kMT;
+  // per row: max, weights and 1 / sum (one wave per row, lanes over the listed splits; m and l of a
+  // lane's splits loaded together)
+  for (int ri = wave; ri < RB; ri += 4) {
+    const int mr = min(m0 + ri, M - 1);
+    const int64_t bs = (pair * a.QT + mr / kMT) * a.S;
+    const int r = mr % kMT;
+    constexpr int JU = kMaxSplits / kWave;  // listed splits per lane, at most
+    float mj[JU], lj[JU];
+#pragma unroll
+    for (int u = 0; u < JU; ++u) {
+      const int j = lane + u * kWave;
+      if (u * kWave < ns) {  // uniform
+        const int sj = s_list[min(j, ns - 1)];
+        mj[u] = a.mpart[(bs + sj) * kMT + r];
+        lj[u] = a.lpart[(bs + sj) * kMT + r];
+      }
+    }
     float mx = -INFINITY;
-    for (int j = lane; j < ns; j += kWave) mx = fmaxf(mx, a.mpart[(bs + s_list[j]) * kMT + r]);
+#pragma unroll
+    for (int u = 0; u < JU; ++u)
+      if (u * kWave < ns && lane + u * kWave < ns) mx = fmaxf(mx, mj[u]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
     const float m_use = mx == -INFINITY ? 0.f : mx;
     float lsum = 0.f;
-    for (int j = lane; j < ns; j += kWave) {
-      const float w = exp2f(a.mpart[(bs + s_list[j]) * kMT + r] - m_use);
-      s_w[i][j] = w;
-      lsum += w * a.lpart[(bs + s_list[j]) * kMT + r];
+#pragma unroll
+    for (int u = 0; u < JU; ++u) {
+      const int j = lane + u * kWave;
+      if (u * kWave < ns && j < ns) {
+        const float w = exp2f(mj[u] - m_use);
+        s_w[ri][j] = w;
+        lsum += w * lj[u];
+      }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, kWave);
-    if (lane == 0) s_inv[i] = lsum > 0.f ? 1.f / lsum : 0.f;
+    if (lane == 0) s_inv[ri] = lsum > 0.f ? 1.f / lsum : 0.f;
   }
   __syncthreads();
-  const int i = tid / per_row;
-  const int m = m0 + i;
-  if (i >= rb || m >= M) return;
-  const int c = (tid % per_row) * 4;
-  const int64_t bs = (((int64_t)b * a.Hkv + hk) * a.QT + m / kMT) * a.S;
-  const int r = m % kMT;
-  const uint16_t* obase = a.opart + (int64_t)r * a.D + c;
-  const int64_t sstride = (int64_t)kMT * a.D;  // elements between consecutive splits
+  const int64_t bs = (pair * a.QT + mc / kMT) * a.S;
+  const uint16_t* obase = a.opart + (int64_t)(mc % kMT) * D + c;
+  const int64_t sstride = (int64_t)kMT * D;  // elements between consecutive splits
   auto ld4 = [](const uint16_t* p) {  // 4 bf16 -> fp32
     const u32x2 w = *reinterpret_cast<const u32x2*>(p);
     return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
                  __uint_as_float(w.y & 0xffff0000u)};
   };
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  int j = 0;
-  for (; j + 4 <= ns; j += 4) {
-    f32x4 x[4];
+  for (int j0 = 0; j0 < ns; j0 += kOB) {
+    f32x4 x[kOB];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = ld4(obase + (bs + s_list[j + u]) * sstride);
+    for (int u = 0; u < kOB; ++u) x[u] = ld4(obase + (bs + s_list[min(j0 + u, ns - 1)]) * sstride);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc += s_w[i][j + u] * x[u];
+    for (int u = 0; u < kOB; ++u)
+      if (j0 + u < ns) acc += s_w[i < RB ? i : 0][j0 + u] * x[u];  // uniform bound; split order kept
   }
-  for (; j < ns; ++j) acc += s_w[i][j] * ld4(obase + (bs + s_list[j]) * sstride);
+  if (i >= RB || m >= M) return;
   const float inv = s_inv[i];
-  const int t = m / a.G, g = m % a.G, hq = hk * a.G + g;
   float y[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
   if (a.gate) {
-    const uint16_t* gp = a.gate + ((int64_t)b * a.T + t) * a.gate_st + (int64_t)hq * a.gate_hs + c;
+    const float gv[4] = {__uint_as_float(gw.x << 16), __uint_as_float(gw.x & 0xffff0000u), __uint_as_float(gw.y << 16),
+                         __uint_as_float(gw.y & 0xffff0000u)};
 #pragma unroll
     for (int u = 0; u < 4; ++u)  // the attention output is rounded to bf16 before the gate, as torch does
-      y[u] = bf2f(f2bf(y[u])) * (1.f / (1.f + __expf(-bf2f(gp[u]))));
+      y[u] = bf2f(f2bf(y[u])) * (1.f / (1.f + __expf(-gv[u])));
   }
-  uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * a.D + c)
-                         : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * a.D + c;
-  *reinterpret_cast<u32x2*>(dst) =
-      u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
+  uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * D + c)
+                         : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + c;
+  *reinterpret_cast<u32x2*>(dst) = u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
 }
 
 // Splits per (sequence, KV head, query tile): as many as keep the grid within one workgroup per CU
@@ -541,8 +571,12 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   CombineArgs c{opart, mpart, lpart, gate, out, (int)T, (int)Hq, (int)Hkv, (int)G, (int)D, (int)S, (int)QT,
                 gate_row_stride, gate_head_stride, frag ? 1 : 0};
   const int64_t rows_per_block = 256 / (D / 4);
-  hipLaunchKernelGGL(attn_combine_kernel, dim3((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv)), dim3(256),
-                     0, st, c);
+  const dim3 cgrid((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv));
+  switch (D) {
+    case 64: hipLaunchKernelGGL(attn_combine_kernel<64>, cgrid, dim3(256), 0, st, c); break;
+    case 128: hipLaunchKernelGGL(attn_combine_kernel<128>, cgrid, dim3(256), 0, st, c); break;
+    default: hipLaunchKernelGGL(attn_combine_kernel<256>, cgrid, dim3(256), 0, st, c); break;
+  }
   return launch_status("attn_canvas/combine");
 }
 }  // namespace
