@@ -372,7 +372,7 @@ struct CombineArgs {
   int frag;
 };
 
-// Block = a group of RB = 1024 / D rows of one (sequence, KV head); thread = (row, 4 output columns).
+// Block = a group of RB = 512 / D rows of one (sequence, KV head); thread = (row, 4 output columns).
 // The split weights exp2(m_s - max) / sum of the group's rows are computed once into LDS; each thread
 // then sums the O rows of the non-empty splits in split order. Every phase issues its loads together
 // (clamped, unconditional): the listing's row statistics, a row's max and sum (one pass over m and l),
@@ -381,14 +381,18 @@ struct CombineArgs {
 constexpr int kMaxSplits = 256;
 constexpr int kOB = 16;  // O rows in flight per thread
 
+constexpr int kCT = 128;  // combine threads per block (2 waves): 2 rows of d 256 per block, so a
+                          // batch-1 canvas (132 rows per KV head) spreads over the CUs
 template <int D>
-__global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
+__global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
   constexpr int PER_ROW = D / 4;
-  constexpr int RB = 256 / PER_ROW;  // rows per block: 4 (D=256), 8 (D=128), 16 (D=64)
+  constexpr int RB = kCT / PER_ROW;  // rows per block: 2 (D=256), 4 (D=128), 8 (D=64)
+  constexpr int NWV = kCT / kWave;
+  constexpr int LP = kMaxSplits / kCT;  // splits per thread in the listing
   __shared__ float s_w[RB][kMaxSplits];  // rows of the group x listed splits
   __shared__ float s_inv[RB];
   __shared__ int s_list[kMaxSplits];
-  __shared__ int s_cnt[4];
+  __shared__ int s_cnt[LP][NWV];
   const int M = a.T * a.G;
   const int b = blockIdx.y / a.Hkv, hk = blockIdx.y % a.Hkv;
   const int m0 = blockIdx.x * RB;
@@ -403,32 +407,47 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(CombineArgs a) {
   u32x2 gw = {0u, 0u};
   if (a.gate)
     gw = *reinterpret_cast<const u32x2*>(a.gate + ((int64_t)b * a.T + t) * a.gate_st + (int64_t)hq * a.gate_hs + c);
-  // list, in split order, the splits with a visible key for some row of the group (one split per
-  // thread, S <= 256; wave ballots give each listed split its position)
-  bool any = false;
+  // list, in split order, the splits with a visible key for some row of the group (splits tid and
+  // tid + kCT of each thread, S <= 256; wave ballots give each listed split its position)
+  bool any[LP];
   {
-    const int sp = min(tid, a.S - 1);
-    float mv[RB];
+    float mv[LP][RB];
 #pragma unroll
-    for (int r = 0; r < RB; ++r) {
-      const int mr = min(m0 + r, M - 1);
-      mv[r] = a.mpart[((pair * a.QT + mr / kMT) * a.S + sp) * kMT + mr % kMT];
+    for (int q = 0; q < LP; ++q) {
+      const int sp = min(tid + q * kCT, a.S - 1);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        const int mr = min(m0 + r, M - 1);
+        mv[q][r] = a.mpart[((pair * a.QT + mr / kMT) * a.S + sp) * kMT + mr % kMT];
+      }
     }
 #pragma unroll
-    for (int r = 0; r < RB; ++r) any |= m0 + r < M && mv[r] != -INFINITY;
-    any &= tid < a.S;
+    for (int q = 0; q < LP; ++q) {
+      any[q] = false;
+#pragma unroll
+      for (int r = 0; r < RB; ++r) any[q] |= m0 + r < M && mv[q][r] != -INFINITY;
+      any[q] &= tid + q * kCT < a.S;
+    }
   }
-  const unsigned long long mask = __ballot(any);
-  if (lane == 0) s_cnt[wave] = __popcll(mask);
+  unsigned long long mask[LP];
+#pragma unroll
+  for (int q = 0; q < LP; ++q) {
+    mask[q] = __ballot(any[q]);
+    if (lane == 0) s_cnt[q][wave] = __popcll(mask[q]);
+  }
   __syncthreads();
-  int off = 0;
-  for (int w = 0; w < wave; ++w) off += s_cnt[w];
-  if (any) s_list[off + __popcll(mask & ((1ull << lane) - 1ull))] = tid;
-  const int ns = s_cnt[0] + s_cnt[1] + s_cnt[2] + s_cnt[3];
+  int ns = 0;
+#pragma unroll
+  for (int q = 0; q < LP; ++q) {
+    int off = ns;
+    for (int w = 0; w < wave; ++w) off += s_cnt[q][w];
+    if (any[q]) s_list[off + __popcll(mask[q] & ((1ull << lane) - 1ull))] = tid + q * kCT;
+    for (int w = 0; w < NWV; ++w) ns += s_cnt[q][w];
+  }
   __syncthreads();
   // per row: max, weights and 1 / sum (one wave per row, lanes over the listed splits; m and l of a
   // lane's splits loaded together)
-  for (int ri = wave; ri < RB; ri += 4) {
+  for (int ri = wave; ri < RB; ri += NWV) {
     const int mr = min(m0 + ri, M - 1);
     const int64_t bs = (pair * a.QT + mr / kMT) * a.S;
     const int r = mr % kMT;
@@ -570,12 +589,12 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   TRIDA_CHECK(!frag || B * T <= 48, TRIDA_ERR_ARG, "attn_canvas_frag: the fragment order holds at most 48 rows");
   CombineArgs c{opart, mpart, lpart, gate, out, (int)T, (int)Hq, (int)Hkv, (int)G, (int)D, (int)S, (int)QT,
                 gate_row_stride, gate_head_stride, frag ? 1 : 0};
-  const int64_t rows_per_block = 256 / (D / 4);
+  const int64_t rows_per_block = kCT / (D / 4);
   const dim3 cgrid((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv));
   switch (D) {
-    case 64: hipLaunchKernelGGL(attn_combine_kernel<64>, cgrid, dim3(256), 0, st, c); break;
-    case 128: hipLaunchKernelGGL(attn_combine_kernel<128>, cgrid, dim3(256), 0, st, c); break;
-    default: hipLaunchKernelGGL(attn_combine_kernel<256>, cgrid, dim3(256), 0, st, c); break;
+    case 64: hipLaunchKernelGGL(attn_combine_kernel<64>, cgrid, dim3(kCT), 0, st, c); break;
+    case 128: hipLaunchKernelGGL(attn_combine_kernel<128>, cgrid, dim3(kCT), 0, st, c); break;
+    default: hipLaunchKernelGGL(attn_combine_kernel<256>, cgrid, dim3(kCT), 0, st, c); break;
   }
   return launch_status("attn_canvas/combine");
 }
