@@ -338,8 +338,8 @@ class TridaRuntime:
             if role == K.WS_PARTS:
                 self.ws_parts = max(self.ws_parts, kg)
         # the LM head (bf16 logits of <= K.WS_MAX_M rows; the fp32 logits_out path keeps hipBLASLt)
-        wl = self.w.get("lm_head", self.w["embed"])
-        if wl.shape[0] % 16 == 0 and wl.shape[1] % 32 == 0:
+        wl = self.w.get("lm_head", self.w.get("embed"))
+        if wl is not None and wl.shape[0] % 16 == 0 and wl.shape[1] % 32 == 0:
             try:
                 kg = K.ws_plan(wl.shape[0], wl.shape[1], K.WS_STORE)
                 self.ws["lm_head"] = (K.ws_shuffle(wl.contiguous()), wl.shape[0], K.WS_STORE, kg)
