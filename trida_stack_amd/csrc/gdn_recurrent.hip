@@ -562,6 +562,36 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     for (int e = tid; e < nm * Dk; e += NW * kWave) s_qf[e] = bf2f(s_q[nc + e / Dk][e % Dk]) * a.scale;
     __syncthreads();
   }
+  if (F32 && a.T <= tcn && nm > 0) {
+    // the whole block is the last staged chunk (s_qf32 holds every row): eight rows at a time, two
+    // interleaved 4-row reductions (each row's fma order and row16 reduction as below), the readouts
+    // kept in LDS and stored together
+    for (int t = nc; t < a.T; t += 8) {
+      float o0[4], o1[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int ta = min(t + j, a.T - 1), tb = min(t + 4 + j, a.T - 1);
+        o0[j] = 0.f;
+        o1[j] = 0.f;
+#pragma unroll
+        for (int i = 0; i < KPL; ++i) {
+          o0[j] = fmaf(s[i], s_qf32[ta][kl * KPL + i], o0[j]);
+          o1[j] = fmaf(s[i], s_qf32[tb][kl * KPL + i], o1[j]);
+        }
+      }
+      row16_sum4(o0);
+      row16_sum4(o1);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (t + j < a.T) s_ob[t + j][vl] = o0[j];
+        if (t + 4 + j < a.T) s_ob[t + 4 + j][vl] = o1[j];
+      }
+    }
+    __syncthreads();
+    uint16_t* otile = a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + vt * VPB;
+    for (int e = tid; e < nm * VPB; e += NW * kWave)
+      otile[(int64_t)(nc + e / VPB) * v_row + e % VPB] = f2bf(s_ob[nc + e / VPB][e % VPB]);
+  } else
   for (int t = nc; t < a.T; t += 4) {
     float o[4];
 #pragma unroll
