@@ -872,7 +872,7 @@ def bench_gdr(args):
                    "kernel_us": {kk: round(vv, 2) for kk, vv in us.items()},
                    "prefix_gflop": round(flops / 1e9, 3), "prefix_hbm_GBps": round(prefix_bytes / us["prefix"] / 1e3, 1),
                    "snapshot_GBps": round(snap_bytes / us["snapshot"] / 1e3, 1)},
-        "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (gdr_prefix, one launch)", "achieved": round(tflops, 1),
+        "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (gdr_prefix_prep + gdr_prefix_scan)", "achieved": round(tflops, 1),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
                      "traffic": _measured_traffic("gdr_prefix")},
         "at_scale": _snapshot_restore_at_scale(dev, H, D, CH),

@@ -154,6 +154,7 @@ struct ChunkArgs {
 // ---------------------------------------------------------------------------------------------- staging
 // Workspace block of one (sequence, chunk, value head): T diag(beta) hi, lo and Aqk hi, 64 x 64 bf16 each.
 constexpr int kWsElems = 3 * kChunk * kChunk;
+static_assert(kWsElems * 2 >= kPrefixWsBytes, "the workspace also serves the prefix kernels");
 
 // Rows [t0, t0 + cc) of one chunk (rows cc..C-1 read as zero), staged in two steps so that every global
 // load of a chunk is in flight at once: load() issues them into registers, store() writes LDS (K
@@ -850,9 +851,10 @@ extern "C" int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint1
     return gdr_block_launch(ba, B, static_cast<hipStream_t>(stream));
   }
   if (!n_keep && gdr_prefix_supported(B, T, Hv, Dk, Dv)) {
-    // a prompt prefix (every row causal, the state after the last row): the pipelined one-launch kernel
-    PrefixArgs pa{q, k, v, g, beta, state_in, out, state_out, (int)T, (int)Hk, (int)Hv, (int)Dv, (int)nchunks,
-                  scale};
+    // a prompt prefix (every row causal, the state after the last row): the chunk-parallel preparation, then
+    // the scan whose chain wave holds the state
+    PrefixArgs pa{q, k, v, g, beta, state_in, out, state_out, workspace, (int)T, (int)Hk, (int)Hv, (int)Dv,
+                  (int)nchunks, scale};
     return gdr_prefix_launch(pa, B, static_cast<hipStream_t>(stream));
   }
   ChunkArgs a{q,        k,   v,       g,         beta,       state_in,      out,

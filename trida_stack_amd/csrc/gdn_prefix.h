@@ -1,4 +1,5 @@
-// The one-launch chunked gated delta rule over a long prefix (gdn_prefix.hip), dispatched by trida_gdr_chunk.
+// The chunked gated delta rule over a long prefix (gdn_prefix.hip: a chunk-parallel preparation, then the
+// scan), dispatched by trida_gdr_chunk.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -15,9 +16,13 @@ struct PrefixArgs {
   const float* state_in;  // [B, Hv, Dv, 128] fp32
   uint16_t* out;          // [B, T, Hv, Dv] bf16 or null
   float* state_out;       // [B, Hv, Dv, 128] fp32 or null (the state after all T rows)
+  void* ws;               // kPrefixWsBytes per (sequence, chunk, value head), 16-byte aligned
   int T, Hk, Hv, Dv, nchunks;
   float scale;
 };
+
+// workspace bytes per (sequence, 64-row chunk, value head): T (bf16 hi + lo) and M (bf16) fragments
+constexpr int64_t kPrefixWsBytes = 18432;
 
 // T > 64, Dk == 128, Dv % 16 == 0, at most 256 workgroups (B * Hv * Dv / 16); every row causal, the state
 // after the last row
