@@ -106,7 +106,9 @@ def test_gdr_chunk_argument_checks():
     lib = _lib.load()
     P = 256
     assert lib.trida_gdr_chunk_workspace_bytes(1, 64, 16) == 0
-    assert lib.trida_gdr_chunk_workspace_bytes(1, 4096, 16) == 64 * 16 * 3 * 64 * 64 * 2
+    # per (chunk, head): the larger of the general path's T hi / lo + M (3 x 64 x 64 bf16) and the prefix
+    # kernels' T and M fragments and decays (19456 bytes)
+    assert lib.trida_gdr_chunk_workspace_bytes(1, 4096, 16) == 64 * 16 * max(3 * 64 * 64 * 2, 19456)
 
     def call(T=100, Dk=128, Dv=128, mode=1, ws=None, ws_bytes=0, n_keep=None):
         return lib.trida_gdr_chunk(P, P, P, P, P, P, P, P, n_keep, 1, 1, T, 16, 16, Dk, Dv, mode, 0, 0.1, ws,

@@ -21,8 +21,9 @@ struct PrefixArgs {
   float scale;
 };
 
-// workspace bytes per (sequence, 64-row chunk, value head): T (bf16 hi + lo) and M (bf16) fragments
-constexpr int64_t kPrefixWsBytes = 18432;
+// workspace bytes per (sequence, 64-row chunk, value head): T (bf16 hi + lo) and M (bf16) fragments, the
+// chunk's decays (fp32)
+constexpr int64_t kPrefixWsBytes = 19456;
 
 // T > 64, Dk == 128, Dv % 16 == 0, at most 256 workgroups (B * Hv * Dv / 16); every row causal, the state
 // after the last row

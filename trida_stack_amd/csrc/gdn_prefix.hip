@@ -60,10 +60,11 @@ constexpr int kPairs = 6;
 __device__ __forceinline__ int pair_it(int p) { return p < 2 ? p : 2 + (p - 2) / 2; }
 __device__ __forceinline__ int pair_kb(int p) { return p < 2 ? 0 : (p - 2) % 2; }
 // workspace per (sequence, chunk, value head) in 16-byte fragments (one per lane): T [pair][hi, lo][lane],
-// then M [pair][lane]
+// M [pair][lane], then the decays beta, e^G, e^{G_L - G}, e^{G_L} as fp32 [4][64]
 constexpr int kWsT = 0;
 constexpr int kWsM = kPairs * 2 * kWave;
-constexpr int kWsFrags = kWsM + kPairs * kWave;
+constexpr int kWsVec = kWsM + kPairs * kWave;
+constexpr int kWsFrags = kWsVec + 4 * CH / 4;
 static_assert(kWsFrags * 16 == kPrefixWsBytes, "prefix workspace layout");
 
 __device__ __forceinline__ f32x4 mma16(s16x4 a, s16x4 b, f32x4 c) {
@@ -364,9 +365,17 @@ __global__ __launch_bounds__(kPrepNT) void gdr_prefix_prep_kernel(PrefixArgs a) 
     *reinterpret_cast<u32x4*>(&sh.K[o]) = kr[u];
     if (OUT) *reinterpret_cast<u32x4*>(&sh.Q[o]) = qr[u];
   }
+  u32x4* dst = static_cast<u32x4*>(a.ws) + ((int64_t)(b * a.nchunks + c) * a.Hv + h) * kWsFrags;
   if (w == 0) {
-    sh.G2[l] = chunk_g2(gv, l);
+    const float G = chunk_g2(gv, l);
+    const float GL = __shfl(G, kWave - 1, kWave);
+    sh.G2[l] = G;
     sh.be[l] = bv;
+    float* vec = reinterpret_cast<float*>(dst + kWsVec);  // the scan's decays
+    vec[l] = bv;
+    vec[CH + l] = ex2(G);
+    vec[2 * CH + l] = ex2(GL - G);
+    vec[3 * CH + l] = ex2(GL);
   }
   bar();
   prep_blocks(sh, w, l);
@@ -376,7 +385,6 @@ __global__ __launch_bounds__(kPrepNT) void gdr_prefix_prep_kernel(PrefixArgs a) 
   bar();
   // the fragments: pair (it, kb) holds rows 16 it + l % 16 at k slots 32 kb + 4 g .. + 3 and 32 kb + 16 +
   // 4 g .. + 3 (g = l / 16); the tiles above the diagonal are zero
-  u32x4* dst = static_cast<u32x4*>(a.ws) + ((int64_t)(b * a.nchunks + c) * a.Hv + h) * kWsFrags;
   for (int p = w; p < kPairs; p += 4) {
     const int it = pair_it(p), kb = pair_kb(p);
     const int o = (16 * it + l % 16) * TS + 32 * kb + 4 * (l / 16);
@@ -405,17 +413,19 @@ struct ScanLds {
   float vec[3][4][CH];              // beta, e^G, e^{G_L - G}, e^{G_L} (every entry); buffer = chunk mod 3
   u32x4 xS[2][4][kWave];            // St hi at the chunk start as B fragments per k block (readout)
   u32x4 xV[2][2][kWave];            // v_new hi as B fragments per k block (readout)
+  uint16_t xO[CH][DS];              // the readout's rows, transposed for 16-byte row stores
 };
 static_assert(sizeof(ScanLds) <= 160 * 1024, "LDS plan exceeds 160 KiB");
 
 // what a staging wave pw (0..3) loads for one chunk: K rows 16 pw + 4 (l / 16) + u, columns 8 (l % 16) ..
 // + 7; the V row 16 pw + l / 4, columns 4 (l % 4) .. + 3 of this workgroup's slice; the T fragments
-// 256 j + 64 pw + l; g and beta of row l
+// 256 j + 64 pw + l; decay entry 64 pw + l. Rows past T read row 0 (in bounds) and are zeroed when staged:
+// nothing consumes a load until the next iteration, so the loads stay in flight across the barrier
 struct Raw {
   u32x4 k[4];
   u32x4 t[3];
   u32x2 v;
-  float g, be;
+  float dec;
 };
 
 __device__ __forceinline__ void load_raw(Raw& r, const PrefixArgs& a, int b, int h, int hk, int dv0, int c, int pw,
@@ -424,33 +434,25 @@ __device__ __forceinline__ void load_raw(Raw& r, const PrefixArgs& a, int b, int
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int t = t0 + 16 * pw + 4 * (l / 16) + u;
-    const bool ok = t < a.T;
-    const int64_t off = ((int64_t)(b * a.T + (ok ? t : 0)) * a.Hk + hk) * DK + 8 * (l % 16);
-    const u32x4 kv = *reinterpret_cast<const u32x4*>(a.k + off);
-    r.k[u] = ok ? kv : u32x4{0u, 0u, 0u, 0u};
+    const int64_t off = ((int64_t)(b * a.T + (t < a.T ? t : 0)) * a.Hk + hk) * DK + 8 * (l % 16);
+    r.k[u] = *reinterpret_cast<const u32x4*>(a.k + off);
   }
   {
     const int t = t0 + 16 * pw + l / 4;
-    const bool ok = t < a.T;
-    const int64_t off = ((int64_t)(b * a.T + (ok ? t : 0)) * a.Hv + h) * a.Dv + dv0 + 4 * (l % 4);
-    const u32x2 vv = *reinterpret_cast<const u32x2*>(a.v + off);
-    r.v = ok ? vv : u32x2{0u, 0u};
+    const int64_t off = ((int64_t)(b * a.T + (t < a.T ? t : 0)) * a.Hv + h) * a.Dv + dv0 + 4 * (l % 4);
+    r.v = *reinterpret_cast<const u32x2*>(a.v + off);
   }
-  const u32x4* src = static_cast<const u32x4*>(a.ws) + ((int64_t)(b * a.nchunks + c) * a.Hv + h) * kWsFrags + kWsT;
+  const u32x4* src = static_cast<const u32x4*>(a.ws) + ((int64_t)(b * a.nchunks + c) * a.Hv + h) * kWsFrags;
 #pragma unroll
-  for (int j = 0; j < 3; ++j) r.t[j] = src[256 * j + 64 * pw + l];
-  if (pw == 0) {
-    const int t = t0 + l;
-    const bool ok = t < a.T;
-    const int64_t gi = (int64_t)(b * a.T + (ok ? t : 0)) * a.Hv + h;
-    const float x = a.g[gi], y = a.beta[gi];
-    r.g = ok ? x : 0.f;
-    r.be = ok ? y : 0.f;
-  }
+  for (int j = 0; j < 3; ++j) r.t[j] = src[kWsT + 256 * j + 64 * pw + l];
+  r.dec = reinterpret_cast<const float*>(src + kWsVec)[64 * pw + l];
 }
 
-__device__ __forceinline__ void stage(ScanLds& sh, const Raw& r, int c, int pw, int l) {
+__device__ __forceinline__ void stage(ScanLds& sh, const Raw& r, int T, int c, int pw, int l) {
   const int kb = c & 1, g = l / 16, cg = l % 16;
+  u32x4 k[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) k[u] = c * CH + 16 * pw + 4 * g + u < T ? r.k[u] : u32x4{0u, 0u, 0u, 0u};
   // The lane holds K[16 pw + 4 g + u][8 cg + e] (u = 0..3, e = 0..7). In the K St fragments (row tile pw,
   // k block cg / 4) its elements e = 0..3 and 4..7 of row u are the halves (cg % 4) / 2 of lanes
   // 16 (2 (cg % 2)) + 4 g + u and 16 (2 (cg % 2) + 1) + 4 g + u
@@ -458,8 +460,8 @@ __device__ __forceinline__ void stage(ScanLds& sh, const Raw& r, int c, int pw, 
   for (int u = 0; u < 4; ++u) {
     uint16_t* f = reinterpret_cast<uint16_t*>(&sh.Kf[kb][pw][cg / 4][0]) + 4 * ((cg % 4) / 2);
     const int ln = 16 * (2 * (cg % 2)) + 4 * g + u;
-    *reinterpret_cast<u32x2*>(f + 8 * kf_slot(ln, cg / 4)) = u32x2{r.k[u][0], r.k[u][1]};
-    *reinterpret_cast<u32x2*>(f + 8 * kf_slot(ln + 16, cg / 4)) = u32x2{r.k[u][2], r.k[u][3]};
+    *reinterpret_cast<u32x2*>(f + 8 * kf_slot(ln, cg / 4)) = u32x2{k[u][0], k[u][1]};
+    *reinterpret_cast<u32x2*>(f + 8 * kf_slot(ln + 16, cg / 4)) = u32x2{k[u][2], k[u][3]};
   }
   // In the state update's K^T fragments (Dk tile cg / 2, k block pw / 2) rows u = 0..3 of column 8 cg + e
   // are the half pw % 2 of lane 16 g + 8 (cg % 2) + e
@@ -467,7 +469,7 @@ __device__ __forceinline__ void stage(ScanLds& sh, const Raw& r, int c, int pw, 
   for (int e = 0; e < 8; ++e) {
     uint32_t x[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = (r.k[u][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+    for (int u = 0; u < 4; ++u) x[u] = (k[u][e >> 1] >> (16 * (e & 1))) & 0xffffu;
     uint16_t* f = reinterpret_cast<uint16_t*>(&sh.KTf[kb][cg / 2][pw / 2][0]) + 4 * (pw % 2);
     *reinterpret_cast<u32x2*>(f + 8 * ktf_slot(16 * g + 8 * (cg % 2) + e, cg / 2)) =
         u32x2{x[0] | (x[1] << 16), x[2] | (x[3] << 16)};
@@ -476,23 +478,16 @@ __device__ __forceinline__ void stage(ScanLds& sh, const Raw& r, int c, int pw, 
   {
     uint16_t* vt = reinterpret_cast<uint16_t*>(&sh.V[kb][pw][0]);
     const int tt = l / 4;
-    const uint16_t e4[4] = {(uint16_t)(r.v.x & 0xffffu), (uint16_t)(r.v.x >> 16), (uint16_t)(r.v.y & 0xffffu),
-                            (uint16_t)(r.v.y >> 16)};
+    const u32x2 vv = c * CH + 16 * pw + tt < T ? r.v : u32x2{0u, 0u};
+    const uint16_t e4[4] = {(uint16_t)(vv.x & 0xffffu), (uint16_t)(vv.x >> 16), (uint16_t)(vv.y & 0xffffu),
+                            (uint16_t)(vv.y >> 16)};
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) vt[(16 * (tt / 4) + 4 * (l % 4) + cc) * 4 + tt % 4] = e4[cc];
   }
   u32x4* tf = &sh.T[kb][0][0][0];
 #pragma unroll
   for (int j = 0; j < 3; ++j) tf[256 * j + 64 * pw + l] = r.t[j];
-  if (pw == 0) {
-    const int vb = c % 3;
-    const float G = chunk_g2(r.g, l);
-    const float GL = __shfl(G, kWave - 1, kWave);
-    sh.vec[vb][0][l] = r.be;
-    sh.vec[vb][1][l] = ex2(G);
-    sh.vec[vb][2][l] = ex2(GL - G);
-    sh.vec[vb][3][l] = ex2(GL);
-  }
+  (&sh.vec[c % 3][0][0])[64 * pw + l] = r.dec;
 }
 
 // the chain's step on chunk i: St (accumulators st, B fragments sh_ / sl_) -> St'
@@ -617,7 +612,7 @@ __global__ __launch_bounds__(kScanNT) void gdr_prefix_scan_kernel(PrefixArgs a) 
     for (int i = -1; i <= n; ++i) {
       const int c = i + 1;
       if (c < n) {
-        stage(sh, r, c, pw, l);
+        stage(sh, r, a.T, c, pw, l);
         if (c + 1 < n) load_raw(r, a, b, h, hk, dv0, c + 1, pw, l);
       }
       bar();
@@ -639,11 +634,19 @@ __global__ __launch_bounds__(kScanNT) void gdr_prefix_scan_kernel(PrefixArgs a) 
           mv = mma32(mf[tt][0], sh.xV[kb][0][l], mv);
           if (rt >= 2) mv = mma32(mf[tt][1], sh.xV[kb][1][l], mv);
           const f32x4 eg4 = *reinterpret_cast<const f32x4*>(&sh.vec[vb][1][16 * rt + g4]);
-          uint16_t* ob = a.out + (int64_t)b * a.T * vrow + (int64_t)h * a.Dv + dv0 + l % 16;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int tg = c * CH + 16 * rt + g4 + e;
-            if (tg < a.T) ob[(int64_t)tg * vrow] = f2bf(a.scale * (eg4[e] * qs[e] + mv[e]));
+          for (int e = 0; e < 4; ++e) sh.xO[16 * rt + g4 + e][l % 16] = f2bf(a.scale * (eg4[e] * qs[e] + mv[e]));
+        }
+        // this wave's 32 rows, half a row (16 bytes) per lane (its own LDS writes above land first); 2-byte
+        // stores when out is not 16-byte aligned
+        const int r = 32 * (w - 6) + l / 2, tg = c * CH + r;
+        if (tg < a.T) {
+          uint16_t* orow = a.out + ((int64_t)b * a.T + tg) * vrow + (int64_t)h * a.Dv + dv0 + 8 * (l % 2);
+          if ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
+            *reinterpret_cast<u32x4*>(orow) = *reinterpret_cast<const u32x4*>(&sh.xO[r][8 * (l % 2)]);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) orow[e] = sh.xO[r][8 * (l % 2) + e];
           }
         }
       }
