@@ -874,7 +874,7 @@ def bench_gdr(args):
                    "snapshot_GBps": round(snap_bytes / us["snapshot"] / 1e3, 1)},
         "roofline": {"bound": "mfma", "kernel": "chunked GDR prefix (gdr_prefix_prep + gdr_prefix_scan)", "achieved": round(tflops, 1),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4),
-                     "traffic": _measured_traffic("gdr_prefix")},
+                     "traffic": _measured_traffic("gdr_prefix_prep", "gdr_prefix_scan")},
         "at_scale": _snapshot_restore_at_scale(dev, H, D, CH),
         "cpu_baseline": cpu,
     }
