@@ -36,28 +36,6 @@ __device__ __forceinline__ float dpp(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
-// four independent 16-lane row reductions (max or sum over each DPP row; every lane of a row receives
-// its total), interleaved so the DPP latencies overlap
-__device__ __forceinline__ void row16_max4(float (&v)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0x128>(v[i]));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0x124>(v[i]));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0x4E>(v[i]));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = fmaxf(v[i], dpp<0xB1>(v[i]));
-}
-__device__ __forceinline__ void row16_sum4(float (&v)[4]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] += dpp<0x128>(v[i]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] += dpp<0x124>(v[i]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] += dpp<0x4E>(v[i]);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] += dpp<0xB1>(v[i]);
-}
 // 2^x with the hardware instruction: exact for the softmax's arguments x <= 0 down to -126, 0 below
 // (where the library exp2f would return a denormal)
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -79,20 +57,21 @@ struct AttnArgs {
 // LDS tiles of one 64-key step, 16-byte groups XOR-swizzled so that both the staging writes and the
 // MFMA fragment reads touch 8 distinct bank groups per 8 lanes:
 //   K   [key][D]   group g of key k stored at g ^ (k & 7)
-//   V^T [d][key]   key group g of column d stored at g ^ (d & 7)
-//   P   [row][key] (per wave) key group g of row r stored at g ^ (r & 7)
+//   V^T [d][key]   group g of column d stored at g ^ (d & 7); the keys of a row in the slot order of the
+//                  P V^T product: group 4 kk + g holds keys 32 kk + 4 g .. + 3, then 32 kk + 16 + 4 g .. + 3
 template <int D>
 __device__ __forceinline__ int k_off(int key, int grp) { return key * D + ((grp ^ (key & 7)) << 3); }
 __device__ __forceinline__ int vt_off(int d, int kgrp) { return d * kKB + ((kgrp ^ (d & 7)) << 3); }
-__device__ __forceinline__ int p_off(int r, int kgrp) { return r * kKB + ((kgrp ^ (r & 7)) << 3); }
 
 // Workgroup = (sequence, KV head, query tile of kMT rows, key split); 8 waves, wave w owns rows
-// [16 w, 16 w + 16) of the tile, so the online softmax of a row lives in one wave (DPP row
-// reductions, no cross-wave statistics). Per 64-key step: K and V^T are staged in LDS (the next
-// step's K / V are loaded into registers meanwhile), S = Q K^T from LDS fragments, P goes through
-// the wave's LDS slice into the A layout, and O += P V accumulates in registers; O is rescaled only
-// when a row's running max moved. Writes the unnormalised O, the row max (log2 domain) and the row
-// sum of its split.
+// [16 w, 16 w + 16) of the tile. Per 64-key step: K and V^T are staged in LDS (the next step's K / V
+// are loaded into registers meanwhile) and the wave forms the transposed products S^T = K Q^T and
+// O^T += V^T P^T on v_mfma_f32_16x16x32_bf16, so lane l holds 16 scores and 256 / 4 output values of
+// one query row (l % 16): the online softmax of a row is the lane's own, completed across its four
+// lane groups by two xor exchanges, and its probabilities are, as computed, the B operand of the
+// product with V (a 32-key block takes slots 8 g + j = keys 32 kk + 4 g + j and 32 kk + 16 + 4 g + j - 4,
+// which is where the two key tiles' accumulators put them). O is rescaled only when a row's running max
+// moved. Writes the unnormalised O, the row max (log2 domain) and the row sum of its split.
 template <int D>
 __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   constexpr int KC = D / 32;         // 32-wide k-chunks of the head dim (QK^T)
@@ -104,7 +83,6 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   __shared__ __align__(16) uint16_t sQ[kMT * D];  // [row][D], groups swizzled by row & 7 (as K)
   __shared__ __align__(16) uint16_t sK[kKB * D];
   __shared__ __align__(16) uint16_t sVt[D * kKB];
-  __shared__ __align__(16) uint16_t sP[kNW][kWR * kKB];
 
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
   const int per_pair = a.S * a.QT;                  // workgroups per (sequence, KV head)
@@ -223,6 +201,9 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     }
     if (tid < NVP) {
       const uint32_t* rw = reinterpret_cast<const uint32_t*>(vreg);
+      // keys 8 a .. + 3 and 8 a + 4 .. + 7 (a = vp_kg) are the halves (a % 4) / 2 of groups 4 (a / 4) +
+      // 2 (a % 2) and that + 1
+      const int grp = 4 * (vp_kg / 4) + 2 * (vp_kg % 2), half = 4 * ((vp_kg % 4) / 2);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {  // column vp_cq*4 + c: element c of each of the 8 key rows
         uint32_t e[8];
@@ -231,31 +212,27 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
           const uint32_t word = rw[j * 2 + c / 2];
           e[j] = (c & 1) ? (word >> 16) : (word & 0xffffu);
         }
-        const u32x4 packed = {e[0] | (e[1] << 16), e[2] | (e[3] << 16), e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
-        *reinterpret_cast<u32x4*>(&sVt[vt_off(vp_cq * 4 + c, vp_kg)]) = packed;
+        const int d = vp_cq * 4 + c;
+        *reinterpret_cast<u32x2*>(&sVt[vt_off(d, grp) + half]) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
+        *reinterpret_cast<u32x2*>(&sVt[vt_off(d, grp + 1) + half]) = u32x2{e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
       }
     }
   };
 
+  // o[ct] holds O[row][16 ct + 4 (l / 16) + e] of this lane's query row 16 w + l % 16
   f32x4 o[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) o[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[4], l_run[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.f;
-  }
-  uint16_t* pw = sP[w];
-  // the keys each of this lane's 4 rows sees are exactly [0, klim): the whole prefix, then the block keys
-  // its mask allows (a prefix of the block for the causal rows, all of it for the others)
-  int klim[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int t = (m0 + w * kWR + (l / 16) * 4 + i) / a.G;
+  float m_run = -INFINITY, l_run = 0.f;
+  // the keys the lane's row sees are exactly [0, klim): the whole prefix, then the block keys its mask
+  // allows (a prefix of the block for the causal rows, all of it for the others)
+  int klim;
+  {
+    const int t = (m0 + w * kWR + (l % 16)) / a.G;
     const bool all = a.mask_mode == 1 || (a.mask_mode == 2 && t >= a.n_clean);
-    klim[i] = all ? nk : min(nk, prefix + t + 1);
+    klim = all ? nk : min(nk, prefix + t + 1);
   }
+  const int g4 = 4 * (l / 16);
 
   for (int kb = kb0; kb < kb1; ++kb) {
     const int key0 = kb * kKB;
@@ -266,7 +243,7 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     // a wave with no row of the tile (the last tile of a canvas, e.g. rows 128..131 of 33 x 4) only helps
     // stage the keys: its fragment reads and MFMAs would be on padding (wave-uniform; no barrier inside)
     if (w * kWR >= rows) continue;
-    // ---- S = Q K^T: this wave's 16 rows x 64 keys (4 key tiles)
+    // ---- S^T = K Q^T: keys 16 kt + 4 (l / 16) + e of this lane's query row (4 key tiles)
     f32x4 sacc[4];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -277,85 +254,80 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
       for (int kt = 0; kt < 4; ++kt) {
         const bf16x8 kf =
             as_bf16x8(*reinterpret_cast<const u32x4*>(&sK[k_off<D>(kt * 16 + (l % 16), kc * 4 + l / 16)]));
-        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf, kf, sacc[kt], 0, 0, 0);
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf, sacc[kt], 0, 0, 0);
       }
     }
-    // ---- mask, scale, online softmax (rows (l/16)*4+i; a row's keys across 16 lanes x 4 tiles). The
-    // mask applies only on steps that reach the block keys or the cache end (uniform)
+    // ---- mask, scale, online softmax of the lane's row. The mask applies only on steps that reach the
+    // block keys or the cache end (uniform)
     const bool edge = key0 + kKB > prefix || key0 + kKB > nk;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sacc[kt][i] *= a.scale_log2;
+      for (int e = 0; e < 4; ++e) sacc[kt][e] *= a.scale_log2;
     if (edge) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const int key = key0 + kt * 16 + (l % 16);
+      for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sacc[kt][i] = key < klim[i] ? sacc[kt][i] : -INFINITY;
+        for (int e = 0; e < 4; ++e) sacc[kt][e] = key0 + 16 * kt + g4 + e < klim ? sacc[kt][e] : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3]));
+#pragma unroll
+    for (int kt = 1; kt < 4; ++kt)
+      mx = fmaxf(mx, fmaxf(fmaxf(sacc[kt][0], sacc[kt][1]), fmaxf(sacc[kt][2], sacc[kt][3])));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2_hw(m_run - m_use);
+    m_run = m_new;
+    // probabilities: the B fragments of the two 32-key blocks
+    u32x4 pb[2];
+    float ps = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      float p[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        p[e] = exp2_hw(sacc[2 * kk][e] - m_use);
+        p[4 + e] = exp2_hw(sacc[2 * kk + 1][e] - m_use);
       }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ps += p[e];
+      pb[kk] = u32x4{f2bf2(p[0], p[1]), f2bf2(p[2], p[3]), f2bf2(p[4], p[5]), f2bf2(p[6], p[7])};
     }
-    float mx[4], alpha[4], m_use[4], ps[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx[i] = fmaxf(fmaxf(sacc[0][i], sacc[1][i]), fmaxf(sacc[2][i], sacc[3][i]));
-    row16_max4(mx);
-    bool moved = false;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float m_new = fmaxf(m_run[i], mx[i]);
-      m_use[i] = m_new == -INFINITY ? 0.f : m_new;
-      alpha[i] = exp2_hw(m_run[i] - m_use[i]);
-      moved |= alpha[i] != 1.f;
-      m_run[i] = m_new;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = (l / 16) * 4 + i;  // row within the wave
-      ps[i] = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 4; kt += 2) {  // two key tiles per packed conversion
-        const float p0 = exp2_hw(sacc[kt][i] - m_use[i]), p1 = exp2_hw(sacc[kt + 1][i] - m_use[i]);
-        ps[i] += p0;
-        ps[i] += p1;
-        const uint32_t w2 = f2bf2(p0, p1);
-        const int k0 = kt * 16 + (l % 16), k1 = k0 + 16;
-        pw[p_off(rr, k0 >> 3) + (k0 & 7)] = (uint16_t)w2;
-        pw[p_off(rr, k1 >> 3) + (k1 & 7)] = (uint16_t)(w2 >> 16);
-      }
-    }
-    row16_sum4(ps);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) l_run[i] = l_run[i] * alpha[i] + ps[i];
+    ps += __shfl_xor(ps, 16, kWave);
+    ps += __shfl_xor(ps, 32, kWave);
+    l_run = l_run * alpha + ps;
     // rescale O only when some row's running max moved (rare once the max settles)
-    if (__ballot(moved)) {
+    if (__ballot(alpha != 1.f)) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[ct][i] *= alpha[i];
+        for (int e = 0; e < 4; ++e) o[ct][e] *= alpha;
     }
-    // ---- O += P V (P from this wave's LDS slice in the A layout, V^T fragments from LDS)
+    // ---- O^T += V^T P^T (V^T fragments from LDS, in the slot order of the probabilities)
 #pragma unroll
     for (int kk = 0; kk < kKB / 32; ++kk) {
-      const bf16x8 pf = as_bf16x8(*reinterpret_cast<const u32x4*>(&pw[p_off(l % 16, kk * 4 + l / 16)]));
+      const bf16x8 pf = as_bf16x8(pb[kk]);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
         const bf16x8 vf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sVt[vt_off(ct * 16 + (l % 16), kk * 4 + l / 16)]));
-        o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, vf, o[ct], 0, 0, 0);
+        o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[ct], 0, 0, 0);
       }
     }
   }
-  // ---- write this split's unnormalised O (bf16: half the partial traffic) and row stats (fp32)
+  // ---- write this split's unnormalised O (bf16: half the partial traffic; 8-byte row pieces) and row
+  // stats (fp32)
   uint16_t* op = a.opart + pbase * kMT * D;
+  const int r = w * kWR + (l % 16);
+  if (r < rows) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = w * kWR + (l / 16) * 4 + i;
-    if (r < rows) {
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct) op[(int64_t)r * D + ct * 16 + (l % 16)] = f2bf(o[ct][i]);
-      if ((l % 16) == 0) {
-        a.mpart[pbase * kMT + r] = m_run[i];
-        a.lpart[pbase * kMT + r] = l_run[i];
-      }
+    for (int ct = 0; ct < CT; ++ct)
+      *reinterpret_cast<u32x2*>(&op[(int64_t)r * D + ct * 16 + g4]) =
+          u32x2{f2bf2(o[ct][0], o[ct][1]), f2bf2(o[ct][2], o[ct][3])};
+    if (l < 16) {
+      a.mpart[pbase * kMT + r] = m_run;
+      a.lpart[pbase * kMT + r] = l_run;
     }
   }
 }
