@@ -228,74 +228,113 @@ struct AttnPrepArgs {
   float eps, log2_theta;
 };
 
+// kHG heads of one kind per wave: their rotary factors (one sincos per dim) are computed once. Large
+// calls (batch 64) take 4 heads per wave; small ones (batch 1) 1, where more waves in flight matter more
+template <int kHG>
 __global__ __launch_bounds__(kThreads) void attn_prep_kernel(AttnPrepArgs a) {
   constexpr int kMaxPer = 4;  // D <= 256
-  const int heads = a.Hq + 2 * a.Hkv;
+  const int qg = (a.Hq + kHG - 1) / kHG, kg = (a.Hkv + kHG - 1) / kHG;
+  const int groups = qg + 2 * kg;
   const int bb = blockIdx.y;  // sequence
-  const int64_t gw = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;  // (t, head) of bb
-  if (gw >= (int64_t)a.T * heads) return;  // whole waves exit together
+  const int64_t gw = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;  // (t, head group) of bb
+  if (gw >= (int64_t)a.T * groups) return;  // whole waves exit together
   const int l = threadIdx.x % kWave;
-  const int t = (int)(gw / heads), hh = (int)(gw % heads);
-  const int per = a.D / kWave;
-  const uint16_t* row = a.qkv + ((int64_t)bb * a.T + t) * a.qkv_st;
-  const uint16_t* src;
-  int kind;  // 0 q, 1 k, 2 v
-  int h;
-  if (hh < a.Hq) {
+  const int t = (int)(gw / groups), gi = (int)(gw % groups);
+  int kind, h0, nh;  // kind 0 q, 1 k, 2 v; heads h0 .. h0 + nh - 1
+  if (gi < qg) {
     kind = 0;
-    h = hh;
-    src = row + (int64_t)h * 2 * a.D;
-  } else if (hh < a.Hq + a.Hkv) {
+    h0 = gi * kHG;
+    nh = min(kHG, a.Hq - h0);
+  } else if (gi < qg + kg) {
     kind = 1;
-    h = hh - a.Hq;
-    src = row + (int64_t)a.Hq * 2 * a.D + (int64_t)h * a.D;
+    h0 = (gi - qg) * kHG;
+    nh = min(kHG, a.Hkv - h0);
   } else {
     kind = 2;
-    h = hh - a.Hq - a.Hkv;
-    src = row + (int64_t)a.Hq * 2 * a.D + (int64_t)a.Hkv * a.D + (int64_t)h * a.D;
+    h0 = (gi - qg - kg) * kHG;
+    nh = min(kHG, a.Hkv - h0);
   }
-  float v[kMaxPer], wnv[kMaxPer];
-  const uint16_t* wn = kind == 0 ? a.qn_w : a.kn_w;  // loaded with the row: one memory round trip
-  for (int j = 0; j < per; ++j) {
-    v[j] = bf2f(src[l * per + j]);
-    wnv[j] = bf2f(wn[l * per + j]);
-  }
+  const int per = a.D / kWave;
   const int64_t slot = (int64_t)a.slot0[bb] + t;
-  // rows past the cache capacity (a caller's overlong decode) write no K / V (one (t, head) per wave,
-  // so the whole wave leaves together)
+  // rows past the cache capacity (a caller's overlong decode) write no K / V (uniform per wave)
   if (kind != 0 && (slot < 0 || slot >= a.Lmax)) return;
+  const uint16_t* row = a.qkv + ((int64_t)bb * a.T + t) * a.qkv_st;
+  const uint16_t* src0 = kind == 0 ? row : kind == 1 ? row + (int64_t)a.Hq * 2 * a.D
+                                                     : row + (int64_t)a.Hq * 2 * a.D + (int64_t)a.Hkv * a.D;
+  const int64_t hstride = kind == 0 ? 2 * a.D : a.D;  // q heads sit beside their output gates
+  // every head of the group and the norm weights loaded together: one memory round trip
+  float v[kHG][kMaxPer], wnv[kMaxPer];
+  const uint16_t* wn = kind == 0 ? a.qn_w : a.kn_w;
+#pragma unroll
+  for (int hh = 0; hh < kHG; ++hh) {
+    const uint16_t* src = src0 + (int64_t)(h0 + (hh < nh ? hh : 0)) * hstride;
+#pragma unroll
+    for (int j = 0; j < kMaxPer; ++j)
+      if (j < per) v[hh][j] = bf2f(src[l * per + j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j)
+    if (j < per) wnv[j] = bf2f(wn[l * per + j]);
   if (kind == 2) {
-    uint16_t* dst = a.v_cache + (((int64_t)bb * a.Hkv + h) * a.Lmax + slot) * a.D + l * per;
-    for (int j = 0; j < per; ++j) dst[j] = f2bf(v[j]);
+#pragma unroll
+    for (int hh = 0; hh < kHG; ++hh) {
+      if (hh < nh) {
+        uint16_t* dst = a.v_cache + (((int64_t)bb * a.Hkv + h0 + hh) * a.Lmax + slot) * a.D + l * per;
+#pragma unroll
+        for (int j = 0; j < kMaxPer; ++j)
+          if (j < per) dst[j] = f2bf(v[hh][j]);
+      }
+    }
     return;
   }
-  float ss = 0.f;
-  for (int j = 0; j < per; ++j) ss = fmaf(v[j], v[j], ss);
-  const float inv = rsqrtf(wave_sum(ss) / a.D + a.eps);
-  for (int j = 0; j < per; ++j) v[j] = bf2f(f2bf(v[j] * inv * (1.f + wnv[j])));
   // partial rotary (rotate-half over the first `rot` dims): x1 = [0, rot/2), x2 = [rot/2, rot).
-  // half is a multiple of the per-lane width, so a lane's partner values sit in one other lane.
+  // half is a multiple of the per-lane width, so a lane's partner values sit in one other lane. The
+  // factors depend on the position and the dim only: one sincos per dim for the group's heads
   const int half = a.rot / 2;
   const int shift = half / per;
   const bool first = l * per < half;
   const int partner = first ? l + shift : l - shift;
   const float pos = (float)(a.pos0[bb] + t);
-  float y[kMaxPer];
-  for (int j = 0; j < per; ++j) {
+  float cs[kMaxPer], sn[kMaxPer];
+#pragma unroll
+  for (int j = 0; j < kMaxPer; ++j) {
+    cs[j] = 1.f;
+    sn[j] = 0.f;
     const int d = l * per + j;
-    const float other = __shfl(v[j], partner < kWave ? partner : l, kWave);
-    y[j] = v[j];
-    if (d < a.rot) {
+    if (j < per && d < a.rot) {
       const int i = first ? d : d - half;
       const float inv_freq = exp2f(-a.log2_theta * (2.f * i) / a.rot);  // theta^(-2i / rot)
-      float sn, cs;
-      sincosf(pos * inv_freq, &sn, &cs);
-      y[j] = first ? v[j] * cs - other * sn : v[j] * cs + other * sn;
+      sincosf(pos * inv_freq, &sn[j], &cs[j]);
     }
   }
-  uint16_t* dst = kind == 0 ? a.q_out + (((int64_t)bb * a.T + t) * a.Hq + h) * a.D + l * per
-                            : a.k_cache + (((int64_t)bb * a.Hkv + h) * a.Lmax + slot) * a.D + l * per;
-  for (int j = 0; j < per; ++j) dst[j] = f2bf(y[j]);
+#pragma unroll
+  for (int hh = 0; hh < kHG; ++hh) {
+    if (hh < nh) {  // uniform
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < kMaxPer; ++j)
+        if (j < per) ss = fmaf(v[hh][j], v[hh][j], ss);
+      const float inv = rsqrtf(wave_sum(ss) / a.D + a.eps);
+#pragma unroll
+      for (int j = 0; j < kMaxPer; ++j)
+        if (j < per) v[hh][j] = bf2f(f2bf(v[hh][j] * inv * (1.f + wnv[j])));
+      float y[kMaxPer];
+#pragma unroll
+      for (int j = 0; j < kMaxPer; ++j) {
+        if (j < per) {
+          const int d = l * per + j;
+          const float other = __shfl(v[hh][j], partner < kWave ? partner : l, kWave);
+          y[j] = v[hh][j];
+          if (d < a.rot) y[j] = first ? v[hh][j] * cs[j] - other * sn[j] : v[hh][j] * cs[j] + other * sn[j];
+        }
+      }
+      uint16_t* dst = kind == 0 ? a.q_out + (((int64_t)bb * a.T + t) * a.Hq + h0 + hh) * a.D + l * per
+                                : a.k_cache + (((int64_t)bb * a.Hkv + h0 + hh) * a.Lmax + slot) * a.D + l * per;
+#pragma unroll
+      for (int j = 0; j < kMaxPer; ++j)
+        if (j < per) dst[j] = f2bf(y[j]);
+    }
+  }
 }
 
 }  // namespace
@@ -402,10 +441,12 @@ extern "C" int trida_attn_prep(const uint16_t* qkv, int64_t qkv_row_stride, cons
               "attn_prep: bad sizes");
   TRIDA_CHECK(rot_dim >= 0 && rot_dim <= D && rot_dim % 2 == 0, TRIDA_ERR_ARG, "attn_prep: bad rotary dim");
   TRIDA_CHECK(qkv_row_stride >= (2 * Hq + 2 * Hkv) * D, TRIDA_ERR_ARG, "attn_prep: qkv row stride too small");
-  const int64_t waves = T * (Hq + 2 * Hkv);
+  const int hg = B * T >= 512 ? 4 : 1;  // heads per wave
+  const int64_t waves = T * (cdiv(Hq, hg) + 2 * cdiv(Hkv, hg));  // (row, group of hg heads of one kind)
   AttnPrepArgs a{qkv, q_norm_w, k_norm_w, pos0, slot0, q_out, k_cache, v_cache, (int)T, (int)Hq, (int)Hkv, (int)D,
                  (int)Lmax, (int)rot_dim, qkv_row_stride, eps, log2f(rope_theta)};
-  hipLaunchKernelGGL(attn_prep_kernel, dim3((unsigned)cdiv(waves, kThreads / kWave), (unsigned)B), dim3(kThreads), 0,
-                     static_cast<hipStream_t>(stream), a);
+  const dim3 grid((unsigned)cdiv(waves, kThreads / kWave), (unsigned)B);
+  if (hg == 4) hipLaunchKernelGGL(attn_prep_kernel<4>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
+  else hipLaunchKernelGGL(attn_prep_kernel<1>, grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream), a);
   return launch_status("attn_prep");
 }
