@@ -59,16 +59,39 @@ def test_attn_split_counts(gpu, splits):
     assert rel(out, ref) < TOL
 
 
-def test_attn_gate_and_crop(gpu):
-    """Output gate fused into the combine; a KV crop is only a prefix-length change."""
+@pytest.mark.parametrize("splits", [0, 1])
+def test_attn_gate_and_crop(gpu, splits):
+    """Output gate fused into the combine (or, with one key split, into the partial kernel's own output);
+    a KV crop is only a prefix-length change."""
     B, T, Hq, Hkv, D, L = 1, 8, 8, 2, 128, 64
     q, kc, vc = inputs(3, B, T, Hq, Hkv, D, L)
     gate = torch.randn(B, T, Hq, 2 * D).to(torch.bfloat16)[..., D:]  # interleaved [q | gate] per head
     for prefix in (30, 21):  # second call: the cache was cropped back to 21 committed keys
         ref = A.canvas_attention(q, kc, vc, [prefix], 0, gate=gate)
         out = kernels.attn_canvas(q.to(DEV), kc.to(DEV), vc.to(DEV), torch.tensor([prefix], dtype=torch.int32, device=DEV),
-                                  mask_mode=0, gate=gate.to(DEV))
+                                  mask_mode=0, gate=gate.to(DEV), splits=splits)
         assert rel(out, ref) < TOL
+
+
+def test_attn_one_split_equals_combine(gpu):
+    """One key split: the partial kernel's direct (gated) output is bitwise what the combine writes from
+    the same single split, row-major and in fragment order."""
+    g = torch.Generator().manual_seed(11)
+    B, T, Hq, Hkv, D, L = 1, 33, 16, 4, 256, 300
+    q = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
+    kc = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16).to(DEV)
+    vc = torch.randn(B, Hkv, L, D, generator=g).to(torch.bfloat16).to(DEV)
+    gate = torch.randn(B, T, Hq, D, generator=g).to(torch.bfloat16).to(DEV)
+    pl = torch.tensor([200], dtype=torch.int32, device=DEV)
+    ref = A.canvas_attention(q.cpu(), kc.cpu(), vc.cpu(), [200], 0, gate=gate.cpu())
+    one = kernels.attn_canvas(q, kc, vc, pl, mask_mode=0, gate=gate, splits=1)
+    assert rel(one, ref) < TOL
+    of = torch.zeros(kernels.ws_frag_numel(Hq * D), dtype=torch.bfloat16, device=DEV)
+    kernels.attn_canvas(q, kc, vc, pl, mask_mode=0, gate=gate, splits=1, out=of, out_frag=True)
+    from test_gpu_wsfused import _frag_mask
+    mask = _frag_mask(B * T, Hq * D)
+    assert torch.equal(kernels.ws_frag(one.view(B * T, -1)).view(torch.int16).cpu()[mask],
+                       of.view(torch.int16).cpu()[mask])
 
 
 def test_attn_clean_rows_equal_verify_rows(gpu):

@@ -52,6 +52,11 @@ struct AttnArgs {
   float* lpart;
   int T, Hq, Hkv, G, Lmax, S, QT, mask_mode, n_clean;
   float scale_log2;         // softmax scale * log2(e)
+  // with one key split (S == 1) the partial kernel writes the final, gated output as the combine would
+  const uint16_t* gate;     // row t, head h, dim d at gate + t * gate_st + h * gate_hs + d; or null
+  int64_t gate_st, gate_hs;
+  uint16_t* out;            // [B, T, Hq, D], or the weight-streaming GEMM's fragment order (frag)
+  int frag;
 };
 
 // LDS tiles of one 64-key step, 16-byte groups XOR-swizzled so that both the staging writes and the
@@ -140,7 +145,8 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   const int64_t pbase = ((((int64_t)b * a.Hkv + hk) * a.QT + qt) * a.S + s);
   if (kb0 >= kb1) {
     // no key of this split is visible to the tile: only the (empty) row stats are written and the
-    // combine skips the split without reading its O
+    // combine skips the split without reading its O (never with one split: its keys start at 0 and every
+    // row sees at least its own)
     for (int r = tid; r < rows; r += NT) {
       a.mpart[pbase * kMT + r] = -INFINITY;
       a.lpart[pbase * kMT + r] = 0.f;
@@ -316,10 +322,36 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
       }
     }
   }
+  const int r = w * kWR + (l % 16);
+  if (a.S == 1) {
+    // ---- the only split: O / l, rounded to bf16, then the gate, exactly as the combine computes it
+    if (r < rows) {
+      const int m = m0 + r, t = m / a.G, hq = hk * a.G + m % a.G;
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const int c = ct * 16 + g4;
+        float y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(o[ct][e])) * inv;
+        if (a.gate) {
+          const u32x2 gw = *reinterpret_cast<const u32x2*>(a.gate + ((int64_t)b * a.T + t) * a.gate_st +
+                                                           (int64_t)hq * a.gate_hs + c);
+          const float gv[4] = {__uint_as_float(gw.x << 16), __uint_as_float(gw.x & 0xffff0000u),
+                               __uint_as_float(gw.y << 16), __uint_as_float(gw.y & 0xffff0000u)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(y[e])) * (1.f / (1.f + __expf(-gv[e])));
+        }
+        uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * D + c)
+                               : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + c;
+        *reinterpret_cast<u32x2*>(dst) = u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
+      }
+    }
+    return;
+  }
   // ---- write this split's unnormalised O (bf16: half the partial traffic; 8-byte row pieces) and row
   // stats (fp32)
   uint16_t* op = a.opart + pbase * kMT * D;
-  const int r = w * kWR + (l % 16);
   if (r < rows) {
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
@@ -548,8 +580,10 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   float* mpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 2, 256));
   float* lpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 2, 256) + align_up(slots * kMT * 4, 256));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  AttnArgs a{q, k_cache, v_cache, prefix_len, opart, mpart, lpart, (int)T, (int)Hq, (int)Hkv, (int)G,
-             (int)Lmax, (int)S, (int)QT, mask_mode, (int)n_clean, scale * kLog2e};
+  TRIDA_CHECK(!frag || B * T <= 48, TRIDA_ERR_ARG, "attn_canvas_frag: the fragment order holds at most 48 rows");
+  AttnArgs a{q,           k_cache,         v_cache,          prefix_len, opart, mpart, lpart, (int)T, (int)Hq, (int)Hkv,
+             (int)G,      (int)Lmax,       (int)S,           (int)QT,    mask_mode, (int)n_clean, scale * kLog2e, gate,
+             gate_row_stride, gate_head_stride, out,         frag ? 1 : 0};
   const dim3 grid((unsigned)slots);
   switch (D) {
     case 64: hipLaunchKernelGGL(attn_partial_kernel<64>, grid, dim3(kNW * kWave), 0, st, a); break;
@@ -557,8 +591,7 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
     default: hipLaunchKernelGGL(attn_partial_kernel<256>, grid, dim3(kNW * kWave), 0, st, a); break;
   }
   int rc = launch_status("attn_canvas/partial");
-  if (rc) return rc;
-  TRIDA_CHECK(!frag || B * T <= 48, TRIDA_ERR_ARG, "attn_canvas_frag: the fragment order holds at most 48 rows");
+  if (rc || S == 1) return rc;  // one split: the partial kernel wrote the output
   CombineArgs c{opart, mpart, lpart, gate, out, (int)T, (int)Hq, (int)Hkv, (int)G, (int)D, (int)S, (int)QT,
                 gate_row_stride, gate_head_stride, frag ? 1 : 0};
   const int64_t rows_per_block = kCT / (D / 4);
