@@ -132,7 +132,10 @@ def prep_inputs(seed, B, T, Hk, Hv, Dk, Dv, Kc=4, pad=0):
 
 
 @pytest.mark.parametrize("shape", [(2, 5, 2, 4, 32, 16), (1, 33, 16, 16, 128, 128), (2, 3, 2, 2, 64, 64),
-                                   (1, 2, 16, 32, 128, 128)])
+                                   (1, 2, 16, 32, 128, 128),
+                                   # >= 512 rows: the wide launch, one 256-thread block per row (at T = 5 most
+                                   # source rows come from the window)
+                                   (16, 33, 16, 16, 128, 128), (64, 9, 2, 4, 64, 32), (128, 5, 2, 4, 32, 16)])
 def test_gdn_prep(gpu, shape):
     B, T, Hk, Hv, Dk, Dv = shape
     x, win, w, a, b, A_log, dt = prep_inputs(sum(shape), *shape, pad=8)
