@@ -106,24 +106,44 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   const int T = a.T;
   const int c0 = grp * NWV * CW + w * CW;  // this wave's first value column
 
-  // ---- 1. rows into LDS (zero past T), g and beta
-  for (int i = tid; i < TP * (DK / 8); i += NT) {
-    const int t = i / (DK / 8), gi = i % (DK / 8);
-    u32x4 kv = {0u, 0u, 0u, 0u}, qv = {0u, 0u, 0u, 0u};
-    if (t < T) {
-      const int64_t row = ((int64_t)b * T + t) * a.Hk + hk;
-      kv = *reinterpret_cast<const u32x4*>(a.k + row * DK + gi * 8);
-      qv = *reinterpret_cast<const u32x4*>(a.q + row * DK + gi * 8);
+  // ---- 1. rows into LDS (zero past T), g and beta. Every load of the staging is issued before the first
+  // store (rows past T read row 0, in bounds, and are zeroed when stored): one memory round trip
+  {
+    constexpr int NKQ = (TP * (DK / 8) + NT - 1) / NT, NVV = (TP * (NWV * CW / 8) + NT - 1) / NT;
+    u32x4 kv[NKQ], qv[NKQ], vv[NVV];
+#pragma unroll
+    for (int j = 0; j < NKQ; ++j) {
+      const int i = min(tid + j * NT, TP * (DK / 8) - 1);
+      const int t = i / (DK / 8), gi = i % (DK / 8);
+      const int64_t row = ((int64_t)b * T + (t < T ? t : 0)) * a.Hk + hk;
+      kv[j] = *reinterpret_cast<const u32x4*>(a.k + row * DK + gi * 8);
+      qv[j] = *reinterpret_cast<const u32x4*>(a.q + row * DK + gi * 8);
     }
-    *reinterpret_cast<u32x4*>(&sh.K[kq_off(t, gi)]) = kv;
-    *reinterpret_cast<u32x4*>(&sh.Q[kq_off(t, gi)]) = qv;
-  }
-  for (int i = tid; i < TP * (NWV * CW / 8); i += NT) {
-    const int t = i / (NWV * CW / 8), gi = i % (NWV * CW / 8);
-    u32x4 vv = {0u, 0u, 0u, 0u};
-    if (t < T)
-      vv = *reinterpret_cast<const u32x4*>(a.v + (((int64_t)b * T + t) * a.Hv + h) * a.Dv + grp * NWV * CW + gi * 8);
-    *reinterpret_cast<u32x4*>(&sV[t * NWV * CW + gi * 8]) = vv;
+#pragma unroll
+    for (int j = 0; j < NVV; ++j) {
+      const int i = min(tid + j * NT, TP * (NWV * CW / 8) - 1);
+      const int t = i / (NWV * CW / 8), gi = i % (NWV * CW / 8);
+      vv[j] = *reinterpret_cast<const u32x4*>(a.v + (((int64_t)b * T + (t < T ? t : 0)) * a.Hv + h) * a.Dv +
+                                              grp * NWV * CW + gi * 8);
+    }
+    const u32x4 z4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < NKQ; ++j) {
+      const int i = tid + j * NT;
+      if (i < TP * (DK / 8)) {
+        const int t = i / (DK / 8), gi = i % (DK / 8);
+        *reinterpret_cast<u32x4*>(&sh.K[kq_off(t, gi)]) = t < T ? kv[j] : z4;
+        *reinterpret_cast<u32x4*>(&sh.Q[kq_off(t, gi)]) = t < T ? qv[j] : z4;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NVV; ++j) {
+      const int i = tid + j * NT;
+      if (i < TP * (NWV * CW / 8)) {
+        const int t = i / (NWV * CW / 8), gi = i % (NWV * CW / 8);
+        *reinterpret_cast<u32x4*>(&sV[t * NWV * CW + gi * 8]) = t < T ? vv[j] : z4;
+      }
+    }
   }
   // this wave's slice of St as 16x16x32 B fragments: column n of tile nt is state row v = c0 + 16 nt + l % 16,
   // k = 32 kb + 8 (l / 16) .. + 8 contiguous in S[v][:], split into hi and lo
@@ -296,15 +316,28 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         const f32x4 mf = *reinterpret_cast<const f32x4*>(&sh.M[(it * 16 + l % 16) * PS + kt * 16 + (l / 16) * 4]);
         c = mm3(mf, vn[kt][nt], c);
       }
+      // into this wave's own columns of sV (read only by this wave, above): rows leave as 16-byte pieces
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = it * 16 + (l / 16) * 4 + i;
-        if (t < T) {
-          const float o = a.scale * (sh.rs[t] * qs[it][nt][i] + c[i]);
-          a.out[(((int64_t)b * T + t) * a.Hv + h) * a.Dv + c0 + nt * 16 + l % 16] = f2bf(o);
-        }
+        sV[t * NWV * CW + w * CW + nt * 16 + l % 16] = f2bf(a.scale * (sh.rs[t] * qs[it][nt][i] + c[i]));
       }
     }
+  // the wave's [TP][32] output: 4 lanes per row (64 bytes), rows < T (its own LDS writes land first)
+#pragma unroll
+  for (int j = 0; j < TP * 4 / kWave; ++j) {
+    const int q = l + j * kWave, t = q / 4, part = q % 4;
+    if (t < T) {
+      uint16_t* dst = a.out + (((int64_t)b * T + t) * a.Hv + h) * a.Dv + c0 + part * 8;
+      const uint16_t* src = &sV[t * NWV * CW + w * CW + part * 8];
+      if ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
+        *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
+      } else {  // out is only 2-byte aligned
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = src[e];
+      }
+    }
+  }
 }
 
 template <int NWV>
