@@ -12,15 +12,17 @@
 // S = e^g S; S += beta (v - S k) k^T; o = S q. Every exponent taken is <= 0.
 //
 // Workgroup = (sequence, value head, NWV x 32 value columns), one wave per 32 columns:
-//   1. K, Q (the head's rows) and the group's V columns into LDS; G by a wave prefix sum;
+//   1. K, Q (the head's rows) and the group's V columns into LDS, the wave's St slice into registers, all
+//      loads in flight together; G by a wave prefix sum;
 //   2. K K^T and Q K^T (16 x 16 tiles over Dk on v_mfma_f32_16x16x32_bf16, shared out among the waves),
 //      decayed and masked into A and M (the readout matrix of every row, causal or block-end);
-//   3. every wave forms K St and Q St for its columns (St from HBM as split bf16 hi + lo, K and Q exact)
-//      while wave 0 solves T = (I + A)^{-1} by forward substitution, one column per lane in registers;
+//   3. every wave forms K St and Q St for its columns (St from HBM as split bf16 hi + lo, K and Q exact);
+//      T = (I + A)^{-1} in fp32 over 16-row blocks: the diagonal blocks by forward substitution (one per
+//      wave), then one block diagonal at a time T[i][j] = -T[i][i] sum_k A[i][k] T[k][j];
 //   4. v_new = T R and o = diag(e^G or e^{G_L}) Q St + M v_new on v_mfma_f32_16x16x16_bf16: the
 //      accumulator layout of R and v_new (rows 4 (l / 16) + i of column l % 16) is the B operand of the
 //      16x16x16 MFMA, so they never leave registers. fp32 operands enter as hi + lo bf16 with
-//      hi*hi + hi*lo + lo*hi (about 16 mantissa bits); fp32 accumulation.
+//      hi*hi + hi*lo + lo*hi (about 16 mantissa bits; each split once); fp32 accumulation.
 #include <math.h>
 
 #include "common.h"
@@ -64,38 +66,48 @@ __device__ __forceinline__ void split8(f32x4 a, f32x4 b, u32x4& hi, u32x4& lo) {
   hi = u32x4{h[0], h[1], h[2], h[3]};
   lo = u32x4{l[0], l[1], l[2], l[3]};
 }
-// hi*hi + hi*lo + lo*hi of an fp32 A fragment and an fp32 B fragment (16x16x16 layouts)
-__device__ __forceinline__ f32x4 mm3(f32x4 a, f32x4 b, f32x4 c) {
-  s16x4 ah, al, bh, bl;
-  split4(a, ah, al);
-  split4(b, bh, bl);
-  c = mma16(ah, bh, c);
-  c = mma16(ah, bl, c);
-  return mma16(al, bh, c);
-}
-
 // K / Q rows [TP][128] bf16 in LDS, 16-byte groups XOR-swizzled by the row (fragment reads of 16 rows
 // touch distinct bank groups)
 __device__ __forceinline__ int kq_off(int r, int grp) { return r * DK + ((grp ^ (r & 15)) << 3); }
 
 template <int TP>
 struct BlockLds {
-  static constexpr int PS = TP + 4;  // fp32 row stride of the TP x TP matrices
+  static constexpr int RT = TP / 16;
+  static constexpr int PS = TP + 4;       // fp32 row stride of A and T
+  static constexpr int MS = RT * 32 + 8;  // bf16 row stride of M: per 16-column tile, 4 groups of [4 hi | 4 lo]
   uint16_t K[TP * DK];
   uint16_t Q[TP * DK];
-  float A[TP * PS];  // A, then T after the solve
-  float M[TP * PS];
+  float A[TP * PS];     // strictly lower A
+  float Tm[TP * PS];    // T = (I + A)^{-1} (lower block triangle)
+  uint16_t M[TP * MS];  // M split into bf16 hi + lo, laid out as 16x16x16 A fragments
   float G[TP];
   float beta[TP];
   float rs[TP];  // the row scale of the Q St term: e^{G_t} (causal) or e^{G_L} (block-end)
 };
 
+// K K^T / Q K^T job -> 16 x 16 tile: jobs < RT (RT + 1) / 2 walk the lower triangle of K K^T row by row,
+// the rest the RT x RT tiles of Q K^T
+template <int RT>
+__device__ __forceinline__ void job_tile(int job, int& ti, int& tj) {
+  constexpr int NKK = RT * (RT + 1) / 2;
+  if (job < NKK) {
+    ti = 0;
+#pragma unroll
+    for (int x = 1; x < RT; ++x)
+      if (job >= x * (x + 1) / 2) ti = x;
+    tj = job - ti * (ti + 1) / 2;
+  } else {
+    ti = (job - NKK) / RT;
+    tj = (job - NKK) % RT;
+  }
+}
+
 template <int TP, int NWV>
 __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   static_assert(TP % 16 == 0 && TP <= 64, "one chunk of <= 64 rows");
   constexpr int NT = NWV * kWave, RT = TP / 16;  // threads, row tiles
-  constexpr int PS = BlockLds<TP>::PS;
-  __shared__ BlockLds<TP> sh;
+  constexpr int PS = BlockLds<TP>::PS, MS = BlockLds<TP>::MS;
+  __shared__ __align__(16) BlockLds<TP> sh;
   __shared__ __align__(16) uint16_t sV[TP * NWV * CW];  // the group's value columns [TP][NWV * 32]
 
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
@@ -106,123 +118,129 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   const int T = a.T;
   const int c0 = grp * NWV * CW + w * CW;  // this wave's first value column
 
-  // ---- 1. rows into LDS (zero past T), g and beta. Every load of the staging is issued before the first
-  // store (rows past T read row 0, in bounds, and are zeroed when stored): one memory round trip
+  // ---- 1. every load of the block is issued before the first use (one memory round trip): g and beta of
+  // row l, the K / Q / V rows (rows past T read row 0, in bounds, and are zeroed when stored) and this
+  // wave's slice of St
+  u32x4 sth[4][2], stl[4][2];  // St as 16x16x32 B fragments (hi, lo): column n of tile nt is state row
+                               // v = c0 + 16 nt + n, k = 32 kb + 8 (l / 16) .. + 8 contiguous in S[v][:]
+  float graw, braw;
   {
+    const int64_t gi = ((int64_t)b * T + min(l, T - 1)) * a.Hv + h;
+    graw = a.g[gi];
+    braw = a.beta[gi];
     constexpr int NKQ = (TP * (DK / 8) + NT - 1) / NT, NVV = (TP * (NWV * CW / 8) + NT - 1) / NT;
     u32x4 kv[NKQ], qv[NKQ], vv[NVV];
+    f32x4 sraw[4][2][2];
 #pragma unroll
     for (int j = 0; j < NKQ; ++j) {
       const int i = min(tid + j * NT, TP * (DK / 8) - 1);
-      const int t = i / (DK / 8), gi = i % (DK / 8);
+      const int t = i / (DK / 8), gi8 = i % (DK / 8);
       const int64_t row = ((int64_t)b * T + (t < T ? t : 0)) * a.Hk + hk;
-      kv[j] = *reinterpret_cast<const u32x4*>(a.k + row * DK + gi * 8);
-      qv[j] = *reinterpret_cast<const u32x4*>(a.q + row * DK + gi * 8);
+      kv[j] = *reinterpret_cast<const u32x4*>(a.k + row * DK + gi8 * 8);
+      qv[j] = *reinterpret_cast<const u32x4*>(a.q + row * DK + gi8 * 8);
     }
 #pragma unroll
     for (int j = 0; j < NVV; ++j) {
       const int i = min(tid + j * NT, TP * (NWV * CW / 8) - 1);
-      const int t = i / (NWV * CW / 8), gi = i % (NWV * CW / 8);
+      const int t = i / (NWV * CW / 8), gi8 = i % (NWV * CW / 8);
       vv[j] = *reinterpret_cast<const u32x4*>(a.v + (((int64_t)b * T + (t < T ? t : 0)) * a.Hv + h) * a.Dv +
-                                              grp * NWV * CW + gi * 8);
+                                              grp * NWV * CW + gi8 * 8);
     }
-    const u32x4 z4 = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int j = 0; j < NKQ; ++j) {
-      const int i = tid + j * NT;
-      if (i < TP * (DK / 8)) {
-        const int t = i / (DK / 8), gi = i % (DK / 8);
-        *reinterpret_cast<u32x4*>(&sh.K[kq_off(t, gi)]) = t < T ? kv[j] : z4;
-        *reinterpret_cast<u32x4*>(&sh.Q[kq_off(t, gi)]) = t < T ? qv[j] : z4;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NVV; ++j) {
-      const int i = tid + j * NT;
-      if (i < TP * (NWV * CW / 8)) {
-        const int t = i / (NWV * CW / 8), gi = i % (NWV * CW / 8);
-        *reinterpret_cast<u32x4*>(&sV[t * NWV * CW + gi * 8]) = t < T ? vv[j] : z4;
-      }
-    }
-  }
-  // this wave's slice of St as 16x16x32 B fragments: column n of tile nt is state row v = c0 + 16 nt + l % 16,
-  // k = 32 kb + 8 (l / 16) .. + 8 contiguous in S[v][:], split into hi and lo
-  u32x4 sth[4][2], stl[4][2];
-  {
     const float* sb = a.state + ((int64_t)b * a.Hv + h) * a.Dv * DK;
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const float* sr = sb + (int64_t)(c0 + nt * 16 + l % 16) * DK + (l / 16) * 8;
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(sr + kb * 32);
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(sr + kb * 32 + 4);
-        split8(x0, x1, sth[kb][nt], stl[kb][nt]);
+        sraw[kb][nt][0] = *reinterpret_cast<const f32x4*>(sr + kb * 32);
+        sraw[kb][nt][1] = *reinterpret_cast<const f32x4*>(sr + kb * 32 + 4);
       }
     }
+    const u32x4 z4 = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < NKQ; ++j) {
+      const int i = tid + j * NT;
+      if (i < TP * (DK / 8)) {
+        const int t = i / (DK / 8), gi8 = i % (DK / 8);
+        *reinterpret_cast<u32x4*>(&sh.K[kq_off(t, gi8)]) = t < T ? kv[j] : z4;
+        *reinterpret_cast<u32x4*>(&sh.Q[kq_off(t, gi8)]) = t < T ? qv[j] : z4;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NVV; ++j) {
+      const int i = tid + j * NT;
+      if (i < TP * (NWV * CW / 8)) {
+        const int t = i / (NWV * CW / 8), gi8 = i % (NWV * CW / 8);
+        *reinterpret_cast<u32x4*>(&sV[t * NWV * CW + gi8 * 8]) = t < T ? vv[j] : z4;
+      }
+    }
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) split8(sraw[kb][nt][0], sraw[kb][nt][1], sth[kb][nt], stl[kb][nt]);
   }
   if (w == 0) {
     // G = inclusive prefix sum of g over the block (lanes past T add 0), and beta
-    const int t = l;
-    float gv = 0.f, bv = 0.f;
-    if (t < T) {
-      const int64_t gi = ((int64_t)b * T + t) * a.Hv + h;
-      gv = a.g[gi];
-      bv = a.beta[gi];
-    }
+    float gv = l < T ? graw : 0.f;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
       const float o = __shfl_up(gv, off, kWave);
       if (l >= off) gv += o;
     }
-    if (t < TP) {
-      sh.G[t] = gv;
-      sh.beta[t] = bv;
+    if (l < TP) {
+      sh.G[l] = gv;
+      sh.beta[l] = l < T ? braw : 0.f;
     }
   }
   __syncthreads();
 
-  // ---- 2. K K^T (lower tiles) and Q K^T (all tiles) -> A and M
+  // ---- 2. K K^T (lower tiles) and Q K^T (all tiles) -> A (fp32) and M (bf16 hi + lo); the wave's LDS reads
+  //         and MFMAs are all issued before its first store
   const float GL = sh.G[T - 1];
-  constexpr int NKK = RT * (RT + 1) / 2, NQK = RT * RT;
-  for (int job = w; job < NKK + NQK; job += NWV) {
-    const bool is_a = job < NKK;
-    int ti, tj;
-    if (is_a) {  // lower-triangular tile index -> (ti, tj), tj <= ti
-      ti = 0;
-      int r = job;
-      while (r > ti) {
-        r -= ti + 1;
-        ++ti;
+  {
+    constexpr int NKK = RT * (RT + 1) / 2, NJ = NKK + RT * RT, JPW = (NJ + NWV - 1) / NWV;
+    f32x4 cj[JPW];
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) {
+      const int job = min(w + jj * NWV, NJ - 1);
+      int ti, tj;
+      job_tile<RT>(job, ti, tj);
+      const uint16_t* X = job < NKK ? sh.K : sh.Q;
+      f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < DK / 32; ++kb) {
+        const u32x4 xa = *reinterpret_cast<const u32x4*>(&X[kq_off(ti * 16 + l % 16, kb * 4 + l / 16)]);
+        const u32x4 kbv = *reinterpret_cast<const u32x4*>(&sh.K[kq_off(tj * 16 + l % 16, kb * 4 + l / 16)]);
+        c = mma32(xa, kbv, c);
       }
-      tj = r;
-    } else {
-      ti = (job - NKK) / RT;
-      tj = (job - NKK) % RT;
+      cj[jj] = c;
     }
-    const uint16_t* X = is_a ? sh.K : sh.Q;
-    f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < DK / 32; ++kb) {
-      const u32x4 xa = *reinterpret_cast<const u32x4*>(&X[kq_off(ti * 16 + l % 16, kb * 4 + l / 16)]);
-      const u32x4 kbv = *reinterpret_cast<const u32x4*>(&sh.K[kq_off(tj * 16 + l % 16, kb * 4 + l / 16)]);
-      c = mma32(xa, kbv, c);
-    }
-    // c holds rows t = 16 ti + 4 (l / 16) + i, column s = 16 tj + l % 16
-    const int s = tj * 16 + l % 16;
-    const float Gs = sh.G[s];
+    for (int jj = 0; jj < JPW; ++jj) {
+      const int job = w + jj * NWV;
+      if (job < NJ) {
+        int ti, tj;
+        job_tile<RT>(job, ti, tj);
+        // cj holds rows t = 16 ti + 4 (l / 16) + i, column s = 16 tj + l % 16
+        const int s = tj * 16 + l % 16;
+        const float Gs = sh.G[s];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int t = ti * 16 + (l / 16) * 4 + i;
-      const float Gt = sh.G[t];
-      if (is_a) {
-        sh.A[t * PS + s] = s < t ? sh.beta[t] * c[i] * __expf(Gt - Gs) : 0.f;
-      } else {
-        const bool causal = a.causal_mode == 1 || t < a.num_clean;
-        float m = 0.f;
-        if (causal) m = s <= t ? c[i] * __expf(Gt - Gs) : 0.f;
-        else m = s < T ? c[i] * __expf(GL - Gs) : 0.f;
-        sh.M[t * PS + s] = m;
+        for (int i = 0; i < 4; ++i) {
+          const int t = ti * 16 + (l / 16) * 4 + i;
+          const float Gt = sh.G[t];
+          if (job < NKK) {
+            sh.A[t * PS + s] = s < t ? sh.beta[t] * cj[jj][i] * __expf(Gt - Gs) : 0.f;
+          } else {
+            const bool causal = a.causal_mode == 1 || t < a.num_clean;
+            float m = 0.f;
+            if (causal) m = s <= t ? cj[jj][i] * __expf(Gt - Gs) : 0.f;
+            else m = s < T ? cj[jj][i] * __expf(GL - Gs) : 0.f;
+            const uint16_t mh = f2bf(m);
+            uint16_t* mp = &sh.M[t * MS + tj * 32 + ((l % 16) / 4) * 8 + (l % 4)];
+            mp[0] = mh;
+            mp[4] = f2bf(m - bf2f(mh));
+          }
+        }
       }
     }
   }
@@ -233,8 +251,8 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   }
   __syncthreads();
 
-  // ---- 3. every wave: K St and Q St for its 32 columns (St hi + lo; K and Q exact), issued before
-  //         the solve so that the MFMAs run while wave 0's substitution occupies its VALU
+  // ---- 3. every wave: K St and Q St for its 32 columns (St hi + lo; K and Q exact), issued before the
+  //         inverse so that the MFMAs run under its VALU work
   f32x4 ks[RT][2], qs[RT][2];
 #pragma unroll
   for (int it = 0; it < RT; ++it)
@@ -257,26 +275,26 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         qs[it][nt] = mma32(qf, stl[kb][nt], qs[it][nt]);
       }
     }
-  // wave 0: T = (I + A)^{-1} by forward substitution, lane j holds column j in registers:
-  //         T[t][j] = [t == j] - sum_{s<t} A[t][s] T[s][j]  (A rows read as LDS broadcasts), then T -> LDS (over A)
-  if (w == 0) {
-    float tc[TP];
+  // T = (I + A)^{-1} in 16-row blocks, in fp32. Diagonal blocks by forward substitution, one block per wave
+  // (lane j < 16 holds column j in registers): T[t][j] = [t == j] - sum_{s<t} A[t][s] T[s][j]
+  for (int bi = w; bi < RT; bi += NWV) {
+    const float* ab = &sh.A[(bi * 16) * PS + bi * 16];
+    float tc[16];
 #pragma unroll
-    for (int t = 0; t < TP; ++t) {
+    for (int t = 0; t < 16; ++t) {
       float acc[4] = {0.f, 0.f, 0.f, 0.f};  // four independent chains (s mod 4), summed at the end
 #pragma unroll
       for (int s4 = 0; s4 < t; s4 += 4) {
-        const f32x4 ar = *reinterpret_cast<const f32x4*>(&sh.A[t * PS + s4]);
+        const f32x4 ar = *reinterpret_cast<const f32x4*>(&ab[t * PS + s4]);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (s4 + e < t) acc[e] = fmaf(ar[e], tc[s4 + e], acc[e]);
       }
-      tc[t] = (t == l ? 1.f : 0.f) - ((acc[0] + acc[1]) + (acc[2] + acc[3]));
+      tc[t] = (t == l % 16 ? 1.f : 0.f) - ((acc[0] + acc[1]) + (acc[2] + acc[3]));
     }
-    // every lane has read its last A row above (one wave: in order), so T may overwrite A
-    if (l < TP) {
+    if (l < 16) {
 #pragma unroll
-      for (int t = 0; t < TP; ++t) sh.A[t * PS + l] = tc[t];
+      for (int t = 0; t < 16; ++t) sh.Tm[(bi * 16 + t) * PS + bi * 16 + l] = tc[t];
     }
   }
   // R = diag(beta) (V - diag(e^G) K St), in the accumulator layout (the B operand of the 16x16x16 MFMA)
@@ -290,31 +308,94 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         const float vv = bf2f(sV[t * NWV * CW + w * CW + nt * 16 + l % 16]);
         ks[it][nt][i] = sh.beta[t] * (vv - __expf(sh.G[t]) * ks[it][nt][i]);
       }
-  __syncthreads();  // T is in LDS
+  __syncthreads();
+  // off-diagonal blocks, one block diagonal d at a time: T[i][j] = -T[i][i] Y, Y = sum_{k=j}^{i-1} A[i][k] T[k][j]
+  // (j = i - d; its T[k][j] come from diagonals < d). Lane l forms row l % 16, columns 4 (l / 16) .. + 4 of
+  // the block; Y passes through the destination block (one wave: its LDS reads and writes run in order)
+#pragma unroll
+  for (int d = 1; d < RT; ++d) {
+    for (int i = d + w; i < RT; i += NWV) {
+      const int j = i - d, r = l % 16, c4 = (l / 16) * 4;
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < d; ++kk) {
+        const int k = j + kk;
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 ar = *reinterpret_cast<const f32x4*>(&sh.A[(i * 16 + r) * PS + k * 16 + q4 * 4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f32x4 tr = *reinterpret_cast<const f32x4*>(&sh.Tm[(k * 16 + q4 * 4 + e) * PS + j * 16 + c4]);
+            y += ar[e] * tr;
+          }
+        }
+      }
+      float* dst = &sh.Tm[(i * 16 + r) * PS + j * 16 + c4];
+      *reinterpret_cast<f32x4*>(dst) = y;
+      f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const f32x4 tr = *reinterpret_cast<const f32x4*>(&sh.Tm[(i * 16 + r) * PS + i * 16 + q4 * 4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f32x4 yr = *reinterpret_cast<const f32x4*>(&sh.Tm[(i * 16 + q4 * 4 + e) * PS + j * 16 + c4]);
+          z -= tr[e] * yr;
+        }
+      }
+      *reinterpret_cast<f32x4*>(dst) = z;
+    }
+    __syncthreads();
+  }
 
-  // ---- 4. v_new = T R (T lower triangular: k-tiles kt <= it), then o = diag(rs) Q St + M v_new
+  // ---- 4. v_new = T R (T lower triangular: k-tiles kt <= it), then o = diag(rs) Q St + M v_new; every
+  //         operand is split into hi + lo once
+  s16x4 rh[RT][2], rl[RT][2];
+#pragma unroll
+  for (int kt = 0; kt < RT; ++kt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) split4(ks[kt][nt], rh[kt][nt], rl[kt][nt]);
   f32x4 vn[RT][2];
 #pragma unroll
-  for (int it = 0; it < RT; ++it)
+  for (int it = 0; it < RT; ++it) {
+    s16x4 th[RT], tl[RT];
+#pragma unroll
+    for (int kt = 0; kt <= it; ++kt)
+      split4(*reinterpret_cast<const f32x4*>(&sh.Tm[(it * 16 + l % 16) * PS + kt * 16 + (l / 16) * 4]), th[kt],
+             tl[kt]);
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt <= it; ++kt) {
-        const f32x4 tf = *reinterpret_cast<const f32x4*>(&sh.A[(it * 16 + l % 16) * PS + kt * 16 + (l / 16) * 4]);
-        c = mm3(tf, ks[kt][nt], c);
+        c = mma16(th[kt], rh[kt][nt], c);
+        c = mma16(th[kt], rl[kt][nt], c);
+        c = mma16(tl[kt], rh[kt][nt], c);
       }
       vn[it][nt] = c;
     }
+  }
+  s16x4 vh[RT][2], vl[RT][2];
 #pragma unroll
-  for (int it = 0; it < RT; ++it)
+  for (int kt = 0; kt < RT; ++kt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) split4(vn[kt][nt], vh[kt][nt], vl[kt][nt]);
+#pragma unroll
+  for (int it = 0; it < RT; ++it) {
+    s16x4 mh[RT], ml[RT];
+#pragma unroll
+    for (int kt = 0; kt < RT; ++kt) {
+      const u32x4 mf = *reinterpret_cast<const u32x4*>(&sh.M[(it * 16 + l % 16) * MS + kt * 32 + (l / 16) * 8]);
+      mh[kt] = __builtin_bit_cast(s16x4, u32x2{mf.x, mf.y});
+      ml[kt] = __builtin_bit_cast(s16x4, u32x2{mf.z, mf.w});
+    }
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kt = 0; kt < RT; ++kt) {
-        const f32x4 mf = *reinterpret_cast<const f32x4*>(&sh.M[(it * 16 + l % 16) * PS + kt * 16 + (l / 16) * 4]);
-        c = mm3(mf, vn[kt][nt], c);
+        c = mma16(mh[kt], vh[kt][nt], c);
+        c = mma16(mh[kt], vl[kt][nt], c);
+        c = mma16(ml[kt], vh[kt][nt], c);
       }
       // into this wave's own columns of sV (read only by this wave, above): rows leave as 16-byte pieces
 #pragma unroll
@@ -323,6 +404,7 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         sV[t * NWV * CW + w * CW + nt * 16 + l % 16] = f2bf(a.scale * (sh.rs[t] * qs[it][nt][i] + c[i]));
       }
     }
+  }
   // the wave's [TP][32] output: 4 lanes per row (64 bytes), rows < T (its own LDS writes land first)
 #pragma unroll
   for (int j = 0; j < TP * 4 / kWave; ++j) {
