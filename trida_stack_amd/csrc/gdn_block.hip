@@ -17,9 +17,9 @@
 //   2. K K^T and Q K^T (16 x 16 tiles over Dk on v_mfma_f32_16x16x32_bf16, shared out among the waves),
 //      decayed and masked into A and M (the readout matrix of every row, causal or block-end);
 //   3. every wave forms K St and Q St for its columns (St from HBM as split bf16 hi + lo, K and Q exact);
-//      T = (I + A)^{-1} in fp32 over 16-row blocks: the diagonal blocks by forward substitution (one per
-//      wave), then one block diagonal at a time T[i][j] = -T[i][i] sum_k A[i][k] T[k][j];
-//   4. v_new = T R and o = diag(e^G or e^{G_L}) Q St + M v_new on v_mfma_f32_16x16x16_bf16: the
+//      the 16 x 16 diagonal blocks T[i][i] = (I + A[i][i])^{-1} by forward substitution in fp32 (one per wave);
+//   4. v_new = T R by blocks, v_new_i = T[i][i] (R_i - sum_{k<i} A[i][k] v_new_k), and
+//      o = diag(e^G or e^{G_L}) Q St + M v_new on v_mfma_f32_16x16x16_bf16: the
 //      accumulator layout of R and v_new (rows 4 (l / 16) + i of column l % 16) is the B operand of the
 //      16x16x16 MFMA, so they never leave registers. fp32 operands enter as hi + lo bf16 with
 //      hi*hi + hi*lo + lo*hi (about 16 mantissa bits; each split once); fp32 accumulation.
@@ -73,13 +73,12 @@ __device__ __forceinline__ int kq_off(int r, int grp) { return r * DK + ((grp ^ 
 template <int TP>
 struct BlockLds {
   static constexpr int RT = TP / 16;
-  static constexpr int PS = TP + 4;       // fp32 row stride of A and T
-  static constexpr int MS = RT * 32 + 8;  // bf16 row stride of M: per 16-column tile, 4 groups of [4 hi | 4 lo]
+  static constexpr int PS = TP + 4;  // fp32 row stride of A
   uint16_t K[TP * DK];
   uint16_t Q[TP * DK];
-  float A[TP * PS];     // strictly lower A
-  float Tm[TP * PS];    // T = (I + A)^{-1} (lower block triangle)
-  uint16_t M[TP * MS];  // M split into bf16 hi + lo, laid out as 16x16x16 A fragments
+  float A[TP * PS];         // strictly lower A
+  float Tm[RT * 16 * 20];   // the diagonal 16 x 16 blocks of T = (I + A)^{-1}, row stride 20
+  u32x4 M[RT * RT * kWave];  // tile (i, j) of M as lane l's 16x16x16 A fragment {4 bf16 hi, 4 bf16 lo}
   float G[TP];
   float beta[TP];
   float rs[TP];  // the row scale of the Q St term: e^{G_t} (causal) or e^{G_L} (block-end)
@@ -106,7 +105,7 @@ template <int TP, int NWV>
 __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   static_assert(TP % 16 == 0 && TP <= 64, "one chunk of <= 64 rows");
   constexpr int NT = NWV * kWave, RT = TP / 16;  // threads, row tiles
-  constexpr int PS = BlockLds<TP>::PS, MS = BlockLds<TP>::MS;
+  constexpr int PS = BlockLds<TP>::PS;
   __shared__ __align__(16) BlockLds<TP> sh;
   __shared__ __align__(16) uint16_t sV[TP * NWV * CW];  // the group's value columns [TP][NWV * 32]
 
@@ -195,7 +194,8 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   __syncthreads();
 
   // ---- 2. K K^T (lower tiles) and Q K^T (all tiles) -> A (fp32) and M (bf16 hi + lo); the wave's LDS reads
-  //         and MFMAs are all issued before its first store
+  //         and MFMAs are all issued before its first store. The K rows go in as the A operand, so that each
+  //         lane ends with 4 consecutive columns of one row: the layout of A's rows and of M's fragments
   const float GL = sh.G[T - 1];
   {
     constexpr int NKK = RT * (RT + 1) / 2, NJ = NKK + RT * RT, JPW = (NJ + NWV - 1) / NWV;
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
       for (int kb = 0; kb < DK / 32; ++kb) {
         const u32x4 xa = *reinterpret_cast<const u32x4*>(&X[kq_off(ti * 16 + l % 16, kb * 4 + l / 16)]);
         const u32x4 kbv = *reinterpret_cast<const u32x4*>(&sh.K[kq_off(tj * 16 + l % 16, kb * 4 + l / 16)]);
-        c = mma32(xa, kbv, c);
+        c = mma32(kbv, xa, c);
       }
       cj[jj] = c;
     }
@@ -221,25 +221,28 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
       if (job < NJ) {
         int ti, tj;
         job_tile<RT>(job, ti, tj);
-        // cj holds rows t = 16 ti + 4 (l / 16) + i, column s = 16 tj + l % 16
-        const int s = tj * 16 + l % 16;
-        const float Gs = sh.G[s];
+        // cj holds row t = 16 ti + l % 16, columns s = 16 tj + 4 (l / 16) + i
+        const int t = ti * 16 + l % 16, s0 = tj * 16 + (l / 16) * 4;
+        const float Gt = sh.G[t];
+        const f32x4 Gs = *reinterpret_cast<const f32x4*>(&sh.G[s0]);
+        f32x4 r;
+        if (job < NKK) {
+          const float bt = sh.beta[t];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int t = ti * 16 + (l / 16) * 4 + i;
-          const float Gt = sh.G[t];
-          if (job < NKK) {
-            sh.A[t * PS + s] = s < t ? sh.beta[t] * cj[jj][i] * __expf(Gt - Gs) : 0.f;
-          } else {
-            const bool causal = a.causal_mode == 1 || t < a.num_clean;
-            float m = 0.f;
-            if (causal) m = s <= t ? cj[jj][i] * __expf(Gt - Gs) : 0.f;
-            else m = s < T ? cj[jj][i] * __expf(GL - Gs) : 0.f;
-            const uint16_t mh = f2bf(m);
-            uint16_t* mp = &sh.M[t * MS + tj * 32 + ((l % 16) / 4) * 8 + (l % 4)];
-            mp[0] = mh;
-            mp[4] = f2bf(m - bf2f(mh));
+          for (int i = 0; i < 4; ++i) r[i] = s0 + i < t ? bt * cj[jj][i] * __expf(Gt - Gs[i]) : 0.f;
+          *reinterpret_cast<f32x4*>(&sh.A[t * PS + s0]) = r;
+        } else {
+          const bool causal = a.causal_mode == 1 || t < a.num_clean;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int s = s0 + i;
+            if (causal) r[i] = s <= t ? cj[jj][i] * __expf(Gt - Gs[i]) : 0.f;
+            else r[i] = s < T ? cj[jj][i] * __expf(GL - Gs[i]) : 0.f;
           }
+          const uint32_t h01 = f2bf2(r.x, r.y), h23 = f2bf2(r.z, r.w);
+          const uint32_t l01 = f2bf2(r.x - __uint_as_float(h01 << 16), r.y - __uint_as_float(h01 & 0xffff0000u));
+          const uint32_t l23 = f2bf2(r.z - __uint_as_float(h23 << 16), r.w - __uint_as_float(h23 & 0xffff0000u));
+          sh.M[(ti * RT + tj) * kWave + l] = u32x4{h01, h23, l01, l23};
         }
       }
     }
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         qs[it][nt] = mma32(qf, stl[kb][nt], qs[it][nt]);
       }
     }
-  // T = (I + A)^{-1} in 16-row blocks, in fp32. Diagonal blocks by forward substitution, one block per wave
+  // the diagonal 16 x 16 blocks of T = (I + A)^{-1} in fp32 by forward substitution, one block per wave
   // (lane j < 16 holds column j in registers): T[t][j] = [t == j] - sum_{s<t} A[t][s] T[s][j]
   for (int bi = w; bi < RT; bi += NWV) {
     const float* ab = &sh.A[(bi * 16) * PS + bi * 16];
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
     }
     if (l < 16) {
 #pragma unroll
-      for (int t = 0; t < 16; ++t) sh.Tm[(bi * 16 + t) * PS + bi * 16 + l] = tc[t];
+      for (int t = 0; t < 16; ++t) sh.Tm[bi * 320 + t * 20 + l] = tc[t];
     }
   }
   // R = diag(beta) (V - diag(e^G) K St), in the accumulator layout (the B operand of the 16x16x16 MFMA)
@@ -309,82 +312,45 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         ks[it][nt][i] = sh.beta[t] * (vv - __expf(sh.G[t]) * ks[it][nt][i]);
       }
   __syncthreads();
-  // off-diagonal blocks, one block diagonal d at a time: T[i][j] = -T[i][i] Y, Y = sum_{k=j}^{i-1} A[i][k] T[k][j]
-  // (j = i - d; its T[k][j] come from diagonals < d). Lane l forms row l % 16, columns 4 (l / 16) .. + 4 of
-  // the block; Y passes through the destination block (one wave: its LDS reads and writes run in order)
-#pragma unroll
-  for (int d = 1; d < RT; ++d) {
-    for (int i = d + w; i < RT; i += NWV) {
-      const int j = i - d, r = l % 16, c4 = (l / 16) * 4;
-      f32x4 y = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < d; ++kk) {
-        const int k = j + kk;
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const f32x4 ar = *reinterpret_cast<const f32x4*>(&sh.A[(i * 16 + r) * PS + k * 16 + q4 * 4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const f32x4 tr = *reinterpret_cast<const f32x4*>(&sh.Tm[(k * 16 + q4 * 4 + e) * PS + j * 16 + c4]);
-            y += ar[e] * tr;
-          }
-        }
-      }
-      float* dst = &sh.Tm[(i * 16 + r) * PS + j * 16 + c4];
-      *reinterpret_cast<f32x4*>(dst) = y;
-      f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const f32x4 tr = *reinterpret_cast<const f32x4*>(&sh.Tm[(i * 16 + r) * PS + i * 16 + q4 * 4]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const f32x4 yr = *reinterpret_cast<const f32x4*>(&sh.Tm[(i * 16 + q4 * 4 + e) * PS + j * 16 + c4]);
-          z -= tr[e] * yr;
-        }
-      }
-      *reinterpret_cast<f32x4*>(dst) = z;
-    }
-    __syncthreads();
-  }
 
-  // ---- 4. v_new = T R (T lower triangular: k-tiles kt <= it), then o = diag(rs) Q St + M v_new; every
-  //         operand is split into hi + lo once
-  s16x4 rh[RT][2], rl[RT][2];
-#pragma unroll
-  for (int kt = 0; kt < RT; ++kt)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) split4(ks[kt][nt], rh[kt][nt], rl[kt][nt]);
-  f32x4 vn[RT][2];
-#pragma unroll
-  for (int it = 0; it < RT; ++it) {
-    s16x4 th[RT], tl[RT];
-#pragma unroll
-    for (int kt = 0; kt <= it; ++kt)
-      split4(*reinterpret_cast<const f32x4*>(&sh.Tm[(it * 16 + l % 16) * PS + kt * 16 + (l / 16) * 4]), th[kt],
-             tl[kt]);
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kt = 0; kt <= it; ++kt) {
-        c = mma16(th[kt], rh[kt][nt], c);
-        c = mma16(th[kt], rl[kt][nt], c);
-        c = mma16(tl[kt], rh[kt][nt], c);
-      }
-      vn[it][nt] = c;
-    }
-  }
+  // ---- 4. v_new by blocks: v_new_i = T[i][i] (R_i - sum_{k<i} A[i][k] v_new_k), then o = diag(rs) Q St + M v_new;
+  //         each fp32 operand is split into hi + lo once
   s16x4 vh[RT][2], vl[RT][2];
 #pragma unroll
-  for (int kt = 0; kt < RT; ++kt)
+  for (int it = 0; it < RT; ++it) {
+    s16x4 ah[RT], al[RT], th, tl;
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) split4(vn[kt][nt], vh[kt][nt], vl[kt][nt]);
+    for (int k = 0; k < it; ++k)
+      split4(*reinterpret_cast<const f32x4*>(&sh.A[(it * 16 + l % 16) * PS + k * 16 + (l / 16) * 4]), ah[k], al[k]);
+    split4(*reinterpret_cast<const f32x4*>(&sh.Tm[it * 320 + (l % 16) * 20 + (l / 16) * 4]), th, tl);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      f32x4 x = ks[it][nt];
+      if (it > 0) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < it; ++k) {
+          c = mma16(ah[k], vh[k][nt], c);
+          c = mma16(ah[k], vl[k][nt], c);
+          c = mma16(al[k], vh[k][nt], c);
+        }
+        x -= c;
+      }
+      s16x4 xh, xl;
+      split4(x, xh, xl);
+      f32x4 v = {0.f, 0.f, 0.f, 0.f};
+      v = mma16(th, xh, v);
+      v = mma16(th, xl, v);
+      v = mma16(tl, xh, v);
+      split4(v, vh[it][nt], vl[it][nt]);
+    }
+  }
 #pragma unroll
   for (int it = 0; it < RT; ++it) {
     s16x4 mh[RT], ml[RT];
 #pragma unroll
     for (int kt = 0; kt < RT; ++kt) {
-      const u32x4 mf = *reinterpret_cast<const u32x4*>(&sh.M[(it * 16 + l % 16) * MS + kt * 32 + (l / 16) * 8]);
+      const u32x4 mf = sh.M[(it * RT + kt) * kWave + l];
       mh[kt] = __builtin_bit_cast(s16x4, u32x2{mf.x, mf.y});
       ml[kt] = __builtin_bit_cast(s16x4, u32x2{mf.z, mf.w});
     }
