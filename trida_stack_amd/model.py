@@ -25,6 +25,7 @@ from __future__ import annotations
 
 import json
 import math
+import os
 from dataclasses import asdict, dataclass, field
 from typing import Dict, List, Optional, Tuple
 
@@ -235,6 +236,23 @@ class _Scratch:
         self.oattf = torch.empty(K.ws_frag_numel(cfg.n_heads * cfg.head_dim), **bf) if frag else None
 
 
+GEMM_CHOICES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_choices_gfx950.csv")
+
+
+def use_gemm_choices(path: str = GEMM_CHOICES) -> bool:
+    """Library GEMM solutions measured per shape of the batch-64 decode step on MI355X (hipBLASLt or rocBLAS,
+    whichever ran fastest; PyTorch TunableOp's results format, lookup only, no tuning at run time). Shapes
+    the file does not list keep the library's own heuristic; a file written for another library version
+    or GPU is ignored by TunableOp's validators. TRIDA_GEMM_CHOICES=0 turns it off."""
+    t = torch.cuda.tunable
+    if os.environ.get("TRIDA_GEMM_CHOICES", "1") == "0" or not os.path.exists(path):
+        return False
+    if not t.is_enabled():
+        t.tuning_enable(False)
+        t.enable(True)
+    return bool(t.read_file(path))
+
+
 class TridaRuntime:
     """The self-spec runtime over one model (see the module docstring for the mode semantics)."""
 
@@ -242,6 +260,8 @@ class TridaRuntime:
                  prefill_chunk: int = 512):
         self.cfg = cfg
         self.dev = torch.device(device)
+        if self.dev.type == "cuda":
+            use_gemm_choices()
         self.w = {k: v.to(self.dev) for k, v in weights.items()}
         self.prefill_chunk = prefill_chunk
         self.attn_layers = [i for i in range(cfg.n_layers) if cfg.is_attention(i)]
