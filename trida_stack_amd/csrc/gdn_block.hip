@@ -73,12 +73,12 @@ __device__ __forceinline__ int kq_off(int r, int grp) { return r * DK + ((grp ^ 
 template <int TP>
 struct BlockLds {
   static constexpr int RT = TP / 16;
-  static constexpr int PS = TP + 4;  // fp32 row stride of A
-  uint16_t K[TP * DK];
+  uint16_t K[TP * DK];  // K rows; in step 4 the output tile [TP][NWV * 32] on its way out
   uint16_t Q[TP * DK];
-  float A[TP * PS];         // strictly lower A
-  float Tm[RT * 16 * 20];   // the diagonal 16 x 16 blocks of T = (I + A)^{-1}, row stride 20
-  u32x4 M[RT * RT * kWave];  // tile (i, j) of M as lane l's 16x16x16 A fragment {4 bf16 hi, 4 bf16 lo}
+  // 16 x 16 tiles as lane l's 16x16x16 A fragment: row l % 16, columns 4 (l / 16) .. + 4
+  f32x4 A[RT * (RT + 1) / 2 * kWave];  // lower tiles (i, j <= i) of the strictly lower A, tile i (i + 1) / 2 + j
+  f32x4 Tm[RT * kWave];                // the diagonal tiles of T = (I + A)^{-1}
+  u32x4 M[RT * RT * kWave];            // tile (i, j) of M, {4 bf16 hi, 4 bf16 lo}
   float G[TP];
   float beta[TP];
   float rs[TP];  // the row scale of the Q St term: e^{G_t} (causal) or e^{G_L} (block-end)
@@ -102,12 +102,10 @@ __device__ __forceinline__ void job_tile(int job, int& ti, int& tj) {
 }
 
 template <int TP, int NWV>
-__global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
+__global__ __launch_bounds__(NWV* kWave, NWV == 4 && TP <= 48 ? 3 : 1) void gdr_block_kernel(BlockArgs a) {
   static_assert(TP % 16 == 0 && TP <= 64, "one chunk of <= 64 rows");
   constexpr int NT = NWV * kWave, RT = TP / 16;  // threads, row tiles
-  constexpr int PS = BlockLds<TP>::PS;
   __shared__ __align__(16) BlockLds<TP> sh;
-  __shared__ __align__(16) uint16_t sV[TP * NWV * CW];  // the group's value columns [TP][NWV * 32]
 
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
   const int groups = a.Dv / (NWV * CW);
@@ -118,8 +116,8 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   const int c0 = grp * NWV * CW + w * CW;  // this wave's first value column
 
   // ---- 1. every load of the block is issued before the first use (one memory round trip): g and beta of
-  // row l, the K / Q / V rows (rows past T read row 0, in bounds, and are zeroed when stored) and this
-  // wave's slice of St
+  // row l, the K / Q rows (rows past T read row 0, in bounds, and are zeroed when stored) and this wave's
+  // slice of St
   u32x4 sth[4][2], stl[4][2];  // St as 16x16x32 B fragments (hi, lo): column n of tile nt is state row
                                // v = c0 + 16 nt + n, k = 32 kb + 8 (l / 16) .. + 8 contiguous in S[v][:]
   float graw, braw;
@@ -127,8 +125,8 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
     const int64_t gi = ((int64_t)b * T + min(l, T - 1)) * a.Hv + h;
     graw = a.g[gi];
     braw = a.beta[gi];
-    constexpr int NKQ = (TP * (DK / 8) + NT - 1) / NT, NVV = (TP * (NWV * CW / 8) + NT - 1) / NT;
-    u32x4 kv[NKQ], qv[NKQ], vv[NVV];
+    constexpr int NKQ = (TP * (DK / 8) + NT - 1) / NT;
+    u32x4 kv[NKQ], qv[NKQ];
     f32x4 sraw[4][2][2];
 #pragma unroll
     for (int j = 0; j < NKQ; ++j) {
@@ -137,13 +135,6 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
       const int64_t row = ((int64_t)b * T + (t < T ? t : 0)) * a.Hk + hk;
       kv[j] = *reinterpret_cast<const u32x4*>(a.k + row * DK + gi8 * 8);
       qv[j] = *reinterpret_cast<const u32x4*>(a.q + row * DK + gi8 * 8);
-    }
-#pragma unroll
-    for (int j = 0; j < NVV; ++j) {
-      const int i = min(tid + j * NT, TP * (NWV * CW / 8) - 1);
-      const int t = i / (NWV * CW / 8), gi8 = i % (NWV * CW / 8);
-      vv[j] = *reinterpret_cast<const u32x4*>(a.v + (((int64_t)b * T + (t < T ? t : 0)) * a.Hv + h) * a.Dv +
-                                              grp * NWV * CW + gi8 * 8);
     }
     const float* sb = a.state + ((int64_t)b * a.Hv + h) * a.Dv * DK;
 #pragma unroll
@@ -163,14 +154,6 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         const int t = i / (DK / 8), gi8 = i % (DK / 8);
         *reinterpret_cast<u32x4*>(&sh.K[kq_off(t, gi8)]) = t < T ? kv[j] : z4;
         *reinterpret_cast<u32x4*>(&sh.Q[kq_off(t, gi8)]) = t < T ? qv[j] : z4;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NVV; ++j) {
-      const int i = tid + j * NT;
-      if (i < TP * (NWV * CW / 8)) {
-        const int t = i / (NWV * CW / 8), gi8 = i % (NWV * CW / 8);
-        *reinterpret_cast<u32x4*>(&sV[t * NWV * CW + gi8 * 8]) = t < T ? vv[j] : z4;
       }
     }
 #pragma unroll
@@ -230,7 +213,7 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
           const float bt = sh.beta[t];
 #pragma unroll
           for (int i = 0; i < 4; ++i) r[i] = s0 + i < t ? bt * cj[jj][i] * __expf(Gt - Gs[i]) : 0.f;
-          *reinterpret_cast<f32x4*>(&sh.A[t * PS + s0]) = r;
+          sh.A[(ti * (ti + 1) / 2 + tj) * kWave + l] = r;
         } else {
           const bool causal = a.causal_mode == 1 || t < a.num_clean;
 #pragma unroll
@@ -255,7 +238,18 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   __syncthreads();
 
   // ---- 3. every wave: K St and Q St for its 32 columns (St hi + lo; K and Q exact), issued before the
-  //         inverse so that the MFMAs run under its VALU work
+  //         inverse so that the MFMAs run under its VALU work; the wave's V in the accumulator layout (rows
+  //         4 (l / 16) + i, column l % 16; rows past T read row T - 1 and meet beta = 0) load meanwhile
+  uint16_t vr[RT][2][4];
+#pragma unroll
+  for (int it = 0; it < RT; ++it)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = min(it * 16 + (l / 16) * 4 + i, T - 1);
+      const uint16_t* vp = a.v + (((int64_t)b * T + t) * a.Hv + h) * a.Dv + c0 + l % 16;
+      vr[it][0][i] = vp[0];
+      vr[it][1][i] = vp[16];
+    }
   f32x4 ks[RT][2], qs[RT][2];
 #pragma unroll
   for (int it = 0; it < RT; ++it)
@@ -281,14 +275,14 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   // the diagonal 16 x 16 blocks of T = (I + A)^{-1} in fp32 by forward substitution, one block per wave
   // (lane j < 16 holds column j in registers): T[t][j] = [t == j] - sum_{s<t} A[t][s] T[s][j]
   for (int bi = w; bi < RT; bi += NWV) {
-    const float* ab = &sh.A[(bi * 16) * PS + bi * 16];
+    const f32x4* ab = &sh.A[(bi * (bi + 1) / 2 + bi) * kWave];  // row t, columns s4 .. + 4: lane t + 4 s4
     float tc[16];
 #pragma unroll
     for (int t = 0; t < 16; ++t) {
       float acc[4] = {0.f, 0.f, 0.f, 0.f};  // four independent chains (s mod 4), summed at the end
 #pragma unroll
       for (int s4 = 0; s4 < t; s4 += 4) {
-        const f32x4 ar = *reinterpret_cast<const f32x4*>(&ab[t * PS + s4]);
+        const f32x4 ar = ab[t + 4 * s4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (s4 + e < t) acc[e] = fmaf(ar[e], tc[s4 + e], acc[e]);
@@ -296,8 +290,9 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
       tc[t] = (t == l % 16 ? 1.f : 0.f) - ((acc[0] + acc[1]) + (acc[2] + acc[3]));
     }
     if (l < 16) {
+      float* tb = reinterpret_cast<float*>(&sh.Tm[bi * kWave]);
 #pragma unroll
-      for (int t = 0; t < 16; ++t) sh.Tm[bi * 320 + t * 20 + l] = tc[t];
+      for (int t = 0; t < 16; ++t) tb[(t + 4 * (l & ~3)) * 4 + (l & 3)] = tc[t];
     }
   }
   // R = diag(beta) (V - diag(e^G) K St), in the accumulator layout (the B operand of the 16x16x16 MFMA)
@@ -308,8 +303,7 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = it * 16 + (l / 16) * 4 + i;
-        const float vv = bf2f(sV[t * NWV * CW + w * CW + nt * 16 + l % 16]);
-        ks[it][nt][i] = sh.beta[t] * (vv - __expf(sh.G[t]) * ks[it][nt][i]);
+        ks[it][nt][i] = sh.beta[t] * (bf2f(vr[it][nt][i]) - __expf(sh.G[t]) * ks[it][nt][i]);
       }
   __syncthreads();
 
@@ -320,9 +314,8 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
   for (int it = 0; it < RT; ++it) {
     s16x4 ah[RT], al[RT], th, tl;
 #pragma unroll
-    for (int k = 0; k < it; ++k)
-      split4(*reinterpret_cast<const f32x4*>(&sh.A[(it * 16 + l % 16) * PS + k * 16 + (l / 16) * 4]), ah[k], al[k]);
-    split4(*reinterpret_cast<const f32x4*>(&sh.Tm[it * 320 + (l % 16) * 20 + (l / 16) * 4]), th, tl);
+    for (int k = 0; k < it; ++k) split4(sh.A[(it * (it + 1) / 2 + k) * kWave + l], ah[k], al[k]);
+    split4(sh.Tm[it * kWave + l], th, tl);
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       f32x4 x = ks[it][nt];
@@ -363,11 +356,12 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
         c = mma16(mh[kt], vl[kt][nt], c);
         c = mma16(ml[kt], vh[kt][nt], c);
       }
-      // into this wave's own columns of sV (read only by this wave, above): rows leave as 16-byte pieces
+      // into this wave's own columns of the output tile (K's LDS, unused since step 3): rows leave as
+      // 16-byte pieces
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = it * 16 + (l / 16) * 4 + i;
-        sV[t * NWV * CW + w * CW + nt * 16 + l % 16] = f2bf(a.scale * (sh.rs[t] * qs[it][nt][i] + c[i]));
+        sh.K[t * NWV * CW + w * CW + nt * 16 + l % 16] = f2bf(a.scale * (sh.rs[t] * qs[it][nt][i] + c[i]));
       }
     }
   }
@@ -377,7 +371,7 @@ __global__ __launch_bounds__(NWV* kWave) void gdr_block_kernel(BlockArgs a) {
     const int q = l + j * kWave, t = q / 4, part = q % 4;
     if (t < T) {
       uint16_t* dst = a.out + (((int64_t)b * T + t) * a.Hv + h) * a.Dv + c0 + part * 8;
-      const uint16_t* src = &sV[t * NWV * CW + w * CW + part * 8];
+      const uint16_t* src = &sh.K[t * NWV * CW + w * CW + part * 8];
       if ((reinterpret_cast<uintptr_t>(a.out) & 15) == 0) {
         *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(src);
       } else {  // out is only 2-byte aligned
