@@ -399,10 +399,10 @@ void launch_tp(const BlockArgs& a, int B, hipStream_t st) {
 bool gdr_block_supported(int64_t T, int64_t Dk, int64_t Dv) { return T >= 1 && T <= 64 && Dk == DK && Dv % 128 == 0; }
 
 int gdr_block_launch(const BlockArgs& a, int64_t B, hipStream_t stream) {
-  // small grids: one wave per 32 columns spreads a head over 4 workgroups; large grids: one workgroup per
-  // head shares the K K^T / Q K^T / inverse work among its 4 waves
-  if (B * a.Hv >= 128) launch_tp<4>(a, (int)B, stream);
-  else launch_tp<1>(a, (int)B, stream);
+  // one workgroup per (sequence, head, 128 value columns): its 4 waves share the K K^T / Q K^T and
+  // inverse work. At every grid size this beat one single-wave workgroup per 32 columns (which repeats
+  // that work per wave): at one sequence of 33 rows x 16 heads 10.4 against 14.1 us
+  launch_tp<4>(a, (int)B, stream);
   return launch_status("gdr_chunk/block");
 }
 
