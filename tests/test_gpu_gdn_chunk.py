@@ -184,3 +184,18 @@ def test_gdr_block_batch64_correctly_rounded(gpu, mode, nc):
     assert float((o != r16).double().mean()) < 1e-2
     assert float((o - r).abs().mean()) < 1.05 * float((r16 - r).abs().mean())
     assert rel(o, r) < 5e-3
+
+
+@pytest.mark.parametrize("T,nc", [(1, 1), (5, 2), (16, 16), (17, 3), (40, 40), (48, 20), (49, 49), (64, 31)])
+def test_gdr_block_row_tiles(gpu, T, nc):
+    """The canvas-block readout at each row-tile count (16, 32, 48 and 64 padded rows) and its edges,
+    GQA (2 key heads for 4 value heads), two 128-column value groups per head, 3 sequences; causal rows
+    for T == nc, else rows >= nc read the block-end state."""
+    shape = (3, T, 2, 4, 128, 256)
+    inp = gdr_inputs(500 + T, *shape)
+    mode = 1 if nc == T else 2
+    o_ref, _, _ = G.canvas(*inp, num_clean=nc, causal_mode=mode)
+    q, k, v, g, beta, s0 = to_dev(*inp)
+    o = kernels.gdr_chunk(q, k, v, g, beta, s0, causal_mode=mode, num_clean=nc)
+    assert rel(o, o_ref) < TOL_BF16, rel(o, o_ref)
+    assert torch.equal(s0.cpu(), inp[5]), "state_in must be left untouched"
