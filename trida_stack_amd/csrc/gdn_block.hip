@@ -66,6 +66,10 @@ __device__ __forceinline__ void split8(f32x4 a, f32x4 b, u32x4& hi, u32x4& lo) {
   hi = u32x4{h[0], h[1], h[2], h[3]};
   lo = u32x4{l[0], l[1], l[2], l[3]};
 }
+// workgroup barrier that orders LDS only: waits for this wave's LDS operations, not for its global loads
+// still in flight (__syncthreads' release fence would also wait for those)
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // K / Q rows [TP][128] bf16 in LDS, 16-byte groups XOR-swizzled by the row (fragment reads of 16 rows
 // touch distinct bank groups)
 __device__ __forceinline__ int kq_off(int r, int grp) { return r * DK + ((grp ^ (r & 15)) << 3); }
@@ -115,11 +119,8 @@ __global__ __launch_bounds__(NWV* kWave, NWV == 4 && TP <= 48 ? 3 : 1) void gdr_
   const int T = a.T;
   const int c0 = grp * NWV * CW + w * CW;  // this wave's first value column
 
-  // ---- 1. every load of the block is issued before the first use (one memory round trip): g and beta of
-  // row l, the K / Q rows (rows past T read row 0, in bounds, and are zeroed when stored) and this wave's
-  // slice of St
-  u32x4 sth[4][2], stl[4][2];  // St as 16x16x32 B fragments (hi, lo): column n of tile nt is state row
-                               // v = c0 + 16 nt + n, k = 32 kb + 8 (l / 16) .. + 8 contiguous in S[v][:]
+  // ---- 1. g and beta of row l and the K / Q rows (rows past T read row 0, in bounds, and are zeroed when
+  // stored), every load issued before the first store
   float graw, braw;
   {
     const int64_t gi = ((int64_t)b * T + min(l, T - 1)) * a.Hv + h;
@@ -127,7 +128,6 @@ __global__ __launch_bounds__(NWV* kWave, NWV == 4 && TP <= 48 ? 3 : 1) void gdr_
     braw = a.beta[gi];
     constexpr int NKQ = (TP * (DK / 8) + NT - 1) / NT;
     u32x4 kv[NKQ], qv[NKQ];
-    f32x4 sraw[4][2][2];
 #pragma unroll
     for (int j = 0; j < NKQ; ++j) {
       const int i = min(tid + j * NT, TP * (DK / 8) - 1);
@@ -135,16 +135,6 @@ __global__ __launch_bounds__(NWV* kWave, NWV == 4 && TP <= 48 ? 3 : 1) void gdr_
       const int64_t row = ((int64_t)b * T + (t < T ? t : 0)) * a.Hk + hk;
       kv[j] = *reinterpret_cast<const u32x4*>(a.k + row * DK + gi8 * 8);
       qv[j] = *reinterpret_cast<const u32x4*>(a.q + row * DK + gi8 * 8);
-    }
-    const float* sb = a.state + ((int64_t)b * a.Hv + h) * a.Dv * DK;
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const float* sr = sb + (int64_t)(c0 + nt * 16 + l % 16) * DK + (l / 16) * 8;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        sraw[kb][nt][0] = *reinterpret_cast<const f32x4*>(sr + kb * 32);
-        sraw[kb][nt][1] = *reinterpret_cast<const f32x4*>(sr + kb * 32 + 4);
-      }
     }
     const u32x4 z4 = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -156,10 +146,6 @@ __global__ __launch_bounds__(NWV* kWave, NWV == 4 && TP <= 48 ? 3 : 1) void gdr_
         *reinterpret_cast<u32x4*>(&sh.Q[kq_off(t, gi8)]) = t < T ? qv[j] : z4;
       }
     }
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) split8(sraw[kb][nt][0], sraw[kb][nt][1], sth[kb][nt], stl[kb][nt]);
   }
   if (w == 0) {
     // G = inclusive prefix sum of g over the block (lanes past T add 0), and beta
@@ -175,6 +161,22 @@ __global__ __launch_bounds__(NWV* kWave, NWV == 4 && TP <= 48 ? 3 : 1) void gdr_
     }
   }
   __syncthreads();
+
+  // this wave's slice of St, loaded while step 2 runs (its barrier orders LDS only): column n of tile nt of
+  // the B fragments is state row v = c0 + 16 nt + n, k = 32 kb + 8 (l / 16) .. + 8 contiguous in S[v][:]
+  f32x4 sraw[4][2][2];
+  {
+    const float* sb = a.state + ((int64_t)b * a.Hv + h) * a.Dv * DK;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const float* sr = sb + (int64_t)(c0 + nt * 16 + l % 16) * DK + (l / 16) * 8;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sraw[kb][nt][0] = *reinterpret_cast<const f32x4*>(sr + kb * 32);
+        sraw[kb][nt][1] = *reinterpret_cast<const f32x4*>(sr + kb * 32 + 4);
+      }
+    }
+  }
 
   // ---- 2. K K^T (lower tiles) and Q K^T (all tiles) -> A (fp32) and M (bf16 hi + lo); the wave's LDS reads
   //         and MFMAs are all issued before its first store. The K rows go in as the A operand, so that each
@@ -235,11 +237,16 @@ __global__ __launch_bounds__(NWV* kWave, NWV == 4 && TP <= 48 ? 3 : 1) void gdr_
     const bool causal = a.causal_mode == 1 || t < a.num_clean;
     sh.rs[t] = __expf(causal ? sh.G[t] : GL);
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 3. every wave: K St and Q St for its 32 columns (St hi + lo; K and Q exact), issued before the
   //         inverse so that the MFMAs run under its VALU work; the wave's V in the accumulator layout (rows
   //         4 (l / 16) + i, column l % 16; rows past T read row T - 1 and meet beta = 0) load meanwhile
+  u32x4 sth[4][2], stl[4][2];  // St split into hi and lo
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) split8(sraw[kb][nt][0], sraw[kb][nt][1], sth[kb][nt], stl[kb][nt]);
   uint16_t vr[RT][2][4];
 #pragma unroll
   for (int it = 0; it < RT; ++it)
