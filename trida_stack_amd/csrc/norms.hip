@@ -262,28 +262,43 @@ __global__ __launch_bounds__(kThreads) void attn_prep_kernel(AttnPrepArgs a) {
   const uint16_t* src0 = kind == 0 ? row : kind == 1 ? row + (int64_t)a.Hq * 2 * a.D
                                                      : row + (int64_t)a.Hq * 2 * a.D + (int64_t)a.Hkv * a.D;
   const int64_t hstride = kind == 0 ? 2 * a.D : a.D;  // q heads sit beside their output gates
-  // every head of the group and the norm weights loaded together: one memory round trip
-  float v[kHG][kMaxPer], wnv[kMaxPer];
+  // every head of the group and the norm weights loaded together: one memory round trip. At D = 256 a
+  // lane's 4 values move as one 8-byte piece when every row and pointer allows it (uniform per launch)
   const uint16_t* wn = kind == 0 ? a.qn_w : a.kn_w;
+  const bool vec4 = per == 4 && (a.qkv_st & 3) == 0 &&
+                    ((reinterpret_cast<uintptr_t>(a.qkv) | reinterpret_cast<uintptr_t>(wn) |
+                      reinterpret_cast<uintptr_t>(a.q_out) | reinterpret_cast<uintptr_t>(a.k_cache) |
+                      reinterpret_cast<uintptr_t>(a.v_cache)) & 7) == 0;
+  auto load_row = [&](const uint16_t* p, float* f) {
+    if (vec4) {
+      const u32x2 w = *reinterpret_cast<const u32x2*>(p);
+      f[0] = bf2f((uint16_t)(w.x & 0xffff));
+      f[1] = bf2f((uint16_t)(w.x >> 16));
+      f[2] = bf2f((uint16_t)(w.y & 0xffff));
+      f[3] = bf2f((uint16_t)(w.y >> 16));
+    } else {
 #pragma unroll
-  for (int hh = 0; hh < kHG; ++hh) {
-    const uint16_t* src = src0 + (int64_t)(h0 + (hh < nh ? hh : 0)) * hstride;
+      for (int j = 0; j < kMaxPer; ++j)
+        if (j < per) f[j] = bf2f(p[j]);
+    }
+  };
+  auto store_row = [&](uint16_t* p, const float* f) {
+    if (vec4) {
+      *reinterpret_cast<u32x2*>(p) = u32x2{f2bf2(f[0], f[1]), f2bf2(f[2], f[3])};
+    } else {
 #pragma unroll
-    for (int j = 0; j < kMaxPer; ++j)
-      if (j < per) v[hh][j] = bf2f(src[l * per + j]);
-  }
+      for (int j = 0; j < kMaxPer; ++j)
+        if (j < per) p[j] = f2bf(f[j]);
+    }
+  };
+  float v[kHG][kMaxPer], wnv[kMaxPer];
 #pragma unroll
-  for (int j = 0; j < kMaxPer; ++j)
-    if (j < per) wnv[j] = bf2f(wn[l * per + j]);
+  for (int hh = 0; hh < kHG; ++hh) load_row(src0 + (int64_t)(h0 + (hh < nh ? hh : 0)) * hstride + l * per, v[hh]);
+  load_row(wn + l * per, wnv);
   if (kind == 2) {
 #pragma unroll
     for (int hh = 0; hh < kHG; ++hh) {
-      if (hh < nh) {
-        uint16_t* dst = a.v_cache + (((int64_t)bb * a.Hkv + h0 + hh) * a.Lmax + slot) * a.D + l * per;
-#pragma unroll
-        for (int j = 0; j < kMaxPer; ++j)
-          if (j < per) dst[j] = f2bf(v[hh][j]);
-      }
+      if (hh < nh) store_row(a.v_cache + (((int64_t)bb * a.Hkv + h0 + hh) * a.Lmax + slot) * a.D + l * per, v[hh]);
     }
     return;
   }
@@ -328,11 +343,9 @@ __global__ __launch_bounds__(kThreads) void attn_prep_kernel(AttnPrepArgs a) {
           if (d < a.rot) y[j] = first ? v[hh][j] * cs[j] - other * sn[j] : v[hh][j] * cs[j] + other * sn[j];
         }
       }
-      uint16_t* dst = kind == 0 ? a.q_out + (((int64_t)bb * a.T + t) * a.Hq + h0 + hh) * a.D + l * per
-                                : a.k_cache + (((int64_t)bb * a.Hkv + h0 + hh) * a.Lmax + slot) * a.D + l * per;
-#pragma unroll
-      for (int j = 0; j < kMaxPer; ++j)
-        if (j < per) dst[j] = f2bf(y[j]);
+      store_row(kind == 0 ? a.q_out + (((int64_t)bb * a.T + t) * a.Hq + h0 + hh) * a.D + l * per
+                          : a.k_cache + (((int64_t)bb * a.Hkv + h0 + hh) * a.Lmax + slot) * a.D + l * per,
+                y);
     }
   }
 }
