@@ -383,8 +383,8 @@ class TridaRuntime:
     fused_gdn = False
 
     # canvas blocks of at least this many (sequence, value head) pairs take the single-block MFMA readout
-    # under "auto" (batch 64 x 16 heads: 49 vs 132-155 us per layer); smaller grids keep the token-recurrent
-    # kernel (batch 1: 12-16 vs 23 us), whose verify rows are bitwise the AR rows
+    # under "auto" (batch 64 x 16 heads: 30 vs 132-155 us per layer); smaller grids keep the token-recurrent
+    # kernel (batch 1: 7.9 vs 10.4 us), whose verify rows are bitwise the AR rows
     GDR_BLOCK_MIN_HEADS = 128
 
     def _chunked_gdr(self, T: int, gdn_mode: int, B: int = 1, persist: bool = True) -> bool:
