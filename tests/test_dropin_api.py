@@ -57,6 +57,58 @@ def test_looping_detects_repeated_blocks():
     assert D.looping([0] * 3 + block * 5) == 0        # 5 repeats fall short
 
 
+def _looping_brute(hist: list) -> int:
+    """decode.py:178-195 as written there: the tail compared with itself shifted, for each p in turn."""
+    n = len(hist)
+    for p in range(1, min(D.LOOP_MAX_PERIOD, n // D.LOOP_MIN_REPEATS) + 1):
+        span = max(p * D.LOOP_MIN_REPEATS, D.LOOP_MIN_SPAN)
+        if span > n:
+            break
+        tail = hist[n - span:]
+        if tail[p:] == tail[:-p]:
+            return p
+    return 0
+
+
+def test_looping_matches_shifted_tail_rule():
+    """The Z-array form answers exactly the shifted-tail comparison of every period."""
+    import random
+
+    rng = random.Random(7)
+    for _ in range(400):
+        p = rng.choice([1, 2, 3, 5, 16, 17, 64, 200, 256, 257])
+        block = [rng.randrange(3) for _ in range(p)]
+        hist = [rng.randrange(3) for _ in range(rng.randrange(40))] + block * rng.randrange(9)
+        hist += [rng.randrange(3) for _ in range(rng.randrange(3))]
+        assert D.looping(hist) == _looping_brute(hist)
+
+
+class _ByteTok:
+    """A byte-level tokenizer: id = one UTF-8 byte."""
+
+    def decode(self, ids, skip_special_tokens=False):
+        return bytes(ids).decode("utf-8", errors="replace")
+
+
+def test_incremental_detokenizer_streams_exact_text():
+    """The deltas concatenate to the full decode, and never end inside a multi-byte character."""
+    import random
+
+    text = "plain ascii, ünïcödé, 漢字かな, emoji 🙂🚀 and more text " * 3
+    ids = list(text.encode("utf-8"))
+    rng = random.Random(3)
+    for _ in range(20):
+        det = E.IncrementalDetokenizer(_ByteTok())
+        out, i = [], 0
+        while i < len(ids):
+            k = rng.randrange(1, 6)
+            piece = det.add(ids[i: i + k])
+            assert "\ufffd" not in piece
+            out.append(piece)
+            i += k
+        assert "".join(out) == text
+
+
 def test_ngram_loop_window():
     ng = D.NgramLoop(n=4, window=40, frac=0.5)
     hist = []

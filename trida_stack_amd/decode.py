@@ -157,54 +157,90 @@ LOOP_WINDOW = 1536
 LOOP_REPEAT_FRAC = 0.5
 
 
+def _z_array(r: list) -> list:
+    """z[i] = length of the longest common prefix of r and r[i:] (z[0] = len(r)); linear time
+    (Gusfield's Z algorithm)."""
+    m = len(r)
+    z = [0] * m
+    if m:
+        z[0] = m
+    lo = hi = 0  # [lo, hi) is the rightmost window known to match a prefix of r
+    for i in range(1, m):
+        k = min(hi - i, z[i - lo]) if i < hi else 0
+        while i + k < m and r[k] == r[i + k]:
+            k += 1
+        z[i] = k
+        if i + k > hi:
+            lo, hi = i, i + k
+    return z
+
+
 def looping(hist: list) -> int:
     """The period p of a block that ends `hist` repeated LOOP_MIN_REPEATS times back to back (the tail of
     max(p * LOOP_MIN_REPEATS, LOOP_MIN_SPAN) tokens equals itself shifted by p), for the smallest such
-    p <= LOOP_MAX_PERIOD; 0 when there is none."""
+    p <= LOOP_MAX_PERIOD; 0 when there is none (the rule of decode.py:178-195).
+
+    Read backwards from the last token, the tail has period p over `span` tokens exactly when the
+    reversed history agrees with itself shifted by p for span - p tokens, i.e. z[p] >= span - p for the
+    Z-array of the reversed tail: one linear pass answers every p at once."""
     n = len(hist)
-    for p in range(1, min(LOOP_MAX_PERIOD, n // LOOP_MIN_REPEATS) + 1):
+    top = min(LOOP_MAX_PERIOD, n // LOOP_MIN_REPEATS)
+    if top < 1 or max(LOOP_MIN_REPEATS, LOOP_MIN_SPAN) > n:
+        return 0
+    reach = min(n, max(top * LOOP_MIN_REPEATS, LOOP_MIN_SPAN))  # the longest span any p can need
+    z = _z_array(hist[: n - reach - 1: -1] if reach < n else hist[::-1])
+    for p in range(1, top + 1):
         span = max(p * LOOP_MIN_REPEATS, LOOP_MIN_SPAN)
         if span > n:
             break
-        if all(hist[i] == hist[i - p] for i in range(n - span + p, n)):
+        if z[p] >= span - p:
             return p
     return 0
 
 
 class NgramLoop:
     """Sliding-window repeat detector (decode.py:198-225): over the last `window` positions, the count
-    of positions whose `n`-token phrase already occurred in the window."""
+    of positions whose `n`-token phrase had already occurred among the `window` phrases before it.
+
+    The window is a ring of (phrase, was-a-repeat) records overwritten in place, with a multiset of
+    the phrases it holds; each add is O(n) for the phrase key and O(1) otherwise."""
 
     def __init__(self, n: int = LOOP_NGRAM, window: int = LOOP_WINDOW, frac: float = LOOP_REPEAT_FRAC):
         self.n, self.window, self.frac = n, window, frac
-        self.seen: dict = {}
-        self.recent = collections.deque()
-        self.repeats = 0
+        self._held = collections.Counter()        # phrase -> occurrences inside the ring
+        self._ring: list = [None] * window         # (phrase, repeat flag) records, oldest at _head when full
+        self._head = 0
+        self._filled = 0
+        self._repeats = 0                          # repeat flags set inside the ring
+        self._need = frac * window
 
     def add(self, hist: list) -> bool:
         """Feeds the history after one new token; True once the window is full and mostly repeats."""
         if len(hist) < self.n:
             return False
-        key = tuple(hist[-self.n:])
-        was = self.seen.get(key, 0) > 0
-        self.seen[key] = self.seen.get(key, 0) + 1
-        self.recent.append((key, was))
-        self.repeats += was
-        if len(self.recent) > self.window:
-            k, w = self.recent.popleft()
-            self.repeats -= w
-            left = self.seen[k] - 1
-            if left:
-                self.seen[k] = left
-            else:
-                del self.seen[k]
-        return len(self.recent) == self.window and self.repeats >= self.frac * self.window
+        phrase = tuple(hist[len(hist) - self.n:])
+        repeat = self._held[phrase] > 0            # judged against the window before this position
+        if self._filled == self.window:            # the record at _head leaves the window
+            old, old_rep = self._ring[self._head]
+            self._repeats -= old_rep
+            self._held[old] -= 1
+            if not self._held[old]:
+                del self._held[old]
+        else:
+            self._filled += 1
+        self._ring[self._head] = (phrase, repeat)
+        self._head = (self._head + 1) % self.window
+        self._held[phrase] += 1
+        self._repeats += repeat
+        return self._filled == self.window and self._repeats >= self._need
 
 
 class _Emitter:
-    """Applies max_new_tokens / EOS / the loop guard to emitted chunks and records stats
-    (decode.py:228-257). The loop guard is off unless the class attribute is set (the server's
-    --loop-guard)."""
+    """The stop rules of a decode (decode.py:228-257) applied to each chunk of new tokens: a token of
+    `eos` ends it before that token ("stop"), the max_new budget ends it after the token that fills it
+    ("length"), and the optional loop guard after the token that completes a loop ("repetition").
+    Records new_tokens / finish_reason / stop_token in `stats`. The guard is off unless the class
+    attribute is set (the server's --loop-guard)."""
 
     loop_guard = False
 
@@ -213,24 +249,39 @@ class _Emitter:
         self.hist: list = []
         self.ngram = NgramLoop()
 
+    def _loops(self) -> bool:
+        periodic = len(self.hist) % 8 == 0 and looping(self.hist) > 0
+        return periodic or self.ngram.add(self.hist)
+
     def __call__(self, toks: list) -> list:
-        out = []
-        for t in toks:
-            if t in self.eos:
-                self.done = True
-                self.stats.finish_reason = "stop"
-                self.stats.stop_token = t
-                break
-            out.append(t)
-            self.hist.append(t)
-            if self.stats.new_tokens + len(out) >= self.max_new:
-                self.done = True
-                self.stats.finish_reason = "length"
-                break
-            if self.loop_guard and ((len(self.hist) % 8 == 0 and looping(self.hist)) or self.ngram.add(self.hist)):
-                self.done = True
-                self.stats.finish_reason = "repetition"
-                break
+        toks = list(toks)
+        # where the chunk ends before the guard: at the first EOS, or once the budget is spent (the
+        # budget always admits one more token, as a decode step always emits at least one)
+        eos_at = next((i for i, t in enumerate(toks) if t in self.eos), len(toks))
+        budget = max(1, self.max_new - self.stats.new_tokens)
+        limit, reason = eos_at, None
+        if budget <= eos_at:
+            limit, reason = budget, "length"
+        elif eos_at < len(toks):
+            reason = "stop"
+        out = toks[:limit]
+        if self.loop_guard:
+            # the guard inspects each token that is kept, except the one that spends the budget
+            guarded = limit - 1 if reason == "length" else limit
+            for i in range(guarded):
+                self.hist.append(out[i])
+                if self._loops():
+                    out, reason = out[: i + 1], "repetition"
+                    break
+            else:
+                self.hist.extend(out[guarded:])
+        else:
+            self.hist.extend(out)
+        if reason is not None:
+            self.done = True
+            self.stats.finish_reason = reason
+            if reason == "stop":
+                self.stats.stop_token = toks[eos_at]
         self.stats.new_tokens += len(out)
         return out
 

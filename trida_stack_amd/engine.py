@@ -20,9 +20,12 @@ or a prebuilt TridaRuntime. Nothing is downloaded.
 """
 from __future__ import annotations
 
+import contextlib
+import itertools
 import os
 import threading
 import time
+from dataclasses import dataclass, field
 from typing import Iterator, Optional, Union
 
 from .decode import DecodeStats, SamplingParams, ar_generate, diffusion_generate, selfspec_generate
@@ -33,31 +36,75 @@ SHAPES = {"random-4b": HybridConfig.four_b, "random-tiny": HybridConfig.tiny}
 
 
 class IncrementalDetokenizer:
-    """Text deltas of a growing id sequence, holding back an incomplete trailing character
-    (engine.py:27-44)."""
+    """Streams the text of a growing list of token ids.
 
-    def __init__(self, tokenizer):
+    Text is final up to `_flushed` ids. Each call decodes the unflushed ids together with up to
+    `context` flushed ids before them (the ids a tokenizer needs to place spaces and merges), and
+    returns what that decode adds to the decode of the context alone. An incomplete UTF-8 sequence
+    at the end (the replacement character) holds the text back until a later id completes it."""
+
+    def __init__(self, tokenizer, context: int = 4):
         self.tok = tokenizer
+        self.context = int(context)
         self.ids: list = []
-        self.prefix = 0
-        self.read = 0
+        self._flushed = 0
+
+    def _text(self, ids: list) -> str:
+        return self.tok.decode(ids, skip_special_tokens=False) if ids else ""
 
     def add(self, new_ids: list) -> str:
-        self.ids.extend(new_ids)
-        before = self.tok.decode(self.ids[self.prefix: self.read], skip_special_tokens=False)
-        text = self.tok.decode(self.ids[self.prefix:], skip_special_tokens=False)
-        if text.endswith("�"):
+        self.ids.extend(int(t) for t in new_ids)
+        lo = max(0, self._flushed - self.context)
+        left = self._text(self.ids[lo: self._flushed])
+        full = self._text(self.ids[lo:])
+        if full.endswith("�") or not full.startswith(left):
             return ""
-        self.prefix, self.read = self.read, len(self.ids)
-        return text[len(before):]
+        self._flushed = len(self.ids)
+        return full[len(left):]
 
 
+def _is_prefix(head: list, seq: list) -> bool:
+    return len(head) <= len(seq) and seq[: len(head)] == head
+
+
+def _snap_tokens(snap) -> list:
+    """Sequence 0's committed ids in a SeqCache.snapshot() tuple."""
+    return snap[4][0]
+
+
+@dataclass(eq=False)
 class _Slot:
-    """One conversation's cache and its resumable snapshots (name -> SeqCache.snapshot())."""
-    __slots__ = ("cache", "snaps", "used")
+    """One conversation: its cache (one sequence), the snapshots it can rewind to (mark name ->
+    SeqCache.snapshot()) and a least-recently-used stamp."""
+    cache: object
+    snaps: dict = field(default_factory=dict)
+    used: int = 0
 
-    def __init__(self, cache):
-        self.cache, self.snaps, self.used = cache, {}, time.monotonic()
+    def held(self) -> list:
+        return self.cache.tokens[0]
+
+    def resume_points(self):
+        """(ids, snapshot) of every point this slot can continue from: the live cache (snapshot None),
+        then each snapshot."""
+        yield self.held(), None
+        for snap in self.snaps.values():
+            yield _snap_tokens(snap), snap
+
+    def drop_stale(self) -> None:
+        """Forgets the snapshots that are no longer a prefix of what the cache holds."""
+        held = self.held()
+        self.snaps = {name: snap for name, snap in self.snaps.items() if _is_prefix(_snap_tokens(snap), held)}
+
+
+def _resume_marks(prompt: list, im_start: int) -> list:
+    """(name, position) of the prompt's snapshot points, in prefill order: "system" at the second
+    <|im_start|> when the prompt opens with one (the end of the system block), and "last" at the last
+    <|im_start|> (before the generation header)."""
+    starts = [i for i, t in enumerate(prompt) if t == im_start]
+    marks = [("system", starts[1])] if len(starts) > 1 and starts[0] == 0 else []
+    if starts:
+        marks.append(("last", starts[-1]))
+    return marks
 
 
 def _load_tokenizer(path: Optional[str]):
@@ -117,6 +164,7 @@ class Engine:
         self.use_prompt_cache = bool(prompt_cache)
         self.cache_slots = max(1, int(cache_slots))
         self.max_context = int(max_context)
+        self._clock = itertools.count(1)
         self.reset_cache()
         self.lock = threading.Lock()
         self.last_stats: Optional[dict] = None
@@ -131,120 +179,139 @@ class Engine:
         return self.rt.make_cache(1, max_len=self.max_context)
 
     def reset_cache(self) -> None:
-        self.cur = _Slot(self._new_cache())
+        self.cur = _Slot(self._new_cache(), used=next(self._clock))
         self.slots = [self.cur]
 
     def cached_tokens(self) -> list:
-        return [len(s.cache.tokens[0]) for s in self.slots]
+        return [len(slot.held()) for slot in self.slots]
+
+    def _best_resume(self, prompt: list):
+        """(slot, snapshot or None) of the longest resumable point that is a proper, non-empty prefix of
+        `prompt` (the first one found on equal lengths), or None."""
+        best_len, best = 0, None
+        for slot in self.slots:
+            for ids, snap in slot.resume_points():
+                if best_len < len(ids) < len(prompt) and _is_prefix(ids, prompt):
+                    best_len, best = len(ids), (slot, snap)
+        return best
+
+    def _free_slot(self) -> _Slot:
+        """An empty slot, else a new one while fewer than cache_slots exist, else the least recently
+        used slot, emptied."""
+        for slot in self.slots:
+            if not slot.held():
+                return slot
+        if len(self.slots) < self.cache_slots:
+            self.slots.append(_Slot(self._new_cache()))
+            return self.slots[-1]
+        slot = min(self.slots, key=lambda s: s.used)
+        slot.cache, slot.snaps = self._new_cache(), {}
+        return slot
 
     def _position_cache(self, prompt: list) -> None:
-        """Points self.cur at the slot holding the longest reusable proper prefix of `prompt` (its live
-        tokens or a snapshot, restored), else at an empty slot, a new one, or the least recently used one
-        (emptied) (engine.py:146-183)."""
-        def usable(tokens):
-            return 0 < len(tokens) < len(prompt) and prompt[: len(tokens)] == tokens
-
+        """Makes self.cur the slot to continue `prompt` from: the one holding its longest reusable proper
+        prefix (live, or a snapshot restored into the slot's cache), else a free slot (the prompt
+        cache of engine.py:146-183)."""
         if not self.use_prompt_cache:
             self.reset_cache()
             return
-        best, best_slot, best_snap = 0, None, None
-        for sl in self.slots:
-            live = sl.cache.tokens[0]
-            if usable(live) and len(live) > best:
-                best, best_slot, best_snap = len(live), sl, None
-            for snap in sl.snaps.values():
-                if usable(snap[4][0]) and len(snap[4][0]) > best:
-                    best, best_slot, best_snap = len(snap[4][0]), sl, snap
-        if best_slot is not None:
-            self.cur = best_slot
-            if best_snap is not None:
-                best_slot.cache.restore(best_snap)
-            held = best_slot.cache.tokens[0]
-            best_slot.snaps = {k: v for k, v in best_slot.snaps.items()
-                               if len(v[4][0]) <= len(held) and held[: len(v[4][0])] == v[4][0]}
-        elif any(len(sl.cache.tokens[0]) == 0 for sl in self.slots):
-            self.cur = next(sl for sl in self.slots if len(sl.cache.tokens[0]) == 0)
-        elif len(self.slots) < self.cache_slots:
-            self.cur = _Slot(self._new_cache())
-            self.slots.append(self.cur)
+        found = self._best_resume(prompt)
+        if found is None:
+            slot = self._free_slot()
         else:
-            self.cur = min(self.slots, key=lambda s: s.used)
-            self.cur.cache, self.cur.snaps = self._new_cache(), {}
-        self.cur.used = time.monotonic()
+            slot, snap = found
+            if snap is not None:
+                slot.cache.restore(snap)
+            slot.drop_stale()
+        slot.used = next(self._clock)
+        self.cur = slot
 
     def _prefill_to_snapshot(self, prompt: list) -> None:
-        """Prefills up to the end of the system block and up to the last <|im_start|>, snapshotting at
-        each (engine.py:185-198)."""
+        """Prefills the prompt up to each snapshot point it has not reached yet and snapshots there
+        (engine.py:185-198)."""
         if not self.use_prompt_cache or self.im_start is None:
             return
-        starts = [i for i, t in enumerate(prompt) if t == self.im_start]
-        marks = []
-        if len(starts) >= 2 and starts[0] == 0:
-            marks.append(("system", starts[1]))
-        if starts:
-            marks.append(("last", starts[-1]))
-        for name, cut in marks:
-            have = len(self.cache.tokens[0])
-            if cut > have:
-                self.rt.prefill(self.cache, prompt[have:cut])
-                self.cur.snaps[name] = self.cache.snapshot()
+        for name, cut in _resume_marks(prompt, self.im_start):
+            have = len(self.cur.held())
+            if cut <= have:
+                continue
+            self.rt.prefill(self.cache, prompt[have:cut])
+            self.cur.snaps[name] = self.cache.snapshot()
 
     # ------------------------------------------------------------------ generation
+    def _rows_per_step(self, mode: str) -> int:
+        if mode in ("causal", "ar"):
+            return 1
+        if mode == "diffusion":
+            return self.canvas
+        return self.n + 1 if self.denoise_steps else 2 * self.n - 1
+
+    def _reserve(self, need: int) -> None:
+        """Grows the current cache (in 1024-position steps) to hold `need` positions."""
+        if need > self.cache.Lmax:
+            self.rt.grow_cache(self.cache, -(-need // 1024) * 1024)
+
+    @contextlib.contextmanager
+    def _reporting(self, progress, total: int):
+        """Routes the runtime's per-chunk prefill counts to progress(done, total) while active."""
+        if progress is None:
+            yield
+            return
+        done = 0
+
+        def tick(k):
+            nonlocal done
+            done += k
+            progress(done, total)
+
+        self.rt.progress_cb = tick
+        try:
+            yield
+        except BaseException:
+            self.rt.progress_cb = None
+            raise
+
+    def _decoder(self, mode: str, prompt: list, max_tokens: int, eos_ids: set, sp: SamplingParams,
+                 stats: DecodeStats):
+        common = dict(max_new_tokens=max_tokens, eos_ids=eos_ids, sp=sp, stats=stats)
+        if mode in ("causal", "ar"):
+            return ar_generate(self.rt, self.cache, prompt, **common)
+        if mode == "diffusion":
+            return diffusion_generate(self.rt, self.cache, prompt, mask_id=self.mask_id, canvas=self.canvas,
+                                      threshold=self.threshold, **common)
+        return selfspec_generate(self.rt, self.cache, prompt, mask_id=self.mask_id, n=self.n,
+                                 denoise_steps=self.denoise_steps, **common)
+
     def generate_ids(self, prompt: list, *, max_tokens: int = 2048, sampling: Optional[SamplingParams] = None,
                      mode: Optional[str] = None, stats: Optional[DecodeStats] = None, progress=None,
                      stop_ids: Optional[set] = None) -> Iterator[list]:
         """Yields lists of new token ids. Callers serialise calls (self.lock). progress(done, total) is
-        called after each prefill chunk; stop_ids end the generation like EOS (engine.py:200-271)."""
-        eos_ids = self.eos_ids | set(stop_ids or ())
+        called after each prefill chunk until the first tokens are out; stop_ids end the generation like
+        EOS (engine.py:228-271)."""
         mode = mode or self.mode
-        if mode == "diffusion" and sampling is None:
-            sampling = SamplingParams(temperature=0.0)
-        sp = sampling or SamplingParams()
-        stats = stats if stats is not None else DecodeStats()
-        if mode == "diffusion" and not sp.greedy:
+        if sampling is None:
+            sampling = SamplingParams(temperature=0.0) if mode == "diffusion" else SamplingParams()
+        if mode == "diffusion" and not sampling.greedy:
             raise ValueError("diffusion mode decodes greedily (temperature 0)")
-        t = time.perf_counter()
+        stats = DecodeStats() if stats is None else stats
+        started = time.perf_counter()
         self._position_cache(prompt)
-        step_rows = {"causal": 1, "ar": 1, "diffusion": self.canvas}.get(
-            mode, (self.n + 1) if self.denoise_steps else (2 * self.n - 1))
-        need = len(prompt) + max_tokens + 2 * step_rows + 16
-        if need > self.cache.Lmax:
-            self.rt.grow_cache(self.cache, -(-need // 1024) * 1024)
-        reused = len(self.cache.tokens[0])
-        if progress is not None:
-            done = [0]
-            total = len(prompt) - reused
-
-            def _cb(k):
-                done[0] += k
-                progress(done[0], total)
-
-            self.rt.progress_cb = _cb
-        try:
+        self._reserve(len(prompt) + max_tokens + 2 * self._rows_per_step(mode) + 16)
+        reused = len(self.cur.held())
+        with self._reporting(progress, len(prompt) - reused):
             self._prefill_to_snapshot(prompt)
-        except BaseException:
-            self.rt.progress_cb = None
-            raise
-        pre_s = time.perf_counter() - t
-        cache = self.cache
-        if mode in ("causal", "ar"):
-            gen = ar_generate(self.rt, cache, prompt, max_new_tokens=max_tokens, eos_ids=eos_ids, sp=sp, stats=stats)
-        elif mode == "diffusion":
-            gen = diffusion_generate(self.rt, cache, prompt, max_new_tokens=max_tokens, eos_ids=eos_ids,
-                                     mask_id=self.mask_id, canvas=self.canvas, threshold=self.threshold, stats=stats,
-                                     sp=sp)
-        else:
-            gen = selfspec_generate(self.rt, cache, prompt, max_new_tokens=max_tokens, eos_ids=eos_ids, sp=sp,
-                                    mask_id=self.mask_id, n=self.n, stats=stats, denoise_steps=self.denoise_steps)
+        setup_s = time.perf_counter() - started
+        gen = self._decoder(mode, prompt, max_tokens, self.eos_ids | set(stop_ids or ()), sampling, stats)
         try:
-            for i, chunk in enumerate(gen):
-                if i == 0:
-                    self.rt.progress_cb = None
+            first = True
+            for chunk in gen:
+                if first:  # the decoder's own prefill is done: no more progress reports
+                    self.rt.progress_cb, first = None, False
                 yield chunk
         finally:
             gen.close()
             self.rt.progress_cb = None
-            stats.prefill_s += pre_s
+            stats.prefill_s += setup_s
             stats.reused_tokens = reused
             self.last_stats = stats.as_dict()
 
@@ -256,24 +323,31 @@ class Engine:
 
     def render(self, messages: list, tools: Optional[list] = None, enable_thinking: bool = True,
                **template_kwargs) -> str:
-        return self._need_tokenizer().apply_chat_template(messages, tools=tools or None, add_generation_prompt=True,
-                                                          tokenize=False, enable_thinking=enable_thinking,
-                                                          **template_kwargs)
+        """The chat template applied to `messages`, ending in the assistant generation header."""
+        opts = dict(template_kwargs, add_generation_prompt=True, tokenize=False, enable_thinking=enable_thinking)
+        if tools:
+            opts["tools"] = tools
+        return self._need_tokenizer().apply_chat_template(messages, **opts)
 
     def encode(self, text: str) -> list:
         return self._need_tokenizer().encode(text, add_special_tokens=False)
 
     def generate_text(self, prompt_text: str, **kw) -> Iterator[str]:
-        detok = IncrementalDetokenizer(self._need_tokenizer())
+        """generate_ids over the encoded text, streamed back as text deltas."""
+        stream = IncrementalDetokenizer(self._need_tokenizer())
         for ids in self.generate_ids(self.encode(prompt_text), **kw):
-            d = detok.add(ids)
-            if d:
-                yield d
+            piece = stream.add(ids)
+            if piece:
+                yield piece
 
     def warmup(self) -> None:
-        """One short greedy generation (kernels, workspaces and graphs built), then empty caches."""
+        """Runs one short greedy generation, so kernels, workspaces and graphs exist before the first
+        request, then empties the caches."""
+        if self.tokenizer is not None:
+            prompt = self.encode("<|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n")
+        else:
+            prompt = [1, 2, 3]
         with self.lock:
-            p = self.encode("<|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n") if self.tokenizer else [1, 2, 3]
-            for _ in self.generate_ids(p, max_tokens=8, sampling=SamplingParams(temperature=0.0)):
+            for _ in self.generate_ids(prompt, max_tokens=8, sampling=SamplingParams(temperature=0.0)):
                 pass
             self.reset_cache()
