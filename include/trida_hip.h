@@ -225,12 +225,26 @@ int trida_sample_rows(const float* logits, int64_t rows, int64_t V, int64_t row_
  * receives a copy of the pre-conv rows x when not NULL: the rows a rollback rebuilds the conv window
  * from (the raw mixed_qkv rows that fused_selfspec_gdn_layer keeps, qwen3_5_diffusion.py:2219).
  * Dk in {32, 64, 128}, Dv % 8 == 0.
+ * State-pool and packed forms (each NULL = the contiguous form above), the arguments of the vLLM
+ * calls this replaces (causal_conv1d_fn(x, weight, bias, conv_states, cache_indices, query_start_loc),
+ * qwen3_5_diffusion.py:2227-2231; fused_selfspec_gdn_layer's conv_bias / win / win_idx / pre_out /
+ * slot_idx, :2211-2220):
+ *   conv_bias [C] bf16, added to the conv before the SiLU (16-byte aligned);
+ *   win_idx [B] int32: sequence b reads window row win_idx[b] of a [rows, Kc-1, C] pool (vLLM's
+ *     ss_slots1_i32 into ss_win_clean / ss_win_kern) and writes window_out row win_idx[b];
+ *   pre_idx [B] int32: sequence b writes pre_out slot pre_idx[b] of a [slots, T, C] pool (slot_idx into
+ *     ss_preconv);
+ *   cu_seqlens [B + 1] int32 (packed ragged batch, query_start_loc): sequence b is rows
+ *     cu_seqlens[b] .. cu_seqlens[b + 1] - 1 of x ([total, C], row stride x_st), a / b (row stride
+ *     ab_st) and the outputs q, k, v, g, beta ([total, ...]); T is then an upper bound of every
+ *     sequence's rows (the launch covers B x T rows; rows past T are not processed).
  */
 int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w, const uint16_t* a,
                    const uint16_t* b, const float* A_log, const float* dt_bias, uint16_t* q, uint16_t* k,
                    uint16_t* v, float* g, float* beta, uint16_t* window_out, uint16_t* pre_out, int64_t B, int64_t T,
                    int64_t Kc, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb, int64_t x_st,
-                   int64_t ab_sb, int64_t ab_st, void* stream);
+                   int64_t ab_sb, int64_t ab_st, const uint16_t* conv_bias, const int32_t* win_idx,
+                   const int32_t* pre_idx, const int32_t* cu_seqlens, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Gated delta rule, recurrent form, with the block-causal canvas readout.
@@ -245,16 +259,34 @@ int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const uint16_t* co
  * state_in [B, Hv, Dv, Dk] fp32 (row v of head h holds S[:, v]); out [B, T, Hv, Dv] bf16.
  * state_out (NULL or, may alias state_in): state after all T rows. state_clean (NULL or a separate
  * buffer): state after min(num_clean, T) rows. Dk in {32, 64, 128, 256}, Dv % 4 == 0.
+ * State-pool, ring and packed forms (each NULL = the contiguous form), the arguments of
+ *   fused_recurrent_block_causal_gated_delta_rule_packed(..., ssm_states, cache_indices, block_size,
+ *   causal_mode, num_clean, intermediate_states_buffer, intermediate_state_indices, cache_steps)
+ *   (qwen3_5_diffusion.py:2234-2240, 2384-2393) and of the legacy call's cu_seqlens (:2408-2415):
+ *   state_idx [B] int32 (cache_indices / ssm_idx): sequence b reads state_in row state_idx[b] of a
+ *     [rows, Hv, Dv, Dk] pool and writes state_out row state_idx[b] (rows must be distinct when
+ *     state_out aliases state_in); state_clean stays [B, Hv, Dv, Dk];
+ *   inter [rows, cache_steps, Hv, Dv, Dk] fp32 (intermediate_states_buffer), inter_idx [B] int32
+ *     (intermediate_state_indices; NULL = row b): entry (inter_idx[b], j) receives the state after
+ *     rows 0..j of sequence b for j < min(cache_steps, rows of b) -- the self-spec ring, from which a
+ *     step with n_acc accepted drafts continues at j = n_acc (:1821-1837, 228-248);
+ *   cu_seqlens [B + 1] int32 (packed ragged batch): sequence b is rows cu_seqlens[b] ..
+ *     cu_seqlens[b + 1] - 1 of q, k, v, g, beta and out ([total, ...]); num_clean counts from each
+ *     sequence's first row; T is an upper bound of every sequence's rows (rows past T are not
+ *     processed).
  */
 int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                         const float* beta, const float* state_in, uint16_t* out, float* state_out,
                         float* state_clean, int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk,
-                        int64_t Dv, int causal_mode, int64_t num_clean, float scale, void* stream);
+                        int64_t Dv, int causal_mode, int64_t num_clean, float scale, const int32_t* cu_seqlens,
+                        const int32_t* state_idx, float* inter, const int32_t* inter_idx, int64_t cache_steps,
+                        void* stream);
 
 /* Fused self-spec GDN layer, one launch for a block of T <= 64 rows: depthwise causal conv over
  * [window ++ x] + SiLU, split, l2norm(q, k), gates, then the recurrence and readout of
  * trida_gdr_recurrent. Replaces fused_selfspec_gdn_layer(mixed_qkv, a, b, A_log, dt_bias, conv_weight,
- *   win, ssm_states, block_size, num_clean, out, pre_out) (inference/zoro-1/vllm/vllm_native_diffusion/
+ *   conv_bias, win, win_idx, ssm_states, ssm_idx, inter, inter_idx, block_size, num_clean, cache_steps,
+ *   out, pre_out, slot_idx) (inference/zoro-1/vllm/vllm_native_diffusion/
  *   qwen3_5_diffusion.py:2207-2221) and the Metal canvas_gdn_fused front half
  *   (inference/zoro-1/mlx/trida_mlx/kernels.py:118-131, model.py:289-303).
  * Inputs as trida_gdn_prep (x, window, conv_w, a, b, A_log, dt_bias, strides) plus state_in; outputs as
@@ -262,14 +294,22 @@ int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v,
  * rollback needs: k_out [B, T, Hk, Dk] bf16, v_out [B, T, Hv, Dv] bf16, g_out, beta_out [B, T, Hv] fp32
  * (given together), pre_out [B, T, C] bf16 raw pre-conv rows, window_out [B, Kc-1, C] (must not alias
  * window). Results are bit-identical to trida_gdn_prep followed by trida_gdr_recurrent.
- * Dk in {32, 64, 128}, Dv % 8 == 0, 2 <= Kc <= 4. */
+ * Dk in {32, 64, 128}, Dv % 8 == 0, 2 <= Kc <= 4.
+ * The vLLM call's pool / ring arguments (each NULL = contiguous): conv_bias (conv_bias), win_idx (win_idx,
+ * the window row read and the window_out row written), state_idx (ssm_idx, into ssm_states =
+ * ring[prev] viewed as [(2R+1) N, Hv, Dv, Dk]), inter / inter_idx / cache_steps (inter = ring[cur] as
+ * [2R+1, N, Hv, Dv, Dk], inter_idx, cache_steps = N: the state after rows 0..j, j < cache_steps),
+ * pre_idx (slot_idx, the pre_out slot of a [slots, T, C] pool), with the meanings of trida_gdn_prep and
+ * trida_gdr_recurrent. The batch is B uniform blocks of T rows (block_size = T). */
 int trida_gdn_fused_layer(const uint16_t* x, const uint16_t* window, const uint16_t* conv_w, const uint16_t* a,
                           const uint16_t* b, const float* A_log, const float* dt_bias, const float* state_in,
                           uint16_t* out, float* state_out, float* state_clean, uint16_t* k_out, uint16_t* v_out,
                           float* g_out, float* beta_out, uint16_t* pre_out, uint16_t* window_out, int64_t B,
                           int64_t T, int64_t Kc, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb,
                           int64_t x_st, int64_t ab_sb, int64_t ab_st, int causal_mode, int64_t num_clean,
-                          float scale, void* stream);
+                          float scale, const uint16_t* conv_bias, const int32_t* win_idx, const int32_t* state_idx,
+                          float* inter, const int32_t* inter_idx, int64_t cache_steps, const int32_t* pre_idx,
+                          void* stream);
 
 /* Block-bidirectional gated delta rule: the training research path _block_bidirectional_gdr
  *   (train/models/hybrid.py:461-536) for blocks of block_size consecutive rows (the last block may be
@@ -301,12 +341,22 @@ int trida_gdr_block_bidir(const uint16_t* q, const uint16_t* k, const uint16_t* 
  * Dk in {32, 64, 128}, Dv % 16 == 0. T <= 64: one launch (prep and scan fused per workgroup); T > 64:
  * a chunk-parallel prep launch then a sequential scan launch, with a workspace of
  * trida_gdr_chunk_workspace_bytes(B, T, Hv) bytes (0 for T <= 64), 16-byte aligned, no initialisation.
+ * Packed and state-pool forms (NULL = contiguous), the prefill call's
+ *   chunk_gated_delta_rule(..., initial_state=ssm_state[indices], cu_seqlens=query_start_loc)
+ *   (FLA's varlen interface as the vLLM Qwen3.5 prefill calls it; the indices as
+ *   qwen3_5_diffusion.py:2384-2393 pass them): cu_seqlens [B + 1] int32: sequence b is rows
+ *   cu_seqlens[b] .. cu_seqlens[b + 1] - 1 of q, k, v, g, beta, out ([total, ...]), at most T of them
+ *   (T: an upper bound of every sequence's rows, which sizes the launch and the workspace);
+ *   state_idx [B] int32: sequence b reads state_in row state_idx[b] and writes state_out row
+ *   state_idx[b] of [rows, Hv, Dv, Dk] pools (distinct rows when they alias). These forms run the
+ *   general chunk kernels (prep + scan, or the fused single chunk for T <= 64).
  */
 int64_t trida_gdr_chunk_workspace_bytes(int64_t B, int64_t T, int64_t Hv);
 int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g, const float* beta,
                     const float* state_in, uint16_t* out, float* state_out, const int32_t* n_keep, int64_t seq_mod,
                     int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int causal_mode,
-                    int64_t num_clean, float scale, void* workspace, int64_t workspace_bytes, void* stream);
+                    int64_t num_clean, float scale, void* workspace, int64_t workspace_bytes,
+                    const int32_t* cu_seqlens, const int32_t* state_idx, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * GDN state snapshot: one coalesced copy of state_elems fp32 recurrent-state values and window_elems
@@ -329,12 +379,17 @@ int trida_gdn_snapshot(const float* state, float* snap_state, int64_t state_elem
  *   window[b] = last Kc-1 rows of (snap_window[b] ++ preconv[b, :n]); may alias snap_window.
  * preconv [NB, T, C] bf16 with strides x_sb, x_st. Either part is skipped when its pointers are NULL.
  * skip_full != 0 leaves slots with n == T untouched (their state already covers the whole block).
+ * Pool form of the window part (NULL = row / slot b): win_idx [NB] int32 picks slot b's row of
+ * snap_window and window ([rows, Kc-1, C] pools; distinct rows when they alias), pre_idx [NB] int32 its
+ * preconv slot (x_sb apart). This is the self-spec sampler's window rebuild over every layer at once,
+ * wc[:, slot + 1] = last Kc-1 rows of (wc[:, slot + 1] ++ preconv[:, slot, :n_acc + 1])
+ * (qwen3_5_diffusion.py:963-975), with win_idx = l (R + 2) + slot + 1 and pre_idx = l (R + 1) + slot.
  */
 int trida_gdn_restore(const float* snap_state, float* state, const uint16_t* k, const uint16_t* v,
                       const float* g, const float* beta, const uint16_t* snap_window, uint16_t* window,
                       const uint16_t* preconv, const int32_t* n_keep, int64_t NB, int64_t seq_mod, int64_t T,
                       int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t C, int64_t Kc, int64_t x_sb,
-                      int64_t x_st, int skip_full, void* stream);
+                      int64_t x_st, int skip_full, const int32_t* win_idx, const int32_t* pre_idx, void* stream);
 
 /* ------------------------------------------------------------------------------------------------
  * Canvas attention over a bf16 KV cache, with the draft / verify / mixed masks and GQA.

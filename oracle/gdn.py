@@ -50,13 +50,16 @@ def gates(a: torch.Tensor, b: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.
     return g, beta
 
 
-def causal_conv(x: torch.Tensor, window: torch.Tensor, weight: torch.Tensor):
-    """x [B, T, C] pre-conv rows, window [B, K-1, C], weight [C, K].
+def causal_conv(x: torch.Tensor, window: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None):
+    """x [B, T, C] pre-conv rows, window [B, K-1, C], weight [C, K], bias [C] or None (the conv1d bias
+    of the layer, qwen3_5_diffusion.py:2211-2212).
     Returns (silu(conv) rounded to bf16 [B, T, C] fp32, new window [B, K-1, C] = last K-1 rows)."""
     K = weight.shape[1]
     full = torch.cat([window.float(), x.float()], dim=1)  # [B, K-1+T, C]
     T = x.shape[1]
     y = torch.zeros(x.shape[0], T, x.shape[2])
+    if bias is not None:
+        y += bias.float()
     w = weight.float()
     for j in range(K):
         y += full[:, j: j + T, :] * w[:, j]
@@ -64,12 +67,12 @@ def causal_conv(x: torch.Tensor, window: torch.Tensor, weight: torch.Tensor):
     return y, full[:, -(K - 1):, :].clone()
 
 
-def prep(mixed_qkv, window, conv_w, a, b, A_log, dt_bias, Hk: int, Hv: int, Dk: int, Dv: int):
+def prep(mixed_qkv, window, conv_w, a, b, A_log, dt_bias, Hk: int, Hv: int, Dk: int, Dv: int, conv_bias=None):
     """Conv + SiLU + split + l2norm(q, k) + gates for one GDN layer input block.
     Returns q, k [B,T,Hk,Dk] (unit-norm, bf16-rounded), v [B,T,Hv,Dv] (bf16-rounded), g, beta [B,T,Hv]
     fp32 and the new conv window."""
     B, T, _ = mixed_qkv.shape
-    y, new_window = causal_conv(mixed_qkv, window, conv_w)
+    y, new_window = causal_conv(mixed_qkv, window, conv_w, conv_bias)
     q, k, v = torch.split(y, [Hk * Dk, Hk * Dk, Hv * Dv], dim=-1)
     q = bf16_round(l2norm(q.reshape(B, T, Hk, Dk)))
     k = bf16_round(l2norm(k.reshape(B, T, Hk, Dk)))

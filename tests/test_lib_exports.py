@@ -112,7 +112,7 @@ def test_gdr_chunk_argument_checks():
 
     def call(T=100, Dk=128, Dv=128, mode=1, ws=None, ws_bytes=0, n_keep=None):
         return lib.trida_gdr_chunk(P, P, P, P, P, P, P, P, n_keep, 1, 1, T, 16, 16, Dk, Dv, mode, 0, 0.1, ws,
-                                   ws_bytes, None)
+                                   ws_bytes, None, None, None)
 
     assert call(Dk=256) == _lib.TRIDA_ERR_ARG and b"Dk" in lib.trida_last_error()
     assert call(Dv=24) == _lib.TRIDA_ERR_ARG

@@ -78,6 +78,23 @@ def test_conv_closed_form():
     assert torch.equal(win, x[:, -3:])
 
 
+def test_conv_bias_matches_torch_conv1d():
+    """With a bias the conv is torch's depthwise conv1d (groups = C, bias added before the SiLU) over
+    [window ++ x], the layer's nn.Conv1d as the vLLM call feeds it (conv_weight, conv_bias)."""
+    g0 = torch.Generator().manual_seed(11)
+    B, T, C, K = 2, 5, 24, 4
+    x, win = torch.randn(B, T, C, generator=g0), torch.randn(B, K - 1, C, generator=g0)
+    w, bias = torch.randn(C, K, generator=g0), torch.randn(C, generator=g0)
+    y, new_win = G.causal_conv(x, win, w, bias)
+    full = torch.cat([win, x], 1).transpose(1, 2)                    # [B, C, K-1+T]
+    ref = F.silu(F.conv1d(full, w[:, None, :], bias, groups=C)).transpose(1, 2)
+    assert torch.allclose(y, G.bf16_round(ref), atol=1e-2, rtol=1e-2)
+    assert torch.equal(new_win, x[:, -3:])
+    # a dropped bias is caught
+    y0, _ = G.causal_conv(x, win, w)
+    assert not torch.allclose(y0, G.bf16_round(ref), atol=1e-2, rtol=1e-2)
+
+
 def test_gates_closed_form():
     a = torch.tensor([[0.0, 30.0]])
     b = torch.tensor([[0.0, -2.0]])

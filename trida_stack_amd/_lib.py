@@ -63,14 +63,14 @@ SIGNATURES = {
     "trida_gated_rmsnorm": (C.c_int, [P, P, P, P, I64, I64, I64, I64, F32, P]),
     "trida_gated_rmsnorm_frag": (C.c_int, [P, P, P, P, I64, I64, I64, I64, F32, P]),
     "trida_attn_prep": (C.c_int, [P, I64, P, P, P, P, P, P, P] + [I64] * 7 + [F32, F32, P]),
-    "trida_gdn_prep": (C.c_int, [P] * 14 + [I64] * 11 + [P]),
-    "trida_gdr_recurrent": (C.c_int, [P] * 9 + [I64] * 6 + [C.c_int, I64, F32, P]),
-    "trida_gdn_fused_layer": (C.c_int, [P] * 17 + [I64] * 11 + [C.c_int, I64, F32, P]),
+    "trida_gdn_prep": (C.c_int, [P] * 14 + [I64] * 11 + [P] * 4 + [P]),
+    "trida_gdr_recurrent": (C.c_int, [P] * 9 + [I64] * 6 + [C.c_int, I64, F32] + [P, P, P, P, I64] + [P]),
+    "trida_gdn_fused_layer": (C.c_int, [P] * 17 + [I64] * 11 + [C.c_int, I64, F32] + [P] * 5 + [I64, P] + [P]),
     "trida_gdr_block_bidir": (C.c_int, [P] * 8 + [I64] * 7 + [F32, P]),
     "trida_gdr_chunk_workspace_bytes": (I64, [I64, I64, I64]),
-    "trida_gdr_chunk": (C.c_int, [P] * 9 + [I64] * 7 + [C.c_int, I64, F32, P, I64, P]),
+    "trida_gdr_chunk": (C.c_int, [P] * 9 + [I64] * 7 + [C.c_int, I64, F32, P, I64] + [P, P] + [P]),
     "trida_gdn_snapshot": (C.c_int, [P, P, I64, P, P, I64, P]),
-    "trida_gdn_restore": (C.c_int, [P] * 10 + [I64] * 11 + [C.c_int, P]),
+    "trida_gdn_restore": (C.c_int, [P] * 10 + [I64] * 11 + [C.c_int, P, P, P]),
     "trida_attn_canvas_scratch_bytes": (I64, [I64] * 7),
     "trida_attn_canvas": (C.c_int, [P, P, P, P, P, I64, I64, P] + [I64] * 6 + [C.c_int, I64, F32, I64, I64, P, I64, P]),
     "trida_attn_canvas_frag": (C.c_int, [P, P, P, P, P, I64, I64, P] + [I64] * 6 + [C.c_int, I64, F32, I64, I64, P, I64,

@@ -149,7 +149,21 @@ struct ChunkArgs {
   uint16_t* ws;            // prep workspace: [B, nchunks, Hv][3][64 x 64] bf16
   int T, Hk, Hv, Dv, nc, seq_mod, nchunks;
   float scale;
+  const int32_t* cu;       // [B + 1] packed ragged rows, or null (B x T rows)
+  const int32_t* sidx;     // [B] state_in / state_out row of sequence b, or null (row b)
 };
+
+// Rows of sequence b: [row0, row0 + n) of the packed arrays (n <= T).
+struct SeqRows {
+  int64_t row0;
+  int n;
+};
+__device__ __forceinline__ SeqRows seq_rows(const ChunkArgs& a, int b) {
+  if (!a.cu) return {(int64_t)b * a.T, a.T};
+  const int lo = a.cu[b];
+  return {lo, max(0, min(a.cu[b + 1] - lo, a.T))};
+}
+__device__ __forceinline__ int64_t state_row(const ChunkArgs& a, int b) { return a.sidx ? a.sidx[b] : b; }
 
 // ---------------------------------------------------------------------------------------------- staging
 // Workspace block of one (sequence, chunk, value head): T diag(beta) hi, lo and Aqk hi, 64 x 64 bf16 each.
@@ -178,11 +192,12 @@ struct Stage {
   u32x4 ws[WP_PT > 0 ? WP_PT : 1];
   float g, beta;
 
-  __device__ __forceinline__ void load(const ChunkArgs& a, int b, int h, int hk, int dv0, int t0, int cc,
-                                       int chunk) {
+  // b: the sequence (workspace block); r0: its first row in the packed arrays
+  __device__ __forceinline__ void load(const ChunkArgs& a, int b, int64_t r0, int h, int hk, int dv0, int t0,
+                                       int cc, int chunk) {
     const int tid = threadIdx.x;
     const int64_t qk_row = (int64_t)a.Hk * DK;
-    const uint16_t* kb = a.k + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK;
+    const uint16_t* kb = a.k + (r0 + t0) * qk_row + (int64_t)hk * DK;
 #pragma unroll
     for (int i = 0; i < KSQ_PT; ++i) {
       const int sq = tid + i * kNT;
@@ -195,7 +210,7 @@ struct Stage {
       }
     }
     if (WANT_Q) {
-      const uint16_t* qb = a.q + ((int64_t)b * a.T + t0) * qk_row + (int64_t)hk * DK;
+      const uint16_t* qb = a.q + (r0 + t0) * qk_row + (int64_t)hk * DK;
 #pragma unroll
       for (int i = 0; i < QP_PT; ++i) {
         const int p = tid + i * kNT;
@@ -206,7 +221,7 @@ struct Stage {
     }
     if (WANT_V) {
       const int64_t v_row = (int64_t)a.Hv * a.Dv;
-      const uint16_t* vb = a.v + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0;
+      const uint16_t* vb = a.v + (r0 + t0) * v_row + (int64_t)h * a.Dv + dv0;
 #pragma unroll
       for (int i = 0; i < VP_PT; ++i) {
         const int p = tid + i * kNT;
@@ -225,7 +240,7 @@ struct Stage {
       }
     }
     if (tid < kWave) {
-      const int64_t gi = ((int64_t)b * a.T + t0 + tid) * a.Hv + h;
+      const int64_t gi = (r0 + t0 + tid) * a.Hv + h;
       const bool in = tid < cc && tid < C;
       g = in ? a.g[gi] : 0.f;
       beta = in ? a.beta[gi] : 0.f;
@@ -686,10 +701,12 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_prep_kernel(ChunkArgs a) {
   const int b = idx / a.nchunks;
   const int hk = h / (a.Hv / a.Hk);
   const int t0 = c * kChunk;
-  const int cc = min(kChunk, a.T - t0);
+  const SeqRows sr = seq_rows(a, b);
+  const int cc = min(kChunk, sr.n - t0);
+  if (cc <= 0) return;  // past a packed sequence's chunks (block-uniform)
   {
     Stage<DK, 4, 16, OUT, false, false> st;
-    st.load(a, b, h, hk, 0, t0, cc, c);
+    st.load(a, b, sr.row0, h, hk, 0, t0, cc, c);
     st.store(smem);
   }
   __syncthreads();
@@ -712,24 +729,25 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_scan_kernel(ChunkArgs a) {
   const int hk = h / (a.Hv / a.Hk);
   const int dv0 = sl * DVS;
   const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
-  const int n_tot = a.n_keep ? min(max(a.n_keep[b % a.seq_mod], 0), a.T) : a.T;
-  // chunks to visit: all of them with a readout, else those holding absorbed rows
-  const int nch = OUT ? a.nchunks : (n_tot + kChunk - 1) / kChunk;
+  const SeqRows sr = seq_rows(a, b);
+  const int n_tot = a.n_keep ? min(max(a.n_keep[b % a.seq_mod], 0), sr.n) : sr.n;
+  // chunks to visit: all of the sequence's with a readout, else those holding absorbed rows
+  const int nch = ((OUT ? sr.n : n_tot) + kChunk - 1) / kChunk;
   f32x4 st[StTiles<DK>::PER][DVS / 16];
-  const int64_t soff = (((int64_t)b * a.Hv + h) * a.Dv + dv0) * DK;
+  const int64_t soff = ((state_row(a, b) * a.Hv + h) * a.Dv + dv0) * DK;
   load_state<DK, DVS>(st, a.state_in + soff, w, l);
   const int64_t v_row = (int64_t)a.Hv * a.Dv;
   Stage<DK, 4, DVS, OUT, true, true> nx;
-  if (nch > 0) nx.load(a, b, h, hk, dv0, 0, min(kChunk, a.T), 0);
+  if (nch > 0) nx.load(a, b, sr.row0, h, hk, dv0, 0, min(kChunk, sr.n), 0);
   for (int c = 0; c < nch; ++c) {
     const int t0 = c * kChunk;
-    const int cc = min(kChunk, a.T - t0);
+    const int cc = min(kChunk, sr.n - t0);
     const int n_abs = min(max(n_tot - t0, 0), cc);
     __syncthreads();  // the previous chunk's LDS reads are done
     nx.store(smem);
     __syncthreads();
-    if (c + 1 < nch) nx.load(a, b, h, hk, dv0, t0 + kChunk, min(kChunk, a.T - t0 - kChunk), c + 1);
-    uint16_t* orow = OUT ? a.out + ((int64_t)b * a.T + t0) * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
+    if (c + 1 < nch) nx.load(a, b, sr.row0, h, hk, dv0, t0 + kChunk, min(kChunk, sr.n - t0 - kChunk), c + 1);
+    uint16_t* orow = OUT ? a.out + (sr.row0 + t0) * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
     scan_chunk<DK, 4, DVS>(smem, st, cc, n_abs, cc, orow, v_row, a.scale);
   }
   if (a.state_out) store_state<DK, DVS>(st, a.state_out + soff, w, l);
@@ -748,20 +766,28 @@ __global__ __launch_bounds__(kNT) void gdr_chunk_fused_kernel(ChunkArgs a) {
   const int hk = h / (a.Hv / a.Hk);
   const int dv0 = sl * DVS;
   const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
-  const int cc = a.T;
+  const SeqRows sr = seq_rows(a, b);
+  const int cc = sr.n;
   const int n_abs = a.n_keep ? min(max(a.n_keep[b % a.seq_mod], 0), cc) : cc;
   f32x4 st[StTiles<DK>::PER][DVS / 16];
-  const int64_t soff = (((int64_t)b * a.Hv + h) * a.Dv + dv0) * DK;
+  const int64_t soff = ((state_row(a, b) * a.Hv + h) * a.Dv + dv0) * DK;
+  if (cc == 0) {  // an empty packed sequence: the state passes through
+    if (a.state_out) {
+      load_state<DK, DVS>(st, a.state_in + soff, w, l);
+      store_state<DK, DVS>(st, a.state_out + soff, w, l);
+    }
+    return;
+  }
   {
     Stage<DK, NB, DVS, OUT, true, false> sg;
-    sg.load(a, b, h, hk, dv0, 0, cc, 0);
+    sg.load(a, b, sr.row0, h, hk, dv0, 0, cc, 0);
     load_state<DK, DVS>(st, a.state_in + soff, w, l);
     sg.store(smem);
   }
   __syncthreads();
   prep_chunk<DK, NB, DVS, OUT>(smem);
   const int64_t v_row = (int64_t)a.Hv * a.Dv;
-  uint16_t* orow = OUT ? a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
+  uint16_t* orow = OUT ? a.out + sr.row0 * v_row + (int64_t)h * a.Dv + dv0 : nullptr;
   const int n_out = min(a.nc, cc);
   scan_chunk<DK, NB, DVS>(smem, st, cc, n_abs, n_out, orow, v_row, a.scale);
   if (OUT && n_out < cc) mask_rows<DK, NB, DVS>(smem, st, n_out, cc, orow, v_row, a.scale);
@@ -819,7 +845,8 @@ extern "C" int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint1
                                const float* beta, const float* state_in, uint16_t* out, float* state_out,
                                const int32_t* n_keep, int64_t seq_mod, int64_t B, int64_t T, int64_t Hk, int64_t Hv,
                                int64_t Dk, int64_t Dv, int causal_mode, int64_t num_clean, float scale,
-                               void* workspace, int64_t workspace_bytes, void* stream) {
+                               void* workspace, int64_t workspace_bytes, const int32_t* cu_seqlens,
+                               const int32_t* state_idx, void* stream) {
   TRIDA_CHECK(k && v && g && beta && state_in, TRIDA_ERR_NULL, "gdr_chunk: k, v, g, beta and state_in are required");
   TRIDA_CHECK(out || state_out, TRIDA_ERR_ARG, "gdr_chunk: nothing to compute (out and state_out are both NULL)");
   TRIDA_CHECK(!out || q, TRIDA_ERR_NULL, "gdr_chunk: q is required with out");
@@ -844,13 +871,14 @@ extern "C" int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint1
   const int64_t need = trida_gdr_chunk_workspace_bytes(B, T, Hv);
   TRIDA_CHECK(need == 0 || (workspace && workspace_bytes >= need && ((uintptr_t)workspace & 15) == 0),
               TRIDA_ERR_WORKSPACE, "gdr_chunk: workspace of %lld bytes (16-byte aligned) required", (long long)need);
-  if (out && !state_out && !n_keep && gdr_block_supported(T, Dk, Dv)) {
+  const bool indexed = cu_seqlens || state_idx;  // the packed / state-pool forms run the kernels below
+  if (!indexed && out && !state_out && !n_keep && gdr_block_supported(T, Dk, Dv)) {
     // a canvas block's readout (draft / verify / canvas passes): the single-block MFMA kernel
     BlockArgs ba{q, k, v, g, beta, state_in, out, (int)T, (int)Hk, (int)Hv, (int)Dv, causal_mode,
                  causal_mode == 2 ? (int)(num_clean < T ? num_clean : T) : (int)T, scale};
     return gdr_block_launch(ba, B, static_cast<hipStream_t>(stream));
   }
-  if (!n_keep && gdr_prefix_supported(B, T, Hv, Dk, Dv)) {
+  if (!indexed && !n_keep && gdr_prefix_supported(B, T, Hv, Dk, Dv)) {
     // a prompt prefix (every row causal, the state after the last row): the chunk-parallel preparation, then
     // the scan whose chain wave holds the state
     PrefixArgs pa{q, k, v, g, beta, state_in, out, state_out, workspace, (int)T, (int)Hk, (int)Hv, (int)Dv,
@@ -860,7 +888,7 @@ extern "C" int trida_gdr_chunk(const uint16_t* q, const uint16_t* k, const uint1
   ChunkArgs a{q,        k,   v,       g,         beta,       state_in,      out,
               state_out, n_keep, static_cast<uint16_t*>(workspace), (int)T, (int)Hk, (int)Hv, (int)Dv,
               causal_mode == 2 ? (int)(num_clean < T ? num_clean : T) : (int)T, n_keep ? (int)seq_mod : 1, (int)nchunks,
-              scale};
+              scale, cu_seqlens, state_idx};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (Dk) {
     case 32: return launch_dk<32>(a, (int)B, st);

@@ -51,9 +51,25 @@ struct PrepArgs {
   float* beta;
   uint16_t* window_out;  // [B, Kc-1, C] or null
   uint16_t* pre_out;     // [B, T, C] copy of the pre-conv rows x, or null
+  const uint16_t* conv_bias;   // [C] or null
+  const int32_t* win_idx;      // [B] window / window_out row of sequence b, or null (row b)
+  const int32_t* pre_idx;      // [B] pre_out slot of sequence b, or null (slot b)
+  const int32_t* cu_seqlens;   // [B + 1] packed ragged rows, or null (B x T rows)
   int T, C, Kc, Hk, Hv, Dk, Dv;
   int64_t x_sb, x_st, ab_sb, ab_st;
 };
+
+// Rows of sequence b: [row0, row0 + n) of the packed arrays. Contiguous form: n = T, row0 = b T (x and
+// a / b rows then also move by their batch strides). Packed form: rows cu[b] .. cu[b + 1] - 1, at most T.
+struct SeqRows {
+  int64_t row0;
+  int n;
+};
+__device__ __forceinline__ SeqRows seq_rows(const PrepArgs& a, int b) {
+  if (!a.cu_seqlens) return {(int64_t)b * a.T, a.T};
+  const int lo = a.cu_seqlens[b];
+  return {lo, max(0, min(a.cu_seqlens[b + 1] - lo, a.T))};
+}
 
 __device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
   f[0] = bf2f((uint16_t)(w.x & 0xffff));
@@ -82,12 +98,19 @@ template <int GW, int KC, int NT, int PASSES>  // lanes per q/k head = Dk / 8; c
 __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
   const int t = blockIdx.x % a.T;
   const int b = blockIdx.x / a.T;
+  const SeqRows sr = seq_rows(a, b);
+  if (t >= sr.n) return;  // past a packed sequence's rows (block-uniform)
+  const int T = sr.n;
   const int tid = threadIdx.x;
   const int key_dim = a.Hk * a.Dk;
   const int pieces = a.C / 8;
   const int pbase = blockIdx.y * NT * PASSES;  // the block's first piece: a multiple of GW
-  const uint16_t* xb = a.x + (int64_t)b * a.x_sb;
-  const uint16_t* wb = a.window + (int64_t)b * (a.Kc - 1) * a.C;
+  // the sequence's source rows (packed: row r of x at r x_st) and its window row
+  const uint16_t* xb = a.cu_seqlens ? a.x + sr.row0 * a.x_st : a.x + (int64_t)b * a.x_sb;
+  const int64_t ab0 = a.cu_seqlens ? sr.row0 * a.ab_st : (int64_t)b * a.ab_sb;
+  const int wrow = a.win_idx ? a.win_idx[b] : b;
+  const uint16_t* wb = a.window + (int64_t)wrow * (a.Kc - 1) * a.C;
+  const int64_t orow = sr.row0 + t;  // output row (q, k, v, g, beta)
 
   // every load of the block first (one memory round trip): per pass, the KC source rows of the thread's
   // 8 channels and their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces), and the
@@ -110,8 +133,8 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
   const int hg = min(tid, a.Hv - 1);
   float av = 0.f, bv = 0.f;
   if (gates) {
-    av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hg]);
-    bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hg]);
+    av = bf2f(a.a_in[ab0 + (int64_t)t * a.ab_st + hg]);
+    bv = bf2f(a.b_in[ab0 + (int64_t)t * a.ab_st + hg]);
   }
 
 #pragma unroll
@@ -122,7 +145,10 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
     const bool live = p < pieces;
     const int c = min(p, pieces - 1) * 8;
     // the pre-conv rows a rollback rebuilds the window from: the block's own row is its last source row
-    if (a.pre_out && live) *reinterpret_cast<u32x4*>(a.pre_out + ((int64_t)b * a.T + t) * a.C + c) = xs[ps][KC - 1];
+    if (a.pre_out && live) {
+      const int64_t prow = (int64_t)(a.pre_idx ? a.pre_idx[b] : b) * a.T + t;
+      *reinterpret_cast<u32x4*>(a.pre_out + prow * a.C + c) = xs[ps][KC - 1];
+    }
     float acc[8];
     {
       float w[8][KC];
@@ -134,8 +160,15 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
           const uint32_t word = wsv[ps][e / 8][(e % 8) / 2];
           w[ch][j] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
         }
+      if (a.conv_bias) {
+        float bias[8];
+        unpack8(*reinterpret_cast<const u32x4*>(a.conv_bias + c), bias);
 #pragma unroll
-      for (int ch = 0; ch < 8; ++ch) acc[ch] = 0.f;
+        for (int ch = 0; ch < 8; ++ch) acc[ch] = bias[ch];
+      } else {
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) acc[ch] = 0.f;
+      }
 #pragma unroll
       for (int j = 0; j < KC; ++j) {
         float f[8];
@@ -162,7 +195,7 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
     }
     if (live) {
       const u32x4 w = pack8(acc);
-      const int64_t row = (int64_t)b * a.T + t;
+      const int64_t row = orow;
       if (c < key_dim)
         *reinterpret_cast<u32x4*>(a.q + row * key_dim + c) = w;
       else if (c < 2 * key_dim)
@@ -171,11 +204,11 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
         *reinterpret_cast<u32x4*>(a.v + row * (int64_t)a.Hv * a.Dv + (c - 2 * key_dim)) = w;
     }
     // the new conv window (last Kc-1 rows of [window ++ x]): the last row's blocks, each its own pieces
-    if (a.window_out && t == a.T - 1 && live) {
+    if (a.window_out && t == T - 1 && live) {
       for (int wr = 0; wr < a.Kc - 1; ++wr) {
-        const int tau = a.T - (a.Kc - 1) + wr;
+        const int tau = T - (a.Kc - 1) + wr;
         const uint16_t* src = tau >= 0 ? xb + (int64_t)tau * a.x_st + c : wb + (int64_t)(a.Kc - 1 + tau) * a.C + c;
-        *reinterpret_cast<u32x4*>(a.window_out + ((int64_t)b * (a.Kc - 1) + wr) * a.C + c) =
+        *reinterpret_cast<u32x4*>(a.window_out + ((int64_t)wrow * (a.Kc - 1) + wr) * a.C + c) =
             *reinterpret_cast<const u32x4*>(src);
       }
     }
@@ -183,10 +216,10 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
   if (gates) {
     for (int hh = tid; hh < a.Hv; hh += NT) {
       if (hh != tid) {  // more heads than threads: the later ones load their own inputs
-        av = bf2f(a.a_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hh]);
-        bv = bf2f(a.b_in[(int64_t)b * a.ab_sb + (int64_t)t * a.ab_st + hh]);
+        av = bf2f(a.a_in[ab0 + (int64_t)t * a.ab_st + hh]);
+        bv = bf2f(a.b_in[ab0 + (int64_t)t * a.ab_st + hh]);
       }
-      const int64_t o = ((int64_t)b * a.T + t) * a.Hv + hh;
+      const int64_t o = orow * a.Hv + hh;
       a.g[o] = -__expf(a.A_log[hh]) * softplus(av + a.dt_bias[hh]);
       a.beta[o] = 1.f / (1.f + __expf(-bv));
     }
@@ -203,7 +236,8 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
                               const float* dt_bias, uint16_t* q, uint16_t* k, uint16_t* v, float* g,
                               float* beta, uint16_t* window_out, uint16_t* pre_out, int64_t B, int64_t T, int64_t Kc,
                               int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv, int64_t x_sb, int64_t x_st,
-                              int64_t ab_sb, int64_t ab_st, void* stream) {
+                              int64_t ab_sb, int64_t ab_st, const uint16_t* conv_bias, const int32_t* win_idx,
+                              const int32_t* pre_idx, const int32_t* cu_seqlens, void* stream) {
   TRIDA_CHECK(x && window && conv_w && a_in && b_in && A_log && dt_bias && q && k && v && g && beta,
               TRIDA_ERR_NULL, "gdn_prep: a required pointer is NULL");
   TRIDA_CHECK(B > 0 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0 && Kc >= 2 && Kc <= kMaxKc, TRIDA_ERR_ARG,
@@ -220,8 +254,11 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
               "gdn_prep: window_out must not alias window");
   TRIDA_CHECK(pre_out == nullptr || (((uintptr_t)pre_out & 15) == 0 && pre_out != x), TRIDA_ERR_ARG,
               "gdn_prep: pre_out must be 16-byte aligned and not alias x");
+  TRIDA_CHECK(conv_bias == nullptr || ((uintptr_t)conv_bias & 15) == 0, TRIDA_ERR_ALIGN,
+              "gdn_prep: conv_bias must be 16-byte aligned");
   TRIDA_CHECK(B * T < INT32_MAX, TRIDA_ERR_ARG, "gdn_prep: too many rows");
   PrepArgs a{x, window, conv_w, a_in, b_in, A_log, dt_bias, q, k, v, g, beta, window_out, pre_out,
+             conv_bias, win_idx, pre_idx, cu_seqlens,
              (int)T, (int)C, (int)Kc, (int)Hk, (int)Hv, (int)Dk, (int)Dv, x_sb, x_st, ab_sb, ab_st};
   hipStream_t st = static_cast<hipStream_t>(stream);
   // small grids: 128-piece slices, one per block; grids of >= 512 rows (which fill the GPU anyway): one

@@ -81,8 +81,11 @@ struct PrepIn {
   uint16_t* v_out;  // [B, T, Hv, Dv] or null
   float* g_out;     // [B, T, Hv] or null (log decay)
   float* beta_out;
-  uint16_t* pre_out;     // [B, T, C] raw pre-conv rows or null
-  uint16_t* window_out;  // [B, Kc-1, C] new window or null
+  uint16_t* pre_out;     // [slots, T, C] raw pre-conv rows or null
+  uint16_t* window_out;  // [rows, Kc-1, C] new window or null
+  const uint16_t* conv_bias;  // [C] or null
+  const int32_t* win_idx;     // [B] window / window_out row of sequence b, or null (row b)
+  const int32_t* pre_idx;     // [B] pre_out slot of sequence b, or null (slot b)
   int64_t x_sb, x_st, ab_sb, ab_st;
   int Kc;
 };
@@ -102,6 +105,11 @@ struct RecArgs {
   float scale;
   int bidir;  // > 0: block-bidirectional readout over blocks of this many rows (causal_mode 1)
   PrepIn p;   // fused layer only
+  const int32_t* cu_seqlens;  // [B + 1] packed ragged rows, or null (B x T rows)
+  const int32_t* state_idx;   // [B] state_in / state_out row of sequence b, or null (row b)
+  float* inter;               // [rows, csteps, Hv, Dv, Dk] states after rows 0..csteps-1, or null
+  const int32_t* inter_idx;   // [B] inter row of sequence b, or null (row b)
+  int csteps;
 };
 
 __device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
@@ -171,6 +179,13 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   const int vl = wave * kVPerWave + lane / kLanesPerV;  // value column within the tile
   const int v = vt * VPB + vl;
   const int kl = lane % kLanesPerV;                      // k slice [kl*KPL, kl*KPL+KPL)
+  // the sequence's rows: [row0, row0 + T) of the packed arrays (B x a.T rows unless cu_seqlens is given)
+  int64_t row0 = (int64_t)b * a.T;
+  int T = a.T;
+  if (a.cu_seqlens) {
+    row0 = a.cu_seqlens[b];
+    T = max(0, min(a.cu_seqlens[b + 1] - (int)row0, a.T));
+  }
 
   __shared__ __align__(16) uint16_t s_q[TC][Dk];
   __shared__ __align__(16) uint16_t s_k[TC][Dk];
@@ -190,20 +205,26 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     else return bf2f(s_q[r][i]) * a.scale;
   };
 
-  const int64_t st_off = (((int64_t)b * a.Hv + h) * a.Dv + v) * Dk + kl * KPL;
+  const int64_t col_off = ((int64_t)h * a.Dv + v) * Dk + kl * KPL;  // within one [Hv, Dv, Dk] state
+  const int64_t hvk = (int64_t)a.Hv * a.Dv * Dk;
+  const int64_t st_off = (a.state_idx ? a.state_idx[b] : b) * hvk + col_off;  // state_in / state_out
+  const int64_t cl_off = (int64_t)b * hvk + col_off;                           // state_clean
   float s[KPL];
 #pragma unroll
   for (int i = 0; i < KPL; ++i) s[i] = a.state_in[st_off + i];
+  // the intermediate states: after row t, t < csteps, of this sequence
+  const int csteps = a.inter ? min(a.csteps, T) : 0;
+  float* inter_col = a.inter ? a.inter + (int64_t)(a.inter_idx ? a.inter_idx[b] : b) * a.csteps * hvk + col_off : nullptr;
 
-  const int nc = a.causal_mode == 2 ? min(a.num_clean, a.T) : a.T;
+  const int nc = a.causal_mode == 2 ? min(a.num_clean, T) : T;
   const int64_t qk_row = (int64_t)a.Hk * Dk;  // elements between rows t and t+1
-  const uint16_t* qb = a.q + (int64_t)b * a.T * qk_row + (int64_t)hk * Dk;
-  const uint16_t* kb = a.k + (int64_t)b * a.T * qk_row + (int64_t)hk * Dk;
+  const uint16_t* qb = a.q + row0 * qk_row + (int64_t)hk * Dk;
+  const uint16_t* kb = a.k + row0 * qk_row + (int64_t)hk * Dk;
   const int64_t v_row = (int64_t)a.Hv * a.Dv;
-  const uint16_t* vb = a.v + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + vt * VPB;
-  uint16_t* ob = a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + v;
-  const float* gb = a.g + (int64_t)b * a.T * a.Hv + h;
-  const float* bb = a.beta + (int64_t)b * a.T * a.Hv + h;
+  const uint16_t* vb = a.v + row0 * v_row + (int64_t)h * a.Dv + vt * VPB;
+  uint16_t* ob = a.out + row0 * v_row + (int64_t)h * a.Dv + v;
+  const float* gb = a.g + row0 * a.Hv + h;
+  const float* bb = a.beta + row0 * a.Hv + h;
 
   // rows staged per chunk: whole blocks when the readout is block-bidirectional
   const int tcn = a.bidir > 0 ? (TC / a.bidir) * a.bidir : TC;
@@ -239,10 +260,12 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     __shared__ __align__(16) uint16_t s_qkw[2][Dk * kMaxKc];  // conv weights [channel][tap], q then k head
     __shared__ __align__(16) uint16_t s_vw[VPB * kMaxKc];
     const PrepIn& p = a.p;
-    const int Kc = p.Kc, W = Kc - 1, nsrc = a.T + W;
+    const int Kc = p.Kc, W = Kc - 1, nsrc = T + W;
     const int key_dim = a.Hk * Dk, C = 2 * key_dim + a.Hv * a.Dv;
     const uint16_t* xs = p.x + (int64_t)b * p.x_sb;
-    const uint16_t* ws = p.window + (int64_t)b * W * C;
+    const int wrow = p.win_idx ? p.win_idx[b] : b;
+    const int pslot = p.pre_idx ? p.pre_idx[b] : b;
+    const uint16_t* ws = p.window + (int64_t)wrow * W * C;
     auto src_row = [&](int i) { return i < W ? ws + (int64_t)i * C : xs + (int64_t)(i - W) * p.x_st; };
     auto qk_chan = [&](int pc) { return (pc < GW ? hk * Dk : key_dim + hk * Dk - GW * 8) + pc * 8; };
     const int vc0 = 2 * key_dim + h * a.Dv + vt * VPB;  // this block's first v channel
@@ -255,7 +278,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     lds_gather<16>(&s_qkw[1][0], Dk * Kc / 8,
                    [&](int i) { return (const void*)(p.conv_w + (int64_t)(key_dim + hk * Dk) * Kc + i * 8); }, NT);
     lds_gather<4>(&s_vw[0], VPB * Kc / 2, [&](int i) { return (const void*)(p.conv_w + (int64_t)vc0 * Kc + i * 2); }, NT);
-    const bool grow = tid < a.T;
+    const bool grow = tid < T;
     float av = 0.f, bv = 0.f;
     if (grow) {
       av = bf2f(p.a_in[(int64_t)b * p.ab_sb + (int64_t)tid * p.ab_st + h]);
@@ -271,7 +294,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       s_g[tid] = __expf(gl);
       s_b[tid] = be;
       if (vt == 0 && p.g_out) {
-        const int64_t o = ((int64_t)b * a.T + tid) * a.Hv + h;
+        const int64_t o = (row0 + tid) * a.Hv + h;
         p.g_out[o] = gl;
         p.beta_out[o] = be;
       }
@@ -287,9 +310,13 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
 #pragma unroll
         for (int j = 0; j < kMaxKc; ++j)
           w[ch][j] = j < Kc ? bf2f(s_qkw[pc < GW ? 0 : 1][((pc % GW) * 8 + ch) * Kc + j]) : 0.f;
-      const int tpad = (a.T + nparts - 1) / nparts * nparts;
+      const int tpad = (T + nparts - 1) / nparts * nparts;
+      float bias[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (p.conv_bias) unpack8(*reinterpret_cast<const u32x4*>(p.conv_bias + qk_chan(pc)), bias);
       for (int t = part; t < tpad; t += nparts) {
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float acc[8];
+#pragma unroll
+        for (int ch = 0; ch < 8; ++ch) acc[ch] = bias[ch];
 #pragma unroll
         for (int j = 0; j < kMaxKc; ++j) {
           if (j < Kc) {
@@ -309,26 +336,26 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
         const float inv = rsqrtf(ss + 1e-6f);
 #pragma unroll
         for (int ch = 0; ch < 8; ++ch) acc[ch] *= inv;
-        if (t < a.T) {
+        if (t < T) {
           const u32x4 pk = pack8(acc);
           if (pc < GW) {
             *reinterpret_cast<u32x4*>(&s_q[t][pc * 8]) = pk;
           } else {
             *reinterpret_cast<u32x4*>(&s_k[t][(pc - GW) * 8]) = pk;
             if (qk_writer && p.k_out)
-              *reinterpret_cast<u32x4*>(p.k_out + (((int64_t)b * a.T + t) * a.Hk + hk) * Dk + (pc - GW) * 8) = pk;
+              *reinterpret_cast<u32x4*>(p.k_out + ((row0 + t) * a.Hk + hk) * Dk + (pc - GW) * 8) = pk;
           }
         }
       }
     }
     // v: one (row, column) per thread
-    for (int e = tid; e < a.T * VPB; e += NT) {
+    for (int e = tid; e < T * VPB; e += NT) {
       const int t = e / VPB, cc = e % VPB;
-      float acc = 0.f;
+      float acc = p.conv_bias ? bf2f(p.conv_bias[vc0 + cc]) : 0.f;
       for (int j = 0; j < Kc; ++j) acc = fmaf(bf2f(s_vw[cc * Kc + j]), bf2f(s_vsrc[t + j][cc]), acc);
       const uint16_t vb16 = f2bf(silu(acc));
       s_v[t][cc] = vb16;
-      if (p.v_out) p.v_out[((int64_t)b * a.T + t) * a.Hv * a.Dv + h * a.Dv + vt * VPB + cc] = vb16;
+      if (p.v_out) p.v_out[(row0 + t) * a.Hv * a.Dv + h * a.Dv + vt * VPB + cc] = vb16;
     }
     // raw pre-conv rows and the new window (last Kc-1 rows of [window ++ x]) of this block's channels
     if (p.pre_out || p.window_out) {
@@ -337,15 +364,15 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
         if (!qk_writer) break;
         const u32x4 val = *reinterpret_cast<const u32x4*>(&s_src[i][pc * 8]);
         if (p.pre_out && i >= W)
-          *reinterpret_cast<u32x4*>(p.pre_out + ((int64_t)b * a.T + (i - W)) * C + qk_chan(pc)) = val;
+          *reinterpret_cast<u32x4*>(p.pre_out + ((int64_t)pslot * T + (i - W)) * C + qk_chan(pc)) = val;
         if (p.window_out && i >= nsrc - W)
-          *reinterpret_cast<u32x4*>(p.window_out + ((int64_t)b * W + (i - (nsrc - W))) * C + qk_chan(pc)) = val;
+          *reinterpret_cast<u32x4*>(p.window_out + ((int64_t)wrow * W + (i - (nsrc - W))) * C + qk_chan(pc)) = val;
       }
       for (int e = tid; e < nsrc * VPB; e += NT) {
         const int i = e / VPB, cc = e % VPB;
         const uint16_t val = s_vsrc[i][cc];
-        if (p.pre_out && i >= W) p.pre_out[((int64_t)b * a.T + (i - W)) * C + vc0 + cc] = val;
-        if (p.window_out && i >= nsrc - W) p.window_out[((int64_t)b * W + (i - (nsrc - W))) * C + vc0 + cc] = val;
+        if (p.pre_out && i >= W) p.pre_out[((int64_t)pslot * T + (i - W)) * C + vc0 + cc] = val;
+        if (p.window_out && i >= nsrc - W) p.window_out[((int64_t)wrow * W + (i - (nsrc - W))) * C + vc0 + cc] = val;
       }
     }
     __syncthreads();
@@ -380,8 +407,8 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     for (int i = 0; i < KPL; ++i) st[i] = fmaf(R.kk[i], delta, st[i]);
     return fmaf(delta, R.kq, sq);
   };
-  for (int t0 = 0; t0 < a.T; t0 += tcn) {
-    const int tn = min(tcn, a.T - t0);
+  for (int t0 = 0; t0 < T; t0 += tcn) {
+    const int tn = min(tcn, T - t0);
     if constexpr (F32) {
       __syncthreads();  // previous chunk fully consumed (its readout rows stored)
       // stage the chunk through registers in one round trip (clamped, unconditional loads): q * scale and
@@ -520,57 +547,69 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
           if (keep && kl == 0) ob[(int64_t)(t0 + r) * v_row] = f2bf(o);
         }
       };
+      // the state after row r, when the caller keeps intermediates (uniform branch)
+      auto stash = [&](int r) {
+        if (t0 + r < csteps) {
+#pragma unroll
+          for (int i = 0; i < KPL; ++i) inter_col[(int64_t)(t0 + r) * hvk + i] = s[i];
+        }
+      };
       Row ra, rb;
       fetch(ra, r0);
       int r = r0;
       for (; r + 1 < r1; r += 2) {
         fetch(rb, r + 1);
         put(r, apply(s, ra));
+        stash(r);
         fetch(ra, min(r + 2, r1 - 1));
         put(r + 1, apply(s, rb));
+        stash(r + 1);
       }
-      if (r < r1) put(r, apply(s, ra));
+      if (r < r1) {
+        put(r, apply(s, ra));
+        stash(r);
+      }
     };
     const int rc = min(max(nc - t0, 0), tn);  // the chunk's rows t < nc, whose readout is kept
     run(0, rc, true);
     if (a.state_clean && rc > 0 && t0 + rc == nc) {  // the state after the last clean row
 #pragma unroll
-      for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = s[i];
+      for (int i = 0; i < KPL; ++i) a.state_clean[cl_off + i] = s[i];
     }
     run(rc, tn, false);
     if constexpr (F32) {
       __syncthreads();
-      uint16_t* otile = a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + vt * VPB;
+      uint16_t* otile = a.out + row0 * v_row + (int64_t)h * a.Dv + vt * VPB;
       for (int e = tid; e < rc * VPB; e += NW * kWave)
         otile[(int64_t)(t0 + e / VPB) * v_row + e % VPB] = f2bf(s_ob[e / VPB][e % VPB]);
     }
   }
   if (nc == 0 && a.state_clean) {
 #pragma unroll
-    for (int i = 0; i < KPL; ++i) a.state_clean[st_off + i] = a.state_in[st_off + i];
+    for (int i = 0; i < KPL; ++i) a.state_clean[cl_off + i] = a.state_in[st_off + i];
   }
   // MASK rows (causal_mode 2): read the block-end state, four rows at a time. On a large grid (many
   // sequences: issue-bound) their q * scale is formed once per block in fp32 (the same products the
   // per-lane path forms) into the k stage, dead after the causal rows: its kTC x Dk bf16 hold kTC / 2
   // rows of Dk fp32 (batch 64: 184 -> 170 us per layer). On a grid of a few hundred blocks (batch 1:
   // latency-bound) the two barriers cost more than they save, so each lane converts its own q.
-  const int nm = a.T - nc;
-  const bool qf_staged = !F32 && (PREP || a.T <= tcn) && nm > 0 && nm <= TC / 2 && gridDim.x >= 1024;  // block-uniform
+  const int nm = T - nc;
+  const bool qf_staged = !F32 && (PREP || T <= tcn) && nm > 0 && nm <= TC / 2 && gridDim.x >= 1024;  // block-uniform
   float* s_qf = reinterpret_cast<float*>(&s_k[0][0]);
   if (qf_staged) {
     __syncthreads();  // every wave is done with the k rows
     for (int e = tid; e < nm * Dk; e += NW * kWave) s_qf[e] = bf2f(s_q[nc + e / Dk][e % Dk]) * a.scale;
     __syncthreads();
   }
-  if (F32 && a.T <= tcn && nm > 0) {
+  if (F32 && T <= tcn && nm > 0) {
     // the whole block is the last staged chunk (s_qf32 holds every row): eight rows at a time, two
     // interleaved 4-row reductions (each row's fma order and row16 reduction as below), the readouts
     // kept in LDS and stored together
-    for (int t = nc; t < a.T; t += 8) {
+    for (int t = nc; t < T; t += 8) {
       float o0[4], o1[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int ta = min(t + j, a.T - 1), tb = min(t + 4 + j, a.T - 1);
+        const int ta = min(t + j, T - 1), tb = min(t + 4 + j, T - 1);
         o0[j] = 0.f;
         o1[j] = 0.f;
 #pragma unroll
@@ -583,22 +622,22 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       row16_sum4(o1);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        if (t + j < a.T) s_ob[t + j][vl] = o0[j];
-        if (t + 4 + j < a.T) s_ob[t + 4 + j][vl] = o1[j];
+        if (t + j < T) s_ob[t + j][vl] = o0[j];
+        if (t + 4 + j < T) s_ob[t + 4 + j][vl] = o1[j];
       }
     }
     __syncthreads();
-    uint16_t* otile = a.out + (int64_t)b * a.T * v_row + (int64_t)h * a.Dv + vt * VPB;
+    uint16_t* otile = a.out + row0 * v_row + (int64_t)h * a.Dv + vt * VPB;
     for (int e = tid; e < nm * VPB; e += NW * kWave)
       otile[(int64_t)(nc + e / VPB) * v_row + e % VPB] = f2bf(s_ob[nc + e / VPB][e % VPB]);
   } else
-  for (int t = nc; t < a.T; t += 4) {
+  for (int t = nc; t < T; t += 4) {
     float o[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int tt = min(t + j, a.T - 1);
+      const int tt = min(t + j, T - 1);
       o[j] = 0.f;
-      if (F32 && a.T <= tcn) {  // the whole block is the last staged chunk
+      if (F32 && T <= tcn) {  // the whole block is the last staged chunk
 #pragma unroll
         for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], s_qf32[tt][kl * KPL + i], o[j]);
       } else if (qf_staged) {
@@ -607,7 +646,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
         for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], qr[i], o[j]);
       } else {
         // the lane's KPL entries of q row tt: from LDS when the whole block was staged
-        const uint16_t* qr = ((PREP || a.T <= tcn) ? &s_q[tt][0] : qb + (int64_t)tt * qk_row) + kl * KPL;
+        const uint16_t* qr = ((PREP || T <= tcn) ? &s_q[tt][0] : qb + (int64_t)tt * qk_row) + kl * KPL;
 #pragma unroll
         for (int i = 0; i < KPL; ++i) o[j] = fmaf(s[i], bf2f(qr[i]) * a.scale, o[j]);
       }
@@ -615,7 +654,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     row16_sum4(o);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      if (t + j < a.T && kl == 0) ob[(int64_t)(t + j) * v_row] = f2bf(o[j]);
+      if (t + j < T && kl == 0) ob[(int64_t)(t + j) * v_row] = f2bf(o[j]);
   }
   if (a.state_out) {
 #pragma unroll
@@ -657,7 +696,8 @@ extern "C" int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const u
                                    const float* beta, const float* state_in, uint16_t* out, float* state_out,
                                    float* state_clean, int64_t B, int64_t T, int64_t Hk, int64_t Hv,
                                    int64_t Dk, int64_t Dv, int causal_mode, int64_t num_clean, float scale,
-                                   void* stream) {
+                                   const int32_t* cu_seqlens, const int32_t* state_idx, float* inter,
+                                   const int32_t* inter_idx, int64_t cache_steps, void* stream) {
   TRIDA_CHECK(q && k && v && g && beta && state_in && out, TRIDA_ERR_NULL,
               "gdr_recurrent: q, k, v, g, beta, state_in and out are required");
   TRIDA_CHECK(B > 0 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0, TRIDA_ERR_ARG,
@@ -673,8 +713,12 @@ extern "C" int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const u
   TRIDA_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 3) == 0, TRIDA_ERR_ALIGN,
               "gdr_recurrent: q and k must be 16-byte aligned, v 4-byte aligned");
   TRIDA_CHECK(B * T * Hv < INT32_MAX, TRIDA_ERR_ARG, "gdr_recurrent: problem too large");
+  TRIDA_CHECK(inter == nullptr || (cache_steps >= 1 && cache_steps <= INT32_MAX), TRIDA_ERR_ARG,
+              "gdr_recurrent: cache_steps >= 1 with inter");
+  TRIDA_CHECK(inter == nullptr || ((uintptr_t)inter & 15) == 0, TRIDA_ERR_ALIGN, "gdr_recurrent: inter 16-byte aligned");
   RecArgs a{q, k, v, g, beta, state_in, out, state_out, state_clean, (int)T, (int)Hk, (int)Hv, (int)Dk,
-            (int)Dv, causal_mode, (int)num_clean, scale, 0, PrepIn{}};
+            (int)Dv, causal_mode, (int)num_clean, scale, 0, PrepIn{}, cu_seqlens, state_idx, inter, inter_idx,
+            inter ? (int)cache_steps : 0};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (Dk) {
     case 32: return launch_kpl<2>(a, (int)B, st);
@@ -716,7 +760,10 @@ extern "C" int trida_gdn_fused_layer(const uint16_t* x, const uint16_t* window, 
                                      float* beta_out, uint16_t* pre_out, uint16_t* window_out, int64_t B,
                                      int64_t T, int64_t Kc, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv,
                                      int64_t x_sb, int64_t x_st, int64_t ab_sb, int64_t ab_st, int causal_mode,
-                                     int64_t num_clean, float scale, void* stream) {
+                                     int64_t num_clean, float scale, const uint16_t* conv_bias,
+                                     const int32_t* win_idx, const int32_t* state_idx, float* inter,
+                                     const int32_t* inter_idx, int64_t cache_steps, const int32_t* pre_idx,
+                                     void* stream) {
   TRIDA_CHECK(x && window && conv_w && a_in && b_in && A_log && dt_bias && state_in && out, TRIDA_ERR_NULL,
               "gdn_fused_layer: x, window, conv_w, a, b, A_log, dt_bias, state_in and out are required");
   TRIDA_CHECK(B > 0 && T > 0 && T <= kTC && Hk > 0 && Hv > 0 && Hv % Hk == 0 && Kc >= 2 && Kc <= kMaxKc,
@@ -738,10 +785,16 @@ extern "C" int trida_gdn_fused_layer(const uint16_t* x, const uint16_t* window, 
                   ((uintptr_t)window_out & 15) == 0,
               TRIDA_ERR_ALIGN, "gdn_fused_layer: x, window, conv_w, k_out, pre_out, window_out 16-byte aligned, x strides in multiples of 8");
   TRIDA_CHECK(B * T * Hv < INT32_MAX && B * T * C < INT32_MAX * 8LL, TRIDA_ERR_ARG, "gdn_fused_layer: problem too large");
+  TRIDA_CHECK(inter == nullptr || (cache_steps >= 1 && cache_steps <= INT32_MAX), TRIDA_ERR_ARG,
+              "gdn_fused_layer: cache_steps >= 1 with inter");
+  TRIDA_CHECK(inter == nullptr || ((uintptr_t)inter & 15) == 0, TRIDA_ERR_ALIGN, "gdn_fused_layer: inter 16-byte aligned");
+  TRIDA_CHECK(conv_bias == nullptr || ((uintptr_t)conv_bias & 15) == 0, TRIDA_ERR_ALIGN,
+              "gdn_fused_layer: conv_bias 16-byte aligned");
   RecArgs a{nullptr, nullptr, nullptr, nullptr, nullptr, state_in, out, state_out, state_clean, (int)T, (int)Hk,
             (int)Hv, (int)Dk, (int)Dv, causal_mode, (int)num_clean, scale, 0,
             PrepIn{x, window, conv_w, a_in, b_in, A_log, dt_bias, k_out, v_out, g_out, beta_out, pre_out, window_out,
-                   x_sb, x_st, ab_sb, ab_st, (int)Kc}};
+                   conv_bias, win_idx, pre_idx, x_sb, x_st, ab_sb, ab_st, (int)Kc},
+            nullptr, state_idx, inter, inter_idx, inter ? (int)cache_steps : 0};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (Dk) {
     case 32: return launch_kpl<2, true>(a, (int)B, st);

@@ -147,6 +147,8 @@ struct WindowArgs {
   int seq_mod, T, C, Kc, skip_full;
   int64_t x_sb, x_st;
   int64_t total;  // NB * C / 8 threads do work
+  const int32_t* win_idx;  // [NB] window row (snapshot and output) of slot b, or null (row b)
+  const int32_t* pre_idx;  // [NB] preconv slot of slot b, or null (slot b)
 };
 
 __global__ __launch_bounds__(256) void restore_window_kernel(WindowArgs a) {
@@ -159,6 +161,8 @@ __global__ __launch_bounds__(256) void restore_window_kernel(WindowArgs a) {
   const int n = min(max(a.n_keep[b % a.seq_mod], 0), a.T);
   if (a.skip_full && n == a.T) return;
   const int W = a.Kc - 1;
+  const int64_t wrow = a.win_idx ? a.win_idx[b] : b;
+  const int64_t prow = a.pre_idx ? a.pre_idx[b] : b;
   u32x4 rows[kMaxRows];
   // window row w of (snapshot ++ preconv[:n]) tail: source index m = n + w over the concatenation
   // all reads before any write: the output may alias the snapshot window
@@ -166,14 +170,14 @@ __global__ __launch_bounds__(256) void restore_window_kernel(WindowArgs a) {
   for (int w = 0; w < kMaxRows; ++w) {
     if (w < W) {
       const int m = n + w;  // position in [snapshot rows 0..W-1, preconv rows 0..n-1]
-      const uint16_t* src = m < W ? a.snap_window + ((int64_t)b * W + m) * a.C + c
-                                  : a.preconv + (int64_t)b * a.x_sb + (int64_t)(m - W) * a.x_st + c;
+      const uint16_t* src = m < W ? a.snap_window + (wrow * W + m) * a.C + c
+                                  : a.preconv + prow * a.x_sb + (int64_t)(m - W) * a.x_st + c;
       rows[w] = *reinterpret_cast<const u32x4*>(src);
     }
   }
 #pragma unroll
   for (int w = 0; w < kMaxRows; ++w)
-    if (w < W) *reinterpret_cast<u32x4*>(a.window + ((int64_t)b * W + w) * a.C + c) = rows[w];
+    if (w < W) *reinterpret_cast<u32x4*>(a.window + (wrow * W + w) * a.C + c) = rows[w];
 }
 
 template <int KPL>
@@ -224,7 +228,7 @@ extern "C" int trida_gdn_restore(const float* snap_state, float* state, const ui
                                  uint16_t* window, const uint16_t* preconv, const int32_t* n_keep,
                                  int64_t NB, int64_t seq_mod, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk,
                                  int64_t Dv, int64_t C, int64_t Kc, int64_t x_sb, int64_t x_st, int skip_full,
-                                 void* stream) {
+                                 const int32_t* win_idx, const int32_t* pre_idx, void* stream) {
   TRIDA_CHECK(n_keep, TRIDA_ERR_NULL, "gdn_restore: n_keep is required");
   TRIDA_CHECK(NB > 0 && T > 0 && seq_mod > 0 && NB % seq_mod == 0, TRIDA_ERR_ARG,
               "gdn_restore: bad NB=%lld seq_mod=%lld T=%lld", (long long)NB, (long long)seq_mod, (long long)T);
@@ -257,7 +261,7 @@ extern "C" int trida_gdn_restore(const float* snap_state, float* state, const ui
                 TRIDA_ERR_ALIGN, "gdn_restore: window buffers must be 16-byte aligned");
     const int64_t threads = NB * (C / 8);
     WindowArgs wa{snap_window, window, preconv, n_keep, (int)seq_mod, (int)T, (int)C, (int)Kc, skip_full,
-                  x_sb, x_st, threads};
+                  x_sb, x_st, threads, win_idx, pre_idx};
     hipLaunchKernelGGL(restore_window_kernel, dim3((unsigned)cdiv(threads, 256)), dim3(256), 0, st, wa);
     return launch_status("gdn_restore/window");
   }

@@ -455,9 +455,29 @@ def _f32(t: torch.Tensor, name: str):
         raise ValueError(f"{name} must be fp32 (got {t.dtype})")
 
 
+def _i32(t: Optional[torch.Tensor], name: str, n: Optional[int] = None):
+    """A contiguous int32 index vector (optionally of n entries), or None."""
+    if t is None:
+        return None
+    if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous() or (n is not None and t.numel() != n):
+        raise ValueError(f"{name} must be a contiguous int32 vector" + (f" of {n} entries" if n is not None else ""))
+    return t
+
+
+def _packed(cu_seqlens: Optional[torch.Tensor], max_rows: Optional[int]):
+    """(B, T) of a packed ragged batch: B sequences, T an upper bound of their rows."""
+    _i32(cu_seqlens, "cu_seqlens")
+    if max_rows is None or int(max_rows) < 1:
+        raise ValueError("a packed batch (cu_seqlens) needs max_rows >= 1, an upper bound of every sequence's rows")
+    return cu_seqlens.numel() - 1, int(max_rows)
+
+
 def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
              A_log: torch.Tensor, dt_bias: torch.Tensor, *, Hk: int, Hv: int, Dk: int, Dv: int,
-             window_out: Optional[torch.Tensor] = None, pre_out: Optional[torch.Tensor] = None, out=None):
+             window_out: Optional[torch.Tensor] = None, pre_out: Optional[torch.Tensor] = None, out=None,
+             conv_bias: Optional[torch.Tensor] = None, win_idx: Optional[torch.Tensor] = None,
+             pre_idx: Optional[torch.Tensor] = None, cu_seqlens: Optional[torch.Tensor] = None,
+             max_rows: Optional[int] = None):
     """Conv + SiLU + split + l2norm(q, k) + gates for a block of rows (one launch).
 
     x [B, T, C] bf16 (last dim contiguous, C = 2*Hk*Dk + Hv*Dv; batch / row strides may be larger),
@@ -465,57 +485,118 @@ def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: tor
     A_log, dt_bias [Hv] fp32. Returns q, k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g, beta [B,T,Hv] fp32.
     window_out (optional, [B, Kc-1, C], not aliasing window) receives the last Kc-1 rows of
     [window ++ x] (the causal-prefill conv state). pre_out (optional, contiguous [B, T, C]) receives a
-    copy of x: the pre-conv rows a rollback rebuilds the window from."""
-    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, window_out, pre_out)
+    copy of x: the pre-conv rows a rollback rebuilds the window from.
+
+    Pool and packed forms (the vLLM conv call's arguments): conv_bias [C] bf16; win_idx int32 [B] picks
+    each sequence's window row of a [rows, Kc-1, C] pool (window_out is then a pool too); pre_idx
+    int32 [B] its pre_out slot of a [slots, T, C] pool; cu_seqlens int32 [B + 1] with max_rows packs the
+    batch: x [total, C], a, b [total, Hv] and the outputs [total, ...]."""
+    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, window_out, pre_out, conv_bias, win_idx, pre_idx,
+                    cu_seqlens)
     for t, n in ((x, "x"), (window, "window"), (conv_w, "conv_w"), (a, "a"), (b, "b")):
         _bf16(t, n)
     _f32(A_log, "A_log")
     _f32(dt_bias, "dt_bias")
-    B, T, C = x.shape
+    packed = cu_seqlens is not None
+    if packed:
+        B, T = _packed(cu_seqlens, max_rows)
+        if x.dim() != 2 or a.dim() != 2:
+            raise ValueError("a packed batch takes x [total, C] and a, b [total, Hv]")
+        rows, C = x.shape
+        lead = (rows,)
+        x_sb, x_st = 0, x.stride(0)
+        ab_sb, ab_st = 0, a.stride(0)
+    else:
+        B, T, C = x.shape
+        lead = (B, T)
+        x_sb, x_st = x.stride(0), x.stride(1)
+        ab_sb, ab_st = a.stride(0), a.stride(1)
     Kc = conv_w.shape[1]
     if C != 2 * Hk * Dk + Hv * Dv or conv_w.shape != (C, Kc) or not conv_w.is_contiguous():
         raise ValueError("x / conv_w do not match the head geometry")
-    if x.stride(2) != 1 or window.shape != (B, Kc - 1, C) or not window.is_contiguous():
-        raise ValueError("x must have a contiguous last dim and window be contiguous [B, Kc-1, C]")
-    if a.shape != (B, T, Hv) or b.shape != (B, T, Hv) or a.stride() != b.stride() or a.stride(2) != 1:
-        raise ValueError("a and b must be [B, T, Hv] with identical strides and a contiguous last dim")
-    if window_out is not None and (window_out.shape != window.shape or not window_out.is_contiguous()
+    win_rows = window.shape[0] if win_idx is not None else B
+    if x.stride(-1) != 1 or window.shape != (win_rows, Kc - 1, C) or not window.is_contiguous():
+        raise ValueError("x must have a contiguous last dim and window be contiguous [B (or pool rows), Kc-1, C]")
+    if a.shape != lead + (Hv,) or b.shape != a.shape or a.stride() != b.stride() or a.stride(-1) != 1:
+        raise ValueError("a and b must be [..., Hv] like x's rows, with identical strides and a contiguous last dim")
+    _i32(win_idx, "win_idx", B)
+    _i32(pre_idx, "pre_idx", B)
+    if conv_bias is not None:
+        _bf16(conv_bias, "conv_bias")
+        if conv_bias.shape != (C,) or not conv_bias.is_contiguous():
+            raise ValueError("conv_bias must be contiguous [C]")
+    if window_out is not None and (window_out.shape[1:] != window.shape[1:] or not window_out.is_contiguous()
+                                   or (win_idx is None and window_out.shape != window.shape)
                                    or window_out.data_ptr() == window.data_ptr()):
-        raise ValueError("window_out must be a separate contiguous [B, Kc-1, C] buffer")
+        raise ValueError("window_out must be a separate contiguous [B (or pool rows), Kc-1, C] buffer")
     if pre_out is not None:
         _bf16(pre_out, "pre_out")
-        if pre_out.shape != (B, T, C) or not pre_out.is_contiguous() or pre_out.data_ptr() == x.data_ptr():
-            raise ValueError("pre_out must be a separate contiguous [B, T, C] buffer")
+        slots = pre_out.shape[0] if pre_idx is not None else B
+        if pre_out.shape != (slots, T, C) or not pre_out.is_contiguous() or pre_out.data_ptr() == x.data_ptr():
+            raise ValueError("pre_out must be a separate contiguous [B (or pool slots), T, C] buffer")
     if out is None:
-        q = torch.empty((B, T, Hk, Dk), dtype=torch.bfloat16, device=dev)
+        q = torch.empty(lead + (Hk, Dk), dtype=torch.bfloat16, device=dev)
         k = torch.empty_like(q)
-        v = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
-        g = torch.empty((B, T, Hv), dtype=torch.float32, device=dev)
+        v = torch.empty(lead + (Hv, Dv), dtype=torch.bfloat16, device=dev)
+        g = torch.empty(lead + (Hv,), dtype=torch.float32, device=dev)
         beta = torch.empty_like(g)
     else:
         q, k, v, g, beta = out
-        if q.shape != (B, T, Hk, Dk) or k.shape != q.shape or v.shape != (B, T, Hv, Dv) or g.shape != (B, T, Hv) \
+        if q.shape != lead + (Hk, Dk) or k.shape != q.shape or v.shape != lead + (Hv, Dv) or g.shape != lead + (Hv,) \
                 or beta.shape != g.shape or not all(t.is_contiguous() for t in out):
             raise ValueError("gdn_prep: out buffers have the wrong shape")
     rc = _lib.load().trida_gdn_prep(
         x.data_ptr(), window.data_ptr(), conv_w.data_ptr(), a.data_ptr(), b.data_ptr(),
         A_log.contiguous().data_ptr(), dt_bias.contiguous().data_ptr(), q.data_ptr(), k.data_ptr(),
         v.data_ptr(), g.data_ptr(), beta.data_ptr(), _ptr(window_out), _ptr(pre_out), B, T, Kc, Hk, Hv, Dk, Dv,
-        x.stride(0), x.stride(1), a.stride(0), a.stride(1), _stream(dev))
+        x_sb, x_st, ab_sb, ab_st, _ptr(conv_bias), _ptr(win_idx), _ptr(pre_idx), _ptr(cu_seqlens), _stream(dev))
     _lib.check(rc, "trida_gdn_prep")
     return q, k, v, g, beta
+
+
+def _state_pool(state: torch.Tensor, B: int, Hv: int, Dv: int, Dk: int, state_idx: Optional[torch.Tensor]):
+    _i32(state_idx, "state_idx", B)
+    rows = state.shape[0] if state_idx is not None else B
+    if state.shape != (rows, Hv, Dv, Dk) or not state.is_contiguous():
+        raise ValueError(f"state must be contiguous [B (or pool rows), Hv, Dv, Dk] = {(rows, Hv, Dv, Dk)}")
+
+
+def _ring(inter: Optional[torch.Tensor], inter_idx: Optional[torch.Tensor], cache_steps: Optional[int], B: int,
+          Hv: int, Dv: int, Dk: int) -> int:
+    """cache_steps of an intermediate-state ring inter [rows, cache_steps, Hv, Dv, Dk] fp32 (0 without)."""
+    if inter is None:
+        if inter_idx is not None:
+            raise ValueError("inter_idx without inter")
+        return 0
+    _f32(inter, "inter")
+    steps = inter.shape[1] if cache_steps is None else int(cache_steps)
+    rows = inter.shape[0] if inter_idx is not None else B
+    if inter.dim() != 5 or inter.shape != (rows, steps, Hv, Dv, Dk) or not inter.is_contiguous() or steps < 1:
+        raise ValueError(f"inter must be contiguous [B (or ring rows), cache_steps, Hv, Dv, Dk] fp32")
+    _i32(inter_idx, "inter_idx", B)
+    return steps
 
 
 def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
                   state: torch.Tensor, *, causal_mode: int = 1, num_clean: Optional[int] = None,
                   state_out: Optional[torch.Tensor] = None, want_clean: bool = False,
-                  scale: Optional[float] = None, out: Optional[torch.Tensor] = None):
+                  scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                  cu_seqlens: Optional[torch.Tensor] = None, max_rows: Optional[int] = None,
+                  state_idx: Optional[torch.Tensor] = None, inter: Optional[torch.Tensor] = None,
+                  inter_idx: Optional[torch.Tensor] = None, cache_steps: Optional[int] = None):
     """Gated delta rule over T rows with the block-causal readout (one launch).
 
     q, k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g (log decay), beta [B,T,Hv] fp32, state [B,Hv,Dv,Dk]
     fp32 (read only unless passed again as state_out). causal_mode 2 with num_clean: rows >= num_clean
-    read the block-end state. Returns (out [B,T,Hv,Dv] bf16, state_clean or None)."""
-    dev = _need_gpu(q, k, v, g, beta, state, state_out)
+    read the block-end state. Returns (out [B,T,Hv,Dv] bf16, state_clean or None).
+
+    Pool, ring and packed forms (fused_recurrent_block_causal_gated_delta_rule[_packed]'s arguments):
+    state_idx int32 [B] picks each sequence's row of a state pool [rows, Hv, Dv, Dk] (read, and written
+    when state_out is the pool); inter [rows, cache_steps, Hv, Dv, Dk] fp32 with inter_idx int32 [B]
+    receives the state after rows 0..j (j < cache_steps) of each sequence; cu_seqlens int32 [B + 1] with
+    max_rows packs the batch: q, k [total, Hk, Dk], v [total, Hv, Dv], g, beta [total, Hv], out
+    [total, Hv, Dv]."""
+    dev = _need_gpu(q, k, v, g, beta, state, state_out, cu_seqlens, state_idx, inter, inter_idx)
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _bf16(t, n)
         if not t.is_contiguous():
@@ -524,26 +605,34 @@ def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
         _f32(t, n)
         if not t.is_contiguous():
             raise ValueError(f"{n} must be contiguous")
-    B, T, Hk, Dk = k.shape
-    Hv, Dv = v.shape[2], v.shape[3]
-    if q.shape != k.shape or v.shape[:2] != (B, T) or g.shape != (B, T, Hv) or beta.shape != g.shape:
+    Hk, Dk = k.shape[-2:]
+    Hv, Dv = v.shape[-2:]
+    if cu_seqlens is not None:
+        B, T = _packed(cu_seqlens, max_rows)
+        if k.dim() != 3:
+            raise ValueError("a packed batch takes q, k [total, Hk, Dk], v [total, Hv, Dv], g, beta [total, Hv]")
+        lead = (k.shape[0],)
+    else:
+        B, T = k.shape[:2]
+        lead = (B, T)
+    if q.shape != k.shape or v.shape[:-2] != lead or g.shape != lead + (Hv,) or beta.shape != g.shape:
         raise ValueError("q/k/v/g/beta shapes disagree")
-    if state.shape != (B, Hv, Dv, Dk):
-        raise ValueError(f"state must be [B, Hv, Dv, Dk] = {(B, Hv, Dv, Dk)}")
+    _state_pool(state, B, Hv, Dv, Dk, state_idx)
     if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
                                   or not state_out.is_contiguous()):
         raise ValueError("state_out must match state")
+    steps = _ring(inter, inter_idx, cache_steps, B, Hv, Dv, Dk)
     nc = T if num_clean is None else int(num_clean)
     if out is None:
-        out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
-    elif out.shape != (B, T, Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
-        raise ValueError("gdr_recurrent: out must be contiguous bf16 [B, T, Hv, Dv]")
-    clean = torch.empty_like(state) if want_clean else None
+        out = torch.empty(lead + (Hv, Dv), dtype=torch.bfloat16, device=dev)
+    elif out.shape != lead + (Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("gdr_recurrent: out must be contiguous bf16 like v")
+    clean = torch.empty((B, Hv, Dv, Dk), dtype=torch.float32, device=dev) if want_clean else None
     sc = Dk ** -0.5 if scale is None else float(scale)
     rc = _lib.load().trida_gdr_recurrent(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), state.data_ptr(),
         out.data_ptr(), _ptr(state_out), _ptr(clean), B, T, Hk, Hv, Dk, Dv, causal_mode, nc, sc,
-        _stream(dev))
+        _ptr(cu_seqlens), _ptr(state_idx), _ptr(inter), _ptr(inter_idx), steps, _stream(dev))
     _lib.check(rc, "trida_gdr_recurrent")
     return out, clean
 
@@ -554,14 +643,20 @@ def gdn_fused_layer(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor,
                     state_out: Optional[torch.Tensor] = None, want_clean: bool = False,
                     rows_out: Optional[tuple] = None, pre_out: Optional[torch.Tensor] = None,
                     window_out: Optional[torch.Tensor] = None, scale: Optional[float] = None,
-                    out: Optional[torch.Tensor] = None):
+                    out: Optional[torch.Tensor] = None, conv_bias: Optional[torch.Tensor] = None,
+                    win_idx: Optional[torch.Tensor] = None, state_idx: Optional[torch.Tensor] = None,
+                    inter: Optional[torch.Tensor] = None, inter_idx: Optional[torch.Tensor] = None,
+                    cache_steps: Optional[int] = None, pre_idx: Optional[torch.Tensor] = None):
     """The GDN layer's conv + prep + recurrence + readout for a block of T <= 64 rows in one launch
     (fused_selfspec_gdn_layer, qwen3_5_diffusion.py:2207-2221); bit-identical to gdn_prep followed by
     gdr_recurrent. Inputs as gdn_prep plus state [B, Hv, Dv, Dk] fp32. Optional outputs:
     rows_out = (k [B,T,Hk,Dk] bf16, v [B,T,Hv,Dv] bf16, g, beta [B,T,Hv] fp32) for a rollback,
     pre_out [B, T, C] bf16 (raw pre-conv rows), window_out [B, Kc-1, C] (not aliasing window).
+    The vLLM call's pool / ring arguments (conv_bias, win_idx, state_idx = ssm_idx, inter / inter_idx /
+    cache_steps, pre_idx = slot_idx) have the meanings of gdn_prep and gdr_recurrent.
     Returns (out [B,T,Hv,Dv] bf16, state_clean or None)."""
-    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, state, state_out, out, pre_out, window_out)
+    dev = _need_gpu(x, window, conv_w, a, b, A_log, dt_bias, state, state_out, out, pre_out, window_out, conv_bias,
+                    win_idx, state_idx, inter, inter_idx, pre_idx)
     for t, n in ((x, "x"), (window, "window"), (conv_w, "conv_w"), (a, "a"), (b, "b")):
         _bf16(t, n)
     for t, n in ((A_log, "A_log"), (dt_bias, "dt_bias"), (state, "state")):
@@ -570,21 +665,30 @@ def gdn_fused_layer(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor,
     Kc = conv_w.shape[1]
     if C != 2 * Hk * Dk + Hv * Dv or conv_w.shape != (C, Kc) or not conv_w.is_contiguous():
         raise ValueError("x / conv_w do not match the head geometry")
-    if x.stride(2) != 1 or window.shape != (B, Kc - 1, C) or not window.is_contiguous():
-        raise ValueError("x must have a contiguous last dim and window be contiguous [B, Kc-1, C]")
+    win_rows = window.shape[0] if win_idx is not None else B
+    if x.stride(2) != 1 or window.shape != (win_rows, Kc - 1, C) or not window.is_contiguous():
+        raise ValueError("x must have a contiguous last dim and window be contiguous [B (or pool rows), Kc-1, C]")
     if a.shape != (B, T, Hv) or b.shape != (B, T, Hv) or a.stride() != b.stride() or a.stride(2) != 1:
         raise ValueError("a and b must be [B, T, Hv] with identical strides and a contiguous last dim")
-    if state.shape != (B, Hv, Dv, Dk) or not state.is_contiguous():
-        raise ValueError(f"state must be contiguous [B, Hv, Dv, Dk] = {(B, Hv, Dv, Dk)}")
+    _i32(win_idx, "win_idx", B)
+    _i32(pre_idx, "pre_idx", B)
+    _state_pool(state, B, Hv, Dv, Dk, state_idx)
     if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
                                   or not state_out.is_contiguous()):
         raise ValueError("state_out must match state")
-    if window_out is not None and (window_out.shape != window.shape or not window_out.is_contiguous()
+    steps = _ring(inter, inter_idx, cache_steps, B, Hv, Dv, Dk)
+    if conv_bias is not None:
+        _bf16(conv_bias, "conv_bias")
+        if conv_bias.shape != (C,) or not conv_bias.is_contiguous():
+            raise ValueError("conv_bias must be contiguous [C]")
+    if window_out is not None and (window_out.shape[1:] != window.shape[1:] or not window_out.is_contiguous()
+                                   or (win_idx is None and window_out.shape != window.shape)
                                    or window_out.data_ptr() == window.data_ptr()):
-        raise ValueError("window_out must be a separate contiguous [B, Kc-1, C] buffer")
-    if pre_out is not None and (pre_out.shape != (B, T, C) or pre_out.dtype != torch.bfloat16
-                                or not pre_out.is_contiguous()):
-        raise ValueError("pre_out must be contiguous bf16 [B, T, C]")
+        raise ValueError("window_out must be a separate contiguous [B (or pool rows), Kc-1, C] buffer")
+    if pre_out is not None:
+        slots = pre_out.shape[0] if pre_idx is not None else B
+        if pre_out.shape != (slots, T, C) or pre_out.dtype != torch.bfloat16 or not pre_out.is_contiguous():
+            raise ValueError("pre_out must be contiguous bf16 [B (or pool slots), T, C]")
     kr = vr = gr = br = None
     if rows_out is not None:
         kr, vr, gr, br = rows_out
@@ -596,13 +700,14 @@ def gdn_fused_layer(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor,
         out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
     elif out.shape != (B, T, Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise ValueError("gdn_fused_layer: out must be contiguous bf16 [B, T, Hv, Dv]")
-    clean = torch.empty_like(state) if want_clean else None
+    clean = torch.empty((B, Hv, Dv, Dk), dtype=torch.float32, device=dev) if want_clean else None
     sc = Dk ** -0.5 if scale is None else float(scale)
     rc = _lib.load().trida_gdn_fused_layer(
         x.data_ptr(), window.data_ptr(), conv_w.data_ptr(), a.data_ptr(), b.data_ptr(),
         A_log.contiguous().data_ptr(), dt_bias.contiguous().data_ptr(), state.data_ptr(), out.data_ptr(),
         _ptr(state_out), _ptr(clean), _ptr(kr), _ptr(vr), _ptr(gr), _ptr(br), _ptr(pre_out), _ptr(window_out),
         B, T, Kc, Hk, Hv, Dk, Dv, x.stride(0), x.stride(1), a.stride(0), a.stride(1), causal_mode, nc, sc,
+        _ptr(conv_bias), _ptr(win_idx), _ptr(state_idx), _ptr(inter), _ptr(inter_idx), steps, _ptr(pre_idx),
         _stream(dev))
     _lib.check(rc, "trida_gdn_fused_layer")
     return out, clean
@@ -646,12 +751,16 @@ def gdr_block_bidir(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.
 def gdr_chunk(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
               state: torch.Tensor, *, causal_mode: int = 1, num_clean: Optional[int] = None,
               state_out: Optional[torch.Tensor] = None, n_keep: Optional[torch.Tensor] = None,
-              want_out: bool = True, scale: Optional[float] = None, out: Optional[torch.Tensor] = None):
+              want_out: bool = True, scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+              cu_seqlens: Optional[torch.Tensor] = None, max_rows: Optional[int] = None,
+              state_idx: Optional[torch.Tensor] = None):
     """Gated delta rule in the chunked WY / UT form on MFMA (chunks of 64 rows; one fused launch for
     T <= 64). Same shapes and readout as gdr_recurrent. n_keep (int32 [B] or [seq_mod] with B a multiple):
     state_out holds the state after the first n_keep[b] rows (the rollback). want_out=False skips the
-    readout (q may be None). Returns out (or None)."""
-    dev = _need_gpu(q, k, v, g, beta, state, state_out, n_keep, out)
+    readout (q may be None). cu_seqlens (int32 [B + 1]) with max_rows packs a ragged batch ([total, ...]
+    rows) and state_idx (int32 [B]) picks each sequence's row of a state pool, as in gdr_recurrent.
+    Returns out (or None)."""
+    dev = _need_gpu(q, k, v, g, beta, state, state_out, n_keep, out, cu_seqlens, state_idx)
     for t, n in ((k, "k"), (v, "v")) + (((q, "q"),) if q is not None else ()):
         _bf16(t, n)
         if not t.is_contiguous():
@@ -660,13 +769,20 @@ def gdr_chunk(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, g: to
         _f32(t, n)
         if not t.is_contiguous():
             raise ValueError(f"{n} must be contiguous")
-    B, T, Hk, Dk = k.shape
-    Hv, Dv = v.shape[2], v.shape[3]
-    if (q is not None and q.shape != k.shape) or v.shape[:2] != (B, T) or g.shape != (B, T, Hv) \
+    Hk, Dk = k.shape[-2:]
+    Hv, Dv = v.shape[-2:]
+    if cu_seqlens is not None:
+        B, T = _packed(cu_seqlens, max_rows)
+        if k.dim() != 3:
+            raise ValueError("a packed batch takes k [total, Hk, Dk], v [total, Hv, Dv], g, beta [total, Hv]")
+        lead = (k.shape[0],)
+    else:
+        B, T = k.shape[:2]
+        lead = (B, T)
+    if (q is not None and q.shape != k.shape) or v.shape[:-2] != lead or g.shape != lead + (Hv,) \
             or beta.shape != g.shape:
         raise ValueError("q/k/v/g/beta shapes disagree")
-    if state.shape != (B, Hv, Dv, Dk):
-        raise ValueError(f"state must be [B, Hv, Dv, Dk] = {(B, Hv, Dv, Dk)}")
+    _state_pool(state, B, Hv, Dv, Dk, state_idx)
     if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
                                   or not state_out.is_contiguous()):
         raise ValueError("state_out must match state")
@@ -679,9 +795,9 @@ def gdr_chunk(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, g: to
         if q is None:
             raise ValueError("q is required for the readout")
         if out is None:
-            out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
-        elif out.shape != (B, T, Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
-            raise ValueError("gdr_chunk: out must be contiguous bf16 [B, T, Hv, Dv]")
+            out = torch.empty(lead + (Hv, Dv), dtype=torch.bfloat16, device=dev)
+        elif out.shape != lead + (Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+            raise ValueError("gdr_chunk: out must be contiguous bf16 like v")
     else:
         out = None
     nc = T if num_clean is None else int(num_clean)
@@ -692,7 +808,7 @@ def gdr_chunk(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, g: to
     rc = lib.trida_gdr_chunk(
         _ptr(q), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), state.data_ptr(), _ptr(out),
         _ptr(state_out), _ptr(n_keep), seq_mod, B, T, Hk, Hv, Dk, Dv, causal_mode, nc, sc, _ptr(ws),
-        ws.numel() if ws is not None else 0, _stream(dev))
+        ws.numel() if ws is not None else 0, _ptr(cu_seqlens), _ptr(state_idx), _stream(dev))
     _lib.check(rc, "trida_gdr_chunk")
     return out
 
@@ -723,14 +839,16 @@ def gdn_restore(n_keep: torch.Tensor, *, snap_state: Optional[torch.Tensor] = No
                 v: Optional[torch.Tensor] = None, g: Optional[torch.Tensor] = None,
                 beta: Optional[torch.Tensor] = None, snap_window: Optional[torch.Tensor] = None,
                 window: Optional[torch.Tensor] = None, preconv: Optional[torch.Tensor] = None,
-                skip_full: bool = False) -> None:
+                skip_full: bool = False, win_idx: Optional[torch.Tensor] = None,
+                pre_idx: Optional[torch.Tensor] = None, slots: Optional[int] = None) -> None:
     """Rolls GDN state and/or conv windows back to the accepted prefix n_keep (one launch each).
 
     The leading dims of every buffer are NB slots (layers stacked on sequences: slot b uses
     n_keep[b % len(n_keep)]). state [NB,Hv,Dv,Dk] fp32, k [NB,T,Hk,Dk], v [NB,T,Hv,Dv] bf16,
     g, beta [NB,T,Hv] fp32, windows [NB,Kc-1,C] bf16, preconv [NB,T,C] bf16 (last dim contiguous).
-    Outputs may alias the snapshots."""
-    dev = _need_gpu(n_keep, snap_state, state, k, v, g, beta, snap_window, window, preconv)
+    Outputs may alias the snapshots. Pool form of the window part: win_idx int32 [NB] picks each slot's
+    row of the window pools ([rows, Kc-1, C]), pre_idx int32 [NB] its preconv slot; `slots` is NB then."""
+    dev = _need_gpu(n_keep, snap_state, state, k, v, g, beta, snap_window, window, preconv, win_idx, pre_idx)
     if n_keep.dtype != torch.int32 or n_keep.dim() != 1 or not n_keep.is_contiguous():
         raise ValueError("n_keep must be int32 [B]")
     seq_mod = n_keep.shape[0]
@@ -754,12 +872,19 @@ def gdn_restore(n_keep: torch.Tensor, *, snap_state: Optional[torch.Tensor] = No
         _bf16(preconv, "preconv")
         NBw, Km1, C = window.shape
         Kc = Km1 + 1
+        if win_idx is not None or pre_idx is not None:
+            if slots is None:
+                raise ValueError("restore: the pool form (win_idx / pre_idx) needs slots = NB")
+            NBw = int(slots)
+            _i32(win_idx, "win_idx", NBw)
+            _i32(pre_idx, "pre_idx", NBw)
         if NB and NBw != NB:
             raise ValueError("restore: window slots differ from state slots")
         NB = NBw
         T = preconv.shape[1] if not T else T
-        if snap_window.shape != window.shape or preconv.shape[0] != NB or preconv.shape[2] != C \
-                or preconv.shape[1] != T or preconv.stride(2) != 1:
+        if snap_window.shape[1:] != window.shape[1:] or (win_idx is None and snap_window.shape != window.shape) \
+                or (win_idx is None and window.shape[0] != NB) or (pre_idx is None and preconv.shape[0] != NB) \
+                or preconv.shape[2] != C or preconv.shape[1] != T or preconv.stride(2) != 1:
             raise ValueError("restore: window / preconv shapes disagree")
         x_sb, x_st = preconv.stride(0), preconv.stride(1)
     if NB == 0 or NB % seq_mod:
@@ -767,7 +892,7 @@ def gdn_restore(n_keep: torch.Tensor, *, snap_state: Optional[torch.Tensor] = No
     rc = _lib.load().trida_gdn_restore(
         _ptr(snap_state), _ptr(state), _ptr(k), _ptr(v), _ptr(g), _ptr(beta), _ptr(snap_window), _ptr(window),
         _ptr(preconv), n_keep.data_ptr(), NB, seq_mod, T, Hk, Hv, Dk, Dv, C, Kc, x_sb, x_st, int(skip_full),
-        _stream(dev))
+        _ptr(win_idx), _ptr(pre_idx), _stream(dev))
     _lib.check(rc, "trida_gdn_restore")
 
 
