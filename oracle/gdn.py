@@ -177,19 +177,15 @@ def restore(snap_state, snap_window, k, v, g, beta, preconv, n_keep):
     n_keep[b] rows from the block-entry snapshot, and the conv window = last K-1 rows of
     (snapshot window ++ preconv[:n_keep]). q is not needed (no readout)."""
     B = k.shape[0]
-    states, windows = [], []
     Km1 = snap_window.shape[1]
-    for b in range(B):
-        a = int(n_keep[b])
-        if a == 0:
-            s = snap_state[b: b + 1].float().clone()
-        else:
-            _, s, _ = recurrent(k[b: b + 1, :a], k[b: b + 1, :a], v[b: b + 1, :a], g[b: b + 1, :a],
-                                beta[b: b + 1, :a], snap_state[b: b + 1])
-        states.append(s)
-        full = torch.cat([snap_window[b].float(), preconv[b, :a].float()], dim=0)
-        windows.append(full[-Km1:])
-    return torch.cat(states), torch.stack(windows)
+    keep = [int(n) for n in n_keep]
+    states = snap_state.float().clone()
+    for a in sorted(set(keep) - {0}):  # the sequences that keep a rows advance together
+        idx = torch.tensor([b for b in range(B) if keep[b] == a])
+        _, s, _ = recurrent(k[idx, :a], k[idx, :a], v[idx, :a], g[idx, :a], beta[idx, :a], snap_state[idx])
+        states[idx] = s
+    windows = [torch.cat([snap_window[b].float(), preconv[b, :keep[b]].float()], dim=0)[-Km1:] for b in range(B)]
+    return states, torch.stack(windows)
 
 
 def block_bidirectional(q, k, v, g, beta, state: Optional[torch.Tensor], block_size: int,

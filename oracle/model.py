@@ -63,6 +63,10 @@ class CpuCache:
 
 
 class CpuHybrid:
+    # causal (persisting) GDN layers run the chunked WY form (oracle.gdn.chunked, pinned equal to the
+    # token recurrence) instead of the token loop: the same states, faster over hundreds of rows
+    gdn_chunked_causal = False
+
     def __init__(self, cfg, weights: Dict[str, torch.Tensor]):
         self.cfg = cfg
         self.w = {k: v.detach().to("cpu", torch.float32) for k, v in weights.items()}
@@ -102,55 +106,97 @@ class CpuHybrid:
         return bf(bf(o).reshape(T, -1) @ w[p + "w_o"].t()), (k, v)
 
     def _gdn(self, i, x, cache: CpuCache, gdn_mode: int, n_clean: int, persist: bool):
+        proj = self.gdn_proj(i, x)
+        y, rec = self.gdn_core(i, proj, cache, gdn_mode, n_clean, persist)
+        return self.gdn_out(i, y, proj), rec
+
+    def gdn_proj(self, i, x):
+        """The GDN layer's in-projection of the normed rows x [T, hidden]: [T, C + VD + 2 Hv] rows stacking
+        the pre-conv q|k|v, z, b and a (bf16-valued)."""
+        return bf(x @ self.w[f"l{i}.w_in"].t())
+
+    def gdn_core(self, i, proj, cache: CpuCache, gdn_mode: int, n_clean: int, persist: bool):
+        """Conv + gates + the gated delta rule of GDN layer i on its projection rows: the readout y
+        [T, Hv, Dv] (bf16-valued) and, unless persisted, the rows a commit needs."""
         c, w = self.cfg, self.w
         p = f"l{i}."
-        T = x.shape[0]
         C, VD, Hv = c.conv_dim, c.value_dim, c.lin_v_heads
-        proj = bf(x @ w[p + "w_in"].t())
         xpre = proj[None, :, :C]
-        z = proj[:, C: C + VD]
         b_in = proj[None, :, C + VD: C + VD + Hv]
         a_in = proj[None, :, C + VD + Hv: C + VD + 2 * Hv]
         q, k, v, g, beta, new_win = OG.prep(xpre, cache.window[i], w[p + "conv_w"], a_in, b_in, w[p + "A_log"],
                                             w[p + "dt_bias"], c.lin_k_heads, Hv, c.lin_k_dim, c.lin_v_dim)
         if persist:
-            o, s_end, _ = OG.recurrent(q, k, v, g, beta, cache.state[i])
+            if self.gdn_chunked_causal:
+                o, s_end = OG.chunked(q, k, v, g, beta, cache.state[i])
+            else:
+                o, s_end, _ = OG.recurrent(q, k, v, g, beta, cache.state[i])
             cache.state[i] = s_end
             cache.window[i] = new_win
             rec = None
         else:
             o, _, _ = OG.canvas(q, k, v, g, beta, cache.state[i], n_clean, causal_mode=gdn_mode)
             rec = (k, v, g, beta, xpre)
-        y = bf(o)[0]                                                   # [T, Hv, Dv]
+        return bf(o)[0], rec
+
+    def gdn_out(self, i, y, proj):
+        """Gated RMSNorm of the readout y [T, Hv, Dv] by z (from the projection rows) and the
+        out-projection: the layer's residual branch [T, hidden]."""
+        c, w = self.cfg, self.w
+        p = f"l{i}."
+        T = y.shape[0]
+        z = proj[:, c.conv_dim: c.conv_dim + c.value_dim]
         yn = bf(y * torch.rsqrt((y * y).mean(-1, keepdim=True) + c.rms_eps))
-        yn = bf(yn * w[p + "gnorm"] * F.silu(z.reshape(T, Hv, c.lin_v_dim)))
-        return bf(yn.reshape(T, -1) @ w[p + "w_out"].t()), rec
+        yn = bf(yn * w[p + "gnorm"] * F.silu(z.reshape(T, c.lin_v_heads, c.lin_v_dim)))
+        return bf(yn.reshape(T, -1) @ w[p + "w_out"].t())
+
+    _MODES = {"causal": (0, 1), "verify": (0, 1), "canvas": (2, 2), "draft": (1, 2)}
+
+    def layer(self, i: int, h: torch.Tensor, cache: CpuCache, mode: str, n_clean: int):
+        """Decoder layer i ([tf]:420-760) on the hidden rows h [T, hidden] of a block on top of `cache`:
+        h + mixer(rmsnorm(h)), then + mlp(rmsnorm(.)). The mixer's mask / readout follow `mode` as in
+        forward (n_clean: the canvas's clean rows; draft passes use 1). A causal layer persists its KV /
+        GDN state into the cache; the others return the rows a commit needs. Returns (h', rec)."""
+        c, w = self.cfg, self.w
+        p = f"l{i}."
+        att_mode, gdn_mode = self._MODES[mode]
+        persist = mode == "causal"
+        x = rmsnorm(h, w[p + "in_norm"], c.rms_eps)
+        if c.is_attention(i):
+            r, rec = self._attention(i, x, cache, att_mode, n_clean, persist)
+        else:
+            r, rec = self._gdn(i, x, cache, gdn_mode, n_clean, persist)
+        return self.mlp(i, bf(h + r)), rec
+
+    def mlp(self, i: int, h: torch.Tensor) -> torch.Tensor:
+        """The second half of layer i: h + SwiGLU MLP(rmsnorm(h))."""
+        return bf(h + self.mlp_branch(i, h))
+
+    def mlp_branch(self, i: int, h: torch.Tensor) -> torch.Tensor:
+        """SwiGLU MLP(rmsnorm(h)) of layer i: the branch added to h (bf16-valued)."""
+        c, w = self.cfg, self.w
+        p = f"l{i}."
+        x = rmsnorm(h, w[p + "post_norm"], c.rms_eps)
+        gu = bf(x @ w[p + "w_gu"].t())
+        I = c.intermediate
+        act = bf(F.silu(gu[:, :I]) * gu[:, I:])
+        return bf(act @ w[p + "w_down"].t())
+
+    def head(self, h: torch.Tensor) -> torch.Tensor:
+        """Final RMSNorm and the (tied) LM head: bf16-valued fp32 logits [T, V]."""
+        x = rmsnorm(h, self.w["final_norm"], self.cfg.rms_eps)
+        return bf(x @ self.w.get("lm_head", self.w["embed"]).t())
 
     def forward(self, tokens: List[int], cache: CpuCache, mode: str, n_clean: int = 0) -> torch.Tensor:
         """mode: causal (persist), verify, canvas (n_clean) or draft. Returns bf16-valued fp32 logits [T, V]."""
-        c, w = self.cfg, self.w
         persist = mode == "causal"
         T = len(tokens)
-        att_mode, gdn_mode, nc = {"causal": (0, 1, T), "verify": (0, 1, T), "canvas": (2, 2, n_clean),
-                                  "draft": (1, 2, 1)}[mode]
-        h = w["embed"][torch.as_tensor(tokens)]
+        nc = {"causal": T, "verify": T, "canvas": n_clean, "draft": 1}[mode]
+        h = self.w["embed"][torch.as_tensor(tokens)]
         recs = {}
-        for i in range(c.n_layers):
-            p = f"l{i}."
-            x = rmsnorm(h, w[p + "in_norm"], c.rms_eps)
-            if c.is_attention(i):
-                r, rec = self._attention(i, x, cache, att_mode, nc, persist)
-            else:
-                r, rec = self._gdn(i, x, cache, gdn_mode, nc, persist)
-            recs[i] = rec
-            h = bf(h + r)
-            x = rmsnorm(h, w[p + "post_norm"], c.rms_eps)
-            gu = bf(x @ w[p + "w_gu"].t())
-            I = c.intermediate
-            act = bf(F.silu(gu[:, :I]) * gu[:, I:])
-            h = bf(h + bf(act @ w[p + "w_down"].t()))
-        x = rmsnorm(h, w["final_norm"], c.rms_eps)
-        logits = bf(x @ w.get("lm_head", w["embed"]).t())
+        for i in range(self.cfg.n_layers):
+            h, recs[i] = self.layer(i, h, cache, mode, nc)
+        logits = self.head(h)
         if persist:
             cache.tokens.extend(tokens)
         else:

@@ -381,6 +381,15 @@ class TridaRuntime:
     # recurrence block would redo its head's q/k front half (16x at batch 1), which measures slower
     # than the separate prep launch (27 vs 23 us per layer at batch 1, 407 vs 236 us at batch 64).
     fused_gdn = False
+    # fn(i, where, *tensors) or None, for tests that check each layer on its own inputs (never set while a
+    # forward is captured into a graph); called in eager forwards with device tensors:
+    #   (i, "in", h, r)     the hidden rows [B * T, hidden] (bf16) entering layer i (i = n_layers: the
+    #                       final norm) and the previous layer's MLP branch r [B * T, hidden] that h
+    #                       received last (None before layer 0)
+    #   (i, "gdn", proj, y) a GDN layer's in-projection rows [B, T, C + VD + 2 Hv] and its delta-rule
+    #                       readout [B, T, Hv, Dv]
+    #   (i, "mid", h, r)    the hidden rows once the mixer's branch r is added (the MLP's input)
+    layer_probe = None
 
     # canvas blocks of at least this many (sequence, value head) pairs take the single-block MFMA readout
     # under "auto" (batch 64 x 16 heads: 30 vs 132-155 us per layer); smaller grids keep the token-recurrent
@@ -458,6 +467,14 @@ class TridaRuntime:
             else:
                 K.add_rmsnorm(s.h, None if pending is None else pending[1], w, s.x, eps=eps)
 
+    def _branch(self, s: "_Scratch", pending) -> Optional[torch.Tensor]:
+        """The residual branch `pending` as the bf16 rows [N, hidden] it adds to h (for the layer probe)."""
+        if pending is None:
+            return None
+        if pending[0] == "bf16":
+            return pending[1]
+        return s.parts[: pending[1] * s.N * self.cfg.hidden].view(pending[1], s.N, -1).sum(0).to(torch.bfloat16)
+
     def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
                 rows: Optional[int] = None, seq: Optional[slice] = None, row0: int = 0,
                 logits_out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -494,10 +511,15 @@ class TridaRuntime:
             with K.timed("residual"):
                 K.residual_parts(s.h, None, 0, s.ss, h_frag=s.hf)
         pending = None  # the residual branch not yet added to h
+        probe = self.layer_probe
+        added = None    # the branch h received last (reported to the probe)
         for i in range(c.n_layers):
             p = f"l{i}."
             if not fused:
                 self._add_norm(s, pending, w[p + "in_norm"])
+                added = pending
+            if probe is not None:  # h is complete here: layer i's input
+                probe(i, "in", s.h, self._branch(s, added))
             j = self._slot[i]
             if c.is_attention(i):
                 self._proj_normed(s, p + "w_qkv", s.qkv_p, fused)
@@ -553,6 +575,8 @@ class TridaRuntime:
                                             state_out=state[j] if persist else None, out=s.y)
                 if persist:
                     window[j].copy_(s.win_tmp)
+                if probe is not None:
+                    probe(i, "gdn", s.proj, s.y)
                 z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
                 if fused:  # straight into the out projection's fragment-order X
                     K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.ynf,
@@ -563,16 +587,22 @@ class TridaRuntime:
                     pending = self._proj(s, p + "w_out", s.yn_p[:N], s.yn_p, s.r_p)
             if fused:
                 self._residual(s, pending)
+                if probe is not None:  # the mixer's branch is in h
+                    probe(i, "mid", s.h, self._branch(s, pending))
                 self._proj_normed(s, p + "w_gu", s.act_p, fused)
             else:
                 self._add_norm(s, pending, w[p + "post_norm"])
+                if probe is not None:
+                    probe(i, "mid", s.h, self._branch(s, pending))
                 if self._proj(s, p + "w_gu", s.x, s.x_p, s.act_p if self._ws_silu(s, p) else s.gu_p) is not None:
                     K.silu_mul(s.gu, s.act)
             pending = self._proj(s, p + "w_down", s.act, s.act_p, s.r_p, xf=s.actf if fused else None)
             if fused:
                 self._residual(s, pending)
-                pending = None
+                added, pending = pending, None
         self._add_norm(s, pending, w["final_norm"])
+        if probe is not None:
+            probe(c.n_layers, "in", s.h, self._branch(s, added if fused else pending))
         x = s.x.view(B, T, -1)
         if rows is not None or row0:
             x = x[:, row0: row0 + (rows if rows is not None else T - row0)]
