@@ -488,6 +488,44 @@ def bench_e2e(args, rt=None):
     }
 
 
+def bench_generate(rt, n_tokens: int) -> dict:
+    """The batch-1 run as the configuration states it: a fresh 2048-token prompt, then draft-then-verify steps
+    (4 denoising passes + verify + greedy acceptance + rollback, one HIP-graph replay each, one host read of
+    the accepted length per step) until n_tokens are generated; the whole generation is timed, so the
+    context grows from 2048 to about 2048 + n_tokens inside the timed region."""
+    import torch
+
+    from trida_stack_amd.decode import BlockSpecStep
+
+    g = torch.Generator().manual_seed(1)
+    prompt = torch.randint(0, rt.cfg.vocab - 1024, (PROMPT_LEN,), generator=g).tolist()
+    cache = rt.make_cache(1, max_len=PROMPT_LEN + n_tokens + 2 * (BLOCK + 1) + 64)
+    logits = rt.prefill(cache, prompt)
+    step = BlockSpecStep(rt, cache, BLOCK, DENOISE)
+    step.t0.fill_(int(logits.argmax()))
+    # one eager step builds the workspaces, then the graph is captured (the decode loop's order); the
+    # timed generation starts from the cache that step left
+    step.run()
+    cache.ctx_hint += int(step.n_acc[0]) - BLOCK
+    step.capture()
+    torch.cuda.synchronize()
+    ctx0 = int(cache.length[0])
+    made, steps = 0, 0
+    t = time.perf_counter()
+    while made < n_tokens:
+        step.replay()
+        n = int(step.n_acc[0])
+        cache.ctx_hint += n - BLOCK
+        made += 1 + n
+        steps += 1
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t
+    return {"value": round(made / elapsed, 2), "unit": "accepted tok/s", "generated_tokens": made, "steps": steps,
+            "ms_per_step": round(elapsed * 1e3 / steps, 3), "context": [ctx0, int(cache.length[0])],
+            "how": f"{n_tokens} tokens generated after a 2048-token prompt, every step timed (HIP-graph replay, one "
+                   "host read per step)"}
+
+
 def _forward_event_us(rt, cache, step, args, reps: int = 5) -> float:
     """Average duration of one verify forward replayed from its own HIP graph (HIP events on the
     capture stream around the replays), on the live cache: the decoder forward with no launch gaps.
@@ -779,6 +817,8 @@ def bench_default(args):
     keep = ("value", "unit", "steps", "warmup", "ms_per_step", "verify_step_us", "verify_step_how", "roofline",
             "cpu_baseline", "speedup_vs_cpu", "config", "prefill_s", "kernel_avg_us")
     res["bs64"] = {k: r64[k] for k in keep}
+    if args.gen_tokens > 0:
+        res[f"gen{args.gen_tokens}"] = bench_generate(rt, args.gen_tokens)
     if args.canvas_steps > 0:
         for n in (4, 8):
             res[f"canvas_n{n}"] = bench_canvas(args, rt, n)
@@ -1007,6 +1047,7 @@ def main():
     ap.add_argument("--bs64-steps", type=int, default=6, help="default workload: timed batch-64 steps")
     ap.add_argument("--bs64-warmup", type=int, default=2)
     ap.add_argument("--canvas-steps", type=int, default=32, help="default workload: timed canvas-algorithm steps")
+    ap.add_argument("--gen-tokens", type=int, default=256, help="default workload: tokens of the timed generation")
     ap.add_argument("--fwd-batch", type=int, default=1, help="fwd workload: sequences per forward")
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--cpu-steps", type=int, default=3, help="timed CPU-oracle steps (median; after one warm-up)")

@@ -491,6 +491,25 @@ int trida_residual_parts(uint16_t* h, int64_t h_row_stride, const float* parts, 
  * (out_row_stride unused). The results are bitwise those of the row-major forms. */
 #define TRIDA_WS_X_FRAG 1
 #define TRIDA_WS_OUT_FRAG 2
+/* Greedy verify fused into the LM head: the LM-head GEMM of a greedy verify block (M = B * R <= 48 rows of
+ * normed hidden states, W the [V, K] embedding / head shuffled by trida_wsgemm_shuffle) with an argmax
+ * epilogue. Replaces lm_head + argmax of the greedy branch of _selfspec_step
+ * (inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:906-914) and of selfspec_generate's
+ * verify (inference/zoro-1/mlx/trida_mlx/decode.py:323-332): each workgroup reduces every row of the bf16
+ * logits of its columns to (max, first index; NaN above every number) while the weights stream, and
+ * writes pval / pidx [M][S] (fp32 / int32, S = trida_wsgemm_argmax_splits(V, K) column splits in column
+ * order); the logits are not written unless `logits` is given (bf16 [M, V], row stride out_row_stride,
+ * bitwise the store epilogue's). trida_greedy_accept_splits then runs the acceptance of
+ * trida_greedy_accept (argmax_out, n_acc, bonus, crop; same arguments and results) from those pairs
+ * (pval / pidx laid out [B, R, S]), so the verify step never reads the logits back: a 33 x 248320 head
+ * leaves 33 x 255 pairs (67 KB) instead of 16.4 MB of logits. flags: TRIDA_WS_X_FRAG. 1 <= S <= 2048. */
+int64_t trida_wsgemm_argmax_splits(int64_t N, int64_t K);
+int trida_wsgemm_argmax(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M, int64_t N, int64_t K,
+                        int flags, uint16_t* logits, int64_t out_row_stride, float* pval, int32_t* pidx, void* stream);
+int trida_greedy_accept_splits(const float* pval, const int32_t* pidx, int64_t B, int64_t R, int64_t S,
+                               const int64_t* drafts, int64_t K, int64_t draft_stride, const int32_t* n_live,
+                               const int64_t* ctx_len, int64_t* argmax_out, int32_t* n_acc, int64_t* bonus,
+                               int64_t* crop, void* stream);
 int64_t trida_ws_frag_elems(int64_t K);
 int trida_ws_frag(const uint16_t* X, int64_t x_row_stride, int64_t M, int64_t K, uint16_t* Xf, void* stream);
 int trida_wsgemm_ex(const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp, int64_t M,

@@ -37,11 +37,7 @@ constexpr int kThreads = 256;
 constexpr int kStage = 2048;  // split results staged per pass by finalize (a pass holds whole rows)
 
 // (a, ia) ranks above (b, ib): NaN above everything, then larger value, then smaller index.
-__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
-  const bool na = a != a, nb = b != b;
-  if (na | nb) return na && (!nb || ia < ib);
-  return (a > b) || (a == b && ia < ib);
-}
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) { return argmax_better(a, ia, b, ib); }
 
 __device__ __forceinline__ void wave_argbest(float& v, int& i) {
 #pragma unroll
@@ -300,6 +296,8 @@ struct FinalArgs {
   int64_t* crop;
 };
 
+__device__ void accept_scan(const FinalArgs& a, int b, const int* s_am, const long long* s_dr, int lane);
+
 __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalArgs a) {
   const int b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -347,8 +345,43 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalArgs a) {
     __syncthreads();
   }
 
-  // wave 0: prefix scan of draft matches (ballot; accepted = count of leading ones)
-  if (wave == 0) {
+  if (wave == 0) accept_scan(a, b, s_am, s_dr, lane);
+}
+
+// Many splits per row (the LM head's argmax epilogue leaves one per workgroup, ~255): one wave per row,
+// its lanes striding over the row's splits with coalesced loads, then a wave reduction; the same scan.
+__global__ __launch_bounds__(kThreads) void wide_finalize_kernel(FinalArgs a) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  __shared__ int s_am[1024];
+  __shared__ long long s_dr[1024];
+  for (int k0 = tid; k0 < a.K; k0 += kThreads) s_dr[k0] = a.drafts[(int64_t)b * a.draft_stride + k0];
+  for (int r = wave; r < a.R; r += kThreads / kWave) {
+    const int64_t base = ((int64_t)b * a.R + r) * a.S;
+    float v = -INFINITY;
+    int i = INT_MAX;
+    for (int s = lane; s < a.S; s += kWave) {  // a lane's splits come in column order
+      const float pv = a.pval[base + s];
+      const int pi = a.pidx[base + s];
+      if (better(pv, pi, v, i)) {
+        v = pv;
+        i = pi;
+      }
+    }
+    wave_argbest(v, i);
+    if (lane == 0) {
+      if (i == INT_MAX) i = 0;  // a row that is all -inf keeps index 0, as torch.argmax does
+      s_am[r] = i;
+      if (a.argmax_out) a.argmax_out[(int64_t)b * a.R + r] = i;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) accept_scan(a, b, s_am, s_dr, lane);
+}
+
+// wave 0 of a finalize block: prefix scan of draft matches (ballot; accepted = count of leading ones)
+__device__ void accept_scan(const FinalArgs& a, int b, const int* s_am, const long long* s_dr, int lane) {
+  {
     const int live = a.n_live ? min(max(a.n_live[b], 0), a.K) : a.K;
     int n_acc = 0;
     bool open = true;
@@ -575,6 +608,25 @@ extern "C" int trida_greedy_accept(const void* logits, int dtype, int64_t B, int
                argmax_out, n_acc, bonus, crop};
   hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)B), dim3(kThreads), 0, st, fa);
   return launch_status("greedy_accept/finalize");
+}
+
+extern "C" int trida_greedy_accept_splits(const float* pval, const int32_t* pidx, int64_t B, int64_t R, int64_t S,
+                                          const int64_t* drafts, int64_t K, int64_t draft_stride,
+                                          const int32_t* n_live, const int64_t* ctx_len, int64_t* argmax_out,
+                                          int32_t* n_acc, int64_t* bonus, int64_t* crop, void* stream) {
+  TRIDA_CHECK(pval && pidx && n_acc && bonus && crop, TRIDA_ERR_NULL,
+              "greedy_accept_splits: pval, pidx, n_acc, bonus and crop are required");
+  TRIDA_CHECK(B > 0 && R > 0 && K >= 0 && S >= 1 && S <= kStage, TRIDA_ERR_ARG,
+              "greedy_accept_splits: bad sizes B=%lld R=%lld S=%lld (1 <= S <= %d) K=%lld", (long long)B, (long long)R,
+              (long long)S, kStage, (long long)K);
+  TRIDA_CHECK(R >= K + 1, TRIDA_ERR_ARG, "greedy_accept_splits: need R >= K + 1 (R=%lld K=%lld)", (long long)R,
+              (long long)K);
+  TRIDA_CHECK(R <= 1024 && B <= 65535, TRIDA_ERR_ARG, "greedy_accept_splits: R <= 1024 and B <= 65535 supported");
+  TRIDA_CHECK(K == 0 || drafts, TRIDA_ERR_NULL, "greedy_accept_splits: drafts is NULL with K > 0");
+  FinalArgs fa{pval, reinterpret_cast<const int*>(pidx), (int)R, (int)S, drafts, draft_stride, (int)K, n_live, ctx_len,
+               argmax_out, n_acc, bonus, crop};
+  hipLaunchKernelGGL(wide_finalize_kernel, dim3((unsigned)B), dim3(kThreads), 0, static_cast<hipStream_t>(stream), fa);
+  return launch_status("greedy_accept_splits");
 }
 
 namespace {

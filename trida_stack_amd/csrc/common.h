@@ -76,6 +76,14 @@ __host__ __device__ inline int64_t ws_frag_off(int m, int64_t k) {
   return (((k / 32) * kWsFragMT + m / 16) * 64 + ((k % 32) / 8) * 16 + m % 16) * 8 + k % 8;
 }
 
+// Argmax order of (value, index) pairs: NaN above every number (the first NaN wins), then the larger
+// value, then the smaller index -- torch.argmax's first-index result, NaN included.
+__device__ __forceinline__ bool argmax_better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na | nb) return na && (!nb || ia < ib);
+  return (a > b) || (a == b && ia < ib);
+}
+
 // ---------------------------------------------------------------- host error plumbing
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);

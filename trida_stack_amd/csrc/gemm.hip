@@ -21,8 +21,10 @@
 //     (trida_residual_parts_frag, trida_gated_rmsnorm_frag, this kernel's own epilogues) write that order;
 //   - K beyond NW * KWS steps is split over kg workgroup groups that write fp32 partial planes
 //     [kg][M][N]; trida_add_rmsnorm_parts (norms.hip) sums them in plane order.
-// Epilogues: bf16 store, fp32 partials, or SwiGLU (silu(gate) * up) over weights whose tiles interleave 8
-// gate rows with the matching 8 up rows. The plan (NW, KWS, T, kg) depends on N, K and the epilogue only:
+// Epilogues: bf16 store, fp32 partials, SwiGLU (silu(gate) * up) over weights whose tiles interleave 8
+// gate rows with the matching 8 up rows, or argmax: the LM head of a greedy verify reduces each row of its
+// bf16 logits to the workgroup's (max, first index) in registers while the weights stream, and writes one
+// pair per row and workgroup (optionally the logits too), so acceptance never reads the logits again. The plan (NW, KWS, T, kg) depends on N, K and the epilogue only:
 // a row of Y is bitwise the same whether X holds 1 row or 48.
 #include <algorithm>
 
@@ -34,7 +36,7 @@ namespace {
 constexpr int kCUs = 256;  // MI355X (gfx950): workgroups of a plan <= one per CU, see plan_for()
 constexpr int kMaxM = 48;
 
-enum Epilogue { kStore = 0, kParts = 1, kSilu = 2 };
+enum Epilogue { kStore = 0, kParts = 1, kSilu = 2, kArgmax = 3 };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ bf16x8 as_bf(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
@@ -53,6 +55,8 @@ struct WsArgs {
   float eps;
   int xf;  // X in fragment order (x_st unused)
   int of;  // bf16 output (store / SwiGLU epilogues) in fragment order for the next GEMM (o_st unused)
+  float* pval;  // argmax epilogue: [M][gridDim.x] best value of each row within each workgroup's columns
+  int* pidx;    // and its column (first on ties, NaN first)
 };
 
 
@@ -140,6 +144,15 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
     inv_s[threadIdx.x] = rsqrtf(sum / (float)a.K + a.eps);
   }
 
+  // argmax epilogue: this thread's running (value, column) of rows mm * 16 + l % 16, over the columns its
+  // flush items covered (the lanes l, l ^ 16, l ^ 32, l ^ 48 and the waves are merged at the end)
+  float hv[MT];
+  int hi[MT];
+#pragma unroll
+  for (int mm = 0; mm < MT; ++mm) {
+    hv[mm] = -INFINITY;
+    hi[mm] = INT32_MAX;
+  }
   // 4 consecutive bf16 outputs (n % 4 == 0) of row m: row-major, or in fragment order for the next GEMM
   auto out_at = [&](int m, int n) -> u32x2* {
     uint16_t* o = static_cast<uint16_t*>(a.out);
@@ -182,6 +195,34 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
           packed.y = f2bf2(y2, y3);
           *out_at(m, f) = packed;
         }
+      } else if (EPI == kArgmax) {
+        // mt is uniform over a wave (its 64 items are consecutive and a tile's items come in whole waves)
+        const int mt = q / kWave, ln = q % kWave;
+        f32x4 sum = red[slot][0][mt][ln];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) sum += red[slot][w][mt][ln];
+        const int m = mt * 16 + (ln % 16);
+        const int n = tile * 16 + (ln / 16) * 4;
+        if (NORM) sum *= inv_s[m];
+        // the bf16 logits, as the store epilogue writes them; the argmax compares their fp32 widening
+        const uint32_t p0 = f2bf2(sum.x, sum.y), p1 = f2bf2(sum.z, sum.w);
+        if (a.out && m < a.M) *out_at(m, n) = u32x2{p0, p1};
+        const float v[4] = {__uint_as_float(p0 << 16), __uint_as_float(p0 & 0xffff0000u), __uint_as_float(p1 << 16),
+                            __uint_as_float(p1 & 0xffff0000u)};
+        float bv = v[0];
+        int bi = n;
+#pragma unroll
+        for (int e = 1; e < 4; ++e)
+          if (argmax_better(v[e], n + e, bv, bi)) {
+            bv = v[e];
+            bi = n + e;
+          }
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm)
+          if (mm == mt && argmax_better(bv, bi, hv[mm], hi[mm])) {
+            hv[mm] = bv;
+            hi[mm] = bi;
+          }
       } else {
         const int mt = q / kWave, ln = q % kWave;
         f32x4 sum = red[slot][0][mt][ln];
@@ -233,6 +274,41 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
         }
         if (slot == NSLOT - 1 || tl == nt - 1) flush(tl - slot, tl);
       }
+    }
+  }
+  if constexpr (EPI == kArgmax) {
+    // merge the four lanes of each row, then the waves in order; one (value, column) per row
+    __shared__ float s_bv[NW][MT * 16];
+    __shared__ int s_bi[NW][MT * 16];
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+#pragma unroll
+      for (int off = 16; off < kWave; off <<= 1) {
+        const float ov = __shfl_xor(hv[mm], off, kWave);
+        const int oi = __shfl_xor(hi[mm], off, kWave);
+        if (argmax_better(ov, oi, hv[mm], hi[mm])) {
+          hv[mm] = ov;
+          hi[mm] = oi;
+        }
+      }
+      if (l < 16) {
+        s_bv[wave][mm * 16 + l] = hv[mm];
+        s_bi[wave][mm * 16 + l] = hi[mm];
+      }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < a.M) {
+      const int m = threadIdx.x;
+      float v = s_bv[0][m];
+      int i = s_bi[0][m];
+#pragma unroll
+      for (int w = 1; w < NW; ++w)
+        if (argmax_better(s_bv[w][m], s_bi[w][m], v, i)) {
+          v = s_bv[w][m];
+          i = s_bi[w][m];
+        }
+      a.pval[(int64_t)m * gridDim.x + blockIdx.x] = v;
+      a.pidx[(int64_t)m * gridDim.x + blockIdx.x] = i;
     }
   }
 }
@@ -419,9 +495,15 @@ namespace {
 // the weight-streaming GEMM behind every entry point: ss null = no RMSNorm prologue; flags TRIDA_WS_X_FRAG /
 // TRIDA_WS_OUT_FRAG select the fragment order of X / of the bf16 output
 int ws_run(const char* name, const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp,
-           int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride, int flags, void* stream) {
-  TRIDA_CHECK(X && Wp && out, TRIDA_ERR_NULL, "%s: X, Wp and out are required", name);
-  TRIDA_CHECK(epilogue >= kStore && epilogue <= kSilu, TRIDA_ERR_ARG, "%s: unknown epilogue %d", name, epilogue);
+           int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride, int flags, void* stream,
+           float* pval = nullptr, int* pidx = nullptr) {
+  const bool amax = epilogue == kArgmax;  // only through trida_wsgemm_argmax (pval / pidx given)
+  TRIDA_CHECK(X && Wp && (out || amax) && (!amax || (pval && pidx)), TRIDA_ERR_NULL,
+              "%s: X, Wp and out (argmax: pval and pidx) are required", name);
+  TRIDA_CHECK(epilogue >= kStore && epilogue <= (amax ? kArgmax : kSilu), TRIDA_ERR_ARG, "%s: unknown epilogue %d",
+              name, epilogue);
+  TRIDA_CHECK(!amax || (!ss && !(flags & TRIDA_WS_OUT_FRAG)), TRIDA_ERR_ARG,
+              "%s: the argmax epilogue takes no RMSNorm prologue and a row-major output", name);
   TRIDA_CHECK(!ss || epilogue != kParts, TRIDA_ERR_ARG,
               "%s: the RMSNorm prologue takes the bf16 (0) or SwiGLU (2) epilogue", name);
   TRIDA_CHECK((flags & ~(TRIDA_WS_X_FRAG | TRIDA_WS_OUT_FRAG)) == 0 &&
@@ -435,18 +517,22 @@ int ws_run(const char* name, const uint16_t* X, int64_t x_row_stride, const floa
   TRIDA_CHECK(!of || (epilogue == kSilu ? N / 2 : N) % 32 == 0, TRIDA_ERR_ARG,
               "%s: a fragment-order output needs a width that is a multiple of 32", name);
   TRIDA_CHECK(xf || (x_row_stride >= K && x_row_stride % 8 == 0), TRIDA_ERR_ARG, "%s: bad X row stride", name);
-  TRIDA_CHECK(epilogue == kParts || of ||
+  TRIDA_CHECK(epilogue == kParts || of || (amax && !out) ||
                   (out_row_stride >= (epilogue == kSilu ? N / 2 : N) && out_row_stride % 4 == 0),
               TRIDA_ERR_ARG, "%s: bad output row stride", name);
+  TRIDA_CHECK(!amax || (N <= INT32_MAX && ((uintptr_t)pval & 3) == 0 && ((uintptr_t)pidx & 3) == 0), TRIDA_ERR_ARG,
+              "%s: argmax needs N < 2^31 and 4-byte aligned pval / pidx", name);
   TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Wp | (uintptr_t)out) & 15) == 0 && ((uintptr_t)ss & 3) == 0,
               TRIDA_ERR_ALIGN, "%s: X, Wp and out must be 16-byte aligned", name);
   const Plan p = plan_for(N, K, epilogue);
   TRIDA_CHECK(p.cfg >= 0 && (!ss || ss_chunks((int)K) <= kMaxSsChunks), TRIDA_ERR_ARG,
               "%s: K too long for one workgroup (epilogue %d needs kg == 1)", name, epilogue);
   WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T, ss,
-           eps, xf ? 1 : 0, of ? 1 : 0};
+           eps, xf ? 1 : 0, of ? 1 : 0, pval, pidx};
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (ss) {
+  if (amax) {
+    launch_cfg<kArgmax, false>(a, p, st);
+  } else if (ss) {
     if (epilogue == kStore) launch_cfg<kStore, true>(a, p, st);
     else launch_cfg<kSilu, true>(a, p, st);
   } else {
@@ -474,6 +560,19 @@ extern "C" int trida_wsgemm_ex(const uint16_t* X, int64_t x_row_stride, const fl
                                int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride,
                                int flags, void* stream) {
   return ws_run("wsgemm_ex", X, x_row_stride, ss, eps, Wp, M, N, K, epilogue, out, out_row_stride, flags, stream);
+}
+
+extern "C" int64_t trida_wsgemm_argmax_splits(int64_t N, int64_t K) {
+  if (!shape_ok(N, K, kArgmax)) return 0;
+  const Plan p = plan_for(N, K, kArgmax);
+  return p.cfg < 0 ? 0 : cdiv(N / 16, p.T);
+}
+
+extern "C" int trida_wsgemm_argmax(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M, int64_t N,
+                                   int64_t K, int flags, uint16_t* logits, int64_t out_row_stride, float* pval,
+                                   int32_t* pidx, void* stream) {
+  return ws_run("wsgemm_argmax", X, x_row_stride, nullptr, 0.f, Wp, M, N, K, kArgmax, logits, out_row_stride, flags,
+                stream, pval, pidx);
 }
 
 extern "C" int64_t trida_ws_frag_elems(int64_t K) { return K > 0 && K % 32 == 0 ? K / 32 * kWsFragMT * 64 * 8 : 0; }

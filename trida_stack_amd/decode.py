@@ -513,12 +513,19 @@ class CanvasSpecStep:
         rt, cache, n = self.rt, self.cache, self.n
         self.live.copy_(self.verify)
         self.live.mul_(n - 1)  # specs that count: n - 1 on a verify canvas, none on a cold one
-        L = rt.forward(self.canvas, cache, "canvas", n_clean=n)
-        if self.rules is not None:
-            self.rules.apply(L, self.raw_p)
         n_acc, bonus, crop = self.acc
-        with K.timed("greedy_accept"):
-            K.greedy_accept(L, self.canvas[:, 1:n], n_live=self.live, out=(self.am, n_acc, bonus, crop))
+        if self.rules is None and rt.greedy_head_ok(cache.B * (2 * n - 1)):
+            # every canvas row's argmax straight from the LM head's epilogue (no logits written or read)
+            pv, pi = rt.forward(self.canvas, cache, "canvas", n_clean=n, head="argmax")
+            with K.timed("greedy_accept"):
+                K.greedy_accept_splits(pv, pi, self.canvas[:, 1:n], R=2 * n - 1, n_live=self.live,
+                                       out=(self.am, n_acc, bonus, crop))
+        else:
+            L = rt.forward(self.canvas, cache, "canvas", n_clean=n)
+            if self.rules is not None:
+                self.rules.apply(L, self.raw_p)
+            with K.timed("greedy_accept"):
+                K.greedy_accept(L, self.canvas[:, 1:n], n_live=self.live, out=(self.am, n_acc, bonus, crop))
         K.canvas_advance(self.am, n_acc, self.canvas, self.verify,
                          (self.n_keep, self.emit, self.n_emit, self.committed, self.kind), rt.mask_id)
         cache.pending = {"T": 2 * n - 1}
@@ -635,12 +642,20 @@ class BlockSpecStep:
         """The verify pass over the canvas, greedy acceptance and the rollback; t0 = the bonus token."""
         rt, cache, blk = self.rt, self.cache, self.block
         vt = K.timed("verify_step").__enter__()
-        L = rt.forward(self.canvas, cache, "verify")
-        if self.rules is not None:
-            self.rules.apply(L, self.raw_p)
-        self.ctx.copy_(cache.length)
-        with K.timed("greedy_accept"):
-            K.greedy_accept(L, self.canvas[:, 1:], ctx_len=self.ctx, out=(self.am, self.n_acc, self.bonus, self.crop))
+        if self.rules is None and rt.greedy_head_ok(cache.B * (blk + 1)):
+            # the LM head leaves per-split (max, index) pairs, not logits: acceptance reads 67 KB, not 16 MB
+            pv, pi = rt.forward(self.canvas, cache, "verify", head="argmax")
+            self.ctx.copy_(cache.length)
+            with K.timed("greedy_accept"):
+                K.greedy_accept_splits(pv, pi, self.canvas[:, 1:], R=blk + 1, ctx_len=self.ctx,
+                                       out=(self.am, self.n_acc, self.bonus, self.crop))
+        else:
+            L = rt.forward(self.canvas, cache, "verify")
+            if self.rules is not None:
+                self.rules.apply(L, self.raw_p)
+            self.ctx.copy_(cache.length)
+            with K.timed("greedy_accept"):
+                K.greedy_accept(L, self.canvas[:, 1:], ctx_len=self.ctx, out=(self.am, self.n_acc, self.bonus, self.crop))
         torch.add(self.n_acc, 1, out=self.n_keep)
         cache.pending = {"T": blk + 1}
         rt.commit(cache, self.n_keep)

@@ -1012,6 +1012,66 @@ def ws_gemm(x: torch.Tensor, wp: torch.Tensor, N: int, out: torch.Tensor, *, epi
     return out
 
 
+def ws_argmax_splits(N: int, Kd: int) -> int:
+    """Column splits (one per workgroup) of the argmax epilogue of an [N, K] weight-streaming GEMM."""
+    S = int(_lib.load().trida_wsgemm_argmax_splits(N, Kd))
+    if S <= 0:
+        raise ValueError(f"ws_gemm_argmax: shape N={N} K={Kd} not supported")
+    return S
+
+
+def ws_gemm_argmax(x: torch.Tensor, wp: torch.Tensor, N: int, pval: torch.Tensor, pidx: torch.Tensor, *,
+                   logits: Optional[torch.Tensor] = None) -> None:
+    """The LM head of a greedy verify with its argmax fused in (trida_wsgemm_argmax): x [M, K] bf16 (M <= 48,
+    contiguous rows) times the ws_shuffle'd head (N rows); pval fp32 / pidx int32 [M, S] (S =
+    ws_argmax_splits(N, K)) receive each row's (bf16 logit max, first column) within each column split;
+    logits [M, N] bf16, when given, receives the logits as ws_gemm's store epilogue would."""
+    dev = _need_gpu(x, wp, pval, pidx, logits)
+    _bf16(x, "x")
+    M, Kd = x.shape
+    S = ws_argmax_splits(N, Kd)
+    if x.stride(1) != 1 or wp.numel() != N * Kd:
+        raise ValueError("ws_gemm_argmax: x needs contiguous rows and wp N * K elements")
+    if pval.dtype != torch.float32 or pidx.dtype != torch.int32 or not pval.is_contiguous() \
+            or not pidx.is_contiguous() or pval.numel() < M * S or pidx.numel() < M * S:
+        raise ValueError(f"ws_gemm_argmax: pval fp32 / pidx int32 of >= {M} x {S} contiguous elements")
+    o_st = 0
+    if logits is not None:
+        _bf16(logits, "logits")
+        if logits.dim() != 2 or logits.shape[0] < M or logits.shape[1] < N or logits.stride(1) != 1:
+            raise ValueError("ws_gemm_argmax: logits must be [>= M, >= N] bf16 with contiguous rows")
+        o_st = logits.stride(0)
+    rc = _lib.load().trida_wsgemm_argmax(x.data_ptr(), x.stride(0), wp.data_ptr(), M, N, Kd, 0, _ptr(logits), o_st,
+                                         pval.data_ptr(), pidx.data_ptr(), _stream(dev))
+    _lib.check(rc, "trida_wsgemm_argmax")
+
+
+def greedy_accept_splits(pval: torch.Tensor, pidx: torch.Tensor, drafts: torch.Tensor, *, R: int,
+                         n_live: Optional[torch.Tensor] = None, ctx_len: Optional[torch.Tensor] = None,
+                         want_argmax: bool = True, out=None):
+    """greedy_accept from the per-split (max, first index) pairs of ws_gemm_argmax: pval / pidx [B, R, S]
+    (the GEMM's [M = B R, S] rows), drafts [B, K] int64. Same outputs and semantics as greedy_accept."""
+    dev = _need_gpu(pval, pidx, drafts, n_live, ctx_len)
+    B = drafts.shape[0]
+    if pval.dtype != torch.float32 or pidx.dtype != torch.int32 or pval.numel() % (B * R) \
+            or pval.numel() != pidx.numel() or not pval.is_contiguous() or not pidx.is_contiguous():
+        raise ValueError("greedy_accept_splits: pval fp32 / pidx int32 [B, R, S], contiguous")
+    S = pval.numel() // (B * R)
+    if drafts.dtype != torch.int64 or drafts.dim() != 2 or drafts.stride(1) != 1:
+        raise ValueError("drafts must be int64 [B, K] with a contiguous last dim")
+    K = drafts.shape[1]
+    if out is None:
+        am = torch.empty((B, R), dtype=torch.int64, device=dev) if want_argmax else None
+        out = (am, torch.empty(B, dtype=torch.int32, device=dev), torch.empty(B, dtype=torch.int64, device=dev),
+               torch.empty(B, dtype=torch.int64, device=dev))
+    am, n_acc, bonus, crop = out
+    rc = _lib.load().trida_greedy_accept_splits(
+        pval.data_ptr(), pidx.data_ptr(), B, R, S, _ptr(drafts), K, drafts.stride(0), _ptr(n_live), _ptr(ctx_len),
+        _ptr(am), n_acc.data_ptr(), bonus.data_ptr(), crop.data_ptr(), _stream(dev))
+    _lib.check(rc, "trida_greedy_accept_splits")
+    return out
+
+
 def ss_chunks(dim: int) -> int:
     """Columns of the per-row sums of squares residual_parts writes (256-element chunks)."""
     return int(_lib.load().trida_residual_ss_chunks(dim))

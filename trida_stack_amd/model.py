@@ -272,6 +272,7 @@ class TridaRuntime:
         for j, i in enumerate(self.gdn_layers):
             self._slot[i] = j
         self._scratch: Dict[tuple, _Scratch] = {}
+        self._head_bufs: Dict[tuple, tuple] = {}  # argmax-head split buffers per row count
         self.ws: Dict[str, tuple] = {}
         self.ws_parts = 0
         self.ws_fused = False
@@ -475,15 +476,24 @@ class TridaRuntime:
             return pending[1]
         return s.parts[: pending[1] * s.N * self.cfg.hidden].view(pending[1], s.N, -1).sum(0).to(torch.bfloat16)
 
+    # a greedy verify of <= WS_MAX_M rows may run its LM head with the argmax epilogue (no logits written)
+    fused_greedy_head = True
+
+    def greedy_head_ok(self, rows: int) -> bool:
+        """Whether forward(..., head="argmax") applies to a block of `rows` rows."""
+        return self.fused_greedy_head and "lm_head" in self.ws and rows <= K.WS_MAX_M
+
     def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
                 rows: Optional[int] = None, seq: Optional[slice] = None, row0: int = 0,
-                logits_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                logits_out: Optional[torch.Tensor] = None, head: str = "logits"):
         """One forward of a [B, T] block of token ids (device int64) on top of the cache.
         Returns bf16 logits [B, rows, V] of block rows row0 .. row0 + rows - 1 (default: every row; the
         LM head runs on those rows only). seq restricts the forward to a contiguous range of the
         cache's sequences (used by per-sequence prefill of ragged prompts). logits_out: a contiguous fp32
         [B, rows, V] buffer the LM head writes instead (its fp32 accumulators, no bf16 rounding); it is
-        returned."""
+        returned. head="argmax" (greedy_head_ok): the LM head reduces each row of its bf16 logits to one
+        (max, first index) pair per column split instead of writing them; returns (pval, pidx)
+        [B, rows, S] for K.greedy_accept_splits."""
         c, w = self.cfg, self.w
         B, T = ids.shape
         sq = seq if seq is not None else slice(0, cache.B)
@@ -609,7 +619,20 @@ class TridaRuntime:
         with K.timed("lm_head"):
             x2 = x.reshape(-1, x.shape[-1])
             wl = w.get("lm_head", w["embed"])
-            if logits_out is not None:
+            if head == "argmax":
+                if logits_out is not None or not self.greedy_head_ok(x2.shape[0]):
+                    raise ValueError("forward: the argmax head needs the weight-streaming LM head and <= "
+                                     f"{K.WS_MAX_M} rows")
+                wp, V, _, _ = self.ws["lm_head"]
+                key = ("head", x2.shape[0])
+                bufs = self._head_bufs.get(key)
+                if bufs is None:  # fixed addresses per row count (graph capture)
+                    S = K.ws_argmax_splits(V, x2.shape[1])
+                    bufs = self._head_bufs[key] = (torch.empty(x2.shape[0] * S, dtype=torch.float32, device=self.dev),
+                                                   torch.empty(x2.shape[0] * S, dtype=torch.int32, device=self.dev))
+                K.ws_gemm_argmax(x2, wp, V, *bufs)
+                logits = (bufs[0].view(B, x.shape[1], -1), bufs[1].view(B, x.shape[1], -1))
+            elif logits_out is not None:
                 # fp32 logits straight from the GEMM's fp32 accumulators (no bf16 output widened again)
                 if logits_out.dtype != torch.float32 or not logits_out.is_contiguous() \
                         or logits_out.numel() != x2.shape[0] * wl.shape[0]:
