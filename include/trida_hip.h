@@ -123,7 +123,10 @@ int trida_canvas_advance(const int64_t* argmax, int64_t argmax_stride, const int
  * trida_gate_tokens: per row, lse = logsumexp of the row; for gate g, p = exp(x[r, ids[g]] - lse)
  *   (written to raw_p [rows, n_gate] fp32 when not NULL; 0 for an id outside [0, V) or a row with no
  *   finite value), and x[r, ids[g]] = -inf where thr[g] > 0 and p < thr[g]. Every p of a row is taken
- *   before any gate writes. Apply the ban first (the reference's order). n_gate <= 512. */
+ *   before any gate writes. Apply the ban first (the reference's order). n_gate <= 512. thr NULL (raw_p
+ *   given): a note-only pass that writes raw_p and leaves the row unchanged -- the raw probabilities
+ *   _gate_note records (decode.py:63-73) come from the rows before the ban, so a caller that logs them
+ *   runs it before trida_ban_tokens. */
 int trida_ban_tokens(void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, const int64_t* ids,
                      int64_t n_ids, void* stream);
 int trida_gate_tokens(void* logits, int dtype, int64_t rows, int64_t V, int64_t row_stride, const int64_t* ids,

@@ -3,6 +3,8 @@ ROCm / PyTorch build and gfx950, and one entry per projection shape of the batch
 import csv
 import os
 
+import pytest
+
 from trida_stack_amd import model as M
 
 
@@ -27,3 +29,26 @@ def test_gemm_choices_switch(monkeypatch):
     assert M.use_gemm_choices() is False
     monkeypatch.delenv("TRIDA_GEMM_CHOICES")
     assert M.use_gemm_choices(os.path.join(os.path.dirname(M.GEMM_CHOICES), "no_such_file.csv")) is False
+
+
+@pytest.mark.gpu
+def test_runtime_leaves_tunableop_state_alone(gpu, tmp_path):
+    """The runtime turns TunableOp lookup on only around its own library GEMMs: a host's settings (off, or
+    on with tuning) are what they were before the runtime was built and after its GEMMs ran."""
+    import torch
+
+    from trida_stack_amd.model import HybridConfig, TridaRuntime, init_weights
+
+    t = torch.cuda.tunable
+    t.set_filename(str(tmp_path / "tunableop_results.csv"))  # anything TunableOp writes stays out of the tree
+    cfg = HybridConfig.tiny(vocab=512)
+    for state in ((False, False), (True, False), (True, True)):
+        t.enable(state[0])
+        t.tuning_enable(state[1])
+        rt = TridaRuntime(cfg, init_weights(cfg, seed=0), device=gpu)
+        c = rt.make_cache(2, max_len=128)
+        rt.forward(torch.zeros(2, 60, dtype=torch.long, device=gpu), c, "causal")  # library GEMMs
+        torch.cuda.synchronize()
+        assert (t.is_enabled(), t.tuning_is_enabled()) == state
+    t.tuning_enable(False)
+    t.enable(False)

@@ -37,10 +37,14 @@ def test_ban_and_gate_match_oracle(gpu, dtype):
     # make some gated tokens likely so that both outcomes of the gate occur
     x[:, ::2, 17] += 12
     x[:, 1::3, 4000] += 9
+    x[:, 1::2, 3] += 11  # a banned token holding much of the mass: the raw and the banned rows' softmax differ
     banned = (3, 4999, 17000, -2, 3)
     gate = ((17, 0.5), (4000, 0.2), (123, 0.0), (9999, 0.3))
     ref = A.apply_ban(x.float().numpy(), banned, gate)
-    ref_p = A.gate_probs(A.apply_ban(x.float().numpy(), banned), gate)
+    # the notes take the raw row's probabilities (_gate_note, decode.py:63-73, gets the unbanned logits);
+    # the gate decides on the banned row (apply_ban, decode.py:88-98)
+    ref_p = A.gate_probs(x.float().numpy(), gate)
+    assert np.abs(ref_p - A.gate_probs(A.apply_ban(x.float().numpy(), banned), gate)).max() > 0.1
     xd = x.to(DEV)
     rules = LogitRules(SamplingParams(banned=banned, gate=gate, gate_log=[]), DEV)
     raw = rules.raw_buffer(3 * 33, DEV)

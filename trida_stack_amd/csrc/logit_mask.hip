@@ -99,6 +99,7 @@ __global__ __launch_bounds__(kGateThreads) void gate_kernel(T* x, int64_t row_st
     if (id >= 0 && id < V && lse != -INFINITY) p = __expf(load_x(row + id) - lse);
     if (raw_p) raw_p[(int64_t)blockIdx.x * n_gate + threadIdx.x] = p;
   }
+  if (!thr) return;  // a note-only pass: the raw probabilities, nothing written to the row
   __syncthreads();
   if ((int)threadIdx.x < n_gate && id >= 0 && id < V && thr[threadIdx.x] > 0.f && p < thr[threadIdx.x])
     store_ninf(row + id);
@@ -137,7 +138,8 @@ extern "C" int trida_gate_tokens(void* logits, int dtype, int64_t rows, int64_t 
               TRIDA_ERR_ARG, "gate_tokens: bad sizes rows=%lld V=%lld n_gate=%lld (<= %d)", (long long)rows,
               (long long)V, (long long)n_gate, kGateThreads);
   if (rows == 0 || n_gate == 0) return TRIDA_OK;
-  TRIDA_CHECK(logits && ids && thr, TRIDA_ERR_NULL, "gate_tokens: logits, ids and thr are required");
+  TRIDA_CHECK(logits && ids && (thr || raw_p), TRIDA_ERR_NULL,
+              "gate_tokens: logits, ids and thr (or, for a note-only pass, raw_p) are required");
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == 0)
     hipLaunchKernelGGL(gate_kernel<float>, dim3((unsigned)rows), dim3(kGateThreads), 0, st,

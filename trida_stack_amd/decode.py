@@ -79,11 +79,15 @@ class LogitRules:
 
     def apply(self, logits: torch.Tensor, raw_p: Optional[torch.Tensor] = None) -> torch.Tensor:
         """logits [..., V] (fp32 or bf16, evenly strided rows) with the rules applied, in place; raw_p
-        [rows, n_gate] fp32 receives the gated tokens' raw probabilities."""
+        [rows, n_gate] fp32 receives the gated tokens' raw probabilities: under the softmax of the raw row,
+        before the ban, as _gate_note takes them (decode.py:63-73). The gate itself decides on the banned
+        row, as apply_ban does (decode.py:88-98)."""
+        if raw_p is not None and self.gate_ids is not None:
+            K.gate_tokens(logits, self.gate_ids, None, raw_p)  # note-only pass over the raw rows
         if self.ban is not None:
             K.ban_tokens(logits, self.ban)
         if self.gate_ids is not None:
-            K.gate_tokens(logits, self.gate_ids, self.gate_thr, raw_p)
+            K.gate_tokens(logits, self.gate_ids, self.gate_thr)
         return logits
 
     def raw_buffer(self, rows: int, device) -> Optional[torch.Tensor]:

@@ -243,21 +243,24 @@ def ban_tokens(logits: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
     return logits
 
 
-def gate_tokens(logits: torch.Tensor, ids: torch.Tensor, thr: torch.Tensor,
+def gate_tokens(logits: torch.Tensor, ids: torch.Tensor, thr: Optional[torch.Tensor],
                 raw_p: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The gate of apply_ban (decode.py:88-98), in place: per row, token ids[g] is set to -inf where its
     probability under the row's softmax, p = exp(x_id - logsumexp(x)), is below thr[g] > 0. raw_p
-    [rows, n] fp32 (optional) receives every p. ids int64 [n], thr fp32 [n]."""
+    [rows, n] fp32 (optional) receives every p. ids int64 [n], thr fp32 [n]. thr None (with raw_p): a
+    note-only pass that writes the probabilities and leaves the logits as they are."""
     dev = _need_gpu(logits, ids, thr, raw_p)
     dt = _logit_dtype(logits)
-    if ids.dtype != torch.int64 or thr.dtype != torch.float32 or ids.shape != thr.shape or ids.dim() != 1 \
-            or not ids.is_contiguous() or not thr.is_contiguous():
+    if thr is None and raw_p is None:
+        raise ValueError("gate_tokens: thr, or raw_p for a note-only pass, is required")
+    if ids.dtype != torch.int64 or ids.dim() != 1 or not ids.is_contiguous() or (thr is not None and (
+            thr.dtype != torch.float32 or thr.shape != ids.shape or not thr.is_contiguous())):
         raise ValueError("ids (int64 [n]) and thr (fp32 [n]) must be contiguous and of one length")
     rows, V, rs = _rows2d(logits)
     if raw_p is not None and (raw_p.dtype != torch.float32 or raw_p.numel() < rows * ids.numel()
                               or not raw_p.is_contiguous()):
         raise ValueError("raw_p must be a contiguous fp32 tensor of rows * n elements")
-    rc = _lib.load().trida_gate_tokens(logits.data_ptr(), dt, rows, V, rs, ids.data_ptr(), thr.data_ptr(), ids.numel(),
+    rc = _lib.load().trida_gate_tokens(logits.data_ptr(), dt, rows, V, rs, ids.data_ptr(), _ptr(thr), ids.numel(),
                                        _ptr(raw_p), _stream(dev))
     _lib.check(rc, "trida_gate_tokens")
     return logits

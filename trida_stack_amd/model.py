@@ -243,25 +243,49 @@ def use_gemm_choices(path: str = GEMM_CHOICES) -> bool:
     """Library GEMM solutions measured per shape of the batch-64 decode step on MI355X (hipBLASLt or rocBLAS,
     whichever ran fastest; PyTorch TunableOp's results format, lookup only, no tuning at run time). Shapes
     the file does not list keep the library's own heuristic; a file written for another library version
-    or GPU is ignored by TunableOp's validators. TRIDA_GEMM_CHOICES=0 turns it off."""
-    t = torch.cuda.tunable
+    or GPU is ignored by TunableOp's validators. TRIDA_GEMM_CHOICES=0 turns it off.
+
+    Loads the entries into TunableOp's results (process-wide: a host that enables TunableOp for its own
+    matmuls of these exact shapes would find them there) without enabling TunableOp; the runtime turns
+    the lookup on only around its own library GEMMs (_GemmChoices)."""
     if os.environ.get("TRIDA_GEMM_CHOICES", "1") == "0" or not os.path.exists(path):
         return False
-    if not t.is_enabled():
-        t.tuning_enable(False)
-        t.enable(True)
-    return bool(t.read_file(path))
+    return bool(torch.cuda.tunable.read_file(path))
+
+
+class _GemmChoices:
+    """TunableOp lookup (no tuning) around one of the runtime's own library GEMMs, the caller's TunableOp
+    state restored afterwards: a host application that embeds the runtime keeps its own settings."""
+
+    def __init__(self, on: bool):
+        self.on = on
+
+    def __enter__(self):
+        if self.on:
+            t = torch.cuda.tunable
+            self.prev = (t.is_enabled(), t.tuning_is_enabled())
+            t.tuning_enable(False)
+            t.enable(True)
+        return self
+
+    def __exit__(self, *exc):
+        if self.on:
+            t = torch.cuda.tunable
+            t.enable(self.prev[0])
+            t.tuning_enable(self.prev[1])
+        return False
 
 
 class TridaRuntime:
     """The self-spec runtime over one model (see the module docstring for the mode semantics)."""
 
     def __init__(self, cfg: HybridConfig, weights: Dict[str, torch.Tensor], device="cuda:0",
-                 prefill_chunk: int = 512):
+                 prefill_chunk: int = 512, gemm_choices: bool = True):
+        """gemm_choices: look the runtime's own library GEMMs up in the bundled solution file
+        (use_gemm_choices), with TunableOp switched on only around those calls."""
         self.cfg = cfg
         self.dev = torch.device(device)
-        if self.dev.type == "cuda":
-            use_gemm_choices()
+        self._choices = _GemmChoices(self.dev.type == "cuda" and gemm_choices and use_gemm_choices())
         self.w = {k: v.to(self.dev) for k, v in weights.items()}
         self.prefill_chunk = prefill_chunk
         self.attn_layers = [i for i in range(cfg.n_layers) if cfg.is_attention(i)]
@@ -409,7 +433,7 @@ class TridaRuntime:
 
     def _mm(self, x: torch.Tensor, w: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x @ w.T on hipBLASLt (torch.matmul): prefill chunks, batched steps and the LM head."""
-        with K.timed("gemm"):
+        with K.timed("gemm"), self._choices:
             if out is None:
                 return torch.matmul(x, w.t())
             return torch.matmul(x, w.t(), out=out)
@@ -637,7 +661,8 @@ class TridaRuntime:
                 if logits_out.dtype != torch.float32 or not logits_out.is_contiguous() \
                         or logits_out.numel() != x2.shape[0] * wl.shape[0]:
                     raise ValueError("forward: logits_out must be contiguous fp32 [B, rows, V]")
-                torch.ops.aten.mm.dtype_out(x2, wl.t(), torch.float32, out=logits_out.view(x2.shape[0], -1))
+                with self._choices:
+                    torch.ops.aten.mm.dtype_out(x2, wl.t(), torch.float32, out=logits_out.view(x2.shape[0], -1))
                 logits = logits_out.view(B, x.shape[1], -1)
             elif x2.shape[0] <= K.WS_MAX_M and "lm_head" in self.ws:
                 wp, V, _, _ = self.ws["lm_head"]
