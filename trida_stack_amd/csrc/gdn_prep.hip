@@ -65,10 +65,10 @@ struct SeqRows {
   int64_t row0;
   int n;
 };
-__device__ __forceinline__ SeqRows seq_rows(const PrepArgs& a, int b) {
-  if (!a.cu_seqlens) return {(int64_t)b * a.T, a.T};
-  const int lo = a.cu_seqlens[b];
-  return {lo, max(0, min(a.cu_seqlens[b + 1] - lo, a.T))};
+__device__ __forceinline__ SeqRows seq_rows(const int32_t* cu_seqlens, int T, int b) {
+  if (!cu_seqlens) return {(int64_t)b * T, T};
+  const int lo = cu_seqlens[b];
+  return {lo, max(0, min(cu_seqlens[b + 1] - lo, T))};
 }
 
 __device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
@@ -94,11 +94,16 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); 
 // torch.nn.functional.softplus with beta 1 and threshold 20
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-template <int GW, int KC, int NT, int PASSES>  // lanes per q/k head = Dk / 8; conv width; threads; passes
+// IDX: the pool / packed forms (slot indices, cu_seqlens) may be in use; without it those pointers are ignored
+// (null) and the plain form compiles without their loads and branches.
+template <int GW, int KC, int NT, int PASSES, bool IDX>  // lanes per q/k head = Dk / 8; conv width; threads; passes
 __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
+  const int32_t* cu_seqlens = IDX ? a.cu_seqlens : nullptr;
+  const int32_t* win_idx = IDX ? a.win_idx : nullptr;
+  const int32_t* pre_idx = IDX ? a.pre_idx : nullptr;
   const int t = blockIdx.x % a.T;
   const int b = blockIdx.x / a.T;
-  const SeqRows sr = seq_rows(a, b);
+  const SeqRows sr = seq_rows(cu_seqlens, a.T, b);
   if (t >= sr.n) return;  // past a packed sequence's rows (block-uniform)
   const int T = sr.n;
   const int tid = threadIdx.x;
@@ -106,17 +111,25 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
   const int pieces = a.C / 8;
   const int pbase = blockIdx.y * NT * PASSES;  // the block's first piece: a multiple of GW
   // the sequence's source rows (packed: row r of x at r x_st) and its window row
-  const uint16_t* xb = a.cu_seqlens ? a.x + sr.row0 * a.x_st : a.x + (int64_t)b * a.x_sb;
-  const int64_t ab0 = a.cu_seqlens ? sr.row0 * a.ab_st : (int64_t)b * a.ab_sb;
-  const int wrow = a.win_idx ? a.win_idx[b] : b;
+  const uint16_t* xb = cu_seqlens ? a.x + sr.row0 * a.x_st : a.x + (int64_t)b * a.x_sb;
+  const int64_t ab0 = cu_seqlens ? sr.row0 * a.ab_st : (int64_t)b * a.ab_sb;
+  const int wrow = win_idx ? win_idx[b] : b;
+  const int prow_b = pre_idx ? pre_idx[b] : b;  // pre_out slot
   const uint16_t* wb = a.window + (int64_t)wrow * (a.Kc - 1) * a.C;
   const int64_t orow = sr.row0 + t;  // output row (q, k, v, g, beta)
 
-  // every load of the block first (one memory round trip): per pass, the KC source rows of the thread's
-  // 8 channels and their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces), and the
-  // gate inputs. Lanes past the last piece load it (clamped) and store nothing; passes past it are
-  // skipped (block-uniform)
-  u32x4 xs[PASSES][KC], wsv[PASSES][KC];
+  // every load of the block first (one memory round trip): the gate inputs, then per pass the KC source rows
+  // of the thread's 8 channels, their conv weights (8 channels x KC taps, contiguous: KC 16-byte pieces) and
+  // bias. The loads are unconditional (the gate inputs of blocks that do not write the gates, the bias from
+  // the conv weights when there is none: in bounds, unused), so that no branch splits the round trip. Lanes
+  // past the last piece load it (clamped) and store nothing; passes past it are skipped (block-uniform)
+  const bool gates = blockIdx.y == 0;  // block-uniform
+  const int hg = min(tid, a.Hv - 1);
+  const uint16_t ar = a.a_in[ab0 + (int64_t)t * a.ab_st + hg];
+  const uint16_t br = a.b_in[ab0 + (int64_t)t * a.ab_st + hg];
+  const float alog = a.A_log[hg], dtb = a.dt_bias[hg];
+  const uint16_t* cbias = a.conv_bias ? a.conv_bias : a.conv_w;
+  u32x4 xs[PASSES][KC], wsv[PASSES][KC], bsv[PASSES];
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
     if (pbase + ps * NT >= pieces) break;
@@ -128,14 +141,9 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
       xs[ps][j] = *reinterpret_cast<const u32x4*>(src);
       wsv[ps][j] = reinterpret_cast<const u32x4*>(a.conv_w + (int64_t)c * KC)[j];
     }
+    bsv[ps] = *reinterpret_cast<const u32x4*>(cbias + c);
   }
-  const bool gates = blockIdx.y == 0;  // block-uniform
-  const int hg = min(tid, a.Hv - 1);
-  float av = 0.f, bv = 0.f;
-  if (gates) {
-    av = bf2f(a.a_in[ab0 + (int64_t)t * a.ab_st + hg]);
-    bv = bf2f(a.b_in[ab0 + (int64_t)t * a.ab_st + hg]);
-  }
+  float av = bf2f(ar), bv = bf2f(br);
 
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
@@ -146,7 +154,7 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
     const int c = min(p, pieces - 1) * 8;
     // the pre-conv rows a rollback rebuilds the window from: the block's own row is its last source row
     if (a.pre_out && live) {
-      const int64_t prow = (int64_t)(a.pre_idx ? a.pre_idx[b] : b) * a.T + t;
+      const int64_t prow = (int64_t)prow_b * a.T + t;
       *reinterpret_cast<u32x4*>(a.pre_out + prow * a.C + c) = xs[ps][KC - 1];
     }
     float acc[8];
@@ -160,15 +168,10 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
           const uint32_t word = wsv[ps][e / 8][(e % 8) / 2];
           w[ch][j] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
         }
-      if (a.conv_bias) {
-        float bias[8];
-        unpack8(*reinterpret_cast<const u32x4*>(a.conv_bias + c), bias);
+      float bias[8];
+      unpack8(bsv[ps], bias);
 #pragma unroll
-        for (int ch = 0; ch < 8; ++ch) acc[ch] = bias[ch];
-      } else {
-#pragma unroll
-        for (int ch = 0; ch < 8; ++ch) acc[ch] = 0.f;
-      }
+      for (int ch = 0; ch < 8; ++ch) acc[ch] = a.conv_bias ? bias[ch] : 0.f;
 #pragma unroll
       for (int j = 0; j < KC; ++j) {
         float f[8];
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(PrepArgs a) {
         bv = bf2f(a.b_in[ab0 + (int64_t)t * a.ab_st + hh]);
       }
       const int64_t o = orow * a.Hv + hh;
-      a.g[o] = -__expf(a.A_log[hh]) * softplus(av + a.dt_bias[hh]);
+      a.g[o] = -__expf(hh == tid ? alog : a.A_log[hh]) * softplus(av + (hh == tid ? dtb : a.dt_bias[hh]));
       a.beta[o] = 1.f / (1.f + __expf(-bv));
     }
   }
@@ -266,11 +269,18 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
   const bool wide = B * T >= 512;
   TRIDA_CHECK(!wide || C <= 8 * 256 * 4, TRIDA_ERR_ARG, "gdn_prep: conv_dim %lld above %d", (long long)C, 8 * 256 * 4);
   const dim3 grid((unsigned)(B * T), wide ? 1u : (unsigned)cdiv(C / 8, 128));
-#define TRIDA_PREP_KC(GW, NT, PS)                                                                          \
+  const bool idx = cu_seqlens || win_idx || pre_idx;
+#define TRIDA_PREP_KC2(GW, NT, PS, IX)                                                                     \
   switch (Kc) {                                                                                            \
-    case 2: hipLaunchKernelGGL((gdn_prep_kernel<GW, 2, NT, PS>), grid, dim3(NT), 0, st, a); break;         \
-    case 3: hipLaunchKernelGGL((gdn_prep_kernel<GW, 3, NT, PS>), grid, dim3(NT), 0, st, a); break;         \
-    default: hipLaunchKernelGGL((gdn_prep_kernel<GW, 4, NT, PS>), grid, dim3(NT), 0, st, a); break;        \
+    case 2: hipLaunchKernelGGL((gdn_prep_kernel<GW, 2, NT, PS, IX>), grid, dim3(NT), 0, st, a); break;     \
+    case 3: hipLaunchKernelGGL((gdn_prep_kernel<GW, 3, NT, PS, IX>), grid, dim3(NT), 0, st, a); break;     \
+    default: hipLaunchKernelGGL((gdn_prep_kernel<GW, 4, NT, PS, IX>), grid, dim3(NT), 0, st, a); break;    \
+  }
+#define TRIDA_PREP_KC(GW, NT, PS)        \
+  if (idx) {                             \
+    TRIDA_PREP_KC2(GW, NT, PS, true)     \
+  } else {                               \
+    TRIDA_PREP_KC2(GW, NT, PS, false)    \
   }
 #define TRIDA_PREP_LAUNCH(GW)      \
   if (wide) {                      \
@@ -285,5 +295,6 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
   }
 #undef TRIDA_PREP_LAUNCH
 #undef TRIDA_PREP_KC
+#undef TRIDA_PREP_KC2
   return launch_status("gdn_prep");
 }

@@ -164,8 +164,14 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // to fp32 once per block, so a row step reads them ready (the bf16 unpack and the scale multiply leave
 // the per-step chain: 24 of ~80 instructions per step); chunks of 40 rows keep the fp32 stages within
 // two blocks per CU. Large grids keep the bf16 stages, whose smaller LDS footprint holds more blocks.
-template <int KPL, int NW, bool PREP, bool F32>
+// IDX: the pool / packed forms (cu_seqlens, state and window slot indices, the intermediate-state ring) may be in
+// use; without it those pointers are ignored (null) and the plain form compiles without their loads and branches.
+template <int KPL, int NW, bool PREP, bool F32, bool IDX>
 __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
+  const int32_t* cu_seqlens = IDX ? a.cu_seqlens : nullptr;
+  const int32_t* state_idx = IDX ? a.state_idx : nullptr;
+  float* inter = IDX ? a.inter : nullptr;
+  const int32_t* inter_idx = IDX ? a.inter_idx : nullptr;
   constexpr int TC = F32 ? 40 : kTC;  // rows staged per chunk
   constexpr int Dk = KPL * kLanesPerV;
   constexpr int VPB = NW * kVPerWave;
@@ -182,9 +188,9 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   // the sequence's rows: [row0, row0 + T) of the packed arrays (B x a.T rows unless cu_seqlens is given)
   int64_t row0 = (int64_t)b * a.T;
   int T = a.T;
-  if (a.cu_seqlens) {
-    row0 = a.cu_seqlens[b];
-    T = max(0, min(a.cu_seqlens[b + 1] - (int)row0, a.T));
+  if (cu_seqlens) {
+    row0 = cu_seqlens[b];
+    T = max(0, min(cu_seqlens[b + 1] - (int)row0, a.T));
   }
 
   __shared__ __align__(16) uint16_t s_q[TC][Dk];
@@ -207,14 +213,14 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
 
   const int64_t col_off = ((int64_t)h * a.Dv + v) * Dk + kl * KPL;  // within one [Hv, Dv, Dk] state
   const int64_t hvk = (int64_t)a.Hv * a.Dv * Dk;
-  const int64_t st_off = (a.state_idx ? a.state_idx[b] : b) * hvk + col_off;  // state_in / state_out
+  const int64_t st_off = (state_idx ? state_idx[b] : b) * hvk + col_off;  // state_in / state_out
   const int64_t cl_off = (int64_t)b * hvk + col_off;                           // state_clean
   float s[KPL];
 #pragma unroll
   for (int i = 0; i < KPL; ++i) s[i] = a.state_in[st_off + i];
   // the intermediate states: after row t, t < csteps, of this sequence
-  const int csteps = a.inter ? min(a.csteps, T) : 0;
-  float* inter_col = a.inter ? a.inter + (int64_t)(a.inter_idx ? a.inter_idx[b] : b) * a.csteps * hvk + col_off : nullptr;
+  const int csteps = inter ? min(a.csteps, T) : 0;
+  float* inter_col = inter ? inter + (int64_t)(inter_idx ? inter_idx[b] : b) * a.csteps * hvk + col_off : nullptr;
 
   const int nc = a.causal_mode == 2 ? min(a.num_clean, T) : T;
   const int64_t qk_row = (int64_t)a.Hk * Dk;  // elements between rows t and t+1
@@ -263,8 +269,8 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     const int Kc = p.Kc, W = Kc - 1, nsrc = T + W;
     const int key_dim = a.Hk * Dk, C = 2 * key_dim + a.Hv * a.Dv;
     const uint16_t* xs = p.x + (int64_t)b * p.x_sb;
-    const int wrow = p.win_idx ? p.win_idx[b] : b;
-    const int pslot = p.pre_idx ? p.pre_idx[b] : b;
+    const int wrow = (IDX && p.win_idx) ? p.win_idx[b] : b;
+    const int pslot = (IDX && p.pre_idx) ? p.pre_idx[b] : b;
     const uint16_t* ws = p.window + (int64_t)wrow * W * C;
     auto src_row = [&](int i) { return i < W ? ws + (int64_t)i * C : xs + (int64_t)(i - W) * p.x_st; };
     auto qk_chan = [&](int pc) { return (pc < GW ? hk * Dk : key_dim + hk * Dk - GW * 8) + pc * 8; };
@@ -549,7 +555,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
       };
       // the state after row r, when the caller keeps intermediates (uniform branch)
       auto stash = [&](int r) {
-        if (t0 + r < csteps) {
+        if (IDX && t0 + r < csteps) {
 #pragma unroll
           for (int i = 0; i < KPL; ++i) inter_col[(int64_t)(t0 + r) * hvk + i] = s[i];
         }
@@ -662,13 +668,20 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   }
 }
 
+template <int KPL, bool PREP, bool F32, bool IDX>
+void launch_nw2(const RecArgs& a, int nw, unsigned grid, hipStream_t st) {
+  switch (nw) {
+    case 4: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 4, PREP, F32, IDX>), dim3(grid), dim3(4 * kWave), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 2, PREP, F32, IDX>), dim3(grid), dim3(2 * kWave), 0, st, a); break;
+    default: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 1, PREP, F32, IDX>), dim3(grid), dim3(kWave), 0, st, a); break;
+  }
+}
 template <int KPL, bool PREP, bool F32>
 void launch_nw(const RecArgs& a, int nw, unsigned grid, hipStream_t st) {
-  switch (nw) {
-    case 4: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 4, PREP, F32>), dim3(grid), dim3(4 * kWave), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 2, PREP, F32>), dim3(grid), dim3(2 * kWave), 0, st, a); break;
-    default: hipLaunchKernelGGL((gdr_recurrent_kernel<KPL, 1, PREP, F32>), dim3(grid), dim3(kWave), 0, st, a); break;
-  }
+  if (a.cu_seqlens || a.state_idx || a.inter || a.inter_idx || a.p.win_idx || a.p.pre_idx)
+    launch_nw2<KPL, PREP, F32, true>(a, nw, grid, st);
+  else
+    launch_nw2<KPL, PREP, F32, false>(a, nw, grid, st);
 }
 
 template <int KPL, bool PREP = false>
