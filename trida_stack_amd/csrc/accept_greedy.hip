@@ -348,31 +348,51 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(FinalArgs a) {
   if (wave == 0) accept_scan(a, b, s_am, s_dr, lane);
 }
 
-// Many splits per row (the LM head's argmax epilogue leaves one per workgroup, ~255): one wave per row,
-// its lanes striding over the row's splits with coalesced loads, then a wave reduction; the same scan.
-__global__ __launch_bounds__(kThreads) void wide_finalize_kernel(FinalArgs a) {
+// Many splits per row (the LM head's argmax epilogue leaves one per workgroup, ~255): 16 waves, each taking
+// rows wave, wave + 16, ... two at a time, its lanes striding over a row's splits with coalesced loads; every
+// load of the two rows' first 256 splits is issued before any is compared (one memory latency per pair of
+// rows instead of one per split step), then a wave reduction; the same scan.
+constexpr int kWideThreads = 1024;
+__global__ __launch_bounds__(kWideThreads) void wide_finalize_kernel(FinalArgs a) {
+  constexpr int NWV = kWideThreads / kWave, PER = 4;  // waves; splits per lane per pass
   const int b = blockIdx.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   __shared__ int s_am[1024];
   __shared__ long long s_dr[1024];
-  for (int k0 = tid; k0 < a.K; k0 += kThreads) s_dr[k0] = a.drafts[(int64_t)b * a.draft_stride + k0];
-  for (int r = wave; r < a.R; r += kThreads / kWave) {
-    const int64_t base = ((int64_t)b * a.R + r) * a.S;
-    float v = -INFINITY;
-    int i = INT_MAX;
-    for (int s = lane; s < a.S; s += kWave) {  // a lane's splits come in column order
-      const float pv = a.pval[base + s];
-      const int pi = a.pidx[base + s];
-      if (better(pv, pi, v, i)) {
-        v = pv;
-        i = pi;
-      }
+  for (int k0 = tid; k0 < a.K; k0 += kWideThreads) s_dr[k0] = a.drafts[(int64_t)b * a.draft_stride + k0];
+  const int64_t total = (int64_t)a.R * a.S;  // pairs of this sequence
+  for (int r0 = wave; r0 < a.R; r0 += 2 * NWV) {
+    float v[2] = {-INFINITY, -INFINITY};
+    int i[2] = {INT_MAX, INT_MAX};
+    for (int s0 = 0; s0 < a.S; s0 += PER * kWave) {
+      float pv[2][PER];
+      int pi[2][PER];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {  // clamped, unconditional loads; out-of-range pairs are masked below
+          const int64_t e = min((int64_t)(r0 + u * NWV) * a.S + s0 + j * kWave + lane, total - 1);
+          pv[u][j] = a.pval[(int64_t)b * total + e];
+          pi[u][j] = a.pidx[(int64_t)b * total + e];
+        }
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int j = 0; j < PER; ++j)  // a lane's splits come in column order
+          if (s0 + j * kWave + lane < a.S && better(pv[u][j], pi[u][j], v[u], i[u])) {
+            v[u] = pv[u][j];
+            i[u] = pi[u][j];
+          }
     }
-    wave_argbest(v, i);
-    if (lane == 0) {
-      if (i == INT_MAX) i = 0;  // a row that is all -inf keeps index 0, as torch.argmax does
-      s_am[r] = i;
-      if (a.argmax_out) a.argmax_out[(int64_t)b * a.R + r] = i;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r = r0 + u * NWV;
+      wave_argbest(v[u], i[u]);
+      if (lane == 0 && r < a.R) {
+        const int x = i[u] == INT_MAX ? 0 : i[u];  // a row that is all -inf keeps index 0, as torch.argmax does
+        s_am[r] = x;
+        if (a.argmax_out) a.argmax_out[(int64_t)b * a.R + r] = x;
+      }
     }
   }
   __syncthreads();
@@ -625,7 +645,7 @@ extern "C" int trida_greedy_accept_splits(const float* pval, const int32_t* pidx
   TRIDA_CHECK(K == 0 || drafts, TRIDA_ERR_NULL, "greedy_accept_splits: drafts is NULL with K > 0");
   FinalArgs fa{pval, reinterpret_cast<const int*>(pidx), (int)R, (int)S, drafts, draft_stride, (int)K, n_live, ctx_len,
                argmax_out, n_acc, bonus, crop};
-  hipLaunchKernelGGL(wide_finalize_kernel, dim3((unsigned)B), dim3(kThreads), 0, static_cast<hipStream_t>(stream), fa);
+  hipLaunchKernelGGL(wide_finalize_kernel, dim3((unsigned)B), dim3(kWideThreads), 0, static_cast<hipStream_t>(stream), fa);
   return launch_status("greedy_accept_splits");
 }
 
