@@ -34,6 +34,15 @@ CASES = [  # B, T, Hq, Hkv, D, L, prefixes
     (8, 33, 16, 4, 256, 700, [600, 10, 333, 600, 0, 59, 512, 256]),
     # 20 sequences x 4 KV heads x 2 query tiles: one key split per tile
     (20, 33, 16, 4, 256, 300, [(37 * i) % 260 for i in range(20)]),
+    # more query tiles than CUs: a last tile of 4 rows joins the tile before it as its extra rows (one key
+    # split; two with 256 (sequence, KV head) pairs), a last tile of 44 rows stays a tile (two splits), as
+    # does a single tile of 64 rows
+    (40, 33, 16, 4, 256, 500, [(97 * i) % 460 for i in range(40)]),
+    (48, 65, 8, 2, 64, 300, [(53 * i) % 236 for i in range(48)]),
+    (128, 33, 8, 2, 64, 200, [(71 * i) % 167 for i in range(128)]),
+    (64, 33, 16, 4, 128, 160, [(31 * i) % 127 for i in range(64)]),
+    (48, 75, 8, 2, 64, 300, [(29 * i) % 226 for i in range(48)]),
+    (136, 16, 8, 2, 64, 200, [(41 * i) % 185 for i in range(136)]),
 ]
 
 

@@ -11,7 +11,10 @@
 //   rows each. Per 64-key step, K and V^T are staged in LDS (XOR-swizzled) while the next step is
 //   loaded into registers; every wave computes S = Q K^T for its rows with v_mfma_f32_16x16x32_bf16 (Q
 //   fragments in registers), runs the online softmax within the wave, and accumulates O += P V.
-//   Writes the unnormalised O (bf16), row max and row sum (fp32) of its split.
+//   Writes the unnormalised O (bf16), row max and row sum (fp32) of its split. A last tile of <= 16
+//   rows joins the tile before it as its extra rows (a canvas of 33 rows x 4 heads = 128 + 4): the 8
+//   waves share their products (each wave one half of one key tile of Q K^T, 1/8 of the columns of
+//   P V, from the K / V fragments it reads for its own rows), so the keys stream once for all rows.
 // attn_combine: merges the splits per row (log-sum-exp weights), applies the optional output gate
 //   sigmoid(gate) and writes bf16.
 #include <math.h>
@@ -25,7 +28,8 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kNW = 8;              // waves per workgroup
 constexpr int kWR = 16;             // query rows per wave (one MFMA row tile)
-constexpr int kMT = kNW * kWR;      // query rows per workgroup
+constexpr int kMT = kNW * kWR;      // query rows per workgroup, before extra rows
+constexpr int kMTX = kMT + kWR;     // with a last tile's <= 16 extra rows
 constexpr int kKB = 64;             // keys per step
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kMaxLptSeqs = 256;  // batches up to this size are scheduled longest-first
@@ -47,8 +51,8 @@ struct AttnArgs {
   const uint16_t* k_cache;  // [B, Hkv, Lmax, D]
   const uint16_t* v_cache;
   const int32_t* prefix;    // [B]
-  uint16_t* opart;          // [B, Hkv, QT, S, kMT, D] bf16
-  float* mpart;             // [B, Hkv, QT, S, kMT]
+  uint16_t* opart;          // [B, Hkv, QT, S, kMTX, D] bf16
+  float* mpart;             // [B, Hkv, QT, S, kMTX]
   float* lpart;
   int T, Hq, Hkv, G, Lmax, S, QT, mask_mode, n_clean;
   float scale_log2;         // softmax scale * log2(e)
@@ -77,6 +81,11 @@ __device__ __forceinline__ int vt_off(int d, int kgrp) { return d * kKB + ((kgrp
 // product with V (a 32-key block takes slots 8 g + j = keys 32 kk + 4 g + j and 32 kk + 16 + 4 g + j - 4,
 // which is where the two key tiles' accumulators put them). O is rescaled only when a row's running max
 // moved. Writes the unnormalised O, the row max (log2 domain) and the row sum of its split.
+// Extra rows (the last tile's kMT .. kMT + 15): wave w adds the half w % 2 of the k-chunks of key tile w / 2
+// of their S^T (its own K fragments, the extra rows' Q from LDS) and parks it in LDS; at the next step's
+// first barrier every wave sums the halves, runs the extra rows' online softmax (the same values in every
+// wave) and accumulates its XCT 16-column tiles of their O^T from the V^T still staged, before the next
+// staging overwrites it.
 template <int D>
 __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   constexpr int KC = D / 32;         // 32-wide k-chunks of the head dim (QK^T)
@@ -85,9 +94,12 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   constexpr int NT = kNW * kWave;
   constexpr int NKG = kKB * GPR / NT;  // K groups staged per thread
   constexpr int NVP = (kKB / 8) * (D / 4);  // V pieces of 8 keys x 4 columns per step
+  constexpr int XCT = CT / kNW > 0 ? CT / kNW : 1;  // O^T column tiles of the extra rows per wave
   __shared__ __align__(16) uint16_t sQ[kMT * D];  // [row][D], groups swizzled by row & 7 (as K)
+  __shared__ __align__(16) uint16_t sQx[kWR * D];  // the extra rows, the same layout
   __shared__ __align__(16) uint16_t sK[kKB * D];
   __shared__ __align__(16) uint16_t sVt[D * kKB];
+  __shared__ f32x4 sSx[kNW][kWave];  // per wave: its half of one key tile of the extra rows' S^T
 
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
   const int per_pair = a.S * a.QT;                  // workgroups per (sequence, KV head)
@@ -129,7 +141,9 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   }
   const int M = a.T * a.G;
   const int m0 = qt * kMT;
-  const int rows = min(kMT, M - m0);
+  // the tile's rows: kMT, or for the last tile all that remain (<= kMTX: nx extra rows past kMT)
+  const int rows = qt == a.QT - 1 ? M - m0 : kMT;
+  const int nx = max(rows - kMT, 0);  // block-uniform
   // a prefix past the cache capacity (a caller's overlong decode) is clamped so that every key read
   // stays inside this sequence's [Lmax, D] rows
   const int prefix = min(max(a.prefix[b], 0), a.Lmax - a.T);
@@ -148,8 +162,8 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     // combine skips the split without reading its O (never with one split: its keys start at 0 and every
     // row sees at least its own)
     for (int r = tid; r < rows; r += NT) {
-      a.mpart[pbase * kMT + r] = -INFINITY;
-      a.lpart[pbase * kMT + r] = 0.f;
+      a.mpart[pbase * kMTX + r] = -INFINITY;
+      a.lpart[pbase * kMTX + r] = 0.f;
     }
     return;
   }
@@ -183,20 +197,26 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   // load of the tile is issued before the first store, so the staging costs one memory latency.
   {
     constexpr int QPT = kMT * GPR / NT;  // 16-byte pieces per thread
-    u32x4 qv[QPT];
+    static_assert(kWR * GPR <= NT, "one piece of the extra rows per thread");
+    u32x4 qv[QPT], qx = u32x4{0u, 0u, 0u, 0u};
+    auto q_at = [&](int m, int grp) {
+      const int t = m / a.G, g = m % a.G;
+      return *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + grp * 8);
+    };
 #pragma unroll
     for (int j = 0; j < QPT; ++j) {
       const int gi = tid + j * NT;
-      const int r = gi / GPR, grp = gi % GPR;
-      const int m = m0 + min(r, rows - 1), t = m / a.G, g = m % a.G;
-      qv[j] = *reinterpret_cast<const u32x4*>(a.q + (((int64_t)b * a.T + t) * a.Hq + hk * a.G + g) * D + grp * 8);
+      qv[j] = q_at(m0 + min(gi / GPR, rows - 1), gi % GPR);
     }
+    if (nx > 0 && tid < kWR * GPR) qx = q_at(m0 + kMT + min(tid / GPR, nx - 1), tid % GPR);
 #pragma unroll
     for (int j = 0; j < QPT; ++j) {
       const int gi = tid + j * NT;
       const int r = gi / GPR, grp = gi % GPR;
       *reinterpret_cast<u32x4*>(&sQ[k_off<D>(r, grp)]) = r < rows ? qv[j] : u32x4{0u, 0u, 0u, 0u};
     }
+    if (nx > 0 && tid < kWR * GPR)
+      *reinterpret_cast<u32x4*>(&sQx[k_off<D>(tid / GPR, tid % GPR)]) = tid / GPR < nx ? qx : u32x4{0u, 0u, 0u, 0u};
   }
 
   auto stage_step = [&]() {
@@ -240,62 +260,39 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   }
   const int g4 = 4 * (l / 16);
 
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int key0 = kb * kKB;
-    __syncthreads();  // the previous step's tiles are consumed
-    stage_step();
-    __syncthreads();
-    if (kb + 1 < kb1) load_step(kb + 1);  // in flight during this step's MFMAs
-    // a wave with no row of the tile (the last tile of a canvas, e.g. rows 128..131 of 33 x 4) only helps
-    // stage the keys: its fragment reads and MFMAs would be on padding (wave-uniform; no barrier inside)
-    if (w * kWR >= rows) continue;
-    // ---- S^T = K Q^T: keys 16 kt + 4 (l / 16) + e of this lane's query row (4 key tiles)
-    f32x4 sacc[4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kc = 0; kc < KC; ++kc) {
-      const bf16x8 qf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sQ[k_off<D>(w * kWR + (l % 16), kc * 4 + l / 16)]));
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        const bf16x8 kf =
-            as_bf16x8(*reinterpret_cast<const u32x4*>(&sK[k_off<D>(kt * 16 + (l % 16), kc * 4 + l / 16)]));
-        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf, sacc[kt], 0, 0, 0);
-      }
-    }
-    // ---- mask, scale, online softmax of the lane's row. The mask applies only on steps that reach the
-    // block keys or the cache end (uniform)
+  // ---- mask, scale and online softmax of one step's scores sc (keys 16 kt + g4 + e of the lane's row, which
+  // sees the keys below lim) against the row's running max m and sum lsum; returns the probabilities as the
+  // B fragments of the two 32-key blocks in pb and the rescale factor of the row's O. The mask applies only
+  // on steps that reach the block keys or the cache end (uniform)
+  auto softmax_step = [&](f32x4 (&sc)[4], int key0, int lim, float& m, float& lsum, u32x4 (&pb)[2]) {
     const bool edge = key0 + kKB > prefix || key0 + kKB > nk;
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sacc[kt][e] *= a.scale_log2;
+      for (int e = 0; e < 4; ++e) sc[kt][e] *= a.scale_log2;
     if (edge) {
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) sacc[kt][e] = key0 + 16 * kt + g4 + e < klim ? sacc[kt][e] : -INFINITY;
+        for (int e = 0; e < 4; ++e) sc[kt][e] = key0 + 16 * kt + g4 + e < lim ? sc[kt][e] : -INFINITY;
     }
-    float mx = fmaxf(fmaxf(sacc[0][0], sacc[0][1]), fmaxf(sacc[0][2], sacc[0][3]));
+    float mx = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
 #pragma unroll
-    for (int kt = 1; kt < 4; ++kt)
-      mx = fmaxf(mx, fmaxf(fmaxf(sacc[kt][0], sacc[kt][1]), fmaxf(sacc[kt][2], sacc[kt][3])));
+    for (int kt = 1; kt < 4; ++kt) mx = fmaxf(mx, fmaxf(fmaxf(sc[kt][0], sc[kt][1]), fmaxf(sc[kt][2], sc[kt][3])));
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx);
+    const float m_new = fmaxf(m, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2_hw(m_run - m_use);
-    m_run = m_new;
-    // probabilities: the B fragments of the two 32-key blocks
-    u32x4 pb[2];
+    const float alpha = exp2_hw(m - m_use);
+    m = m_new;
     float ps = 0.f;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       float p[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        p[e] = exp2_hw(sacc[2 * kk][e] - m_use);
-        p[4 + e] = exp2_hw(sacc[2 * kk + 1][e] - m_use);
+        p[e] = exp2_hw(sc[2 * kk][e] - m_use);
+        p[4 + e] = exp2_hw(sc[2 * kk + 1][e] - m_use);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) ps += p[e];
@@ -303,7 +300,86 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     }
     ps += __shfl_xor(ps, 16, kWave);
     ps += __shfl_xor(ps, 32, kWave);
-    l_run = l_run * alpha + ps;
+    lsum = lsum * alpha + ps;
+    return alpha;
+  };
+
+  // the extra rows: this wave's O^T column tiles w * XCT .. (waves past CT / XCT have none), their running
+  // max and sum (the same in every wave), and the keys their lanes' rows see
+  const bool xw = w * XCT < CT;
+  f32x4 ox[XCT];
+#pragma unroll
+  for (int j = 0; j < XCT; ++j) ox[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float mx_run = -INFINITY, lx_run = 0.f;
+  int klim_x = 0;
+  if (nx > 0) {
+    const int t = (m0 + kMT + min(l % 16, nx - 1)) / a.G;
+    const bool all = a.mask_mode == 1 || (a.mask_mode == 2 && t >= a.n_clean);
+    klim_x = all ? nk : min(nk, prefix + t + 1);
+  }
+  const int ktx = w / 2, hx = w % 2;  // this wave's share of the extra rows' S^T: key tile, k-chunk half
+  auto extra_step = [&](int kbp) {
+    f32x4 sc[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) sc[kt] = sSx[2 * kt][l] + sSx[2 * kt + 1][l];
+    u32x4 pb[2];
+    const float alpha = softmax_step(sc, kbp * kKB, klim_x, mx_run, lx_run, pb);
+    if (!xw) return;  // wave-uniform
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int j = 0; j < XCT; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ox[j][e] *= alpha;
+    }
+#pragma unroll
+    for (int kk = 0; kk < kKB / 32; ++kk) {
+      const bf16x8 pf = as_bf16x8(pb[kk]);
+#pragma unroll
+      for (int j = 0; j < XCT; ++j) {
+        const int ct = w * XCT + j;
+        const bf16x8 vf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sVt[vt_off(ct * 16 + (l % 16), kk * 4 + l / 16)]));
+        ox[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, ox[j], 0, 0, 0);
+      }
+    }
+  };
+
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int key0 = kb * kKB;
+    __syncthreads();  // the previous step's tiles are consumed
+    if (nx > 0 && kb > kb0) {
+      extra_step(kb - 1);  // the extra rows of the previous step, whose V^T and S^T halves are still staged
+      __syncthreads();
+    }
+    stage_step();
+    __syncthreads();
+    if (kb + 1 < kb1) load_step(kb + 1);  // in flight during this step's MFMAs
+    // a wave with no row of the tile (a last tile of fewer rows) only helps stage the keys: its fragment
+    // reads and MFMAs would be on padding (wave-uniform; no barrier inside)
+    if (w * kWR >= rows) continue;
+    // ---- S^T = K Q^T: keys 16 kt + 4 (l / 16) + e of this lane's query row (4 key tiles), and this wave's
+    // half of key tile ktx for the extra rows
+    f32x4 sacc[4], sx = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) {
+      const bf16x8 qf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sQ[k_off<D>(w * kWR + (l % 16), kc * 4 + l / 16)]));
+      bf16x8 kfx = qf;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        const bf16x8 kf =
+            as_bf16x8(*reinterpret_cast<const u32x4*>(&sK[k_off<D>(kt * 16 + (l % 16), kc * 4 + l / 16)]));
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf, sacc[kt], 0, 0, 0);
+        if (kt == ktx) kfx = kf;
+      }
+      if (nx > 0 && kc / (KC / 2) == hx) {  // wave-uniform
+        const bf16x8 qxf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sQx[k_off<D>(l % 16, kc * 4 + l / 16)]));
+        sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfx, qxf, sx, 0, 0, 0);
+      }
+    }
+    if (nx > 0) sSx[w][l] = sx;
+    u32x4 pb[2];
+    const float alpha = softmax_step(sacc, key0, klim, m_run, l_run, pb);
     // rescale O only when some row's running max moved (rare once the max settles)
     if (__ballot(alpha != 1.f)) {
 #pragma unroll
@@ -322,44 +398,63 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
       }
     }
   }
-  const int r = w * kWR + (l % 16);
+  if (nx > 0) {
+    __syncthreads();  // the last step's S^T halves are parked; its V^T is still staged
+    extra_step(kb1 - 1);
+  }
+  const int r = w * kWR + (l % 16), rx = kMT + (l % 16);  // the lane's row and extra row of the tile
+  const bool own = r < rows, extra = xw && l % 16 < nx;
   if (a.S == 1) {
     // ---- the only split: O / l, rounded to bf16, then the gate, exactly as the combine computes it
-    if (r < rows) {
-      const int m = m0 + r, t = m / a.G, hq = hk * a.G + m % a.G;
-      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    auto emit = [&](int rr, float lsum, const f32x4& v, int ct) {
+      const int m = m0 + rr, t = m / a.G, hq = hk * a.G + m % a.G;
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      const int c = ct * 16 + g4;
+      float y[4];
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) {
-        const int c = ct * 16 + g4;
-        float y[4];
+      for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(v[e])) * inv;
+      if (a.gate) {
+        const u32x2 gw = *reinterpret_cast<const u32x2*>(a.gate + ((int64_t)b * a.T + t) * a.gate_st +
+                                                         (int64_t)hq * a.gate_hs + c);
+        const float gv[4] = {__uint_as_float(gw.x << 16), __uint_as_float(gw.x & 0xffff0000u),
+                             __uint_as_float(gw.y << 16), __uint_as_float(gw.y & 0xffff0000u)};
 #pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(o[ct][e])) * inv;
-        if (a.gate) {
-          const u32x2 gw = *reinterpret_cast<const u32x2*>(a.gate + ((int64_t)b * a.T + t) * a.gate_st +
-                                                           (int64_t)hq * a.gate_hs + c);
-          const float gv[4] = {__uint_as_float(gw.x << 16), __uint_as_float(gw.x & 0xffff0000u),
-                               __uint_as_float(gw.y << 16), __uint_as_float(gw.y & 0xffff0000u)};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(y[e])) * (1.f / (1.f + __expf(-gv[e])));
-        }
-        uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * D + c)
-                               : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + c;
-        *reinterpret_cast<u32x2*>(dst) = u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
+        for (int e = 0; e < 4; ++e) y[e] = bf2f(f2bf(y[e])) * (1.f / (1.f + __expf(-gv[e])));
       }
+      uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * D + c)
+                             : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + c;
+      *reinterpret_cast<u32x2*>(dst) = u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
+    };
+    if (own) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) emit(r, l_run, o[ct], ct);
+    }
+    if (extra) {
+#pragma unroll
+      for (int j = 0; j < XCT; ++j) emit(rx, lx_run, ox[j], w * XCT + j);
     }
     return;
   }
   // ---- write this split's unnormalised O (bf16: half the partial traffic; 8-byte row pieces) and row
   // stats (fp32)
-  uint16_t* op = a.opart + pbase * kMT * D;
-  if (r < rows) {
+  uint16_t* op = a.opart + pbase * kMTX * D;
+  auto park = [&](int rr, const f32x4& v, int ct) {
+    *reinterpret_cast<u32x2*>(&op[(int64_t)rr * D + ct * 16 + g4]) = u32x2{f2bf2(v[0], v[1]), f2bf2(v[2], v[3])};
+  };
+  if (own) {
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-      *reinterpret_cast<u32x2*>(&op[(int64_t)r * D + ct * 16 + g4]) =
-          u32x2{f2bf2(o[ct][0], o[ct][1]), f2bf2(o[ct][2], o[ct][3])};
+    for (int ct = 0; ct < CT; ++ct) park(r, o[ct], ct);
     if (l < 16) {
-      a.mpart[pbase * kMT + r] = m_run;
-      a.lpart[pbase * kMT + r] = l_run;
+      a.mpart[pbase * kMTX + r] = m_run;
+      a.lpart[pbase * kMTX + r] = l_run;
+    }
+  }
+  if (extra) {
+#pragma unroll
+    for (int j = 0; j < XCT; ++j) park(rx, ox[j], w * XCT + j);
+    if (w == 0 && l < 16) {
+      a.mpart[pbase * kMTX + rx] = mx_run;
+      a.lpart[pbase * kMTX + rx] = lx_run;
     }
   }
 }
@@ -422,7 +517,8 @@ __global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
 #pragma unroll
       for (int r = 0; r < RB; ++r) {
         const int mr = min(m0 + r, M - 1);
-        mv[q][r] = a.mpart[((pair * a.QT + mr / kMT) * a.S + sp) * kMT + mr % kMT];
+        const int tq = min(mr / kMT, a.QT - 1);
+        mv[q][r] = a.mpart[((pair * a.QT + tq) * a.S + sp) * kMTX + (mr - tq * kMT)];
       }
     }
 #pragma unroll
@@ -453,8 +549,9 @@ __global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
   // lane's splits loaded together)
   for (int ri = wave; ri < RB; ri += NWV) {
     const int mr = min(m0 + ri, M - 1);
-    const int64_t bs = (pair * a.QT + mr / kMT) * a.S;
-    const int r = mr % kMT;
+    const int tq = min(mr / kMT, a.QT - 1);  // the last tile holds its extra rows past kMT
+    const int64_t bs = (pair * a.QT + tq) * a.S;
+    const int r = mr - tq * kMT;
     constexpr int JU = kMaxSplits / kWave;  // listed splits per lane, at most
     float mj[JU], lj[JU];
 #pragma unroll
@@ -462,8 +559,8 @@ __global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
       const int j = lane + u * kWave;
       if (u * kWave < ns) {  // uniform
         const int sj = s_list[min(j, ns - 1)];
-        mj[u] = a.mpart[(bs + sj) * kMT + r];
-        lj[u] = a.lpart[(bs + sj) * kMT + r];
+        mj[u] = a.mpart[(bs + sj) * kMTX + r];
+        lj[u] = a.lpart[(bs + sj) * kMTX + r];
       }
     }
     float mx = -INFINITY;
@@ -488,9 +585,10 @@ __global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
     if (lane == 0) s_inv[ri] = lsum > 0.f ? 1.f / lsum : 0.f;
   }
   __syncthreads();
-  const int64_t bs = (pair * a.QT + mc / kMT) * a.S;
-  const uint16_t* obase = a.opart + (int64_t)(mc % kMT) * D + c;
-  const int64_t sstride = (int64_t)kMT * D;  // elements between consecutive splits
+  const int tqc = min(mc / kMT, a.QT - 1);
+  const int64_t bs = (pair * a.QT + tqc) * a.S;
+  const uint16_t* obase = a.opart + (int64_t)(mc - tqc * kMT) * D + c;
+  const int64_t sstride = (int64_t)kMTX * D;  // elements between consecutive splits
   auto ld4 = [](const uint16_t* p) {  // 4 bf16 -> fp32
     const u32x2 w = *reinterpret_cast<const u32x2*>(p);
     return f32x4{__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xffff0000u), __uint_as_float(w.y << 16),
@@ -523,16 +621,28 @@ __global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
 // Splits per (sequence, KV head, query tile): as many as keep the grid within one workgroup per CU
 // (a workgroup holds a CU's LDS), at least one key block each. Measured at batch 1 (33 canvas rows,
 // 16 / 4 heads, d 256): 2200 keys 30.0 -> 25 us, 8192 keys 54.2 -> 40 us against splits of >= 4 key
-// blocks; a grid just past the CU count (33 splits) runs a ragged second round and is slower. At
-// batch 64 one split per query tile is best (the grid already exceeds the CUs).
+// blocks; a grid just past the CU count (33 splits) runs a ragged second round and is slower.
+// When the query tiles alone fill the CUs (a batch of sequences), two splits per tile, so that the
+// longest sequences of a ragged batch are not one workgroup's serial walk over their keys (64 sequences
+// of 512-4096 keys, 32 rows x 4 heads: 245 -> 201 us).
 constexpr int64_t kCUs = 256;
 int64_t plan_splits(int64_t B, int64_t Hkv, int64_t QT, int64_t max_keys, int64_t splits) {
   if (splits > 0) return splits;
   const int64_t nblk = cdiv(max_keys, kKB);
+  if (B * Hkv * QT >= kCUs) return std::max<int64_t>(1, std::min<int64_t>(2, nblk));
   int64_t s = kCUs / (B * Hkv * QT);
   if (s > nblk) s = nblk;
   if (s > kMaxSplits) s = kMaxSplits;
   return s < 1 ? 1 : s;
+}
+
+// Query tiles of M rows per (sequence, KV head): kMT rows each. A last one of <= 16 rows joins the tile
+// before it as its extra rows when its own workgroups would not fit beside the others on the CUs (a batch
+// of sequences; 64 x 33 rows x 4 heads, 512-4096 keys: 277 -> 243 us). Where they fit (batch 1) they run
+// on otherwise idle CUs and the extra rows' work would only lengthen the full tile's (23.1 -> 25.5 us).
+int64_t query_tiles(int64_t B, int64_t Hkv, int64_t M) {
+  const int64_t qt = cdiv(M, kMT);
+  return qt > 1 && M - (qt - 1) * kMT <= kWR && B * Hkv * qt > kCUs ? qt - 1 : qt;
 }
 
 }  // namespace
@@ -543,10 +653,10 @@ using namespace trida;
 extern "C" int64_t trida_attn_canvas_scratch_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
                                                    int64_t max_keys, int64_t splits) {
   if (B <= 0 || T <= 0 || Hkv <= 0 || Hq % Hkv || D <= 0) return 0;
-  const int64_t QT = cdiv(T * (Hq / Hkv), kMT);
+  const int64_t QT = query_tiles(B, Hkv, T * (Hq / Hkv));
   const int64_t S = plan_splits(B, Hkv, QT, max_keys, splits);
   const int64_t slots = B * Hkv * QT * S;
-  return align_up(slots * kMT * D * 2, 256) + 2 * align_up(slots * kMT * 4, 256);
+  return align_up(slots * kMTX * D * 2, 256) + 2 * align_up(slots * kMTX * 4, 256);
 }
 
 namespace {
@@ -567,7 +677,7 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   TRIDA_CHECK(gate == nullptr || (gate_head_stride >= D && gate_row_stride >= Hq * gate_head_stride - (gate_head_stride - D)),
               TRIDA_ERR_ARG, "attn_canvas: gate strides");
   const int64_t G = Hq / Hkv;
-  const int64_t QT = cdiv(T * G, kMT);
+  const int64_t QT = query_tiles(B, Hkv, T * G);
   const int64_t S = plan_splits(B, Hkv, QT, max_keys > 0 ? max_keys : Lmax, splits);
   TRIDA_CHECK(S >= 1 && S <= kMaxSplits, TRIDA_ERR_ARG, "attn_canvas: 1..%d key splits", kMaxSplits);
   const int64_t need = trida_attn_canvas_scratch_bytes(B, T, Hq, Hkv, D, max_keys > 0 ? max_keys : Lmax, S);
@@ -577,8 +687,8 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   TRIDA_CHECK(slots < INT32_MAX && B * Hkv < 65535, TRIDA_ERR_ARG, "attn_canvas: grid too large");
   char* ws = static_cast<char*>(scratch);
   uint16_t* opart = reinterpret_cast<uint16_t*>(ws);
-  float* mpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 2, 256));
-  float* lpart = reinterpret_cast<float*>(ws + align_up(slots * kMT * D * 2, 256) + align_up(slots * kMT * 4, 256));
+  float* mpart = reinterpret_cast<float*>(ws + align_up(slots * kMTX * D * 2, 256));
+  float* lpart = reinterpret_cast<float*>(ws + align_up(slots * kMTX * D * 2, 256) + align_up(slots * kMTX * 4, 256));
   hipStream_t st = static_cast<hipStream_t>(stream);
   TRIDA_CHECK(!frag || B * T <= 48, TRIDA_ERR_ARG, "attn_canvas_frag: the fragment order holds at most 48 rows");
   AttnArgs a{q,           k_cache,         v_cache,          prefix_len, opart, mpart, lpart, (int)T, (int)Hq, (int)Hkv,
