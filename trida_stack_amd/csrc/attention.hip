@@ -12,9 +12,10 @@
 //   loaded into registers; every wave computes S = Q K^T for its rows with v_mfma_f32_16x16x32_bf16 (Q
 //   fragments in registers), runs the online softmax within the wave, and accumulates O += P V.
 //   Writes the unnormalised O (bf16), row max and row sum (fp32) of its split. A last tile of <= 16
-//   rows joins the tile before it as its extra rows (a canvas of 33 rows x 4 heads = 128 + 4): the 8
-//   waves share their products (each wave one half of one key tile of Q K^T, 1/8 of the columns of
-//   P V, from the K / V fragments it reads for its own rows), so the keys stream once for all rows.
+//   rows can join the tile before it as its extra rows (a canvas of 33 rows x 4 heads = 128 + 4), so
+//   the keys stream once for all rows: wave w takes key tile w % 4 of every step for them (an online
+//   softmax of its own over those keys) and half w / 4 of their output columns, from the K / V
+//   fragments it reads for its own rows; the workgroup merges the four key-tile states at the end.
 // attn_combine: merges the splits per row (log-sum-exp weights), applies the optional output gate
 //   sigmoid(gate) and writes bf16.
 #include <math.h>
@@ -25,6 +26,7 @@ namespace trida {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kNW = 8;              // waves per workgroup
 constexpr int kWR = 16;             // query rows per wave (one MFMA row tile)
@@ -81,11 +83,12 @@ __device__ __forceinline__ int vt_off(int d, int kgrp) { return d * kKB + ((kgrp
 // product with V (a 32-key block takes slots 8 g + j = keys 32 kk + 4 g + j and 32 kk + 16 + 4 g + j - 4,
 // which is where the two key tiles' accumulators put them). O is rescaled only when a row's running max
 // moved. Writes the unnormalised O, the row max (log2 domain) and the row sum of its split.
-// Extra rows (the last tile's kMT .. kMT + 15): wave w adds the half w % 2 of the k-chunks of key tile w / 2
-// of their S^T (its own K fragments, the extra rows' Q from LDS) and parks it in LDS; at the next step's
-// first barrier every wave sums the halves, runs the extra rows' online softmax (the same values in every
-// wave) and accumulates its XCT 16-column tiles of their O^T from the V^T still staged, before the next
-// staging overwrites it.
+// Extra rows (the last tile's kMT .. kMT + 15): wave w forms the 16 keys x 16 rows of key tile w % 4 of
+// their S^T with the K fragments of its own product (the extra rows' Q from LDS), runs an online softmax
+// over the keys it sees this way, and accumulates columns [D/2 (w / 4), D/2 (w / 4 + 1)) of their O^T on
+// v_mfma_f32_16x16x16_bf16, whose B operand is the S^T accumulator layout as it stands (A: 4 keys of a
+// V^T row from the staged tile). No barrier inside a step; after the last one the waves of each column
+// half merge their four key tiles' states through LDS in key-tile order.
 template <int D>
 __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   constexpr int KC = D / 32;         // 32-wide k-chunks of the head dim (QK^T)
@@ -94,12 +97,12 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   constexpr int NT = kNW * kWave;
   constexpr int NKG = kKB * GPR / NT;  // K groups staged per thread
   constexpr int NVP = (kKB / 8) * (D / 4);  // V pieces of 8 keys x 4 columns per step
-  constexpr int XCT = CT / kNW > 0 ? CT / kNW : 1;  // O^T column tiles of the extra rows per wave
+  constexpr int XH = CT / 2;  // O^T column tiles of the extra rows per wave (half of them)
   __shared__ __align__(16) uint16_t sQ[kMT * D];  // [row][D], groups swizzled by row & 7 (as K)
   __shared__ __align__(16) uint16_t sQx[kWR * D];  // the extra rows, the same layout
   __shared__ __align__(16) uint16_t sK[kKB * D];
   __shared__ __align__(16) uint16_t sVt[D * kKB];
-  __shared__ f32x4 sSx[kNW][kWave];  // per wave: its half of one key tile of the extra rows' S^T
+  __shared__ float sXm[kNW][kWR], sXl[kNW][kWR];  // the extra rows' per-wave running max and sum
 
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
   const int per_pair = a.S * a.QT;                  // workgroups per (sequence, KV head)
@@ -304,12 +307,12 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     return alpha;
   };
 
-  // the extra rows: this wave's O^T column tiles w * XCT .. (waves past CT / XCT have none), their running
-  // max and sum (the same in every wave), and the keys their lanes' rows see
-  const bool xw = w * XCT < CT;
-  f32x4 ox[XCT];
+  // the extra rows: this wave's key tile and column half, its running max / sum over the keys of that tile,
+  // its O^T column tiles, and the keys the lanes' rows see
+  const int ktx = w % 4, dh = w / 4;
+  f32x4 ox[XH];
 #pragma unroll
-  for (int j = 0; j < XCT; ++j) ox[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < XH; ++j) ox[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float mx_run = -INFINITY, lx_run = 0.f;
   int klim_x = 0;
   if (nx > 0) {
@@ -317,47 +320,56 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     const bool all = a.mask_mode == 1 || (a.mask_mode == 2 && t >= a.n_clean);
     klim_x = all ? nk : min(nk, prefix + t + 1);
   }
-  const int ktx = w / 2, hx = w % 2;  // this wave's share of the extra rows' S^T: key tile, k-chunk half
-  auto extra_step = [&](int kbp) {
-    f32x4 sc[4];
+  // one step of the extra rows: sx = S^T of key tile ktx (keys 16 ktx + g4 + e of the lane's row)
+  auto extra_step = [&](f32x4 sx, int key0) {
+    const bool edge = key0 + kKB > prefix || key0 + kKB > nk;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) sc[kt] = sSx[2 * kt][l] + sSx[2 * kt + 1][l];
-    u32x4 pb[2];
-    const float alpha = softmax_step(sc, kbp * kKB, klim_x, mx_run, lx_run, pb);
-    if (!xw) return;  // wave-uniform
+    for (int e = 0; e < 4; ++e) {
+      sx[e] *= a.scale_log2;
+      if (edge) sx[e] = key0 + 16 * ktx + g4 + e < klim_x ? sx[e] : -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(sx[0], sx[1]), fmaxf(sx[2], sx[3]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(mx_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2_hw(mx_run - m_use);
+    mx_run = m_new;
+    float p[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) p[e] = exp2_hw(sx[e] - m_use);
+    float ps = (p[0] + p[1]) + (p[2] + p[3]);
+    ps += __shfl_xor(ps, 16, kWave);
+    ps += __shfl_xor(ps, 32, kWave);
+    lx_run = lx_run * alpha + ps;
     if (__ballot(alpha != 1.f)) {
 #pragma unroll
-      for (int j = 0; j < XCT; ++j)
+      for (int j = 0; j < XH; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) ox[j][e] *= alpha;
     }
+    const s16x4 pf = __builtin_bit_cast(s16x4, u32x2{f2bf2(p[0], p[1]), f2bf2(p[2], p[3])});
+    // V^T row d, keys 16 ktx + g4 .. + 3: the first (ktx even) or second half of group 4 (ktx / 2) + l / 16
 #pragma unroll
-    for (int kk = 0; kk < kKB / 32; ++kk) {
-      const bf16x8 pf = as_bf16x8(pb[kk]);
-#pragma unroll
-      for (int j = 0; j < XCT; ++j) {
-        const int ct = w * XCT + j;
-        const bf16x8 vf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sVt[vt_off(ct * 16 + (l % 16), kk * 4 + l / 16)]));
-        ox[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, ox[j], 0, 0, 0);
-      }
+    for (int j = 0; j < XH; ++j) {
+      const int d = (dh * XH + j) * 16 + (l % 16);
+      const s16x4 vf = __builtin_bit_cast(
+          s16x4, *reinterpret_cast<const u32x2*>(&sVt[vt_off(d, 4 * (ktx / 2) + l / 16) + 4 * (ktx % 2)]));
+      ox[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf, ox[j], 0, 0, 0);
     }
   };
 
   for (int kb = kb0; kb < kb1; ++kb) {
     const int key0 = kb * kKB;
     __syncthreads();  // the previous step's tiles are consumed
-    if (nx > 0 && kb > kb0) {
-      extra_step(kb - 1);  // the extra rows of the previous step, whose V^T and S^T halves are still staged
-      __syncthreads();
-    }
     stage_step();
     __syncthreads();
     if (kb + 1 < kb1) load_step(kb + 1);  // in flight during this step's MFMAs
     // a wave with no row of the tile (a last tile of fewer rows) only helps stage the keys: its fragment
     // reads and MFMAs would be on padding (wave-uniform; no barrier inside)
     if (w * kWR >= rows) continue;
-    // ---- S^T = K Q^T: keys 16 kt + 4 (l / 16) + e of this lane's query row (4 key tiles), and this wave's
-    // half of key tile ktx for the extra rows
+    // ---- S^T = K Q^T: keys 16 kt + 4 (l / 16) + e of this lane's query row (4 key tiles), and key tile ktx
+    // of the extra rows
     f32x4 sacc[4], sx = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) sacc[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -372,12 +384,11 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
         sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf, sacc[kt], 0, 0, 0);
         if (kt == ktx) kfx = kf;
       }
-      if (nx > 0 && kc / (KC / 2) == hx) {  // wave-uniform
+      if (nx > 0) {  // block-uniform
         const bf16x8 qxf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sQx[k_off<D>(l % 16, kc * 4 + l / 16)]));
         sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfx, qxf, sx, 0, 0, 0);
       }
     }
-    if (nx > 0) sSx[w][l] = sx;
     u32x4 pb[2];
     const float alpha = softmax_step(sacc, key0, klim, m_run, l_run, pb);
     // rescale O only when some row's running max moved (rare once the max settles)
@@ -397,13 +408,52 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
         o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[ct], 0, 0, 0);
       }
     }
+    if (nx > 0) extra_step(sx, key0);
   }
   if (nx > 0) {
-    __syncthreads();  // the last step's S^T halves are parked; its V^T is still staged
-    extra_step(kb1 - 1);
+    // merge the extra rows' four key-tile states of each column half into its first wave (w % 4 == 0), in
+    // key-tile order; the K / V tiles and Q are no longer read, and sQ holds the other waves' O^T tiles
+    __syncthreads();
+    f32x4* xo = reinterpret_cast<f32x4*>(sQ);  // [column half][key tile 1..3][XH][lane]
+    static_assert(2 * 3 * XH * kWave * 16 <= kMT * D * 2, "the merge's O^T tiles fit in sQ");
+    if (ktx > 0) {
+#pragma unroll
+      for (int j = 0; j < XH; ++j) xo[((dh * 3 + ktx - 1) * XH + j) * kWave + l] = ox[j];
+    }
+    if (l < kWR) {
+      sXm[w][l] = mx_run;
+      sXl[w][l] = lx_run;
+    }
+    __syncthreads();
+    if (ktx == 0) {
+      const int rr = l % 16;
+      float mm = mx_run;
+#pragma unroll
+      for (int k = 1; k < 4; ++k) mm = fmaxf(mm, sXm[dh * 4 + k][rr]);
+      const float m_use = mm == -INFINITY ? 0.f : mm;
+      const float e0 = exp2_hw(mx_run - m_use);
+      float ls = lx_run * e0;
+#pragma unroll
+      for (int j = 0; j < XH; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ox[j][e] *= e0;
+#pragma unroll
+      for (int k = 1; k < 4; ++k) {
+        const float ek = exp2_hw(sXm[dh * 4 + k][rr] - m_use);
+        ls += ek * sXl[dh * 4 + k][rr];
+#pragma unroll
+        for (int j = 0; j < XH; ++j) {
+          const f32x4 v = xo[((dh * 3 + k - 1) * XH + j) * kWave + l];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ox[j][e] += ek * v[e];
+        }
+      }
+      mx_run = mm;
+      lx_run = ls;
+    }
   }
   const int r = w * kWR + (l % 16), rx = kMT + (l % 16);  // the lane's row and extra row of the tile
-  const bool own = r < rows, extra = xw && l % 16 < nx;
+  const bool own = r < rows, extra = ktx == 0 && l % 16 < nx;
   if (a.S == 1) {
     // ---- the only split: O / l, rounded to bf16, then the gate, exactly as the combine computes it
     auto emit = [&](int rr, float lsum, const f32x4& v, int ct) {
@@ -431,7 +481,7 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     }
     if (extra) {
 #pragma unroll
-      for (int j = 0; j < XCT; ++j) emit(rx, lx_run, ox[j], w * XCT + j);
+      for (int j = 0; j < XH; ++j) emit(rx, lx_run, ox[j], dh * XH + j);
     }
     return;
   }
@@ -451,7 +501,7 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   }
   if (extra) {
 #pragma unroll
-    for (int j = 0; j < XCT; ++j) park(rx, ox[j], w * XCT + j);
+    for (int j = 0; j < XH; ++j) park(rx, ox[j], dh * XH + j);
     if (w == 0 && l < 16) {
       a.mpart[pbase * kMTX + rx] = mx_run;
       a.lpart[pbase * kMTX + rx] = lx_run;
