@@ -265,7 +265,10 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
              (int)T, (int)C, (int)Kc, (int)Hk, (int)Hv, (int)Dk, (int)Dv, x_sb, x_st, ab_sb, ab_st};
   hipStream_t st = static_cast<hipStream_t>(stream);
   // small grids: 128-piece slices, one per block; grids of >= 512 rows (which fill the GPU anyway): one
-  // block of 256 threads per row, up to 4 passes over its pieces, every pass's loads in flight together
+  // block of 256 threads per row, up to 4 passes over its pieces, every pass's loads in flight together.
+  // The passes are a template argument: each holds its loads in registers (4 x 16-byte source pieces,
+  // 4 of weights, 1 of bias per thread), so a kernel built for more passes than the row needs would hold
+  // registers for nothing and fit fewer blocks per CU
   const bool wide = B * T >= 512;
   TRIDA_CHECK(!wide || C <= 8 * 256 * 4, TRIDA_ERR_ARG, "gdn_prep: conv_dim %lld above %d", (long long)C, 8 * 256 * 4);
   const dim3 grid((unsigned)(B * T), wide ? 1u : (unsigned)cdiv(C / 8, 128));
@@ -282,11 +285,18 @@ extern "C" int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const u
   } else {                               \
     TRIDA_PREP_KC2(GW, NT, PS, false)    \
   }
-#define TRIDA_PREP_LAUNCH(GW)      \
-  if (wide) {                      \
-    TRIDA_PREP_KC(GW, 256, 4)      \
-  } else {                         \
-    TRIDA_PREP_KC(GW, 128, 1)      \
+  const int64_t passes = wide ? cdiv(C / 8, 256) : 1;
+#define TRIDA_PREP_LAUNCH(GW)          \
+  if (!wide) {                         \
+    TRIDA_PREP_KC(GW, 128, 1)          \
+  } else if (passes <= 1) {            \
+    TRIDA_PREP_KC(GW, 256, 1)          \
+  } else if (passes == 2) {            \
+    TRIDA_PREP_KC(GW, 256, 2)          \
+  } else if (passes == 3) {            \
+    TRIDA_PREP_KC(GW, 256, 3)          \
+  } else {                             \
+    TRIDA_PREP_KC(GW, 256, 4)          \
   }
   switch (Dk) {
     case 32: TRIDA_PREP_LAUNCH(4) break;
