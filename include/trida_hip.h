@@ -513,6 +513,18 @@ int trida_greedy_accept_splits(const float* pval, const int32_t* pidx, int64_t B
                                const int64_t* drafts, int64_t K, int64_t draft_stride, const int32_t* n_live,
                                const int64_t* ctx_len, int64_t* argmax_out, int32_t* n_acc, int64_t* bonus,
                                int64_t* crop, void* stream);
+/* A denoise pass's readout fused into the LM head: lm_head + the argmax and its softmax probability per row
+ * (the confidence of _denoise_shift_step, inference/zoro-1/vllm/vllm_native_diffusion/qwen3_5_diffusion.py:446-467,
+ * that trida_row_argmax computes from logits). trida_wsgemm_argmax_conf is trida_wsgemm_argmax with psum [M][S]
+ * too: sum exp(x - pval) over the workgroup's bf16 logits. trida_argmax_conf_splits reduces the triples of rows
+ * [B, R] (laid out [B, R, S], S <= 256) to argmax (int64) and conf (fp32) at b * out_row_stride + r: the
+ * argmax is trida_row_argmax's (first index, NaN first), conf = 1 / sum_s psum_s e^{pval_s - max} (the same
+ * value up to the fp32 summation order). */
+int trida_wsgemm_argmax_conf(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M, int64_t N,
+                             int64_t K, int flags, uint16_t* logits, int64_t out_row_stride, float* pval,
+                             int32_t* pidx, float* psum, void* stream);
+int trida_argmax_conf_splits(const float* pval, const int32_t* pidx, const float* psum, int64_t B, int64_t R,
+                             int64_t S, int64_t* argmax, float* conf, int64_t out_row_stride, void* stream);
 int64_t trida_ws_frag_elems(int64_t K);
 int trida_ws_frag(const uint16_t* X, int64_t x_row_stride, int64_t M, int64_t K, uint16_t* Xf, void* stream);
 int trida_wsgemm_ex(const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp, int64_t M,

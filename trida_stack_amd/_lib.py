@@ -57,6 +57,8 @@ SIGNATURES = {
     "trida_wsgemm_argmax_splits": (I64, [I64, I64]),
     "trida_wsgemm_argmax": (C.c_int, [P, I64, P, I64, I64, I64, C.c_int, P, I64, P, P, P]),
     "trida_greedy_accept_splits": (C.c_int, [P, P, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, P]),
+    "trida_wsgemm_argmax_conf": (C.c_int, [P, I64, P, I64, I64, I64, C.c_int, P, I64, P, P, P, P]),
+    "trida_argmax_conf_splits": (C.c_int, [P, P, P, I64, I64, I64, P, P, I64, P]),
     "trida_ws_frag": (C.c_int, [P, I64, I64, I64, P, P]),
     "trida_wsgemm_ex": (C.c_int, [P, I64, P, F32, P, I64, I64, I64, C.c_int, P, I64, C.c_int, P]),
     "trida_residual_parts_frag": (C.c_int, [P, I64, P, I64, I64, I64, I64, P, P, P]),

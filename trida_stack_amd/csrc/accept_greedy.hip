@@ -97,17 +97,6 @@ struct Vec<uint16_t> {  // bf16
   }
 };
 
-// Online softmax denominator over the elements a thread has seen: s = sum exp(x - m).
-__device__ __forceinline__ void acc_exp(float x, bool valid, float& m, float& s) {
-  if (!valid || x != x) return;
-  if (x > m) {
-    s = s * __expf(m - x) + 1.f;
-    m = x;
-  } else {
-    s += __expf(x - m);
-  }
-}
-
 // Element e of load u of a tile, as fp32.
 template <typename TIn>
 __device__ __forceinline__ float elem(const u32x4 w, int e) {
@@ -399,6 +388,55 @@ __global__ __launch_bounds__(kWideThreads) void wide_finalize_kernel(FinalArgs a
   if (wave == 0) accept_scan(a, b, s_am, s_dr, lane);
 }
 
+// A denoise pass's readout from the per-split (max, index, sum exp(x - max)) triples of the LM head's argmax +
+// confidence epilogue: per row, the argmax over the splits and the softmax probability of the argmax,
+// 1 / sum_s psum_s e^{pval_s - max}. Block = one sequence (16 waves, a wave per row; two rows per wave per
+// pass, every split load of both rows issued before the compares). S <= 256: one pass, the sum from the
+// same loads.
+constexpr int kConfPer = 4;
+__global__ __launch_bounds__(kWideThreads) void conf_finalize_kernel(const float* pval, const int* pidx,
+                                                                     const float* psum, int R, int S, int64_t* argmax,
+                                                                     float* conf, int64_t out_st) {
+  constexpr int NWV = kWideThreads / kWave;
+  const int b = blockIdx.x, wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t total = (int64_t)R * S, base = (int64_t)b * total;
+  for (int r0 = wave; r0 < R; r0 += 2 * NWV) {
+    float pv[2][kConfPer], ps[2][kConfPer];
+    int pi[2][kConfPer];
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int j = 0; j < kConfPer; ++j) {  // clamped, unconditional loads; out-of-range splits are masked below
+        const int64_t e = min((int64_t)(r0 + u * NWV) * S + j * kWave + lane, total - 1);
+        pv[u][j] = pval[base + e];
+        pi[u][j] = pidx[base + e];
+        ps[u][j] = psum[base + e];
+      }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r = r0 + u * NWV;
+      float v = -INFINITY;
+      int i = INT_MAX;
+#pragma unroll
+      for (int j = 0; j < kConfPer; ++j)  // a lane's splits come in column order
+        if (j * kWave + lane < S && better(pv[u][j], pi[u][j], v, i)) {
+          v = pv[u][j];
+          i = pi[u][j];
+        }
+      wave_argbest(v, i);  // every lane holds the row's (max, index)
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < kConfPer; ++j)
+        if (j * kWave + lane < S) sum += ps[u][j] * __expf(pv[u][j] - v);
+      sum = wave_sum(sum);
+      if (lane == 0 && r < R) {
+        argmax[(int64_t)b * out_st + r] = i == INT_MAX ? 0 : i;  // an all -inf row keeps index 0
+        conf[(int64_t)b * out_st + r] = sum > 0.f ? 1.f / sum : 0.f;
+      }
+    }
+  }
+}
+
 // wave 0 of a finalize block: prefix scan of draft matches (ballot; accepted = count of leading ones)
 __device__ void accept_scan(const FinalArgs& a, int b, const int* s_am, const long long* s_dr, int lane) {
   {
@@ -647,6 +685,19 @@ extern "C" int trida_greedy_accept_splits(const float* pval, const int32_t* pidx
                argmax_out, n_acc, bonus, crop};
   hipLaunchKernelGGL(wide_finalize_kernel, dim3((unsigned)B), dim3(kWideThreads), 0, static_cast<hipStream_t>(stream), fa);
   return launch_status("greedy_accept_splits");
+}
+
+extern "C" int trida_argmax_conf_splits(const float* pval, const int32_t* pidx, const float* psum, int64_t B,
+                                        int64_t R, int64_t S, int64_t* argmax, float* conf, int64_t out_row_stride,
+                                        void* stream) {
+  TRIDA_CHECK(pval && pidx && psum && argmax && conf, TRIDA_ERR_NULL,
+              "argmax_conf_splits: pval, pidx, psum, argmax and conf are required");
+  TRIDA_CHECK(B > 0 && B <= 65535 && R > 0 && S >= 1 && S <= kConfPer * kWave && out_row_stride >= R,
+              TRIDA_ERR_ARG, "argmax_conf_splits: bad sizes B=%lld R=%lld S=%lld (1 <= S <= %d) row stride %lld",
+              (long long)B, (long long)R, (long long)S, kConfPer * kWave, (long long)out_row_stride);
+  hipLaunchKernelGGL(conf_finalize_kernel, dim3((unsigned)B), dim3(kWideThreads), 0, static_cast<hipStream_t>(stream),
+                     pval, reinterpret_cast<const int*>(pidx), psum, (int)R, (int)S, argmax, conf, out_row_stride);
+  return launch_status("argmax_conf_splits");
 }
 
 namespace {

@@ -84,6 +84,23 @@ __device__ __forceinline__ bool argmax_better(float a, int ia, float b, int ib) 
   return (a > b) || (a == b && ia < ib);
 }
 
+// Online softmax denominator over the elements one thread has seen: s = sum exp(x - m) (NaN skipped).
+__device__ __forceinline__ void acc_exp(float x, bool valid, float& m, float& s) {
+  if (!valid || x != x) return;
+  if (x > m) {
+    s = s * __expf(m - x) + 1.f;
+    m = x;
+  } else {
+    s += __expf(x - m);
+  }
+}
+// Two such (m, s) states merged into (m, s).
+__device__ __forceinline__ void merge_exp(float& m, float& s, float om, float os) {
+  const float nm = fmaxf(m, om);
+  s = (nm == -INFINITY) ? 0.f : s * __expf(m - nm) + os * __expf(om - nm);
+  m = nm;
+}
+
 // ---------------------------------------------------------------- host error plumbing
 void set_error(const char* fmt, ...);
 int launch_status(const char* what);

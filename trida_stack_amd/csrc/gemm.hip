@@ -24,7 +24,9 @@
 // Epilogues: bf16 store, fp32 partials, SwiGLU (silu(gate) * up) over weights whose tiles interleave 8
 // gate rows with the matching 8 up rows, or argmax: the LM head of a greedy verify reduces each row of its
 // bf16 logits to the workgroup's (max, first index) in registers while the weights stream, and writes one
-// pair per row and workgroup (optionally the logits too), so acceptance never reads the logits again. The plan (NW, KWS, T, kg) depends on N, K and the epilogue only:
+// pair per row and workgroup (optionally the logits too), so acceptance never reads the logits again; with
+// the softmax denominator too (argmax + confidence, a denoise pass's readout): sum exp(x - max) over the
+// workgroup's columns, relative to its max. The plan (NW, KWS, T, kg) depends on N, K and the epilogue only:
 // a row of Y is bitwise the same whether X holds 1 row or 48.
 #include <algorithm>
 
@@ -36,7 +38,7 @@ namespace {
 constexpr int kCUs = 256;  // MI355X (gfx950): workgroups of a plan <= one per CU, see plan_for()
 constexpr int kMaxM = 48;
 
-enum Epilogue { kStore = 0, kParts = 1, kSilu = 2, kArgmax = 3 };
+enum Epilogue { kStore = 0, kParts = 1, kSilu = 2, kArgmax = 3, kArgmaxConf = 4 };
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ bf16x8 as_bf(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
@@ -57,6 +59,7 @@ struct WsArgs {
   int of;  // bf16 output (store / SwiGLU epilogues) in fragment order for the next GEMM (o_st unused)
   float* pval;  // argmax epilogue: [M][gridDim.x] best value of each row within each workgroup's columns
   int* pidx;    // and its column (first on ties, NaN first)
+  float* psum;  // argmax + confidence: [M][gridDim.x] sum exp(x - pval) over the workgroup's columns
 };
 
 
@@ -73,6 +76,7 @@ constexpr int nslot() {
 template <int NW, int KWS, int D, int MT, int EPI, bool NORM>
 __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
   static_assert(KWS % D == 0 || D % KWS == 0, "the ring and the K slice must tile the unrolled loop");
+  constexpr bool AMAX = EPI == kArgmax || EPI == kArgmaxConf, CONF = EPI == kArgmaxConf;
   constexpr int NSLOT = nslot<NW, MT>();
   static_assert(NSLOT >= 2, "LDS slots");
   __shared__ f32x4 red[NSLOT][NW][MT][kWave];
@@ -148,10 +152,13 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
   // flush items covered (the lanes l, l ^ 16, l ^ 32, l ^ 48 and the waves are merged at the end)
   float hv[MT];
   int hi[MT];
+  float sm[MT], ss[MT];  // CONF: the running (max, sum exp(x - max)) of the same rows and columns
 #pragma unroll
   for (int mm = 0; mm < MT; ++mm) {
     hv[mm] = -INFINITY;
     hi[mm] = INT32_MAX;
+    sm[mm] = -INFINITY;
+    ss[mm] = 0.f;
   }
   // 4 consecutive bf16 outputs (n % 4 == 0) of row m: row-major, or in fragment order for the next GEMM
   auto out_at = [&](int m, int n) -> u32x2* {
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
           packed.y = f2bf2(y2, y3);
           *out_at(m, f) = packed;
         }
-      } else if (EPI == kArgmax) {
+      } else if (AMAX) {
         // mt is uniform over a wave (its 64 items are consecutive and a tile's items come in whole waves)
         const int mt = q / kWave, ln = q % kWave;
         f32x4 sum = red[slot][0][mt][ln];
@@ -218,11 +225,16 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
             bi = n + e;
           }
 #pragma unroll
-        for (int mm = 0; mm < MT; ++mm)
+        for (int mm = 0; mm < MT; ++mm) {
           if (mm == mt && argmax_better(bv, bi, hv[mm], hi[mm])) {
             hv[mm] = bv;
             hi[mm] = bi;
           }
+          if (CONF && mm == mt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc_exp(v[e], true, sm[mm], ss[mm]);
+          }
+        }
       } else {
         const int mt = q / kWave, ln = q % kWave;
         f32x4 sum = red[slot][0][mt][ln];
@@ -276,10 +288,11 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
       }
     }
   }
-  if constexpr (EPI == kArgmax) {
+  if constexpr (AMAX) {
     // merge the four lanes of each row, then the waves in order; one (value, column) per row
     __shared__ float s_bv[NW][MT * 16];
     __shared__ int s_bi[NW][MT * 16];
+    __shared__ float s_sm[CONF ? NW : 1][MT * 16], s_ss[CONF ? NW : 1][MT * 16];
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm) {
 #pragma unroll
@@ -290,10 +303,18 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
           hv[mm] = ov;
           hi[mm] = oi;
         }
+        if (CONF) {
+          const float om = __shfl_xor(sm[mm], off, kWave), os = __shfl_xor(ss[mm], off, kWave);
+          merge_exp(sm[mm], ss[mm], om, os);
+        }
       }
       if (l < 16) {
         s_bv[wave][mm * 16 + l] = hv[mm];
         s_bi[wave][mm * 16 + l] = hi[mm];
+        if (CONF) {
+          s_sm[wave][mm * 16 + l] = sm[mm];
+          s_ss[wave][mm * 16 + l] = ss[mm];
+        }
       }
     }
     __syncthreads();
@@ -309,6 +330,13 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
         }
       a.pval[(int64_t)m * gridDim.x + blockIdx.x] = v;
       a.pidx[(int64_t)m * gridDim.x + blockIdx.x] = i;
+      if (CONF) {
+        float mx = s_sm[0][m], sum = s_ss[0][m];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) merge_exp(mx, sum, s_sm[w][m], s_ss[w][m]);
+        // relative to the workgroup's argmax value (the row max is found among these)
+        a.psum[(int64_t)m * gridDim.x + blockIdx.x] = (mx == -INFINITY || v != v) ? 0.f : sum * __expf(mx - v);
+      }
     }
   }
 }
@@ -496,12 +524,13 @@ namespace {
 // TRIDA_WS_OUT_FRAG select the fragment order of X / of the bf16 output
 int ws_run(const char* name, const uint16_t* X, int64_t x_row_stride, const float* ss, float eps, const uint16_t* Wp,
            int64_t M, int64_t N, int64_t K, int epilogue, void* out, int64_t out_row_stride, int flags, void* stream,
-           float* pval = nullptr, int* pidx = nullptr) {
-  const bool amax = epilogue == kArgmax;  // only through trida_wsgemm_argmax (pval / pidx given)
-  TRIDA_CHECK(X && Wp && (out || amax) && (!amax || (pval && pidx)), TRIDA_ERR_NULL,
-              "%s: X, Wp and out (argmax: pval and pidx) are required", name);
-  TRIDA_CHECK(epilogue >= kStore && epilogue <= (amax ? kArgmax : kSilu), TRIDA_ERR_ARG, "%s: unknown epilogue %d",
-              name, epilogue);
+           float* pval = nullptr, int* pidx = nullptr, float* psum = nullptr) {
+  // argmax (+ confidence) only through trida_wsgemm_argmax (_conf), which pass pval / pidx (/ psum)
+  const bool amax = epilogue == kArgmax || epilogue == kArgmaxConf;
+  TRIDA_CHECK(X && Wp && (out || amax) && (!amax || (pval && pidx)) && (epilogue != kArgmaxConf || psum),
+              TRIDA_ERR_NULL, "%s: X, Wp and out (argmax: pval and pidx; with confidence psum) are required", name);
+  TRIDA_CHECK(epilogue >= kStore && epilogue <= (amax ? kArgmaxConf : kSilu), TRIDA_ERR_ARG,
+              "%s: unknown epilogue %d", name, epilogue);
   TRIDA_CHECK(!amax || (!ss && !(flags & TRIDA_WS_OUT_FRAG)), TRIDA_ERR_ARG,
               "%s: the argmax epilogue takes no RMSNorm prologue and a row-major output", name);
   TRIDA_CHECK(!ss || epilogue != kParts, TRIDA_ERR_ARG,
@@ -520,18 +549,20 @@ int ws_run(const char* name, const uint16_t* X, int64_t x_row_stride, const floa
   TRIDA_CHECK(epilogue == kParts || of || (amax && !out) ||
                   (out_row_stride >= (epilogue == kSilu ? N / 2 : N) && out_row_stride % 4 == 0),
               TRIDA_ERR_ARG, "%s: bad output row stride", name);
-  TRIDA_CHECK(!amax || (N <= INT32_MAX && ((uintptr_t)pval & 3) == 0 && ((uintptr_t)pidx & 3) == 0), TRIDA_ERR_ARG,
-              "%s: argmax needs N < 2^31 and 4-byte aligned pval / pidx", name);
+  TRIDA_CHECK(!amax || (N <= INT32_MAX && ((uintptr_t)pval & 3) == 0 && ((uintptr_t)pidx & 3) == 0 &&
+                        ((uintptr_t)psum & 3) == 0),
+              TRIDA_ERR_ARG, "%s: argmax needs N < 2^31 and 4-byte aligned pval / pidx / psum", name);
   TRIDA_CHECK(((((uintptr_t)X) | (uintptr_t)Wp | (uintptr_t)out) & 15) == 0 && ((uintptr_t)ss & 3) == 0,
               TRIDA_ERR_ALIGN, "%s: X, Wp and out must be 16-byte aligned", name);
   const Plan p = plan_for(N, K, epilogue);
   TRIDA_CHECK(p.cfg >= 0 && (!ss || ss_chunks((int)K) <= kMaxSsChunks), TRIDA_ERR_ARG,
               "%s: K too long for one workgroup (epilogue %d needs kg == 1)", name, epilogue);
   WsArgs a{X, reinterpret_cast<const u32x4*>(Wp), out, x_row_stride, out_row_stride, (int)M, (int)N, (int)K, p.T, ss,
-           eps, xf ? 1 : 0, of ? 1 : 0, pval, pidx};
+           eps, xf ? 1 : 0, of ? 1 : 0, pval, pidx, psum};
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (amax) {
-    launch_cfg<kArgmax, false>(a, p, st);
+    if (epilogue == kArgmaxConf) launch_cfg<kArgmaxConf, false>(a, p, st);
+    else launch_cfg<kArgmax, false>(a, p, st);
   } else if (ss) {
     if (epilogue == kStore) launch_cfg<kStore, true>(a, p, st);
     else launch_cfg<kSilu, true>(a, p, st);
@@ -573,6 +604,13 @@ extern "C" int trida_wsgemm_argmax(const uint16_t* X, int64_t x_row_stride, cons
                                    int32_t* pidx, void* stream) {
   return ws_run("wsgemm_argmax", X, x_row_stride, nullptr, 0.f, Wp, M, N, K, kArgmax, logits, out_row_stride, flags,
                 stream, pval, pidx);
+}
+
+extern "C" int trida_wsgemm_argmax_conf(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M,
+                                        int64_t N, int64_t K, int flags, uint16_t* logits, int64_t out_row_stride,
+                                        float* pval, int32_t* pidx, float* psum, void* stream) {
+  return ws_run("wsgemm_argmax_conf", X, x_row_stride, nullptr, 0.f, Wp, M, N, K, kArgmaxConf, logits, out_row_stride,
+                flags, stream, pval, pidx, psum);
 }
 
 extern "C" int64_t trida_ws_frag_elems(int64_t K) { return K > 0 && K % 32 == 0 ? K / 32 * kWsFragMT * 64 * 8 : 0; }

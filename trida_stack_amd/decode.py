@@ -632,13 +632,22 @@ class BlockSpecStep:
         self.canvas.fill_(rt.mask_id)
         self.canvas[:, 0] = self.t0
         self.masked.fill_(True)
+        B, blk = cache.B, self.block
+        # without ban / gate rules (which edit the logits) the LM head reduces its rows to per-split (max,
+        # index, softmax denominator) triples itself: no logits are written or read back
+        fused = self.rules is None and rt.greedy_head_ok(B * blk) and rt.argmax_conf_ok()
         for p in range(self.denoise):
-            L = rt.forward(self.canvas, cache, "draft")
-            if self.rules is not None:
-                self.rules.apply(L)
             # row j predicts slot j + 1 (shift readout); the last row is not used
-            with K.timed("row_argmax"):
-                K.row_argmax(L, out=(self.d_am, self.d_conf))
+            if fused:
+                pv, pi, ps = rt.forward(self.canvas, cache, "draft", rows=blk, head="argmax_conf")
+                with K.timed("row_argmax"):
+                    K.argmax_conf_splits(pv, pi, ps, B=B, R=blk, out=(self.d_am, self.d_conf))
+            else:
+                L = rt.forward(self.canvas, cache, "draft")
+                if self.rules is not None:
+                    self.rules.apply(L)
+                with K.timed("row_argmax"):
+                    K.row_argmax(L, out=(self.d_am, self.d_conf))
             # the per[p] most confident MASK slots (ties: the lower slot first) take their predictions
             K.unmask_top(self.d_am, self.d_conf, self.masked, self.canvas, self.per[p])
 

@@ -1049,6 +1049,49 @@ def ws_gemm_argmax(x: torch.Tensor, wp: torch.Tensor, N: int, pval: torch.Tensor
     _lib.check(rc, "trida_wsgemm_argmax")
 
 
+def ws_gemm_argmax_conf(x: torch.Tensor, wp: torch.Tensor, N: int, pval: torch.Tensor, pidx: torch.Tensor,
+                        psum: torch.Tensor) -> None:
+    """ws_gemm_argmax with each split's softmax denominator too (trida_wsgemm_argmax_conf): psum fp32 [M, S]
+    receives sum exp(x - pval) over the split's bf16 logits. For argmax_conf_splits (a denoise pass's readout)."""
+    dev = _need_gpu(x, wp, pval, pidx, psum)
+    _bf16(x, "x")
+    M, Kd = x.shape
+    S = ws_argmax_splits(N, Kd)
+    if x.stride(1) != 1 or wp.numel() != N * Kd:
+        raise ValueError("ws_gemm_argmax_conf: x needs contiguous rows and wp N * K elements")
+    for t, dt, name in ((pval, torch.float32, "pval"), (pidx, torch.int32, "pidx"), (psum, torch.float32, "psum")):
+        if t.dtype != dt or not t.is_contiguous() or t.numel() < M * S:
+            raise ValueError(f"ws_gemm_argmax_conf: {name} must be contiguous {dt} of >= {M} x {S} elements")
+    rc = _lib.load().trida_wsgemm_argmax_conf(x.data_ptr(), x.stride(0), wp.data_ptr(), M, N, Kd, 0, None, 0,
+                                              pval.data_ptr(), pidx.data_ptr(), psum.data_ptr(), _stream(dev))
+    _lib.check(rc, "trida_wsgemm_argmax_conf")
+
+
+CONF_MAX_SPLITS = 256  # column splits argmax_conf_splits reduces (trida_argmax_conf_splits)
+
+
+def argmax_conf_splits(pval: torch.Tensor, pidx: torch.Tensor, psum: torch.Tensor, *, B: int, R: int, out=None):
+    """row_argmax's (argmax, conf) from the per-split triples of ws_gemm_argmax_conf, rows [B, R] (pval / pidx /
+    psum [B, R, S]). out: (argmax int64, conf fp32) [B, >= R] with the same row stride and contiguous rows."""
+    dev = _need_gpu(pval, pidx, psum)
+    n = pval.numel()
+    if n % (B * R) or pidx.numel() != n or psum.numel() != n or pval.dtype != torch.float32 \
+            or pidx.dtype != torch.int32 or psum.dtype != torch.float32 \
+            or not (pval.is_contiguous() and pidx.is_contiguous() and psum.is_contiguous()):
+        raise ValueError("argmax_conf_splits: pval / psum fp32 and pidx int32 [B, R, S], contiguous")
+    S = n // (B * R)
+    if out is None:
+        out = (torch.empty((B, R), dtype=torch.int64, device=dev), torch.empty((B, R), dtype=torch.float32, device=dev))
+    am, conf = out
+    if am.dtype != torch.int64 or conf.dtype != torch.float32 or am.stride() != conf.stride() or am.stride(1) != 1 \
+            or am.shape[0] != B or am.shape[1] < R or conf.shape[0] != B or conf.shape[1] < R:
+        raise ValueError("argmax_conf_splits: out must be int64 / fp32 [B, >= R] with equal strides")
+    rc = _lib.load().trida_argmax_conf_splits(pval.data_ptr(), pidx.data_ptr(), psum.data_ptr(), B, R, S,
+                                              am.data_ptr(), conf.data_ptr(), am.stride(0), _stream(dev))
+    _lib.check(rc, "trida_argmax_conf_splits")
+    return out
+
+
 def greedy_accept_splits(pval: torch.Tensor, pidx: torch.Tensor, drafts: torch.Tensor, *, R: int,
                          n_live: Optional[torch.Tensor] = None, ctx_len: Optional[torch.Tensor] = None,
                          want_argmax: bool = True, out=None):

@@ -507,6 +507,17 @@ class TridaRuntime:
         """Whether forward(..., head="argmax") applies to a block of `rows` rows."""
         return self.fused_greedy_head and "lm_head" in self.ws and rows <= K.WS_MAX_M
 
+    # a denoise pass of <= WS_MAX_M rows may read its argmax and confidence from the LM head's epilogue
+    fused_draft_head = True
+
+    def argmax_conf_ok(self) -> bool:
+        """Whether forward(..., head="argmax_conf") applies (with greedy_head_ok for the row count): the LM
+        head's column splits fit K.argmax_conf_splits."""
+        if not (self.fused_draft_head and "lm_head" in self.ws):
+            return False
+        wp, V, _, _ = self.ws["lm_head"]
+        return K.ws_argmax_splits(V, self.cfg.hidden) <= K.CONF_MAX_SPLITS
+
     def forward(self, ids: torch.Tensor, cache: SeqCache, mode: str, n_clean: int = 0,
                 rows: Optional[int] = None, seq: Optional[slice] = None, row0: int = 0,
                 logits_out: Optional[torch.Tensor] = None, head: str = "logits"):
@@ -517,7 +528,8 @@ class TridaRuntime:
         [B, rows, V] buffer the LM head writes instead (its fp32 accumulators, no bf16 rounding); it is
         returned. head="argmax" (greedy_head_ok): the LM head reduces each row of its bf16 logits to one
         (max, first index) pair per column split instead of writing them; returns (pval, pidx)
-        [B, rows, S] for K.greedy_accept_splits."""
+        [B, rows, S] for K.greedy_accept_splits. head="argmax_conf": the same with each split's softmax
+        denominator; returns (pval, pidx, psum) [B, rows, S] for K.argmax_conf_splits."""
         c, w = self.cfg, self.w
         B, T = ids.shape
         sq = seq if seq is not None else slice(0, cache.B)
@@ -643,19 +655,24 @@ class TridaRuntime:
         with K.timed("lm_head"):
             x2 = x.reshape(-1, x.shape[-1])
             wl = w.get("lm_head", w["embed"])
-            if head == "argmax":
+            if head in ("argmax", "argmax_conf"):
                 if logits_out is not None or not self.greedy_head_ok(x2.shape[0]):
                     raise ValueError("forward: the argmax head needs the weight-streaming LM head and <= "
                                      f"{K.WS_MAX_M} rows")
                 wp, V, _, _ = self.ws["lm_head"]
-                key = ("head", x2.shape[0])
+                conf = head == "argmax_conf"
+                key = (head, x2.shape[0])
                 bufs = self._head_bufs.get(key)
                 if bufs is None:  # fixed addresses per row count (graph capture)
-                    S = K.ws_argmax_splits(V, x2.shape[1])
-                    bufs = self._head_bufs[key] = (torch.empty(x2.shape[0] * S, dtype=torch.float32, device=self.dev),
-                                                   torch.empty(x2.shape[0] * S, dtype=torch.int32, device=self.dev))
-                K.ws_gemm_argmax(x2, wp, V, *bufs)
-                logits = (bufs[0].view(B, x.shape[1], -1), bufs[1].view(B, x.shape[1], -1))
+                    n = x2.shape[0] * K.ws_argmax_splits(V, x2.shape[1])
+                    bufs = self._head_bufs[key] = tuple(
+                        torch.empty(n, dtype=dt, device=self.dev)
+                        for dt in ((torch.float32, torch.int32, torch.float32) if conf else (torch.float32, torch.int32)))
+                if conf:
+                    K.ws_gemm_argmax_conf(x2, wp, V, *bufs)
+                else:
+                    K.ws_gemm_argmax(x2, wp, V, *bufs)
+                logits = tuple(t.view(B, x.shape[1], -1) for t in bufs)
             elif logits_out is not None:
                 # fp32 logits straight from the GEMM's fp32 accumulators (no bf16 output widened again)
                 if logits_out.dtype != torch.float32 or not logits_out.is_contiguous() \
