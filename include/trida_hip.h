@@ -532,6 +532,26 @@ int trida_wsgemm_ex(const uint16_t* X, int64_t x_row_stride, const float* ss, fl
 int trida_residual_parts_frag(uint16_t* h, int64_t h_row_stride, const float* parts, int64_t n_parts,
                               int64_t plane_stride, int64_t rows, int64_t dim, float* ss, uint16_t* h_frag,
                               void* stream);
+/* A GDN layer's gated RMSNorm folded into its recurrence and out projection (no reference counterpart as a
+ * call: the decode step's gdr -> RMSNormGated(o, z) -> out_proj, inference/zoro-1/vllm/vllm_native_diffusion/
+ * qwen3_5_diffusion.py:2207-2221 and the mlx model's GDN mixer, with no kernel between the recurrence and the
+ * projection). trida_gdr_recurrent_gnorm is trida_gdr_recurrent (contiguous form, B * T <= 48, T <= 40) that
+ * also writes u = bf16(bf16(o) * gnorm_w * silu(z)) in the weight-streaming GEMM's fragment order (u_frag,
+ * trida_ws_frag_elems(Hv * Dv) elements) and ss_parts [B * T][Hv][Dv / 8], the sums of bf16(o)^2 over each 8
+ * columns; z rows of Hv * Dv at z_row_stride. trida_wsgemm_headnorm is the partial-plane projection of those u
+ * rows (K = heads * head width, a multiple of 32 columns per head) with each head's partial sums of a row
+ * scaled by rsqrt(sum of its ss_parts / head width + eps): planes = trida_wsgemm_headnorm_planes(N, K, heads).
+ * The result equals trida_gated_rmsnorm_frag then trida_wsgemm_ex epilogue 1 up to where the bf16 roundings
+ * fall (bf16(o * inv) is not formed). */
+int trida_gdr_recurrent_gnorm(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                              const float* beta, const float* state_in, uint16_t* out, float* state_out,
+                              float* state_clean, int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk, int64_t Dv,
+                              int causal_mode, int64_t num_clean, float scale, const uint16_t* z,
+                              int64_t z_row_stride, const uint16_t* gnorm_w, uint16_t* u_frag, float* ss_parts,
+                              void* stream);
+int trida_wsgemm_headnorm_planes(int64_t N, int64_t K, int64_t heads, int32_t* kgroups);
+int trida_wsgemm_headnorm(const uint16_t* Xf, const uint16_t* Wp, int64_t M, int64_t N, int64_t K,
+                          const float* ss_parts, int64_t heads, float eps, float* parts, void* stream);
 
 int trida_add_rmsnorm(uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* out, int64_t rows, int64_t dim,
                       int64_t x_st, int64_t r_st, int64_t o_st, float eps, int zero_centred, void* stream);

@@ -59,6 +59,9 @@ SIGNATURES = {
     "trida_greedy_accept_splits": (C.c_int, [P, P, I64, I64, I64, P, I64, I64, P, P, P, P, P, P, P]),
     "trida_wsgemm_argmax_conf": (C.c_int, [P, I64, P, I64, I64, I64, C.c_int, P, I64, P, P, P, P]),
     "trida_argmax_conf_splits": (C.c_int, [P, P, P, I64, I64, I64, P, P, I64, P]),
+    "trida_gdr_recurrent_gnorm": (C.c_int, [P] * 9 + [I64] * 6 + [C.c_int, I64, C.c_float, P, I64, P, P, P, P]),
+    "trida_wsgemm_headnorm_planes": (C.c_int, [I64, I64, I64, P]),
+    "trida_wsgemm_headnorm": (C.c_int, [P, P, I64, I64, I64, P, I64, C.c_float, P, P]),
     "trida_ws_frag": (C.c_int, [P, I64, I64, I64, P, P]),
     "trida_wsgemm_ex": (C.c_int, [P, I64, P, F32, P, I64, I64, I64, C.c_int, P, I64, C.c_int, P]),
     "trida_residual_parts_frag": (C.c_int, [P, I64, P, I64, I64, I64, I64, P, P, P]),

@@ -20,6 +20,12 @@
 // v, g, beta are staged through LDS 32 at a time (all loads of a chunk in flight together).
 // Critical path per step: decay, two independent dots (S'k and S'q), two interleaved row reductions,
 // then o = S'q + delta (k.q); the state update itself is off the path.
+//
+// Gated-norm outputs (trida_gdr_recurrent_gnorm, small grids, one staged chunk): besides o, the block
+// writes u = bf16(bf16(o) * w * silu(z)) of its value columns in the weight-streaming GEMM's fragment order
+// and the sum of bf16(o)^2 over each 8 of its columns. The layer's gated RMSNorm, bf16(o * inv) * w * silu(z)
+// with inv = rsqrt(mean_head(o^2) + eps), is then inv times u up to the rounding order: the out projection
+// applies inv per row and head to its partial sums (trida_wsgemm_headnorm), so no kernel runs between the two.
 #include "common.h"
 
 namespace trida {
@@ -28,6 +34,7 @@ namespace {
 constexpr int kLanesPerV = 16;
 constexpr int kVPerWave = kWave / kLanesPerV;  // 4
 constexpr int kTC = 64;                        // rows staged per LDS chunk (a canvas block fits in one)
+constexpr int kTCF32 = 40;                     // the same, fp32-stage form
 
 // A DPP lane permutation within 16-lane rows (row_ror and quad_perm read lanes of the same row only).
 // Written as update_dpp with a defined old value and bound_ctrl so that the compiler folds it into the
@@ -110,6 +117,13 @@ struct RecArgs {
   float* inter;               // [rows, csteps, Hv, Dv, Dk] states after rows 0..csteps-1, or null
   const int32_t* inter_idx;   // [B] inter row of sequence b, or null (row b)
   int csteps;
+  // gated-norm outputs (F32 form, T <= one chunk): z rows (row stride gz_st), the norm weight [Dv], u in
+  // fragment order [rows][Hv * Dv] and the partial sums of squares [rows][Hv][Dv / 8]; or null
+  const uint16_t* gz;
+  int64_t gz_st;
+  const uint16_t* gw;
+  uint16_t* gu;
+  float* gss;
 };
 
 __device__ __forceinline__ void unpack8(const u32x4 w, float* f) {
@@ -172,7 +186,7 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   const int32_t* state_idx = IDX ? a.state_idx : nullptr;
   float* inter = IDX ? a.inter : nullptr;
   const int32_t* inter_idx = IDX ? a.inter_idx : nullptr;
-  constexpr int TC = F32 ? 40 : kTC;  // rows staged per chunk
+  constexpr int TC = F32 ? kTCF32 : kTC;  // rows staged per chunk
   constexpr int Dk = KPL * kLanesPerV;
   constexpr int VPB = NW * kVPerWave;
   const int tiles = a.Dv / VPB;
@@ -212,6 +226,16 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
   };
 
   const int64_t col_off = ((int64_t)h * a.Dv + v) * Dk + kl * KPL;  // within one [Hv, Dv, Dk] state
+  // gated-norm outputs: thread e < T * VPB / 8 owns row e / (VPB / 8), 8 columns; its z and w pieces load
+  // with the first memory round trip
+  constexpr int GPR = VPB / 8 > 0 ? VPB / 8 : 1;  // 8-column pieces of a row of the tile
+  u32x4 gzr = u32x4{0u, 0u, 0u, 0u}, gwr = u32x4{0u, 0u, 0u, 0u};
+  const bool gown = F32 && a.gu && tid < T * GPR;
+  if (gown) {
+    const int gc = h * a.Dv + vt * VPB + (tid % GPR) * 8;  // first column within the z row / u row
+    gzr = *reinterpret_cast<const u32x4*>(a.gz + (row0 + tid / GPR) * a.gz_st + gc);
+    gwr = *reinterpret_cast<const u32x4*>(a.gw + vt * VPB + (tid % GPR) * 8);
+  }
   const int64_t hvk = (int64_t)a.Hv * a.Dv * Dk;
   const int64_t st_off = (state_idx ? state_idx[b] : b) * hvk + col_off;  // state_in / state_out
   const int64_t cl_off = (int64_t)b * hvk + col_off;                           // state_clean
@@ -662,6 +686,24 @@ __global__ __launch_bounds__(NW* kWave) void gdr_recurrent_kernel(RecArgs a) {
     for (int j = 0; j < 4; ++j)
       if (t + j < T && kl == 0) ob[(int64_t)(t + j) * v_row] = f2bf(o[j]);
   }
+  if (F32 && a.gu) {
+    __syncthreads();  // every row's readout is in s_ob (T <= one chunk)
+    if (gown) {
+      const int t = tid / GPR, pc = tid % GPR;
+      float zf[8], wf[8], u[8];
+      unpack8(gzr, zf);
+      unpack8(gwr, wf);
+      float ss = 0.f;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float o = bf2f(f2bf(s_ob[t][pc * 8 + c]));  // the bf16 output the norm reads
+        ss = fmaf(o, o, ss);
+        u[c] = o * wf[c] * (zf[c] / (1.f + __expf(-zf[c])));
+      }
+      *reinterpret_cast<u32x4*>(a.gu + ws_frag_off((int)(row0 + t), (int64_t)h * a.Dv + vt * VPB + pc * 8)) = pack8(u);
+      a.gss[((row0 + t) * a.Hv + h) * (a.Dv / 8) + vt * GPR + pc] = ss;
+    }
+  }
   if (a.state_out) {
 #pragma unroll
     for (int i = 0; i < KPL; ++i) a.state_out[st_off + i] = s[i];
@@ -688,12 +730,20 @@ template <int KPL, bool PREP = false>
 int launch_kpl(const RecArgs& a, int B, hipStream_t st) {
   // widest block whose v-tile divides Dv; more, narrower blocks when the grid would be small
   int nw = 4;
-  while (nw > 1 && (a.Dv % (nw * kVPerWave) != 0 || (int64_t)B * a.Hv * (a.Dv / (nw * kVPerWave)) < 256)) nw /= 2;
+  const int nw_min = a.gu ? 2 : 1;  // the gated-norm outputs take whole 8-column pieces
+  while (nw > nw_min && (a.Dv % (nw * kVPerWave) != 0 || (int64_t)B * a.Hv * (a.Dv / (nw * kVPerWave)) < 256)) nw /= 2;
   if (a.Dv % (nw * kVPerWave) != 0) return TRIDA_ERR_ARG;
   const unsigned grid = (unsigned)((int64_t)B * a.Hv * (a.Dv / (nw * kVPerWave)));
   // fp32 stages on grids of fewer than 1024 blocks (batch 1: 512), where a block's row chain is the
   // critical path and two blocks per CU already hold the grid
-  if (!PREP && a.bidir == 0 && grid < 1024)
+  const bool f32 = !PREP && a.bidir == 0 && grid < 1024;
+  // the gated-norm outputs: the fp32-stage form with one chunk, whole 8-column pieces, one per thread
+  if (a.gu && (!f32 || a.T > kTCF32 || (nw * kVPerWave) % 8 != 0 || a.T * (nw * kVPerWave / 8) > nw * kWave)) {
+    set_error("gdr_recurrent_gnorm: needs a grid of < 1024 blocks and T <= %d (got T=%d, %u blocks)", kTCF32, a.T,
+              grid);
+    return TRIDA_ERR_ARG;
+  }
+  if (f32)
     launch_nw<KPL, PREP, !PREP>(a, nw, grid, st);
   else
     launch_nw<KPL, PREP, false>(a, nw, grid, st);
@@ -732,6 +782,41 @@ extern "C" int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const u
   RecArgs a{q, k, v, g, beta, state_in, out, state_out, state_clean, (int)T, (int)Hk, (int)Hv, (int)Dk,
             (int)Dv, causal_mode, (int)num_clean, scale, 0, PrepIn{}, cu_seqlens, state_idx, inter, inter_idx,
             inter ? (int)cache_steps : 0};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (Dk) {
+    case 32: return launch_kpl<2>(a, (int)B, st);
+    case 64: return launch_kpl<4>(a, (int)B, st);
+    case 128: return launch_kpl<8>(a, (int)B, st);
+    default: return launch_kpl<16>(a, (int)B, st);
+  }
+}
+
+extern "C" int trida_gdr_recurrent_gnorm(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
+                                         const float* beta, const float* state_in, uint16_t* out, float* state_out,
+                                         float* state_clean, int64_t B, int64_t T, int64_t Hk, int64_t Hv, int64_t Dk,
+                                         int64_t Dv, int causal_mode, int64_t num_clean, float scale,
+                                         const uint16_t* z, int64_t z_row_stride, const uint16_t* gnorm_w,
+                                         uint16_t* u_frag, float* ss_parts, void* stream) {
+  TRIDA_CHECK(q && k && v && g && beta && state_in && out && z && gnorm_w && u_frag && ss_parts, TRIDA_ERR_NULL,
+              "gdr_recurrent_gnorm: q, k, v, g, beta, state_in, out, z, gnorm_w, u_frag and ss_parts are required");
+  TRIDA_CHECK(B > 0 && T > 0 && Hk > 0 && Hv > 0 && Hv % Hk == 0 && B * T <= 48, TRIDA_ERR_ARG,
+              "gdr_recurrent_gnorm: bad sizes B=%lld T=%lld Hk=%lld Hv=%lld (B T <= 48)", (long long)B, (long long)T,
+              (long long)Hk, (long long)Hv);
+  TRIDA_CHECK(Dk == 32 || Dk == 64 || Dk == 128 || Dk == 256, TRIDA_ERR_ARG,
+              "gdr_recurrent_gnorm: Dk must be 32, 64, 128 or 256 (got %lld)", (long long)Dk);
+  TRIDA_CHECK(Dv % 32 == 0, TRIDA_ERR_ARG, "gdr_recurrent_gnorm: Dv must be a multiple of 32");
+  TRIDA_CHECK(causal_mode == 1 || causal_mode == 2, TRIDA_ERR_ARG, "gdr_recurrent_gnorm: causal_mode is 1 or 2");
+  TRIDA_CHECK(num_clean >= 0, TRIDA_ERR_ARG, "gdr_recurrent_gnorm: num_clean >= 0");
+  TRIDA_CHECK(state_clean == nullptr || (state_clean != state_in && state_clean != state_out), TRIDA_ERR_ARG,
+              "gdr_recurrent_gnorm: state_clean must not alias state_in or state_out");
+  TRIDA_CHECK(((uintptr_t)q & 15) == 0 && ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 3) == 0 &&
+                  ((uintptr_t)z & 15) == 0 && z_row_stride % 8 == 0 && z_row_stride >= Hv * Dv &&
+                  ((uintptr_t)gnorm_w & 15) == 0 && ((uintptr_t)u_frag & 15) == 0 && ((uintptr_t)ss_parts & 3) == 0,
+              TRIDA_ERR_ALIGN, "gdr_recurrent_gnorm: q, k, z, gnorm_w and u_frag 16-byte aligned (z rows of >= Hv Dv "
+              "elements, a multiple of 8), v and ss_parts 4-byte aligned");
+  RecArgs a{q, k, v, g, beta, state_in, out, state_out, state_clean, (int)T, (int)Hk, (int)Hv, (int)Dk,
+            (int)Dv, causal_mode, (int)num_clean, scale, 0, PrepIn{}, nullptr, nullptr, nullptr, nullptr, 0,
+            z, z_row_stride, gnorm_w, u_frag, ss_parts};
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (Dk) {
     case 32: return launch_kpl<2>(a, (int)B, st);

@@ -20,7 +20,11 @@
 //     a 33-row canvas: 2.4 instead of 4.6 us per workgroup). The producers of the decode-step activations
 //     (trida_residual_parts_frag, trida_gated_rmsnorm_frag, this kernel's own epilogues) write that order;
 //   - K beyond NW * KWS steps is split over kg workgroup groups that write fp32 partial planes
-//     [kg][M][N]; trida_add_rmsnorm_parts (norms.hip) sums them in plane order.
+//     [kg][M][N]; trida_add_rmsnorm_parts (norms.hip) sums them in plane order;
+//   - per-head row scales (trida_wsgemm_headnorm, partial planes): when a wave's K slice is one head of X
+//     (KWS * 32 = the head width), its partial sums of a row are multiplied by rsqrt(mean of the row's head
+//     squares + eps) from per-piece sums of squares before they are parked: the gated RMSNorm of a GDN
+//     layer applied to X = o * w * silu(z) after the product instead of before it.
 // Epilogues: bf16 store, fp32 partials, SwiGLU (silu(gate) * up) over weights whose tiles interleave 8
 // gate rows with the matching 8 up rows, or argmax: the LM head of a greedy verify reduces each row of its
 // bf16 logits to the workgroup's (max, first index) in registers while the weights stream, and writes one
@@ -60,6 +64,10 @@ struct WsArgs {
   float* pval;  // argmax epilogue: [M][gridDim.x] best value of each row within each workgroup's columns
   int* pidx;    // and its column (first on ties, NaN first)
   float* psum;  // argmax + confidence: [M][gridDim.x] sum exp(x - pval) over the workgroup's columns
+  // per-head row scales: [M][h_heads][head width / 8] sums of squares of X's 8-column pieces, or null
+  const float* hss;
+  int h_heads;
+  float h_eps;
 };
 
 
@@ -125,6 +133,30 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
         if (m < a.M && j < my_steps)
           xs[j][mt] = *reinterpret_cast<const u32x4*>(a.X + (int64_t)m * a.x_st + s * 32 + (l / 16) * 8);
       }
+    }
+  }
+  // per-head row scales of this wave's head (K slice = one head): lane group l / 16 sums a quarter of the
+  // row's piece sums, two xor exchanges the rest
+  float hinv[MT];
+  const bool hscale = EPI == kParts && a.hss;  // the partial-plane kernels only
+  if (hscale) {
+    constexpr int P = KWS * 32 / 8;  // 8-column pieces of the head
+    const int head = min((int)blockIdx.y * NW + wave, a.h_heads - 1);
+    float hp[MT][P / 4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float* src = a.hss + ((int64_t)min(mt * 16 + (l % 16), a.M - 1) * a.h_heads + head) * P + (l / 16) * (P / 4);
+#pragma unroll
+      for (int j = 0; j < P / 4; ++j) hp[mt][j] = src[j];
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float q = 0.f;
+#pragma unroll
+      for (int j = 0; j < P / 4; ++j) q += hp[mt][j];
+      q += __shfl_xor(q, 16, kWave);
+      q += __shfl_xor(q, 32, kWave);
+      hinv[mt] = rsqrtf(q / (float)(KWS * 32) + a.h_eps);
     }
   }
   // Wait for the prologue's loads here: the first MFMA needs the last of them anyway (X was issued after
@@ -281,7 +313,7 @@ __global__ __launch_bounds__(NW* kWave) void wsgemm_kernel(WsArgs a) {
         const int slot = tl % NSLOT;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          red[slot][wave][mt][l] = acc[mt];
+          red[slot][wave][mt][l] = hscale ? acc[mt] * hinv[mt] : acc[mt];
           acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         if (slot == NSLOT - 1 || tl == nt - 1) flush(tl - slot, tl);
@@ -372,8 +404,10 @@ __global__ __launch_bounds__(256) void shuffle_kernel(const uint16_t* W, int64_t
 // ---------------------------------------------------------------- plans
 struct Cfg {
   int nw, kws;
+  bool head_only;  // only for per-head-scaled products whose heads are kws k-steps wide
 };
-constexpr Cfg kCfgs[] = {{8, 10}, {8, 5}, {8, 4}};  // 16-wave workgroups measured 10-15% slower
+// 16-wave workgroups measured 10-15% slower; {8, 2} serves heads of 64 columns (partial planes only)
+constexpr Cfg kCfgs[] = {{8, 10, false}, {8, 5, false}, {8, 4, false}, {8, 2, true}};
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 struct Plan {
@@ -386,11 +420,13 @@ struct Plan {
 // + 4 per k-step of X slice (its load precedes the stream, ~0.2 us each), + 6 per extra partial plane
 // (read again by its consumer: ~0.3 us per plane at 33 rows). Bf16 and SwiGLU epilogues need the whole K
 // in one workgroup (kg == 1); ties go to the thinner X slice.
-Plan plan_for(int64_t N, int64_t K, int epi) {
+// kws > 0: only the configuration whose waves take kws k-steps each (a head per wave).
+Plan plan_for(int64_t N, int64_t K, int epi, int kws = 0) {
   const int64_t tiles = N / 16, nsteps = K / 32;
   Plan best{-1, 0, 0};
   int64_t best_cost = INT64_MAX;
   for (int c = 0; c < kNumCfgs; ++c) {
+    if (kws > 0 ? kCfgs[c].kws != kws : kCfgs[c].head_only) continue;
     const int64_t per = (int64_t)kCfgs[c].nw * kCfgs[c].kws;
     const int64_t kg = cdiv(nsteps, per);
     if (epi != kParts && kg != 1) continue;
@@ -424,7 +460,10 @@ void launch_cfg(const WsArgs& a, const Plan& p, hipStream_t st) {
   switch (p.cfg) {
     case 0: launch_mt<8, 10, 10, EPI, NORM>(a, p.kg, st); break;
     case 1: launch_mt<8, 5, 10, EPI, NORM>(a, p.kg, st); break;
-    default: launch_mt<8, 4, 8, EPI, NORM>(a, p.kg, st); break;
+    case 2: launch_mt<8, 4, 8, EPI, NORM>(a, p.kg, st); break;
+    default:
+      if constexpr (EPI == kParts && !NORM) launch_mt<8, 2, 10, EPI, NORM>(a, p.kg, st);
+      break;
   }
 }
 
@@ -604,6 +643,41 @@ extern "C" int trida_wsgemm_argmax(const uint16_t* X, int64_t x_row_stride, cons
                                    int32_t* pidx, void* stream) {
   return ws_run("wsgemm_argmax", X, x_row_stride, nullptr, 0.f, Wp, M, N, K, kArgmax, logits, out_row_stride, flags,
                 stream, pval, pidx);
+}
+
+// the configuration of a per-head-scaled product: every wave's K slice one head of K / heads columns
+int headnorm_plan(int64_t N, int64_t K, int64_t heads, Plan* p) {
+  TRIDA_CHECK(heads > 0 && K % heads == 0 && (K / heads) % 32 == 0 && shape_ok(N, K, kParts), TRIDA_ERR_ARG,
+              "wsgemm_headnorm: need N %% 16 == 0 and heads of a multiple of 32 columns (N=%lld K=%lld heads=%lld)",
+              (long long)N, (long long)K, (long long)heads);
+  *p = plan_for(N, K, kParts, (int)(K / heads / 32));
+  TRIDA_CHECK(p->cfg >= 0, TRIDA_ERR_ARG, "wsgemm_headnorm: no plan takes heads of %lld columns",
+              (long long)(K / heads));
+  return TRIDA_OK;
+}
+
+extern "C" int trida_wsgemm_headnorm_planes(int64_t N, int64_t K, int64_t heads, int32_t* kgroups) {
+  TRIDA_CHECK(kgroups, TRIDA_ERR_NULL, "wsgemm_headnorm_planes: kgroups is required");
+  Plan p;
+  const int rc = headnorm_plan(N, K, heads, &p);
+  if (rc != TRIDA_OK) return rc;
+  *kgroups = p.kg;
+  return TRIDA_OK;
+}
+
+extern "C" int trida_wsgemm_headnorm(const uint16_t* Xf, const uint16_t* Wp, int64_t M, int64_t N, int64_t K,
+                                     const float* ss_parts, int64_t heads, float eps, float* parts, void* stream) {
+  TRIDA_CHECK(Xf && Wp && ss_parts && parts, TRIDA_ERR_NULL, "wsgemm_headnorm: Xf, Wp, ss_parts and parts are required");
+  TRIDA_CHECK(M >= 1 && M <= kMaxM, TRIDA_ERR_ARG, "wsgemm_headnorm: need 1 <= M <= %d", kMaxM);
+  TRIDA_CHECK(((((uintptr_t)Xf) | (uintptr_t)Wp | (uintptr_t)parts) & 15) == 0 && ((uintptr_t)ss_parts & 3) == 0,
+              TRIDA_ERR_ALIGN, "wsgemm_headnorm: Xf, Wp and parts 16-byte aligned, ss_parts 4-byte aligned");
+  Plan p;
+  const int rc = headnorm_plan(N, K, heads, &p);
+  if (rc != TRIDA_OK) return rc;
+  WsArgs a{Xf, reinterpret_cast<const u32x4*>(Wp), parts, 0, 0, (int)M, (int)N, (int)K, p.T, nullptr, 0.f, 1, 0,
+           nullptr, nullptr, nullptr, ss_parts, (int)heads, eps};
+  launch_cfg<kParts, false>(a, p, static_cast<hipStream_t>(stream));
+  return launch_status("wsgemm_headnorm");
 }
 
 extern "C" int trida_wsgemm_argmax_conf(const uint16_t* X, int64_t x_row_stride, const uint16_t* Wp, int64_t M,

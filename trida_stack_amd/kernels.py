@@ -640,6 +640,52 @@ def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
     return out, clean
 
 
+def gdr_recurrent_gnorm(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+                        state: torch.Tensor, z: torch.Tensor, gnorm_w: torch.Tensor, u_frag: torch.Tensor,
+                        ss_parts: torch.Tensor, *, causal_mode: int = 1, num_clean: Optional[int] = None,
+                        state_out: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+                        out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """gdr_recurrent (contiguous form, B * T <= 48, T <= 40) that also leaves the gated RMSNorm's inputs for
+    ws_gemm_headnorm: u_frag (ws_frag_numel(Hv * Dv) bf16) = bf16(bf16(o) * gnorm_w * silu(z)) in fragment
+    order and ss_parts fp32 [B * T, Hv, Dv / 8] = the sums of bf16(o)^2 over each 8 columns. z [B * T,
+    >= Hv * Dv] bf16 with contiguous rows; gnorm_w [Dv] bf16. Returns out [B, T, Hv, Dv] bf16 (o)."""
+    dev = _need_gpu(q, k, v, g, beta, state, z, gnorm_w, u_frag, ss_parts, state_out, out)
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (gnorm_w, "gnorm_w")):
+        _bf16(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    for t, n in ((g, "g"), (beta, "beta"), (state, "state"), (ss_parts, "ss_parts")):
+        _f32(t, n)
+        if not t.is_contiguous():
+            raise ValueError(f"{n} must be contiguous")
+    B, T, Hk, Dk = k.shape
+    Hv, Dv = v.shape[-2:]
+    if q.shape != k.shape or v.shape[:2] != (B, T) or g.shape != (B, T, Hv) or beta.shape != g.shape \
+            or state.shape != (B, Hv, Dv, Dk):
+        raise ValueError("q/k/v/g/beta/state shapes disagree")
+    _bf16(z, "z")
+    if z.dim() != 2 or z.shape[0] != B * T or z.shape[1] < Hv * Dv or z.stride(1) != 1 or gnorm_w.numel() != Dv:
+        raise ValueError("gdr_recurrent_gnorm: z [B T, >= Hv Dv] with contiguous rows and gnorm_w [Dv]")
+    _frag_buf(u_frag, Hv * Dv, "u_frag")
+    if ss_parts.numel() < B * T * Hv * (Dv // 8):
+        raise ValueError("gdr_recurrent_gnorm: ss_parts needs B T Hv Dv / 8 floats")
+    if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
+                                  or not state_out.is_contiguous()):
+        raise ValueError("state_out must match state")
+    if out is None:
+        out = torch.empty(B, T, Hv, Dv, dtype=torch.bfloat16, device=dev)
+    elif out.shape != (B, T, Hv, Dv) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError("gdr_recurrent_gnorm: out must be contiguous bf16 like v")
+    nc = T if num_clean is None else int(num_clean)
+    sc = Dk ** -0.5 if scale is None else float(scale)
+    rc = _lib.load().trida_gdr_recurrent_gnorm(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), state.data_ptr(), out.data_ptr(),
+        _ptr(state_out), None, B, T, Hk, Hv, Dk, Dv, causal_mode, nc, sc, z.data_ptr(), z.stride(0),
+        gnorm_w.data_ptr(), u_frag.data_ptr(), ss_parts.data_ptr(), _stream(dev))
+    _lib.check(rc, "trida_gdr_recurrent_gnorm")
+    return out
+
+
 def gdn_fused_layer(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
                     A_log: torch.Tensor, dt_bias: torch.Tensor, state: torch.Tensor, *, Hk: int, Hv: int, Dk: int,
                     Dv: int, causal_mode: int = 1, num_clean: Optional[int] = None,
@@ -1211,6 +1257,36 @@ def ws_gemm_frag(xf: torch.Tensor, M: int, wp: torch.Tensor, N: int, out: torch.
                                      out.data_ptr(), o_st, flags, _stream(dev))
     _lib.check(rc, "trida_wsgemm_ex")
     return out
+
+
+def ws_headnorm_planes(N: int, Kd: int, heads: int) -> int:
+    """Partial planes ws_gemm_headnorm writes for an [N, K] weight over `heads` heads of X."""
+    kg = ctypes.c_int32(0)
+    rc = _lib.load().trida_wsgemm_headnorm_planes(N, Kd, heads, ctypes.byref(kg))
+    _lib.check(rc, "trida_wsgemm_headnorm_planes")
+    return kg.value
+
+
+def ws_gemm_headnorm(uf: torch.Tensor, M: int, wp: torch.Tensor, N: int, ss_parts: torch.Tensor, heads: int,
+                     out: torch.Tensor, *, eps: float = 1e-6) -> int:
+    """Partial planes (fp32 [kg, M, N], kg = ws_headnorm_planes) of the M rows of u in fragment order (uf, from
+    gdr_recurrent_gnorm) times the ws_shuffle'd weight, each head's partial sums of a row scaled by
+    rsqrt(sum of the row's ss_parts of that head / head width + eps): the out projection of the gated
+    RMSNorm's output. Returns kg."""
+    dev = _need_gpu(uf, wp, ss_parts, out)
+    Kd = wp.numel() // N
+    _frag_buf(uf, Kd, "uf")
+    kg = ws_headnorm_planes(N, Kd, heads)
+    if ss_parts.dtype != torch.float32 or not ss_parts.is_contiguous() or ss_parts.numel() < M * Kd // 8:
+        raise ValueError("ws_gemm_headnorm: ss_parts must be contiguous fp32 [M, heads, K / heads / 8]")
+    if out.dtype != torch.float32 or not out.is_contiguous() or out.numel() < kg * M * N:
+        raise ValueError(f"ws_gemm_headnorm: out must be contiguous fp32 of >= {kg} x {M} x {N}")
+    if not 1 <= M <= WS_MAX_M:
+        raise ValueError(f"ws_gemm_headnorm: need 1 <= M <= {WS_MAX_M}")
+    rc = _lib.load().trida_wsgemm_headnorm(uf.data_ptr(), wp.data_ptr(), M, N, Kd, ss_parts.data_ptr(), heads, eps,
+                                           out.data_ptr(), _stream(dev))
+    _lib.check(rc, "trida_wsgemm_headnorm")
+    return kg
 
 
 def ws_gemm_norm(h: torch.Tensor, ss: torch.Tensor, wp: torch.Tensor, N: int, out: torch.Tensor, *,

@@ -234,6 +234,10 @@ class _Scratch:
         self.actf = torch.empty(K.ws_frag_numel(cfg.intermediate), **bf) if frag else None
         self.ynf = torch.empty(K.ws_frag_numel(cfg.lin_v_heads * cfg.lin_v_dim), **bf) if frag else None
         self.oattf = torch.empty(K.ws_frag_numel(cfg.n_heads * cfg.head_dim), **bf) if frag else None
+        # the gated RMSNorm's per-8-column sums of squares of the GDN output, when the recurrence leaves them
+        # for the out projection (gdr_recurrent_gnorm)
+        self.gss = (torch.empty(N * cfg.lin_v_heads * max(1, cfg.lin_v_dim // 8), **f32)
+                    if frag and cfg.lin_v_dim % 32 == 0 else None)
 
 
 GEMM_CHOICES = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_choices_gfx950.csv")
@@ -382,6 +386,8 @@ class TridaRuntime:
             self.ws[key] = (wp, wt.shape[0], role, kg)
             if role == K.WS_PARTS:
                 self.ws_parts = max(self.ws_parts, kg)
+            if name == "w_out" and c.lin_v_dim % 32 == 0:  # the gated-norm fold's projection (ws_gemm_headnorm)
+                self.ws_parts = max(self.ws_parts, K.ws_headnorm_planes(wt.shape[0], wt.shape[1], c.lin_v_heads))
         # the LM head (bf16 logits of <= K.WS_MAX_M rows; the fp32 logits_out path keeps hipBLASLt)
         wl = self.w.get("lm_head", self.w.get("embed"))
         if wl is not None and wl.shape[0] % 16 == 0 and wl.shape[1] % 32 == 0:
@@ -406,6 +412,10 @@ class TridaRuntime:
     # recurrence block would redo its head's q/k front half (16x at batch 1), which measures slower
     # than the separate prep launch (27 vs 23 us per layer at batch 1, 407 vs 236 us at batch 64).
     fused_gdn = False
+    # in the fused forward (<= K.WS_MAX_M rows, one staged chunk of recurrence rows), the GDN layer's gated
+    # RMSNorm runs inside the recurrence (u = o * w * silu(z) and per-head sums of squares) and the out
+    # projection (its per-head rsqrt scale on the partial sums): no gated_rmsnorm launch between them
+    fold_gnorm = True
     # fn(i, where, *tensors) or None, for tests that check each layer on its own inputs (never set while a
     # forward is captured into a graph); called in eager forwards with device tensors:
     #   (i, "in", h, r)     the hidden rows [B * T, hidden] (bf16) entering layer i (i = n_layers: the
@@ -594,6 +604,11 @@ class TridaRuntime:
                 rec = (s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j])
                 chunked = self._chunked_gdr(T, gdn_mode, B, persist)
                 keep = mode != "draft"  # a draft pass is never committed
+                z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
+                # the gated RMSNorm folded into the recurrence and the out projection (fused forward, one
+                # staged chunk of rows)
+                fold = (fused and self.fold_gnorm and s.gss is not None and not chunked and not self.fused_gdn
+                        and T <= 40)
                 if not chunked and self.fused_gdn and T <= 64 and c.lin_k_dim in (32, 64, 128):
                     with K.timed("gdn_fused"):
                         K.gdn_fused_layer(xv, window[j], w[p + "conv_w"], a_in, b_in, w[p + "A_log"],
@@ -614,6 +629,11 @@ class TridaRuntime:
                             K.gdr_chunk(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
                                         causal_mode=gdn_mode, num_clean=nc, state_out=state[j] if persist else None,
                                         out=s.y)
+                    elif fold:
+                        with K.timed("gdr_recurrent"):
+                            K.gdr_recurrent_gnorm(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
+                                                  z, w[p + "gnorm"], s.ynf, s.gss, causal_mode=gdn_mode,
+                                                  num_clean=nc, state_out=state[j] if persist else None, out=s.y)
                     else:
                         with K.timed("gdr_recurrent"):
                             K.gdr_recurrent(s.q, s.k_rec[j], s.v_rec[j], s.g_rec[j], s.b_rec[j], state[j],
@@ -623,8 +643,12 @@ class TridaRuntime:
                     window[j].copy_(s.win_tmp)
                 if probe is not None:
                     probe(i, "gdn", s.proj, s.y)
-                z = s.proj.view(N, -1)[:, c.conv_dim: c.conv_dim + c.value_dim]
-                if fused:  # straight into the out projection's fragment-order X
+                if fold:  # the recurrence left u and the sums of squares: the projection applies the norm
+                    wp, Nout, _, _ = self.ws[p + "w_out"]
+                    with K.timed("ws_gemm"):
+                        kg = K.ws_gemm_headnorm(s.ynf, N, wp, Nout, s.gss, c.lin_v_heads, s.parts, eps=c.rms_eps)
+                    pending = ("parts", kg)
+                elif fused:  # straight into the out projection's fragment-order X
                     K.gated_rmsnorm(s.y.view(N, c.lin_v_heads, c.lin_v_dim), z, w[p + "gnorm"], s.ynf,
                                     eps=c.rms_eps, out_frag=True)
                     pending = self._proj(s, p + "w_out", s.yn_p[:N], s.yn_p, s.r_p, xf=s.ynf)
