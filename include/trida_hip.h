@@ -277,6 +277,10 @@ int trida_gdn_prep(const uint16_t* x, const uint16_t* window, const uint16_t* co
  *     cu_seqlens[b + 1] - 1 of q, k, v, g, beta and out ([total, ...]); num_clean counts from each
  *     sequence's first row; T is an upper bound of every sequence's rows (rows past T are not
  *     processed).
+ * The index vectors and cu_seqlens (here and in trida_gdn_prep / trida_gdn_fused_layer) are read on the
+ * device as given, as the reference's kernels read theirs: an entry outside [0, rows) of its pool, or a
+ * cu_seqlens past the packed tensors, addresses memory outside them. The Python wrappers check them on
+ * the host before the launch whenever the stream is not being captured.
  */
 int trida_gdr_recurrent(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g,
                         const float* beta, const float* state_in, uint16_t* out, float* state_out,

@@ -223,3 +223,47 @@ def test_window_rebuild_over_layer_pools(gpu):
                         preconv=bf(pre).view(L * (R + 1), blk, C), win_idx=win_idx, pre_idx=pre_idx, slots=L * n)
     torch.cuda.synchronize()
     assert torch.equal(wc_d.cpu().float(), want)
+
+
+def test_out_of_range_indices_are_refused_before_launch(gpu):
+    """Pool / ring indices and cu_seqlens that would address memory outside their buffers raise on the host
+    (the wrappers read them back outside graph capture); nothing is launched, the pools stay untouched."""
+    g0 = torch.Generator().manual_seed(11)
+    Hk, Hv, Dk, Dv, T = 2, 4, 32, 64, 5
+    C = 2 * Hk * Dk + Hv * Dv
+    x = bf(torch.randn(2, T, C, generator=g0))
+    ab = bf(torch.randn(2, T, Hv, generator=g0))
+    conv_w = bf(torch.randn(C, 4, generator=g0) * 0.3)
+    A_log = torch.zeros(Hv, device=DEV)
+    dt = torch.zeros(Hv, device=DEV)
+    pool = bf(torch.randn(3, 3, C, generator=g0))
+    before = pool.clone()
+    with pytest.raises(ValueError, match="win_idx"):
+        kernels.gdn_prep(x, pool, conv_w, ab, ab, A_log, dt, Hk=Hk, Hv=Hv, Dk=Dk, Dv=Dv, win_idx=i32([0, 3]))
+    with pytest.raises(ValueError, match="win_idx"):
+        kernels.gdn_prep(x, pool, conv_w, ab, ab, A_log, dt, Hk=Hk, Hv=Hv, Dk=Dk, Dv=Dv, win_idx=i32([-1, 1]))
+    assert torch.equal(pool, before)
+    q = bf(torch.randn(2, T, Hk, Dk, generator=g0))
+    v = bf(torch.randn(2, T, Hv, Dv, generator=g0))
+    gl = -torch.rand(2, T, Hv, generator=g0).to(DEV)
+    beta = torch.rand(2, T, Hv, generator=g0).to(DEV)
+    states = torch.randn(3, Hv, Dv, Dk, generator=g0).to(DEV)
+    s_before = states.clone()
+    with pytest.raises(ValueError, match="state_idx"):
+        kernels.gdr_recurrent(q, q, v, gl, beta, states, state_idx=i32([1, 5]))
+    with pytest.raises(ValueError, match="distinct"):  # written in place: two sequences on one pool row
+        kernels.gdr_recurrent(q, q, v, gl, beta, states, state_out=states, state_idx=i32([2, 2]))
+    ring = torch.zeros(2, 3, Hv, Dv, Dk, device=DEV)
+    with pytest.raises(ValueError, match="inter_idx"):
+        kernels.gdr_recurrent(q, q, v, gl, beta, states, state_idx=i32([0, 1]), inter=ring, inter_idx=i32([0, 2]))
+    qp, vp = q.view(2 * T, Hk, Dk), v.view(2 * T, Hv, Dv)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        kernels.gdr_recurrent(qp, qp, vp, gl.view(2 * T, Hv), beta.view(2 * T, Hv), states[:2],
+                              cu_seqlens=i32([0, 6, 2 * T + 1]), max_rows=T + 1)
+    with pytest.raises(ValueError, match="cu_seqlens"):
+        kernels.gdr_recurrent(qp, qp, vp, gl.view(2 * T, Hv), beta.view(2 * T, Hv), states[:2],
+                              cu_seqlens=i32([0, 7, 6]), max_rows=T + 2)
+    assert torch.equal(states, s_before) and torch.equal(ring, torch.zeros_like(ring))
+    # in range, the same calls run
+    out, _ = kernels.gdr_recurrent(q, q, v, gl, beta, states, state_idx=i32([2, 0]))
+    assert torch.isfinite(out.float()).all()

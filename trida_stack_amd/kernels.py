@@ -475,6 +475,34 @@ def _packed(cu_seqlens: Optional[torch.Tensor], max_rows: Optional[int]):
     return cu_seqlens.numel() - 1, int(max_rows)
 
 
+# The kernels take the pool / ring indices and cu_seqlens as given (as the reference's kernels do): an entry
+# out of range would address memory outside the pools. Outside graph capture the wrappers read them back
+# (one small device-to-host copy) and refuse such entries before any launch; under capture they are trusted.
+def _checkable(t: Optional[torch.Tensor]) -> bool:
+    return t is not None and t.numel() > 0 and not torch.cuda.is_current_stream_capturing()
+
+
+def _idx_range(idx: Optional[torch.Tensor], rows: int, name: str, distinct: bool = False) -> None:
+    """Every entry of the index vector in [0, rows) (and pairwise distinct when asked)."""
+    if not _checkable(idx):
+        return
+    v = idx.cpu()
+    lo, hi = int(v.min()), int(v.max())
+    if lo < 0 or hi >= rows:
+        raise ValueError(f"{name}: entries must lie in [0, {rows}) (got {lo} .. {hi})")
+    if distinct and torch.unique(v).numel() != v.numel():
+        raise ValueError(f"{name}: entries must be distinct when the pool is written in place")
+
+
+def _seqlens_range(cu_seqlens: Optional[torch.Tensor], total: int) -> None:
+    """cu_seqlens starts at >= 0, never decreases and ends within the total rows of the packed tensors."""
+    if not _checkable(cu_seqlens):
+        return
+    v = cu_seqlens.cpu().long()
+    if int(v[0]) < 0 or int(v[-1]) > total or bool((v[1:] < v[:-1]).any()):
+        raise ValueError(f"cu_seqlens must be non-decreasing within [0, {total}] (got {v.tolist()[:8]} ...)")
+
+
 def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
              A_log: torch.Tensor, dt_bias: torch.Tensor, *, Hk: int, Hv: int, Dk: int, Dv: int,
              window_out: Optional[torch.Tensor] = None, pre_out: Optional[torch.Tensor] = None, out=None,
@@ -537,6 +565,11 @@ def gdn_prep(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor, a: tor
         slots = pre_out.shape[0] if pre_idx is not None else B
         if pre_out.shape != (slots, T, C) or not pre_out.is_contiguous() or pre_out.data_ptr() == x.data_ptr():
             raise ValueError("pre_out must be a separate contiguous [B (or pool slots), T, C] buffer")
+    _idx_range(win_idx, min(win_rows, window_out.shape[0]) if window_out is not None else win_rows, "win_idx")
+    if pre_out is not None:
+        _idx_range(pre_idx, pre_out.shape[0], "pre_idx")
+    if packed:
+        _seqlens_range(cu_seqlens, lead[0])
     if out is None:
         q = torch.empty(lead + (Hk, Dk), dtype=torch.bfloat16, device=dev)
         k = torch.empty_like(q)
@@ -625,6 +658,12 @@ def gdr_recurrent(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Te
                                   or not state_out.is_contiguous()):
         raise ValueError("state_out must match state")
     steps = _ring(inter, inter_idx, cache_steps, B, Hv, Dv, Dk)
+    _idx_range(state_idx, state.shape[0], "state_idx",
+               distinct=state_out is not None and state_out.data_ptr() == state.data_ptr())
+    if inter is not None:
+        _idx_range(inter_idx, inter.shape[0], "inter_idx")
+    if cu_seqlens is not None:
+        _seqlens_range(cu_seqlens, lead[0])
     nc = T if num_clean is None else int(num_clean)
     if out is None:
         out = torch.empty(lead + (Hv, Dv), dtype=torch.bfloat16, device=dev)
@@ -738,6 +777,13 @@ def gdn_fused_layer(x: torch.Tensor, window: torch.Tensor, conv_w: torch.Tensor,
         slots = pre_out.shape[0] if pre_idx is not None else B
         if pre_out.shape != (slots, T, C) or pre_out.dtype != torch.bfloat16 or not pre_out.is_contiguous():
             raise ValueError("pre_out must be contiguous bf16 [B (or pool slots), T, C]")
+    _idx_range(win_idx, min(win_rows, window_out.shape[0]) if window_out is not None else win_rows, "win_idx")
+    if pre_out is not None:
+        _idx_range(pre_idx, pre_out.shape[0], "pre_idx")
+    _idx_range(state_idx, state.shape[0], "state_idx",
+               distinct=state_out is not None and state_out.data_ptr() == state.data_ptr())
+    if inter is not None:
+        _idx_range(inter_idx, inter.shape[0], "inter_idx")
     kr = vr = gr = br = None
     if rows_out is not None:
         kr, vr, gr, br = rows_out
@@ -835,6 +881,10 @@ def gdr_chunk(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor, g: to
     if state_out is not None and (state_out.shape != state.shape or state_out.dtype != torch.float32
                                   or not state_out.is_contiguous()):
         raise ValueError("state_out must match state")
+    _idx_range(state_idx, state.shape[0], "state_idx",
+               distinct=state_out is not None and state_out.data_ptr() == state.data_ptr())
+    if cu_seqlens is not None:
+        _seqlens_range(cu_seqlens, lead[0])
     seq_mod = 0
     if n_keep is not None:
         if n_keep.dtype != torch.int32 or n_keep.dim() != 1 or not n_keep.is_contiguous() or B % n_keep.shape[0]:
@@ -935,6 +985,8 @@ def gdn_restore(n_keep: torch.Tensor, *, snap_state: Optional[torch.Tensor] = No
                 or (win_idx is None and window.shape[0] != NB) or (pre_idx is None and preconv.shape[0] != NB) \
                 or preconv.shape[2] != C or preconv.shape[1] != T or preconv.stride(2) != 1:
             raise ValueError("restore: window / preconv shapes disagree")
+        _idx_range(win_idx, min(window.shape[0], snap_window.shape[0]), "win_idx")
+        _idx_range(pre_idx, preconv.shape[0], "pre_idx")
         x_sb, x_st = preconv.stride(0), preconv.stride(1)
     if NB == 0 or NB % seq_mod:
         raise ValueError("restore: nothing to do or slots not a multiple of len(n_keep)")
