@@ -66,13 +66,28 @@ struct AttnArgs {
 };
 
 // LDS tiles of one 64-key step, 16-byte groups XOR-swizzled so that both the staging writes and the
-// MFMA fragment reads touch 8 distinct bank groups per 8 lanes:
-//   K   [key][D]   group g of key k stored at g ^ (k & 7)
-//   V^T [d][key]   group g of column d stored at g ^ (d & 7); the keys of a row in the slot order of the
-//                  P V^T product: group 4 kk + g holds keys 32 kk + 4 g .. + 3, then 32 kk + 16 + 4 g .. + 3
+// MFMA fragment reads touch distinct bank groups:
+//   K [key][D]   group g of key k stored at g ^ (k & 7) (16-byte fragment reads, 8 keys per 8 lanes)
+//   V [key][D + 16] row-major, rows padded by 32 bytes: the V^T fragments of the P V^T product come from
+//                ds_read_b64_tr_b16 (8 bytes of one key per lane, handed out transposed), and the 32 lanes
+//                of a half-wave, 8 keys x 32 bytes, then fall on distinct banks; a fragment's address is
+//                linear in its column tile (immediate offsets)
 template <int D>
 __device__ __forceinline__ int k_off(int key, int grp) { return key * D + ((grp ^ (key & 7)) << 3); }
-__device__ __forceinline__ int vt_off(int d, int kgrp) { return d * kKB + ((kgrp ^ (d & 7)) << 3); }
+constexpr int kVPad = 16;
+template <int D>
+__device__ __forceinline__ int v_off(int key, int grp) { return key * (D + kVPad) + (grp << 3); }
+// ds_read_b64_tr_b16 (gfx950): in each group of 16 lanes, lane 4 a + b receives element b of the 8-byte
+// reads of lanes a, a + 4, a + 8 and a + 12 (in that order). A lane of group g reading key key0 + 4 g +
+// (lane % 16) / 4 at columns d0 + 4 (lane % 4) .. + 3 thus receives V[key0 + 4 g + j][d0 + lane % 16] for
+// j = 0..3: four keys of its V^T row, in the k slots of the MFMA's A operand.
+template <int D>
+__device__ __forceinline__ s16x4 vt_frag4(const uint16_t* sV, int key0, int d0, int l) {
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const int key = key0 + 4 * (l / 16) + (l % 16) / 4, col = d0 + 4 * (l % 4);
+  const uint16_t* p = sV + v_off<D>(key, col / 8) + col % 8;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uint32_t)(uintptr_t)p);
+}
 
 // Workgroup = (sequence, KV head, query tile of kMT rows, key split); 8 waves, wave w owns rows
 // [16 w, 16 w + 16) of the tile. Per 64-key step: K and V^T are staged in LDS (the next step's K / V
@@ -96,12 +111,11 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   constexpr int GPR = D / 8;         // 16-byte groups per K row
   constexpr int NT = kNW * kWave;
   constexpr int NKG = kKB * GPR / NT;  // K groups staged per thread
-  constexpr int NVP = (kKB / 8) * (D / 4);  // V pieces of 8 keys x 4 columns per step
   constexpr int XH = CT / 2;  // O^T column tiles of the extra rows per wave (half of them)
   __shared__ __align__(16) uint16_t sQ[kMT * D];  // [row][D], groups swizzled by row & 7 (as K)
   __shared__ __align__(16) uint16_t sQx[kWR * D];  // the extra rows, the same layout
   __shared__ __align__(16) uint16_t sK[kKB * D];
-  __shared__ __align__(16) uint16_t sVt[D * kKB];
+  __shared__ __align__(16) uint16_t sV[kKB * (D + kVPad)];
   __shared__ float sXm[kNW][kWR], sXl[kNW][kWR];  // the extra rows' per-wave running max and sum
 
   const int tid = threadIdx.x, w = tid / kWave, l = tid % kWave;
@@ -173,10 +187,8 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
   const uint16_t* kh = a.k_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
   const uint16_t* vh = a.v_cache + ((int64_t)b * a.Hkv + hk) * a.Lmax * D;
 
-  // ---- prefetch registers: K groups (coalesced rows) and one V piece (8 keys x 4 columns)
-  u32x4 kreg[NKG];
-  u32x2 vreg[8];
-  const int vp_kg = tid % 8, vp_cq = tid / 8;  // V piece: keys vp_kg*8.., columns vp_cq*4..
+  // ---- prefetch registers: K and V groups (coalesced rows)
+  u32x4 kreg[NKG], vreg[NKG];
   auto load_step = [&](int kb) {
     const int key0 = kb * kKB;
 #pragma unroll
@@ -184,13 +196,7 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
       const int gi = tid + j * NT;
       const int key = min(key0 + gi / GPR, nk - 1);
       kreg[j] = *reinterpret_cast<const u32x4*>(kh + (int64_t)key * D + (gi % GPR) * 8);
-    }
-    if (tid < NVP) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int key = min(key0 + vp_kg * 8 + j, nk - 1);
-        vreg[j] = *reinterpret_cast<const u32x2*>(vh + (int64_t)key * D + vp_cq * 4);
-      }
+      vreg[j] = *reinterpret_cast<const u32x4*>(vh + (int64_t)key * D + (gi % GPR) * 8);
     }
   };
   // the first step's K / V loads go out with the Q loads: one memory latency for both
@@ -227,24 +233,7 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
     for (int j = 0; j < NKG; ++j) {
       const int gi = tid + j * NT;
       *reinterpret_cast<u32x4*>(&sK[k_off<D>(gi / GPR, gi % GPR)]) = kreg[j];
-    }
-    if (tid < NVP) {
-      const uint32_t* rw = reinterpret_cast<const uint32_t*>(vreg);
-      // keys 8 a .. + 3 and 8 a + 4 .. + 7 (a = vp_kg) are the halves (a % 4) / 2 of groups 4 (a / 4) +
-      // 2 (a % 2) and that + 1
-      const int grp = 4 * (vp_kg / 4) + 2 * (vp_kg % 2), half = 4 * ((vp_kg % 4) / 2);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {  // column vp_cq*4 + c: element c of each of the 8 key rows
-        uint32_t e[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint32_t word = rw[j * 2 + c / 2];
-          e[j] = (c & 1) ? (word >> 16) : (word & 0xffffu);
-        }
-        const int d = vp_cq * 4 + c;
-        *reinterpret_cast<u32x2*>(&sVt[vt_off(d, grp) + half]) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
-        *reinterpret_cast<u32x2*>(&sVt[vt_off(d, grp + 1) + half]) = u32x2{e[4] | (e[5] << 16), e[6] | (e[7] << 16)};
-      }
+      *reinterpret_cast<u32x4*>(&sV[v_off<D>(gi / GPR, gi % GPR)]) = vreg[j];
     }
   };
 
@@ -349,12 +338,10 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
         for (int e = 0; e < 4; ++e) ox[j][e] *= alpha;
     }
     const s16x4 pf = __builtin_bit_cast(s16x4, u32x2{f2bf2(p[0], p[1]), f2bf2(p[2], p[3])});
-    // V^T row d, keys 16 ktx + g4 .. + 3: the first (ktx even) or second half of group 4 (ktx / 2) + l / 16
+    // V^T row (dh XH + j) 16 + l % 16, keys 16 ktx + g4 .. + 3
 #pragma unroll
     for (int j = 0; j < XH; ++j) {
-      const int d = (dh * XH + j) * 16 + (l % 16);
-      const s16x4 vf = __builtin_bit_cast(
-          s16x4, *reinterpret_cast<const u32x2*>(&sVt[vt_off(d, 4 * (ktx / 2) + l / 16) + 4 * (ktx % 2)]));
+      const s16x4 vf = vt_frag4<D>(sV, 16 * ktx, (dh * XH + j) * 16, l);
       ox[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vf, pf, ox[j], 0, 0, 0);
     }
   };
@@ -398,13 +385,16 @@ __global__ __launch_bounds__(kNW* kWave) void attn_partial_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[ct][e] *= alpha;
     }
-    // ---- O^T += V^T P^T (V^T fragments from LDS, in the slot order of the probabilities)
+    // ---- O^T += V^T P^T (V^T fragments by transposed LDS reads, in the slot order of the probabilities:
+    // keys 32 kk + g4 .. + 3, then 32 kk + 16 + g4 .. + 3)
 #pragma unroll
     for (int kk = 0; kk < kKB / 32; ++kk) {
       const bf16x8 pf = as_bf16x8(pb[kk]);
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        const bf16x8 vf = as_bf16x8(*reinterpret_cast<const u32x4*>(&sVt[vt_off(ct * 16 + (l % 16), kk * 4 + l / 16)]));
+        const s16x4 v0 = vt_frag4<D>(sV, 32 * kk, ct * 16, l), v1 = vt_frag4<D>(sV, 32 * kk + 16, ct * 16, l);
+        const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+        const bf16x8 vf = as_bf16x8(u32x4{w0.x, w0.y, w1.x, w1.y});
         o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[ct], 0, 0, 0);
       }
     }
