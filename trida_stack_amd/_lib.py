@@ -80,6 +80,7 @@ SIGNATURES = {
     "trida_gdn_snapshot": (C.c_int, [P, P, I64, P, P, I64, P]),
     "trida_gdn_restore": (C.c_int, [P] * 10 + [I64] * 11 + [C.c_int, P, P, P]),
     "trida_attn_canvas_scratch_bytes": (I64, [I64] * 7),
+    "trida_attn_set_combine_general": (C.c_int, [C.c_int]),
     "trida_attn_canvas": (C.c_int, [P, P, P, P, P, I64, I64, P] + [I64] * 6 + [C.c_int, I64, F32, I64, I64, P, I64, P]),
     "trida_attn_canvas_frag": (C.c_int, [P, P, P, P, P, I64, I64, P] + [I64] * 6 + [C.c_int, I64, F32, I64, I64, P, I64,
                                                                                    P]),

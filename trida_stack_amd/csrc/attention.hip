@@ -8,16 +8,18 @@
 //   mask 2 (canvas, mixed)        j <= t for t < n_clean, always for t >= n_clean
 //
 // attn_partial: workgroup = (sequence, KV head, query tile of <= 128 rows, key split), 8 waves of 16
-//   rows each. Per 64-key step, K and V^T are staged in LDS (XOR-swizzled) while the next step is
-//   loaded into registers; every wave computes S = Q K^T for its rows with v_mfma_f32_16x16x32_bf16 (Q
-//   fragments in registers), runs the online softmax within the wave, and accumulates O += P V.
+//   rows each. Per 64-key step, K (XOR-swizzled) and V (row-major, padded rows) are staged in LDS while
+//   the next step is loaded into registers; every wave computes S^T = K Q^T for its rows with
+//   v_mfma_f32_16x16x32_bf16 (Q and K fragments from LDS), runs the online softmax within the wave, and
+//   accumulates O^T += V^T P^T with the V^T fragments read by ds_read_b64_tr_b16.
 //   Writes the unnormalised O (bf16), row max and row sum (fp32) of its split. A last tile of <= 16
 //   rows can join the tile before it as its extra rows (a canvas of 33 rows x 4 heads = 128 + 4), so
 //   the keys stream once for all rows: wave w takes key tile w % 4 of every step for them (an online
 //   softmax of its own over those keys) and half w / 4 of their output columns, from the K / V
 //   fragments it reads for its own rows; the workgroup merges the four key-tile states at the end.
 // attn_combine: merges the splits per row (log-sum-exp weights), applies the optional output gate
-//   sigmoid(gate) and writes bf16.
+//   sigmoid(gate) and writes bf16; attn_combine2 does the same for exactly two splits in one memory round
+//   trip per row.
 #include <math.h>
 
 #include "common.h"
@@ -658,6 +660,69 @@ __global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
   *reinterpret_cast<u32x2*>(dst) = u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
 }
 
+// Two splits (batches of sequences): thread = (row, 4 output columns), 256 threads = 1024 / D rows. Every
+// load of a row -- both splits' statistics and O pieces, the gate -- is issued at once, so the combine is
+// one memory round trip. The arithmetic is attn_combine_kernel's: a split whose row sees no key (m = -inf)
+// adds nothing (and its O, which an empty split never wrote, is not used); with two terms the order of the
+// sums cannot differ, so the results are bitwise equal.
+constexpr int kC2T = 256;
+bool combine_general = false;  // trida_attn_set_combine_general: the general combine for two splits too
+template <int D>
+__global__ __launch_bounds__(kC2T) void attn_combine2_kernel(CombineArgs a) {
+  constexpr int PER_ROW = D / 4;
+  constexpr int RB = kC2T / PER_ROW;
+  const int M = a.T * a.G;
+  const int b = blockIdx.y / a.Hkv, hk = blockIdx.y % a.Hkv;
+  const int tid = threadIdx.x, i = tid / PER_ROW, c = (tid % PER_ROW) * 4;
+  const int m = blockIdx.x * RB + i;
+  if (m >= M) return;  // no barrier in this kernel
+  const int t = m / a.G, g = m % a.G, hq = hk * a.G + g;
+  const int64_t pair = (int64_t)b * a.Hkv + hk;
+  const int tq = min(m / kMT, a.QT - 1);  // the last tile holds its extra rows past kMT
+  const int64_t bs = (pair * a.QT + tq) * 2;
+  const int r = m - tq * kMT;
+  u32x2 gw = {0u, 0u};
+  if (a.gate)
+    gw = *reinterpret_cast<const u32x2*>(a.gate + ((int64_t)b * a.T + t) * a.gate_st + (int64_t)hq * a.gate_hs + c);
+  const float m0 = a.mpart[bs * kMTX + r], m1 = a.mpart[(bs + 1) * kMTX + r];
+  const float l0 = a.lpart[bs * kMTX + r], l1 = a.lpart[(bs + 1) * kMTX + r];
+  const uint16_t* o0 = a.opart + (bs * kMTX + r) * D + c;
+  const u32x2 x0w = *reinterpret_cast<const u32x2*>(o0);
+  const u32x2 x1w = *reinterpret_cast<const u32x2*>(o0 + (int64_t)kMTX * D);
+  const float mx = fmaxf(m0, m1);
+  const float m_use = mx == -INFINITY ? 0.f : mx;
+  const bool u0 = m0 != -INFINITY, u1 = m1 != -INFINITY;
+  const float w0 = u0 ? exp2f(m0 - m_use) : 0.f, w1 = u1 ? exp2f(m1 - m_use) : 0.f;
+  float lsum;
+  {
+#pragma clang fp contract(off)
+    lsum = w0 * l0 + w1 * l1;  // each product rounded, as the lanes of the general combine's sum hold them
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const float x0[4] = {__uint_as_float(x0w.x << 16), __uint_as_float(x0w.x & 0xffff0000u), __uint_as_float(x0w.y << 16),
+                       __uint_as_float(x0w.y & 0xffff0000u)};
+  const float x1[4] = {__uint_as_float(x1w.x << 16), __uint_as_float(x1w.x & 0xffff0000u), __uint_as_float(x1w.y << 16),
+                       __uint_as_float(x1w.y & 0xffff0000u)};
+  float y[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float acc = 0.f;
+    if (u0) acc = fmaf(w0, x0[e], acc);
+    if (u1) acc = fmaf(w1, x1[e], acc);
+    y[e] = acc * inv;
+  }
+  if (a.gate) {
+    const float gv[4] = {__uint_as_float(gw.x << 16), __uint_as_float(gw.x & 0xffff0000u), __uint_as_float(gw.y << 16),
+                         __uint_as_float(gw.y & 0xffff0000u)};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)  // the attention output is rounded to bf16 before the gate, as torch does
+      y[e] = bf2f(f2bf(y[e])) * (1.f / (1.f + __expf(-gv[e])));
+  }
+  uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * D + c)
+                         : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + c;
+  *reinterpret_cast<u32x2*>(dst) = u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
+}
+
 // Splits per (sequence, KV head, query tile): as many as keep the grid within one workgroup per CU
 // (a workgroup holds a CU's LDS), at least one key block each. Measured at batch 1 (33 canvas rows,
 // 16 / 4 heads, d 256): 2200 keys 30.0 -> 25 us, 8192 keys 54.2 -> 40 us against splits of >= 4 key
@@ -744,6 +809,15 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   if (rc || S == 1) return rc;  // one split: the partial kernel wrote the output
   CombineArgs c{opart, mpart, lpart, gate, out, (int)T, (int)Hq, (int)Hkv, (int)G, (int)D, (int)S, (int)QT,
                 gate_row_stride, gate_head_stride, frag ? 1 : 0};
+  if (S == 2 && !combine_general) {
+    const dim3 cgrid((unsigned)cdiv(T * G, kC2T / (D / 4)), (unsigned)(B * Hkv));
+    switch (D) {
+      case 64: hipLaunchKernelGGL(attn_combine2_kernel<64>, cgrid, dim3(kC2T), 0, st, c); break;
+      case 128: hipLaunchKernelGGL(attn_combine2_kernel<128>, cgrid, dim3(kC2T), 0, st, c); break;
+      default: hipLaunchKernelGGL(attn_combine2_kernel<256>, cgrid, dim3(kC2T), 0, st, c); break;
+    }
+    return launch_status("attn_canvas/combine2");
+  }
   const int64_t rows_per_block = kCT / (D / 4);
   const dim3 cgrid((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv));
   switch (D) {
@@ -754,6 +828,11 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
   return launch_status("attn_canvas/combine");
 }
 }  // namespace
+
+extern "C" int trida_attn_set_combine_general(int on) {
+  combine_general = on != 0;
+  return TRIDA_OK;
+}
 
 extern "C" int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                  const int32_t* prefix_len, const uint16_t* gate, int64_t gate_row_stride,
