@@ -113,17 +113,23 @@ def test_attn_clean_rows_equal_verify_rows(gpu):
     assert torch.equal(o0[:, :17], o2[:, :17])
 
 
-@pytest.mark.parametrize("case", [
-    (1, 33, 16, 4, 256, 2400, [2100]),                          # the 4B-shape canvas, two splits forced
-    (1, 33, 16, 4, 256, 64, [0]),                               # one key block: the second split is empty
-    (40, 33, 16, 4, 256, 500, [(97 * i) % 460 for i in range(40)]),  # a batch: two splits of its own plan
-    (3, 9, 8, 2, 128, 520, [1, 77, 500]),
-    (4, 7, 8, 2, 64, 400, [5, 390, 120, 390]),
+@pytest.mark.parametrize("case,splits", [
+    ((1, 33, 16, 4, 256, 2400, [2100]), 2),                     # the 4B-shape canvas, two splits forced
+    ((1, 33, 16, 4, 256, 64, [0]), 2),                          # one key block: the second split is empty
+    ((40, 33, 16, 4, 256, 500, [(97 * i) % 460 for i in range(40)]), 2),  # a batch: two splits of its plan
+    ((3, 9, 8, 2, 128, 520, [1, 77, 500]), 2),
+    ((4, 7, 8, 2, 64, 400, [5, 390, 120, 390]), 2),
+    ((1, 33, 16, 4, 256, 2400, [2100]), 0),                     # the plan's own split count (32)
+    ((1, 32, 16, 4, 256, 8224, [8192]), 0),                     # config 3
+    ((1, 33, 16, 4, 256, 2400, [2100]), 3),
+    ((1, 33, 16, 4, 256, 300, [200]), 8),                       # 5 key blocks over 8 splits: 3 empty ones
+    ((2, 20, 16, 4, 256, 1500, [1400, 7]), 32),                 # a short sequence: most splits empty
+    ((1, 33, 16, 4, 256, 5000, [4900]), 64),
 ])
 @pytest.mark.parametrize("mode", [0, 2])
-def test_attn_two_split_combine_equals_general(gpu, case, mode):
-    """Two key splits: the one-round-trip combine writes bitwise what the general combine writes (gated and
-    not, row-major and in fragment order), and both match the oracle."""
+def test_attn_fast_combines_equal_general(gpu, case, splits, mode):
+    """The one-round-trip combines (two splits; up to 64 splits at d 256) write bitwise what the general
+    combine writes (gated and not, row-major and in fragment order), and both match the oracle."""
     from trida_stack_amd import _lib
     B, T, Hq, Hkv, D, L, prefix = case
     q, kc, vc = [t.to(DEV) for t in inputs(B * 3 + T + D + mode, B, T, Hq, Hkv, D, L)]
@@ -133,10 +139,10 @@ def test_attn_two_split_combine_equals_general(gpu, case, mode):
     nc = T // 2
     lib = _lib.load()
     for gt in (None, gate):
-        fast = kernels.attn_canvas(q, kc, vc, pl, mask_mode=mode, n_clean=nc, gate=gt, splits=2)
+        fast = kernels.attn_canvas(q, kc, vc, pl, mask_mode=mode, n_clean=nc, gate=gt, splits=splits)
         assert lib.trida_attn_set_combine_general(1) == 0
         try:
-            general = kernels.attn_canvas(q, kc, vc, pl, mask_mode=mode, n_clean=nc, gate=gt, splits=2)
+            general = kernels.attn_canvas(q, kc, vc, pl, mask_mode=mode, n_clean=nc, gate=gt, splits=splits)
         finally:
             lib.trida_attn_set_combine_general(0)
         assert torch.equal(fast.view(torch.int16), general.view(torch.int16))
@@ -144,7 +150,8 @@ def test_attn_two_split_combine_equals_general(gpu, case, mode):
         assert rel(fast, ref) < TOL
     if B * T <= 48:
         of = torch.zeros(kernels.ws_frag_numel(Hq * D), dtype=torch.bfloat16, device=DEV)
-        kernels.attn_canvas(q, kc, vc, pl, mask_mode=mode, n_clean=nc, gate=gate, splits=2, out=of, out_frag=True)
+        kernels.attn_canvas(q, kc, vc, pl, mask_mode=mode, n_clean=nc, gate=gate, splits=splits, out=of,
+                            out_frag=True)
         from test_gpu_wsfused import _frag_mask
         mask = _frag_mask(B * T, Hq * D)
         assert torch.equal(kernels.ws_frag(fast.view(B * T, -1)).view(torch.int16).cpu()[mask],
