@@ -417,9 +417,9 @@ int trida_gdn_restore(const float* snap_state, float* state, const uint16_t* k, 
 int64_t trida_attn_canvas_scratch_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
                                         int64_t max_keys, int64_t splits);
 /* Diagnostic switch (no reference counterpart; for checking one combine against the other): with on != 0
- * the key splits of trida_attn_canvas are always merged by the general combine, also for two splits and
- * for up to 64 splits at D 256, which otherwise take one-round-trip kernels of the same arithmetic
- * (bitwise the same results). Process-wide; not for use while another thread launches attention. */
+ * the key splits of trida_attn_canvas are always merged by the general combine, also for two splits, which
+ * otherwise take a one-round-trip kernel of the same arithmetic (bitwise the same results). Process-wide;
+ * not for use while another thread launches attention. */
 int trida_attn_set_combine_general(int on);
 int trida_attn_canvas(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                       const int32_t* prefix_len, const uint16_t* gate, int64_t gate_row_stride,

@@ -18,8 +18,8 @@
 //   softmax of its own over those keys) and half w / 4 of their output columns, from the K / V
 //   fragments it reads for its own rows; the workgroup merges the four key-tile states at the end.
 // attn_combine: merges the splits per row (log-sum-exp weights), applies the optional output gate
-//   sigmoid(gate) and writes bf16; attn_combine2 (two splits) and attn_combine_fast (up to 64 splits at
-//   d 256) do the same in one memory round trip per row.
+//   sigmoid(gate) and writes bf16; attn_combine2 does the same for exactly two splits in one memory round
+//   trip per row.
 #include <math.h>
 
 #include "common.h"
@@ -666,7 +666,7 @@ __global__ __launch_bounds__(kCT) void attn_combine_kernel(CombineArgs a) {
 // adds nothing (and its O, which an empty split never wrote, is not used); with two terms the order of the
 // sums cannot differ, so the results are bitwise equal.
 constexpr int kC2T = 256;
-bool combine_general = false;  // trida_attn_set_combine_general: the general combine for every split count
+bool combine_general = false;  // trida_attn_set_combine_general: the general combine for two splits too
 template <int D>
 __global__ __launch_bounds__(kC2T) void attn_combine2_kernel(CombineArgs a) {
   constexpr int PER_ROW = D / 4;
@@ -711,73 +711,6 @@ __global__ __launch_bounds__(kC2T) void attn_combine2_kernel(CombineArgs a) {
     if (u1) acc = fmaf(w1, x1[e], acc);
     y[e] = acc * inv;
   }
-  if (a.gate) {
-    const float gv[4] = {__uint_as_float(gw.x << 16), __uint_as_float(gw.x & 0xffff0000u), __uint_as_float(gw.y << 16),
-                         __uint_as_float(gw.y & 0xffff0000u)};
-#pragma unroll
-    for (int e = 0; e < 4; ++e)  // the attention output is rounded to bf16 before the gate, as torch does
-      y[e] = bf2f(f2bf(y[e])) * (1.f / (1.f + __expf(-gv[e])));
-  }
-  uint16_t* dst = a.frag ? a.out + ws_frag_off(b * a.T + t, (int64_t)hq * D + c)
-                         : a.out + (((int64_t)b * a.T + t) * a.Hq + hq) * D + c;
-  *reinterpret_cast<u32x2*>(dst) = u32x2{f2bf2(y[0], y[1]), f2bf2(y[2], y[3])};
-}
-
-// Up to 64 splits at d 256 (a single sequence's canvas): wave = one row, lane = 4 output columns, and lane
-// s also holds split s's row statistics. Every O piece of the row is loaded at once with the statistics,
-// so the combine is one memory round trip. Bitwise attn_combine_kernel's results: the splits with no
-// visible key for a whole row group are always the last ones (their key ranges start past the tile's last
-// visible key), so lane s holds what the general combine's lane s holds, the row max and the weight sum
-// run over the same lanes in the same butterfly order, and O sums the splits in split order; a split
-// whose row sees no key (m = -inf) adds nothing (and its O, which an empty split never wrote, is not used).
-constexpr int kCFS = 64;  // splits of the one-pass combine (one per lane, as in the general combine up to 64)
-template <int D>
-__global__ __launch_bounds__(256) void attn_combine_fast_kernel(CombineArgs a) {
-  static_assert(D / 4 == kWave, "one wave per row");
-  const int M = a.T * a.G;
-  const int b = blockIdx.y / a.Hkv, hk = blockIdx.y % a.Hkv;
-  const int lane = threadIdx.x % kWave, c = lane * 4;
-  const int m = blockIdx.x * 4 + threadIdx.x / kWave;
-  if (m >= M) return;  // wave-uniform; no barrier in this kernel
-  const int t = m / a.G, g = m % a.G, hq = hk * a.G + g;
-  const int64_t pair = (int64_t)b * a.Hkv + hk;
-  const int tq = min(m / kMT, a.QT - 1);  // the last tile holds its extra rows past kMT
-  const int64_t bs = (pair * a.QT + tq) * a.S;
-  const int r = m - tq * kMT, S = a.S;
-  u32x2 gw = {0u, 0u};
-  if (a.gate)
-    gw = *reinterpret_cast<const u32x2*>(a.gate + ((int64_t)b * a.T + t) * a.gate_st + (int64_t)hq * a.gate_hs + c);
-  const uint16_t* ob = a.opart + (bs * kMTX + r) * D + c;
-  u32x2 xw[kCFS];
-#pragma unroll
-  for (int sp = 0; sp < kCFS; ++sp) xw[sp] = *reinterpret_cast<const u32x2*>(ob + (int64_t)min(sp, S - 1) * kMTX * D);
-  const int sl = min(lane, S - 1);
-  float ml = a.mpart[(bs + sl) * kMTX + r], ll = a.lpart[(bs + sl) * kMTX + r];
-  if (lane >= S) {
-    ml = -INFINITY;
-    ll = 0.f;
-  }
-  float mx = ml;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
-  const float m_use = mx == -INFINITY ? 0.f : mx;
-  const float w = exp2f(ml - m_use);
-  float lsum = lane < S ? w * ll : 0.f;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, kWave);
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int sp = 0; sp < kCFS; ++sp) {
-    const float ws = __shfl(w, sp, kWave), ms = __shfl(ml, sp, kWave);
-    if (sp < S && ms != -INFINITY) {  // uniform
-      const f32x4 x = {__uint_as_float(xw[sp].x << 16), __uint_as_float(xw[sp].x & 0xffff0000u),
-                       __uint_as_float(xw[sp].y << 16), __uint_as_float(xw[sp].y & 0xffff0000u)};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = fmaf(ws, x[e], acc[e]);
-    }
-  }
-  float y[4] = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
   if (a.gate) {
     const float gv[4] = {__uint_as_float(gw.x << 16), __uint_as_float(gw.x & 0xffff0000u), __uint_as_float(gw.y << 16),
                          __uint_as_float(gw.y & 0xffff0000u)};
@@ -884,11 +817,6 @@ int attn_canvas_run(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
       default: hipLaunchKernelGGL(attn_combine2_kernel<256>, cgrid, dim3(kC2T), 0, st, c); break;
     }
     return launch_status("attn_canvas/combine2");
-  }
-  if (D == 256 && S <= kCFS && !combine_general) {
-    const dim3 cgrid((unsigned)cdiv(T * G, 4), (unsigned)(B * Hkv));
-    hipLaunchKernelGGL(attn_combine_fast_kernel<256>, cgrid, dim3(256), 0, st, c);
-    return launch_status("attn_canvas/combine_fast");
   }
   const int64_t rows_per_block = kCT / (D / 4);
   const dim3 cgrid((unsigned)cdiv(T * G, rows_per_block), (unsigned)(B * Hkv));
